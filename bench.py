@@ -1,0 +1,213 @@
+"""Energy + forces throughput of the FACE hot path on one MI355X.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload 3] [--also 2] [--no-cpu]
+
+A step is one energy + forces evaluation of the whole synthetic system with its pair list
+already resident in HBM (the pair-list build is timed separately, as the reference excludes
+it from its timings). Workloads (face_amd.systems.workload):
+  0  64 x C9H8O4 molecules, FACE C96 B16 K32 rc 4.5
+  1  512 x C9H8O4 molecules, FACE-CP C160 rc 4.5
+  2  FCC Ag 6x6x6 = 864 atoms, FACE C96 B16 K32 rc 4.5
+  3  24,000-atom H:C:O liquid, FACE-CP C160 rc 5.0            (headline `value`)
+  4  100,000-atom H:C:O liquid, FACE C256 B16 K64 rc 5.5
+Prints ONE JSON line; progress goes to stderr.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for p in (REPO, os.path.join(REPO, "face-mlip_amd")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+import numpy as np  # noqa: E402
+import torch  # noqa: E402
+
+METRIC = "atom-steps/s (E+F, fp32) at 864 & 24k atoms; density-kernel HBM GB/s"
+HBM_PEAK_GBS = 8000.0
+TIMED = ["density_fwd20", "density_bwd20", "density_fwd4", "density_bwd4", "cp_fwd", "cp_bwd", "node_fwd",
+         "node_bwd", "edge_fwd", "edge_bwd", "force_scatter", "gather_bwd"]
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def algorithmic_bytes(label, g, kw):
+    """Bytes per launch: every operand of the kernel's interface read once, every output written
+    once, fp32 / int32 (valid pairs E only)."""
+    E, N = g.E, g.N
+    B, C = kw["B"], kw["C"]
+    K = C if kw.get("cp") else kw["K"]
+    Kt = 9 * kw["K_dir"]
+    if label == "density_fwd20":
+        return 4 * (E * (B + K + 20) + 20 * N * B * K)
+    if label == "density_bwd20":
+        return 4 * (2 * E * (B + K + 20) + 20 * N * B * K)
+    if label == "density_fwd4":
+        return 4 * (E * (B + Kt + 4) + 4 * N * B * Kt)
+    if label == "density_bwd4":
+        return 4 * (2 * E * (B + Kt + 4) + 4 * N * B * Kt)
+    if label == "cp_fwd":
+        return 4 * (E * (5 * C + 20) + 20 * N * C)
+    if label == "cp_bwd":
+        return 4 * (2 * E * (5 * C + 20) + 20 * N * C)
+    if label == "node_fwd":
+        return 4 * 64 * N * C           # 47 in, 8 invariants + 3 V + 6 symmetric M out (eq pass)
+    if label == "node_bwd":
+        return 4 * 111 * N * C          # 47 in, 8 + 3 + 6 upstream, 47 out
+    if label == "edge_fwd":
+        return 4 * E * (11 + 29)
+    if label == "edge_bwd":
+        return 4 * E * (11 + 29 + 3)
+    if label == "force_scatter":
+        return 4 * (3 * E + E + 3 * N)
+    return None
+
+
+def model_for(kw, el):
+    from face_amd import model as fm
+    torch.manual_seed(0)
+    m = fm.FACE(el, **kw)
+    fm.unit_parameterise(m)
+    return m.cuda().eval()
+
+
+def run_gpu(k, steps, warmup):
+    from face_amd import _lib, systems
+    from face_amd.neighbors import build_graph
+    sts, kw, el, desc = systems.workload(k)
+    log(f"[bench] workload {k}: {desc}")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    g = build_graph(sts, kw["rc"])
+    torch.cuda.synchronize()
+    t_nbr = time.perf_counter() - t0
+    log(f"[bench]   pair list: N={g.N} E={g.E} max_row={g.max_row} ({t_nbr * 1e3:.1f} ms incl. host staging)")
+    m = model_for(kw, el)
+
+    def step():
+        return m(g.with_pos(g.pos.clone()))["forces"]
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    log(f"[bench]   warm-up done ({warmup} steps)")
+    timers = _lib.time_calls(TIMED)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    _lib.stop_timing()
+    kern = {}
+    for label, evs in timers.items():
+        if not evs:
+            continue
+        ms = [s.elapsed_time(e) for s, e in evs]
+        avg_us = 1e3 * float(np.mean(ms))
+        byts = algorithmic_bytes(label, g, kw)
+        kern[label] = {"launches_per_step": len(evs) / steps, "avg_us": avg_us,
+                       "ms_per_step": float(np.sum(ms)) / steps,
+                       "alg_bytes": byts, "GBps": (byts / (avg_us * 1e-6) / 1e9) if byts else None}
+    ms_step = 1e3 * dt / steps
+    log(f"[bench]   {ms_step:.3f} ms/step, {g.N * steps / dt:.0f} atom-steps/s")
+    return {"N": g.N, "E": g.E, "ms_per_step": ms_step, "atom_steps_per_s": g.N * steps / dt, "kernels": kern,
+            "pairlist_ms": 1e3 * t_nbr, "desc": desc, "kw": kw}
+
+
+def run_cpu(k, n_atoms, rounds=5, warm=2):
+    """The CPU oracle (pure-torch restatement of the reference path) on a bounded sample."""
+    from face_amd import systems
+    from oracle import model as om
+    from oracle.neighbors import padded_graph as opad
+    cores = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(cores)
+    sts, kw, el, desc = systems.workload(k, n_atoms=n_atoms)
+    if n_atoms and k in (0, 1):
+        sts = sts[:max(1, n_atoms // 21)]
+    torch.manual_seed(0)
+    m = om.unit_parameterise(om.FACE(el, **kw)).eval()
+    g = opad(sts, kw["rc"])
+    gg = {kk: g[kk] for kk in ("pos", "Z", "nbr", "shift", "mask", "batch")}
+    N = gg["pos"].shape[0]
+    for _ in range(warm):
+        m(dict(gg, pos=gg["pos"].clone()))
+    t0 = time.perf_counter()
+    for _ in range(rounds):
+        m(dict(gg, pos=gg["pos"].clone()))
+    dt = time.perf_counter() - t0
+    return {"value": N * rounds / dt, "unit": "atom-steps/s", "cores": cores, "kind": "port",
+            "sample": f"{N}-atom sample of the same recipe and model ({desc.split(',')[-1].strip()}), "
+                      f"oracle torch path, {rounds} timed E+F calls after {warm} warm-ups, "
+                      f"torch.set_num_threads({cores})"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--workload", type=int, default=3)
+    ap.add_argument("--also", default="2", help="comma list of extra workloads reported under 'also'")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-atoms", type=int, default=1500)
+    a = ap.parse_args()
+    if a.gpus != 1:
+        print("bench.py measures one GPU: every box here has one MI355X and this build has no multi-GPU "
+              "path (see DESIGN.md for how the work would shard). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(2)
+    torch.backends.cuda.matmul.allow_tf32 = False
+    torch.backends.cudnn.allow_tf32 = False
+    torch.set_float32_matmul_precision("highest")
+    main_run = run_gpu(a.workload, a.steps, a.warmup)
+    also = {}
+    for k in [int(x) for x in a.also.split(",") if x.strip()]:
+        if k != a.workload:
+            r = run_gpu(k, a.steps, a.warmup)
+            also[f"workload{k}"] = {"desc": r["desc"], "atoms": r["N"], "pairs": r["E"],
+                                    "atom_steps_per_s": r["atom_steps_per_s"], "ms_per_step": r["ms_per_step"],
+                                    "pairlist_ms": r["pairlist_ms"],
+                                    "kernels": {kk: {"avg_us": v["avg_us"], "GBps": v["GBps"]}
+                                                for kk, v in r["kernels"].items()}}
+    kern = main_run["kernels"]
+    hbm = {k: v for k, v in kern.items() if v["alg_bytes"]}
+    dom = max(hbm, key=lambda k: hbm[k]["ms_per_step"]) if hbm else None
+    roofline = None
+    if dom:
+        ach = hbm[dom]["GBps"]
+        roofline = {"kernel": dom, "bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": ach / HBM_PEAK_GBS, "traffic": None, "alg_bytes_per_launch": hbm[dom]["alg_bytes"],
+                    "avg_launch_us": hbm[dom]["avg_us"]}
+    cpu = None
+    if not a.no_cpu:
+        log("[bench] cpu baseline ...")
+        cpu = run_cpu(a.workload, a.cpu_atoms)
+        log(f"[bench]   cpu {cpu['value']:.1f} atom-steps/s on {cpu['cores']} cores")
+    kw = main_run["kw"]
+    out = {
+        "metric": METRIC, "value": main_run["atom_steps_per_s"], "unit": "atom-steps/s", "n_gpus": 1,
+        "steps": a.steps, "warmup": a.warmup, "ms_per_step": main_run["ms_per_step"], "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": main_run["desc"], "atoms": main_run["N"], "pairs": main_run["E"],
+                   "model": {k: kw[k] for k in ("C", "B", "K", "rc") if k in kw} | {"cp": bool(kw.get("cp"))},
+                   "weights": "random init, torch.manual_seed(0) + unit_parameterise", "parallelism": "single GPU"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "kernels": {k: {"avg_us": v["avg_us"], "launches_per_step": v["launches_per_step"], "GBps": v["GBps"],
+                        "frac_hbm": (v["GBps"] / HBM_PEAK_GBS) if v["GBps"] else None} for k, v in kern.items()},
+        "pairlist_ms": main_run["pairlist_ms"],
+        "also": also,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,40 @@
+// Shared definitions for the FACE hot-path kernels (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/face_hip.h"
+
+#define FACE_LAUNCH_CHECK()                               \
+    do {                                                  \
+        hipError_t e_ = hipGetLastError();                \
+        if (e_ != hipSuccess) return (int)e_;             \
+    } while (0)
+
+namespace face {
+
+constexpr int kWave = 64;
+
+// Rank of each of the 20 symmetric monomials (1 | x y z | 6 rank-2 | 10 rank-3).
+__host__ __device__ constexpr int rank_of(int x) { return x == 0 ? 0 : (x < 4 ? 1 : (x < 10 ? 2 : 3)); }
+
+// Edge range of receiver atom i: CSR row_ptr, or the uniform padded stride M when row_ptr is null.
+__device__ __forceinline__ void row_range(const int32_t* __restrict__ row_ptr, int64_t i, int M, int64_t& e0,
+                                          int64_t& e1) {
+    if (row_ptr) {
+        e0 = row_ptr[i];
+        e1 = row_ptr[i + 1];
+    } else {
+        e0 = i * (int64_t)M;
+        e1 = e0 + M;
+    }
+}
+
+// Butterfly sum over aligned groups of `width` lanes (width a power of two <= 64); every
+// lane of the group ends with the group total.
+__device__ __forceinline__ float group_sum(float v, int width) {
+    for (int o = width >> 1; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+}
+
+}  // namespace face

@@ -1,0 +1,510 @@
+// Receiver-segmented density reductions for FACE (gfx950).
+//
+// Factor density  D[i,x,b*K+k] = sum_{e in row i} phi[e,b] msg[m(e),k] Y[e,x]     (face/kernels.py:3,170-178)
+// CP density      A[i,x,c]     = sum_{e in row i} R[e,l(x),c] msg[m(e),c] Y[e,x]  (face/model.py:496-502)
+//
+// Every output row belongs to exactly one workgroup, so the reductions run in registers and
+// LDS with no global atomics; results are bitwise reproducible run to run.
+#include "common.h"
+
+namespace face {
+
+constexpr int kBlock = 256;
+constexpr int kTileE = 32;   // edges staged per LDS tile (forward kernels)
+
+// ------------------------------------------------------------------ factor forward
+// Workgroup = (atom i, column chunk). Thread owns CPT columns (b,k) and NX accumulators
+// per column; the edge tile (phi, msg, Y) is staged in LDS and read as broadcasts.
+template <int NX, int CPT>
+__global__ __launch_bounds__(kBlock) void density_fwd_kernel(
+    const float* __restrict__ phi, int ld_phi, const float* __restrict__ msg, int ld_msg,
+    const int32_t* __restrict__ msg_row, const float* __restrict__ Y, int ld_Y, const int32_t* __restrict__ row_ptr,
+    int M, int B, int K, float* __restrict__ D) {
+    extern __shared__ float lds[];
+    float* s_phi = lds;                    // kTileE * B
+    float* s_msg = s_phi + kTileE * B;     // kTileE * K
+    float* s_Y = s_msg + kTileE * K;       // kTileE * NX
+    const int64_t i = blockIdx.x;
+    const int BK = B * K;
+    const int tid = threadIdx.x;
+    int bcol[CPT], kcol[CPT];
+    bool ok[CPT];
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+        const int c = blockIdx.y * (kBlock * CPT) + j * kBlock + tid;
+        ok[j] = c < BK;
+        bcol[j] = ok[j] ? c / K : 0;
+        kcol[j] = ok[j] ? c - bcol[j] * K : 0;
+    }
+    float acc[CPT][NX];
+#pragma unroll
+    for (int j = 0; j < CPT; ++j)
+#pragma unroll
+        for (int x = 0; x < NX; ++x) acc[j][x] = 0.f;
+
+    int64_t e0, e1;
+    row_range(row_ptr, i, M, e0, e1);
+    for (int64_t t0 = e0; t0 < e1; t0 += kTileE) {
+        const int nt = (int)min((int64_t)kTileE, e1 - t0);
+        for (int q = tid; q < nt * B; q += kBlock) {
+            const int t = q / B;
+            s_phi[q] = phi[(t0 + t) * ld_phi + (q - t * B)];
+        }
+        for (int q = tid; q < nt * K; q += kBlock) {
+            const int t = q / K;
+            const int64_t row = msg_row ? (int64_t)msg_row[t0 + t] : t0 + t;
+            s_msg[q] = msg[row * ld_msg + (q - t * K)];
+        }
+        for (int q = tid; q < nt * NX; q += kBlock) {
+            const int t = q / NX;
+            s_Y[q] = Y[(t0 + t) * ld_Y + (q - t * NX)];
+        }
+        __syncthreads();
+        for (int t = 0; t < nt; ++t) {
+            float p[CPT];
+#pragma unroll
+            for (int j = 0; j < CPT; ++j) p[j] = s_phi[t * B + bcol[j]] * s_msg[t * K + kcol[j]];
+            const float* y = s_Y + t * NX;
+#pragma unroll
+            for (int x = 0; x < NX; ++x) {
+                const float yx = y[x];
+#pragma unroll
+                for (int j = 0; j < CPT; ++j) acc[j][x] = fmaf(p[j], yx, acc[j][x]);
+            }
+        }
+        __syncthreads();
+    }
+    float* Di = D + i * (int64_t)NX * BK;
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+        if (!ok[j]) continue;
+        const int c = blockIdx.y * (kBlock * CPT) + j * kBlock + tid;
+#pragma unroll
+        for (int x = 0; x < NX; ++x) Di[(int64_t)x * BK + c] = acc[j][x];
+    }
+}
+
+// ------------------------------------------------------------------ factor backward
+// Workgroup = atom i; G[i] (NX x B x K) is staged in LDS, split in GN k-slices of KS
+// columns (slice stride KSP, 16-byte aligned). A lane is (edge slot, k-slice g): it keeps
+// phi[e,:], its msg slice and their gradients in registers and walks every (x, b):
+//   s = sum_k G[x,b,k] msg[k]          -> dphi[b] += s Y[x],  dY[x] += s phi[b]
+//   dmsg[k] += G[x,b,k] Y[x] phi[b]
+// dY and dphi are then summed over the GN lanes of the edge (butterfly shuffles).
+template <int NX, int B, int KS>
+__global__ __launch_bounds__(kBlock) void density_bwd_kernel(
+    const float* __restrict__ phi, int ld_phi, const float* __restrict__ msg, int ld_msg,
+    const int32_t* __restrict__ msg_row, const float* __restrict__ Y, int ld_Y, const int32_t* __restrict__ row_ptr,
+    int M, int K, int glog, const float* __restrict__ G, float* __restrict__ dphi, int ld_dphi,
+    float* __restrict__ dmsg, int ld_dmsg, float* __restrict__ dY, int ld_dY) {
+    constexpr int KSP = (KS + 3) & ~3;
+    extern __shared__ float lds[];
+    const int GN = 1 << glog;
+    const int64_t i = blockIdx.x;
+    const int BK = B * K;
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    const float* Gi = G + i * (int64_t)NX * BK;
+    const int nslot = NX * B * GN * KSP;
+    for (int p = tid; p < nslot; p += nthr) {
+        const int kk = p % KSP;
+        int r = p / KSP;
+        const int g = r % GN;
+        r /= GN;
+        const int b = r % B, x = r / B;
+        const int k = g * KS + kk;
+        lds[p] = (kk < KS && k < K) ? Gi[x * BK + b * K + k] : 0.f;
+    }
+    __syncthreads();
+
+    const int g = tid & (GN - 1);
+    const int slot = tid >> glog;
+    const int nslots = nthr >> glog;
+    int64_t e0, e1;
+    row_range(row_ptr, i, M, e0, e1);
+    for (int64_t base = e0; base < e1; base += nslots) {   // same trip count for every lane
+        const int64_t e = base + slot;
+        const bool valid = e < e1;
+        float ph[B], dph[B], mg[KS], dmg[KS];
+        const int64_t row = valid ? (msg_row ? (int64_t)msg_row[e] : e) : 0;
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            ph[b] = valid ? phi[e * ld_phi + b] : 0.f;
+            dph[b] = 0.f;
+        }
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) {
+            const int k = g * KS + kk;
+            mg[kk] = (valid && k < K) ? msg[row * ld_msg + k] : 0.f;
+            dmg[kk] = 0.f;
+        }
+        for (int x = 0; x < NX; ++x) {
+            const float y = valid ? Y[e * ld_Y + x] : 0.f;
+            const float* gx = lds + ((x * B) * GN + g) * KSP;
+            float dy = 0.f;
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                const float* gp = gx + b * GN * KSP;
+                const float yp = y * ph[b];
+                float s = 0.f;
+#pragma unroll
+                for (int kk = 0; kk < KS; ++kk) {
+                    const float gv = gp[kk];
+                    s = fmaf(gv, mg[kk], s);
+                    dmg[kk] = fmaf(gv, yp, dmg[kk]);
+                }
+                dph[b] = fmaf(s, y, dph[b]);
+                dy = fmaf(s, ph[b], dy);
+            }
+            dy = group_sum(dy, GN);
+            if (dY && valid && g == 0) dY[e * ld_dY + x] = dy;
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) dph[b] = group_sum(dph[b], GN);
+        if (valid) {
+            if (dphi) {
+#pragma unroll
+                for (int b = 0; b < B; ++b)
+                    if ((b & (GN - 1)) == g) dphi[e * ld_dphi + b] = dph[b];
+            }
+            if (dmsg) {
+#pragma unroll
+                for (int kk = 0; kk < KS; ++kk) {
+                    const int k = g * KS + kk;
+                    if (k < K) dmsg[e * ld_dmsg + k] = dmg[kk];
+                }
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------ CP forward
+// Workgroup = (atom i, channel chunk); thread = channel c with 20 accumulators. Per edge it
+// streams R[e,0..3,c] and msg[m(e),c] (coalesced over c); Y is staged in LDS.
+constexpr int kTileCP = 16;
+
+__global__ __launch_bounds__(kBlock) void cp_density_fwd_kernel(
+    const float* __restrict__ R, int ld_R, const float* __restrict__ msg, int ld_msg,
+    const int32_t* __restrict__ msg_row, const float* __restrict__ Y, int ld_Y, const int32_t* __restrict__ row_ptr,
+    int M, int C, float* __restrict__ A) {
+    __shared__ float s_Y[kTileCP * 20];
+    const int64_t i = blockIdx.x;
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    const int c = blockIdx.y * nthr + tid;
+    const bool ok = c < C;
+    float acc[20];
+#pragma unroll
+    for (int x = 0; x < 20; ++x) acc[x] = 0.f;
+    int64_t e0, e1;
+    row_range(row_ptr, i, M, e0, e1);
+    for (int64_t t0 = e0; t0 < e1; t0 += kTileCP) {
+        const int nt = (int)min((int64_t)kTileCP, e1 - t0);
+        for (int q = tid; q < nt * 20; q += nthr) {
+            const int t = q / 20;
+            s_Y[q] = Y[(t0 + t) * ld_Y + (q - t * 20)];
+        }
+        __syncthreads();
+        if (ok) {
+#pragma unroll 2
+            for (int t = 0; t < nt; ++t) {
+                const int64_t e = t0 + t;
+                const int64_t row = msg_row ? (int64_t)msg_row[e] : e;
+                const float m = msg[row * ld_msg + c];
+                const float* Re = R + e * ld_R + c;
+                const float w0 = Re[0] * m, w1 = Re[C] * m, w2 = Re[2 * C] * m, w3 = Re[3 * C] * m;
+                const float* y = s_Y + t * 20;
+                acc[0] = fmaf(w0, y[0], acc[0]);
+#pragma unroll
+                for (int x = 1; x < 4; ++x) acc[x] = fmaf(w1, y[x], acc[x]);
+#pragma unroll
+                for (int x = 4; x < 10; ++x) acc[x] = fmaf(w2, y[x], acc[x]);
+#pragma unroll
+                for (int x = 10; x < 20; ++x) acc[x] = fmaf(w3, y[x], acc[x]);
+            }
+        }
+        __syncthreads();
+    }
+    if (ok) {
+        float* Ai = A + i * (int64_t)20 * C + c;
+#pragma unroll
+        for (int x = 0; x < 20; ++x) Ai[(int64_t)x * C] = acc[x];
+    }
+}
+
+// ------------------------------------------------------------------ CP backward
+// Workgroup = atom i, one thread per channel (C <= 256). gA[i] sits in registers (channel
+// view) and in LDS (monomial view). Per tile of edges:
+//   channel phase:  t_l = sum_{x in l} gA[x,c] Y[e,x];  dR[e,l,c] = msg t_l;
+//                   dmsg[e,c] = sum_l R[e,l,c] t_l;      w[e,l,c] = R msg -> LDS
+//   monomial phase: dY[e,x] = sum_c gA[x,c] w[e,l(x),c]   (lane = (edge, x), dot over c)
+constexpr int kTileCPB = 8;
+
+__global__ __launch_bounds__(kBlock) void cp_density_bwd_kernel(
+    const float* __restrict__ R, int ld_R, const float* __restrict__ msg, int ld_msg,
+    const int32_t* __restrict__ msg_row, const float* __restrict__ Y, int ld_Y, const int32_t* __restrict__ row_ptr,
+    int M, int C, const float* __restrict__ gA, float* __restrict__ dR, int ld_dR, float* __restrict__ dmsg,
+    int ld_dmsg, float* __restrict__ dY, int ld_dY) {
+    extern __shared__ float lds[];
+    const int CP1 = C + 1;                       // padded row: conflict-free column walks
+    float* s_g = lds;                            // 20 x CP1
+    float* s_w = s_g + 20 * CP1;                 // kTileCPB*4 x CP1
+    float* s_Y = s_w + kTileCPB * 4 * CP1;       // kTileCPB x 20
+    const int64_t i = blockIdx.x;
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    const float* gAi = gA + i * (int64_t)20 * C;
+    for (int q = tid; q < 20 * C; q += nthr) {
+        const int x = q / C;
+        s_g[x * CP1 + (q - x * C)] = gAi[q];
+    }
+    const int c = tid;
+    const bool ok = c < C;
+    float g[20];
+#pragma unroll
+    for (int x = 0; x < 20; ++x) g[x] = ok ? gAi[x * C + c] : 0.f;
+    int64_t e0, e1;
+    row_range(row_ptr, i, M, e0, e1);
+    for (int64_t t0 = e0; t0 < e1; t0 += kTileCPB) {
+        const int nt = (int)min((int64_t)kTileCPB, e1 - t0);
+        for (int q = tid; q < nt * 20; q += nthr) {
+            const int t = q / 20;
+            s_Y[q] = Y[(t0 + t) * ld_Y + (q - t * 20)];
+        }
+        __syncthreads();
+        if (ok) {
+            for (int t = 0; t < nt; ++t) {
+                const int64_t e = t0 + t;
+                const int64_t row = msg_row ? (int64_t)msg_row[e] : e;
+                const float m = msg[row * ld_msg + c];
+                const float* Re = R + e * ld_R + c;
+                const float r0 = Re[0], r1 = Re[C], r2 = Re[2 * C], r3 = Re[3 * C];
+                const float* y = s_Y + t * 20;
+                float t0v = g[0] * y[0], t1v = 0.f, t2v = 0.f, t3v = 0.f;
+#pragma unroll
+                for (int x = 1; x < 4; ++x) t1v = fmaf(g[x], y[x], t1v);
+#pragma unroll
+                for (int x = 4; x < 10; ++x) t2v = fmaf(g[x], y[x], t2v);
+#pragma unroll
+                for (int x = 10; x < 20; ++x) t3v = fmaf(g[x], y[x], t3v);
+                if (dR) {
+                    float* dRe = dR + e * ld_dR + c;
+                    dRe[0] = m * t0v;
+                    dRe[C] = m * t1v;
+                    dRe[2 * C] = m * t2v;
+                    dRe[3 * C] = m * t3v;
+                }
+                if (dmsg) dmsg[e * ld_dmsg + c] = r0 * t0v + r1 * t1v + r2 * t2v + r3 * t3v;
+                float* w = s_w + (t * 4) * CP1 + c;
+                w[0] = r0 * m;
+                w[CP1] = r1 * m;
+                w[2 * CP1] = r2 * m;
+                w[3 * CP1] = r3 * m;
+            }
+        }
+        __syncthreads();
+        if (dY) {
+            for (int q = tid; q < nt * 20; q += nthr) {
+                const int t = q / 20, x = q - t * 20;
+                const float* gx = s_g + x * CP1;
+                const float* wx = s_w + (t * 4 + rank_of(x)) * CP1;
+                float s = 0.f;
+                for (int cc = 0; cc < C; ++cc) s = fmaf(gx[cc], wx[cc], s);
+                dY[(t0 + t) * ld_dY + x] = s;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// ------------------------------------------------------------------ launch helpers
+template <int NX>
+static int launch_fwd_nx(int cpt, dim3 grid, size_t lds, hipStream_t st, const float* phi, int ld_phi,
+                         const float* msg, int ld_msg, const int32_t* msg_row, const float* Y, int ld_Y,
+                         const int32_t* row_ptr, int M, int B, int K, float* D) {
+#define FACE_FWD(C_)                                                                                          \
+    hipLaunchKernelGGL((density_fwd_kernel<NX, C_>), grid, dim3(kBlock), lds, st, phi, ld_phi, msg, ld_msg,  \
+                       msg_row, Y, ld_Y, row_ptr, M, B, K, D)
+    switch (cpt) {
+        case 1: FACE_FWD(1); break;
+        case 2: FACE_FWD(2); break;
+        case 4: FACE_FWD(4); break;
+        case 9: FACE_FWD(9); break;
+        default: return FACE_ERR_UNSUPPORTED;
+    }
+#undef FACE_FWD
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+static int max_lds_bytes() {
+    static int v = -1;
+    if (v < 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+            v = 65536;
+    }
+    return v;
+}
+
+template <int NX, int B, int KS>
+static int launch_bwd3(int glog, int nthr, int64_t N, hipStream_t st, const float* phi, int ld_phi,
+                       const float* msg, int ld_msg, const int32_t* msg_row, const float* Y, int ld_Y,
+                       const int32_t* row_ptr, int M, int K, const float* G, float* dphi, int ld_dphi, float* dmsg,
+                       int ld_dmsg, float* dY, int ld_dY) {
+    constexpr int KSP = (KS + 3) & ~3;
+    const size_t lds = (size_t)NX * B * (1 << glog) * KSP * sizeof(float);
+    if ((int64_t)lds > max_lds_bytes()) return FACE_ERR_UNSUPPORTED;
+    auto kern = density_bwd_kernel<NX, B, KS>;
+    if (lds > 65536 &&
+        hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+        return FACE_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL(kern, dim3((unsigned)N), dim3(nthr), lds, st, phi, ld_phi, msg, ld_msg, msg_row, Y, ld_Y,
+                       row_ptr, M, K, glog, G, dphi, ld_dphi, dmsg, ld_dmsg, dY, ld_dY);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+template <int NX, int B>
+static int launch_bwd_b(int ks, int glog, int nthr, int64_t N, hipStream_t st, const float* phi, int ld_phi,
+                        const float* msg, int ld_msg, const int32_t* msg_row, const float* Y, int ld_Y,
+                        const int32_t* row_ptr, int M, int K, const float* G, float* dphi, int ld_dphi,
+                        float* dmsg, int ld_dmsg, float* dY, int ld_dY) {
+#define FACE_BWD(KS_)                                                                                            \
+    return launch_bwd3<NX, B, KS_>(glog, nthr, N, st, phi, ld_phi, msg, ld_msg, msg_row, Y, ld_Y, row_ptr, M, K, \
+                                   G, dphi, ld_dphi, dmsg, ld_dmsg, dY, ld_dY)
+    switch (ks) {
+        case 4: FACE_BWD(4);
+        case 8: FACE_BWD(8);
+        case 9: FACE_BWD(9);
+        default: return FACE_ERR_UNSUPPORTED;
+    }
+#undef FACE_BWD
+}
+
+template <int NX>
+static int launch_bwd_nx(int B, int ks, int glog, int nthr, int64_t N, hipStream_t st, const float* phi,
+                         int ld_phi, const float* msg, int ld_msg, const int32_t* msg_row, const float* Y, int ld_Y,
+                         const int32_t* row_ptr, int M, int K, const float* G, float* dphi, int ld_dphi,
+                         float* dmsg, int ld_dmsg, float* dY, int ld_dY) {
+#define FACE_BWDB(B_)                                                                                       \
+    return launch_bwd_b<NX, B_>(ks, glog, nthr, N, st, phi, ld_phi, msg, ld_msg, msg_row, Y, ld_Y, row_ptr, \
+                                M, K, G, dphi, ld_dphi, dmsg, ld_dmsg, dY, ld_dY)
+    switch (B) {
+        case 4: FACE_BWDB(4);
+        case 8: FACE_BWDB(8);
+        case 16: FACE_BWDB(16);
+        case 32: FACE_BWDB(32);
+        default: return FACE_ERR_UNSUPPORTED;
+    }
+#undef FACE_BWDB
+}
+
+// Chooses the k-slice split (GN lanes of KS columns per edge) and the workgroup size that
+// waste the fewest lanes for rows of length max_row.
+static bool plan_bwd(int K, int max_row, int& ks_out, int& glog_out, int& nthr_out) {
+    const int ks_opts[3] = {4, 8, 9};
+    double best = -1.0;
+    for (int glog = 0; glog <= 5; ++glog) {
+        const int GN = 1 << glog;
+        for (int ks : ks_opts) {
+            if (GN * ks < K || (GN > 1 && (GN / 2) * ks >= K)) continue;   // minimal GN for this ks
+            const int per_wave = kWave / GN;
+            int nw = (max_row + per_wave - 1) / per_wave;
+            nw = nw < 1 ? 1 : (nw > 4 ? 4 : nw);
+            const int slots = nw * per_wave;
+            const int passes = (max_row + slots - 1) / slots;
+            const double lane_eff = (double)max_row / (double)(passes * slots > 0 ? passes * slots : 1);
+            const double k_eff = (double)K / (double)(GN * ks);
+            const double score = lane_eff * k_eff + 1e-3 * ks;   // prefer fewer shuffles on ties
+            if (score > best) {
+                best = score;
+                ks_out = ks;
+                glog_out = glog;
+                nthr_out = nw * kWave;
+            }
+        }
+    }
+    return best > 0.0;
+}
+
+}  // namespace face
+
+using namespace face;
+
+extern "C" int face_density_fwd(const float* phi, int32_t ld_phi, const float* msg, int32_t ld_msg,
+                                const int32_t* msg_row, const float* Y, int32_t ld_Y, int32_t NX,
+                                const int32_t* row_ptr, int64_t N, int32_t M, int32_t B, int32_t K, float* D,
+                                void* stream) {
+    if (N < 0 || B <= 0 || K <= 0 || (NX != 4 && NX != 20)) return FACE_ERR_ARG;
+    if (ld_phi < B || ld_msg < K || ld_Y < NX || (!row_ptr && M < 0)) return FACE_ERR_ARG;
+    if (N == 0) return 0;
+    if (!phi || !msg || !Y || !D) return FACE_ERR_ARG;
+    const int BK = B * K;
+    const int opts20[3] = {1, 2, 4}, opts4[4] = {1, 2, 4, 9};
+    const int* opts = NX == 20 ? opts20 : opts4;
+    const int nopt = NX == 20 ? 3 : 4;
+    int cpt = opts[nopt - 1];
+    for (int q = 0; q < nopt; ++q)
+        if (kBlock * opts[q] >= BK) { cpt = opts[q]; break; }
+    const unsigned chunks = (unsigned)((BK + kBlock * cpt - 1) / (kBlock * cpt));
+    const size_t lds = (size_t)kTileE * (B + K + NX) * sizeof(float);
+    if ((int64_t)lds > 65536) return FACE_ERR_UNSUPPORTED;
+    dim3 grid((unsigned)N, chunks);
+    hipStream_t st = (hipStream_t)stream;
+    if (NX == 20)
+        return launch_fwd_nx<20>(cpt, grid, lds, st, phi, ld_phi, msg, ld_msg, msg_row, Y, ld_Y, row_ptr, M, B, K, D);
+    return launch_fwd_nx<4>(cpt, grid, lds, st, phi, ld_phi, msg, ld_msg, msg_row, Y, ld_Y, row_ptr, M, B, K, D);
+}
+
+extern "C" int face_density_bwd(const float* phi, int32_t ld_phi, const float* msg, int32_t ld_msg,
+                                const int32_t* msg_row, const float* Y, int32_t ld_Y, int32_t NX,
+                                const int32_t* row_ptr, int64_t N, int32_t M, int32_t max_row, int32_t B, int32_t K,
+                                const float* G, float* dphi, int32_t ld_dphi, float* dmsg, int32_t ld_dmsg, float* dY,
+                                int32_t ld_dY, void* stream) {
+    if (N < 0 || B <= 0 || K <= 0 || (NX != 4 && NX != 20) || max_row < 0) return FACE_ERR_ARG;
+    if (ld_phi < B || ld_msg < K || ld_Y < NX || (!row_ptr && M < 0)) return FACE_ERR_ARG;
+    if ((dphi && ld_dphi < B) || (dmsg && ld_dmsg < K) || (dY && ld_dY < NX)) return FACE_ERR_ARG;
+    if (N == 0 || max_row == 0) return 0;
+    if (!phi || !msg || !Y || !G) return FACE_ERR_ARG;
+    int ks = 8, glog = 2, nthr = 128;
+    if (!plan_bwd(K, max_row, ks, glog, nthr)) return FACE_ERR_UNSUPPORTED;
+    hipStream_t st = (hipStream_t)stream;
+    if (NX == 20)
+        return launch_bwd_nx<20>(B, ks, glog, nthr, N, st, phi, ld_phi, msg, ld_msg, msg_row, Y, ld_Y, row_ptr, M, K,
+                                 G, dphi, ld_dphi, dmsg, ld_dmsg, dY, ld_dY);
+    return launch_bwd_nx<4>(B, ks, glog, nthr, N, st, phi, ld_phi, msg, ld_msg, msg_row, Y, ld_Y, row_ptr, M, K, G,
+                            dphi, ld_dphi, dmsg, ld_dmsg, dY, ld_dY);
+}
+
+extern "C" int face_cp_density_fwd(const float* R, int32_t ld_R, const float* msg, int32_t ld_msg,
+                                   const int32_t* msg_row, const float* Y, int32_t ld_Y, const int32_t* row_ptr,
+                                   int64_t N, int32_t M, int32_t C, float* A, void* stream) {
+    if (N < 0 || C <= 0 || ld_R < 4 * C || ld_msg < C || ld_Y < 20 || (!row_ptr && M < 0)) return FACE_ERR_ARG;
+    if (N == 0) return 0;
+    if (!R || !msg || !Y || !A) return FACE_ERR_ARG;
+    int nthr = ((C + kWave - 1) / kWave) * kWave;
+    if (nthr > kBlock) nthr = kBlock;
+    dim3 grid((unsigned)N, (unsigned)((C + nthr - 1) / nthr));
+    hipLaunchKernelGGL(cp_density_fwd_kernel, grid, dim3(nthr), 0, (hipStream_t)stream, R, ld_R, msg, ld_msg, msg_row,
+                       Y, ld_Y, row_ptr, M, C, A);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int face_cp_density_bwd(const float* R, int32_t ld_R, const float* msg, int32_t ld_msg,
+                                   const int32_t* msg_row, const float* Y, int32_t ld_Y, const int32_t* row_ptr,
+                                   int64_t N, int32_t M, int32_t max_row, int32_t C, const float* gA, float* dR,
+                                   int32_t ld_dR, float* dmsg, int32_t ld_dmsg, float* dY, int32_t ld_dY,
+                                   void* stream) {
+    if (N < 0 || C <= 0 || C > kBlock || ld_R < 4 * C || ld_msg < C || ld_Y < 20 || (!row_ptr && M < 0))
+        return FACE_ERR_ARG;
+    if ((dR && ld_dR < 4 * C) || (dmsg && ld_dmsg < C) || (dY && ld_dY < 20)) return FACE_ERR_ARG;
+    if (N == 0 || max_row == 0) return 0;
+    if (!R || !msg || !Y || !gA) return FACE_ERR_ARG;
+    const int nthr = ((C + kWave - 1) / kWave) * kWave;
+    const size_t lds = ((size_t)(20 + kTileCPB * 4) * (C + 1) + kTileCPB * 20) * sizeof(float);
+    if ((int64_t)lds > 65536) return FACE_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL(cp_density_bwd_kernel, dim3((unsigned)N), dim3(nthr), lds, (hipStream_t)stream, R, ld_R, msg,
+                       ld_msg, msg_row, Y, ld_Y, row_ptr, M, C, gA, dR, ld_dR, dmsg, ld_dmsg, dY, ld_dY);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}

@@ -1,0 +1,252 @@
+// Edge front-end (geometry, Bessel basis, envelope, monomials), row gathers and the
+// atomic-free scatters that replace autograd's index_add (gfx950).
+//
+// Forward follows face/model.py:670-677 and :28-40, face/cartesian.py:34-46. The backward
+// scatters use the reverse-edge map of a symmetric pair list: the edges whose neighbour is
+// atom k are exactly the reverses of row k, so every scatter becomes a row reduction.
+#include "common.h"
+
+namespace face {
+
+__device__ __forceinline__ void monomials20(float x, float y, float z, float* Y) {
+    Y[0] = 1.f;
+    Y[1] = x; Y[2] = y; Y[3] = z;
+    Y[4] = x * x; Y[5] = y * y; Y[6] = z * z; Y[7] = x * y; Y[8] = x * z; Y[9] = y * z;
+    Y[10] = x * x * x; Y[11] = y * y * y; Y[12] = z * z * z; Y[13] = x * x * y; Y[14] = x * x * z;
+    Y[15] = x * y * y; Y[16] = y * y * z; Y[17] = x * z * z; Y[18] = y * z * z; Y[19] = x * y * z;
+}
+
+struct EdgeGeom {
+    float v[3], r, u[3], x;
+    bool valid;
+};
+
+__device__ __forceinline__ EdgeGeom edge_geom(const float* __restrict__ pos, const int32_t* __restrict__ recv,
+                                              const int32_t* __restrict__ col, const float* __restrict__ shift,
+                                              const uint8_t* __restrict__ mask, int64_t e, float rc) {
+    EdgeGeom g;
+    const int64_t i = recv[e], j = col[e];
+#pragma unroll
+    for (int a = 0; a < 3; ++a) g.v[a] = (pos[j * 3 + a] - pos[i * 3 + a]) + shift[e * 3 + a];
+    g.valid = mask ? mask[e] != 0 : true;
+    const float r2 = g.v[0] * g.v[0] + g.v[1] * g.v[1] + g.v[2] * g.v[2];
+    g.r = sqrtf(g.valid ? r2 : 1.f);
+#pragma unroll
+    for (int a = 0; a < 3; ++a) g.u[a] = g.v[a] / g.r;
+    g.x = g.r / rc;
+    return g;
+}
+
+// envelope 1 - 28 x^6 + 48 x^7 - 21 x^8 (p = 6), zero at and beyond x = 1 and on masked edges
+__device__ __forceinline__ float envelope(const EdgeGeom& g) {
+    if (!g.valid || !(g.x < 1.f)) return 0.f;
+    const float x2 = g.x * g.x, x6 = x2 * x2 * x2;
+    return 1.f - 28.f * x6 + 48.f * x6 * g.x - 21.f * x6 * x2;
+}
+__device__ __forceinline__ float envelope_dr(const EdgeGeom& g, float rc) {
+    if (!g.valid || !(g.x < 1.f)) return 0.f;
+    const float x = g.x, x2 = x * x, x5 = x2 * x2 * x;
+    return (-168.f * x5 + 336.f * x5 * x - 168.f * x5 * x2) / rc;
+}
+
+__global__ __launch_bounds__(256) void edge_geom_fwd_kernel(const float* __restrict__ pos,
+                                                            const int32_t* __restrict__ recv,
+                                                            const int32_t* __restrict__ col,
+                                                            const float* __restrict__ shift,
+                                                            const uint8_t* __restrict__ mask, int64_t E,
+                                                            const float* __restrict__ freq, int nb, float rc,
+                                                            float bes_scale, float* __restrict__ Y,
+                                                            float* __restrict__ rb, float* __restrict__ env,
+                                                            float* __restrict__ rout) {
+    const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    const EdgeGeom g = edge_geom(pos, recv, col, shift, mask, e, rc);
+    float y[20];
+    monomials20(g.u[0], g.u[1], g.u[2], y);
+#pragma unroll
+    for (int x = 0; x < 20; ++x) Y[e * 20 + x] = y[x];
+    const float ev = envelope(g);
+    if (env) env[e] = ev;
+    if (rout) rout[e] = g.r;
+    if (rb) {
+        for (int n = 0; n < nb; ++n) rb[e * nb + n] = sinf(freq[n] * g.r) / g.r * bes_scale * ev;
+    }
+}
+
+__global__ __launch_bounds__(256) void edge_geom_bwd_kernel(
+    const float* __restrict__ pos, const int32_t* __restrict__ recv, const int32_t* __restrict__ col,
+    const float* __restrict__ shift, const uint8_t* __restrict__ mask, int64_t E, const float* __restrict__ freq,
+    int nb, float rc, float bes_scale, const float* __restrict__ gY, const float* __restrict__ grb,
+    const float* __restrict__ genv, const float* __restrict__ gr, float* __restrict__ gvec) {
+    const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    const EdgeGeom g = edge_geom(pos, recv, col, shift, mask, e, rc);
+    // d/du of the monomials contracted with gY
+    float gu[3] = {0.f, 0.f, 0.f};
+    if (gY) {
+        const float* q = gY + e * 20;
+        const float x = g.u[0], y = g.u[1], z = g.u[2];
+        gu[0] = q[1] + 2.f * x * q[4] + y * q[7] + z * q[8] + 3.f * x * x * q[10] + 2.f * x * y * q[13] +
+                2.f * x * z * q[14] + y * y * q[15] + z * z * q[17] + y * z * q[19];
+        gu[1] = q[2] + 2.f * y * q[5] + x * q[7] + z * q[9] + 3.f * y * y * q[11] + x * x * q[13] +
+                2.f * x * y * q[15] + 2.f * y * z * q[16] + z * z * q[18] + x * z * q[19];
+        gu[2] = q[3] + 2.f * z * q[6] + x * q[8] + y * q[9] + 3.f * z * z * q[12] + x * x * q[14] +
+                y * y * q[16] + 2.f * x * z * q[17] + 2.f * y * z * q[18] + x * y * q[19];
+    }
+    float out[3];
+    if (g.valid) {
+        const float ev = envelope(g);
+        float genv_t = genv ? genv[e] : 0.f;
+        float g_r = gr ? gr[e] : 0.f;
+        if (grb) {
+            const float inv_r = 1.f / g.r;
+            for (int n = 0; n < nb; ++n) {
+                const float fr = freq[n] * g.r;
+                const float s = sinf(fr), c = cosf(fr);
+                const float bes = s * inv_r * bes_scale;
+                const float dbes = bes_scale * (freq[n] * c * inv_r - s * inv_r * inv_r);
+                const float q = grb[e * nb + n];
+                genv_t = fmaf(q, bes, genv_t);
+                g_r = fmaf(q * ev, dbes, g_r);
+            }
+        }
+        g_r = fmaf(genv_t, envelope_dr(g, rc), g_r);
+        const float gdotu = gu[0] * g.u[0] + gu[1] * g.u[1] + gu[2] * g.u[2];
+#pragma unroll
+        for (int a = 0; a < 3; ++a) out[a] = (gu[a] - gdotu * g.u[a]) / g.r + g_r * g.u[a];
+    } else {
+#pragma unroll
+        for (int a = 0; a < 3; ++a) out[a] = gu[a];   // r := 1 is a constant on masked slots
+    }
+#pragma unroll
+    for (int a = 0; a < 3; ++a) gvec[e * 3 + a] = out[a];
+}
+
+__global__ __launch_bounds__(256) void gather_rows_kernel(const float* __restrict__ X, int ld_X,
+                                                          const int32_t* __restrict__ idx, int64_t E, int F,
+                                                          float* __restrict__ out, int ld_out) {
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (t >= E * F) return;
+    const int64_t e = t / F;
+    const int f = (int)(t - e * F);
+    out[e * ld_out + f] = X[(int64_t)idx[e] * ld_X + f];
+}
+
+// dX[k, f] = sum_{e in row k} g[rev[e], f]; thread = (k, f), row walked in order.
+__global__ __launch_bounds__(256) void gather_rows_bwd_kernel(const float* __restrict__ g, int ld_g,
+                                                              const int32_t* __restrict__ row_ptr,
+                                                              const int32_t* __restrict__ rev, int64_t N, int F,
+                                                              float* __restrict__ dX, int ld_dX) {
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (t >= N * F) return;
+    const int64_t k = t / F;
+    const int f = (int)(t - k * F);
+    float s = 0.f;
+    for (int64_t e = row_ptr[k]; e < row_ptr[k + 1]; ++e) s += g[(int64_t)rev[e] * ld_g + f];
+    dX[k * ld_dX + f] = s;
+}
+
+__global__ __launch_bounds__(256) void segment_sum_kernel(const float* __restrict__ g, int ld_g,
+                                                          const int32_t* __restrict__ row_ptr, int64_t N, int F,
+                                                          float* __restrict__ out, int ld_out) {
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (t >= N * F) return;
+    const int64_t k = t / F;
+    const int f = (int)(t - k * F);
+    float s = 0.f;
+    for (int64_t e = row_ptr[k]; e < row_ptr[k + 1]; ++e) s += g[e * ld_g + f];
+    out[k * ld_out + f] = s;
+}
+
+__global__ __launch_bounds__(256) void force_scatter_kernel(const float* __restrict__ gvec,
+                                                            const int32_t* __restrict__ row_ptr,
+                                                            const int32_t* __restrict__ rev, int64_t N, float sign,
+                                                            float* __restrict__ grad) {
+    const int64_t k = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (k >= N) return;
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f;
+    for (int64_t e = row_ptr[k]; e < row_ptr[k + 1]; ++e) {
+        const int64_t r = rev[e];
+        s0 += gvec[r * 3 + 0] - gvec[e * 3 + 0];
+        s1 += gvec[r * 3 + 1] - gvec[e * 3 + 1];
+        s2 += gvec[r * 3 + 2] - gvec[e * 3 + 2];
+    }
+    grad[k * 3 + 0] = sign * s0;
+    grad[k * 3 + 1] = sign * s1;
+    grad[k * 3 + 2] = sign * s2;
+}
+
+static unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
+
+}  // namespace face
+
+using namespace face;
+
+extern "C" int face_edge_geom_fwd(const float* pos, const int32_t* recv, const int32_t* col, const float* shift,
+                                  const uint8_t* mask, int64_t E, const float* freq, int32_t n_basis, float rc,
+                                  float bes_scale, float* Y, float* rb, float* env, float* r, void* stream) {
+    if (E < 0 || n_basis < 0 || !(rc > 0.f) || (rb && (!freq || n_basis == 0))) return FACE_ERR_ARG;
+    if (E == 0) return 0;
+    if (!pos || !recv || !col || !shift || !Y) return FACE_ERR_ARG;
+    hipLaunchKernelGGL(edge_geom_fwd_kernel, dim3(blocks_for(E)), dim3(256), 0, (hipStream_t)stream, pos, recv, col,
+                       shift, mask, E, freq, n_basis, rc, bes_scale, Y, rb, env, r);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int face_edge_geom_bwd(const float* pos, const int32_t* recv, const int32_t* col, const float* shift,
+                                  const uint8_t* mask, int64_t E, const float* freq, int32_t n_basis, float rc,
+                                  float bes_scale, const float* gY, const float* grb, const float* genv,
+                                  const float* gr, float* gvec, void* stream) {
+    if (E < 0 || n_basis < 0 || !(rc > 0.f) || (grb && (!freq || n_basis == 0))) return FACE_ERR_ARG;
+    if (E == 0) return 0;
+    if (!pos || !recv || !col || !shift || !gvec) return FACE_ERR_ARG;
+    hipLaunchKernelGGL(edge_geom_bwd_kernel, dim3(blocks_for(E)), dim3(256), 0, (hipStream_t)stream, pos, recv, col,
+                       shift, mask, E, freq, n_basis, rc, bes_scale, gY, grb, genv, gr, gvec);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int face_gather_rows(const float* X, int32_t ld_X, const int32_t* idx, int64_t E, int32_t F, float* out,
+                                int32_t ld_out, void* stream) {
+    if (E < 0 || F < 0 || ld_X < F || ld_out < F) return FACE_ERR_ARG;
+    if (E == 0 || F == 0) return 0;
+    if (!X || !idx || !out) return FACE_ERR_ARG;
+    hipLaunchKernelGGL(gather_rows_kernel, dim3(blocks_for(E * F)), dim3(256), 0, (hipStream_t)stream, X, ld_X, idx,
+                       E, F, out, ld_out);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int face_gather_rows_bwd(const float* g, int32_t ld_g, const int32_t* row_ptr, const int32_t* rev,
+                                    int64_t N, int32_t F, float* dX, int32_t ld_dX, void* stream) {
+    if (N < 0 || F < 0 || ld_g < F || ld_dX < F) return FACE_ERR_ARG;
+    if (N == 0 || F == 0) return 0;
+    if (!g || !row_ptr || !rev || !dX) return FACE_ERR_ARG;
+    hipLaunchKernelGGL(gather_rows_bwd_kernel, dim3(blocks_for(N * F)), dim3(256), 0, (hipStream_t)stream, g, ld_g,
+                       row_ptr, rev, N, F, dX, ld_dX);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int face_segment_sum(const float* g, int32_t ld_g, const int32_t* row_ptr, int64_t N, int32_t F,
+                                float* out, int32_t ld_out, void* stream) {
+    if (N < 0 || F < 0 || ld_g < F || ld_out < F) return FACE_ERR_ARG;
+    if (N == 0 || F == 0) return 0;
+    if (!g || !row_ptr || !out) return FACE_ERR_ARG;
+    hipLaunchKernelGGL(segment_sum_kernel, dim3(blocks_for(N * F)), dim3(256), 0, (hipStream_t)stream, g, ld_g,
+                       row_ptr, N, F, out, ld_out);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int face_force_scatter(const float* gvec, const int32_t* row_ptr, const int32_t* rev, int64_t N,
+                                  float sign, float* grad, void* stream) {
+    if (N < 0) return FACE_ERR_ARG;
+    if (N == 0) return 0;
+    if (!gvec || !row_ptr || !rev || !grad) return FACE_ERR_ARG;
+    hipLaunchKernelGGL(force_scatter_kernel, dim3(blocks_for(N)), dim3(256), 0, (hipStream_t)stream, gvec, row_ptr,
+                       rev, N, sign, grad);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}

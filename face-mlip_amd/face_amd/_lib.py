@@ -1,0 +1,135 @@
+"""ctypes binding of libface_hip.so (the C-ABI declared in include/face_hip.h).
+
+The library is loaded once, lazily; a missing or unloadable library raises at the first call
+(there is no fallback path). Every entry point returns an int status that is turned into a
+RuntimeError carrying face_hip_error_string().
+"""
+import ctypes
+import os
+import threading
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.environ.get("FACE_HIP_LIB", os.path.join(_HERE, "libface_hip.so"))
+_lib = None
+_lock = threading.Lock()
+
+P = ctypes.c_void_p
+I32 = ctypes.c_int32
+I64 = ctypes.c_int64
+F32 = ctypes.c_float
+F64 = ctypes.c_double
+
+_SIGS = {
+    "face_hip_error_string": (ctypes.c_char_p, [ctypes.c_int]),
+    "face_hip_abi_version": (ctypes.c_int, []),
+    "face_density_fwd": (ctypes.c_int, [P, I32, P, I32, P, P, I32, I32, P, I64, I32, I32, I32, P, P]),
+    "face_density_bwd": (ctypes.c_int, [P, I32, P, I32, P, P, I32, I32, P, I64, I32, I32, I32, I32, P, P, I32, P,
+                                        I32, P, I32, P]),
+    "face_cp_density_fwd": (ctypes.c_int, [P, I32, P, I32, P, P, I32, P, I64, I32, I32, P, P]),
+    "face_cp_density_bwd": (ctypes.c_int, [P, I32, P, I32, P, P, I32, P, I64, I32, I32, I32, P, P, I32, P, I32, P,
+                                           I32, P]),
+    "face_node_fwd": (ctypes.c_int, [P, P, P, P, P, P, P, P, P, P, I32, I64, I32, I32, P]),
+    "face_node_bwd": (ctypes.c_int, [P, P, P, P, P, P, P, P, P, P, I32, P, P, P, P, I64, I32, I32, P]),
+    "face_nbr_bin": (ctypes.c_int, [P, I64, P, P, P, P, P, P, P, P, P]),
+    "face_nbr_count": (ctypes.c_int, [P, I64, P, P, P, P, P, F64, P, P, P, P, P, P, P]),
+    "face_nbr_fill": (ctypes.c_int, [P, I64, P, P, P, P, P, F64, P, P, P, P, P, P, P, P, P, P, P, P]),
+    "face_nbr_rev": (ctypes.c_int, [P, P, P, I64, P, P, P]),
+    "face_nbr_rev_shift": (ctypes.c_int, [P, P, P, I64, P, P, P]),
+    "face_nbr_padded": (ctypes.c_int, [P, P, P, P, P, I64, I32, P, P, P, P]),
+    "face_edge_geom_fwd": (ctypes.c_int, [P, P, P, P, P, I64, P, I32, F32, F32, P, P, P, P, P]),
+    "face_edge_geom_bwd": (ctypes.c_int, [P, P, P, P, P, I64, P, I32, F32, F32, P, P, P, P, P, P]),
+    "face_gather_rows": (ctypes.c_int, [P, I32, P, I64, I32, P, I32, P]),
+    "face_gather_rows_bwd": (ctypes.c_int, [P, I32, P, P, I64, I32, P, I32, P]),
+    "face_segment_sum": (ctypes.c_int, [P, I32, P, I64, I32, P, I32, P]),
+    "face_force_scatter": (ctypes.c_int, [P, P, P, I64, F32, P, P]),
+}
+
+ABI_VERSION = 1
+
+
+def lib():
+    """The loaded library (loads on first use; raises if it is missing)."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not os.path.exists(LIB_PATH):
+                    raise RuntimeError(f"libface_hip.so not found at {LIB_PATH}: build it with "
+                                       f"`python face-mlip_amd/csrc/build.py` (or __graft_entry__.build())")
+                L = ctypes.CDLL(LIB_PATH)
+                for name, (res, args) in _SIGS.items():
+                    fn = getattr(L, name)
+                    fn.restype = res
+                    fn.argtypes = args
+                if L.face_hip_abi_version() != ABI_VERSION:
+                    raise RuntimeError("libface_hip.so ABI version mismatch: rebuild it")
+                _lib = L
+    return _lib
+
+
+def exported_symbols():
+    return list(_SIGS)
+
+
+# Optional per-entry-point launch timing: {name: [(start_event, end_event), ...]}; events are
+# recorded on torch's current stream, the stream every entry point is launched on.
+_timing = None
+
+
+def time_calls(names):
+    """Start recording HIP events around every call of the given entry points."""
+    global _timing
+    _timing = {n: [] for n in names}
+    return _timing
+
+
+def stop_timing():
+    global _timing
+    t, _timing = _timing, None
+    return t
+
+
+def call(name, *args, label=None):
+    """Call entry point `name`; raise RuntimeError on a non-zero status. `label` names the
+    launch for time_calls (defaults to the entry-point name)."""
+    fn = getattr(lib(), name)
+    key = label or name
+    if _timing is not None and key in _timing:
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        code = fn(*args)
+        e.record()
+        _timing[key].append((s, e))
+    else:
+        code = fn(*args)
+    if code != 0:
+        msg = lib().face_hip_error_string(code).decode()
+        raise RuntimeError(f"{name} failed: {msg} (code {code})")
+
+
+def ptr(t):
+    """Device pointer of a tensor (or None -> NULL)."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t=None):
+    """Raw HIP stream handle of torch's current stream on the tensor's device."""
+    dev = t.device if t is not None else torch.device("cuda")
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def require_gpu(*ts):
+    for t in ts:
+        if t is not None and (not t.is_cuda):
+            raise RuntimeError("face_amd kernels need tensors on a HIP device (got "
+                               f"{t.device}); there is no CPU path")
+
+
+def ptr_array(ts):
+    return (P * len(ts))(*[ptr(t) for t in ts])
+
+
+def i64_array(vals):
+    return (I64 * len(vals))(*vals)

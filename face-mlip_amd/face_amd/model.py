@@ -1,0 +1,327 @@
+"""FACE energy + forces on the MI355X path (host mirror of face/model.py).
+
+The module tree, parameter names and construction order are those of the reference's
+FACE with factorised passes (face/model.py:99-158, :431-458, :559-590), so
+torch.manual_seed(s) + FACE(...) gives the reference's random-init weights and
+reference state_dicts load unchanged. The forward differs in layout and in where the work
+runs:
+
+  * edges are a receiver-grouped CSR list (no padded slots); geometry, basis, envelope and
+    monomials come from one HIP kernel whose backward also performs the force scatter
+    through the reverse-edge map (no atomics);
+  * the factor density (face/kernels.py), the CP pooling (face/model.py:496-502) and the
+    transport sums (face/model.py:515-522, the same contraction with 4 monomials) run in
+    the segmented HIP density kernels, reading gathered neighbour tables in place;
+  * moments are kept channel-last (N, k_l, C), so `mix`, `proj` and the readout are plain
+    row-major GEMMs, and the node kernel reads P/Q/S straight out of the projection output
+    and writes the invariant families straight into the readout row;
+  * only the projection columns the algebra uses are computed (P0 of rank 0; P3, Q3 of rank 3).
+
+Supported configuration: factor=True (cp on or off), transport/eqmsg on or off, n_passes >= 1,
+norm="layer", terms=(), training toggles at their defaults; first-order forces
+(create_graph=False), which is what the reference's fused kernels support (face/kernels.py:10-11).
+"""
+import math
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import ops
+from .neighbors import graph_from_padded
+from .ops import Graph
+
+RANKS = [(0, 1), (1, 4), (4, 10), (10, 20)]   # monomial range of each rank (face/cartesian.py:18)
+Y2_W = (1.0, 1.0, 1.0, 2.0, 2.0, 2.0)        # u^T M u weights in sym storage (face/cartesian.py:81)
+
+
+def transport_map():
+    """(36 = bond monomial p*9 + table component q, 18) map of the transport sums.
+
+    Columns: [sum phi V (3) | sum phi M u (3) | sum phi M (6) | sum phi sym(u (x) V) (6)],
+    q = [V_x V_y V_z | M_xx M_yy M_zz M_xy M_xz M_yz], p = [1, u_x, u_y, u_z]
+    (the map of face/model.py:342-362, derived here from those definitions).
+    """
+    pairs = [(0, 0), (1, 1), (2, 2), (0, 1), (0, 2), (1, 2)]
+    comp = {}
+    for k, (a, b) in enumerate(pairs):
+        comp[(a, b)] = comp[(b, a)] = k
+    T = torch.zeros(36, 18, dtype=torch.float64)
+    for a in range(3):
+        T[0 * 9 + a, a] = 1.0                                  # V_a
+        for c in range(3):
+            T[(c + 1) * 9 + 3 + comp[(a, c)], 3 + a] += 1.0     # M_ac u_c
+    for k, (a, b) in enumerate(pairs):
+        T[3 + k, 6 + k] = 1.0                                  # M_k
+        T[(a + 1) * 9 + b, 12 + k] += 0.5                      # (u_a V_b + u_b V_a) / 2
+        T[(b + 1) * 9 + a, 12 + k] += 0.5
+    return T
+
+
+class BesselEnvelope(nn.Module):
+    """Radial basis constants (face/model.py:28-40); evaluated inside the edge kernel."""
+
+    def __init__(self, n, rc, p=6):
+        super().__init__()
+        if p != 6:
+            raise NotImplementedError("the edge kernel implements the p = 6 envelope")
+        self.rc, self.p = rc, p
+        self.register_buffer("freq", torch.arange(1, n + 1) * math.pi / rc)
+
+
+class UnitLinear(nn.Module):
+    """Unit-variance stored weight with forward factor fan_in**-0.5 (face/model.py:43-55)."""
+
+    def __init__(self, fan_in, fan_out, bias=True):
+        super().__init__()
+        self.weight = nn.Parameter(torch.randn(fan_out, fan_in))
+        self.bias = nn.Parameter(torch.zeros(fan_out)) if bias else None
+        self.alpha = fan_in ** -0.5
+
+    def forward(self, x):
+        return F.linear(x, self.weight * self.alpha, self.bias)
+
+
+def unit_parameterise(module):
+    """Swap every nn.Linear for an equal-at-init UnitLinear, in place (face/model.py:58-70)."""
+    for name, child in list(module.named_children()):
+        if isinstance(child, nn.Linear):
+            u = UnitLinear(child.in_features, child.out_features, child.bias is not None).to(child.weight)
+            with torch.no_grad():
+                u.weight.copy_(child.weight / u.alpha)
+                if child.bias is not None:
+                    u.bias.copy_(child.bias)
+            setattr(module, name, u)
+        else:
+            unit_parameterise(child)
+    return module
+
+
+def weight(mod):
+    """Effective (weight, bias) of an nn.Linear or UnitLinear."""
+    if isinstance(mod, UnitLinear):
+        return mod.weight * mod.alpha, mod.bias
+    return mod.weight, mod.bias
+
+
+def mlp(sizes):
+    layers = []
+    for a, b in zip(sizes[:-1], sizes[1:]):
+        layers += [nn.Linear(a, b), nn.SiLU()]
+    return nn.Sequential(*layers[:-1])
+
+
+def run_mlp(seq, x):
+    for m in seq:
+        x = m(x)
+    return x
+
+
+class FactorBlock(nn.Module):
+    """One factorised interaction pass; registrations follow MomentBlock then FactorBlock."""
+    N_INV = 9
+
+    def __init__(self, C, n_basis, n_sets, radial_hidden=64, n_elem=10, K_dir=16, norm="layer", transport=False,
+                 eq_in=False, eq_out=False, B=16, K=32, cp=False):
+        super().__init__()
+        self.C, self.n_elem, self.K = C, n_elem, K_dir
+        self.eq_in, self.eq_out = eq_in, eq_out
+        self.pqs_gate = nn.Embedding(n_elem, 4 * 3 * C)
+        nn.init.ones_(self.pqs_gate.weight)
+        self.register_buffer("mom_scale", torch.ones(4))
+        self.register_buffer("eq_scale", torch.ones(2))
+        self.register_buffer("inv_scale", torch.ones(self.N_INV))
+        self.register_buffer("calibrated", torch.tensor(False))
+        self.rad_in = nn.Linear(n_basis, radial_hidden)
+        self.pair = nn.Embedding(n_elem * n_elem, radial_hidden)
+        nn.init.zeros_(self.pair.weight)
+        self.directional = n_sets > 1
+        self.transport = transport and self.directional
+        self.radial = mlp([radial_hidden, radial_hidden, (8 if self.transport else 4) * C])
+        cin = C * n_sets
+        self.proj = nn.ModuleList([nn.Linear(cin, 3 * C, bias=False) for _ in range(4)])
+        self.elem_scale = nn.Embedding(n_elem, 4 * C)
+        nn.init.ones_(self.elem_scale.weight)
+        self.out = mlp([self.N_INV * C + C + 4, 2 * C, 2 * C, C + 1])
+        if norm != "layer":
+            raise NotImplementedError("norm='layer' only")
+        self.norm = nn.LayerNorm(self.N_INV * C)
+        if self.directional:
+            cprev = C if eq_in else C * (n_sets - 1)
+            self.pv = nn.Linear(cprev, K_dir, bias=False)
+            self.pm = nn.Linear(cprev, K_dir, bias=False)
+            self.dir_mix = nn.Linear(4 * K_dir, C)
+        if self.transport:
+            self.tv = nn.Linear(cprev, C, bias=False)
+            self.tm = nn.Linear(cprev, C, bias=False)
+        if eq_out:
+            self.vpath = nn.Parameter(torch.ones(4, C))
+            self.mpath = nn.Parameter(torch.ones(4, C))
+            self.gate = nn.Linear(self.N_INV * C, 2 * C)
+            nn.init.zeros_(self.gate.weight)
+            nn.init.ones_(self.gate.bias)
+        # factorised pass
+        self.cp = cp
+        if cp:
+            K = C
+        self.B, self.Km = B, K
+        self.radial = mlp([radial_hidden, radial_hidden, B + (4 * C if cp else 0)])
+        self.msg = nn.Linear(C, K)
+        self.mix = nn.ModuleList([nn.Linear(C if cp else B * K, C, bias=False) for _ in range(4)])
+        if self.directional:
+            self.dir_mix = nn.Linear(4 * K_dir, K)
+            nt = 2 if self.transport else 1
+            del self.pv, self.pm
+            self.pvt = nn.Linear(cprev, nt * K_dir, bias=False)
+            self.pmt = nn.Linear(cprev, nt * K_dir, bias=False)
+        if self.transport:
+            del self.tv, self.tm
+            self.tmix1 = nn.Linear(B * 2 * K_dir, C, bias=False)
+            self.tmix2 = nn.Linear(B * 2 * K_dir, C, bias=False)
+            self.tmix3 = nn.Linear(B * 2 * K_dir, C, bias=False)
+
+    # ------------------------------------------------------------------ moments
+    def moments(self, h, rb, Y, env, zp, zidx, avg_nb, sets, eq, g, tmap):
+        N, E = g.N, g.E
+        B, C, Kd = self.B, self.C, self.K
+        hid = F.silu(self.rad_in(rb) + self.pair.weight[zp])
+        phi_all = run_mlp(self.radial, hid) * env[:, None]                       # (E, B [+4C])
+        phi = phi_all[:, :B]
+        msg_n = self.msg(h)                                                      # (N, K)
+        if self.directional:
+            if self.eq_in:
+                src1, src2 = eq
+            else:
+                src1 = torch.cat([S[1] for S in sets], -1)
+                src2 = torch.cat([S[2] for S in sets], -1)
+            Vb = self.pvt(src1)                                                  # (N, 3, nt*Kd)
+            Mb = self.pmt(src2)                                                  # (N, 6, nt*Kd)
+            T = torch.cat([Vb[..., :Kd], Mb[..., :Kd]], 1).reshape(N, 9 * Kd)    # [component][kd]
+            Tj = ops.gather_neighbour(T, g).view(E, 9, Kd)
+            Ti = ops.gather_receiver(T, g).view(E, 9, Kd)
+            u = Y[:, 1:4]
+            Y2 = Y[:, 4:10] * Y.new_tensor(Y2_W)
+            d = torch.cat([torch.einsum("ea,eak->ek", u, Tj[:, :3]), torch.einsum("ea,eak->ek", Y2, Tj[:, 3:]),
+                           torch.einsum("ea,eak->ek", u, Ti[:, :3]), torch.einsum("ea,eak->ek", Y2, Ti[:, 3:])], -1)
+            mj, gathered = ops.gather_neighbour(msg_n, g) + self.dir_mix(d), False
+        else:
+            mj, gathered = msg_n, True
+        s = self.elem_scale(zidx).view(N, 4, C) / avg_nb
+        if self.cp:
+            Af = ops.cp_density(phi_all[:, B:], mj, Y, g, gathered)                # (N, 20, C)
+        else:
+            Af = ops.density(phi, mj, Y, g, 20, gathered)                         # (N, 20, B*K)
+        A = [self.mix[l](Af[:, a:b]) * s[:, l, None, :] for l, (a, b) in enumerate(RANKS)]   # (N, k_l, C)
+        if self.transport:
+            table = torch.cat([Vb[..., Kd:], Mb[..., Kd:]], 1).transpose(1, 2).reshape(N, Kd * 9)
+            St = ops.density(phi, table, Y, g, 4, True)                           # (N, 4, B*9Kd)
+            X = St.view(N, 4, B, Kd, 9).permute(0, 2, 3, 1, 4).reshape(N, B, Kd, 36) / avg_nb
+            D = X @ tmap                                                          # (N, B, Kd, 18)
+            D1 = D[..., :6].reshape(N, B, Kd, 2, 3).permute(0, 4, 1, 3, 2).reshape(N, 3, B * 2 * Kd)
+            D2 = D[..., 6:18].reshape(N, B, Kd, 2, 6).permute(0, 4, 1, 3, 2).reshape(N, 6, B * 2 * Kd)
+            A[1] = A[1] + self.tmix1(D1) * (s[:, 1, None, :] * avg_nb)
+            A[2] = A[2] + self.tmix2(D2) * (s[:, 2, None, :] * avg_nb)
+        return A
+
+    # ------------------------------------------------------------------ invariants + readout
+    def forward(self, h, rb, Y, env, zp, zidx, avg_nb, sets, eq, g, tmap):
+        C = self.C
+        A = self.moments(h, rb, Y, env, zp, zidx, avg_nb, sets, eq, g, tmap)
+        allsets = sets + [A]
+        ys = []
+        for l in range(4):
+            x = torch.cat([S[l] for S in allsets], -1)                            # (N, k_l, cin)
+            W, _ = weight(self.proj[l])
+            if l == 0:
+                W = W[:C]                                                         # only P0 is used
+            elif l == 3:
+                W = W[:2 * C]                                                     # S3 is unused
+            ys.append(F.linear(x, W))
+        if self.eq_out:
+            feats, V, Ms = ops.node_features(ys[0], ys[1], ys[2], ys[3], self.vpath, self.mpath, True, C)
+        else:
+            feats, V, Ms = ops.node_features(ys[0], ys[1], ys[2], ys[3], None, None, False, C)
+        inv = self.norm(feats)
+        W0, b0 = weight(self.out[0])
+        z = F.linear(torch.cat([inv, h], 1), W0[:, :-4], b0)   # the 4 trailing inputs are zeros
+        o = run_mlp(self.out[2:], F.silu(z))
+        eq_new = None
+        if self.eq_out:
+            gv, gm = self.gate(inv).chunk(2, dim=-1)
+            eq_new = (V * gv[:, None, :], Ms * gm[:, None, :])
+        return o[:, :1], h + o[:, 1:], A, eq_new
+
+
+class FACE(nn.Module):
+    """face/model.py:558-590 (factor=True, terms=()), forward on the HIP path."""
+
+    def __init__(self, elements, C=64, n_basis=8, rc=5.0, n_passes=2, terms=(), radial_hidden=64, K_dir=16,
+                 norm="layer", transport=False, eqmsg=False, factor=True, B=16, K=32, cp=False):
+        super().__init__()
+        if not factor:
+            raise NotImplementedError("the MI355X path serves factorised models (factor=True)")
+        if terms:
+            raise NotImplementedError("physics terms are outside the accelerated path")
+        self.rc, self.C = rc, C
+        zmap = torch.full((119,), -1, dtype=torch.long)
+        for k, z in enumerate(elements):
+            zmap[z] = k
+        self.register_buffer("zmap", zmap)
+        n_el = len(elements)
+        self.basis = BesselEnvelope(n_basis, rc)
+        self.embed = nn.Embedding(n_el, C)
+        self.blocks = nn.ModuleList([FactorBlock(C, n_basis, t + 1, radial_hidden, n_el, K_dir, norm, transport,
+                                                 eq_in=eqmsg and t > 0, eq_out=eqmsg and t < n_passes - 1,
+                                                 B=B, K=K, cp=cp) for t in range(n_passes)])
+        self.register_buffer("E0", torch.zeros(n_el))
+        self.register_buffer("scale", torch.tensor(1.0))
+        self.register_buffer("avg_nb", torch.tensor(10.0))
+        self.terms = nn.ModuleDict()
+        self.register_buffer("tmap", transport_map().float(), persistent=False)
+        self._padded_cache = {}
+
+    def fuse(self, on=True):
+        """Kept for API compatibility (face/model.py:657-663): this path is always fused."""
+        return self
+
+    def _graph(self, g):
+        if isinstance(g, Graph):
+            return g
+        if "csr" in g:
+            gr = g["csr"]
+            return gr if gr.pos is g["pos"] else gr.with_pos(g["pos"])
+        key = (g["nbr"].data_ptr(), g["mask"].data_ptr(), g["shift"].data_ptr(), tuple(g["nbr"].shape))
+        gr = self._padded_cache.get(key)
+        if gr is None:
+            self._padded_cache.clear()
+            gr = graph_from_padded(g)
+            self._padded_cache[key] = gr
+        return gr.with_pos(g["pos"])
+
+    def forward(self, g, forces=True, create_graph=False):
+        if create_graph:
+            raise NotImplementedError("first-order forces only (inference / MD)")
+        graph = self._graph(g)
+        pos = graph.pos
+        if forces and not pos.requires_grad:
+            pos.requires_grad_(True)
+        Y, rb, env = ops.edge_geometry(pos, graph, self.basis.freq, self.rc)
+        zidx = self.zmap[graph.Z]
+        zkey = ("zp", len(self.E0))
+        zp = graph.cache.get(zkey)
+        if zp is None:
+            zp = zidx[graph.recv.long()] * len(self.E0) + zidx[graph.col.long()]
+            graph.cache[zkey] = zp
+        h = self.embed(zidx)
+        e_at = self.E0[zidx].clone()
+        sets, eq = [], None
+        for blk in self.blocks:
+            e, h, A, eq = blk(h, rb, Y, env, zp, zidx, self.avg_nb, sets, eq, graph, self.tmap)
+            sets.append(A)
+            e_at = e_at + self.scale * e.squeeze(-1)
+        E = ops.StructureSum.apply(e_at, graph.struct_ptr, graph.batch, graph.nstr)
+        out = {"energy": E, "atom_energy": e_at}
+        if forces:
+            (grad,) = torch.autograd.grad(E.sum(), pos)
+            out["forces"] = -grad
+        return out

@@ -1,0 +1,354 @@
+"""Autograd operators over the HIP kernels (CSR edge layout).
+
+Every operator here launches the kernels of libface_hip.so on torch's current stream; none
+has a torch or CPU fallback. Edge tensors are grouped by receiver atom (CSR `row_ptr`), and
+the backward of every neighbour gather is a row reduction through the reverse-edge map
+(`rev`) instead of an atomic scatter, so forces are bitwise reproducible.
+"""
+import math
+
+import torch
+
+from . import _lib
+from ._lib import call, ptr
+
+
+def _rows(t, width):
+    """(rows, >= width) fp32 view with unit column stride -> (tensor, row stride)."""
+    if t.dtype != torch.float32:
+        t = t.float()
+    if t.dim() != 2 or t.stride(1) != 1 or t.stride(0) < width:
+        t = t.contiguous()
+    return t, t.stride(0)
+
+
+class Graph:
+    """Receiver-grouped (CSR) edge list of a batch of structures on the device.
+
+    pos (N,3) fp32, Z (N,) int64, batch (N,) int64, nstr, struct_ptr (nstr+1) int32,
+    row_ptr (N+1) int32, col (E) int32 neighbour, recv (E) int32 receiver, shift (E,3) fp32,
+    rev (E) int32 reverse edge, max_row (host int), optional S (E,3) int32 image offsets.
+    """
+
+    def __init__(self, pos, Z, batch, nstr, struct_ptr, row_ptr, col, recv, shift, rev, max_row, S=None):
+        self.pos, self.Z, self.batch, self.nstr = pos, Z, batch, nstr
+        self.struct_ptr, self.row_ptr, self.col, self.recv = struct_ptr, row_ptr, col, recv
+        self.shift, self.rev, self.max_row, self.S = shift, rev, max_row, S
+        self.cache = {}
+
+    @property
+    def N(self):
+        return self.pos.shape[0]
+
+    @property
+    def E(self):
+        return self.col.shape[0]
+
+    def with_pos(self, pos):
+        g = Graph(pos, self.Z, self.batch, self.nstr, self.struct_ptr, self.row_ptr, self.col, self.recv,
+                  self.shift, self.rev, self.max_row, self.S)
+        g.cache = self.cache
+        return g
+
+
+# ----------------------------------------------------------------------------- edge geometry
+class EdgeGeometry(torch.autograd.Function):
+    """pos -> (Y (E,20), rb (E,nb), env (E)) for the edges of `graph` (face/model.py:670-677)."""
+
+    @staticmethod
+    def forward(ctx, pos, graph, freq, rc, bes_scale):
+        _lib.require_gpu(pos)
+        pos = pos.contiguous().float()
+        E, nb = graph.E, freq.numel()
+        Y = torch.empty(E, 20, device=pos.device)
+        rb = torch.empty(E, nb, device=pos.device)
+        env = torch.empty(E, device=pos.device)
+        call("face_edge_geom_fwd", ptr(pos), ptr(graph.recv), ptr(graph.col), ptr(graph.shift), None, E, ptr(freq),
+             nb, float(rc), float(bes_scale), ptr(Y), ptr(rb), ptr(env), None, _lib.stream_of(pos), label="edge_fwd")
+        ctx.save_for_backward(pos, freq)
+        ctx.graph, ctx.rc, ctx.bes_scale = graph, rc, bes_scale
+        return Y, rb, env
+
+    @staticmethod
+    def backward(ctx, gY, grb, genv):
+        pos, freq = ctx.saved_tensors
+        g = ctx.graph
+        gvec = torch.empty(g.E, 3, device=pos.device)
+        cont = lambda t: None if t is None else t.contiguous().float()
+        gY, grb, genv = cont(gY), cont(grb), cont(genv)
+        st = _lib.stream_of(pos)
+        call("face_edge_geom_bwd", ptr(pos), ptr(g.recv), ptr(g.col), ptr(g.shift), None, g.E, ptr(freq), freq.numel(),
+             float(ctx.rc), float(ctx.bes_scale), ptr(gY), ptr(grb), ptr(genv), None, ptr(gvec), st, label="edge_bwd")
+        gpos = torch.empty_like(pos)
+        call("face_force_scatter", ptr(gvec), ptr(g.row_ptr), ptr(g.rev), g.N, 1.0, ptr(gpos), st, label="force_scatter")
+        return gpos, None, None, None, None
+
+
+def edge_geometry(pos, graph, freq, rc):
+    return EdgeGeometry.apply(pos, graph, freq, rc, math.sqrt(2.0 / rc))
+
+
+# ----------------------------------------------------------------------------- gathers
+class GatherNeighbour(torch.autograd.Function):
+    """X (N,F) -> X[col] (E,F); backward dX[k] = sum_{e in row k} g[rev e] (no atomics)."""
+
+    @staticmethod
+    def forward(ctx, X, graph):
+        X, ld = _rows(X, X.shape[1])
+        F = X.shape[1]
+        out = torch.empty(graph.E, F, device=X.device)
+        call("face_gather_rows", ptr(X), ld, ptr(graph.col), graph.E, F, ptr(out), F, _lib.stream_of(X))
+        ctx.graph, ctx.N = graph, X.shape[0]
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        gr = ctx.graph
+        g, ld = _rows(g, g.shape[1])
+        F = g.shape[1]
+        dX = torch.empty(ctx.N, F, device=g.device)
+        call("face_gather_rows_bwd", ptr(g), ld, ptr(gr.row_ptr), ptr(gr.rev), gr.N, F, ptr(dX), F,
+             _lib.stream_of(g))
+        return dX, None
+
+
+class GatherReceiver(torch.autograd.Function):
+    """X (N,F) -> X[recv] (E,F); backward is the row sum dX[k] = sum_{e in row k} g[e]."""
+
+    @staticmethod
+    def forward(ctx, X, graph):
+        X, ld = _rows(X, X.shape[1])
+        F = X.shape[1]
+        out = torch.empty(graph.E, F, device=X.device)
+        call("face_gather_rows", ptr(X), ld, ptr(graph.recv), graph.E, F, ptr(out), F, _lib.stream_of(X))
+        ctx.graph, ctx.N = graph, X.shape[0]
+        return out
+
+    @staticmethod
+    def backward(ctx, g):
+        gr = ctx.graph
+        g, ld = _rows(g, g.shape[1])
+        F = g.shape[1]
+        dX = torch.empty(ctx.N, F, device=g.device)
+        call("face_segment_sum", ptr(g), ld, ptr(gr.row_ptr), gr.N, F, ptr(dX), F, _lib.stream_of(g))
+        return dX, None
+
+
+def gather_neighbour(X, graph):
+    shp = X.shape
+    out = GatherNeighbour.apply(X.reshape(shp[0], -1), graph)
+    return out.view(graph.E, *shp[1:])
+
+
+def gather_receiver(X, graph):
+    shp = X.shape
+    out = GatherReceiver.apply(X.reshape(shp[0], -1), graph)
+    return out.view(graph.E, *shp[1:])
+
+
+class StructureSum(torch.autograd.Function):
+    """Per-structure sum of per-atom values (atoms of a structure are contiguous)."""
+
+    @staticmethod
+    def forward(ctx, e_at, struct_ptr, batch, nstr):
+        e = e_at.contiguous().float().view(-1, 1)
+        out = torch.empty(nstr, 1, device=e.device)
+        call("face_segment_sum", ptr(e), 1, ptr(struct_ptr), nstr, 1, ptr(out), 1, _lib.stream_of(e))
+        ctx.save_for_backward(batch)
+        return out.view(nstr)
+
+    @staticmethod
+    def backward(ctx, g):
+        (batch,) = ctx.saved_tensors
+        return g[batch], None, None, None
+
+
+# ----------------------------------------------------------------------------- densities
+class Density(torch.autograd.Function):
+    """D (N, NX, B*K) = sum over row i of phi (x) msg (x) Y[:, :NX]  (face/kernels.py:170-178).
+
+    msg is per edge (E, K) when gathered is False, else a node table (N, K) read through col
+    (its gradient is then reduced back to the table through the reverse-edge map).
+    """
+
+    @staticmethod
+    def forward(ctx, phi, msg, Y, graph, nx, gathered):
+        _lib.require_gpu(phi, msg, Y)
+        B, K = phi.shape[1], msg.shape[1]
+        phi_, ld_phi = _rows(phi, B)
+        msg_, ld_msg = _rows(msg, K)
+        Y_, ld_Y = _rows(Y, nx)
+        N = graph.N
+        D = torch.empty(N, nx, B * K, device=phi.device)
+        row = graph.col if gathered else None
+        call("face_density_fwd", ptr(phi_), ld_phi, ptr(msg_), ld_msg, ptr(row), ptr(Y_), ld_Y, nx, ptr(graph.row_ptr),
+             N, 0, B, K, ptr(D), _lib.stream_of(phi), label=f"density_fwd{nx}")
+        ctx.save_for_backward(phi_, msg_, Y_)
+        ctx.graph, ctx.nx, ctx.gathered, ctx.BK = graph, nx, gathered, (B, K)
+        ctx.ywidth = Y.shape[1]
+        return D
+
+    @staticmethod
+    def backward(ctx, G):
+        phi, msg, Y = ctx.saved_tensors
+        g, nx, (B, K) = ctx.graph, ctx.nx, ctx.BK
+        G = G.contiguous().float()
+        dev = G.device
+        need_phi, need_msg, need_Y = ctx.needs_input_grad[:3]
+        dphi = torch.empty(g.E, B, device=dev) if need_phi else None
+        dmsg = torch.empty(g.E, K, device=dev) if need_msg else None
+        dY = torch.empty(g.E, nx, device=dev) if need_Y else None
+        row = g.col if ctx.gathered else None
+        st = _lib.stream_of(G)
+        call("face_density_bwd", ptr(phi), phi.stride(0), ptr(msg), msg.stride(0), ptr(row), ptr(Y), Y.stride(0), nx,
+             ptr(g.row_ptr), g.N, 0, g.max_row, B, K, ptr(G), ptr(dphi), B, ptr(dmsg), K, ptr(dY), nx, st,
+             label=f"density_bwd{nx}")
+        if dmsg is not None and ctx.gathered:
+            dtab = torch.empty(g.N, K, device=dev)
+            call("face_gather_rows_bwd", ptr(dmsg), K, ptr(g.row_ptr), ptr(g.rev), g.N, K, ptr(dtab), K, st,
+                 label="gather_bwd")
+            dmsg = dtab
+        if dY is not None and ctx.ywidth != nx:
+            dY = torch.nn.functional.pad(dY, (0, ctx.ywidth - nx))
+        return dphi, dmsg, dY, None, None, None
+
+
+def density(phi, msg, Y, graph, nx=20, gathered=False):
+    return Density.apply(phi, msg, Y, graph, nx, gathered)
+
+
+class CPDensity(torch.autograd.Function):
+    """A (N,20,C) = sum over row i of R[:, l(x), c] msg[:, c] Y[:, x]  (face/model.py:496-502)."""
+
+    @staticmethod
+    def forward(ctx, R, msg, Y, graph, gathered):
+        _lib.require_gpu(R, msg, Y)
+        C = msg.shape[1]
+        R_, ld_R = _rows(R, 4 * C)
+        msg_, ld_msg = _rows(msg, C)
+        Y_, ld_Y = _rows(Y, 20)
+        A = torch.empty(graph.N, 20, C, device=R.device)
+        row = graph.col if gathered else None
+        call("face_cp_density_fwd", ptr(R_), ld_R, ptr(msg_), ld_msg, ptr(row), ptr(Y_), ld_Y, ptr(graph.row_ptr),
+             graph.N, 0, C, ptr(A), _lib.stream_of(R), label="cp_fwd")
+        ctx.save_for_backward(R_, msg_, Y_)
+        ctx.graph, ctx.gathered, ctx.C = graph, gathered, C
+        return A
+
+    @staticmethod
+    def backward(ctx, gA):
+        R, msg, Y = ctx.saved_tensors
+        g, C = ctx.graph, ctx.C
+        gA = gA.contiguous().float()
+        dev = gA.device
+        need_R, need_msg, need_Y = ctx.needs_input_grad[:3]
+        dR = torch.empty(g.E, 4 * C, device=dev) if need_R else None
+        dmsg = torch.empty(g.E, C, device=dev) if need_msg else None
+        dY = torch.empty(g.E, 20, device=dev) if need_Y else None
+        row = g.col if ctx.gathered else None
+        st = _lib.stream_of(gA)
+        call("face_cp_density_bwd", ptr(R), R.stride(0), ptr(msg), msg.stride(0), ptr(row), ptr(Y), Y.stride(0),
+             ptr(g.row_ptr), g.N, 0, g.max_row, C, ptr(gA), ptr(dR), 4 * C, ptr(dmsg), C, ptr(dY), 20, st,
+             label="cp_bwd")
+        if dmsg is not None and ctx.gathered:
+            dtab = torch.empty(g.N, C, device=dev)
+            call("face_gather_rows_bwd", ptr(dmsg), C, ptr(g.row_ptr), ptr(g.rev), g.N, C, ptr(dtab), C, st,
+                 label="gather_bwd")
+            dmsg = dtab
+        return dR, dmsg, dY, None, None
+
+
+def cp_density(R, msg, Y, graph, gathered=False):
+    return CPDensity.apply(R, msg, Y, graph, gathered)
+
+
+# ----------------------------------------------------------------------------- node algebra
+def _s3(t):
+    """(atom, channel, component) element strides of a 3-d view."""
+    return [t.stride(0), t.stride(1), t.stride(2)]
+
+
+class NodeFeatures(torch.autograd.Function):
+    """Invariant families and gated products from the projection outputs (channel-last).
+
+    y0 (N,1,>=C), y1 (N,3,3C), y2 (N,6,3C), y3 (N,10,>=2C): P|Q|S blocks of C channels.
+    Returns feats (N,9C) = [P0 | inv1..inv8] (family-major, face/model.py:244-249,254-264),
+    and when eq: V (N,3,C), Ms (N,6,C) = symmetrised Mf in sym storage (face/model.py:288-294).
+    """
+
+    @staticmethod
+    def forward(ctx, y0, y1, y2, y3, a, b, eq, C):
+        _lib.require_gpu(y0, y1, y2, y3)
+        N = y1.shape[0]
+        dev = y1.device
+        ys = [y.contiguous().float() for y in (y0, y1, y2, y3)]
+        y0, y1, y2, y3 = ys
+        ins = [y1[:, :, :C], y1[:, :, C:2 * C], y1[:, :, 2 * C:], y2[:, :, :C], y2[:, :, C:2 * C], y2[:, :, 2 * C:],
+               y3[:, :, :C], y3[:, :, C:2 * C]]
+        ins = [t.transpose(1, 2) for t in ins]                                  # (N,C,k) views
+        feats = torch.empty(N, 9 * C, device=dev)
+        feats[:, :C] = y0[:, 0, :C]
+        inv_view = feats[:, C:].view(N, 8, C).transpose(1, 2)                   # (N,C,8)
+        st = sum((_s3(t) for t in ins), [])
+        V = Ms = None
+        if eq:
+            V = torch.empty(N, 3, C, device=dev)
+            Ms = torch.empty(N, 6, C, device=dev)
+            a_, b_ = a.contiguous().float(), b.contiguous().float()
+        else:
+            a_ = b_ = None
+        call("face_node_fwd", _lib.ptr_array(ins), _lib.i64_array(st), ptr(a_), ptr(b_), ptr(inv_view),
+             _lib.i64_array(_s3(inv_view)), ptr(V), _lib.i64_array(_s3(V.transpose(1, 2)) if eq else [0, 0, 0]),
+             ptr(Ms), _lib.i64_array(_s3(Ms.transpose(1, 2)) if eq else [0, 0, 0]), 1, N, C, int(bool(eq)),
+             _lib.stream_of(y1), label="node_fwd")
+        ctx.save_for_backward(y0, y1, y2, y3, a_ if eq else torch.empty(0), b_ if eq else torch.empty(0))
+        ctx.eq, ctx.C = eq, C
+        if eq:
+            return feats, V, Ms
+        return feats, None, None
+
+    @staticmethod
+    def backward(ctx, gfeats, gV, gMs):
+        y0, y1, y2, y3, a, b = ctx.saved_tensors
+        C, eq = ctx.C, ctx.eq
+        N = y1.shape[0]
+        dev = y1.device
+        ins = [y1[:, :, :C], y1[:, :, C:2 * C], y1[:, :, 2 * C:], y2[:, :, :C], y2[:, :, C:2 * C], y2[:, :, 2 * C:],
+               y3[:, :, :C], y3[:, :, C:2 * C]]
+        ins = [t.transpose(1, 2) for t in ins]
+        st = sum((_s3(t) for t in ins), [])
+        dy0 = torch.zeros_like(y0)
+        dy1 = torch.empty_like(y1)
+        dy2 = torch.empty_like(y2)
+        dy3 = torch.empty_like(y3)
+        if dy3.shape[2] > 2 * C:
+            dy3[:, :, 2 * C:] = 0
+        outs = [dy1[:, :, :C], dy1[:, :, C:2 * C], dy1[:, :, 2 * C:], dy2[:, :, :C], dy2[:, :, C:2 * C],
+                dy2[:, :, 2 * C:], dy3[:, :, :C], dy3[:, :, C:2 * C]]
+        outs = [t.transpose(1, 2) for t in outs]
+        gI = None
+        if gfeats is not None:
+            gfeats = gfeats.contiguous().float()
+            dy0[:, 0, :C] = gfeats[:, :C]
+            gI = gfeats[:, C:].view(N, 8, C).transpose(1, 2)
+        need_ab = eq and (ctx.needs_input_grad[4] or ctx.needs_input_grad[5])
+        da = torch.empty(N, C, 4, device=dev) if need_ab else None
+        db = torch.empty(N, C, 4, device=dev) if need_ab else None
+        if gV is not None:
+            gV = gV.contiguous().float()
+        if gMs is not None:
+            gMs = gMs.contiguous().float()
+        z3 = [0, 0, 0]
+        call("face_node_bwd", _lib.ptr_array(ins), _lib.i64_array(st), ptr(a) if eq else None,
+             ptr(b) if eq else None, ptr(gI), _lib.i64_array(_s3(gI) if gI is not None else z3),
+             ptr(gV), _lib.i64_array(_s3(gV.transpose(1, 2)) if gV is not None else z3),
+             ptr(gMs), _lib.i64_array(_s3(gMs.transpose(1, 2)) if gMs is not None else z3), 1,
+             _lib.ptr_array(outs), _lib.i64_array(sum((_s3(t) for t in outs), [])), ptr(da), ptr(db), N, C,
+             int(bool(eq)), _lib.stream_of(y1), label="node_bwd")
+        ga = da.sum(0).t() if need_ab else None
+        gb = db.sum(0).t() if need_ab else None
+        return dy0, dy1, dy2, dy3, ga, gb, None, None
+
+
+def node_features(y0, y1, y2, y3, a, b, eq, C):
+    return NodeFeatures.apply(y0, y1, y2, y3, a, b, eq, C)

@@ -1,0 +1,185 @@
+/* C-ABI of the MI355X-native FACE hot path (libface_hip.so, gfx950).
+ *
+ * Conventions
+ *   - Every pointer is a device pointer unless the comment says "host".
+ *   - Every entry point enqueues work on `stream` (a hipStream_t; NULL = the null stream),
+ *     never synchronises, never allocates: outputs and workspaces are passed in.
+ *   - Return value: 0 on success, a positive hipError_t from the launch, or a negative
+ *     FACE_ERR_* code for an argument the kernels cannot serve. face_hip_error_string()
+ *     names either kind.
+ *   - Floating point data are fp32, row-major; `ld_*` arguments are row strides in elements.
+ *   - Edge lists are grouped by receiver atom i. `row_ptr` (N+1, int32) gives row i as edges
+ *     [row_ptr[i], row_ptr[i+1]); row_ptr == NULL means the reference's padded-dense layout
+ *     (N, M): row i is edges [i*M, (i+1)*M), masked slots included (their radial weight is 0).
+ *
+ * Reference interfaces replaced (albert-hzbn/face-mlip):
+ *   face/kernels.py:135-172      FactorDensity / factor_density   -> face_density_fwd / _bwd
+ *   face/model.py:496-502        CP pooling bmm                   -> face_cp_density_fwd / _bwd
+ *   face/node_kernel.py:164-209  NodeAlgebra / node_algebra       -> face_node_fwd / _bwd
+ *   face/neighbors.py:7-37       padded_graph (ASE neighbor_list) -> face_nbr_* (count, fill, rev, padded)
+ *   face/model.py:670-677        edge geometry + Bessel basis     -> face_edge_geom_fwd / _bwd
+ *   face/model.py:670,464,692-694 index_select gathers and their index_add backward
+ *                                                                  -> face_gather_rows, face_gather_rows_bwd,
+ *                                                                     face_force_scatter
+ */
+#ifndef FACE_HIP_H
+#define FACE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FACE_ERR_ARG (-1)         /* invalid shape, stride or null pointer */
+#define FACE_ERR_UNSUPPORTED (-2) /* shape outside the instantiated kernel variants */
+#define FACE_ERR_CAPACITY (-3)    /* a row or bin exceeds the kernel's capacity */
+
+const char* face_hip_error_string(int code);
+/* ABI version of this header (bumped on any signature change). */
+int face_hip_abi_version(void);
+
+/* ---------------------------------------------------------------- factor density
+ * D[i, x, b*K + k] = sum_{e in row i} phi[e, b] * msg[m(e), k] * Y[e, x],  x < NX
+ * where m(e) = msg_row ? msg_row[e] : e (msg_row gathers rows of a node table directly).
+ * phi (E, ld_phi >= B), msg (*, ld_msg >= K), Y (E, ld_Y >= NX), D (N, NX, B*K).
+ * NX is 20 (monomials up to rank 3, face/cartesian.py:11-17) or 4 (1, u: the transport sums
+ * of face/model.py:515-522, which are this contraction with msg = gathered transport tables).
+ * Replaces FactorDensity.forward / dens_fwd (face/kernels.py:137-149, :22-54).            */
+int face_density_fwd(const float* phi, int32_t ld_phi, const float* msg, int32_t ld_msg, const int32_t* msg_row,
+                     const float* Y, int32_t ld_Y, int32_t NX, const int32_t* row_ptr, int64_t N, int32_t M,
+                     int32_t B, int32_t K, float* D, void* stream);
+
+/* Backward of face_density_fwd for upstream G = dL/dD (N, NX, B*K):
+ *   dphi[e,b] = sum_{x,k} G[i,x,b,k] Y[e,x] msg[m(e),k]
+ *   dmsg[e,k] = sum_{x,b} G[i,x,b,k] Y[e,x] phi[e,b]     (per EDGE, also when msg_row != NULL)
+ *   dY[e,x]   = sum_{b,k} G[i,x,b,k] phi[e,b] msg[m(e),k]
+ * Any of dphi / dmsg / dY may be NULL (not computed). max_row = longest row (M when padded).
+ * Replaces FactorDensity.backward / dens_bwd (face/kernels.py:151-167, :56-118).           */
+int face_density_bwd(const float* phi, int32_t ld_phi, const float* msg, int32_t ld_msg, const int32_t* msg_row,
+                     const float* Y, int32_t ld_Y, int32_t NX, const int32_t* row_ptr, int64_t N, int32_t M,
+                     int32_t max_row, int32_t B, int32_t K, const float* G, float* dphi, int32_t ld_dphi,
+                     float* dmsg, int32_t ld_dmsg, float* dY, int32_t ld_dY, void* stream);
+
+/* ---------------------------------------------------------------- CP density
+ * A[i, x, c] = sum_{e in row i} R[e, l(x), c] * msg[m(e), c] * Y[e, x],  l(x) = rank of monomial x
+ * R (E, ld_R >= 4C) laid out [rank][channel], msg (*, ld_msg >= C), Y (E, ld_Y >= 20), A (N, 20, C).
+ * The rank-diagonal blocks of the reference's (N,20,4,C) bmm (face/model.py:496-502).     */
+int face_cp_density_fwd(const float* R, int32_t ld_R, const float* msg, int32_t ld_msg, const int32_t* msg_row,
+                        const float* Y, int32_t ld_Y, const int32_t* row_ptr, int64_t N, int32_t M, int32_t C,
+                        float* A, void* stream);
+
+/* Backward for gA = dL/dA (N, 20, C): dR (E, ld_dR), dmsg (E, ld_dmsg) per edge, dY (E, ld_dY).
+ * Any output may be NULL. */
+int face_cp_density_bwd(const float* R, int32_t ld_R, const float* msg, int32_t ld_msg, const int32_t* msg_row,
+                        const float* Y, int32_t ld_Y, const int32_t* row_ptr, int64_t N, int32_t M, int32_t max_row,
+                        int32_t C, const float* gA, float* dR, int32_t ld_dR, float* dmsg, int32_t ld_dmsg, float* dY,
+                        int32_t ld_dY, void* stream);
+
+/* ---------------------------------------------------------------- node algebra
+ * Per (atom n, channel c) invariants of symmetric Cartesian tensors
+ *   inputs  P1,Q1,S1 (3 comps), P2,Q2,S2 (6, order xx,yy,zz,xy,xz,yz), P3,Q3 (10, face/cartesian.py:14-15)
+ *   inv[0..7] = P1.Q1, P2:Q2, P3:Q3, P1.Q2.S1, tr(P2 Q2 S2), (P3:Q2).S1, (P3:Q3):S2, P3[Q1,S1,Q1]
+ *   V  = a0 P1 + a1 Q2 S1 + a2 P3:Q2 + a3 P2 Q1
+ *   Mf = b0 P2 + b1 P1 (x) Q1 + b2 P2 Q2 + b3 P3.S1                      (only when eq != 0)
+ * ins: host array of 8 device pointers (P1,Q1,S1,P2,Q2,S2,P3,Q3); in_strides: host array of
+ * 8 x 3 int64 element strides (atom, channel, component). a, b: (4, C) contiguous device arrays.
+ * inv: strides (atom, channel, family); V: (atom, channel, component).
+ * Mf: mf_mode 0 -> full 3x3 (component a*3+d); 1 -> symmetrised 0.5(Mf+Mf^T) in 6-component storage.
+ * Replaces NodeAlgebra.forward / node_fwd (face/node_kernel.py:168-184, :18-64).          */
+int face_node_fwd(const float* const* ins, const int64_t* in_strides, const float* a, const float* b, float* inv,
+                  const int64_t* inv_strides, float* V, const int64_t* V_strides, float* Mf,
+                  const int64_t* Mf_strides, int32_t mf_mode, int64_t N, int32_t C, int32_t eq, void* stream);
+
+/* Backward: gI (8 families), gV (3), gM (mf_mode as above) with host stride arrays; any of them
+ * may be NULL (= zero). outs: host array of 8 device pointers dP1..dQ3 (symmetric storage) with
+ * out_strides (8 x 3). da, db: (N, C, 4) per-(atom, channel) partials, or NULL when not needed
+ * (forces only). Replaces NodeAlgebra.backward / node_bwd (face/node_kernel.py:186-204, :66-151). */
+int face_node_bwd(const float* const* ins, const int64_t* in_strides, const float* a, const float* b,
+                  const float* gI, const int64_t* gI_strides, const float* gV, const int64_t* gV_strides,
+                  const float* gM, const int64_t* gM_strides, int32_t mf_mode, float* const* outs,
+                  const int64_t* out_strides, float* da, float* db, int64_t N, int32_t C, int32_t eq, void* stream);
+
+/* ---------------------------------------------------------------- neighbour build
+ * Pair set of ASE neighbor_list("ijS", atoms, rc) as used by face/neighbors.py:12-15 and
+ * face/datasets.py:51: all (i, j, S) with |pos[j] - pos[i] + S.cell| < rc in fp64,
+ * S integer (0 on non-periodic axes), (i, i, 0) excluded; rows sorted by j then S.
+ *
+ * Batch description (device): pos (N,3) fp64; atom_struct (N) int32 structure of each atom;
+ * struct_ptr (nstr+1) int32 atom ranges; cell (nstr,9) fp64 rows = lattice vectors;
+ * inv_cell (nstr,9) fp64 = inverse of cell (zeros for non-periodic structures);
+ * pbc (nstr,3) int32.
+ *
+ * Small-structure path (bin_atoms == NULL): every atom tests every atom of its structure and
+ * every image that can lie within rc. Cell-list path (one fully periodic structure, nstr == 1,
+ * cell / inv_cell then point at its 9 values): nb is a HOST int32[6] = bins per axis (3) then
+ * bins searched on each side (3), each bin at least rc wide along its reciprocal axis unless
+ * the search width compensates; bin_of (N), wrap (N,3) = floor(fractional coordinate),
+ * bin_start (nbins+1) and bin_atoms (N) come from face_nbr_bin (bin_count, bin_fill: nbins
+ * int32 workspaces).                                                                        */
+int face_nbr_bin(const double* pos, int64_t N, const double* inv_cell, const int32_t* nb, int32_t* bin_of,
+                 int32_t* wrap, int32_t* bin_count, int32_t* bin_start, int32_t* bin_fill, int32_t* bin_atoms,
+                 void* stream);
+/* counts[i] = number of pairs of atom i. */
+int face_nbr_count(const double* pos, int64_t N, const int32_t* atom_struct, const int32_t* struct_ptr,
+                   const double* cell, const double* inv_cell, const int32_t* pbc, double rc, const int32_t* nb,
+                   const int32_t* bin_of, const int32_t* wrap, const int32_t* bin_start, const int32_t* bin_atoms,
+                   int32_t* counts, void* stream);
+/* Writes row i of the CSR list: col (E) int32 global neighbour index, S (E,3) int32,
+ * shift (E,3) fp32 = fp32(S . cell) computed in fp64; row_ptr (N+1) int32 from a scan of counts.
+ * key (E) int64 is workspace. Returns FACE_ERR_CAPACITY via *overflow (device int32) if a row
+ * found more pairs than counted (cannot happen for unchanged inputs).                    */
+int face_nbr_fill(const double* pos, int64_t N, const int32_t* atom_struct, const int32_t* struct_ptr,
+                  const double* cell, const double* inv_cell, const int32_t* pbc, double rc, const int32_t* nb,
+                  const int32_t* bin_of, const int32_t* wrap, const int32_t* bin_start, const int32_t* bin_atoms,
+                  const int32_t* row_ptr, int64_t* key, int32_t* col, int32_t* S, float* shift, int32_t* overflow,
+                  void* stream);
+/* rev[e] = index of the reverse edge (j, i, -S) of e = (i, j, S); missing[0] counts edges
+ * without one (a non-symmetric list). */
+int face_nbr_rev(const int32_t* row_ptr, const int32_t* col, const int32_t* S, int64_t N, int32_t* rev,
+                 int32_t* missing, void* stream);
+/* Reverse map for an edge list given by fp32 shift vectors (e.g. a padded graph converted
+ * to CSR): the reverse of (i, j, shift) is (j, i, -shift) with bitwise-equal components. */
+int face_nbr_rev_shift(const int32_t* row_ptr, const int32_t* col, const float* shift, int64_t N, int32_t* rev,
+                       int32_t* missing, void* stream);
+/* Padded view of face/neighbors.py:27-33: nbr (N,M) int64 (padding -> first atom of the
+ * atom's structure), shift_pad (N,M,3) fp32 (padding 0), mask (N,M) uint8. */
+int face_nbr_padded(const int32_t* row_ptr, const int32_t* col, const float* shift, const int32_t* atom_struct,
+                    const int32_t* struct_ptr, int64_t N, int32_t M, int64_t* nbr, float* shift_pad, uint8_t* mask,
+                    void* stream);
+
+/* ---------------------------------------------------------------- edge geometry
+ * Per edge e = (i -> col[e], shift[e]) (recv[e] = i): vec = pos[col] - pos[i] + shift,
+ * r = |vec| (r := 1 where mask[e] == 0), u = vec / r, Y = monomials(u) (20),
+ * bes_n = sin(freq[n] r) / r * bes_scale (freq[n] = (n+1) pi / rc, bes_scale = sqrt(2/rc) as the
+ * caller computes them), env = (1 - 28x^6 + 48x^7 - 21x^8)[x<1] * mask, x = r/rc, rb = bes * env. face/model.py:670-677, :28-40, face/cartesian.py:34-46.
+ * mask may be NULL (all edges valid). Outputs: Y (E,20), rb (E,nb), env (E), r (E) (may be NULL). */
+int face_edge_geom_fwd(const float* pos, const int32_t* recv, const int32_t* col, const float* shift,
+                       const uint8_t* mask, int64_t E, const float* freq, int32_t n_basis, float rc, float bes_scale,
+                       float* Y, float* rb, float* env, float* r, void* stream);
+/* dL/dvec (E,3) from gY (E,20), grb (E,nb), genv (E), gr (E) (any may be NULL = 0). */
+int face_edge_geom_bwd(const float* pos, const int32_t* recv, const int32_t* col, const float* shift,
+                       const uint8_t* mask, int64_t E, const float* freq, int32_t n_basis, float rc, float bes_scale,
+                       const float* gY, const float* grb, const float* genv, const float* gr, float* gvec,
+                       void* stream);
+
+/* ---------------------------------------------------------------- gathers and scatters
+ * out[e, :] = X[idx[e], :] for F features (X row stride ld_X, out row stride ld_out). */
+int face_gather_rows(const float* X, int32_t ld_X, const int32_t* idx, int64_t E, int32_t F, float* out,
+                     int32_t ld_out, void* stream);
+/* Backward of a gather along col of a symmetric edge list, without atomics:
+ * dX[k, :] = sum_{e in row k} g[rev[e], :]  (the edges with col == k are the reverses of row k). */
+int face_gather_rows_bwd(const float* g, int32_t ld_g, const int32_t* row_ptr, const int32_t* rev, int64_t N,
+                         int32_t F, float* dX, int32_t ld_dX, void* stream);
+/* Row sums: out[k, :] = sum_{e in row k} g[e, :]. */
+int face_segment_sum(const float* g, int32_t ld_g, const int32_t* row_ptr, int64_t N, int32_t F, float* out,
+                     int32_t ld_out, void* stream);
+/* dE/dpos from dE/dvec (vec_e = pos[col e] - pos[i] + shift): grad[k] = sum_{e in row k} (gvec[rev e] - gvec[e]).
+ * Writes grad (N,3) (forces are its negative: sign = -1 writes -grad). */
+int face_force_scatter(const float* gvec, const int32_t* row_ptr, const int32_t* rev, int64_t N, float sign,
+                       float* grad, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

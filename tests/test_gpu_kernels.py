@@ -1,0 +1,264 @@
+"""GPU parity of the HIP kernels against the CPU oracle (fp64 einsums + autograd).
+
+Tolerances follow the reference's own kernel tests: max-abs error / max-abs reference
+< 1e-4 for every output and gradient (tests/test_kernels.py:17-19, tests/test_node_kernel.py:84-89).
+"""
+import itertools
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import cartesian
+from oracle import ops as oops
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = 1e-4
+
+
+def rel(a, b):
+    a, b = a.detach().double().cpu(), b.detach().double().cpu()
+    return ((a - b).abs().max() / b.abs().max().clamp_min(1e-30)).item()
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+# ----------------------------------------------------------------------------- factor density
+@pytest.mark.parametrize("B,K", [(16, 32), (32, 32), (8, 16), (16, 64)])
+def test_factor_density_dropin_matches_reference_spec(B, K):
+    """tests/test_kernels.py:7-20: N=300, M=37, seed 0, randn inputs and upstream G."""
+    from face_amd.kernels import factor_density
+    say("factor_density", B, K)
+    N, M = 300, 37
+    torch.manual_seed(0)
+    phi = torch.randn(N, M, B, device=DEV, requires_grad=True)
+    msg = torch.randn(N, M, K, device=DEV, requires_grad=True)
+    Y = torch.randn(N, M, 20, device=DEV, requires_grad=True)
+    G = torch.randn(N, 20, B * K, device=DEV)
+    D1 = factor_density(phi, msg, Y)
+    g1 = torch.autograd.grad((D1 * G).sum(), (phi, msg, Y))
+    ins = [t.detach().double().cpu().requires_grad_(True) for t in (phi, msg, Y)]
+    D2 = oops.factor_density(*ins)
+    g2 = torch.autograd.grad((D2 * G.double().cpu()).sum(), ins)
+    errs = [rel(D1, D2)] + [rel(a, b) for a, b in zip(g1, g2)]
+    assert max(errs) < TOL, errs
+
+
+class _G:
+    """Random symmetric CSR graph for operator tests: unique undirected pairs, a hub row,
+    isolated atoms; rows sorted by neighbour; reverse map computed on the host."""
+
+    def __init__(self, N, n_pairs, seed, hub=70):
+        from face_amd.ops import Graph
+        rng = np.random.default_rng(seed)
+        pairs = set()
+        while len(pairs) < n_pairs:
+            i, j = rng.integers(0, N - 3, 2)          # the last 3 atoms stay isolated
+            if i != j:
+                pairs.add((min(i, j), max(i, j)))
+        for j in range(1, min(hub, N - 3)):
+            pairs.add((0, j))
+        directed = sorted([(i, j) for i, j in pairs] + [(j, i) for i, j in pairs])
+        index = {e: k for k, e in enumerate(directed)}
+        recv = np.array([e[0] for e in directed], np.int32)
+        col = np.array([e[1] for e in directed], np.int32)
+        rev = np.array([index[(j, i)] for i, j in directed], np.int32)
+        counts = np.bincount(recv, minlength=N)
+        row_ptr = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+        self.counts = counts.tolist()
+        t = lambda a: torch.as_tensor(a, device=DEV)
+        self.G = Graph(torch.zeros(N, 3, device=DEV), None, None, 1, None, t(row_ptr), t(col), t(recv), None, t(rev),
+                       int(counts.max()))
+
+
+def _pad(x_edge, counts, M):
+    """(E, ...) edge tensor -> (N, M, ...) zero padded (for the padded oracle)."""
+    N = len(counts)
+    out = x_edge.new_zeros(N, M, *x_edge.shape[1:])
+    off = 0
+    for i, c in enumerate(counts):
+        out[i, :c] = x_edge[off:off + c]
+        off += c
+    return out
+
+
+@pytest.mark.parametrize("nx,gathered,B,K", [(20, False, 16, 32), (20, True, 16, 32), (4, True, 16, 144),
+                                             (20, False, 8, 16), (4, True, 8, 36)])
+def test_csr_density_ragged_rows(nx, gathered, B, K):
+    from face_amd import ops
+    say("csr density", nx, gathered, B, K)
+    g = _G(57, 500, 2)
+    counts = g.counts
+    E = sum(counts)
+    torch.manual_seed(3)
+    phi = torch.randn(E, B + 5, device=DEV)[:, :B].requires_grad_(True)   # strided rows
+    tab_rows = 57 if gathered else E
+    msg = torch.randn(tab_rows, K, device=DEV, requires_grad=True)
+    Y = torch.randn(E, 20, device=DEV, requires_grad=True)
+    D = ops.density(phi, msg, Y, g.G, nx, gathered)
+    G = torch.randn_like(D)
+    gr = torch.autograd.grad((D * G).sum(), (phi, msg, Y))
+    # oracle on the padded layout
+    M = max(counts)
+    col = g.G.col.long().cpu()
+    pd = lambda t: _pad(t, counts, M)
+    ph = phi.detach().double().cpu().requires_grad_(True)
+    ms = msg.detach().double().cpu().requires_grad_(True)
+    Yc = Y.detach().double().cpu().requires_grad_(True)
+    msg_e = ms[col] if gathered else ms
+    D2 = oops.factor_density(pd(ph), pd(msg_e), pd(Yc)[..., :nx])
+    gr2 = torch.autograd.grad((D2 * G.double().cpu()).sum(), (ph, ms, Yc))
+    errs = [rel(D, D2)] + [rel(a, b) for a, b in zip(gr, gr2)]
+    assert max(errs) < TOL, errs
+    # bitwise reproducible (no atomics)
+    D3 = ops.density(phi, msg, Y, g.G, nx, gathered)
+    assert torch.equal(D, D3)
+
+
+@pytest.mark.parametrize("gathered,C", [(False, 160), (True, 160), (False, 96), (True, 40)])
+def test_cp_density_ragged_rows(gathered, C):
+    from face_amd import ops
+    say("cp density", gathered, C)
+    g = _G(41, 600, 5)
+    counts = g.counts
+    E = sum(counts)
+    torch.manual_seed(6)
+    R = torch.randn(E, 16 + 4 * C, device=DEV)[:, 16:].requires_grad_(True)
+    msg = torch.randn(41 if gathered else E, C, device=DEV, requires_grad=True)
+    Y = torch.randn(E, 20, device=DEV, requires_grad=True)
+    A = ops.cp_density(R, msg, Y, g.G, gathered)
+    G = torch.randn_like(A)
+    gr = torch.autograd.grad((A * G).sum(), (R, msg, Y))
+    M = max(counts)
+    col = g.G.col.long().cpu()
+    pd = lambda t: _pad(t, counts, M)
+    Rc = R.detach().double().cpu().requires_grad_(True)
+    ms = msg.detach().double().cpu().requires_grad_(True)
+    Yc = Y.detach().double().cpu().requires_grad_(True)
+    A2 = oops.cp_density(pd(Rc.view(E, 4, C)), pd(ms[col] if gathered else ms), pd(Yc))
+    gr2 = torch.autograd.grad((A2 * G.double().cpu()).sum(), (Rc, ms, Yc))
+    errs = [rel(A, A2)] + [rel(a, b) for a, b in zip(gr, gr2)]
+    assert max(errs) < TOL, errs
+
+
+# ----------------------------------------------------------------------------- node algebra
+@pytest.mark.parametrize("eq", [True, False])
+def test_node_algebra_dropin_matches_reference_spec(eq):
+    """tests/test_node_kernel.py:8-28: N=50, C=24, seed 1, outputs and every gradient incl. da, db."""
+    from face_amd.node_kernel import node_algebra
+    say("node_algebra eq", eq)
+    torch.manual_seed(1)
+    N, C = 50, 24
+    shapes = [(3,), (3,), (3,), (6,), (6,), (6,), (10,), (10,)]
+    xs = [torch.randn(N, C, *s, device=DEV, requires_grad=True) for s in shapes]
+    a = torch.randn(4, C, device=DEV, requires_grad=True)
+    b = torch.randn(4, C, device=DEV, requires_grad=True)
+    gI, gV, gM = torch.randn(N, C, 8, device=DEV), torch.randn(N, C, 3, device=DEV), torch.randn(N, C, 3, 3, device=DEV)
+    o1 = node_algebra(*xs, a, b, eq)
+    L = lambda o, gi, gv, gm: (o[0] * gi).sum() + (((o[1] * gv).sum() + (o[2] * gm).sum()) if eq else 0)
+    vars1 = xs + ([a, b] if eq else [])
+    g1 = torch.autograd.grad(L(o1, gI, gV, gM), vars1, allow_unused=True)
+    xc = [t.detach().double().cpu().requires_grad_(True) for t in xs]
+    ac, bc = a.detach().double().cpu().requires_grad_(True), b.detach().double().cpu().requires_grad_(True)
+    o2 = oops.node_algebra_sym(*xc, ac, bc)
+    vars2 = xc + ([ac, bc] if eq else [])
+    g2 = torch.autograd.grad(L(o2, gI.double().cpu(), gV.double().cpu(), gM.double().cpu()), vars2,
+                             allow_unused=True)
+    outs1 = list(o1[:3] if eq else o1[:1])
+    outs2 = list(o2[:3] if eq else o2[:1])
+    errs = [rel(u, v) for u, v in zip(outs1 + list(g1), outs2 + list(g2))]
+    assert max(errs) < TOL, errs
+
+
+def test_node_features_product_layout():
+    """Strided P/Q/S read from projection outputs, families written into the readout row,
+    symmetrised gated products (face/model.py:244-249,274-276)."""
+    from face_amd import ops
+    say("node features")
+    torch.manual_seed(2)
+    N, C = 37, 20
+    y0 = torch.randn(N, 1, C, device=DEV, requires_grad=True)
+    y1 = torch.randn(N, 3, 3 * C, device=DEV, requires_grad=True)
+    y2 = torch.randn(N, 6, 3 * C, device=DEV, requires_grad=True)
+    y3 = torch.randn(N, 10, 2 * C, device=DEV, requires_grad=True)
+    a = torch.randn(4, C, device=DEV, requires_grad=True)
+    b = torch.randn(4, C, device=DEV, requires_grad=True)
+    feats, V, Ms = ops.node_features(y0, y1, y2, y3, a, b, True, C)
+    gf, gv, gm = torch.randn_like(feats), torch.randn_like(V), torch.randn_like(Ms)
+    vars1 = [y0, y1, y2, y3, a, b]
+    g1 = torch.autograd.grad((feats * gf).sum() + (V * gv).sum() + (Ms * gm).sum(), vars1)
+    yc = [t.detach().double().cpu().requires_grad_(True) for t in vars1]
+    c0, c1, c2, c3, ac, bc = yc
+    split = lambda y, k: [y[..., j * C:(j + 1) * C].transpose(1, 2) for j in range(k)]
+    P1, Q1, S1 = split(c1, 3)
+    P2, Q2, S2 = split(c2, 3)
+    P3, Q3 = split(c3, 2)
+    inv, Vr, Mf = oops.node_algebra_sym(P1, Q1, S1, P2, Q2, S2, P3, Q3, ac, bc)
+    feats2 = torch.cat([c0[:, 0]] + list(inv.unbind(-1)), 1)
+    Ms2 = cartesian.to_sym2(0.5 * (Mf + Mf.transpose(-1, -2))).transpose(1, 2)
+    V2 = Vr.transpose(1, 2)
+    L2 = (feats2 * gf.double().cpu()).sum() + (V2 * gv.double().cpu()).sum() + (Ms2 * gm.double().cpu()).sum()
+    g2 = torch.autograd.grad(L2, yc)
+    errs = [rel(feats, feats2), rel(V, V2), rel(Ms, Ms2)] + [rel(u, v) for u, v in zip(g1, g2)]
+    assert max(errs) < TOL, errs
+
+
+# ----------------------------------------------------------------------------- gathers / scatter
+def test_gathers_and_force_scatter_match_index_add():
+    from face_amd import ops
+    from face_amd.neighbors import build_graph
+    from face_amd import systems
+    say("gathers / scatter")
+    (liq,) = [systems.liquid(500, np.random.default_rng(9), rho=0.1, dmin=0.9)]
+    g = build_graph([liq], 4.0)
+    torch.manual_seed(0)
+    X = torch.randn(g.N, 7, device=DEV, requires_grad=True)
+    Xj = ops.gather_neighbour(X, g)
+    Xi = ops.gather_receiver(X, g)
+    col, recv = g.col.long(), g.recv.long()
+    assert torch.equal(Xj, X[col]) and torch.equal(Xi, X[recv])
+    w1, w2 = torch.randn_like(Xj), torch.randn_like(Xi)
+    (gx,) = torch.autograd.grad((Xj * w1).sum() + (Xi * w2).sum(), X)
+    ref = torch.zeros_like(X).index_add(0, col, w1).index_add(0, recv, w2)
+    assert rel(gx, ref) < 1e-5
+    gvec = torch.randn(g.E, 3, device=DEV)
+    grad = torch.empty(g.N, 3, device=DEV)
+    from face_amd._lib import call, ptr, stream_of
+    call("face_force_scatter", ptr(gvec), ptr(g.row_ptr), ptr(g.rev), g.N, 1.0, ptr(grad), stream_of(gvec))
+    ref = torch.zeros(g.N, 3, device=DEV).index_add(0, col, gvec).index_add(0, recv, -gvec)
+    assert rel(grad, ref) < 1e-5
+
+
+# ----------------------------------------------------------------------------- edge geometry
+def test_edge_geometry_forward_and_backward():
+    from face_amd import ops
+    from face_amd.neighbors import build_graph
+    from face_amd import systems
+    say("edge geometry")
+    st = systems.molecules(6, np.random.default_rng(2))
+    rc = 4.5
+    g = build_graph(st, rc)
+    pos = g.pos.clone().requires_grad_(True)
+    freq = (torch.arange(1, 9) * np.pi / rc).float().to(DEV)
+    Y, rb, env = ops.edge_geometry(pos, g, freq, rc)
+    wY, wr, we = torch.randn_like(Y), torch.randn_like(rb), torch.randn_like(env)
+    (gp,) = torch.autograd.grad((Y * wY).sum() + (rb * wr).sum() + (env * we).sum(), pos)
+    # oracle: the reference formulas in fp64 on the CPU (face/model.py:670-677, :28-40)
+    pc = g.pos.detach().double().cpu().requires_grad_(True)
+    col, recv = g.col.long().cpu(), g.recv.long().cpu()
+    vec = pc[col] - pc[recv] + g.shift.double().cpu()
+    r = torch.sqrt((vec * vec).sum(-1))
+    u = vec / r[:, None]
+    x = r / rc
+    e_ref = (1 - 28 * x ** 6 + 48 * x ** 7 - 21 * x ** 8) * (x < 1)
+    bes = torch.sin(torch.arange(1, 9, dtype=torch.float64) * np.pi / rc * r[:, None]) / r[:, None] * np.sqrt(2 / rc)
+    Y2, rb2 = cartesian.monomials(u), bes * e_ref[:, None]
+    (gp2,) = torch.autograd.grad((Y2 * wY.double().cpu()).sum() + (rb2 * wr.double().cpu()).sum()
+                                 + (e_ref * we.double().cpu()).sum(), pc)
+    errs = [rel(Y, Y2), rel(rb, rb2), rel(env, e_ref), rel(gp, gp2)]
+    assert max(errs) < TOL, errs

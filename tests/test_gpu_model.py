@@ -1,0 +1,124 @@
+"""Model-level parity on the GPU: energies within 1e-5 relative and forces within
+1e-4 x RMS(F) max-abs of the reference torch path (golden vectors written from the
+reference itself) and of the CPU oracle at benchmark shapes."""
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from golden.cases import BIG_CASES, SMALL_CASES
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+E_TOL, F_TOL = 1e-5, 1e-4
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def product_model(kw, elements, seed=0):
+    from face_amd import model as fm
+    torch.manual_seed(seed)
+    m = fm.FACE(elements, **kw)
+    fm.unit_parameterise(m)
+    return m.cuda().eval()
+
+
+def check(E, F, Eg, Fg):
+    E, F = np.asarray(E, np.float64), np.asarray(F, np.float64)
+    dE = np.abs(E - Eg).max() / np.abs(Eg).max()
+    rms = np.sqrt((np.asarray(Fg, np.float64) ** 2).mean())
+    dF = np.abs(F - Fg).max() / rms
+    assert dE <= E_TOL and dF <= F_TOL, (dE, dF)
+    return dE, dF
+
+
+def golden_graph(d):
+    t = lambda k, dt=None: torch.as_tensor(d[k], device="cuda", dtype=dt)
+    return {"pos": t("pos", torch.float32), "Z": t("Z"), "nbr": t("nbr"), "shift": t("shift", torch.float32),
+            "mask": t("mask"), "batch": t("batch")}
+
+
+@pytest.mark.parametrize("name", list(SMALL_CASES) + list(BIG_CASES))
+def test_energy_forces_match_reference_golden(name):
+    kw, el, _ = (SMALL_CASES if name in SMALL_CASES else BIG_CASES)[name]
+    say("golden", name)
+    d = np.load(os.path.join(GOLD, f"{name}_f32.npz"))
+    m = product_model(kw, el)
+    o = m(golden_graph(d))
+    dE, dF = check(o["energy"].detach().cpu(), o["forces"].detach().cpu(), d["energy"], d["forces"])
+    say(f"  dE/E {dE:.2e}  max|dF|/rms {dF:.2e}")
+    # the same structures through the GPU pair-list build give the same E/F
+    from face_amd.neighbors import graph_from_padded
+    o2 = m(golden_graph(d))
+    assert torch.equal(o["forces"], o2["forces"])               # bitwise reproducible
+
+
+def test_gpu_graph_path_equals_padded_path():
+    from face_amd import systems
+    from face_amd.neighbors import padded_graph, build_graph
+    say("graph paths")
+    kw, el, _ = SMALL_CASES["small_flag_mol"]
+    m = product_model(kw, el)
+    sts = systems.molecules(3, np.random.default_rng(2))
+    g = padded_graph(sts, kw["rc"])
+    o1 = m({k: g[k] for k in ("pos", "Z", "nbr", "shift", "mask", "batch")})
+    o2 = m(g)
+    o3 = m(build_graph(sts, kw["rc"]))
+    for o in (o2, o3):
+        assert torch.allclose(o["energy"], o1["energy"], rtol=1e-6, atol=0)
+        assert (o["forces"] - o1["forces"]).abs().max() <= 1e-5 * o1["forces"].abs().max()
+
+
+def _oracle_EF(structures, kw, el):
+    from oracle import model as om
+    from oracle.neighbors import padded_graph as opad
+    torch.manual_seed(0)
+    m = om.FACE(el, **kw)
+    om.unit_parameterise(m)
+    g = opad(structures, kw["rc"])
+    o = m({k: g[k] for k in ("pos", "Z", "nbr", "shift", "mask", "batch")})
+    return o["energy"].detach().numpy(), o["forces"].detach().numpy()
+
+
+@pytest.mark.parametrize("k,n_atoms,n_mol", [(0, None, None), (1, None, 48), (2, None, None), (3, 1500, None),
+                                             (4, 1200, None)])
+def test_workload_shapes_match_oracle(k, n_atoms, n_mol):
+    """Benchmark models (C96/C160/C256, seed 0) on the benchmark recipes; liquids and the CP
+    molecule batch are cut to sizes the CPU oracle finishes in seconds."""
+    from face_amd import systems
+    from face_amd.neighbors import build_graph
+    sts, kw, el, desc = systems.workload(k, n_atoms=n_atoms)
+    if n_mol:
+        sts = sts[:n_mol]
+    say("workload", k, desc, "atoms", sum(len(s["pos"]) for s in sts))
+    m = product_model(kw, el)
+    o = m(build_graph(sts, kw["rc"]))
+    Eo, Fo = _oracle_EF(sts, kw, el)
+    dE, dF = check(o["energy"].detach().cpu(), o["forces"].detach().cpu(), Eo, Fo)
+    say(f"  dE/E {dE:.2e}  max|dF|/rms {dF:.2e}")
+
+
+def test_forces_are_minus_energy_gradient_fd():
+    """Central differences of the GPU energy (fp32, h = 1e-2 A on a smooth small model)."""
+    from face_amd.neighbors import build_graph
+    from face_amd import systems
+    say("finite differences")
+    kw, el, _ = SMALL_CASES["small_flag_mol"]
+    m = product_model(kw, el)
+    st = systems.molecules(1, np.random.default_rng(12))
+    o = m(build_graph(st, kw["rc"]))
+    F = o["forces"].detach().cpu().numpy()
+    h = 1e-2
+    for i, c in [(0, 0), (5, 1), (17, 2)]:
+        vals = []
+        for sgn in (1, -1):
+            s2 = [dict(st[0], pos=st[0]["pos"].copy())]
+            s2[0]["pos"][i, c] += sgn * h
+            vals.append(m(build_graph(s2, kw["rc"]), forces=False)["energy"].item())
+        fd = -(vals[0] - vals[1]) / (2 * h)
+        assert abs(fd - F[i, c]) < 2e-3 * (1 + abs(F[i, c])), (fd, F[i, c])

@@ -1,0 +1,103 @@
+"""CPU checks of the boundary: the C-ABI library loads and exports every declared entry point,
+the host-side model mirror constructs the reference's seeded weights. No GPU calls."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+import torch
+
+from golden.cases import BIG_CASES, SMALL_CASES
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+GOLD = os.path.join(REPO, "tests", "golden")
+
+
+def header_symbols():
+    src = open(os.path.join(REPO, "include", "face_hip.h")).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+(face_\w+)\s*\(", src, re.M)))
+
+
+def test_header_declares_the_boundary():
+    names = header_symbols()
+    for n in ["face_density_fwd", "face_density_bwd", "face_cp_density_fwd", "face_cp_density_bwd",
+              "face_node_fwd", "face_node_bwd", "face_nbr_count", "face_nbr_fill", "face_nbr_rev",
+              "face_edge_geom_fwd", "face_edge_geom_bwd", "face_force_scatter"]:
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol():
+    from face_amd import _lib
+    L = ctypes.CDLL(_lib.LIB_PATH)
+    for n in header_symbols():
+        assert hasattr(L, n), n
+    assert set(header_symbols()) == set(_lib.exported_symbols())
+
+
+def test_library_metadata_without_gpu():
+    from face_amd import _lib
+    L = _lib.lib()
+    assert L.face_hip_abi_version() == _lib.ABI_VERSION
+    assert b"invalid argument" in L.face_hip_error_string(-1)
+    assert b"capacity" in L.face_hip_error_string(-3)
+
+
+def test_host_rejects_bad_shapes_before_launch():
+    from face_amd import _lib
+    L = _lib.lib()
+    # negative sizes / unsupported monomial counts are refused without touching the device
+    assert L.face_density_fwd(None, 16, None, 32, None, None, 20, 7, None, 10, 4, 16, 32, None, None) == -1
+    assert L.face_cp_density_bwd(None, 4, None, 1, None, None, 20, None, 1, 1, 1, 300, None, None, 0, None, 0,
+                                 None, 0, None) == -1
+    assert L.face_density_fwd(None, 16, None, 32, None, None, 20, 20, None, 0, 4, 16, 32, None, None) == 0
+
+
+def test_cpu_tensors_are_refused():
+    from face_amd.kernels import factor_density
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        factor_density(torch.zeros(2, 3, 4), torch.zeros(2, 3, 5), torch.zeros(2, 3, 20))
+
+
+@pytest.mark.parametrize("name", list(SMALL_CASES))
+def test_product_model_is_seed_faithful(name):
+    from face_amd import model as fm
+    kw, el, _ = SMALL_CASES[name]
+    d = np.load(os.path.join(GOLD, f"{name}_f32.npz"))
+    torch.manual_seed(0)
+    m = fm.FACE(el, **kw)
+    fm.unit_parameterise(m)
+    sd = m.state_dict()
+    assert list(sd.keys()) == list(d["state_keys"])
+    for k, v in sd.items():
+        assert np.array_equal(v.numpy(), d["state/" + k]), k
+
+
+@pytest.mark.parametrize("name", list(BIG_CASES))
+def test_product_model_checksums_at_benchmark_widths(name):
+    from face_amd import model as fm
+    kw, el, _ = BIG_CASES[name]
+    d = np.load(os.path.join(GOLD, f"{name}_f32.npz"))
+    torch.manual_seed(0)
+    m = fm.FACE(el, **kw)
+    fm.unit_parameterise(m)
+    for k, v in m.state_dict().items():
+        assert np.array_equal(v.double().numpy().reshape(-1)[:4], d["head/" + k]), k
+
+
+def test_synthetic_workloads_follow_the_recipes():
+    from face_amd import systems
+    mols, kw, el, _ = systems.workload(0)
+    assert len(mols) == 64 and all(len(m["pos"]) == 21 for m in mols)
+    for m in mols[:8]:
+        p = m["pos"]
+        d = np.linalg.norm(p[:, None] - p[None], axis=-1) + np.eye(21) * 9
+        assert d.min() > 1.0 - 0.5 and np.linalg.norm(p, axis=1).max() < 3.5 + 0.3
+    (fcc,), kw2, el2, _ = systems.workload(2)
+    assert len(fcc["pos"]) == 864 and el2 == [47] and abs(fcc["cell"][0, 0] - 24.54) < 1e-9
+    (liq,), kw3, _, _ = systems.workload(3, n_atoms=3000)
+    assert len(liq["pos"]) == 3000 and kw3["cp"] and kw3["C"] == 160
+    L = liq["cell"][0, 0]
+    assert abs(3000 / L ** 3 - 0.10) < 1e-9
+    assert systems.liquid_counts(24000) == [9143, 10286, 4571]
+    assert systems.liquid_counts(100000) == [38095, 42857, 19048]

@@ -1,0 +1,317 @@
+"""Pins the CPU oracle: golden vectors from the reference, closed forms, brute force,
+invariances. No GPU needed."""
+import itertools
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import cartesian, ops
+from oracle import model as omodel
+from oracle.neighbors import pair_list, padded_graph
+from golden.cases import BIG_CASES, SMALL_CASES
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def load(name):
+    return np.load(os.path.join(GOLD, name + ".npz"))
+
+
+def graph_of(d, dtype):
+    return {"pos": torch.tensor(d["pos"], dtype=dtype), "Z": torch.tensor(d["Z"]), "nbr": torch.tensor(d["nbr"]),
+            "shift": torch.tensor(d["shift"], dtype=dtype), "mask": torch.tensor(d["mask"]),
+            "batch": torch.tensor(d["batch"])}
+
+
+def build_oracle(kw, elements, dtype, seed=0):
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(dtype)
+    try:
+        torch.manual_seed(seed)
+        m = omodel.FACE(elements, **kw)
+        omodel.unit_parameterise(m)
+    finally:
+        torch.set_default_dtype(prev)
+    return m.eval()
+
+
+# ----------------------------------------------------------------------------- cartesian tables
+def test_monomials_are_outer_products():
+    torch.manual_seed(0)
+    u = torch.nn.functional.normalize(torch.randn(9, 3, dtype=torch.float64), dim=-1)
+    Y = cartesian.monomials(u)
+    for l, sl in cartesian.RANK_SLICE.items():
+        full = torch.ones(9, dtype=torch.float64)
+        for _ in range(l):
+            full = full[..., None] * u.view(9, *([1] * (full.dim() - 1)), 3)
+        assert torch.allclose(cartesian.expand(Y[:, sl], l), full.reshape(9, *([3] * l)), atol=1e-15)
+
+
+def test_sym_tables_cover_each_multiset_once():
+    for l in range(4):
+        tuples = cartesian.SYM_IDX[l]
+        assert sorted(set(tuples)) == sorted(set(tuple(sorted(t)) for t in itertools.product(range(3), repeat=l)))
+        assert len(tuples) == len(set(tuples))
+        idx = cartesian.full_to_sym_index(l)
+        assert idx.numel() == 3 ** l and torch.bincount(idx).sum() == 3 ** l
+
+
+# ----------------------------------------------------------------------------- density
+def test_factor_density_matches_loops_and_gradients():
+    torch.manual_seed(0)
+    N, M, B, K = 3, 4, 2, 3
+    phi = torch.randn(N, M, B, dtype=torch.float64, requires_grad=True)
+    msg = torch.randn(N, M, K, dtype=torch.float64, requires_grad=True)
+    Y = torch.randn(N, M, 20, dtype=torch.float64, requires_grad=True)
+    D = ops.factor_density(phi, msg, Y)
+    ref = torch.zeros(N, 20, B * K, dtype=torch.float64)
+    for i, m, b, k, x in itertools.product(range(N), range(M), range(B), range(K), range(20)):
+        ref[i, x, b * K + k] += phi[i, m, b] * msg[i, m, k] * Y[i, m, x]
+    assert torch.allclose(D, ref.detach(), atol=1e-13)
+    assert torch.autograd.gradcheck(ops.factor_density, (phi, msg, Y))
+
+
+def test_cp_density_is_rank_diagonal_of_full_pooling():
+    torch.manual_seed(1)
+    N, M, C = 2, 5, 3
+    R = torch.randn(N, M, 4, C, dtype=torch.float64)
+    msg = torch.randn(N, M, C, dtype=torch.float64)
+    Y = torch.randn(N, M, 20, dtype=torch.float64)
+    A = ops.cp_density(R, msg, Y)
+    full = torch.einsum("nmlc,nmc,nmx->nxlc", R, msg, Y)       # all 20 x 4 blocks
+    for l, sl in cartesian.RANK_SLICE.items():
+        assert torch.allclose(A[:, sl], full[:, sl, l], atol=1e-13)
+
+
+# ----------------------------------------------------------------------------- node algebra
+def _rot(seed):
+    g = torch.Generator().manual_seed(seed)
+    q, _ = torch.linalg.qr(torch.randn(3, 3, generator=g, dtype=torch.float64))
+    return q * torch.sign(torch.det(q))
+
+
+def _sym_inputs(N, C, seed):
+    g = torch.Generator().manual_seed(seed)
+    shapes = [3, 3, 3, 6, 6, 6, 10, 10]
+    return [torch.randn(N, C, s, generator=g, dtype=torch.float64) for s in shapes]
+
+
+def test_node_algebra_invariance_and_equivariance():
+    xs = _sym_inputs(4, 5, 0)
+    a = torch.randn(4, 5, dtype=torch.float64)
+    b = torch.randn(4, 5, dtype=torch.float64)
+    ranks = [1, 1, 1, 2, 2, 2, 3, 3]
+    full = [cartesian.expand(x, l) for x, l in zip(xs, ranks)]
+    inv, V, Mf = ops.node_algebra_full(*full, a, b)
+    Q = _rot(3)
+    rot = []
+    for x, l in zip(full, ranks):
+        for ax in range(l):
+            x = torch.movedim(torch.tensordot(x, Q, dims=([x.dim() - l + ax], [1])), -1, x.dim() - l + ax)
+        rot.append(x)
+    inv2, V2, Mf2 = ops.node_algebra_full(*rot, a, b)
+    assert torch.allclose(inv2, inv, atol=1e-10)
+    assert torch.allclose(V2, V @ Q.T, atol=1e-10)
+    assert torch.allclose(Mf2, Q @ Mf @ Q.T, atol=1e-10)
+
+
+def test_node_algebra_hand_expanded_tiny_case():
+    # one atom, one channel: explicit index sums of the eight families and the two products
+    xs = _sym_inputs(1, 1, 5)
+    a = torch.tensor([[0.3], [-1.1], [0.7], [2.0]], dtype=torch.float64)
+    b = torch.tensor([[1.3], [0.4], [-0.6], [0.9]], dtype=torch.float64)
+    ranks = [1, 1, 1, 2, 2, 2, 3, 3]
+    P1, Q1, S1, P2, Q2, S2, P3, Q3 = [cartesian.expand(x, l)[0, 0] for x, l in zip(xs, ranks)]
+    R3 = range(3)
+    want = [
+        sum(P1[i] * Q1[i] for i in R3),
+        sum(P2[i, j] * Q2[i, j] for i in R3 for j in R3),
+        sum(P3[i, j, k] * Q3[i, j, k] for i in R3 for j in R3 for k in R3),
+        sum(P1[i] * Q2[i, j] * S1[j] for i in R3 for j in R3),
+        sum(P2[i, j] * Q2[j, k] * S2[k, i] for i in R3 for j in R3 for k in R3),
+        sum(P3[i, j, k] * Q2[j, k] * S1[i] for i in R3 for j in R3 for k in R3),
+        sum(P3[i, j, k] * Q3[i, j, m] * S2[k, m] for i in R3 for j in R3 for k in R3 for m in R3),
+        sum(P3[i, j, k] * Q1[i] * S1[j] * Q1[k] for i in R3 for j in R3 for k in R3),
+    ]
+    inv, V, Mf = ops.node_algebra_sym(*xs, a, b)
+    assert torch.allclose(inv[0, 0], torch.stack(want), rtol=1e-12, atol=1e-12)
+    Vw = torch.stack([a[0, 0] * P1[i] + a[1, 0] * sum(Q2[i, j] * S1[j] for j in R3)
+                      + a[2, 0] * sum(P3[i, j, k] * Q2[j, k] for j in R3 for k in R3)
+                      + a[3, 0] * sum(P2[i, j] * Q1[j] for j in R3) for i in R3])
+    assert torch.allclose(V[0, 0], Vw, atol=1e-12)
+    Mw = torch.stack([torch.stack([b[0, 0] * P2[i, k] + b[1, 0] * P1[i] * Q1[k]
+                                   + b[2, 0] * sum(P2[i, j] * Q2[j, k] for j in R3)
+                                   + b[3, 0] * sum(P3[i, k, j] * S1[j] for j in R3) for k in R3]) for i in R3])
+    assert torch.allclose(Mf[0, 0], Mw, atol=1e-12)
+
+
+# ----------------------------------------------------------------------------- transport
+def test_transport_sums_explicit_per_edge():
+    """The reference's own per-edge transport check (tests/test_transport_map.py), restated."""
+    torch.manual_seed(0)
+    N, M, B, Kd = 2, 3, 2, 2
+    phi = torch.randn(N, M, B, dtype=torch.float64)
+    u = torch.nn.functional.normalize(torch.randn(N, M, 3, dtype=torch.float64), dim=-1)
+    Vt = torch.randn(N, M, Kd, 3, dtype=torch.float64)
+    Mt = torch.randn(N, M, Kd, 6, dtype=torch.float64)
+    D1, D2 = ops.transport_sums(phi, u, Vt, Mt, 2.0)
+    Mf = cartesian.expand(Mt, 2)
+    for n, b, k in itertools.product(range(N), range(B), range(Kd)):
+        V = sum(phi[n, m, b] * Vt[n, m, k] for m in range(M)) / 2
+        Mu = sum(phi[n, m, b] * (Mf[n, m, k] @ u[n, m]) for m in range(M)) / 2
+        Ms = sum(phi[n, m, b] * Mt[n, m, k] for m in range(M)) / 2
+        uv = sum(phi[n, m, b] * 0.5 * (torch.outer(u[n, m], Vt[n, m, k]) + torch.outer(Vt[n, m, k], u[n, m]))
+                 for m in range(M)) / 2
+        assert torch.allclose(D1[n, b * 2 * Kd + k], V)
+        assert torch.allclose(D1[n, b * 2 * Kd + Kd + k], Mu)
+        assert torch.allclose(D2[n, b * 2 * Kd + k], Ms)
+        assert torch.allclose(D2[n, b * 2 * Kd + Kd + k], cartesian.to_sym2(uv))
+
+
+def test_product_transport_map_matches_explicit_sums():
+    """The (36,18) map the GPU model applies after the 4-monomial density reproduces the
+    explicit per-edge transport tensors."""
+    from face_amd.model import transport_map
+    torch.manual_seed(2)
+    E = 7
+    u = torch.nn.functional.normalize(torch.randn(E, 3, dtype=torch.float64), dim=-1)
+    V = torch.randn(E, 3, dtype=torch.float64)
+    Ms = torch.randn(E, 6, dtype=torch.float64)
+    Y4 = torch.cat([torch.ones(E, 1, dtype=torch.float64), u], 1)
+    X = (Y4[:, :, None] * torch.cat([V, Ms], 1)[:, None, :]).reshape(E, 36)
+    D = X @ transport_map()
+    M = cartesian.expand(Ms, 2)
+    uV = 0.5 * (torch.einsum("ea,eb->eab", u, V) + torch.einsum("ea,eb->eab", V, u))
+    want = torch.cat([V, torch.einsum("eab,eb->ea", M, u), Ms, cartesian.to_sym2(uV)], 1)
+    assert torch.allclose(D, want, atol=1e-13)
+
+
+# ----------------------------------------------------------------------------- neighbour list
+def _naive_pairs(pos, cell, pbc, rc, span=3):
+    out = []
+    rng = [range(-span, span + 1) if p else range(0, 1) for p in pbc]
+    for i in range(len(pos)):
+        for j in range(len(pos)):
+            for S in itertools.product(*rng):
+                if i == j and S == (0, 0, 0):
+                    continue
+                d = pos[j] - pos[i] + np.asarray(S) @ cell
+                if np.sqrt((d * d).sum()) < rc:
+                    out.append((i, j, *S))
+    return sorted(out)
+
+
+@pytest.mark.parametrize("pbc", [(1, 1, 1), (1, 0, 1), (0, 0, 0)])
+def test_pair_list_matches_naive_images(pbc):
+    rng = np.random.default_rng(3)
+    cell = np.array([[5.0, 0.3, 0.0], [0.4, 4.6, 0.2], [0.1, -0.3, 5.4]])
+    pos = rng.random((9, 3)) @ cell + rng.normal(0, 2.0, (9, 3))     # not wrapped
+    i, j, S = pair_list(pos, cell, pbc, 4.1)
+    got = sorted(zip(i.tolist(), j.tolist(), *S.T.tolist()))
+    assert got == _naive_pairs(pos, cell, pbc, 4.1)
+    # canonical order and symmetry
+    assert [tuple(x) for x in np.c_[i, j, S]] == got
+    fw = {(a, b, *s) for a, b, s in zip(i, j, S.tolist())}
+    assert all((b, a, *(-np.asarray(s))) in fw for a, b, *s in fw)
+
+
+def test_fcc_shell_counts():
+    from face_amd import systems
+    st = systems.fcc(4.09, 3, 0.0, np.random.default_rng(0))
+    i, _, _ = pair_list(st["pos"], st["cell"], st["pbc"], 4.5)
+    assert (np.bincount(i) == 18).all()          # 12 nearest (2.89 A) + 6 second shell (4.09 A)
+
+
+# ----------------------------------------------------------------------------- model vs golden
+@pytest.mark.parametrize("name", list(SMALL_CASES))
+@pytest.mark.parametrize("tag", ["f64", "f32"])
+def test_oracle_state_dict_is_seed_faithful(name, tag):
+    kw, el, _ = SMALL_CASES[name]
+    d = load(f"{name}_{tag}")
+    m = build_oracle(kw, el, torch.float64 if tag == "f64" else torch.float32)
+    sd = m.state_dict()
+    assert list(sd.keys()) == list(d["state_keys"])
+    for k, v in sd.items():
+        assert np.array_equal(v.numpy(), d["state/" + k]), k
+
+
+@pytest.mark.parametrize("name", list(BIG_CASES))
+def test_oracle_weights_checksums_at_benchmark_widths(name):
+    kw, el, _ = BIG_CASES[name]
+    d = load(f"{name}_f32")
+    m = build_oracle(kw, el, torch.float32)
+    sd = m.state_dict()
+    assert list(sd.keys()) == list(d["state_keys"])
+    for k, v in sd.items():
+        v = v.double().numpy()
+        assert np.array_equal(v.reshape(-1)[:4], d["head/" + k]), k
+        assert np.allclose([v.sum(), np.abs(v).sum(), (v * v).sum()], d["sum/" + k], rtol=1e-12, atol=0), k
+
+
+def _check_EF(m, d, dtype, rtolE, ftol):
+    o = m(graph_of(d, dtype))
+    E, F = o["energy"].detach().numpy(), o["forces"].detach().numpy()
+    Eg, Fg = d["energy"], d["forces"]
+    assert np.abs(E - Eg).max() <= rtolE * np.abs(Eg).max(), (E, Eg)
+    rms = np.sqrt((Fg ** 2).mean())
+    assert np.abs(F - Fg).max() <= ftol * rms, np.abs(F - Fg).max() / rms
+
+
+@pytest.mark.parametrize("name", list(SMALL_CASES))
+def test_oracle_energy_forces_f64(name):
+    kw, el, _ = SMALL_CASES[name]
+    d = load(f"{name}_f64")
+    _check_EF(build_oracle(kw, el, torch.float64), d, torch.float64, 1e-11, 1e-9)
+
+
+@pytest.mark.parametrize("name", list(SMALL_CASES))
+def test_oracle_energy_forces_f32(name):
+    kw, el, _ = SMALL_CASES[name]
+    d = load(f"{name}_f32")
+    _check_EF(build_oracle(kw, el, torch.float32), d, torch.float32, 1e-5, 1e-4)
+
+
+@pytest.mark.parametrize("name", list(BIG_CASES))
+def test_oracle_energy_forces_benchmark_widths(name):
+    kw, el, _ = BIG_CASES[name]
+    d = load(f"{name}_f32")
+    _check_EF(build_oracle(kw, el, torch.float32), d, torch.float32, 1e-5, 1e-4)
+
+
+def test_oracle_model_invariances_f64():
+    """Rotation/reflection, translation, permutation and finite-difference forces
+    (tests/test_symmetry.py:24-52 of the reference), on the small flagship model."""
+    kw, el, _ = SMALL_CASES["small_flag_mol"]
+    m = build_oracle(kw, el, torch.float64)
+    g0 = torch.Generator().manual_seed(0)
+    with torch.no_grad():
+        for p in m.parameters():
+            p.add_(0.1 * torch.randn(p.shape, generator=g0, dtype=p.dtype))
+    rng = np.random.default_rng(5)
+    pos = rng.normal(0, 1.4, (10, 3))
+    Z = np.array([1, 6, 8, 6, 1, 8, 6, 1, 6, 8])
+
+    def run(p, forces=True):
+        st = [{"pos": p, "Z": Z, "cell": np.zeros((3, 3)), "pbc": np.zeros(3, bool)}]
+        g = padded_graph(st, kw["rc"], dtype=torch.float64)
+        return m({k: g[k] for k in ("pos", "Z", "nbr", "shift", "mask", "batch")}, forces=forces)
+
+    o = run(pos)
+    E, F = o["energy"].item(), o["forces"].detach().numpy()
+    Q = _rot(7).numpy()
+    o2 = run(pos @ Q.T + np.array([0.3, -1.2, 2.0]))
+    assert abs(o2["energy"].item() - E) < 1e-9 and np.abs(o2["forces"].detach().numpy() - F @ Q.T).max() < 1e-8
+    perm = rng.permutation(10)
+    st = [{"pos": pos[perm], "Z": Z[perm], "cell": np.zeros((3, 3)), "pbc": np.zeros(3, bool)}]
+    g = padded_graph(st, kw["rc"], dtype=torch.float64)
+    o3 = m({k: g[k] for k in ("pos", "Z", "nbr", "shift", "mask", "batch")})
+    assert abs(o3["energy"].item() - E) < 1e-9 and np.abs(o3["forces"].detach().numpy() - F[perm]).max() < 1e-8
+    h = 1e-5
+    for i, c in [(0, 0), (3, 2), (7, 1)]:
+        pp, pm = pos.copy(), pos.copy()
+        pp[i, c] += h
+        pm[i, c] -= h
+        fd = -(run(pp, False)["energy"].item() - run(pm, False)["energy"].item()) / (2 * h)
+        assert abs(fd - F[i, c]) < 1e-6 * (1 + abs(fd))
