@@ -76,7 +76,7 @@ def model_for(kw, el):
     return m.cuda().eval()
 
 
-def run_gpu(k, steps, warmup):
+def run_gpu(k, steps, warmup, use_graph=True):
     from face_amd import _lib, systems
     from face_amd.neighbors import build_graph
     sts, kw, el, desc = systems.workload(k)
@@ -96,14 +96,34 @@ def run_gpu(k, steps, warmup):
         step()
     torch.cuda.synchronize()
     log(f"[bench]   warm-up done ({warmup} steps)")
+    # eager pass: HIP events around every hot-kernel launch (kernel durations)
     timers = _lib.time_calls(TIMED)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
         step()
     torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
+    dt_eager = time.perf_counter() - t0
     _lib.stop_timing()
+    log(f"[bench]   eager: {1e3 * dt_eager / steps:.3f} ms/step")
+    dt = dt_eager
+    mode = "eager"
+    if use_graph:
+        # HIP-graph replay of the whole E+F step, positions copied into the static input
+        from face_amd.runner import StepGraph
+        run = StepGraph(m, g)
+        pos = g.pos.clone()
+        for _ in range(warmup):
+            run(pos)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            run(pos)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        mode = "hipgraph"
+        log(f"[bench]   graph replay: {1e3 * dt / steps:.3f} ms/step")
+        del run
     kern = {}
     for label, evs in timers.items():
         if not evs:
@@ -117,7 +137,8 @@ def run_gpu(k, steps, warmup):
     ms_step = 1e3 * dt / steps
     log(f"[bench]   {ms_step:.3f} ms/step, {g.N * steps / dt:.0f} atom-steps/s")
     return {"N": g.N, "E": g.E, "ms_per_step": ms_step, "atom_steps_per_s": g.N * steps / dt, "kernels": kern,
-            "pairlist_ms": 1e3 * t_nbr, "desc": desc, "kw": kw}
+            "pairlist_ms": 1e3 * t_nbr, "desc": desc, "kw": kw, "mode": mode,
+            "eager_ms_per_step": 1e3 * dt_eager / steps}
 
 
 def run_cpu(k, n_atoms, rounds=5, warm=2):
@@ -156,6 +177,7 @@ def main():
     ap.add_argument("--also", default="2", help="comma list of extra workloads reported under 'also'")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-atoms", type=int, default=1500)
+    ap.add_argument("--eager", action="store_true", help="time eager steps instead of HIP-graph replays")
     a = ap.parse_args()
     if a.gpus != 1:
         print("bench.py measures one GPU: every box here has one MI355X and this build has no multi-GPU "
@@ -167,14 +189,15 @@ def main():
     torch.backends.cuda.matmul.allow_tf32 = False
     torch.backends.cudnn.allow_tf32 = False
     torch.set_float32_matmul_precision("highest")
-    main_run = run_gpu(a.workload, a.steps, a.warmup)
+    main_run = run_gpu(a.workload, a.steps, a.warmup, not a.eager)
     also = {}
     for k in [int(x) for x in a.also.split(",") if x.strip()]:
         if k != a.workload:
-            r = run_gpu(k, a.steps, a.warmup)
+            r = run_gpu(k, a.steps, a.warmup, not a.eager)
             also[f"workload{k}"] = {"desc": r["desc"], "atoms": r["N"], "pairs": r["E"],
                                     "atom_steps_per_s": r["atom_steps_per_s"], "ms_per_step": r["ms_per_step"],
-                                    "pairlist_ms": r["pairlist_ms"],
+                                    "pairlist_ms": r["pairlist_ms"], "mode": r["mode"],
+                                    "eager_ms_per_step": r["eager_ms_per_step"],
                                     "kernels": {kk: {"avg_us": v["avg_us"], "GBps": v["GBps"]}
                                                 for kk, v in r["kernels"].items()}}
     kern = main_run["kernels"]
@@ -198,7 +221,8 @@ def main():
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": main_run["desc"], "atoms": main_run["N"], "pairs": main_run["E"],
                    "model": {k: kw[k] for k in ("C", "B", "K", "rc") if k in kw} | {"cp": bool(kw.get("cp"))},
-                   "weights": "random init, torch.manual_seed(0) + unit_parameterise", "parallelism": "single GPU"},
+                   "weights": "random init, torch.manual_seed(0) + unit_parameterise", "parallelism": "single GPU",
+                   "step": main_run["mode"], "eager_ms_per_step": main_run["eager_ms_per_step"]},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": {k: {"avg_us": v["avg_us"], "launches_per_step": v["launches_per_step"], "GBps": v["GBps"],

@@ -176,6 +176,110 @@ __global__ __launch_bounds__(256) void force_scatter_kernel(const float* __restr
     grad[k * 3 + 2] = sign * s2;
 }
 
+// ---------------------------------------------------------------- directional edge features
+// Node table T (N, 9, Kd): per channel k, rows 0-2 = V, rows 3-8 = M in sym storage.
+// d[e] = [u.V_j | Y2w.M_j | u.V_i | Y2w.M_i] (4 x Kd), u = Y[1:4], Y2w = Y[4:10] * (1,1,1,2,2,2),
+// j = col[e], i = recv[e]   (face/model.py:474-493).
+__device__ __forceinline__ void dir_weights(const float* __restrict__ y, float* w) {
+    w[0] = y[1]; w[1] = y[2]; w[2] = y[3];
+    w[3] = y[4]; w[4] = y[5]; w[5] = y[6];
+    w[6] = y[7] * 2.f; w[7] = y[8] * 2.f; w[8] = y[9] * 2.f;
+}
+
+__global__ __launch_bounds__(256) void dir_feats_fwd_kernel(const float* __restrict__ T, int Kd,
+                                                            const int32_t* __restrict__ recv,
+                                                            const int32_t* __restrict__ col,
+                                                            const float* __restrict__ Y, int64_t E,
+                                                            float* __restrict__ d) {
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (t >= E * Kd) return;
+    const int64_t e = t / Kd;
+    const int k = (int)(t - e * Kd);
+    float w[9];
+    dir_weights(Y + e * 20, w);
+    const float* Tj = T + (int64_t)col[e] * 9 * Kd + k;
+    const float* Ti = T + (int64_t)recv[e] * 9 * Kd + k;
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+    for (int q = 0; q < 3; ++q) {
+        a0 = fmaf(w[q], Tj[q * Kd], a0);
+        a2 = fmaf(w[q], Ti[q * Kd], a2);
+    }
+#pragma unroll
+    for (int q = 3; q < 9; ++q) {
+        a1 = fmaf(w[q], Tj[q * Kd], a1);
+        a3 = fmaf(w[q], Ti[q * Kd], a3);
+    }
+    float* de = d + e * 4 * Kd + k;
+    de[0] = a0;
+    de[Kd] = a1;
+    de[2 * Kd] = a2;
+    de[3 * Kd] = a3;
+}
+
+// dL/dY for the directional features (monomials 1..9 only; 0 and 10..19 are written as 0).
+__global__ __launch_bounds__(256) void dir_feats_bwd_edge_kernel(const float* __restrict__ T, int Kd,
+                                                                 const int32_t* __restrict__ recv,
+                                                                 const int32_t* __restrict__ col,
+                                                                 const float* __restrict__ gd, int64_t E,
+                                                                 float* __restrict__ gY) {
+    const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    const float* Tj = T + (int64_t)col[e] * 9 * Kd;
+    const float* Ti = T + (int64_t)recv[e] * 9 * Kd;
+    const float* g = gd + e * 4 * Kd;
+    float acc[9];
+#pragma unroll
+    for (int q = 0; q < 9; ++q) acc[q] = 0.f;
+    for (int k = 0; k < Kd; ++k) {
+        const float g0 = g[k], g1 = g[Kd + k], g2 = g[2 * Kd + k], g3 = g[3 * Kd + k];
+#pragma unroll
+        for (int q = 0; q < 3; ++q) acc[q] += g0 * Tj[q * Kd + k] + g2 * Ti[q * Kd + k];
+#pragma unroll
+        for (int q = 3; q < 9; ++q) acc[q] += g1 * Tj[q * Kd + k] + g3 * Ti[q * Kd + k];
+    }
+    float* o = gY + e * 20;
+    o[0] = 0.f;
+#pragma unroll
+    for (int q = 0; q < 6; ++q) o[1 + q] = acc[q];
+#pragma unroll
+    for (int q = 6; q < 9; ++q) o[1 + q] = 2.f * acc[q];
+#pragma unroll
+    for (int x = 10; x < 20; ++x) o[x] = 0.f;
+}
+
+// dL/dT[n, q, k] = sum_{e in row n} ( gd[rev e, s(q) Kd + k] w_q(rev e) + gd[e, (2 + s(q)) Kd + k] w_q(e) ),
+// s(q) = 0 for the V rows, 1 for the M rows: the neighbour half through the reverse map, the
+// receiver half from the row itself. Thread = (atom n, channel k).
+__global__ __launch_bounds__(256) void dir_feats_bwd_node_kernel(int Kd, const int32_t* __restrict__ row_ptr,
+                                                                 const int32_t* __restrict__ rev,
+                                                                 const float* __restrict__ Y,
+                                                                 const float* __restrict__ gd, int64_t N,
+                                                                 float* __restrict__ gT) {
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (t >= N * Kd) return;
+    const int64_t n = t / Kd;
+    const int k = (int)(t - n * Kd);
+    float acc[9];
+#pragma unroll
+    for (int q = 0; q < 9; ++q) acc[q] = 0.f;
+    for (int64_t e = row_ptr[n]; e < row_ptr[n + 1]; ++e) {
+        const int64_t r = rev[e];
+        float wr[9], we[9];
+        dir_weights(Y + r * 20, wr);
+        dir_weights(Y + e * 20, we);
+        const float gr0 = gd[r * 4 * Kd + k], gr1 = gd[r * 4 * Kd + Kd + k];
+        const float ge2 = gd[e * 4 * Kd + 2 * Kd + k], ge3 = gd[e * 4 * Kd + 3 * Kd + k];
+#pragma unroll
+        for (int q = 0; q < 3; ++q) acc[q] += gr0 * wr[q] + ge2 * we[q];
+#pragma unroll
+        for (int q = 3; q < 9; ++q) acc[q] += gr1 * wr[q] + ge3 * we[q];
+    }
+    float* o = gT + n * 9 * Kd + k;
+#pragma unroll
+    for (int q = 0; q < 9; ++q) o[q * Kd] = acc[q];
+}
+
 static unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace face
@@ -247,6 +351,33 @@ extern "C" int face_force_scatter(const float* gvec, const int32_t* row_ptr, con
     if (!gvec || !row_ptr || !rev || !grad) return FACE_ERR_ARG;
     hipLaunchKernelGGL(force_scatter_kernel, dim3(blocks_for(N)), dim3(256), 0, (hipStream_t)stream, gvec, row_ptr,
                        rev, N, sign, grad);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int face_dir_feats_fwd(const float* T, int32_t Kd, const int32_t* recv, const int32_t* col, const float* Y,
+                                  int64_t E, float* d, void* stream) {
+    if (E < 0 || Kd <= 0) return FACE_ERR_ARG;
+    if (E == 0) return 0;
+    if (!T || !recv || !col || !Y || !d) return FACE_ERR_ARG;
+    hipLaunchKernelGGL(dir_feats_fwd_kernel, dim3(blocks_for(E * Kd)), dim3(256), 0, (hipStream_t)stream, T, Kd, recv,
+                       col, Y, E, d);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int face_dir_feats_bwd(const float* T, int32_t Kd, const int32_t* row_ptr, const int32_t* recv,
+                                  const int32_t* col, const int32_t* rev, const float* Y, const float* gd, int64_t N,
+                                  int64_t E, float* gT, float* gY, void* stream) {
+    if (E < 0 || N < 0 || Kd <= 0) return FACE_ERR_ARG;
+    if (!T || !row_ptr || !recv || !col || !rev || !Y || !gd) return FACE_ERR_ARG;
+    hipStream_t st = (hipStream_t)stream;
+    if (gY && E > 0)
+        hipLaunchKernelGGL(dir_feats_bwd_edge_kernel, dim3(blocks_for(E)), dim3(256), 0, st, T, Kd, recv, col, gd, E,
+                           gY);
+    if (gT && N > 0)
+        hipLaunchKernelGGL(dir_feats_bwd_node_kernel, dim3(blocks_for(N * Kd)), dim3(256), 0, st, Kd, row_ptr, rev,
+                           Y, gd, N, gT);
     FACE_LAUNCH_CHECK();
     return 0;
 }

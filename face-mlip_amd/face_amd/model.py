@@ -32,7 +32,6 @@ from .neighbors import graph_from_padded
 from .ops import Graph
 
 RANKS = [(0, 1), (1, 4), (4, 10), (10, 20)]   # monomial range of each rank (face/cartesian.py:18)
-Y2_W = (1.0, 1.0, 1.0, 2.0, 2.0, 2.0)        # u^T M u weights in sym storage (face/cartesian.py:81)
 
 
 def transport_map():
@@ -185,8 +184,11 @@ class FactorBlock(nn.Module):
         N, E = g.N, g.E
         B, C, Kd = self.B, self.C, self.K
         hid = F.silu(self.rad_in(rb) + self.pair.weight[zp])
-        phi_all = run_mlp(self.radial, hid) * env[:, None]                       # (E, B [+4C])
-        phi = phi_all[:, :B]
+        h2 = F.silu(self.radial[0](hid))
+        W2, b2 = weight(self.radial[2])
+        envc = env[:, None]
+        # the last radial layer split into its phi (B) and CP (4C) column blocks: no slice copies
+        phi = F.linear(h2, W2[:B], b2[:B]) * envc                                # (E, B)
         msg_n = self.msg(h)                                                      # (N, K)
         if self.directional:
             if self.eq_in:
@@ -196,19 +198,15 @@ class FactorBlock(nn.Module):
                 src2 = torch.cat([S[2] for S in sets], -1)
             Vb = self.pvt(src1)                                                  # (N, 3, nt*Kd)
             Mb = self.pmt(src2)                                                  # (N, 6, nt*Kd)
-            T = torch.cat([Vb[..., :Kd], Mb[..., :Kd]], 1).reshape(N, 9 * Kd)    # [component][kd]
-            Tj = ops.gather_neighbour(T, g).view(E, 9, Kd)
-            Ti = ops.gather_receiver(T, g).view(E, 9, Kd)
-            u = Y[:, 1:4]
-            Y2 = Y[:, 4:10] * Y.new_tensor(Y2_W)
-            d = torch.cat([torch.einsum("ea,eak->ek", u, Tj[:, :3]), torch.einsum("ea,eak->ek", Y2, Tj[:, 3:]),
-                           torch.einsum("ea,eak->ek", u, Ti[:, :3]), torch.einsum("ea,eak->ek", Y2, Ti[:, 3:])], -1)
+            T = torch.cat([Vb[..., :Kd], Mb[..., :Kd]], 1)                       # (N, 9, Kd)
+            d = ops.dir_features(T, Y, g)                                         # (E, 4Kd)
             mj, gathered = ops.gather_neighbour(msg_n, g) + self.dir_mix(d), False
         else:
             mj, gathered = msg_n, True
         s = self.elem_scale(zidx).view(N, 4, C) / avg_nb
         if self.cp:
-            Af = ops.cp_density(phi_all[:, B:], mj, Y, g, gathered)                # (N, 20, C)
+            R = F.linear(h2, W2[B:], b2[B:]) * envc                              # (E, 4C)
+            Af = ops.cp_density(R, mj, Y, g, gathered)                            # (N, 20, C)
         else:
             Af = ops.density(phi, mj, Y, g, 20, gathered)                         # (N, 20, B*K)
         A = [self.mix[l](Af[:, a:b]) * s[:, l, None, :] for l, (a, b) in enumerate(RANKS)]   # (N, k_l, C)

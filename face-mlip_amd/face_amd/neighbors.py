@@ -20,7 +20,7 @@ from .ops import Graph
 
 # Structures with more atoms than this that are periodic on all three axes use the cell list;
 # all others use the all-pairs generator of their own structure.
-CELL_LIST_MIN_ATOMS = 1024
+CELL_LIST_MIN_ATOMS = 128
 
 
 def _as_struct(s):

@@ -146,6 +146,40 @@ def gather_receiver(X, graph):
     return out.view(graph.E, *shp[1:])
 
 
+class DirFeatures(torch.autograd.Function):
+    """Directional edge features d (E, 4Kd) from the node table T (N, 9, Kd) and the monomials
+    (face/model.py:474-493), without materialising the gathered tables."""
+
+    @staticmethod
+    def forward(ctx, T, Y, graph):
+        _lib.require_gpu(T, Y)
+        T = T.contiguous().float()
+        Y = Y.contiguous().float()
+        Kd = T.shape[2]
+        d = torch.empty(graph.E, 4 * Kd, device=T.device)
+        call("face_dir_feats_fwd", ptr(T), Kd, ptr(graph.recv), ptr(graph.col), ptr(Y), graph.E, ptr(d),
+             _lib.stream_of(T), label="dir_fwd")
+        ctx.save_for_backward(T, Y)
+        ctx.graph = graph
+        return d
+
+    @staticmethod
+    def backward(ctx, gd):
+        T, Y = ctx.saved_tensors
+        g = ctx.graph
+        gd = gd.contiguous().float()
+        Kd = T.shape[2]
+        gT = torch.empty_like(T) if ctx.needs_input_grad[0] else None
+        gY = torch.empty_like(Y) if ctx.needs_input_grad[1] else None
+        call("face_dir_feats_bwd", ptr(T), Kd, ptr(g.row_ptr), ptr(g.recv), ptr(g.col), ptr(g.rev), ptr(Y), ptr(gd),
+             g.N, g.E, ptr(gT), ptr(gY), _lib.stream_of(gd), label="dir_bwd")
+        return gT, gY, None
+
+
+def dir_features(T, Y, graph):
+    return DirFeatures.apply(T, Y, graph)
+
+
 class StructureSum(torch.autograd.Function):
     """Per-structure sum of per-atom values (atoms of a structure are contiguous)."""
 

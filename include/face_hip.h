@@ -18,6 +18,7 @@
  *   face/node_kernel.py:164-209  NodeAlgebra / node_algebra       -> face_node_fwd / _bwd
  *   face/neighbors.py:7-37       padded_graph (ASE neighbor_list) -> face_nbr_* (count, fill, rev, padded)
  *   face/model.py:670-677        edge geometry + Bessel basis     -> face_edge_geom_fwd / _bwd
+ *   face/model.py:474-493        directional edge features        -> face_dir_feats_fwd / _bwd
  *   face/model.py:670,464,692-694 index_select gathers and their index_add backward
  *                                                                  -> face_gather_rows, face_gather_rows_bwd,
  *                                                                     face_force_scatter
@@ -162,6 +163,19 @@ int face_edge_geom_bwd(const float* pos, const int32_t* recv, const int32_t* col
                        const uint8_t* mask, int64_t E, const float* freq, int32_t n_basis, float rc, float bes_scale,
                        const float* gY, const float* grb, const float* genv, const float* gr, float* gvec,
                        void* stream);
+
+/* ---------------------------------------------------------------- directional edge features
+ * Node table T (N, 9, Kd): per channel k, rows 0-2 = V_k, rows 3-8 = M_k (sym storage).
+ * d (E, 4*Kd) = [u.V_j | u^T M_j u | u.V_i | u^T M_i u] with u = Y[e,1:4], u^T M u =
+ * sum_q Y[e,4+q] * (1,1,1,2,2,2)_q * M_q, j = col[e], i = recv[e]
+ * (face/model.py:474-493, the per-edge d fed to dir_mix).                                  */
+int face_dir_feats_fwd(const float* T, int32_t Kd, const int32_t* recv, const int32_t* col, const float* Y,
+                       int64_t E, float* d, void* stream);
+/* Backward for gd = dL/dd (E, 4*Kd): gT (N, 9, Kd) through the reverse-edge map (no atomics),
+ * gY (E, 20) (monomials 0 and 10..19 written as zero). Either output may be NULL. */
+int face_dir_feats_bwd(const float* T, int32_t Kd, const int32_t* row_ptr, const int32_t* recv, const int32_t* col,
+                       const int32_t* rev, const float* Y, const float* gd, int64_t N, int64_t E, float* gT,
+                       float* gY, void* stream);
 
 /* ---------------------------------------------------------------- gathers and scatters
  * out[e, :] = X[idx[e], :] for F features (X row stride ld_X, out row stride ld_out). */

@@ -262,3 +262,29 @@ def test_edge_geometry_forward_and_backward():
                                  + (e_ref * we.double().cpu()).sum(), pc)
     errs = [rel(Y, Y2), rel(rb, rb2), rel(env, e_ref), rel(gp, gp2)]
     assert max(errs) < TOL, errs
+
+
+def test_directional_features_and_gradients():
+    """d = [u.V_j, u^T M_j u, u.V_i, u^T M_i u] (face/model.py:474-493) vs gathered einsums."""
+    from face_amd import ops
+    say("directional features")
+    for Kd, seed in ((16, 0), (4, 1), (5, 2)):
+        g = _G(37, 300, seed + 10)
+        E = sum(g.counts)
+        torch.manual_seed(seed)
+        T = torch.randn(37, 9, Kd, device=DEV, requires_grad=True)
+        Y = torch.randn(E, 20, device=DEV, requires_grad=True)
+        d = ops.dir_features(T, Y, g.G)
+        w = torch.randn_like(d)
+        gT, gY = torch.autograd.grad((d * w).sum(), (T, Y))
+        Tc = T.detach().double().cpu().requires_grad_(True)
+        Yc = Y.detach().double().cpu().requires_grad_(True)
+        col, recv = g.G.col.long().cpu(), g.G.recv.long().cpu()
+        u = Yc[:, 1:4]
+        Y2 = Yc[:, 4:10] * torch.tensor([1.0, 1, 1, 2, 2, 2], dtype=torch.float64)
+        Tj, Ti = Tc[col], Tc[recv]
+        d2 = torch.cat([(u[:, :, None] * Tj[:, :3]).sum(1), (Y2[:, :, None] * Tj[:, 3:]).sum(1),
+                        (u[:, :, None] * Ti[:, :3]).sum(1), (Y2[:, :, None] * Ti[:, 3:]).sum(1)], -1)
+        gT2, gY2 = torch.autograd.grad((d2 * w.double().cpu()).sum(), (Tc, Yc))
+        errs = [rel(d, d2), rel(gT, gT2), rel(gY, gY2)]
+        assert max(errs) < TOL, (Kd, errs)

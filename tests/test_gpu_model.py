@@ -122,3 +122,29 @@ def test_forces_are_minus_energy_gradient_fd():
             vals.append(m(build_graph(s2, kw["rc"]), forces=False)["energy"].item())
         fd = -(vals[0] - vals[1]) / (2 * h)
         assert abs(fd - F[i, c]) < 2e-3 * (1 + abs(F[i, c])), (fd, F[i, c])
+
+
+@pytest.mark.parametrize("case", ["small_flag_mol", "cfg2"])
+def test_graph_replay_matches_eager(case):
+    """HIP-graph replays with new positions, eager work in between, every replay checked."""
+    from face_amd import systems
+    from face_amd.neighbors import build_graph
+    from face_amd.runner import StepGraph
+    say("graph replay", case)
+    if case == "cfg2":
+        sts, kw, el, _ = systems.workload(2)
+    else:
+        kw, el, _ = SMALL_CASES[case]
+        sts = systems.molecules(4, np.random.default_rng(3))
+    m = product_model(kw, el)
+    g = build_graph(sts, kw["rc"])
+    run = StepGraph(m, g)
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    for k in range(4):
+        pos = g.pos + 0.01 * torch.randn(g.pos.shape, device="cuda", generator=gen)
+        E1, F1 = run(pos)
+        E1, F1 = E1.clone(), F1.clone()
+        o = m(g.with_pos(pos.clone()))                         # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.allclose(E1, o["energy"], rtol=1e-6, atol=0), (k, E1, o["energy"])
+        assert (F1 - o["forces"]).abs().max() <= 1e-5 * o["forces"].abs().max(), k
