@@ -1,16 +1,40 @@
 // Receiver-segmented density reductions for FACE (gfx950).
 //
-// Factor density  D[i,x,b*K+k] = sum_{e in row i} phi[e,b] msg[m(e),k] Y[e,x]     (face/kernels.py:3,170-178)
-// CP density      A[i,x,c]     = sum_{e in row i} R[e,l(x),c] msg[m(e),c] Y[e,x]  (face/model.py:496-502)
+// Factor density  D[i,x,b*K+k] = sum_{e in row i} phi[e,b] msg[m(e),k] Y[e,x]            (face/kernels.py:3,170-178)
+// CP density      A[i,x,c]     = sum_{e in row i} env[e] R[e,l(x),c] msg[m(e),c] Y[e,x]   (face/model.py:496-502)
 //
 // Every output row belongs to exactly one workgroup, so the reductions run in registers and
 // LDS with no global atomics; results are bitwise reproducible run to run.
+//
+// Outputs (and upstream gradients) are addressed per rank block: element (atom i, monomial x,
+// column c) lives at p[l(x)] + i*sa + (x - x0(l))*sx + c. The reference layout (N, NX, W) is
+// p[l] = base + x0(l)*W, sa = NX*W, sx = W; the model keeps each rank as its own (k_l, N, W)
+// tensor (p[l] = D_l, sa = W, sx = N*W) so the channel-mixing GEMMs read contiguous blocks.
 #include "common.h"
 
 namespace face {
 
 constexpr int kBlock = 256;
-constexpr int kTileE = 32;   // edges staged per LDS tile (forward kernels)
+constexpr int kTileE = 32;   // edges staged per LDS tile (factor forward)
+
+__host__ __device__ constexpr int rank_start(int l) { return l == 0 ? 0 : (l == 1 ? 1 : (l == 2 ? 4 : 10)); }
+
+struct RankOut {
+    float* p[4];
+    int64_t sa, sx;
+    __device__ __forceinline__ float* at(int64_t i, int x) const {
+        float* b = x < 1 ? p[0] : (x < 4 ? p[1] : (x < 10 ? p[2] : p[3]));
+        return b + i * sa + (int64_t)(x - rank_start(rank_of(x))) * sx;
+    }
+};
+struct RankIn {
+    const float* p[4];
+    int64_t sa, sx;
+    __device__ __forceinline__ const float* at(int64_t i, int x) const {
+        const float* b = x < 1 ? p[0] : (x < 4 ? p[1] : (x < 10 ? p[2] : p[3]));
+        return b + i * sa + (int64_t)(x - rank_start(rank_of(x))) * sx;
+    }
+};
 
 // ------------------------------------------------------------------ factor forward
 // Workgroup = (atom i, column chunk). Thread owns CPT columns (b,k) and NX accumulators
@@ -19,7 +43,7 @@ template <int NX, int CPT>
 __global__ __launch_bounds__(kBlock) void density_fwd_kernel(
     const float* __restrict__ phi, int ld_phi, const float* __restrict__ msg, int ld_msg,
     const int32_t* __restrict__ msg_row, const float* __restrict__ Y, int ld_Y, const int32_t* __restrict__ row_ptr,
-    int M, int B, int K, float* __restrict__ D) {
+    int M, int B, int K, RankOut D) {
     extern __shared__ float lds[];
     float* s_phi = lds;                    // kTileE * B
     float* s_msg = s_phi + kTileE * B;     // kTileE * K
@@ -74,13 +98,12 @@ __global__ __launch_bounds__(kBlock) void density_fwd_kernel(
         }
         __syncthreads();
     }
-    float* Di = D + i * (int64_t)NX * BK;
 #pragma unroll
     for (int j = 0; j < CPT; ++j) {
         if (!ok[j]) continue;
         const int c = blockIdx.y * (kBlock * CPT) + j * kBlock + tid;
 #pragma unroll
-        for (int x = 0; x < NX; ++x) Di[(int64_t)x * BK + c] = acc[j][x];
+        for (int x = 0; x < NX; ++x) D.at(i, x)[c] = acc[j][x];
     }
 }
 
@@ -95,15 +118,13 @@ template <int NX, int B, int KS>
 __global__ __launch_bounds__(kBlock) void density_bwd_kernel(
     const float* __restrict__ phi, int ld_phi, const float* __restrict__ msg, int ld_msg,
     const int32_t* __restrict__ msg_row, const float* __restrict__ Y, int ld_Y, const int32_t* __restrict__ row_ptr,
-    int M, int K, int glog, const float* __restrict__ G, float* __restrict__ dphi, int ld_dphi,
-    float* __restrict__ dmsg, int ld_dmsg, float* __restrict__ dY, int ld_dY) {
+    int M, int K, int glog, RankIn G, float* __restrict__ dphi, int ld_dphi, float* __restrict__ dmsg, int ld_dmsg,
+    float* __restrict__ dY, int ld_dY) {
     constexpr int KSP = (KS + 3) & ~3;
     extern __shared__ float lds[];
     const int GN = 1 << glog;
     const int64_t i = blockIdx.x;
-    const int BK = B * K;
     const int tid = threadIdx.x, nthr = blockDim.x;
-    const float* Gi = G + i * (int64_t)NX * BK;
     const int nslot = NX * B * GN * KSP;
     for (int p = tid; p < nslot; p += nthr) {
         const int kk = p % KSP;
@@ -112,7 +133,7 @@ __global__ __launch_bounds__(kBlock) void density_bwd_kernel(
         r /= GN;
         const int b = r % B, x = r / B;
         const int k = g * KS + kk;
-        lds[p] = (kk < KS && k < K) ? Gi[x * BK + b * K + k] : 0.f;
+        lds[p] = (kk < KS && k < K) ? G.at(i, x)[b * K + k] : 0.f;
     }
     __syncthreads();
 
@@ -137,6 +158,7 @@ __global__ __launch_bounds__(kBlock) void density_bwd_kernel(
             mg[kk] = (valid && k < K) ? msg[row * ld_msg + k] : 0.f;
             dmg[kk] = 0.f;
         }
+#pragma unroll 1
         for (int x = 0; x < NX; ++x) {
             const float y = valid ? Y[e * ld_Y + x] : 0.f;
             const float* gx = lds + ((x * B) * GN + g) * KSP;
@@ -179,14 +201,15 @@ __global__ __launch_bounds__(kBlock) void density_bwd_kernel(
 
 // ------------------------------------------------------------------ CP forward
 // Workgroup = (atom i, channel chunk); thread = channel c with 20 accumulators. Per edge it
-// streams R[e,0..3,c] and msg[m(e),c] (coalesced over c); Y is staged in LDS.
+// streams R[e,0..3,c] and msg[m(e),c] (coalesced over c); Y and env are staged in LDS.
 constexpr int kTileCP = 16;
 
 __global__ __launch_bounds__(kBlock) void cp_density_fwd_kernel(
-    const float* __restrict__ R, int ld_R, const float* __restrict__ msg, int ld_msg,
+    const float* __restrict__ R, int ld_R, const float* __restrict__ env, const float* __restrict__ msg, int ld_msg,
     const int32_t* __restrict__ msg_row, const float* __restrict__ Y, int ld_Y, const int32_t* __restrict__ row_ptr,
-    int M, int C, float* __restrict__ A) {
+    int M, int C, RankOut A) {
     __shared__ float s_Y[kTileCP * 20];
+    __shared__ float s_env[kTileCP];
     const int64_t i = blockIdx.x;
     const int tid = threadIdx.x, nthr = blockDim.x;
     const int c = blockIdx.y * nthr + tid;
@@ -202,13 +225,14 @@ __global__ __launch_bounds__(kBlock) void cp_density_fwd_kernel(
             const int t = q / 20;
             s_Y[q] = Y[(t0 + t) * ld_Y + (q - t * 20)];
         }
+        if (tid < nt) s_env[tid] = env ? env[t0 + tid] : 1.f;
         __syncthreads();
         if (ok) {
-#pragma unroll 2
+#pragma unroll 4
             for (int t = 0; t < nt; ++t) {
                 const int64_t e = t0 + t;
                 const int64_t row = msg_row ? (int64_t)msg_row[e] : e;
-                const float m = msg[row * ld_msg + c];
+                const float m = msg[row * ld_msg + c] * s_env[t];
                 const float* Re = R + e * ld_R + c;
                 const float w0 = Re[0] * m, w1 = Re[C] * m, w2 = Re[2 * C] * m, w3 = Re[3 * C] * m;
                 const float* y = s_Y + t * 20;
@@ -224,42 +248,45 @@ __global__ __launch_bounds__(kBlock) void cp_density_fwd_kernel(
         __syncthreads();
     }
     if (ok) {
-        float* Ai = A + i * (int64_t)20 * C + c;
 #pragma unroll
-        for (int x = 0; x < 20; ++x) Ai[(int64_t)x * C] = acc[x];
+        for (int x = 0; x < 20; ++x) A.at(i, x)[c] = acc[x];
     }
 }
 
 // ------------------------------------------------------------------ CP backward
-// Workgroup = atom i, one thread per channel (C <= 256). gA[i] sits in registers (channel
+// Workgroup = atom i, one thread per channel (C <= 256); gA[i] sits in registers (channel
 // view) and in LDS (monomial view). Per tile of edges:
-//   channel phase:  t_l = sum_{x in l} gA[x,c] Y[e,x];  dR[e,l,c] = msg t_l;
-//                   dmsg[e,c] = sum_l R[e,l,c] t_l;      w[e,l,c] = R msg -> LDS
-//   monomial phase: dY[e,x] = sum_c gA[x,c] w[e,l(x),c]   (lane = (edge, x), dot over c)
+//   channel phase:  t_l = sum_{x in l} gA[x,c] Y[e,x];   dR[e,l,c] = env m t_l;
+//                   dmsg[e,c] = env sum_l R[e,l,c] t_l;   w[e,l,c] = R m -> LDS
+//   monomial phase: P[e,x] = sum_c gA[x,c] w[e,l(x),c]   (lane = (edge pair, x), float4 walks)
+//                   dY[e,x] = env P[e,x];  denv[e] = sum_x Y[e,x] P[e,x]
 constexpr int kTileCPB = 8;
 
 __global__ __launch_bounds__(kBlock) void cp_density_bwd_kernel(
-    const float* __restrict__ R, int ld_R, const float* __restrict__ msg, int ld_msg,
+    const float* __restrict__ R, int ld_R, const float* __restrict__ env, const float* __restrict__ msg, int ld_msg,
     const int32_t* __restrict__ msg_row, const float* __restrict__ Y, int ld_Y, const int32_t* __restrict__ row_ptr,
-    int M, int C, const float* __restrict__ gA, float* __restrict__ dR, int ld_dR, float* __restrict__ dmsg,
-    int ld_dmsg, float* __restrict__ dY, int ld_dY) {
+    int M, int C, RankIn gA, float* __restrict__ dR, int ld_dR, float* __restrict__ dmsg, int ld_dmsg,
+    float* __restrict__ dY, int ld_dY, float* __restrict__ denv) {
     extern __shared__ float lds[];
-    const int CP1 = C + 1;                       // padded row: conflict-free column walks
-    float* s_g = lds;                            // 20 x CP1
-    float* s_w = s_g + 20 * CP1;                 // kTileCPB*4 x CP1
-    float* s_Y = s_w + kTileCPB * 4 * CP1;       // kTileCPB x 20
+    const int CS = ((C + 3) & ~3) + 4;           // row stride: float4-aligned, staggered banks
+    float* s_g = lds;                            // 20 x CS
+    float* s_w = s_g + 20 * CS;                  // kTileCPB*4 x CS
+    float* s_Y = s_w + kTileCPB * 4 * CS;        // kTileCPB x 20
+    float* s_P = s_Y + kTileCPB * 20;            // kTileCPB x 20
+    float* s_env = s_P + kTileCPB * 20;          // kTileCPB
     const int64_t i = blockIdx.x;
     const int tid = threadIdx.x, nthr = blockDim.x;
-    const float* gAi = gA + i * (int64_t)20 * C;
-    for (int q = tid; q < 20 * C; q += nthr) {
-        const int x = q / C;
-        s_g[x * CP1 + (q - x * C)] = gAi[q];
+    for (int q = tid; q < 20 * CS; q += nthr) {
+        const int x = q / CS, c = q - x * CS;
+        s_g[q] = c < C ? gA.at(i, x)[c] : 0.f;
     }
+    for (int q = tid; q < kTileCPB * 4 * CS; q += nthr) s_w[q] = 0.f;   // padding columns stay zero
     const int c = tid;
     const bool ok = c < C;
     float g[20];
 #pragma unroll
-    for (int x = 0; x < 20; ++x) g[x] = ok ? gAi[x * C + c] : 0.f;
+    for (int x = 0; x < 20; ++x) g[x] = ok ? gA.at(i, x)[c] : 0.f;
+    const int nc4 = (C + 3) >> 2;
     int64_t e0, e1;
     row_range(row_ptr, i, M, e0, e1);
     for (int64_t t0 = e0; t0 < e1; t0 += kTileCPB) {
@@ -268,14 +295,30 @@ __global__ __launch_bounds__(kBlock) void cp_density_bwd_kernel(
             const int t = q / 20;
             s_Y[q] = Y[(t0 + t) * ld_Y + (q - t * 20)];
         }
+        if (tid < nt) s_env[tid] = env ? env[t0 + tid] : 1.f;
         __syncthreads();
         if (ok) {
-            for (int t = 0; t < nt; ++t) {
+            float rv[kTileCPB][4], mv[kTileCPB];
+#pragma unroll
+            for (int t = 0; t < kTileCPB; ++t) {        // every load of the tile in flight at once
+                if (t < nt) {
+                    const int64_t e = t0 + t;
+                    const int64_t row = msg_row ? (int64_t)msg_row[e] : e;
+                    mv[t] = msg[row * ld_msg + c];
+                    const float* Re = R + e * ld_R + c;
+                    rv[t][0] = Re[0];
+                    rv[t][1] = Re[C];
+                    rv[t][2] = Re[2 * C];
+                    rv[t][3] = Re[3 * C];
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < kTileCPB; ++t) {
+                if (t >= nt) break;
                 const int64_t e = t0 + t;
-                const int64_t row = msg_row ? (int64_t)msg_row[e] : e;
-                const float m = msg[row * ld_msg + c];
-                const float* Re = R + e * ld_R + c;
-                const float r0 = Re[0], r1 = Re[C], r2 = Re[2 * C], r3 = Re[3 * C];
+                const float m = mv[t];
+                const float ev = s_env[t];
+                const float r0 = rv[t][0], r1 = rv[t][1], r2 = rv[t][2], r3 = rv[t][3];
                 const float* y = s_Y + t * 20;
                 float t0v = g[0] * y[0], t1v = 0.f, t2v = 0.f, t3v = 0.f;
 #pragma unroll
@@ -285,29 +328,50 @@ __global__ __launch_bounds__(kBlock) void cp_density_bwd_kernel(
 #pragma unroll
                 for (int x = 10; x < 20; ++x) t3v = fmaf(g[x], y[x], t3v);
                 if (dR) {
+                    const float em = ev * m;
                     float* dRe = dR + e * ld_dR + c;
-                    dRe[0] = m * t0v;
-                    dRe[C] = m * t1v;
-                    dRe[2 * C] = m * t2v;
-                    dRe[3 * C] = m * t3v;
+                    dRe[0] = em * t0v;
+                    dRe[C] = em * t1v;
+                    dRe[2 * C] = em * t2v;
+                    dRe[3 * C] = em * t3v;
                 }
-                if (dmsg) dmsg[e * ld_dmsg + c] = r0 * t0v + r1 * t1v + r2 * t2v + r3 * t3v;
-                float* w = s_w + (t * 4) * CP1 + c;
+                if (dmsg) dmsg[e * ld_dmsg + c] = ev * (r0 * t0v + r1 * t1v + r2 * t2v + r3 * t3v);
+                float* w = s_w + (t * 4) * CS + c;
                 w[0] = r0 * m;
-                w[CP1] = r1 * m;
-                w[2 * CP1] = r2 * m;
-                w[3 * CP1] = r3 * m;
+                w[CS] = r1 * m;
+                w[2 * CS] = r2 * m;
+                w[3 * CS] = r3 * m;
             }
         }
         __syncthreads();
-        if (dY) {
-            for (int q = tid; q < nt * 20; q += nthr) {
-                const int t = q / 20, x = q - t * 20;
-                const float* gx = s_g + x * CP1;
-                const float* wx = s_w + (t * 4 + rank_of(x)) * CP1;
+        if (dY || denv) {
+            const int npair = (nt + 1) >> 1;
+            for (int q = tid; q < npair * 20; q += nthr) {
+                const int tp = q / 20, x = q - tp * 20;
+                const int ta = 2 * tp, tb = ta + 1;
+                const int l = rank_of(x);
+                const float4* gx = reinterpret_cast<const float4*>(s_g + x * CS);
+                const float4* wa = reinterpret_cast<const float4*>(s_w + (ta * 4 + l) * CS);
+                const float4* wb = reinterpret_cast<const float4*>(s_w + ((tb < nt ? tb : ta) * 4 + l) * CS);
+                float sa = 0.f, sb = 0.f;
+                for (int c4 = 0; c4 < nc4; ++c4) {
+                    const float4 gv = gx[c4], av = wa[c4], bv = wb[c4];
+                    sa = fmaf(gv.x, av.x, sa); sa = fmaf(gv.y, av.y, sa); sa = fmaf(gv.z, av.z, sa); sa = fmaf(gv.w, av.w, sa);
+                    sb = fmaf(gv.x, bv.x, sb); sb = fmaf(gv.y, bv.y, sb); sb = fmaf(gv.z, bv.z, sb); sb = fmaf(gv.w, bv.w, sb);
+                }
+                s_P[ta * 20 + x] = sa;
+                if (dY) dY[(t0 + ta) * ld_dY + x] = s_env[ta] * sa;
+                if (tb < nt) {
+                    s_P[tb * 20 + x] = sb;
+                    if (dY) dY[(t0 + tb) * ld_dY + x] = s_env[tb] * sb;
+                }
+            }
+            __syncthreads();
+            if (denv && tid < nt) {
                 float s = 0.f;
-                for (int cc = 0; cc < C; ++cc) s = fmaf(gx[cc], wx[cc], s);
-                dY[(t0 + t) * ld_dY + x] = s;
+#pragma unroll
+                for (int x = 0; x < 20; ++x) s = fmaf(s_Y[tid * 20 + x], s_P[tid * 20 + x], s);
+                denv[t0 + tid] = s;
             }
         }
         __syncthreads();
@@ -315,10 +379,21 @@ __global__ __launch_bounds__(kBlock) void cp_density_bwd_kernel(
 }
 
 // ------------------------------------------------------------------ launch helpers
+static int max_lds_bytes() {
+    static int v = -1;
+    if (v < 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
+            v = 65536;
+    }
+    return v;
+}
+
 template <int NX>
 static int launch_fwd_nx(int cpt, dim3 grid, size_t lds, hipStream_t st, const float* phi, int ld_phi,
                          const float* msg, int ld_msg, const int32_t* msg_row, const float* Y, int ld_Y,
-                         const int32_t* row_ptr, int M, int B, int K, float* D) {
+                         const int32_t* row_ptr, int M, int B, int K, RankOut D) {
 #define FACE_FWD(C_)                                                                                          \
     hipLaunchKernelGGL((density_fwd_kernel<NX, C_>), grid, dim3(kBlock), lds, st, phi, ld_phi, msg, ld_msg,  \
                        msg_row, Y, ld_Y, row_ptr, M, B, K, D)
@@ -334,21 +409,10 @@ static int launch_fwd_nx(int cpt, dim3 grid, size_t lds, hipStream_t st, const f
     return 0;
 }
 
-static int max_lds_bytes() {
-    static int v = -1;
-    if (v < 0) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
-            v = 65536;
-    }
-    return v;
-}
-
 template <int NX, int B, int KS>
 static int launch_bwd3(int glog, int nthr, int64_t N, hipStream_t st, const float* phi, int ld_phi,
                        const float* msg, int ld_msg, const int32_t* msg_row, const float* Y, int ld_Y,
-                       const int32_t* row_ptr, int M, int K, const float* G, float* dphi, int ld_dphi, float* dmsg,
+                       const int32_t* row_ptr, int M, int K, RankIn G, float* dphi, int ld_dphi, float* dmsg,
                        int ld_dmsg, float* dY, int ld_dY) {
     constexpr int KSP = (KS + 3) & ~3;
     const size_t lds = (size_t)NX * B * (1 << glog) * KSP * sizeof(float);
@@ -366,8 +430,8 @@ static int launch_bwd3(int glog, int nthr, int64_t N, hipStream_t st, const floa
 template <int NX, int B>
 static int launch_bwd_b(int ks, int glog, int nthr, int64_t N, hipStream_t st, const float* phi, int ld_phi,
                         const float* msg, int ld_msg, const int32_t* msg_row, const float* Y, int ld_Y,
-                        const int32_t* row_ptr, int M, int K, const float* G, float* dphi, int ld_dphi,
-                        float* dmsg, int ld_dmsg, float* dY, int ld_dY) {
+                        const int32_t* row_ptr, int M, int K, RankIn G, float* dphi, int ld_dphi, float* dmsg,
+                        int ld_dmsg, float* dY, int ld_dY) {
 #define FACE_BWD(KS_)                                                                                            \
     return launch_bwd3<NX, B, KS_>(glog, nthr, N, st, phi, ld_phi, msg, ld_msg, msg_row, Y, ld_Y, row_ptr, M, K, \
                                    G, dphi, ld_dphi, dmsg, ld_dmsg, dY, ld_dY)
@@ -383,8 +447,8 @@ static int launch_bwd_b(int ks, int glog, int nthr, int64_t N, hipStream_t st, c
 template <int NX>
 static int launch_bwd_nx(int B, int ks, int glog, int nthr, int64_t N, hipStream_t st, const float* phi,
                          int ld_phi, const float* msg, int ld_msg, const int32_t* msg_row, const float* Y, int ld_Y,
-                         const int32_t* row_ptr, int M, int K, const float* G, float* dphi, int ld_dphi,
-                         float* dmsg, int ld_dmsg, float* dY, int ld_dY) {
+                         const int32_t* row_ptr, int M, int K, RankIn G, float* dphi, int ld_dphi, float* dmsg,
+                         int ld_dmsg, float* dY, int ld_dY) {
 #define FACE_BWDB(B_)                                                                                       \
     return launch_bwd_b<NX, B_>(ks, glog, nthr, N, st, phi, ld_phi, msg, ld_msg, msg_row, Y, ld_Y, row_ptr, \
                                 M, K, G, dphi, ld_dphi, dmsg, ld_dmsg, dY, ld_dY)
@@ -426,25 +490,49 @@ static bool plan_bwd(int K, int max_row, int& ks_out, int& glog_out, int& nthr_o
     return best > 0.0;
 }
 
+// Rank-block descriptors from the C-ABI arguments; every rank the NX monomials touch needs a pointer.
+static bool rank_out(float* const* p, int64_t sa, int64_t sx, int NX, RankOut& r) {
+    const int nr = NX == 20 ? 4 : 2;
+    for (int l = 0; l < 4; ++l) r.p[l] = (p && l < nr) ? p[l] : nullptr;
+    r.sa = sa;
+    r.sx = sx;
+    for (int l = 0; l < nr; ++l)
+        if (!r.p[l]) return false;
+    return sa > 0 && sx > 0;
+}
+static bool rank_in(const float* const* p, int64_t sa, int64_t sx, int NX, RankIn& r) {
+    const int nr = NX == 20 ? 4 : 2;
+    for (int l = 0; l < 4; ++l) r.p[l] = (p && l < nr) ? p[l] : nullptr;
+    r.sa = sa;
+    r.sx = sx;
+    for (int l = 0; l < nr; ++l)
+        if (!r.p[l]) return false;
+    return sa > 0 && sx > 0;
+}
+
 }  // namespace face
 
 using namespace face;
 
 extern "C" int face_density_fwd(const float* phi, int32_t ld_phi, const float* msg, int32_t ld_msg,
                                 const int32_t* msg_row, const float* Y, int32_t ld_Y, int32_t NX,
-                                const int32_t* row_ptr, int64_t N, int32_t M, int32_t B, int32_t K, float* D,
-                                void* stream) {
+                                const int32_t* row_ptr, int64_t N, int32_t M, int32_t B, int32_t K,
+                                float* const* D_ranks, int64_t atom_stride, int64_t x_stride, void* stream) {
     if (N < 0 || B <= 0 || K <= 0 || (NX != 4 && NX != 20)) return FACE_ERR_ARG;
     if (ld_phi < B || ld_msg < K || ld_Y < NX || (!row_ptr && M < 0)) return FACE_ERR_ARG;
     if (N == 0) return 0;
-    if (!phi || !msg || !Y || !D) return FACE_ERR_ARG;
+    RankOut D;
+    if (!phi || !msg || !Y || !rank_out(D_ranks, atom_stride, x_stride, NX, D)) return FACE_ERR_ARG;
     const int BK = B * K;
     const int opts20[3] = {1, 2, 4}, opts4[4] = {1, 2, 4, 9};
     const int* opts = NX == 20 ? opts20 : opts4;
     const int nopt = NX == 20 ? 3 : 4;
     int cpt = opts[nopt - 1];
     for (int q = 0; q < nopt; ++q)
-        if (kBlock * opts[q] >= BK) { cpt = opts[q]; break; }
+        if (kBlock * opts[q] >= BK) {
+            cpt = opts[q];
+            break;
+        }
     const unsigned chunks = (unsigned)((BK + kBlock * cpt - 1) / (kBlock * cpt));
     const size_t lds = (size_t)kTileE * (B + K + NX) * sizeof(float);
     if ((int64_t)lds > 65536) return FACE_ERR_UNSUPPORTED;
@@ -458,13 +546,15 @@ extern "C" int face_density_fwd(const float* phi, int32_t ld_phi, const float* m
 extern "C" int face_density_bwd(const float* phi, int32_t ld_phi, const float* msg, int32_t ld_msg,
                                 const int32_t* msg_row, const float* Y, int32_t ld_Y, int32_t NX,
                                 const int32_t* row_ptr, int64_t N, int32_t M, int32_t max_row, int32_t B, int32_t K,
-                                const float* G, float* dphi, int32_t ld_dphi, float* dmsg, int32_t ld_dmsg, float* dY,
-                                int32_t ld_dY, void* stream) {
+                                const float* const* G_ranks, int64_t atom_stride, int64_t x_stride, float* dphi,
+                                int32_t ld_dphi, float* dmsg, int32_t ld_dmsg, float* dY, int32_t ld_dY,
+                                void* stream) {
     if (N < 0 || B <= 0 || K <= 0 || (NX != 4 && NX != 20) || max_row < 0) return FACE_ERR_ARG;
     if (ld_phi < B || ld_msg < K || ld_Y < NX || (!row_ptr && M < 0)) return FACE_ERR_ARG;
     if ((dphi && ld_dphi < B) || (dmsg && ld_dmsg < K) || (dY && ld_dY < NX)) return FACE_ERR_ARG;
     if (N == 0 || max_row == 0) return 0;
-    if (!phi || !msg || !Y || !G) return FACE_ERR_ARG;
+    RankIn G;
+    if (!phi || !msg || !Y || !rank_in(G_ranks, atom_stride, x_stride, NX, G)) return FACE_ERR_ARG;
     int ks = 8, glog = 2, nthr = 128;
     if (!plan_bwd(K, max_row, ks, glog, nthr)) return FACE_ERR_UNSUPPORTED;
     hipStream_t st = (hipStream_t)stream;
@@ -475,36 +565,40 @@ extern "C" int face_density_bwd(const float* phi, int32_t ld_phi, const float* m
                             dphi, ld_dphi, dmsg, ld_dmsg, dY, ld_dY);
 }
 
-extern "C" int face_cp_density_fwd(const float* R, int32_t ld_R, const float* msg, int32_t ld_msg,
+extern "C" int face_cp_density_fwd(const float* R, int32_t ld_R, const float* env, const float* msg, int32_t ld_msg,
                                    const int32_t* msg_row, const float* Y, int32_t ld_Y, const int32_t* row_ptr,
-                                   int64_t N, int32_t M, int32_t C, float* A, void* stream) {
+                                   int64_t N, int32_t M, int32_t C, float* const* A_ranks, int64_t atom_stride,
+                                   int64_t x_stride, void* stream) {
     if (N < 0 || C <= 0 || ld_R < 4 * C || ld_msg < C || ld_Y < 20 || (!row_ptr && M < 0)) return FACE_ERR_ARG;
     if (N == 0) return 0;
-    if (!R || !msg || !Y || !A) return FACE_ERR_ARG;
+    RankOut A;
+    if (!R || !msg || !Y || !rank_out(A_ranks, atom_stride, x_stride, 20, A)) return FACE_ERR_ARG;
     int nthr = ((C + kWave - 1) / kWave) * kWave;
     if (nthr > kBlock) nthr = kBlock;
     dim3 grid((unsigned)N, (unsigned)((C + nthr - 1) / nthr));
-    hipLaunchKernelGGL(cp_density_fwd_kernel, grid, dim3(nthr), 0, (hipStream_t)stream, R, ld_R, msg, ld_msg, msg_row,
-                       Y, ld_Y, row_ptr, M, C, A);
+    hipLaunchKernelGGL(cp_density_fwd_kernel, grid, dim3(nthr), 0, (hipStream_t)stream, R, ld_R, env, msg, ld_msg,
+                       msg_row, Y, ld_Y, row_ptr, M, C, A);
     FACE_LAUNCH_CHECK();
     return 0;
 }
 
-extern "C" int face_cp_density_bwd(const float* R, int32_t ld_R, const float* msg, int32_t ld_msg,
+extern "C" int face_cp_density_bwd(const float* R, int32_t ld_R, const float* env, const float* msg, int32_t ld_msg,
                                    const int32_t* msg_row, const float* Y, int32_t ld_Y, const int32_t* row_ptr,
-                                   int64_t N, int32_t M, int32_t max_row, int32_t C, const float* gA, float* dR,
-                                   int32_t ld_dR, float* dmsg, int32_t ld_dmsg, float* dY, int32_t ld_dY,
-                                   void* stream) {
+                                   int64_t N, int32_t M, int32_t max_row, int32_t C, const float* const* gA_ranks,
+                                   int64_t atom_stride, int64_t x_stride, float* dR, int32_t ld_dR, float* dmsg,
+                                   int32_t ld_dmsg, float* dY, int32_t ld_dY, float* denv, void* stream) {
     if (N < 0 || C <= 0 || C > kBlock || ld_R < 4 * C || ld_msg < C || ld_Y < 20 || (!row_ptr && M < 0))
         return FACE_ERR_ARG;
     if ((dR && ld_dR < 4 * C) || (dmsg && ld_dmsg < C) || (dY && ld_dY < 20)) return FACE_ERR_ARG;
     if (N == 0 || max_row == 0) return 0;
-    if (!R || !msg || !Y || !gA) return FACE_ERR_ARG;
+    RankIn gA;
+    if (!R || !msg || !Y || !rank_in(gA_ranks, atom_stride, x_stride, 20, gA)) return FACE_ERR_ARG;
     const int nthr = ((C + kWave - 1) / kWave) * kWave;
-    const size_t lds = ((size_t)(20 + kTileCPB * 4) * (C + 1) + kTileCPB * 20) * sizeof(float);
+    const int CS = ((C + 3) & ~3) + 4;
+    const size_t lds = ((size_t)(20 + kTileCPB * 4) * CS + kTileCPB * 41) * sizeof(float);
     if ((int64_t)lds > 65536) return FACE_ERR_UNSUPPORTED;
-    hipLaunchKernelGGL(cp_density_bwd_kernel, dim3((unsigned)N), dim3(nthr), lds, (hipStream_t)stream, R, ld_R, msg,
-                       ld_msg, msg_row, Y, ld_Y, row_ptr, M, C, gA, dR, ld_dR, dmsg, ld_dmsg, dY, ld_dY);
+    hipLaunchKernelGGL(cp_density_bwd_kernel, dim3((unsigned)N), dim3(nthr), lds, (hipStream_t)stream, R, ld_R, env,
+                       msg, ld_msg, msg_row, Y, ld_Y, row_ptr, M, C, gA, dR, ld_dR, dmsg, ld_dmsg, dY, ld_dY, denv);
     FACE_LAUNCH_CHECK();
     return 0;
 }

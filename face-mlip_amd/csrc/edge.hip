@@ -177,7 +177,8 @@ __global__ __launch_bounds__(256) void force_scatter_kernel(const float* __restr
 }
 
 // ---------------------------------------------------------------- directional edge features
-// Node table T (N, 9, Kd): per channel k, rows 0-2 = V, rows 3-8 = M in sym storage.
+// Node table T: element (atom n, row q, channel k) at T[q*sq + n*sn + k]; rows 0-2 = V,
+// rows 3-8 = M in sym storage.
 // d[e] = [u.V_j | Y2w.M_j | u.V_i | Y2w.M_i] (4 x Kd), u = Y[1:4], Y2w = Y[4:10] * (1,1,1,2,2,2),
 // j = col[e], i = recv[e]   (face/model.py:474-493).
 __device__ __forceinline__ void dir_weights(const float* __restrict__ y, float* w) {
@@ -186,8 +187,8 @@ __device__ __forceinline__ void dir_weights(const float* __restrict__ y, float* 
     w[6] = y[7] * 2.f; w[7] = y[8] * 2.f; w[8] = y[9] * 2.f;
 }
 
-__global__ __launch_bounds__(256) void dir_feats_fwd_kernel(const float* __restrict__ T, int Kd,
-                                                            const int32_t* __restrict__ recv,
+__global__ __launch_bounds__(256) void dir_feats_fwd_kernel(const float* __restrict__ T, int Kd, int64_t sn,
+                                                            int64_t sq, const int32_t* __restrict__ recv,
                                                             const int32_t* __restrict__ col,
                                                             const float* __restrict__ Y, int64_t E,
                                                             float* __restrict__ d) {
@@ -197,18 +198,18 @@ __global__ __launch_bounds__(256) void dir_feats_fwd_kernel(const float* __restr
     const int k = (int)(t - e * Kd);
     float w[9];
     dir_weights(Y + e * 20, w);
-    const float* Tj = T + (int64_t)col[e] * 9 * Kd + k;
-    const float* Ti = T + (int64_t)recv[e] * 9 * Kd + k;
+    const float* Tj = T + (int64_t)col[e] * sn + k;
+    const float* Ti = T + (int64_t)recv[e] * sn + k;
     float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
 #pragma unroll
     for (int q = 0; q < 3; ++q) {
-        a0 = fmaf(w[q], Tj[q * Kd], a0);
-        a2 = fmaf(w[q], Ti[q * Kd], a2);
+        a0 = fmaf(w[q], Tj[q * sq], a0);
+        a2 = fmaf(w[q], Ti[q * sq], a2);
     }
 #pragma unroll
     for (int q = 3; q < 9; ++q) {
-        a1 = fmaf(w[q], Tj[q * Kd], a1);
-        a3 = fmaf(w[q], Ti[q * Kd], a3);
+        a1 = fmaf(w[q], Tj[q * sq], a1);
+        a3 = fmaf(w[q], Ti[q * sq], a3);
     }
     float* de = d + e * 4 * Kd + k;
     de[0] = a0;
@@ -217,41 +218,51 @@ __global__ __launch_bounds__(256) void dir_feats_fwd_kernel(const float* __restr
     de[3 * Kd] = a3;
 }
 
-// dL/dY for the directional features (monomials 1..9 only; 0 and 10..19 are written as 0).
-__global__ __launch_bounds__(256) void dir_feats_bwd_edge_kernel(const float* __restrict__ T, int Kd,
+// dL/dY for the directional features (monomials 1..9; 0 and 10..19 are written as 0).
+// Thread = (edge, channel slot); the KP lanes of an edge (KP = Kd rounded up to a power of two,
+// <= 64) sum their partial products with butterfly shuffles.
+__global__ __launch_bounds__(256) void dir_feats_bwd_edge_kernel(const float* __restrict__ T, int Kd, int KP,
+                                                                 int64_t sn, int64_t sq,
                                                                  const int32_t* __restrict__ recv,
                                                                  const int32_t* __restrict__ col,
                                                                  const float* __restrict__ gd, int64_t E,
                                                                  float* __restrict__ gY) {
-    const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    if (e >= E) return;
-    const float* Tj = T + (int64_t)col[e] * 9 * Kd;
-    const float* Ti = T + (int64_t)recv[e] * 9 * Kd;
-    const float* g = gd + e * 4 * Kd;
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;   // grid covers E*KP rounded up to 256
+    const int64_t e = t / KP;
+    const int k = (int)(t - e * KP);
+    const bool ok = e < E && k < Kd;
     float acc[9];
 #pragma unroll
     for (int q = 0; q < 9; ++q) acc[q] = 0.f;
-    for (int k = 0; k < Kd; ++k) {
-        const float g0 = g[k], g1 = g[Kd + k], g2 = g[2 * Kd + k], g3 = g[3 * Kd + k];
+    if (ok) {
+        const float* Tj = T + (int64_t)col[e] * sn + k;
+        const float* Ti = T + (int64_t)recv[e] * sn + k;
+        const float* g = gd + e * 4 * Kd + k;
+        const float g0 = g[0], g1 = g[Kd], g2 = g[2 * Kd], g3 = g[3 * Kd];
 #pragma unroll
-        for (int q = 0; q < 3; ++q) acc[q] += g0 * Tj[q * Kd + k] + g2 * Ti[q * Kd + k];
+        for (int q = 0; q < 3; ++q) acc[q] = g0 * Tj[q * sq] + g2 * Ti[q * sq];
 #pragma unroll
-        for (int q = 3; q < 9; ++q) acc[q] += g1 * Tj[q * Kd + k] + g3 * Ti[q * Kd + k];
+        for (int q = 3; q < 9; ++q) acc[q] = g1 * Tj[q * sq] + g3 * Ti[q * sq];
     }
-    float* o = gY + e * 20;
-    o[0] = 0.f;
 #pragma unroll
-    for (int q = 0; q < 6; ++q) o[1 + q] = acc[q];
+    for (int q = 0; q < 9; ++q) acc[q] = group_sum(acc[q], KP);
+    if (e < E && k == 0) {
+        float* o = gY + e * 20;
+        o[0] = 0.f;
 #pragma unroll
-    for (int q = 6; q < 9; ++q) o[1 + q] = 2.f * acc[q];
+        for (int q = 0; q < 6; ++q) o[1 + q] = acc[q];
 #pragma unroll
-    for (int x = 10; x < 20; ++x) o[x] = 0.f;
+        for (int q = 6; q < 9; ++q) o[1 + q] = 2.f * acc[q];
+#pragma unroll
+        for (int x = 10; x < 20; ++x) o[x] = 0.f;
+    }
 }
 
 // dL/dT[n, q, k] = sum_{e in row n} ( gd[rev e, s(q) Kd + k] w_q(rev e) + gd[e, (2 + s(q)) Kd + k] w_q(e) ),
 // s(q) = 0 for the V rows, 1 for the M rows: the neighbour half through the reverse map, the
 // receiver half from the row itself. Thread = (atom n, channel k).
-__global__ __launch_bounds__(256) void dir_feats_bwd_node_kernel(int Kd, const int32_t* __restrict__ row_ptr,
+__global__ __launch_bounds__(256) void dir_feats_bwd_node_kernel(int Kd, int64_t sn, int64_t sq,
+                                                                 const int32_t* __restrict__ row_ptr,
                                                                  const int32_t* __restrict__ rev,
                                                                  const float* __restrict__ Y,
                                                                  const float* __restrict__ gd, int64_t N,
@@ -275,9 +286,27 @@ __global__ __launch_bounds__(256) void dir_feats_bwd_node_kernel(int Kd, const i
 #pragma unroll
         for (int q = 3; q < 9; ++q) acc[q] += gr1 * wr[q] + ge3 * we[q];
     }
-    float* o = gT + n * 9 * Kd + k;
+    float* o = gT + n * sn + k;
 #pragma unroll
-    for (int q = 0; q < 9; ++q) o[q * Kd] = acc[q];
+    for (int q = 0; q < 9; ++q) o[q * sq] = acc[q];
+}
+
+// Per-row scalar sums with one workgroup per row (few, long rows: energies per structure).
+__global__ __launch_bounds__(256) void row_sum_kernel(const float* __restrict__ g, int ld_g,
+                                                      const int32_t* __restrict__ row_ptr,
+                                                      float* __restrict__ out, int ld_out) {
+    __shared__ float part[256];
+    const int64_t k = blockIdx.x;
+    const int tid = threadIdx.x;
+    float s = 0.f;
+    for (int64_t e = row_ptr[k] + tid; e < row_ptr[k + 1]; e += 256) s += g[e * ld_g];
+    part[tid] = s;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (tid < o) part[tid] += part[tid + o];
+        __syncthreads();
+    }
+    if (tid == 0) out[k * ld_out] = part[0];
 }
 
 static unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
@@ -338,8 +367,12 @@ extern "C" int face_segment_sum(const float* g, int32_t ld_g, const int32_t* row
     if (N < 0 || F < 0 || ld_g < F || ld_out < F) return FACE_ERR_ARG;
     if (N == 0 || F == 0) return 0;
     if (!g || !row_ptr || !out) return FACE_ERR_ARG;
-    hipLaunchKernelGGL(segment_sum_kernel, dim3(blocks_for(N * F)), dim3(256), 0, (hipStream_t)stream, g, ld_g,
-                       row_ptr, N, F, out, ld_out);
+    if (F == 1)
+        hipLaunchKernelGGL(row_sum_kernel, dim3((unsigned)N), dim3(256), 0, (hipStream_t)stream, g, ld_g, row_ptr, out,
+                           ld_out);
+    else
+        hipLaunchKernelGGL(segment_sum_kernel, dim3(blocks_for(N * F)), dim3(256), 0, (hipStream_t)stream, g, ld_g,
+                           row_ptr, N, F, out, ld_out);
     FACE_LAUNCH_CHECK();
     return 0;
 }
@@ -355,29 +388,32 @@ extern "C" int face_force_scatter(const float* gvec, const int32_t* row_ptr, con
     return 0;
 }
 
-extern "C" int face_dir_feats_fwd(const float* T, int32_t Kd, const int32_t* recv, const int32_t* col, const float* Y,
-                                  int64_t E, float* d, void* stream) {
-    if (E < 0 || Kd <= 0) return FACE_ERR_ARG;
+extern "C" int face_dir_feats_fwd(const float* T, int32_t Kd, int64_t sn, int64_t sq, const int32_t* recv,
+                                  const int32_t* col, const float* Y, int64_t E, float* d, void* stream) {
+    if (E < 0 || Kd <= 0 || sn < Kd || sq < Kd) return FACE_ERR_ARG;
     if (E == 0) return 0;
     if (!T || !recv || !col || !Y || !d) return FACE_ERR_ARG;
-    hipLaunchKernelGGL(dir_feats_fwd_kernel, dim3(blocks_for(E * Kd)), dim3(256), 0, (hipStream_t)stream, T, Kd, recv,
-                       col, Y, E, d);
+    hipLaunchKernelGGL(dir_feats_fwd_kernel, dim3(blocks_for(E * Kd)), dim3(256), 0, (hipStream_t)stream, T, Kd, sn,
+                       sq, recv, col, Y, E, d);
     FACE_LAUNCH_CHECK();
     return 0;
 }
 
-extern "C" int face_dir_feats_bwd(const float* T, int32_t Kd, const int32_t* row_ptr, const int32_t* recv,
-                                  const int32_t* col, const int32_t* rev, const float* Y, const float* gd, int64_t N,
-                                  int64_t E, float* gT, float* gY, void* stream) {
-    if (E < 0 || N < 0 || Kd <= 0) return FACE_ERR_ARG;
+extern "C" int face_dir_feats_bwd(const float* T, int32_t Kd, int64_t sn, int64_t sq, const int32_t* row_ptr,
+                                  const int32_t* recv, const int32_t* col, const int32_t* rev, const float* Y,
+                                  const float* gd, int64_t N, int64_t E, float* gT, float* gY, void* stream) {
+    if (E < 0 || N < 0 || Kd <= 0 || Kd > 64 || sn < Kd || sq < Kd) return FACE_ERR_ARG;
     if (!T || !row_ptr || !recv || !col || !rev || !Y || !gd) return FACE_ERR_ARG;
     hipStream_t st = (hipStream_t)stream;
-    if (gY && E > 0)
-        hipLaunchKernelGGL(dir_feats_bwd_edge_kernel, dim3(blocks_for(E)), dim3(256), 0, st, T, Kd, recv, col, gd, E,
-                           gY);
+    if (gY && E > 0) {
+        int KP = 1;
+        while (KP < Kd) KP <<= 1;
+        hipLaunchKernelGGL(dir_feats_bwd_edge_kernel, dim3(blocks_for(E * KP)), dim3(256), 0, st, T, Kd, KP, sn, sq,
+                           recv, col, gd, E, gY);
+    }
     if (gT && N > 0)
-        hipLaunchKernelGGL(dir_feats_bwd_node_kernel, dim3(blocks_for(N * Kd)), dim3(256), 0, st, Kd, row_ptr, rev,
-                           Y, gd, N, gT);
+        hipLaunchKernelGGL(dir_feats_bwd_node_kernel, dim3(blocks_for(N * Kd)), dim3(256), 0, st, Kd, sn, sq, row_ptr,
+                           rev, Y, gd, N, gT);
     FACE_LAUNCH_CHECK();
     return 0;
 }

@@ -24,12 +24,12 @@ F64 = ctypes.c_double
 _SIGS = {
     "face_hip_error_string": (ctypes.c_char_p, [ctypes.c_int]),
     "face_hip_abi_version": (ctypes.c_int, []),
-    "face_density_fwd": (ctypes.c_int, [P, I32, P, I32, P, P, I32, I32, P, I64, I32, I32, I32, P, P]),
-    "face_density_bwd": (ctypes.c_int, [P, I32, P, I32, P, P, I32, I32, P, I64, I32, I32, I32, I32, P, P, I32, P,
-                                        I32, P, I32, P]),
-    "face_cp_density_fwd": (ctypes.c_int, [P, I32, P, I32, P, P, I32, P, I64, I32, I32, P, P]),
-    "face_cp_density_bwd": (ctypes.c_int, [P, I32, P, I32, P, P, I32, P, I64, I32, I32, I32, P, P, I32, P, I32, P,
-                                           I32, P]),
+    "face_density_fwd": (ctypes.c_int, [P, I32, P, I32, P, P, I32, I32, P, I64, I32, I32, I32, P, I64, I64, P]),
+    "face_density_bwd": (ctypes.c_int, [P, I32, P, I32, P, P, I32, I32, P, I64, I32, I32, I32, I32, P, I64, I64, P,
+                                        I32, P, I32, P, I32, P]),
+    "face_cp_density_fwd": (ctypes.c_int, [P, I32, P, P, I32, P, P, I32, P, I64, I32, I32, P, I64, I64, P]),
+    "face_cp_density_bwd": (ctypes.c_int, [P, I32, P, P, I32, P, P, I32, P, I64, I32, I32, I32, P, I64, I64, P, I32,
+                                           P, I32, P, I32, P, P]),
     "face_node_fwd": (ctypes.c_int, [P, P, P, P, P, P, P, P, P, P, I32, I64, I32, I32, P]),
     "face_node_bwd": (ctypes.c_int, [P, P, P, P, P, P, P, P, P, P, I32, P, P, P, P, I64, I32, I32, P]),
     "face_nbr_bin": (ctypes.c_int, [P, I64, P, P, P, P, P, P, P, P, P]),
@@ -40,15 +40,15 @@ _SIGS = {
     "face_nbr_padded": (ctypes.c_int, [P, P, P, P, P, I64, I32, P, P, P, P]),
     "face_edge_geom_fwd": (ctypes.c_int, [P, P, P, P, P, I64, P, I32, F32, F32, P, P, P, P, P]),
     "face_edge_geom_bwd": (ctypes.c_int, [P, P, P, P, P, I64, P, I32, F32, F32, P, P, P, P, P, P]),
-    "face_dir_feats_fwd": (ctypes.c_int, [P, I32, P, P, P, I64, P, P]),
-    "face_dir_feats_bwd": (ctypes.c_int, [P, I32, P, P, P, P, P, P, I64, I64, P, P, P]),
+    "face_dir_feats_fwd": (ctypes.c_int, [P, I32, I64, I64, P, P, P, I64, P, P]),
+    "face_dir_feats_bwd": (ctypes.c_int, [P, I32, I64, I64, P, P, P, P, P, P, I64, I64, P, P, P]),
     "face_gather_rows": (ctypes.c_int, [P, I32, P, I64, I32, P, I32, P]),
     "face_gather_rows_bwd": (ctypes.c_int, [P, I32, P, P, I64, I32, P, I32, P]),
     "face_segment_sum": (ctypes.c_int, [P, I32, P, I64, I32, P, I32, P]),
     "face_force_scatter": (ctypes.c_int, [P, P, P, I64, F32, P, P]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 
 def lib():
@@ -135,3 +135,22 @@ def ptr_array(ts):
 
 def i64_array(vals):
     return (I64 * len(vals))(*vals)
+
+
+RANK_X0 = (0, 1, 4, 10)
+
+
+def ranks_of_dense(t):
+    """Rank-block descriptor of a reference-layout (N, NX, W) contiguous tensor."""
+    N, NX, W = t.shape
+    base = t.data_ptr()
+    nr = 4 if NX == 20 else 2
+    ptrs = [base + 4 * RANK_X0[l] * W if l < nr else None for l in range(4)]
+    return (P * 4)(*ptrs), NX * W, W
+
+
+def ranks_of_blocks(blocks):
+    """Rank-block descriptor of per-rank (k_l, N, W) contiguous tensors (2 or 4 of them)."""
+    k, N, W = blocks[0].shape
+    ptrs = [b.data_ptr() for b in blocks] + [None] * (4 - len(blocks))
+    return (P * 4)(*ptrs), W, N * W

@@ -24,8 +24,8 @@ class FactorDensity(torch.autograd.Function):
             raise ValueError(f"factor_density: shapes {tuple(phi.shape)}, {tuple(msg.shape)}, {tuple(Y.shape)}")
         phi, msg, Y = phi.contiguous().float(), msg.contiguous().float(), Y.contiguous().float()
         D = torch.empty(N, 20, B * K, device=phi.device, dtype=torch.float32)
-        call("face_density_fwd", ptr(phi), B, ptr(msg), K, None, ptr(Y), 20, 20, None, N, M, B, K, ptr(D),
-             _lib.stream_of(phi))
+        call("face_density_fwd", ptr(phi), B, ptr(msg), K, None, ptr(Y), 20, 20, None, N, M, B, K,
+             *_lib.ranks_of_dense(D), _lib.stream_of(phi))
         ctx.save_for_backward(phi, msg, Y)
         return D
 
@@ -36,8 +36,8 @@ class FactorDensity(torch.autograd.Function):
         K = msg.shape[-1]
         G = G.contiguous().float()
         dphi, dmsg, dY = torch.empty_like(phi), torch.empty_like(msg), torch.empty_like(Y)
-        call("face_density_bwd", ptr(phi), B, ptr(msg), K, None, ptr(Y), 20, 20, None, N, M, M, B, K, ptr(G),
-             ptr(dphi), B, ptr(dmsg), K, ptr(dY), 20, _lib.stream_of(G))
+        call("face_density_bwd", ptr(phi), B, ptr(msg), K, None, ptr(Y), 20, 20, None, N, M, M, B, K,
+             *_lib.ranks_of_dense(G), ptr(dphi), B, ptr(dmsg), K, ptr(dY), 20, _lib.stream_of(G))
         return dphi, dmsg, dY
 
 

@@ -12,9 +12,10 @@ runs:
   * the factor density (face/kernels.py), the CP pooling (face/model.py:496-502) and the
     transport sums (face/model.py:515-522, the same contraction with 4 monomials) run in
     the segmented HIP density kernels, reading gathered neighbour tables in place;
-  * moments are kept channel-last (N, k_l, C), so `mix`, `proj` and the readout are plain
-    row-major GEMMs, and the node kernel reads P/Q/S straight out of the projection output
-    and writes the invariant families straight into the readout row;
+  * moments are kept monomial-major, one (k_l, N, C) tensor per rank, so `mix`, `proj` and
+    the readout are plain row-major GEMMs on contiguous blocks, and the node kernel reads
+    P/Q/S straight out of the projection output and writes the invariant families straight
+    into the readout row;
   * only the projection columns the algebra uses are computed (P0 of rank 0; P3, Q3 of rank 3).
 
 Supported configuration: factor=True (cp on or off), transport/eqmsg on or off, n_passes >= 1,
@@ -181,44 +182,44 @@ class FactorBlock(nn.Module):
 
     # ------------------------------------------------------------------ moments
     def moments(self, h, rb, Y, env, zp, zidx, avg_nb, sets, eq, g, tmap):
+        """Moments A_l as monomial-major (k_l, N, C) blocks (face/model.py:460-534)."""
         N, E = g.N, g.E
         B, C, Kd = self.B, self.C, self.K
         hid = F.silu(self.rad_in(rb) + self.pair.weight[zp])
         h2 = F.silu(self.radial[0](hid))
         W2, b2 = weight(self.radial[2])
-        envc = env[:, None]
         # the last radial layer split into its phi (B) and CP (4C) column blocks: no slice copies
-        phi = F.linear(h2, W2[:B], b2[:B]) * envc                                # (E, B)
+        phi = F.linear(h2, W2[:B], b2[:B]) * env[:, None]                        # (E, B)
         msg_n = self.msg(h)                                                      # (N, K)
         if self.directional:
             if self.eq_in:
-                src1, src2 = eq
+                src1, src2 = eq                                                  # (3,N,C), (6,N,C)
             else:
                 src1 = torch.cat([S[1] for S in sets], -1)
                 src2 = torch.cat([S[2] for S in sets], -1)
-            Vb = self.pvt(src1)                                                  # (N, 3, nt*Kd)
-            Mb = self.pmt(src2)                                                  # (N, 6, nt*Kd)
-            T = torch.cat([Vb[..., :Kd], Mb[..., :Kd]], 1)                       # (N, 9, Kd)
+            Vb = self.pvt(src1)                                                  # (3, N, nt*Kd)
+            Mb = self.pmt(src2)                                                  # (6, N, nt*Kd)
+            T = torch.cat([Vb[..., :Kd], Mb[..., :Kd]], 0)                       # (9, N, Kd)
             d = ops.dir_features(T, Y, g)                                         # (E, 4Kd)
             mj, gathered = ops.gather_neighbour(msg_n, g) + self.dir_mix(d), False
         else:
             mj, gathered = msg_n, True
         s = self.elem_scale(zidx).view(N, 4, C) / avg_nb
         if self.cp:
-            R = F.linear(h2, W2[B:], b2[B:]) * envc                              # (E, 4C)
-            Af = ops.cp_density(R, mj, Y, g, gathered)                            # (N, 20, C)
+            R = F.linear(h2, W2[B:], b2[B:])                                      # (E, 4C), envelope in-kernel
+            Af = ops.cp_density(R, env, mj, Y, g, gathered)                       # 4 x (k_l, N, C)
         else:
-            Af = ops.density(phi, mj, Y, g, 20, gathered)                         # (N, 20, B*K)
-        A = [self.mix[l](Af[:, a:b]) * s[:, l, None, :] for l, (a, b) in enumerate(RANKS)]   # (N, k_l, C)
+            Af = ops.density(phi, mj, Y, g, 20, gathered)                         # 4 x (k_l, N, B*K)
+        A = [self.mix[l](Af[l]) * s[None, :, l, :] for l in range(4)]             # 4 x (k_l, N, C)
         if self.transport:
-            table = torch.cat([Vb[..., Kd:], Mb[..., Kd:]], 1).transpose(1, 2).reshape(N, Kd * 9)
-            St = ops.density(phi, table, Y, g, 4, True)                           # (N, 4, B*9Kd)
-            X = St.view(N, 4, B, Kd, 9).permute(0, 2, 3, 1, 4).reshape(N, B, Kd, 36) / avg_nb
+            table = torch.cat([Vb[..., Kd:], Mb[..., Kd:]], 0).permute(1, 2, 0).reshape(N, Kd * 9)
+            St = ops.density(phi, table, Y, g, 4, True)                           # (4, N, B*9Kd)
+            X = St.view(4, N, B, Kd, 9).permute(1, 2, 3, 0, 4).reshape(N, B, Kd, 36) / avg_nb
             D = X @ tmap                                                          # (N, B, Kd, 18)
-            D1 = D[..., :6].reshape(N, B, Kd, 2, 3).permute(0, 4, 1, 3, 2).reshape(N, 3, B * 2 * Kd)
-            D2 = D[..., 6:18].reshape(N, B, Kd, 2, 6).permute(0, 4, 1, 3, 2).reshape(N, 6, B * 2 * Kd)
-            A[1] = A[1] + self.tmix1(D1) * (s[:, 1, None, :] * avg_nb)
-            A[2] = A[2] + self.tmix2(D2) * (s[:, 2, None, :] * avg_nb)
+            D1 = D[..., :6].reshape(N, B, Kd, 2, 3).permute(4, 0, 1, 3, 2).reshape(3, N, B * 2 * Kd)
+            D2 = D[..., 6:18].reshape(N, B, Kd, 2, 6).permute(4, 0, 1, 3, 2).reshape(6, N, B * 2 * Kd)
+            A[1] = A[1] + self.tmix1(D1) * (s[None, :, 1, :] * avg_nb)
+            A[2] = A[2] + self.tmix2(D2) * (s[None, :, 2, :] * avg_nb)
         return A
 
     # ------------------------------------------------------------------ invariants + readout
@@ -228,13 +229,17 @@ class FactorBlock(nn.Module):
         allsets = sets + [A]
         ys = []
         for l in range(4):
-            x = torch.cat([S[l] for S in allsets], -1)                            # (N, k_l, cin)
             W, _ = weight(self.proj[l])
             if l == 0:
                 W = W[:C]                                                         # only P0 is used
             elif l == 3:
                 W = W[:2 * C]                                                     # S3 is unused
-            ys.append(F.linear(x, W))
+            # proj over the concatenated moment sets as a sum of per-set GEMMs (no concat copy)
+            y = None
+            for si, S in enumerate(allsets):
+                Ws = W[:, si * C:(si + 1) * C]
+                y = F.linear(S[l], Ws) if y is None else y + F.linear(S[l], Ws)
+            ys.append(y)                                                          # (k_l, N, 3C | C | 2C)
         if self.eq_out:
             feats, V, Ms = ops.node_features(ys[0], ys[1], ys[2], ys[3], self.vpath, self.mpath, True, C)
         else:
@@ -246,7 +251,7 @@ class FactorBlock(nn.Module):
         eq_new = None
         if self.eq_out:
             gv, gm = self.gate(inv).chunk(2, dim=-1)
-            eq_new = (V * gv[:, None, :], Ms * gm[:, None, :])
+            eq_new = (V * gv[None], Ms * gm[None])                                # (3,N,C), (6,N,C)
         return o[:, :1], h + o[:, 1:], A, eq_new
 
 

@@ -147,8 +147,8 @@ def gather_receiver(X, graph):
 
 
 class DirFeatures(torch.autograd.Function):
-    """Directional edge features d (E, 4Kd) from the node table T (N, 9, Kd) and the monomials
-    (face/model.py:474-493), without materialising the gathered tables."""
+    """Directional edge features d (E, 4Kd) from the node table T (9, N, Kd) (rows: V then M
+    components) and the monomials (face/model.py:474-493), without materialising gathers."""
 
     @staticmethod
     def forward(ctx, T, Y, graph):
@@ -157,8 +157,8 @@ class DirFeatures(torch.autograd.Function):
         Y = Y.contiguous().float()
         Kd = T.shape[2]
         d = torch.empty(graph.E, 4 * Kd, device=T.device)
-        call("face_dir_feats_fwd", ptr(T), Kd, ptr(graph.recv), ptr(graph.col), ptr(Y), graph.E, ptr(d),
-             _lib.stream_of(T), label="dir_fwd")
+        call("face_dir_feats_fwd", ptr(T), Kd, T.stride(1), T.stride(0), ptr(graph.recv), ptr(graph.col), ptr(Y),
+             graph.E, ptr(d), _lib.stream_of(T), label="dir_fwd")
         ctx.save_for_backward(T, Y)
         ctx.graph = graph
         return d
@@ -171,8 +171,8 @@ class DirFeatures(torch.autograd.Function):
         Kd = T.shape[2]
         gT = torch.empty_like(T) if ctx.needs_input_grad[0] else None
         gY = torch.empty_like(Y) if ctx.needs_input_grad[1] else None
-        call("face_dir_feats_bwd", ptr(T), Kd, ptr(g.row_ptr), ptr(g.recv), ptr(g.col), ptr(g.rev), ptr(Y), ptr(gd),
-             g.N, g.E, ptr(gT), ptr(gY), _lib.stream_of(gd), label="dir_bwd")
+        call("face_dir_feats_bwd", ptr(T), Kd, T.stride(1), T.stride(0), ptr(g.row_ptr), ptr(g.recv), ptr(g.col),
+             ptr(g.rev), ptr(Y), ptr(gd), g.N, g.E, ptr(gT), ptr(gY), _lib.stream_of(gd), label="dir_bwd")
         return gT, gY, None
 
 
@@ -198,9 +198,24 @@ class StructureSum(torch.autograd.Function):
 
 
 # ----------------------------------------------------------------------------- densities
-class Density(torch.autograd.Function):
-    """D (N, NX, B*K) = sum over row i of phi (x) msg (x) Y[:, :NX]  (face/kernels.py:170-178).
+RANK_K = (1, 3, 6, 10)
 
+
+def _ranks_xmajor(t):
+    """Rank descriptor of one (NX, N, W) monomial-major tensor."""
+    NX, N, W = t.shape
+    base = t.data_ptr()
+    nr = 4 if NX == 20 else 2
+    ptrs = [base + 4 * _lib.RANK_X0[l] * N * W if l < nr else None for l in range(4)]
+    return (_lib.P * 4)(*ptrs), W, N * W
+
+
+class Density(torch.autograd.Function):
+    """Factor density sum over row i of phi (x) msg (x) Y[:, :nx]  (face/kernels.py:170-178).
+
+    nx = 20: returns the four rank blocks D_l (k_l, N, B*K) (monomial-major), each a separate
+    tensor so the channel-mixing GEMMs read them in place and their gradients arrive without
+    slice/concat copies. nx = 4: returns one (4, N, B*K) tensor.
     msg is per edge (E, K) when gathered is False, else a node table (N, K) read through col
     (its gradient is then reduced back to the table through the reverse-edge map).
     """
@@ -213,29 +228,40 @@ class Density(torch.autograd.Function):
         msg_, ld_msg = _rows(msg, K)
         Y_, ld_Y = _rows(Y, nx)
         N = graph.N
-        D = torch.empty(N, nx, B * K, device=phi.device)
+        if nx == 20:
+            outs = [torch.empty(k, N, B * K, device=phi.device) for k in RANK_K]
+            desc = _lib.ranks_of_blocks(outs)
+        else:
+            outs = [torch.empty(nx, N, B * K, device=phi.device)]
+            desc = _ranks_xmajor(outs[0])
         row = graph.col if gathered else None
         call("face_density_fwd", ptr(phi_), ld_phi, ptr(msg_), ld_msg, ptr(row), ptr(Y_), ld_Y, nx, ptr(graph.row_ptr),
-             N, 0, B, K, ptr(D), _lib.stream_of(phi), label=f"density_fwd{nx}")
+             N, 0, B, K, *desc, _lib.stream_of(phi), label=f"density_fwd{nx}")
         ctx.save_for_backward(phi_, msg_, Y_)
         ctx.graph, ctx.nx, ctx.gathered, ctx.BK = graph, nx, gathered, (B, K)
         ctx.ywidth = Y.shape[1]
-        return D
+        return tuple(outs) if nx == 20 else outs[0]
 
     @staticmethod
-    def backward(ctx, G):
+    def backward(ctx, *grads):
         phi, msg, Y = ctx.saved_tensors
         g, nx, (B, K) = ctx.graph, ctx.nx, ctx.BK
-        G = G.contiguous().float()
-        dev = G.device
+        dev = phi.device
+        if nx == 20:
+            Gs = [(t.contiguous().float() if t is not None else torch.zeros(k, g.N, B * K, device=dev))
+                  for t, k in zip(grads, RANK_K)]
+            desc = _lib.ranks_of_blocks(Gs)
+        else:
+            Gs = [grads[0].contiguous().float()]
+            desc = _ranks_xmajor(Gs[0])
         need_phi, need_msg, need_Y = ctx.needs_input_grad[:3]
         dphi = torch.empty(g.E, B, device=dev) if need_phi else None
         dmsg = torch.empty(g.E, K, device=dev) if need_msg else None
         dY = torch.empty(g.E, nx, device=dev) if need_Y else None
         row = g.col if ctx.gathered else None
-        st = _lib.stream_of(G)
+        st = _lib.stream_of(phi)
         call("face_density_bwd", ptr(phi), phi.stride(0), ptr(msg), msg.stride(0), ptr(row), ptr(Y), Y.stride(0), nx,
-             ptr(g.row_ptr), g.N, 0, g.max_row, B, K, ptr(G), ptr(dphi), B, ptr(dmsg), K, ptr(dY), nx, st,
+             ptr(g.row_ptr), g.N, 0, g.max_row, B, K, *desc, ptr(dphi), B, ptr(dmsg), K, ptr(dY), nx, st,
              label=f"density_bwd{nx}")
         if dmsg is not None and ctx.gathered:
             dtab = torch.empty(g.N, K, device=dev)
@@ -252,48 +278,52 @@ def density(phi, msg, Y, graph, nx=20, gathered=False):
 
 
 class CPDensity(torch.autograd.Function):
-    """A (N,20,C) = sum over row i of R[:, l(x), c] msg[:, c] Y[:, x]  (face/model.py:496-502)."""
+    """CP pooling A_l (k_l, N, C) = sum over row i of env R[:, l, c] msg[:, c] Y[:, x in l]
+    (face/model.py:496-502, envelope of face/model.py:469 folded in); four rank blocks."""
 
     @staticmethod
-    def forward(ctx, R, msg, Y, graph, gathered):
-        _lib.require_gpu(R, msg, Y)
+    def forward(ctx, R, env, msg, Y, graph, gathered):
+        _lib.require_gpu(R, env, msg, Y)
         C = msg.shape[1]
         R_, ld_R = _rows(R, 4 * C)
+        env_ = env.contiguous().float()
         msg_, ld_msg = _rows(msg, C)
         Y_, ld_Y = _rows(Y, 20)
-        A = torch.empty(graph.N, 20, C, device=R.device)
+        outs = [torch.empty(k, graph.N, C, device=R.device) for k in RANK_K]
         row = graph.col if gathered else None
-        call("face_cp_density_fwd", ptr(R_), ld_R, ptr(msg_), ld_msg, ptr(row), ptr(Y_), ld_Y, ptr(graph.row_ptr),
-             graph.N, 0, C, ptr(A), _lib.stream_of(R), label="cp_fwd")
-        ctx.save_for_backward(R_, msg_, Y_)
+        call("face_cp_density_fwd", ptr(R_), ld_R, ptr(env_), ptr(msg_), ld_msg, ptr(row), ptr(Y_), ld_Y,
+             ptr(graph.row_ptr), graph.N, 0, C, *_lib.ranks_of_blocks(outs), _lib.stream_of(R), label="cp_fwd")
+        ctx.save_for_backward(R_, env_, msg_, Y_)
         ctx.graph, ctx.gathered, ctx.C = graph, gathered, C
-        return A
+        return tuple(outs)
 
     @staticmethod
-    def backward(ctx, gA):
-        R, msg, Y = ctx.saved_tensors
+    def backward(ctx, *grads):
+        R, env, msg, Y = ctx.saved_tensors
         g, C = ctx.graph, ctx.C
-        gA = gA.contiguous().float()
-        dev = gA.device
-        need_R, need_msg, need_Y = ctx.needs_input_grad[:3]
+        dev = R.device
+        Gs = [(t.contiguous().float() if t is not None else torch.zeros(k, g.N, C, device=dev))
+              for t, k in zip(grads, RANK_K)]
+        need_R, need_env, need_msg, need_Y = ctx.needs_input_grad[:4]
         dR = torch.empty(g.E, 4 * C, device=dev) if need_R else None
+        denv = torch.empty(g.E, device=dev) if need_env else None
         dmsg = torch.empty(g.E, C, device=dev) if need_msg else None
         dY = torch.empty(g.E, 20, device=dev) if need_Y else None
         row = g.col if ctx.gathered else None
-        st = _lib.stream_of(gA)
-        call("face_cp_density_bwd", ptr(R), R.stride(0), ptr(msg), msg.stride(0), ptr(row), ptr(Y), Y.stride(0),
-             ptr(g.row_ptr), g.N, 0, g.max_row, C, ptr(gA), ptr(dR), 4 * C, ptr(dmsg), C, ptr(dY), 20, st,
-             label="cp_bwd")
+        st = _lib.stream_of(R)
+        call("face_cp_density_bwd", ptr(R), R.stride(0), ptr(env), ptr(msg), msg.stride(0), ptr(row), ptr(Y),
+             Y.stride(0), ptr(g.row_ptr), g.N, 0, g.max_row, C, *_lib.ranks_of_blocks(Gs), ptr(dR), 4 * C, ptr(dmsg),
+             C, ptr(dY), 20, ptr(denv), st, label="cp_bwd")
         if dmsg is not None and ctx.gathered:
             dtab = torch.empty(g.N, C, device=dev)
             call("face_gather_rows_bwd", ptr(dmsg), C, ptr(g.row_ptr), ptr(g.rev), g.N, C, ptr(dtab), C, st,
                  label="gather_bwd")
             dmsg = dtab
-        return dR, dmsg, dY, None, None
+        return dR, denv, dmsg, dY, None, None
 
 
-def cp_density(R, msg, Y, graph, gathered=False):
-    return CPDensity.apply(R, msg, Y, graph, gathered)
+def cp_density(R, env, msg, Y, graph, gathered=False):
+    return CPDensity.apply(R, env, msg, Y, graph, gathered)
 
 
 # ----------------------------------------------------------------------------- node algebra
@@ -302,38 +332,43 @@ def _s3(t):
     return [t.stride(0), t.stride(1), t.stride(2)]
 
 
-class NodeFeatures(torch.autograd.Function):
-    """Invariant families and gated products from the projection outputs (channel-last).
+def _pqs_views(y1, y2, y3, C):
+    """(atom, channel, component) views of P1..Q3 inside monomial-major projection outputs
+    y1 (3, N, 3C), y2 (6, N, 3C), y3 (10, N, >=2C)."""
+    v = lambda y, j: y[:, :, j * C:(j + 1) * C].permute(1, 2, 0)
+    return [v(y1, 0), v(y1, 1), v(y1, 2), v(y2, 0), v(y2, 1), v(y2, 2), v(y3, 0), v(y3, 1)]
 
-    y0 (N,1,>=C), y1 (N,3,3C), y2 (N,6,3C), y3 (N,10,>=2C): P|Q|S blocks of C channels.
-    Returns feats (N,9C) = [P0 | inv1..inv8] (family-major, face/model.py:244-249,254-264),
-    and when eq: V (N,3,C), Ms (N,6,C) = symmetrised Mf in sym storage (face/model.py:288-294).
+
+class NodeFeatures(torch.autograd.Function):
+    """Invariant families and gated products from the monomial-major projection outputs.
+
+    y0 (1, N, >=C), y1 (3, N, 3C), y2 (6, N, 3C), y3 (10, N, >=2C): P|Q|S blocks of C channels.
+    Returns feats (N, 9C) = [P0 | inv1..inv8] (family-major, face/model.py:244-249,254-264) and,
+    when eq: V (3, N, C), Ms (6, N, C) = symmetrised Mf in sym storage (face/model.py:288-294).
     """
 
     @staticmethod
     def forward(ctx, y0, y1, y2, y3, a, b, eq, C):
         _lib.require_gpu(y0, y1, y2, y3)
-        N = y1.shape[0]
+        N = y1.shape[1]
         dev = y1.device
-        ys = [y.contiguous().float() for y in (y0, y1, y2, y3)]
-        y0, y1, y2, y3 = ys
-        ins = [y1[:, :, :C], y1[:, :, C:2 * C], y1[:, :, 2 * C:], y2[:, :, :C], y2[:, :, C:2 * C], y2[:, :, 2 * C:],
-               y3[:, :, :C], y3[:, :, C:2 * C]]
-        ins = [t.transpose(1, 2) for t in ins]                                  # (N,C,k) views
+        y0, y1, y2, y3 = [y.contiguous().float() for y in (y0, y1, y2, y3)]
+        ins = _pqs_views(y1, y2, y3, C)
         feats = torch.empty(N, 9 * C, device=dev)
-        feats[:, :C] = y0[:, 0, :C]
+        feats[:, :C] = y0[0, :, :C]
         inv_view = feats[:, C:].view(N, 8, C).transpose(1, 2)                   # (N,C,8)
         st = sum((_s3(t) for t in ins), [])
         V = Ms = None
+        z3 = [0, 0, 0]
         if eq:
-            V = torch.empty(N, 3, C, device=dev)
-            Ms = torch.empty(N, 6, C, device=dev)
+            V = torch.empty(3, N, C, device=dev)
+            Ms = torch.empty(6, N, C, device=dev)
             a_, b_ = a.contiguous().float(), b.contiguous().float()
         else:
             a_ = b_ = None
         call("face_node_fwd", _lib.ptr_array(ins), _lib.i64_array(st), ptr(a_), ptr(b_), ptr(inv_view),
-             _lib.i64_array(_s3(inv_view)), ptr(V), _lib.i64_array(_s3(V.transpose(1, 2)) if eq else [0, 0, 0]),
-             ptr(Ms), _lib.i64_array(_s3(Ms.transpose(1, 2)) if eq else [0, 0, 0]), 1, N, C, int(bool(eq)),
+             _lib.i64_array(_s3(inv_view)), ptr(V), _lib.i64_array(_s3(V.permute(1, 2, 0)) if eq else z3),
+             ptr(Ms), _lib.i64_array(_s3(Ms.permute(1, 2, 0)) if eq else z3), 1, N, C, int(bool(eq)),
              _lib.stream_of(y1), label="node_fwd")
         ctx.save_for_backward(y0, y1, y2, y3, a_ if eq else torch.empty(0), b_ if eq else torch.empty(0))
         ctx.eq, ctx.C = eq, C
@@ -345,11 +380,9 @@ class NodeFeatures(torch.autograd.Function):
     def backward(ctx, gfeats, gV, gMs):
         y0, y1, y2, y3, a, b = ctx.saved_tensors
         C, eq = ctx.C, ctx.eq
-        N = y1.shape[0]
+        N = y1.shape[1]
         dev = y1.device
-        ins = [y1[:, :, :C], y1[:, :, C:2 * C], y1[:, :, 2 * C:], y2[:, :, :C], y2[:, :, C:2 * C], y2[:, :, 2 * C:],
-               y3[:, :, :C], y3[:, :, C:2 * C]]
-        ins = [t.transpose(1, 2) for t in ins]
+        ins = _pqs_views(y1, y2, y3, C)
         st = sum((_s3(t) for t in ins), [])
         dy0 = torch.zeros_like(y0)
         dy1 = torch.empty_like(y1)
@@ -357,13 +390,12 @@ class NodeFeatures(torch.autograd.Function):
         dy3 = torch.empty_like(y3)
         if dy3.shape[2] > 2 * C:
             dy3[:, :, 2 * C:] = 0
-        outs = [dy1[:, :, :C], dy1[:, :, C:2 * C], dy1[:, :, 2 * C:], dy2[:, :, :C], dy2[:, :, C:2 * C],
-                dy2[:, :, 2 * C:], dy3[:, :, :C], dy3[:, :, C:2 * C]]
-        outs = [t.transpose(1, 2) for t in outs]
+        outs = _pqs_views(dy1, dy2, dy3, C)
         gI = None
+        z3 = [0, 0, 0]
         if gfeats is not None:
             gfeats = gfeats.contiguous().float()
-            dy0[:, 0, :C] = gfeats[:, :C]
+            dy0[0, :, :C] = gfeats[:, :C]
             gI = gfeats[:, C:].view(N, 8, C).transpose(1, 2)
         need_ab = eq and (ctx.needs_input_grad[4] or ctx.needs_input_grad[5])
         da = torch.empty(N, C, 4, device=dev) if need_ab else None
@@ -372,11 +404,10 @@ class NodeFeatures(torch.autograd.Function):
             gV = gV.contiguous().float()
         if gMs is not None:
             gMs = gMs.contiguous().float()
-        z3 = [0, 0, 0]
         call("face_node_bwd", _lib.ptr_array(ins), _lib.i64_array(st), ptr(a) if eq else None,
              ptr(b) if eq else None, ptr(gI), _lib.i64_array(_s3(gI) if gI is not None else z3),
-             ptr(gV), _lib.i64_array(_s3(gV.transpose(1, 2)) if gV is not None else z3),
-             ptr(gMs), _lib.i64_array(_s3(gMs.transpose(1, 2)) if gMs is not None else z3), 1,
+             ptr(gV), _lib.i64_array(_s3(gV.permute(1, 2, 0)) if gV is not None else z3),
+             ptr(gMs), _lib.i64_array(_s3(gMs.permute(1, 2, 0)) if gMs is not None else z3), 1,
              _lib.ptr_array(outs), _lib.i64_array(sum((_s3(t) for t in outs), [])), ptr(da), ptr(db), N, C,
              int(bool(eq)), _lib.stream_of(y1), label="node_bwd")
         ga = da.sum(0).t() if need_ab else None

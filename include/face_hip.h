@@ -40,18 +40,27 @@ const char* face_hip_error_string(int code);
 /* ABI version of this header (bumped on any signature change). */
 int face_hip_abi_version(void);
 
-/* ---------------------------------------------------------------- factor density
+/* ---------------------------------------------------------------- rank-block outputs
+ * Density outputs and their upstream gradients are addressed per monomial rank l (x ranges
+ * 0 | 1-3 | 4-9 | 10-19): element (atom i, monomial x, column c) lives at
+ *     ranks[l(x)] + i * atom_stride + (x - x0(l)) * x_stride + c
+ * ranks: host array of 4 device pointers (only ranks 0 and 1 are read when NX == 4).
+ * The reference layout (N, NX, W) is ranks[l] = base + x0(l) * W, atom_stride = NX * W,
+ * x_stride = W; a (k_l, N, W) tensor per rank is ranks[l] = D_l, atom_stride = W, x_stride = N * W.
+ *
+ * ---------------------------------------------------------------- factor density
  * D[i, x, b*K + k] = sum_{e in row i} phi[e, b] * msg[m(e), k] * Y[e, x],  x < NX
  * where m(e) = msg_row ? msg_row[e] : e (msg_row gathers rows of a node table directly).
- * phi (E, ld_phi >= B), msg (*, ld_msg >= K), Y (E, ld_Y >= NX), D (N, NX, B*K).
+ * phi (E, ld_phi >= B), msg (*, ld_msg >= K), Y (E, ld_Y >= NX), D: rank blocks of width B*K.
  * NX is 20 (monomials up to rank 3, face/cartesian.py:11-17) or 4 (1, u: the transport sums
  * of face/model.py:515-522, which are this contraction with msg = gathered transport tables).
  * Replaces FactorDensity.forward / dens_fwd (face/kernels.py:137-149, :22-54).            */
 int face_density_fwd(const float* phi, int32_t ld_phi, const float* msg, int32_t ld_msg, const int32_t* msg_row,
                      const float* Y, int32_t ld_Y, int32_t NX, const int32_t* row_ptr, int64_t N, int32_t M,
-                     int32_t B, int32_t K, float* D, void* stream);
+                     int32_t B, int32_t K, float* const* D_ranks, int64_t atom_stride, int64_t x_stride,
+                     void* stream);
 
-/* Backward of face_density_fwd for upstream G = dL/dD (N, NX, B*K):
+/* Backward of face_density_fwd for upstream G = dL/dD (rank blocks of width B*K):
  *   dphi[e,b] = sum_{x,k} G[i,x,b,k] Y[e,x] msg[m(e),k]
  *   dmsg[e,k] = sum_{x,b} G[i,x,b,k] Y[e,x] phi[e,b]     (per EDGE, also when msg_row != NULL)
  *   dY[e,x]   = sum_{b,k} G[i,x,b,k] phi[e,b] msg[m(e),k]
@@ -59,23 +68,28 @@ int face_density_fwd(const float* phi, int32_t ld_phi, const float* msg, int32_t
  * Replaces FactorDensity.backward / dens_bwd (face/kernels.py:151-167, :56-118).           */
 int face_density_bwd(const float* phi, int32_t ld_phi, const float* msg, int32_t ld_msg, const int32_t* msg_row,
                      const float* Y, int32_t ld_Y, int32_t NX, const int32_t* row_ptr, int64_t N, int32_t M,
-                     int32_t max_row, int32_t B, int32_t K, const float* G, float* dphi, int32_t ld_dphi,
-                     float* dmsg, int32_t ld_dmsg, float* dY, int32_t ld_dY, void* stream);
+                     int32_t max_row, int32_t B, int32_t K, const float* const* G_ranks, int64_t atom_stride,
+                     int64_t x_stride, float* dphi, int32_t ld_dphi, float* dmsg, int32_t ld_dmsg, float* dY,
+                     int32_t ld_dY, void* stream);
 
 /* ---------------------------------------------------------------- CP density
- * A[i, x, c] = sum_{e in row i} R[e, l(x), c] * msg[m(e), c] * Y[e, x],  l(x) = rank of monomial x
- * R (E, ld_R >= 4C) laid out [rank][channel], msg (*, ld_msg >= C), Y (E, ld_Y >= 20), A (N, 20, C).
- * The rank-diagonal blocks of the reference's (N,20,4,C) bmm (face/model.py:496-502).     */
-int face_cp_density_fwd(const float* R, int32_t ld_R, const float* msg, int32_t ld_msg, const int32_t* msg_row,
-                        const float* Y, int32_t ld_Y, const int32_t* row_ptr, int64_t N, int32_t M, int32_t C,
-                        float* A, void* stream);
+ * A[i, x, c] = sum_{e in row i} env[e] * R[e, l(x), c] * msg[m(e), c] * Y[e, x],  l(x) = rank of x
+ * R (E, ld_R >= 4C) laid out [rank][channel] (the radial output BEFORE the cutoff envelope),
+ * env (E) the envelope (NULL = 1), msg (*, ld_msg >= C), Y (E, ld_Y >= 20), A: rank blocks of
+ * width C. The rank-diagonal blocks of the reference's (N,20,4,C) bmm with the envelope
+ * multiply of face/model.py:469 folded in (face/model.py:496-502).                          */
+int face_cp_density_fwd(const float* R, int32_t ld_R, const float* env, const float* msg, int32_t ld_msg,
+                        const int32_t* msg_row, const float* Y, int32_t ld_Y, const int32_t* row_ptr, int64_t N,
+                        int32_t M, int32_t C, float* const* A_ranks, int64_t atom_stride, int64_t x_stride,
+                        void* stream);
 
-/* Backward for gA = dL/dA (N, 20, C): dR (E, ld_dR), dmsg (E, ld_dmsg) per edge, dY (E, ld_dY).
- * Any output may be NULL. */
-int face_cp_density_bwd(const float* R, int32_t ld_R, const float* msg, int32_t ld_msg, const int32_t* msg_row,
-                        const float* Y, int32_t ld_Y, const int32_t* row_ptr, int64_t N, int32_t M, int32_t max_row,
-                        int32_t C, const float* gA, float* dR, int32_t ld_dR, float* dmsg, int32_t ld_dmsg, float* dY,
-                        int32_t ld_dY, void* stream);
+/* Backward for gA = dL/dA (rank blocks): dR (E, ld_dR), dmsg (E, ld_dmsg) per edge, dY (E, ld_dY),
+ * denv (E). Any output may be NULL. C <= 256. */
+int face_cp_density_bwd(const float* R, int32_t ld_R, const float* env, const float* msg, int32_t ld_msg,
+                        const int32_t* msg_row, const float* Y, int32_t ld_Y, const int32_t* row_ptr, int64_t N,
+                        int32_t M, int32_t max_row, int32_t C, const float* const* gA_ranks, int64_t atom_stride,
+                        int64_t x_stride, float* dR, int32_t ld_dR, float* dmsg, int32_t ld_dmsg, float* dY,
+                        int32_t ld_dY, float* denv, void* stream);
 
 /* ---------------------------------------------------------------- node algebra
  * Per (atom n, channel c) invariants of symmetric Cartesian tensors
@@ -165,17 +179,19 @@ int face_edge_geom_bwd(const float* pos, const int32_t* recv, const int32_t* col
                        void* stream);
 
 /* ---------------------------------------------------------------- directional edge features
- * Node table T (N, 9, Kd): per channel k, rows 0-2 = V_k, rows 3-8 = M_k (sym storage).
+ * Node table T: element (atom n, row q, channel k) at T[q*sq + n*sn + k], rows 0-2 = V_k,
+ * rows 3-8 = M_k (sym storage), Kd channels.
  * d (E, 4*Kd) = [u.V_j | u^T M_j u | u.V_i | u^T M_i u] with u = Y[e,1:4], u^T M u =
  * sum_q Y[e,4+q] * (1,1,1,2,2,2)_q * M_q, j = col[e], i = recv[e]
  * (face/model.py:474-493, the per-edge d fed to dir_mix).                                  */
-int face_dir_feats_fwd(const float* T, int32_t Kd, const int32_t* recv, const int32_t* col, const float* Y,
-                       int64_t E, float* d, void* stream);
-/* Backward for gd = dL/dd (E, 4*Kd): gT (N, 9, Kd) through the reverse-edge map (no atomics),
- * gY (E, 20) (monomials 0 and 10..19 written as zero). Either output may be NULL. */
-int face_dir_feats_bwd(const float* T, int32_t Kd, const int32_t* row_ptr, const int32_t* recv, const int32_t* col,
-                       const int32_t* rev, const float* Y, const float* gd, int64_t N, int64_t E, float* gT,
-                       float* gY, void* stream);
+int face_dir_feats_fwd(const float* T, int32_t Kd, int64_t sn, int64_t sq, const int32_t* recv, const int32_t* col,
+                       const float* Y, int64_t E, float* d, void* stream);
+/* Backward for gd = dL/dd (E, 4*Kd): gT (same layout as T) through the reverse-edge map (no
+ * atomics), gY (E, 20) (monomials 0 and 10..19 written as zero). Either output may be NULL.
+ * Kd <= 64. */
+int face_dir_feats_bwd(const float* T, int32_t Kd, int64_t sn, int64_t sq, const int32_t* row_ptr,
+                       const int32_t* recv, const int32_t* col, const int32_t* rev, const float* Y, const float* gd,
+                       int64_t N, int64_t E, float* gT, float* gY, void* stream);
 
 /* ---------------------------------------------------------------- gathers and scatters
  * out[e, :] = X[idx[e], :] for F features (X row stride ld_X, out row stride ld_out). */

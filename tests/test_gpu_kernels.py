@@ -100,7 +100,10 @@ def test_csr_density_ragged_rows(nx, gathered, B, K):
     tab_rows = 57 if gathered else E
     msg = torch.randn(tab_rows, K, device=DEV, requires_grad=True)
     Y = torch.randn(E, 20, device=DEV, requires_grad=True)
-    D = ops.density(phi, msg, Y, g.G, nx, gathered)
+    out = ops.density(phi, msg, Y, g.G, nx, gathered)
+    D = torch.cat(out, 0) if nx == 20 else out              # monomial-major (nx, N, B*K)
+    assert D.shape == (nx, 57, B * K)
+    D = D.permute(1, 0, 2)
     G = torch.randn_like(D)
     gr = torch.autograd.grad((D * G).sum(), (phi, msg, Y))
     # oracle on the padded layout
@@ -116,7 +119,8 @@ def test_csr_density_ragged_rows(nx, gathered, B, K):
     errs = [rel(D, D2)] + [rel(a, b) for a, b in zip(gr, gr2)]
     assert max(errs) < TOL, errs
     # bitwise reproducible (no atomics)
-    D3 = ops.density(phi, msg, Y, g.G, nx, gathered)
+    out3 = ops.density(phi, msg, Y, g.G, nx, gathered)
+    D3 = (torch.cat(out3, 0) if nx == 20 else out3).permute(1, 0, 2)
     assert torch.equal(D, D3)
 
 
@@ -129,19 +133,21 @@ def test_cp_density_ragged_rows(gathered, C):
     E = sum(counts)
     torch.manual_seed(6)
     R = torch.randn(E, 16 + 4 * C, device=DEV)[:, 16:].requires_grad_(True)
+    env = torch.rand(E, device=DEV, requires_grad=True)
     msg = torch.randn(41 if gathered else E, C, device=DEV, requires_grad=True)
     Y = torch.randn(E, 20, device=DEV, requires_grad=True)
-    A = ops.cp_density(R, msg, Y, g.G, gathered)
+    A = torch.cat(ops.cp_density(R, env, msg, Y, g.G, gathered), 0).permute(1, 0, 2)   # (N, 20, C)
     G = torch.randn_like(A)
-    gr = torch.autograd.grad((A * G).sum(), (R, msg, Y))
+    gr = torch.autograd.grad((A * G).sum(), (R, env, msg, Y))
     M = max(counts)
     col = g.G.col.long().cpu()
     pd = lambda t: _pad(t, counts, M)
     Rc = R.detach().double().cpu().requires_grad_(True)
+    ec = env.detach().double().cpu().requires_grad_(True)
     ms = msg.detach().double().cpu().requires_grad_(True)
     Yc = Y.detach().double().cpu().requires_grad_(True)
-    A2 = oops.cp_density(pd(Rc.view(E, 4, C)), pd(ms[col] if gathered else ms), pd(Yc))
-    gr2 = torch.autograd.grad((A2 * G.double().cpu()).sum(), (Rc, ms, Yc))
+    A2 = oops.cp_density(pd((Rc * ec[:, None]).view(E, 4, C)), pd(ms[col] if gathered else ms), pd(Yc))
+    gr2 = torch.autograd.grad((A2 * G.double().cpu()).sum(), (Rc, ec, ms, Yc))
     errs = [rel(A, A2)] + [rel(a, b) for a, b in zip(gr, gr2)]
     assert max(errs) < TOL, errs
 
@@ -182,10 +188,10 @@ def test_node_features_product_layout():
     say("node features")
     torch.manual_seed(2)
     N, C = 37, 20
-    y0 = torch.randn(N, 1, C, device=DEV, requires_grad=True)
-    y1 = torch.randn(N, 3, 3 * C, device=DEV, requires_grad=True)
-    y2 = torch.randn(N, 6, 3 * C, device=DEV, requires_grad=True)
-    y3 = torch.randn(N, 10, 2 * C, device=DEV, requires_grad=True)
+    y0 = torch.randn(1, N, C, device=DEV, requires_grad=True)
+    y1 = torch.randn(3, N, 3 * C, device=DEV, requires_grad=True)
+    y2 = torch.randn(6, N, 3 * C, device=DEV, requires_grad=True)
+    y3 = torch.randn(10, N, 2 * C, device=DEV, requires_grad=True)
     a = torch.randn(4, C, device=DEV, requires_grad=True)
     b = torch.randn(4, C, device=DEV, requires_grad=True)
     feats, V, Ms = ops.node_features(y0, y1, y2, y3, a, b, True, C)
@@ -194,14 +200,14 @@ def test_node_features_product_layout():
     g1 = torch.autograd.grad((feats * gf).sum() + (V * gv).sum() + (Ms * gm).sum(), vars1)
     yc = [t.detach().double().cpu().requires_grad_(True) for t in vars1]
     c0, c1, c2, c3, ac, bc = yc
-    split = lambda y, k: [y[..., j * C:(j + 1) * C].transpose(1, 2) for j in range(k)]
+    split = lambda y, k: [y[..., j * C:(j + 1) * C].permute(1, 2, 0) for j in range(k)]
     P1, Q1, S1 = split(c1, 3)
     P2, Q2, S2 = split(c2, 3)
     P3, Q3 = split(c3, 2)
     inv, Vr, Mf = oops.node_algebra_sym(P1, Q1, S1, P2, Q2, S2, P3, Q3, ac, bc)
-    feats2 = torch.cat([c0[:, 0]] + list(inv.unbind(-1)), 1)
-    Ms2 = cartesian.to_sym2(0.5 * (Mf + Mf.transpose(-1, -2))).transpose(1, 2)
-    V2 = Vr.transpose(1, 2)
+    feats2 = torch.cat([c0[0]] + list(inv.unbind(-1)), 1)
+    Ms2 = cartesian.to_sym2(0.5 * (Mf + Mf.transpose(-1, -2))).permute(2, 0, 1)
+    V2 = Vr.permute(2, 0, 1)
     L2 = (feats2 * gf.double().cpu()).sum() + (V2 * gv.double().cpu()).sum() + (Ms2 * gm.double().cpu()).sum()
     g2 = torch.autograd.grad(L2, yc)
     errs = [rel(feats, feats2), rel(V, V2), rel(Ms, Ms2)] + [rel(u, v) for u, v in zip(g1, g2)]
@@ -272,12 +278,13 @@ def test_directional_features_and_gradients():
         g = _G(37, 300, seed + 10)
         E = sum(g.counts)
         torch.manual_seed(seed)
-        T = torch.randn(37, 9, Kd, device=DEV, requires_grad=True)
+        T = torch.randn(9, 37, Kd, device=DEV, requires_grad=True)
         Y = torch.randn(E, 20, device=DEV, requires_grad=True)
         d = ops.dir_features(T, Y, g.G)
         w = torch.randn_like(d)
         gT, gY = torch.autograd.grad((d * w).sum(), (T, Y))
-        Tc = T.detach().double().cpu().requires_grad_(True)
+        gT = gT.permute(1, 0, 2)
+        Tc = T.detach().double().cpu().permute(1, 0, 2).contiguous().requires_grad_(True)
         Yc = Y.detach().double().cpu().requires_grad_(True)
         col, recv = g.G.col.long().cpu(), g.G.recv.long().cpu()
         u = Yc[:, 1:4]

@@ -47,10 +47,12 @@ def test_host_rejects_bad_shapes_before_launch():
     from face_amd import _lib
     L = _lib.lib()
     # negative sizes / unsupported monomial counts are refused without touching the device
-    assert L.face_density_fwd(None, 16, None, 32, None, None, 20, 7, None, 10, 4, 16, 32, None, None) == -1
-    assert L.face_cp_density_bwd(None, 4, None, 1, None, None, 20, None, 1, 1, 1, 300, None, None, 0, None, 0,
-                                 None, 0, None) == -1
-    assert L.face_density_fwd(None, 16, None, 32, None, None, 20, 20, None, 0, 4, 16, 32, None, None) == 0
+    assert L.face_density_fwd(None, 16, None, 32, None, None, 20, 7, None, 10, 4, 16, 32, None, 1, 1, None) == -1
+    assert L.face_cp_density_bwd(None, 4, None, None, 1, None, None, 20, None, 1, 1, 1, 300, None, 1, 1, None, 0,
+                                 None, 0, None, 0, None, None) == -1
+    assert L.face_density_fwd(None, 16, None, 32, None, None, 20, 20, None, 0, 4, 16, 32, None, 1, 1, None) == 0
+    # a rank-block descriptor with a missing block is refused
+    assert L.face_density_fwd(1, 16, 1, 32, None, 1, 20, 20, None, 5, 4, 16, 32, None, 1, 1, None) == -1
 
 
 def test_cpu_tensors_are_refused():
