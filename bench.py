@@ -28,8 +28,8 @@ import torch  # noqa: E402
 
 METRIC = "atom-steps/s (E+F, fp32) at 864 & 24k atoms; density-kernel HBM GB/s"
 HBM_PEAK_GBS = 8000.0
-TIMED = ["density_fwd20", "density_bwd20", "density_fwd4", "density_bwd4", "cp_fwd", "cp_bwd", "node_fwd",
-         "node_bwd", "edge_fwd", "edge_bwd", "force_scatter", "gather_bwd"]
+TIMED = ["density_fwd20", "density_bwd20", "cp_fwd", "cp_bwd", "transport_fwd", "transport_bwd", "dir_fwd",
+         "dir_bwd", "node_fwd", "node_bwd", "edge_fwd", "edge_bwd", "force_scatter", "gather_bwd"]
 
 
 def log(*a):
@@ -42,15 +42,15 @@ def algorithmic_bytes(label, g, kw):
     E, N = g.E, g.N
     B, C = kw["B"], kw["C"]
     K = C if kw.get("cp") else kw["K"]
-    Kt = 9 * kw["K_dir"]
+    Kt = 18 * kw["K_dir"]                 # transport table: 9 components x 2Kd channels
     if label == "density_fwd20":
         return 4 * (E * (B + K + 20) + 20 * N * B * K)
     if label == "density_bwd20":
         return 4 * (2 * E * (B + K + 20) + 20 * N * B * K)
-    if label == "density_fwd4":
-        return 4 * (E * (B + Kt + 4) + 4 * N * B * Kt)
-    if label == "density_bwd4":
-        return 4 * (2 * E * (B + Kt + 4) + 4 * N * B * Kt)
+    if label == "transport_fwd":          # phi, u, gathered V|M of Kd channels in; 18 sums per (b, kd) out
+        return 4 * (E * (B + 3 + Kt // 2) + 18 * N * B * kw["K_dir"])
+    if label == "transport_bwd":          # + upstream sums; dphi, du, per-edge table gradient out
+        return 4 * (E * (B + 3 + Kt // 2) + 18 * N * B * kw["K_dir"] + E * (B + 3 + Kt // 2))
     if label == "cp_fwd":
         return 4 * (E * (5 * C + 20) + 20 * N * C)
     if label == "cp_bwd":

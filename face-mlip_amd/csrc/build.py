@@ -19,7 +19,8 @@ ARCH = os.environ.get("FACE_OFFLOAD_ARCH", "gfx950")
 FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-target-feature", "-Xclang",
          "-packed-fp32-ops", "-Wall"]
 # graph.hip evaluates the pair-acceptance test in fp64 with a fixed operation order: no contraction.
-SOURCES = {"capi.hip": "fast", "density.hip": "fast", "node.hip": "fast", "edge.hip": "fast", "graph.hip": "off"}
+SOURCES = {"capi.hip": "fast", "density.hip": "fast", "node.hip": "fast", "edge.hip": "fast", "graph.hip": "off",
+           "transport.hip": "fast"}
 
 
 def compile_one(src):

@@ -177,18 +177,26 @@ __global__ __launch_bounds__(256) void force_scatter_kernel(const float* __restr
 }
 
 // ---------------------------------------------------------------- directional edge features
-// Node table T: element (atom n, row q, channel k) at T[q*sq + n*sn + k]; rows 0-2 = V,
-// rows 3-8 = M in sym storage.
+// Node tables: V element (component a, atom n, channel k) at V[a*v_sq + n*v_sn + k] (3 rows),
+// M likewise (6 rows, sym storage).
 // d[e] = [u.V_j | Y2w.M_j | u.V_i | Y2w.M_i] (4 x Kd), u = Y[1:4], Y2w = Y[4:10] * (1,1,1,2,2,2),
 // j = col[e], i = recv[e]   (face/model.py:474-493).
+struct DirTables {
+    const float* V;
+    const float* M;
+    int64_t v_sn, v_sq, m_sn, m_sq;
+    __device__ __forceinline__ float at(int q, int64_t n, int k) const {
+        return q < 3 ? V[q * v_sq + n * v_sn + k] : M[(q - 3) * m_sq + n * m_sn + k];
+    }
+};
+
 __device__ __forceinline__ void dir_weights(const float* __restrict__ y, float* w) {
     w[0] = y[1]; w[1] = y[2]; w[2] = y[3];
     w[3] = y[4]; w[4] = y[5]; w[5] = y[6];
     w[6] = y[7] * 2.f; w[7] = y[8] * 2.f; w[8] = y[9] * 2.f;
 }
 
-__global__ __launch_bounds__(256) void dir_feats_fwd_kernel(const float* __restrict__ T, int Kd, int64_t sn,
-                                                            int64_t sq, const int32_t* __restrict__ recv,
+__global__ __launch_bounds__(256) void dir_feats_fwd_kernel(DirTables T, int Kd, const int32_t* __restrict__ recv,
                                                             const int32_t* __restrict__ col,
                                                             const float* __restrict__ Y, int64_t E,
                                                             float* __restrict__ d) {
@@ -198,18 +206,17 @@ __global__ __launch_bounds__(256) void dir_feats_fwd_kernel(const float* __restr
     const int k = (int)(t - e * Kd);
     float w[9];
     dir_weights(Y + e * 20, w);
-    const float* Tj = T + (int64_t)col[e] * sn + k;
-    const float* Ti = T + (int64_t)recv[e] * sn + k;
+    const int64_t j = col[e], i = recv[e];
     float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
 #pragma unroll
     for (int q = 0; q < 3; ++q) {
-        a0 = fmaf(w[q], Tj[q * sq], a0);
-        a2 = fmaf(w[q], Ti[q * sq], a2);
+        a0 = fmaf(w[q], T.at(q, j, k), a0);
+        a2 = fmaf(w[q], T.at(q, i, k), a2);
     }
 #pragma unroll
     for (int q = 3; q < 9; ++q) {
-        a1 = fmaf(w[q], Tj[q * sq], a1);
-        a3 = fmaf(w[q], Ti[q * sq], a3);
+        a1 = fmaf(w[q], T.at(q, j, k), a1);
+        a3 = fmaf(w[q], T.at(q, i, k), a3);
     }
     float* de = d + e * 4 * Kd + k;
     de[0] = a0;
@@ -221,8 +228,7 @@ __global__ __launch_bounds__(256) void dir_feats_fwd_kernel(const float* __restr
 // dL/dY for the directional features (monomials 1..9; 0 and 10..19 are written as 0).
 // Thread = (edge, channel slot); the KP lanes of an edge (KP = Kd rounded up to a power of two,
 // <= 64) sum their partial products with butterfly shuffles.
-__global__ __launch_bounds__(256) void dir_feats_bwd_edge_kernel(const float* __restrict__ T, int Kd, int KP,
-                                                                 int64_t sn, int64_t sq,
+__global__ __launch_bounds__(256) void dir_feats_bwd_edge_kernel(DirTables T, int Kd, int KP,
                                                                  const int32_t* __restrict__ recv,
                                                                  const int32_t* __restrict__ col,
                                                                  const float* __restrict__ gd, int64_t E,
@@ -235,14 +241,13 @@ __global__ __launch_bounds__(256) void dir_feats_bwd_edge_kernel(const float* __
 #pragma unroll
     for (int q = 0; q < 9; ++q) acc[q] = 0.f;
     if (ok) {
-        const float* Tj = T + (int64_t)col[e] * sn + k;
-        const float* Ti = T + (int64_t)recv[e] * sn + k;
+        const int64_t j = col[e], i = recv[e];
         const float* g = gd + e * 4 * Kd + k;
         const float g0 = g[0], g1 = g[Kd], g2 = g[2 * Kd], g3 = g[3 * Kd];
 #pragma unroll
-        for (int q = 0; q < 3; ++q) acc[q] = g0 * Tj[q * sq] + g2 * Ti[q * sq];
+        for (int q = 0; q < 3; ++q) acc[q] = g0 * T.at(q, j, k) + g2 * T.at(q, i, k);
 #pragma unroll
-        for (int q = 3; q < 9; ++q) acc[q] = g1 * Tj[q * sq] + g3 * Ti[q * sq];
+        for (int q = 3; q < 9; ++q) acc[q] = g1 * T.at(q, j, k) + g3 * T.at(q, i, k);
     }
 #pragma unroll
     for (int q = 0; q < 9; ++q) acc[q] = group_sum(acc[q], KP);
@@ -258,15 +263,15 @@ __global__ __launch_bounds__(256) void dir_feats_bwd_edge_kernel(const float* __
     }
 }
 
-// dL/dT[n, q, k] = sum_{e in row n} ( gd[rev e, s(q) Kd + k] w_q(rev e) + gd[e, (2 + s(q)) Kd + k] w_q(e) ),
+// dL/dT[q, n, k] = sum_{e in row n} ( gd[rev e, s(q) Kd + k] w_q(rev e) + gd[e, (2 + s(q)) Kd + k] w_q(e) ),
 // s(q) = 0 for the V rows, 1 for the M rows: the neighbour half through the reverse map, the
-// receiver half from the row itself. Thread = (atom n, channel k).
-__global__ __launch_bounds__(256) void dir_feats_bwd_node_kernel(int Kd, int64_t sn, int64_t sq,
-                                                                 const int32_t* __restrict__ row_ptr,
+// receiver half from the row itself. Thread = (atom n, channel k). gV / gM share V / M's layout.
+__global__ __launch_bounds__(256) void dir_feats_bwd_node_kernel(int Kd, int64_t v_sn, int64_t v_sq, int64_t m_sn,
+                                                                 int64_t m_sq, const int32_t* __restrict__ row_ptr,
                                                                  const int32_t* __restrict__ rev,
                                                                  const float* __restrict__ Y,
                                                                  const float* __restrict__ gd, int64_t N,
-                                                                 float* __restrict__ gT) {
+                                                                 float* __restrict__ gV, float* __restrict__ gM) {
     const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     if (t >= N * Kd) return;
     const int64_t n = t / Kd;
@@ -286,9 +291,10 @@ __global__ __launch_bounds__(256) void dir_feats_bwd_node_kernel(int Kd, int64_t
 #pragma unroll
         for (int q = 3; q < 9; ++q) acc[q] += gr1 * wr[q] + ge3 * we[q];
     }
-    float* o = gT + n * sn + k;
 #pragma unroll
-    for (int q = 0; q < 9; ++q) o[q * sq] = acc[q];
+    for (int q = 0; q < 3; ++q) gV[q * v_sq + n * v_sn + k] = acc[q];
+#pragma unroll
+    for (int q = 3; q < 9; ++q) gM[(q - 3) * m_sq + n * m_sn + k] = acc[q];
 }
 
 // Per-row scalar sums with one workgroup per row (few, long rows: energies per structure).
@@ -388,32 +394,36 @@ extern "C" int face_force_scatter(const float* gvec, const int32_t* row_ptr, con
     return 0;
 }
 
-extern "C" int face_dir_feats_fwd(const float* T, int32_t Kd, int64_t sn, int64_t sq, const int32_t* recv,
-                                  const int32_t* col, const float* Y, int64_t E, float* d, void* stream) {
-    if (E < 0 || Kd <= 0 || sn < Kd || sq < Kd) return FACE_ERR_ARG;
+extern "C" int face_dir_feats_fwd(const float* V, int64_t v_sn, int64_t v_sq, const float* M, int64_t m_sn,
+                                  int64_t m_sq, int32_t Kd, const int32_t* recv, const int32_t* col, const float* Y,
+                                  int64_t E, float* d, void* stream) {
+    if (E < 0 || Kd <= 0) return FACE_ERR_ARG;
     if (E == 0) return 0;
-    if (!T || !recv || !col || !Y || !d) return FACE_ERR_ARG;
-    hipLaunchKernelGGL(dir_feats_fwd_kernel, dim3(blocks_for(E * Kd)), dim3(256), 0, (hipStream_t)stream, T, Kd, sn,
-                       sq, recv, col, Y, E, d);
+    if (!V || !M || !recv || !col || !Y || !d) return FACE_ERR_ARG;
+    DirTables T{V, M, v_sn, v_sq, m_sn, m_sq};
+    hipLaunchKernelGGL(dir_feats_fwd_kernel, dim3(blocks_for(E * Kd)), dim3(256), 0, (hipStream_t)stream, T, Kd, recv,
+                       col, Y, E, d);
     FACE_LAUNCH_CHECK();
     return 0;
 }
 
-extern "C" int face_dir_feats_bwd(const float* T, int32_t Kd, int64_t sn, int64_t sq, const int32_t* row_ptr,
-                                  const int32_t* recv, const int32_t* col, const int32_t* rev, const float* Y,
-                                  const float* gd, int64_t N, int64_t E, float* gT, float* gY, void* stream) {
-    if (E < 0 || N < 0 || Kd <= 0 || Kd > 64 || sn < Kd || sq < Kd) return FACE_ERR_ARG;
-    if (!T || !row_ptr || !recv || !col || !rev || !Y || !gd) return FACE_ERR_ARG;
+extern "C" int face_dir_feats_bwd(const float* V, int64_t v_sn, int64_t v_sq, const float* M, int64_t m_sn,
+                                  int64_t m_sq, int32_t Kd, const int32_t* row_ptr, const int32_t* recv,
+                                  const int32_t* col, const int32_t* rev, const float* Y, const float* gd, int64_t N,
+                                  int64_t E, float* gV, float* gM, float* gY, void* stream) {
+    if (E < 0 || N < 0 || Kd <= 0 || Kd > 64) return FACE_ERR_ARG;
+    if (!V || !M || !row_ptr || !recv || !col || !rev || !Y || !gd || (!gV != !gM)) return FACE_ERR_ARG;
+    DirTables T{V, M, v_sn, v_sq, m_sn, m_sq};
     hipStream_t st = (hipStream_t)stream;
     if (gY && E > 0) {
         int KP = 1;
         while (KP < Kd) KP <<= 1;
-        hipLaunchKernelGGL(dir_feats_bwd_edge_kernel, dim3(blocks_for(E * KP)), dim3(256), 0, st, T, Kd, KP, sn, sq,
-                           recv, col, gd, E, gY);
+        hipLaunchKernelGGL(dir_feats_bwd_edge_kernel, dim3(blocks_for(E * KP)), dim3(256), 0, st, T, Kd, KP, recv, col,
+                           gd, E, gY);
     }
-    if (gT && N > 0)
-        hipLaunchKernelGGL(dir_feats_bwd_node_kernel, dim3(blocks_for(N * Kd)), dim3(256), 0, st, Kd, sn, sq, row_ptr,
-                           rev, Y, gd, N, gT);
+    if (gV && N > 0)
+        hipLaunchKernelGGL(dir_feats_bwd_node_kernel, dim3(blocks_for(N * Kd)), dim3(256), 0, st, Kd, v_sn, v_sq,
+                           m_sn, m_sq, row_ptr, rev, Y, gd, N, gV, gM);
     FACE_LAUNCH_CHECK();
     return 0;
 }

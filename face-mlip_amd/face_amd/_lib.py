@@ -40,15 +40,19 @@ _SIGS = {
     "face_nbr_padded": (ctypes.c_int, [P, P, P, P, P, I64, I32, P, P, P, P]),
     "face_edge_geom_fwd": (ctypes.c_int, [P, P, P, P, P, I64, P, I32, F32, F32, P, P, P, P, P]),
     "face_edge_geom_bwd": (ctypes.c_int, [P, P, P, P, P, I64, P, I32, F32, F32, P, P, P, P, P, P]),
-    "face_dir_feats_fwd": (ctypes.c_int, [P, I32, I64, I64, P, P, P, I64, P, P]),
-    "face_dir_feats_bwd": (ctypes.c_int, [P, I32, I64, I64, P, P, P, P, P, P, I64, I64, P, P, P]),
+    "face_dir_feats_fwd": (ctypes.c_int, [P, I64, I64, P, I64, I64, I32, P, P, P, I64, P, P]),
+    "face_dir_feats_bwd": (ctypes.c_int, [P, I64, I64, P, I64, I64, I32, P, P, P, P, P, P, I64, I64, P, P, P, P]),
+    "face_transport_fwd": (ctypes.c_int, [P, I32, I32, P, I64, I64, P, I64, I64, I32, P, I32, P, P, I64, F32, P, P,
+                                          P]),
+    "face_transport_bwd": (ctypes.c_int, [P, I32, I32, P, I64, I64, P, I64, I64, I32, P, I32, P, P, P, I64, I32, F32,
+                                          P, P, P, I32, P, P, P, P, P]),
     "face_gather_rows": (ctypes.c_int, [P, I32, P, I64, I32, P, I32, P]),
     "face_gather_rows_bwd": (ctypes.c_int, [P, I32, P, P, I64, I32, P, I32, P]),
     "face_segment_sum": (ctypes.c_int, [P, I32, P, I64, I32, P, I32, P]),
     "face_force_scatter": (ctypes.c_int, [P, P, P, I64, F32, P, P]),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 def lib():

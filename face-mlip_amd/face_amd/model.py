@@ -9,9 +9,10 @@ runs:
   * edges are a receiver-grouped CSR list (no padded slots); geometry, basis, envelope and
     monomials come from one HIP kernel whose backward also performs the force scatter
     through the reverse-edge map (no atomics);
-  * the factor density (face/kernels.py), the CP pooling (face/model.py:496-502) and the
-    transport sums (face/model.py:515-522, the same contraction with 4 monomials) run in
-    the segmented HIP density kernels, reading gathered neighbour tables in place;
+  * the factor density (face/kernels.py) and the CP pooling (face/model.py:496-502, with the
+    cutoff envelope folded in) run in segmented HIP density kernels; the directional features
+    and the transport moments (face/model.py:474-533) run in one fused HIP operator that
+    reads the neighbour tables in place and writes the transport sums already mapped;
   * moments are kept monomial-major, one (k_l, N, C) tensor per rank, so `mix`, `proj` and
     the readout are plain row-major GEMMs on contiguous blocks, and the node kernel reads
     P/Q/S straight out of the projection output and writes the invariant families straight
@@ -33,29 +34,6 @@ from .neighbors import graph_from_padded
 from .ops import Graph
 
 RANKS = [(0, 1), (1, 4), (4, 10), (10, 20)]   # monomial range of each rank (face/cartesian.py:18)
-
-
-def transport_map():
-    """(36 = bond monomial p*9 + table component q, 18) map of the transport sums.
-
-    Columns: [sum phi V (3) | sum phi M u (3) | sum phi M (6) | sum phi sym(u (x) V) (6)],
-    q = [V_x V_y V_z | M_xx M_yy M_zz M_xy M_xz M_yz], p = [1, u_x, u_y, u_z]
-    (the map of face/model.py:342-362, derived here from those definitions).
-    """
-    pairs = [(0, 0), (1, 1), (2, 2), (0, 1), (0, 2), (1, 2)]
-    comp = {}
-    for k, (a, b) in enumerate(pairs):
-        comp[(a, b)] = comp[(b, a)] = k
-    T = torch.zeros(36, 18, dtype=torch.float64)
-    for a in range(3):
-        T[0 * 9 + a, a] = 1.0                                  # V_a
-        for c in range(3):
-            T[(c + 1) * 9 + 3 + comp[(a, c)], 3 + a] += 1.0     # M_ac u_c
-    for k, (a, b) in enumerate(pairs):
-        T[3 + k, 6 + k] = 1.0                                  # M_k
-        T[(a + 1) * 9 + b, 12 + k] += 0.5                      # (u_a V_b + u_b V_a) / 2
-        T[(b + 1) * 9 + a, 12 + k] += 0.5
-    return T
 
 
 class BesselEnvelope(nn.Module):
@@ -181,7 +159,7 @@ class FactorBlock(nn.Module):
             self.tmix3 = nn.Linear(B * 2 * K_dir, C, bias=False)
 
     # ------------------------------------------------------------------ moments
-    def moments(self, h, rb, Y, env, zp, zidx, avg_nb, sets, eq, g, tmap):
+    def moments(self, h, rb, Y, env, zp, zidx, avg_nb, sets, eq, g):
         """Moments A_l as monomial-major (k_l, N, C) blocks (face/model.py:460-534)."""
         N, E = g.N, g.E
         B, C, Kd = self.B, self.C, self.K
@@ -199,8 +177,7 @@ class FactorBlock(nn.Module):
                 src2 = torch.cat([S[2] for S in sets], -1)
             Vb = self.pvt(src1)                                                  # (3, N, nt*Kd)
             Mb = self.pmt(src2)                                                  # (6, N, nt*Kd)
-            T = torch.cat([Vb[..., :Kd], Mb[..., :Kd]], 0)                       # (9, N, Kd)
-            d = ops.dir_features(T, Y, g)                                         # (E, 4Kd)
+            d, D1, D2 = ops.dir_transport(Vb, Mb, phi, Y, g, Kd, self.transport)   # (E, 4Kd), transport sums
             mj, gathered = ops.gather_neighbour(msg_n, g) + self.dir_mix(d), False
         else:
             mj, gathered = msg_n, True
@@ -212,20 +189,16 @@ class FactorBlock(nn.Module):
             Af = ops.density(phi, mj, Y, g, 20, gathered)                         # 4 x (k_l, N, B*K)
         A = [self.mix[l](Af[l]) * s[None, :, l, :] for l in range(4)]             # 4 x (k_l, N, C)
         if self.transport:
-            table = torch.cat([Vb[..., Kd:], Mb[..., Kd:]], 0).permute(1, 2, 0).reshape(N, Kd * 9)
-            St = ops.density(phi, table, Y, g, 4, True)                           # (4, N, B*9Kd)
-            X = St.view(4, N, B, Kd, 9).permute(1, 2, 3, 0, 4).reshape(N, B, Kd, 36) / avg_nb
-            D = X @ tmap                                                          # (N, B, Kd, 18)
-            D1 = D[..., :6].reshape(N, B, Kd, 2, 3).permute(4, 0, 1, 3, 2).reshape(3, N, B * 2 * Kd)
-            D2 = D[..., 6:18].reshape(N, B, Kd, 2, 6).permute(4, 0, 1, 3, 2).reshape(6, N, B * 2 * Kd)
-            A[1] = A[1] + self.tmix1(D1) * (s[None, :, 1, :] * avg_nb)
-            A[2] = A[2] + self.tmix2(D2) * (s[None, :, 2, :] * avg_nb)
+            # D1/D2 are the raw sums; the reference's 1/avg_nb (face/model.py:522) and its avg_nb
+            # factor (:532-533) cancel through the linear tmix, leaving s = elem_scale / avg_nb
+            A[1] = A[1] + self.tmix1(D1) * s[None, :, 1, :]
+            A[2] = A[2] + self.tmix2(D2) * s[None, :, 2, :]
         return A
 
     # ------------------------------------------------------------------ invariants + readout
-    def forward(self, h, rb, Y, env, zp, zidx, avg_nb, sets, eq, g, tmap):
+    def forward(self, h, rb, Y, env, zp, zidx, avg_nb, sets, eq, g):
         C = self.C
-        A = self.moments(h, rb, Y, env, zp, zidx, avg_nb, sets, eq, g, tmap)
+        A = self.moments(h, rb, Y, env, zp, zidx, avg_nb, sets, eq, g)
         allsets = sets + [A]
         ys = []
         for l in range(4):
@@ -280,7 +253,6 @@ class FACE(nn.Module):
         self.register_buffer("scale", torch.tensor(1.0))
         self.register_buffer("avg_nb", torch.tensor(10.0))
         self.terms = nn.ModuleDict()
-        self.register_buffer("tmap", transport_map().float(), persistent=False)
         self._padded_cache = {}
 
     def fuse(self, on=True):
@@ -319,7 +291,7 @@ class FACE(nn.Module):
         e_at = self.E0[zidx].clone()
         sets, eq = [], None
         for blk in self.blocks:
-            e, h, A, eq = blk(h, rb, Y, env, zp, zidx, self.avg_nb, sets, eq, graph, self.tmap)
+            e, h, A, eq = blk(h, rb, Y, env, zp, zidx, self.avg_nb, sets, eq, graph)
             sets.append(A)
             e_at = e_at + self.scale * e.squeeze(-1)
         E = ops.StructureSum.apply(e_at, graph.struct_ptr, graph.batch, graph.nstr)

@@ -146,38 +146,71 @@ def gather_receiver(X, graph):
     return out.view(graph.E, *shp[1:])
 
 
-class DirFeatures(torch.autograd.Function):
-    """Directional edge features d (E, 4Kd) from the node table T (9, N, Kd) (rows: V then M
-    components) and the monomials (face/model.py:474-493), without materialising gathers."""
+class DirTransport(torch.autograd.Function):
+    """Directional edge features and transport moments from the node tables Vb (3, N, nt*Kd),
+    Mb (6, N, nt*Kd) (component-major; channels [0, Kd) directional, [Kd, 2Kd) transport).
+
+    d (E, 4Kd) = [u.V_j | u^T M_j u | u.V_i | u^T M_i u]          (face/model.py:474-493)
+    D1 (3, N, B*2Kd), D2 (6, N, B*2Kd): sum_e phi[e, b] F(u, V_j, M_j)  (face/model.py:514-528)
+    One autograd node for both, so the tables' gradient is assembled in place (no slices).
+    """
 
     @staticmethod
-    def forward(ctx, T, Y, graph):
-        _lib.require_gpu(T, Y)
-        T = T.contiguous().float()
+    def forward(ctx, Vb, Mb, phi, Y, graph, Kd, transport):
+        _lib.require_gpu(Vb, Mb, phi, Y)
+        Vb, Mb = Vb.contiguous().float(), Mb.contiguous().float()
         Y = Y.contiguous().float()
-        Kd = T.shape[2]
-        d = torch.empty(graph.E, 4 * Kd, device=T.device)
-        call("face_dir_feats_fwd", ptr(T), Kd, T.stride(1), T.stride(0), ptr(graph.recv), ptr(graph.col), ptr(Y),
-             graph.E, ptr(d), _lib.stream_of(T), label="dir_fwd")
-        ctx.save_for_backward(T, Y)
-        ctx.graph = graph
-        return d
+        N, E = graph.N, graph.E
+        dev = Vb.device
+        st = _lib.stream_of(Vb)
+        d = torch.empty(E, 4 * Kd, device=dev)
+        call("face_dir_feats_fwd", ptr(Vb), Vb.stride(1), Vb.stride(0), ptr(Mb), Mb.stride(1), Mb.stride(0), Kd,
+             ptr(graph.recv), ptr(graph.col), ptr(Y), E, ptr(d), st, label="dir_fwd")
+        D1 = D2 = None
+        phi_ = phi
+        if transport:
+            phi_, ld_phi = _rows(phi, phi.shape[1])
+            B = phi.shape[1]
+            D1 = torch.empty(3, N, B * 2 * Kd, device=dev)
+            D2 = torch.empty(6, N, B * 2 * Kd, device=dev)
+            call("face_transport_fwd", ptr(phi_), ld_phi, B, ptr(Vb) + 4 * Kd, Vb.stride(1), Vb.stride(0),
+                 ptr(Mb) + 4 * Kd, Mb.stride(1), Mb.stride(0), Kd, ptr(Y), 20, ptr(graph.col), ptr(graph.row_ptr), N,
+                 1.0, ptr(D1), ptr(D2), st, label="transport_fwd")
+        ctx.save_for_backward(Vb, Mb, phi_ if transport else torch.empty(0), Y)
+        ctx.graph, ctx.Kd, ctx.transport = graph, Kd, transport
+        return d, D1, D2
 
     @staticmethod
-    def backward(ctx, gd):
-        T, Y = ctx.saved_tensors
-        g = ctx.graph
-        gd = gd.contiguous().float()
-        Kd = T.shape[2]
-        gT = torch.empty_like(T) if ctx.needs_input_grad[0] else None
-        gY = torch.empty_like(Y) if ctx.needs_input_grad[1] else None
-        call("face_dir_feats_bwd", ptr(T), Kd, T.stride(1), T.stride(0), ptr(g.row_ptr), ptr(g.recv), ptr(g.col),
-             ptr(g.rev), ptr(Y), ptr(gd), g.N, g.E, ptr(gT), ptr(gY), _lib.stream_of(gd), label="dir_bwd")
-        return gT, gY, None
+    def backward(ctx, gd, gD1, gD2):
+        Vb, Mb, phi, Y = ctx.saved_tensors
+        g, Kd = ctx.graph, ctx.Kd
+        N, E = g.N, g.E
+        dev = Vb.device
+        st = _lib.stream_of(Vb)
+        gd = torch.zeros(E, 4 * Kd, device=dev) if gd is None else gd.contiguous().float()
+        gVb = torch.empty_like(Vb)
+        gMb = torch.empty_like(Mb)
+        gY = torch.empty_like(Y)
+        call("face_dir_feats_bwd", ptr(Vb), Vb.stride(1), Vb.stride(0), ptr(Mb), Mb.stride(1), Mb.stride(0), Kd,
+             ptr(g.row_ptr), ptr(g.recv), ptr(g.col), ptr(g.rev), ptr(Y), ptr(gd), N, E, ptr(gVb), ptr(gMb), ptr(gY),
+             st, label="dir_bwd")
+        dphi = None
+        if ctx.transport:
+            B = phi.shape[1]
+            W = B * 2 * Kd
+            gD1 = torch.zeros(3, N, W, device=dev) if gD1 is None else gD1.contiguous().float()
+            gD2 = torch.zeros(6, N, W, device=dev) if gD2 is None else gD2.contiguous().float()
+            dphi = torch.empty(E, B, device=dev)
+            dT = torch.empty(E, 9, Kd, device=dev)
+            call("face_transport_bwd", ptr(phi), phi.stride(0), B, ptr(Vb) + 4 * Kd, Vb.stride(1), Vb.stride(0),
+                 ptr(Mb) + 4 * Kd, Mb.stride(1), Mb.stride(0), Kd, ptr(Y), 20, ptr(g.col), ptr(g.row_ptr), ptr(g.rev),
+                 N, g.max_row, 1.0, ptr(gD1), ptr(gD2), ptr(dphi), B, ptr(dT), ptr(gVb) + 4 * Kd, ptr(gMb) + 4 * Kd,
+                 ptr(gY), st, label="transport_bwd")
+        return gVb, gMb, dphi, gY, None, None, None
 
 
-def dir_features(T, Y, graph):
-    return DirFeatures.apply(T, Y, graph)
+def dir_transport(Vb, Mb, phi, Y, graph, Kd, transport):
+    return DirTransport.apply(Vb, Mb, phi, Y, graph, Kd, transport)
 
 
 class StructureSum(torch.autograd.Function):

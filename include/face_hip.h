@@ -19,6 +19,7 @@
  *   face/neighbors.py:7-37       padded_graph (ASE neighbor_list) -> face_nbr_* (count, fill, rev, padded)
  *   face/model.py:670-677        edge geometry + Bessel basis     -> face_edge_geom_fwd / _bwd
  *   face/model.py:474-493        directional edge features        -> face_dir_feats_fwd / _bwd
+ *   face/model.py:514-533        transport sums + transport map   -> face_transport_fwd / _bwd
  *   face/model.py:670,464,692-694 index_select gathers and their index_add backward
  *                                                                  -> face_gather_rows, face_gather_rows_bwd,
  *                                                                     face_force_scatter
@@ -179,19 +180,42 @@ int face_edge_geom_bwd(const float* pos, const int32_t* recv, const int32_t* col
                        void* stream);
 
 /* ---------------------------------------------------------------- directional edge features
- * Node table T: element (atom n, row q, channel k) at T[q*sq + n*sn + k], rows 0-2 = V_k,
- * rows 3-8 = M_k (sym storage), Kd channels.
+ * Node tables of Kd channels: V element (component a, atom n, channel k) at
+ * V[a*v_sq + n*v_sn + k] (3 components), M likewise (6 components, sym storage).
  * d (E, 4*Kd) = [u.V_j | u^T M_j u | u.V_i | u^T M_i u] with u = Y[e,1:4], u^T M u =
  * sum_q Y[e,4+q] * (1,1,1,2,2,2)_q * M_q, j = col[e], i = recv[e]
  * (face/model.py:474-493, the per-edge d fed to dir_mix).                                  */
-int face_dir_feats_fwd(const float* T, int32_t Kd, int64_t sn, int64_t sq, const int32_t* recv, const int32_t* col,
-                       const float* Y, int64_t E, float* d, void* stream);
-/* Backward for gd = dL/dd (E, 4*Kd): gT (same layout as T) through the reverse-edge map (no
- * atomics), gY (E, 20) (monomials 0 and 10..19 written as zero). Either output may be NULL.
+int face_dir_feats_fwd(const float* V, int64_t v_sn, int64_t v_sq, const float* M, int64_t m_sn, int64_t m_sq,
+                       int32_t Kd, const int32_t* recv, const int32_t* col, const float* Y, int64_t E, float* d,
+                       void* stream);
+/* Backward for gd = dL/dd (E, 4*Kd): gV, gM (same layouts as V, M; both or neither) through the
+ * reverse-edge map (no atomics), gY (E, 20) (monomials 0 and 10..19 written as zero; may be NULL).
  * Kd <= 64. */
-int face_dir_feats_bwd(const float* T, int32_t Kd, int64_t sn, int64_t sq, const int32_t* row_ptr,
-                       const int32_t* recv, const int32_t* col, const int32_t* rev, const float* Y, const float* gd,
-                       int64_t N, int64_t E, float* gT, float* gY, void* stream);
+int face_dir_feats_bwd(const float* V, int64_t v_sn, int64_t v_sq, const float* M, int64_t m_sn, int64_t m_sq,
+                       int32_t Kd, const int32_t* row_ptr, const int32_t* recv, const int32_t* col, const int32_t* rev,
+                       const float* Y, const float* gd, int64_t N, int64_t E, float* gV, float* gM, float* gY,
+                       void* stream);
+
+/* ---------------------------------------------------------------- transport moments
+ * D[i, b, kd, :] = scale * sum_{e in row i} phi[e, b] * F(u_e, V_j[kd], M_j[kd]),
+ * F = [V (3) | M u (3) | M (6) | sym(u (x) V) (6)], j = col[e], u = Y[e, 1:4]: the transport sums of
+ * face/model.py:514-528 ([1,u] (x) phi (x) [V|M] mapped by its (36,18) transport map), written as
+ * D1 (3, N, B*2*Kd) = [V | M u] and D2 (6, N, B*2*Kd) = [M | sym(u V)], channel b*2Kd + t*Kd + kd.
+ * Tables V, M as for the directional features (the transport half of the channels).
+ * B * Kd <= 1024.                                                                            */
+int face_transport_fwd(const float* phi, int32_t ld_phi, int32_t B, const float* V, int64_t v_sn, int64_t v_sq,
+                       const float* M, int64_t m_sn, int64_t m_sq, int32_t Kd, const float* Y, int32_t ld_Y,
+                       const int32_t* col, const int32_t* row_ptr, int64_t N, float scale, float* D1, float* D2,
+                       void* stream);
+/* Backward for gD1, gD2 (layouts of D1, D2): dphi (E, ld_dphi) (may be NULL), dT_edge (E, 9, Kd)
+ * per-edge table gradient (workspace), gV / gM (table gradients through the reverse map; both or
+ * neither, written in V / M's layout), gY: du is ADDED to gY[e, 1..3] (gY must hold the other
+ * contributions, e.g. face_dir_feats_bwd's output; may be NULL). B <= 32, Kd <= 64.          */
+int face_transport_bwd(const float* phi, int32_t ld_phi, int32_t B, const float* V, int64_t v_sn, int64_t v_sq,
+                       const float* M, int64_t m_sn, int64_t m_sq, int32_t Kd, const float* Y, int32_t ld_Y,
+                       const int32_t* col, const int32_t* row_ptr, const int32_t* rev, int64_t N, int32_t max_row,
+                       float scale, const float* gD1, const float* gD2, float* dphi, int32_t ld_dphi, float* dT_edge,
+                       float* gV, float* gM, float* gY, void* stream);
 
 /* ---------------------------------------------------------------- gathers and scatters
  * out[e, :] = X[idx[e], :] for F features (X row stride ld_X, out row stride ld_out). */

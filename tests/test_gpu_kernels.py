@@ -270,28 +270,53 @@ def test_edge_geometry_forward_and_backward():
     assert max(errs) < TOL, errs
 
 
-def test_directional_features_and_gradients():
-    """d = [u.V_j, u^T M_j u, u.V_i, u^T M_i u] (face/model.py:474-493) vs gathered einsums."""
+@pytest.mark.parametrize("Kd,B,transport", [(16, 16, True), (4, 8, True), (5, 4, False), (16, 16, False)])
+def test_dir_transport_and_gradients(Kd, B, transport):
+    """Directional features d = [u.V_j, u^T M_j u, u.V_i, u^T M_i u] (face/model.py:474-493) and the
+    transport sums D1 = [sum phi V, sum phi M u], D2 = [sum phi M, sum phi sym(u V)] (face/model.py:
+    514-528) vs gathered einsums and the oracle's explicit per-edge transport tensors."""
     from face_amd import ops
-    say("directional features")
-    for Kd, seed in ((16, 0), (4, 1), (5, 2)):
-        g = _G(37, 300, seed + 10)
-        E = sum(g.counts)
-        torch.manual_seed(seed)
-        T = torch.randn(9, 37, Kd, device=DEV, requires_grad=True)
-        Y = torch.randn(E, 20, device=DEV, requires_grad=True)
-        d = ops.dir_features(T, Y, g.G)
-        w = torch.randn_like(d)
-        gT, gY = torch.autograd.grad((d * w).sum(), (T, Y))
-        gT = gT.permute(1, 0, 2)
-        Tc = T.detach().double().cpu().permute(1, 0, 2).contiguous().requires_grad_(True)
-        Yc = Y.detach().double().cpu().requires_grad_(True)
-        col, recv = g.G.col.long().cpu(), g.G.recv.long().cpu()
-        u = Yc[:, 1:4]
-        Y2 = Yc[:, 4:10] * torch.tensor([1.0, 1, 1, 2, 2, 2], dtype=torch.float64)
-        Tj, Ti = Tc[col], Tc[recv]
-        d2 = torch.cat([(u[:, :, None] * Tj[:, :3]).sum(1), (Y2[:, :, None] * Tj[:, 3:]).sum(1),
-                        (u[:, :, None] * Ti[:, :3]).sum(1), (Y2[:, :, None] * Ti[:, 3:]).sum(1)], -1)
-        gT2, gY2 = torch.autograd.grad((d2 * w.double().cpu()).sum(), (Tc, Yc))
-        errs = [rel(d, d2), rel(gT, gT2), rel(gY, gY2)]
-        assert max(errs) < TOL, (Kd, errs)
+    say("dir/transport", Kd, B, transport)
+    g = _G(37, 300, Kd + 10)
+    counts = g.counts
+    E = sum(counts)
+    nt = 2 if transport else 1
+    torch.manual_seed(Kd)
+    Vb = torch.randn(3, 37, nt * Kd, device=DEV, requires_grad=True)
+    Mb = torch.randn(6, 37, nt * Kd, device=DEV, requires_grad=True)
+    phi = torch.randn(E, B, device=DEV, requires_grad=True)
+    Y = torch.randn(E, 20, device=DEV, requires_grad=True)
+    d, D1, D2 = ops.dir_transport(Vb, Mb, phi, Y, g.G, Kd, transport)
+    wd = torch.randn_like(d)
+    L = (d * wd).sum()
+    if transport:
+        w1, w2 = torch.randn_like(D1), torch.randn_like(D2)
+        L = L + (D1 * w1).sum() + (D2 * w2).sum()
+    ins = [Vb, Mb, Y] + ([phi] if transport else [])
+    grads = torch.autograd.grad(L, ins)
+    # oracle (fp64, CPU)
+    c = [t.detach().double().cpu().requires_grad_(True) for t in ins]
+    Vc, Mc, Yc = c[:3]
+    col, recv = g.G.col.long().cpu(), g.G.recv.long().cpu()
+    u = Yc[:, 1:4]
+    Y2 = Yc[:, 4:10] * torch.tensor([1.0, 1, 1, 2, 2, 2], dtype=torch.float64)
+    Vj, Mj = Vc[:, col, :Kd], Mc[:, col, :Kd]            # (3|6, E, Kd)
+    Vi, Mi = Vc[:, recv, :Kd], Mc[:, recv, :Kd]
+    d2 = torch.cat([torch.einsum("ea,aek->ek", u, Vj), torch.einsum("ea,aek->ek", Y2, Mj),
+                    torch.einsum("ea,aek->ek", u, Vi), torch.einsum("ea,aek->ek", Y2, Mi)], -1)
+    L2 = (d2 * wd.double().cpu()).sum()
+    outs, refs = [d], [d2]
+    if transport:
+        pc = c[3]
+        M = max(counts)
+        pd = lambda t: _pad(t, counts, M)
+        Vt = Vc[:, col, Kd:].permute(1, 2, 0)            # (E, Kd, 3)
+        Mt = Mc[:, col, Kd:].permute(1, 2, 0)            # (E, Kd, 6)
+        R1, R2 = oops.transport_sums(pd(pc), pd(u), pd(Vt), pd(Mt), 1.0)   # (N, B*2Kd, 3|6)
+        R1, R2 = R1.permute(2, 0, 1), R2.permute(2, 0, 1)
+        L2 = L2 + (R1 * w1.double().cpu()).sum() + (R2 * w2.double().cpu()).sum()
+        outs += [D1, D2]
+        refs += [R1, R2]
+    grads2 = torch.autograd.grad(L2, c)
+    errs = [rel(a, b) for a, b in zip(outs, refs)] + [rel(a, b) for a, b in zip(grads, grads2)]
+    assert max(errs) < TOL, errs

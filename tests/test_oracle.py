@@ -170,24 +170,6 @@ def test_transport_sums_explicit_per_edge():
         assert torch.allclose(D2[n, b * 2 * Kd + Kd + k], cartesian.to_sym2(uv))
 
 
-def test_product_transport_map_matches_explicit_sums():
-    """The (36,18) map the GPU model applies after the 4-monomial density reproduces the
-    explicit per-edge transport tensors."""
-    from face_amd.model import transport_map
-    torch.manual_seed(2)
-    E = 7
-    u = torch.nn.functional.normalize(torch.randn(E, 3, dtype=torch.float64), dim=-1)
-    V = torch.randn(E, 3, dtype=torch.float64)
-    Ms = torch.randn(E, 6, dtype=torch.float64)
-    Y4 = torch.cat([torch.ones(E, 1, dtype=torch.float64), u], 1)
-    X = (Y4[:, :, None] * torch.cat([V, Ms], 1)[:, None, :]).reshape(E, 36)
-    D = X @ transport_map()
-    M = cartesian.expand(Ms, 2)
-    uV = 0.5 * (torch.einsum("ea,eb->eab", u, V) + torch.einsum("ea,eb->eab", V, u))
-    want = torch.cat([V, torch.einsum("eab,eb->ea", M, u), Ms, cartesian.to_sym2(uV)], 1)
-    assert torch.allclose(D, want, atol=1e-13)
-
-
 # ----------------------------------------------------------------------------- neighbour list
 def _naive_pairs(pos, cell, pbc, rc, span=3):
     out = []
