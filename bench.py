@@ -56,9 +56,9 @@ def algorithmic_bytes(label, g, kw):
     if label == "cp_bwd":
         return 4 * (2 * E * (5 * C + 20) + 20 * N * C)
     if label == "node_fwd":
-        return 4 * 64 * N * C           # 47 in, 8 invariants + 3 V + 6 symmetric M out (eq pass)
+        return 4 * 67 * N * C           # 47 in; 8 invariants + V (3) + full Mf (9) out
     if label == "node_bwd":
-        return 4 * 111 * N * C          # 47 in, 8 + 3 + 6 upstream, 47 out
+        return 4 * 114 * N * C          # 47 in, 20 upstream, 47 out
     if label == "edge_fwd":
         return 4 * E * (11 + 29)
     if label == "edge_bwd":
@@ -96,6 +96,7 @@ def run_gpu(k, steps, warmup, use_graph=True):
         step()
     torch.cuda.synchronize()
     log(f"[bench]   warm-up done ({warmup} steps)")
+    torch.cuda.reset_peak_memory_stats()
     # eager pass: HIP events around every hot-kernel launch (kernel durations)
     timers = _lib.time_calls(TIMED)
     torch.cuda.synchronize()
@@ -105,7 +106,8 @@ def run_gpu(k, steps, warmup, use_graph=True):
     torch.cuda.synchronize()
     dt_eager = time.perf_counter() - t0
     _lib.stop_timing()
-    log(f"[bench]   eager: {1e3 * dt_eager / steps:.3f} ms/step")
+    peak_gb = torch.cuda.max_memory_allocated() / 1e9
+    log(f"[bench]   eager: {1e3 * dt_eager / steps:.3f} ms/step, peak device memory {peak_gb:.2f} GB")
     dt = dt_eager
     mode = "eager"
     if use_graph:
@@ -138,7 +140,44 @@ def run_gpu(k, steps, warmup, use_graph=True):
     log(f"[bench]   {ms_step:.3f} ms/step, {g.N * steps / dt:.0f} atom-steps/s")
     return {"N": g.N, "E": g.E, "ms_per_step": ms_step, "atom_steps_per_s": g.N * steps / dt, "kernels": kern,
             "pairlist_ms": 1e3 * t_nbr, "desc": desc, "kw": kw, "mode": mode,
-            "eager_ms_per_step": 1e3 * dt_eager / steps}
+            "eager_ms_per_step": 1e3 * dt_eager / steps, "peak_mem_gb": peak_gb}
+
+
+def pmc_probe(k, steps=2, copy_floats=1 << 28):
+    """Short run for hardware-counter passes: a few eager E+F steps of workload k, then a plain
+    device-to-device copy of a known size, whose FETCH_SIZE / WRITE_SIZE readings calibrate the
+    counters (bytes known / counter reading)."""
+    from face_amd import systems
+    from face_amd.neighbors import build_graph
+    sts, kw, el, desc = systems.workload(k)
+    g = build_graph(sts, kw["rc"])
+    m = model_for(kw, el)
+    for _ in range(steps):
+        m(g.with_pos(g.pos.clone()))["forces"]
+    torch.cuda.synchronize()
+    src = torch.ones(copy_floats, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    out = {"probe": desc, "steps": steps, "copy_bytes_read": 4 * copy_floats, "copy_bytes_written": 4 * copy_floats,
+           "alg_bytes": {lab: algorithmic_bytes(lab, g, kw) for lab in TIMED}}
+    print(json.dumps(out), flush=True)
+
+
+def measured_traffic(label):
+    """HBM bytes per launch of a labelled kernel from the committed counter summary, or None."""
+    path = os.path.join(REPO, "profiles", "traffic_liquid24k_cp160.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        parts = [x.strip() for x in line.strip().strip("|").split("|")]
+        if len(parts) >= 6 and parts[0] == label:
+            try:
+                return float(parts[5])
+            except ValueError:
+                return None
+    return None
 
 
 def run_cpu(k, n_atoms, rounds=5, warm=2):
@@ -178,10 +217,12 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-atoms", type=int, default=1500)
     ap.add_argument("--eager", action="store_true", help="time eager steps instead of HIP-graph replays")
+    ap.add_argument("--pmc-probe", action="store_true", help="short run for rocprofv3 --pmc passes")
     a = ap.parse_args()
     if a.gpus != 1:
-        print("bench.py measures one GPU: every box here has one MI355X and this build has no multi-GPU "
-              "path (see DESIGN.md for how the work would shard). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU only: there is no multi-GPU path in this library (the pair list "
+              "would shard by spatial domain with halo atoms; nothing here runs it). Run with --gpus 1.",
+              file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
@@ -189,6 +230,9 @@ def main():
     torch.backends.cuda.matmul.allow_tf32 = False
     torch.backends.cudnn.allow_tf32 = False
     torch.set_float32_matmul_precision("highest")
+    if a.pmc_probe:
+        pmc_probe(a.workload)
+        return
     main_run = run_gpu(a.workload, a.steps, a.warmup, not a.eager)
     also = {}
     for k in [int(x) for x in a.also.split(",") if x.strip()]:
@@ -207,7 +251,8 @@ def main():
     if dom:
         ach = hbm[dom]["GBps"]
         roofline = {"kernel": dom, "bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": ach / HBM_PEAK_GBS, "traffic": None, "alg_bytes_per_launch": hbm[dom]["alg_bytes"],
+                    "frac": ach / HBM_PEAK_GBS,
+                    "traffic": measured_traffic(dom) if a.workload == 3 else None, "alg_bytes_per_launch": hbm[dom]["alg_bytes"],
                     "avg_launch_us": hbm[dom]["avg_us"]}
     cpu = None
     if not a.no_cpu:
@@ -222,7 +267,8 @@ def main():
         "config": {"workload": main_run["desc"], "atoms": main_run["N"], "pairs": main_run["E"],
                    "model": {k: kw[k] for k in ("C", "B", "K", "rc") if k in kw} | {"cp": bool(kw.get("cp"))},
                    "weights": "random init, torch.manual_seed(0) + unit_parameterise", "parallelism": "single GPU",
-                   "step": main_run["mode"], "eager_ms_per_step": main_run["eager_ms_per_step"]},
+                   "step": main_run["mode"], "eager_ms_per_step": main_run["eager_ms_per_step"],
+                   "peak_mem_gb": main_run["peak_mem_gb"]},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": {k: {"avg_us": v["avg_us"], "launches_per_step": v["launches_per_step"], "GBps": v["GBps"],

@@ -13,8 +13,8 @@ Contents (each function cites the reference file:line it restates):
                  order, so torch.manual_seed(s) gives the same random-init weights
                  (face/model.py:28-77,90-339,421-534,558-590,665-695)
   neighbors.py   brute-force periodic pair list in fp64 with ASE neighbor_list semantics
-                 (ase 3.29.0, called at face/neighbors.py:12), C core in neighbors.c
-  graphs.py      padded-dense graph layout of face/neighbors.py:7-37 built from a pair list
+                 (ase 3.29.0, called at face/neighbors.py:12), C core in neighbors.c, and the
+                 padded-dense graph layout of face/neighbors.py:7-37 built from that pair list
 
 How each part is pinned is stated in the docstring of the function.
 """
