@@ -378,6 +378,138 @@ __global__ __launch_bounds__(kBlock) void cp_density_bwd_kernel(
     }
 }
 
+// ------------------------------------------------------------------ CP backward on MFMA
+// One wave per atom row, no workgroup barriers. The row is walked in tiles of 16 edges and,
+// inside a tile, in steps of 32 channels (two 16-channel MFMA blocks h); both contractions
+// run on v_mfma_f32_16x16x4f32:
+//   t_l[c, e] = sum_{x in l} gA[x, c] Y[e, x]         (M = channels, N = edges, K = monomials)
+//   P[x, e]   = sum_c gA[x, c] R[e, l(x), c] msg[e, c] (M = monomials, N = edges, K = channels)
+// Operand layouts of the 16x16x4 f32 instruction: A[i][k] in lane i + 16k, B[k][j] in lane
+// j + 16k, D[4q + r][j] in register r of lane j + 16q. Lane (j, q) therefore holds t for edge
+// j and channels 16h + 4q + r, which is where it loads R / msg as float4 and writes dR / dmsg
+// (each wave-wide access covers 64 contiguous bytes per edge), and register r of R*msg is the
+// B operand of the P chain with K index = channel 16h + 4q + r.
+// P rows: accumulator lo holds x = 0..3 (rank 0 in row 0, rank 1 in rows 1-3), hi holds
+// x = 4..19 (rank 2 in rows 0-5, rank 3 in rows 6-15); each chain alternates the two ranks it
+// serves, with the A operand zeroed outside the rank's rows. The atom's gA (20 x C) is staged
+// in the wave's own LDS slice.
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4f mfma_16x16x4(float a, float b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ v4f ld4(const float* p) { return *reinterpret_cast<const v4f*>(p); }
+__device__ __forceinline__ void st4(float* p, v4f v) { *reinterpret_cast<v4f*>(p) = v; }
+
+// Monomial chunks of the t contraction (K = 4 per instruction): chunk k covers
+// x = kChunkX0[k] + q for q < kChunkLen[k], rank kChunkRank[k]; rank l owns chunks
+// [kRankChunk0[l], kRankChunk1[l]).
+__device__ constexpr int kChunkX0[7] = {0, 1, 4, 8, 10, 14, 18};
+__device__ constexpr int kChunkLen[7] = {1, 3, 4, 2, 4, 4, 2};
+__device__ constexpr int kRankChunk0[4] = {0, 1, 2, 4};
+__device__ constexpr int kRankChunk1[4] = {1, 2, 4, 7};
+
+constexpr int kCpStep = 32;                           // channels per step (C % kCpStep == 0)
+constexpr int kCpRowsPerBlock = 2;                    // waves (= atom rows) per workgroup
+// LDS row stride of the staged gA (floats).
+__host__ __device__ constexpr int cp_mfma_stride(int C) { return C + 4; }
+
+__global__ __launch_bounds__(kCpRowsPerBlock * kWave) void cp_density_bwd_mfma_kernel(
+    const float* __restrict__ R, int ld_R, const float* __restrict__ env, const float* __restrict__ msg, int ld_msg,
+    const int32_t* __restrict__ msg_row, const float* __restrict__ Y, int ld_Y, const int32_t* __restrict__ row_ptr,
+    int64_t N, int M, int C, RankIn gA, float* __restrict__ dR, int ld_dR, float* __restrict__ dmsg, int ld_dmsg,
+    float* __restrict__ dY, int ld_dY, float* __restrict__ denv) {
+    extern __shared__ float lds[];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int w = threadIdx.x / kWave;
+    const int64_t i = (int64_t)blockIdx.x * kCpRowsPerBlock + w;
+    if (i >= N) return;                               // uniform per wave
+    const int GS = cp_mfma_stride(C);
+    float* sg = lds + (size_t)w * 20 * GS;
+    const int j = lane & 15, q = lane >> 4;
+    const int nc4 = C >> 2;
+    for (int v = lane; v < 20 * nc4; v += kWave) {
+        const int x = v / nc4, c4 = v - x * nc4;
+        *reinterpret_cast<v4f*>(sg + x * GS + 4 * c4) = ld4(gA.at(i, x) + 4 * c4);
+    }
+    __builtin_amdgcn_wave_barrier();
+    const int t_off = q * GS + j;                     // + kChunkX0[k] * GS + channel block start
+    const int own = 4 * q;                            // + channel block start
+    const int plo_off = (j < 4 ? j : 0) * GS + own, phi_off = (4 + j) * GS + own;
+    const float sel0 = j == 0 ? 1.f : 0.f, sel1 = (j >= 1 && j < 4) ? 1.f : 0.f;
+    const float sel2 = j < 6 ? 1.f : 0.f, sel3 = j >= 6 ? 1.f : 0.f;
+    const v4f z4 = {0.f, 0.f, 0.f, 0.f};
+    int64_t e0, e1;
+    row_range(row_ptr, i, M, e0, e1);
+    for (int64_t t0 = e0; t0 < e1; t0 += 16) {
+        const int64_t e = t0 + j;
+        const bool ok = e < e1;
+        float yq[7];
+#pragma unroll
+        for (int k = 0; k < 7; ++k) yq[k] = (ok && q < kChunkLen[k]) ? Y[e * ld_Y + kChunkX0[k] + q] : 0.f;
+        const float ev = ok ? (env ? env[e] : 1.f) : 0.f;
+        const int64_t mrow = ok ? (msg_row ? (int64_t)msg_row[e] : e) : 0;
+        const float* Re = R + e * ld_R + own;
+        const float* me = msg + mrow * ld_msg + own;
+        v4f plo = z4, phi = z4;
+#pragma unroll 1
+        for (int cs = 0; cs < C; cs += kCpStep) {
+            v4f r[2][4], m[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                for (int l = 0; l < 4; ++l) r[h][l] = ok ? ld4(Re + l * C + cs + 16 * h) : z4;
+                m[h] = ok ? ld4(me + cs + 16 * h) : z4;
+            }
+            v4f dm[2] = {z4, z4};
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    v4f t = z4;
+#pragma unroll
+                    for (int k = kRankChunk0[l]; k < kRankChunk1[l]; ++k) {
+                        const float a = q < kChunkLen[k] ? sg[t_off + kChunkX0[k] * GS + cs + 16 * h] : 0.f;
+                        t = mfma_16x16x4(a, yq[k], t);
+                    }
+                    if (ok && dR) st4(dR + e * ld_dR + l * C + cs + own + 16 * h, (ev * m[h]) * t);
+                    dm[h] += r[h][l] * t;
+                }
+            }
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                if (ok && dmsg) st4(dmsg + e * ld_dmsg + cs + own + 16 * h, ev * dm[h]);
+                const v4f alo = *reinterpret_cast<const v4f*>(sg + plo_off + cs + 16 * h);
+                const v4f ahi = *reinterpret_cast<const v4f*>(sg + phi_off + cs + 16 * h);
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) {
+                    const float mm = m[h][rr];
+                    plo = mfma_16x16x4(sel0 * alo[rr], r[h][0][rr] * mm, plo);
+                    phi = mfma_16x16x4(sel2 * ahi[rr], r[h][2][rr] * mm, phi);
+                    plo = mfma_16x16x4(sel1 * alo[rr], r[h][1][rr] * mm, plo);
+                    phi = mfma_16x16x4(sel3 * ahi[rr], r[h][3][rr] * mm, phi);
+                }
+            }
+        }
+        // lane (j, q) holds P[x, e] for x = 4 + 4q + r (hi) and, in lanes q == 0, x = r (lo)
+        float s = 0.f;
+        if (ok) {
+            const v4f yhi = ld4(Y + e * ld_Y + 4 + 4 * q);
+            s = yhi[0] * phi[0] + yhi[1] * phi[1] + yhi[2] * phi[2] + yhi[3] * phi[3];
+            if (dY) st4(dY + e * ld_dY + 4 + 4 * q, ev * phi);
+            if (q == 0) {
+                const v4f ylo = ld4(Y + e * ld_Y);
+                s += ylo[0] * plo[0] + ylo[1] * plo[1] + ylo[2] * plo[2] + ylo[3] * plo[3];
+                if (dY) st4(dY + e * ld_dY, ev * plo);
+            }
+        }
+        s += __shfl_xor(s, 16, kWave);
+        s += __shfl_xor(s, 32, kWave);
+        if (denv && ok && q == 0) denv[e] = s;
+    }
+}
+
 // ------------------------------------------------------------------ launch helpers
 static int max_lds_bytes() {
     static int v = -1;
@@ -565,6 +697,22 @@ extern "C" int face_density_bwd(const float* phi, int32_t ld_phi, const float* m
                             dphi, ld_dphi, dmsg, ld_dmsg, dY, ld_dY);
 }
 
+// The MFMA backward reads and writes float4s: whole channel steps, 16-byte aligned rows and
+// rank blocks.
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+static bool mfma_layout_ok(const float* R, int ld_R, const float* msg, int ld_msg, const float* Y, int ld_Y, int C,
+                           const RankIn& gA, const float* dR, int ld_dR, const float* dmsg, int ld_dmsg,
+                           const float* dY, int ld_dY) {
+    if (C % kCpStep || ld_R % 4 || ld_msg % 4 || ld_Y % 4 || gA.sa % 4 || gA.sx % 4) return false;
+    if (!aligned16(R) || !aligned16(msg) || !aligned16(Y)) return false;
+    for (int l = 0; l < 4; ++l)
+        if (!aligned16(gA.p[l])) return false;
+    if (dR && (ld_dR % 4 || !aligned16(dR))) return false;
+    if (dmsg && (ld_dmsg % 4 || !aligned16(dmsg))) return false;
+    if (dY && (ld_dY % 4 || !aligned16(dY))) return false;
+    return true;
+}
+
 extern "C" int face_cp_density_fwd(const float* R, int32_t ld_R, const float* env, const float* msg, int32_t ld_msg,
                                    const int32_t* msg_row, const float* Y, int32_t ld_Y, const int32_t* row_ptr,
                                    int64_t N, int32_t M, int32_t C, float* const* A_ranks, int64_t atom_stride,
@@ -587,12 +735,23 @@ extern "C" int face_cp_density_bwd(const float* R, int32_t ld_R, const float* en
                                    int64_t N, int32_t M, int32_t max_row, int32_t C, const float* const* gA_ranks,
                                    int64_t atom_stride, int64_t x_stride, float* dR, int32_t ld_dR, float* dmsg,
                                    int32_t ld_dmsg, float* dY, int32_t ld_dY, float* denv, void* stream) {
-    if (N < 0 || C <= 0 || C > kBlock || ld_R < 4 * C || ld_msg < C || ld_Y < 20 || (!row_ptr && M < 0))
-        return FACE_ERR_ARG;
+    if (N < 0 || C <= 0 || ld_R < 4 * C || ld_msg < C || ld_Y < 20 || (!row_ptr && M < 0)) return FACE_ERR_ARG;
     if ((dR && ld_dR < 4 * C) || (dmsg && ld_dmsg < C) || (dY && ld_dY < 20)) return FACE_ERR_ARG;
     if (N == 0 || max_row == 0) return 0;
     RankIn gA;
     if (!R || !msg || !Y || !rank_in(gA_ranks, atom_stride, x_stride, 20, gA)) return FACE_ERR_ARG;
+    if (mfma_layout_ok(R, ld_R, msg, ld_msg, Y, ld_Y, C, gA, dR, ld_dR, dmsg, ld_dmsg, dY, ld_dY)) {
+        // one atom row per wave, kCpRowsPerBlock rows per workgroup, each with its gA slice in LDS
+        const size_t lds = (size_t)kCpRowsPerBlock * 20 * cp_mfma_stride(C) * sizeof(float);
+        if (lds > 65536) return FACE_ERR_UNSUPPORTED;
+        hipLaunchKernelGGL(cp_density_bwd_mfma_kernel, dim3((unsigned)((N + kCpRowsPerBlock - 1) / kCpRowsPerBlock)),
+                           dim3(kCpRowsPerBlock * kWave), lds,
+                           (hipStream_t)stream, R, ld_R, env, msg, ld_msg, msg_row, Y, ld_Y, row_ptr, N, M, C, gA, dR,
+                           ld_dR, dmsg, ld_dmsg, dY, ld_dY, denv);
+        FACE_LAUNCH_CHECK();
+        return 0;
+    }
+    if (C > kBlock) return FACE_ERR_UNSUPPORTED;
     const int nthr = ((C + kWave - 1) / kWave) * kWave;
     const int CS = ((C + 3) & ~3) + 4;
     const size_t lds = ((size_t)(20 + kTileCPB * 4) * CS + kTileCPB * 41) * sizeof(float);

@@ -85,7 +85,8 @@ int face_cp_density_fwd(const float* R, int32_t ld_R, const float* env, const fl
                         void* stream);
 
 /* Backward for gA = dL/dA (rank blocks): dR (E, ld_dR), dmsg (E, ld_dmsg) per edge, dY (E, ld_dY),
- * denv (E). Any output may be NULL. C <= 256. */
+ * denv (E). Any output may be NULL. Served on the matrix cores when C is a multiple of 32
+ * (C <= 800) and every row / rank block is 16-byte aligned; otherwise C <= 256. */
 int face_cp_density_bwd(const float* R, int32_t ld_R, const float* env, const float* msg, int32_t ld_msg,
                         const int32_t* msg_row, const float* Y, int32_t ld_Y, const int32_t* row_ptr, int64_t N,
                         int32_t M, int32_t max_row, int32_t C, const float* const* gA_ranks, int64_t atom_stride,
