@@ -29,7 +29,8 @@ import torch  # noqa: E402
 METRIC = "atom-steps/s (E+F, fp32) at 864 & 24k atoms; density-kernel HBM GB/s"
 HBM_PEAK_GBS = 8000.0
 TIMED = ["density_fwd20", "density_bwd20", "cp_fwd", "cp_bwd", "transport_fwd", "transport_bwd", "dir_fwd",
-         "dir_bwd", "node_fwd", "node_bwd", "edge_fwd", "edge_bwd", "force_scatter", "gather_bwd"]
+         "dir_bwd", "node_fwd", "node_bwd", "edge_fwd", "edge_bwd", "force_scatter", "gather_bwd", "radial_fwd",
+         "radial_bwd"]
 
 
 def log(*a):
@@ -65,6 +66,11 @@ def algorithmic_bytes(label, g, kw):
         return 4 * E * (11 + 29 + 3)
     if label == "force_scatter":
         return 4 * (3 * E + E + 3 * N)
+    H, nb = kw.get("radial_hidden", 64), kw.get("n_basis", 8)
+    if label == "radial_fwd":           # rb, pair, env in; phi (and h2 in CP mode) out
+        return 4 * E * (nb + 2 + B + (H if kw.get("cp") else 0))
+    if label == "radial_bwd":           # + upstream phi (and h2) gradients; d rb, d env out
+        return 4 * E * (nb + 2 + B + (H if kw.get("cp") else 0) + nb + 1)
     return None
 
 

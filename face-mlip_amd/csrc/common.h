@@ -37,4 +37,15 @@ __device__ __forceinline__ float group_sum(float v, int width) {
     return v;
 }
 
+// fp32 matrix-core helpers. v_mfma_f32_16x16x4f32 operand layouts (wave64): A[i][k] in lane
+// i + 16k, B[k][j] in lane j + 16k, D[4q + r][j] in register r of lane j + 16q.
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4f mfma_16x16x4(float a, float b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ v4f ld4(const float* p) { return *reinterpret_cast<const v4f*>(p); }
+__device__ __forceinline__ void st4(float* p, v4f v) { *reinterpret_cast<v4f*>(p) = v; }
+
 }  // namespace face

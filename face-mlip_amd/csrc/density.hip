@@ -393,15 +393,6 @@ __global__ __launch_bounds__(kBlock) void cp_density_bwd_kernel(
 // x = 4..19 (rank 2 in rows 0-5, rank 3 in rows 6-15); each chain alternates the two ranks it
 // serves, with the A operand zeroed outside the rank's rows. The atom's gA (20 x C) is staged
 // in the wave's own LDS slice.
-typedef float v4f __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ v4f mfma_16x16x4(float a, float b, v4f c) {
-    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
-
-__device__ __forceinline__ v4f ld4(const float* p) { return *reinterpret_cast<const v4f*>(p); }
-__device__ __forceinline__ void st4(float* p, v4f v) { *reinterpret_cast<v4f*>(p) = v; }
-
 // Monomial chunks of the t contraction (K = 4 per instruction): chunk k covers
 // x = kChunkX0[k] + q for q < kChunkLen[k], rank kChunkRank[k]; rank l owns chunks
 // [kRankChunk0[l], kRankChunk1[l]).

@@ -1,0 +1,341 @@
+// Radial MLP of a factorised pass on the fp32 matrix cores (face/model.py:465-469):
+//   u1  = rb W_in^T + b_in + pair_tab[pair]     hid = silu(u1)        (E, H)
+//   u2  = hid W1^T + b1                         h2  = silu(u2)        (E, H)
+//   phi = (h2 W_phi^T + b_phi) * env                                  (E, B)
+// rb already carries the envelope (face/model.py:676). The last layer's 4C CP columns are a
+// plain GEMM on h2 outside this kernel.
+//
+// Work: one wave per tile of 16 edges, all layers in the transposed orientation (features x
+// edges): each layer is D = W . X^T with M = output features, N = edges, K = input features,
+// so the D layout of one v_mfma_f32_16x16x4f32 chain (feature 4q + r, edge j in register r of
+// lane j + 16q) is directly the B operand of the next chain, whose K index q of instruction r
+// is input feature 4q + r of the block. Weights, biases and the pair table sit in LDS.
+#include "common.h"
+
+namespace face {
+
+constexpr int kRadWaves = 4;                           // waves per workgroup
+
+struct RadialWeights {
+    const float *w_in, *b_in, *pair_tab, *w1, *b1, *w_phi, *b_phi;
+};
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
+__device__ __forceinline__ v4f silu4(v4f u) {
+    v4f o;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o[r] = u[r] * sigmoidf_(u[r]);
+    return o;
+}
+// d silu(u) / du = s (1 + u (1 - s)), s = sigmoid(u)
+__device__ __forceinline__ v4f dsilu4(v4f u) {
+    v4f o;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float s = sigmoidf_(u[r]);
+        o[r] = s * (1.f + u[r] * (1.f - s));
+    }
+    return o;
+}
+
+// LDS image of the weights (floats): w_in [H][SI] (zero beyond n_basis), b_in [H],
+// pair_tab [n_pair][H], w1 [H][S1], b1 [H], w_phi [16 BB][S1] (zero rows >= B), b_phi [16 BB].
+struct RadialLds {
+    int SI, S1, o_bin, o_pt, o_w1, o_b1, o_wp, o_bp, total;
+    __host__ __device__ RadialLds(int H, int BB, int n_pair) {
+        SI = 16;
+        S1 = H + 4;
+        o_bin = H * SI;
+        o_pt = o_bin + H;
+        o_w1 = o_pt + n_pair * H;
+        o_b1 = o_w1 + H * S1;
+        o_wp = o_b1 + H;
+        o_bp = o_wp + 16 * BB * S1;
+        total = o_bp + 16 * BB;
+    }
+};
+
+__device__ void radial_stage(float* lds, const RadialLds& L, const RadialWeights& W, int H, int BB, int nbasis,
+                             int n_pair, int B) {
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    for (int v = tid; v < H * L.SI; v += nthr) {
+        const int h = v / L.SI, k = v - h * L.SI;
+        lds[v] = k < nbasis ? W.w_in[h * nbasis + k] : 0.f;
+    }
+    for (int v = tid; v < H; v += nthr) {
+        lds[L.o_bin + v] = W.b_in[v];
+        lds[L.o_b1 + v] = W.b1[v];
+    }
+    for (int v = tid; v < n_pair * H; v += nthr) lds[L.o_pt + v] = W.pair_tab[v];
+    for (int v = tid; v < H * L.S1; v += nthr) {
+        const int h = v / L.S1, k = v - h * L.S1;
+        lds[L.o_w1 + v] = k < H ? W.w1[h * H + k] : 0.f;
+    }
+    for (int v = tid; v < 16 * BB * L.S1; v += nthr) {
+        const int b = v / L.S1, k = v - b * L.S1;
+        lds[L.o_wp + v] = (b < B && k < H) ? W.w_phi[b * H + k] : 0.f;
+    }
+    for (int v = tid; v < 16 * BB; v += nthr) lds[L.o_bp + v] = v < B ? W.b_phi[v] : 0.f;
+}
+
+__device__ __forceinline__ v4f lds4(const float* p) { return *reinterpret_cast<const v4f*>(p); }
+
+// Forward chain of one tile: pre-activations u1, u2 (D layout) and phi before the envelope.
+template <int HB, int BB>
+__device__ __forceinline__ void radial_chain(const float* lds, const RadialLds& L, const float* xb, int nkb, int p,
+                                             int j, int q, v4f (&u1)[HB], v4f (&u2)[HB], v4f (&hh)[HB],
+                                             v4f (&pl)[BB]) {
+    constexpr int H = 16 * HB;
+    const v4f z4 = {0.f, 0.f, 0.f, 0.f};
+    v4f hid[HB];
+#pragma unroll
+    for (int hb = 0; hb < HB; ++hb) {
+        v4f acc = z4;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+            if (kb < nkb) acc = mfma_16x16x4(lds[(16 * hb + j) * L.SI + 4 * kb + q], xb[kb], acc);
+        u1[hb] = acc + lds4(lds + L.o_bin + 16 * hb + 4 * q) + lds4(lds + L.o_pt + p * H + 16 * hb + 4 * q);
+        hid[hb] = silu4(u1[hb]);
+    }
+#pragma unroll
+    for (int h2b = 0; h2b < HB; ++h2b) {
+        v4f acc = z4;
+#pragma unroll
+        for (int hb = 0; hb < HB; ++hb) {
+            const v4f a = lds4(lds + L.o_w1 + (16 * h2b + j) * L.S1 + 16 * hb + 4 * q);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc = mfma_16x16x4(a[r], hid[hb][r], acc);
+        }
+        u2[h2b] = acc + lds4(lds + L.o_b1 + 16 * h2b + 4 * q);
+        hh[h2b] = silu4(u2[h2b]);
+    }
+#pragma unroll
+    for (int bb = 0; bb < BB; ++bb) {
+        v4f acc = z4;
+#pragma unroll
+        for (int hb = 0; hb < HB; ++hb) {
+            const v4f a = lds4(lds + L.o_wp + (16 * bb + j) * L.S1 + 16 * hb + 4 * q);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc = mfma_16x16x4(a[r], hh[hb][r], acc);
+        }
+        pl[bb] = acc + lds4(lds + L.o_bp + 16 * bb + 4 * q);
+    }
+}
+
+// Row e, columns c0 .. c0+3 (those < n) of a row-major (*, ld) array.
+__device__ __forceinline__ void store_cols(float* row, int c0, int n, v4f v) {
+    if (c0 + 3 < n && ((reinterpret_cast<uintptr_t>(row + c0) & 15) == 0)) {
+        st4(row + c0, v);
+    } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (c0 + r < n) row[c0 + r] = v[r];
+    }
+}
+__device__ __forceinline__ v4f load_cols(const float* row, int c0, int n) {
+    if (c0 + 3 < n && ((reinterpret_cast<uintptr_t>(row + c0) & 15) == 0)) return ld4(row + c0);
+    v4f v = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        if (c0 + r < n) v[r] = row[c0 + r];
+    return v;
+}
+
+template <int HB, int BB>
+__global__ __launch_bounds__(kRadWaves * kWave) void radial_fwd_kernel(
+    const float* __restrict__ rb, int ld_rb, int nbasis, const int32_t* __restrict__ pair,
+    const float* __restrict__ env, int64_t E, RadialWeights W, int n_pair, int B, float* __restrict__ h2, int ld_h2,
+    float* __restrict__ phi, int ld_phi, int tiles_per_wave) {
+    extern __shared__ float lds[];
+    constexpr int H = 16 * HB;
+    const RadialLds L(H, BB, n_pair);
+    radial_stage(lds, L, W, H, BB, nbasis, n_pair, B);
+    __syncthreads();
+    const int lane = threadIdx.x & (kWave - 1);
+    const int j = lane & 15, q = lane >> 4;
+    const int nkb = (nbasis + 3) >> 2;
+    const int64_t wave = (int64_t)blockIdx.x * kRadWaves + threadIdx.x / kWave;
+    for (int s = 0; s < tiles_per_wave; ++s) {
+        const int64_t t0 = (wave * tiles_per_wave + s) * 16;
+        if (t0 >= E) break;                            // uniform per wave
+        const int64_t e = t0 + j;
+        const bool ok = e < E;
+        float xb[4];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) xb[kb] = (ok && 4 * kb + q < nbasis) ? rb[e * ld_rb + 4 * kb + q] : 0.f;
+        int p = ok ? pair[e] : 0;
+        p = p < 0 ? 0 : (p >= n_pair ? n_pair - 1 : p);
+        v4f u1[HB], u2[HB], hh[HB], pl[BB];
+        radial_chain<HB, BB>(lds, L, xb, nkb, p, j, q, u1, u2, hh, pl);
+        if (ok) {
+            if (h2) {
+#pragma unroll
+                for (int hb = 0; hb < HB; ++hb) st4(h2 + e * ld_h2 + 16 * hb + 4 * q, hh[hb]);
+            }
+            const float ev = env ? env[e] : 1.f;
+#pragma unroll
+            for (int bb = 0; bb < BB; ++bb) store_cols(phi + e * ld_phi, 16 * bb + 4 * q, B, pl[bb] * ev);
+        }
+    }
+}
+
+template <int HB, int BB>
+__global__ __launch_bounds__(kRadWaves * kWave) void radial_bwd_kernel(
+    const float* __restrict__ rb, int ld_rb, int nbasis, const int32_t* __restrict__ pair,
+    const float* __restrict__ env, int64_t E, RadialWeights W, int n_pair, int B, const float* __restrict__ gh2,
+    int ld_gh2, const float* __restrict__ gphi, int ld_gphi, float* __restrict__ grb, int ld_grb,
+    float* __restrict__ genv, int tiles_per_wave) {
+    extern __shared__ float lds[];
+    constexpr int H = 16 * HB;
+    const RadialLds L(H, BB, n_pair);
+    radial_stage(lds, L, W, H, BB, nbasis, n_pair, B);
+    __syncthreads();
+    const int lane = threadIdx.x & (kWave - 1);
+    const int j = lane & 15, q = lane >> 4;
+    const int nkb = (nbasis + 3) >> 2;
+    const int64_t wave = (int64_t)blockIdx.x * kRadWaves + threadIdx.x / kWave;
+    const v4f z4 = {0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < tiles_per_wave; ++s) {
+        const int64_t t0 = (wave * tiles_per_wave + s) * 16;
+        if (t0 >= E) break;                            // uniform per wave
+        const int64_t e = t0 + j;
+        const bool ok = e < E;
+        float xb[4];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) xb[kb] = (ok && 4 * kb + q < nbasis) ? rb[e * ld_rb + 4 * kb + q] : 0.f;
+        int p = ok ? pair[e] : 0;
+        p = p < 0 ? 0 : (p >= n_pair ? n_pair - 1 : p);
+        v4f u1[HB], u2[HB], hh[HB], pl[BB];
+        radial_chain<HB, BB>(lds, L, xb, nkb, p, j, q, u1, u2, hh, pl);
+        const float ev = ok ? (env ? env[e] : 1.f) : 0.f;
+        // phi = pl * env: d env = sum_b gphi pl; d pl = gphi * env
+        v4f gp[BB];
+        float sden = 0.f;
+#pragma unroll
+        for (int bb = 0; bb < BB; ++bb) {
+            gp[bb] = ok ? load_cols(gphi + e * ld_gphi, 16 * bb + 4 * q, B) : z4;
+            sden += gp[bb][0] * pl[bb][0] + gp[bb][1] * pl[bb][1] + gp[bb][2] * pl[bb][2] + gp[bb][3] * pl[bb][3];
+            gp[bb] = gp[bb] * ev;
+        }
+        sden += __shfl_xor(sden, 16, kWave);
+        sden += __shfl_xor(sden, 32, kWave);
+        if (ok && genv && q == 0) genv[e] = sden;
+        // d h2 = gh2 + W_phi^T d pl;  d u2 = d h2 * silu'(u2)
+        v4f du2[HB];
+#pragma unroll
+        for (int hb = 0; hb < HB; ++hb) {
+            v4f acc = (ok && gh2) ? ld4(gh2 + e * ld_gh2 + 16 * hb + 4 * q) : z4;
+#pragma unroll
+            for (int bb = 0; bb < BB; ++bb) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc = mfma_16x16x4(lds[L.o_wp + (16 * bb + 4 * q + r) * L.S1 + 16 * hb + j], gp[bb][r], acc);
+            }
+            du2[hb] = acc * dsilu4(u2[hb]);
+        }
+        // d hid = W1^T d u2;  d u1 = d hid * silu'(u1)
+        v4f du1[HB];
+#pragma unroll
+        for (int hb = 0; hb < HB; ++hb) {
+            v4f acc = z4;
+#pragma unroll
+            for (int h2b = 0; h2b < HB; ++h2b) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc = mfma_16x16x4(lds[L.o_w1 + (16 * h2b + 4 * q + r) * L.S1 + 16 * hb + j], du2[h2b][r], acc);
+            }
+            du1[hb] = acc * dsilu4(u1[hb]);
+        }
+        // d rb = W_in^T d u1 (M = basis functions, one block of 16)
+        v4f acc = z4;
+#pragma unroll
+        for (int hb = 0; hb < HB; ++hb) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc = mfma_16x16x4(lds[(16 * hb + 4 * q + r) * L.SI + j], du1[hb][r], acc);
+        }
+        if (ok && grb) store_cols(grb + e * ld_grb, 4 * q, nbasis, acc);
+    }
+}
+
+static size_t radial_lds_bytes(int H, int B, int n_pair) {
+    return (size_t)RadialLds(H, (B + 15) / 16, n_pair).total * sizeof(float);
+}
+
+static int radial_tiles_per_wave(int64_t E) {
+    const int64_t tiles = (E + 15) / 16;
+    int64_t t = tiles / (256 * kRadWaves * 2);
+    return (int)(t < 1 ? 1 : (t > 8 ? 8 : t));
+}
+
+static bool radial_args_ok(const float* rb, int ld_rb, int nbasis, const int32_t* pair, int64_t E,
+                           const RadialWeights& W, int n_pair, int H, int B) {
+    if (E < 0 || nbasis < 1 || nbasis > 16 || ld_rb < nbasis || n_pair < 1 || H < 16 || H > 64 || H % 16 ||
+        B < 1 || B > 64)
+        return false;
+    if (E > 0 && (!rb || !pair)) return false;
+    return W.w_in && W.b_in && W.pair_tab && W.w1 && W.b1 && W.w_phi && W.b_phi;
+}
+
+}  // namespace face
+
+using namespace face;
+
+#define FACE_RADIAL_DISPATCH(KERNEL, ...)                                                               \
+    do {                                                                                                \
+        const int hb_ = H / 16, bb_ = (B + 15) / 16;                                                    \
+        const int64_t waves_ = ((E + 15) / 16 + tpw - 1) / tpw;                                         \
+        const dim3 grid_((unsigned)((waves_ + kRadWaves - 1) / kRadWaves)), block_(kRadWaves * kWave);   \
+        const hipStream_t st_ = (hipStream_t)stream;                                                    \
+        switch (hb_ * 10 + bb_) {                                                                       \
+            case 11: hipLaunchKernelGGL((KERNEL<1, 1>), grid_, block_, lds, st_, __VA_ARGS__); break;   \
+            case 12: hipLaunchKernelGGL((KERNEL<1, 2>), grid_, block_, lds, st_, __VA_ARGS__); break;   \
+            case 21: hipLaunchKernelGGL((KERNEL<2, 1>), grid_, block_, lds, st_, __VA_ARGS__); break;   \
+            case 22: hipLaunchKernelGGL((KERNEL<2, 2>), grid_, block_, lds, st_, __VA_ARGS__); break;   \
+            case 31: hipLaunchKernelGGL((KERNEL<3, 1>), grid_, block_, lds, st_, __VA_ARGS__); break;   \
+            case 32: hipLaunchKernelGGL((KERNEL<3, 2>), grid_, block_, lds, st_, __VA_ARGS__); break;   \
+            case 41: hipLaunchKernelGGL((KERNEL<4, 1>), grid_, block_, lds, st_, __VA_ARGS__); break;   \
+            case 42: hipLaunchKernelGGL((KERNEL<4, 2>), grid_, block_, lds, st_, __VA_ARGS__); break;   \
+            case 43: hipLaunchKernelGGL((KERNEL<4, 3>), grid_, block_, lds, st_, __VA_ARGS__); break;   \
+            case 44: hipLaunchKernelGGL((KERNEL<4, 4>), grid_, block_, lds, st_, __VA_ARGS__); break;   \
+            default: return FACE_ERR_UNSUPPORTED;                                                       \
+        }                                                                                               \
+    } while (0)
+
+extern "C" int face_radial_fwd(const float* rb, int32_t ld_rb, int32_t n_basis, const int32_t* pair,
+                               const float* env, int64_t E, const float* w_in, const float* b_in,
+                               const float* pair_tab, int32_t n_pair, int32_t H, const float* w1, const float* b1,
+                               const float* w_phi, const float* b_phi, int32_t B, float* h2, int32_t ld_h2,
+                               float* phi, int32_t ld_phi, void* stream) {
+    const RadialWeights W{w_in, b_in, pair_tab, w1, b1, w_phi, b_phi};
+    if (!radial_args_ok(rb, ld_rb, n_basis, pair, E, W, n_pair, H, B) || ld_phi < B || (E > 0 && !phi) ||
+        (h2 && (ld_h2 < H || ld_h2 % 4 || ((uintptr_t)h2 & 15))))
+        return FACE_ERR_ARG;
+    if (E == 0) return 0;
+    const size_t lds = radial_lds_bytes(H, B, n_pair);
+    if (lds > 65536) return FACE_ERR_UNSUPPORTED;
+    const int tpw = radial_tiles_per_wave(E);
+    FACE_RADIAL_DISPATCH(radial_fwd_kernel, rb, ld_rb, n_basis, pair, env, E, W, n_pair, B, h2, ld_h2, phi, ld_phi,
+                         tpw);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int face_radial_bwd(const float* rb, int32_t ld_rb, int32_t n_basis, const int32_t* pair,
+                               const float* env, int64_t E, const float* w_in, const float* b_in,
+                               const float* pair_tab, int32_t n_pair, int32_t H, const float* w1, const float* b1,
+                               const float* w_phi, const float* b_phi, int32_t B, const float* gh2, int32_t ld_gh2,
+                               const float* gphi, int32_t ld_gphi, float* grb, int32_t ld_grb, float* genv,
+                               void* stream) {
+    const RadialWeights W{w_in, b_in, pair_tab, w1, b1, w_phi, b_phi};
+    if (!radial_args_ok(rb, ld_rb, n_basis, pair, E, W, n_pair, H, B) || (E > 0 && !gphi) || ld_gphi < B ||
+        (gh2 && (ld_gh2 < H || ld_gh2 % 4 || ((uintptr_t)gh2 & 15))) || (grb && ld_grb < n_basis))
+        return FACE_ERR_ARG;
+    if (E == 0) return 0;
+    const size_t lds = radial_lds_bytes(H, B, n_pair);
+    if (lds > 65536) return FACE_ERR_UNSUPPORTED;
+    const int tpw = radial_tiles_per_wave(E);
+    FACE_RADIAL_DISPATCH(radial_bwd_kernel, rb, ld_rb, n_basis, pair, env, E, W, n_pair, B, gh2, ld_gh2, gphi,
+                         ld_gphi, grb, ld_grb, genv, tpw);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}

@@ -20,8 +20,9 @@ runs:
   * only the projection columns the algebra uses are computed (P0 of rank 0; P3, Q3 of rank 3).
 
 Supported configuration: factor=True (cp on or off), transport/eqmsg on or off, n_passes >= 1,
-norm="layer", terms=(), training toggles at their defaults; first-order forces
-(create_graph=False), which is what the reference's fused kernels support (face/kernels.py:10-11).
+norm="layer", terms=(), radial_hidden in {16, 32, 48, 64}, training toggles at their defaults;
+evaluation mode and first-order forces (create_graph=False), which is what the reference's fused
+kernels support (face/kernels.py:10-11).
 """
 import math
 
@@ -163,11 +164,13 @@ class FactorBlock(nn.Module):
         """Moments A_l as monomial-major (k_l, N, C) blocks (face/model.py:460-534)."""
         N, E = g.N, g.E
         B, C, Kd = self.B, self.C, self.K
-        hid = F.silu(self.rad_in(rb) + self.pair.weight[zp])
-        h2 = F.silu(self.radial[0](hid))
+        # hidden layers and phi columns of the radial MLP in one HIP kernel; the CP columns of the
+        # last layer are a GEMM on its h2 output
+        Wi, bi = weight(self.rad_in)
+        W1, b1 = weight(self.radial[0])
         W2, b2 = weight(self.radial[2])
-        # the last radial layer split into its phi (B) and CP (4C) column blocks: no slice copies
-        phi = F.linear(h2, W2[:B], b2[:B]) * env[:, None]                        # (E, B)
+        phi, h2 = ops.radial_mlp(rb, env, zp, Wi.detach(), bi.detach(), self.pair.weight.detach(), W1.detach(),
+                                 b1.detach(), W2[:B].detach(), b2[:B].detach(), self.cp)          # (E, B), (E, H)
         msg_n = self.msg(h)                                                      # (N, K)
         if self.directional:
             if self.eq_in:
@@ -276,6 +279,9 @@ class FACE(nn.Module):
     def forward(self, g, forces=True, create_graph=False):
         if create_graph:
             raise NotImplementedError("first-order forces only (inference / MD)")
+        if self.training and torch.is_grad_enabled():
+            raise NotImplementedError("this path evaluates energies and forces of a trained model: call .eval() "
+                                      "(the fused radial kernel gives no weight gradients)")
         graph = self._graph(g)
         pos = graph.pos
         if forces and not pos.requires_grad:
@@ -285,7 +291,7 @@ class FACE(nn.Module):
         zkey = ("zp", len(self.E0))
         zp = graph.cache.get(zkey)
         if zp is None:
-            zp = zidx[graph.recv.long()] * len(self.E0) + zidx[graph.col.long()]
+            zp = (zidx[graph.recv.long()] * len(self.E0) + zidx[graph.col.long()]).to(torch.int32)
             graph.cache[zkey] = zp
         h = self.embed(zidx)
         e_at = self.E0[zidx].clone()

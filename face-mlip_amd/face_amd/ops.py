@@ -359,6 +359,50 @@ def cp_density(R, env, msg, Y, graph, gathered=False):
     return CPDensity.apply(R, env, msg, Y, graph, gathered)
 
 
+# ----------------------------------------------------------------------------- radial MLP
+class RadialMLP(torch.autograd.Function):
+    """phi (E, B) = (silu(silu(rb W_in^T + b_in + pair_tab[pair]) W1^T + b1) W_phi^T + b_phi) * env and,
+    when want_h2, the last hidden activation h2 (E, H) (face/model.py:465-469). Gradients flow to rb and
+    env only: the fused radial kernel serves forces, not training."""
+
+    @staticmethod
+    def forward(ctx, rb, env, pair, w_in, b_in, pair_tab, w1, b1, w_phi, b_phi, want_h2):
+        _lib.require_gpu(rb, env)
+        E, nb = rb.shape
+        H, B = w1.shape[0], w_phi.shape[0]
+        rb_, ld_rb = _rows(rb, nb)
+        env_ = env.contiguous().float()
+        ws = [t.detach().contiguous().float() for t in (w_in, b_in, pair_tab, w1, b1, w_phi, b_phi)]
+        h2 = torch.empty(E, H, device=rb.device) if want_h2 else torch.empty(0, H, device=rb.device)
+        phi = torch.empty(E, B, device=rb.device)
+        call("face_radial_fwd", ptr(rb_), ld_rb, nb, ptr(pair), ptr(env_), E, ptr(ws[0]), ptr(ws[1]), ptr(ws[2]),
+             ws[2].shape[0], H, ptr(ws[3]), ptr(ws[4]), ptr(ws[5]), ptr(ws[6]), B, ptr(h2) if want_h2 else None, H,
+             ptr(phi), B, _lib.stream_of(rb), label="radial_fwd")
+        ctx.save_for_backward(rb_, env_, pair, *ws)
+        ctx.dims = (E, nb, H, B)
+        return phi, h2
+
+    @staticmethod
+    def backward(ctx, gphi, gh2):
+        if any(ctx.needs_input_grad[2:]):
+            raise NotImplementedError("the fused radial MLP gives no weight gradients (forces only)")
+        rb, env, pair, *ws = ctx.saved_tensors
+        E, nb, H, B = ctx.dims
+        dev = rb.device
+        gphi = torch.zeros(E, B, device=dev) if gphi is None else gphi.contiguous().float()
+        gh2 = gh2.contiguous().float() if (gh2 is not None and gh2.numel()) else None
+        grb = torch.empty(E, nb, device=dev) if ctx.needs_input_grad[0] else None
+        genv = torch.empty(E, device=dev) if ctx.needs_input_grad[1] else None
+        call("face_radial_bwd", ptr(rb), rb.stride(0), nb, ptr(pair), ptr(env), E, ptr(ws[0]), ptr(ws[1]), ptr(ws[2]),
+             ws[2].shape[0], H, ptr(ws[3]), ptr(ws[4]), ptr(ws[5]), ptr(ws[6]), B, ptr(gh2), H, ptr(gphi), B,
+             ptr(grb), nb, ptr(genv), _lib.stream_of(rb), label="radial_bwd")
+        return grb, genv, None, None, None, None, None, None, None, None, None
+
+
+def radial_mlp(rb, env, pair, w_in, b_in, pair_tab, w1, b1, w_phi, b_phi, want_h2):
+    return RadialMLP.apply(rb, env, pair, w_in, b_in, pair_tab, w1, b1, w_phi, b_phi, want_h2)
+
+
 # ----------------------------------------------------------------------------- node algebra
 def _s3(t):
     """(atom, channel, component) element strides of a 3-d view."""

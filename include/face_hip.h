@@ -18,6 +18,7 @@
  *   face/node_kernel.py:164-209  NodeAlgebra / node_algebra       -> face_node_fwd / _bwd
  *   face/neighbors.py:7-37       padded_graph (ASE neighbor_list) -> face_nbr_* (count, fill, rev, padded)
  *   face/model.py:670-677        edge geometry + Bessel basis     -> face_edge_geom_fwd / _bwd
+ *   face/model.py:465-469        radial MLP (rad_in, pair, radial) -> face_radial_fwd / _bwd
  *   face/model.py:474-493        directional edge features        -> face_dir_feats_fwd / _bwd
  *   face/model.py:514-533        transport sums + transport map   -> face_transport_fwd / _bwd
  *   face/model.py:670,464,692-694 index_select gathers and their index_add backward
@@ -179,6 +180,30 @@ int face_edge_geom_bwd(const float* pos, const int32_t* recv, const int32_t* col
                        const uint8_t* mask, int64_t E, const float* freq, int32_t n_basis, float rc, float bes_scale,
                        const float* gY, const float* grb, const float* genv, const float* gr, float* gvec,
                        void* stream);
+
+/* ---------------------------------------------------------------- radial MLP
+ * Hidden layers and the phi columns of the radial MLP of a factorised pass
+ * (face/model.py:465-469, rb = bessel * envelope as at face/model.py:676):
+ *   u1 = rb W_in^T + b_in + pair_tab[pair[e]],  hid = silu(u1)          (E, H)
+ *   u2 = hid W1^T + b1,                         h2  = silu(u2)          (E, H)
+ *   phi = (h2 W_phi^T + b_phi) * env[e]                                 (E, B)
+ * rb (E, ld_rb >= n_basis), n_basis <= 16; pair (E) int32 element-pair row of pair_tab
+ * (n_pair, H); W_in (H, n_basis), W1 (H, H), W_phi (B, H) row-major effective weights
+ * (any 1/sqrt(fan_in) factor applied); H in {16, 32, 48, 64}, B <= 64. env may be NULL (= 1).
+ * h2 (E, ld_h2) is optional (NULL: not written; 16-byte aligned rows otherwise) -- the CP
+ * columns of the last radial layer are a GEMM on it.                                       */
+int face_radial_fwd(const float* rb, int32_t ld_rb, int32_t n_basis, const int32_t* pair, const float* env,
+                    int64_t E, const float* w_in, const float* b_in, const float* pair_tab, int32_t n_pair,
+                    int32_t H, const float* w1, const float* b1, const float* w_phi, const float* b_phi, int32_t B,
+                    float* h2, int32_t ld_h2, float* phi, int32_t ld_phi, void* stream);
+/* Backward for gh2 = dL/dh2 (may be NULL = 0; 16-byte aligned rows) and gphi = dL/dphi:
+ * grb (E, ld_grb) = dL/drb, genv (E) = dL/denv through phi (either may be NULL). The
+ * weights receive no gradient (forces only). */
+int face_radial_bwd(const float* rb, int32_t ld_rb, int32_t n_basis, const int32_t* pair, const float* env,
+                    int64_t E, const float* w_in, const float* b_in, const float* pair_tab, int32_t n_pair,
+                    int32_t H, const float* w1, const float* b1, const float* w_phi, const float* b_phi, int32_t B,
+                    const float* gh2, int32_t ld_gh2, const float* gphi, int32_t ld_gphi, float* grb, int32_t ld_grb,
+                    float* genv, void* stream);
 
 /* ---------------------------------------------------------------- directional edge features
  * Node tables of Kd channels: V element (component a, atom n, channel k) at

@@ -320,3 +320,44 @@ def test_dir_transport_and_gradients(Kd, B, transport):
     grads2 = torch.autograd.grad(L2, c)
     errs = [rel(a, b) for a, b in zip(outs, refs)] + [rel(a, b) for a, b in zip(grads, grads2)]
     assert max(errs) < TOL, errs
+
+
+# ----------------------------------------------------------------------------- radial MLP
+@pytest.mark.parametrize("E,nb,H,B,n_pair,want_h2", [(20000, 8, 64, 16, 9, True), (20000, 8, 64, 16, 1, False),
+                                                      (1001, 8, 16, 8, 9, False), (37, 8, 32, 20, 4, True),
+                                                      (5, 12, 48, 32, 9, True), (0, 8, 64, 16, 9, True)])
+def test_radial_mlp_matches_torch(E, nb, H, B, n_pair, want_h2):
+    """phi = (silu(silu(rb W_in^T + b_in + pair_tab[pair]) W1^T + b1) W_phi^T + b_phi) * env and h2
+    (face/model.py:465-469) vs the same layers in torch fp64, with the gradients of rb and env."""
+    from face_amd import ops
+    say("radial", E, nb, H, B, n_pair, want_h2)
+    torch.manual_seed(E + H)
+    rb = torch.randn(E, nb, device=DEV, requires_grad=True)
+    env = torch.rand(E, device=DEV, requires_grad=True)
+    pair = torch.randint(0, n_pair, (E,), device=DEV, dtype=torch.int32)
+    ws = [torch.randn(H, nb) / nb ** 0.5, torch.randn(H) * 0.1, torch.randn(n_pair, H) * 0.3,
+          torch.randn(H, H) / H ** 0.5, torch.randn(H) * 0.1, torch.randn(B, H) / H ** 0.5, torch.randn(B) * 0.1]
+    ws = [w.to(DEV) for w in ws]
+    phi, h2 = ops.radial_mlp(rb, env, pair, *ws, want_h2)
+    assert phi.shape == (E, B) and h2.shape == ((E, H) if want_h2 else (0, H))
+    if E == 0:
+        return
+    gp = torch.randn_like(phi)
+    L = (phi * gp).sum()
+    gh = torch.randn(E, H, device=DEV)
+    if want_h2:
+        L = L + (h2 * gh).sum()
+    grads = torch.autograd.grad(L, [rb, env])
+    # torch fp64 reference
+    rc = rb.detach().double().requires_grad_(True)
+    ec = env.detach().double().requires_grad_(True)
+    w = [t.double() for t in ws]
+    hid = torch.nn.functional.silu(rc @ w[0].T + w[1] + w[2][pair.long()])
+    h2r = torch.nn.functional.silu(hid @ w[3].T + w[4])
+    phir = (h2r @ w[5].T + w[6]) * ec[:, None]
+    L2 = (phir * gp.double()).sum() + ((h2r * gh.double()).sum() if want_h2 else 0)
+    grads2 = torch.autograd.grad(L2, [rc, ec])
+    outs, refs = [phi] + ([h2] if want_h2 else []), [phir] + ([h2r] if want_h2 else [])
+    errs = [rel(a, b) for a, b in zip(outs, refs)] + [rel(a, b) for a, b in zip(grads, grads2)]
+    say("   errs", errs)
+    assert max(errs) < TOL, errs
