@@ -406,11 +406,17 @@ constexpr int kCpRowsPerBlock = 2;                    // waves (= atom rows) per
 // LDS row stride of the staged gA (floats).
 __host__ __device__ constexpr int cp_mfma_stride(int C) { return C + 4; }
 
-__global__ __launch_bounds__(kCpRowsPerBlock * kWave) void cp_density_bwd_mfma_kernel(
+// HB > 0: instead of writing dR, multiply it by the CP columns of the last radial layer on the
+// matrix cores: dh2[e, h] = sum_{l,c} dR[e, l, c] W[l C + c, h] for 16 HB hidden units, with
+// w_t = W^T (16 HB, 4C) row-major (M = edges, N = hidden units, K = (rank, channel): the t
+// registers, scaled to dR, are the A operand; D rows are edges 4q + r).
+template <int HB>
+__global__ __launch_bounds__(kCpRowsPerBlock * kWave) __attribute__((amdgpu_waves_per_eu(2))) void cp_density_bwd_mfma_kernel(
     const float* __restrict__ R, int ld_R, const float* __restrict__ env, const float* __restrict__ msg, int ld_msg,
     const int32_t* __restrict__ msg_row, const float* __restrict__ Y, int ld_Y, const int32_t* __restrict__ row_ptr,
     int64_t N, int M, int C, RankIn gA, float* __restrict__ dR, int ld_dR, float* __restrict__ dmsg, int ld_dmsg,
-    float* __restrict__ dY, int ld_dY, float* __restrict__ denv) {
+    float* __restrict__ dY, int ld_dY, float* __restrict__ denv, const float* __restrict__ w_t,
+    float* __restrict__ dh2, int ld_dh2) {
     extern __shared__ float lds[];
     const int lane = threadIdx.x & (kWave - 1);
     const int w = threadIdx.x / kWave;
@@ -444,6 +450,9 @@ __global__ __launch_bounds__(kCpRowsPerBlock * kWave) void cp_density_bwd_mfma_k
         const float* Re = R + e * ld_R + own;
         const float* me = msg + mrow * ld_msg + own;
         v4f plo = z4, phi = z4;
+        v4f dacc[HB > 0 ? HB : 1];
+#pragma unroll
+        for (int hb = 0; hb < (HB > 0 ? HB : 1); ++hb) dacc[hb] = z4;
 #pragma unroll 1
         for (int cs = 0; cs < C; cs += kCpStep) {
             v4f r[2][4], m[2];
@@ -454,17 +463,42 @@ __global__ __launch_bounds__(kCpRowsPerBlock * kWave) void cp_density_bwd_mfma_k
                 m[h] = ok ? ld4(me + cs + 16 * h) : z4;
             }
             v4f dm[2] = {z4, z4};
+            // W operands of (rank l, block h) pairs, one pair ahead of the MFMAs that use them
+            constexpr int NH = HB > 0 ? HB : 1;
+            const float* wrow = w_t + (int64_t)j * 4 * C + cs + own;
+            v4f wcur[NH], wnxt[NH];
+            if (HB > 0) {
+#pragma unroll
+                for (int hb = 0; hb < NH; ++hb) wcur[hb] = ld4(wrow + (int64_t)hb * 16 * 4 * C);
+            }
 #pragma unroll
             for (int l = 0; l < 4; ++l) {
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
+                    if (HB > 0 && (l < 3 || h == 0)) {
+                        const int ln = h == 1 ? l + 1 : l, hn = h == 1 ? 0 : 1;
+#pragma unroll
+                        for (int hb = 0; hb < NH; ++hb)
+                            wnxt[hb] = ld4(wrow + (int64_t)hb * 16 * 4 * C + ln * C + 16 * hn);
+                    }
                     v4f t = z4;
 #pragma unroll
                     for (int k = kRankChunk0[l]; k < kRankChunk1[l]; ++k) {
                         const float a = q < kChunkLen[k] ? sg[t_off + kChunkX0[k] * GS + cs + 16 * h] : 0.f;
                         t = mfma_16x16x4(a, yq[k], t);
                     }
-                    if (ok && dR) st4(dR + e * ld_dR + l * C + cs + own + 16 * h, (ev * m[h]) * t);
+                    if (HB > 0) {
+                        const v4f g = (ev * m[h]) * t;
+#pragma unroll
+                        for (int rr = 0; rr < 4; ++rr) {
+#pragma unroll
+                            for (int hb = 0; hb < NH; ++hb) dacc[hb] = mfma_16x16x4(g[rr], wcur[hb][rr], dacc[hb]);
+                        }
+#pragma unroll
+                        for (int hb = 0; hb < NH; ++hb) wcur[hb] = wnxt[hb];
+                    } else if (ok && dR) {
+                        st4(dR + e * ld_dR + l * C + cs + own + 16 * h, (ev * m[h]) * t);
+                    }
                     dm[h] += r[h][l] * t;
                 }
             }
@@ -498,6 +532,17 @@ __global__ __launch_bounds__(kCpRowsPerBlock * kWave) void cp_density_bwd_mfma_k
         s += __shfl_xor(s, 16, kWave);
         s += __shfl_xor(s, 32, kWave);
         if (denv && ok && q == 0) denv[e] = s;
+        if (HB > 0) {
+            // dacc[hb] register r of lane (j, q): edge t0 + 4q + r, hidden unit 16 hb + j
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const int64_t er = t0 + 4 * q + rr;
+                if (er < e1) {
+#pragma unroll
+                    for (int hb = 0; hb < (HB > 0 ? HB : 1); ++hb) dh2[er * ld_dh2 + 16 * hb + j] = dacc[hb][rr];
+                }
+            }
+        }
     }
 }
 
@@ -735,10 +780,10 @@ extern "C" int face_cp_density_bwd(const float* R, int32_t ld_R, const float* en
         // one atom row per wave, kCpRowsPerBlock rows per workgroup, each with its gA slice in LDS
         const size_t lds = (size_t)kCpRowsPerBlock * 20 * cp_mfma_stride(C) * sizeof(float);
         if (lds > 65536) return FACE_ERR_UNSUPPORTED;
-        hipLaunchKernelGGL(cp_density_bwd_mfma_kernel, dim3((unsigned)((N + kCpRowsPerBlock - 1) / kCpRowsPerBlock)),
-                           dim3(kCpRowsPerBlock * kWave), lds,
-                           (hipStream_t)stream, R, ld_R, env, msg, ld_msg, msg_row, Y, ld_Y, row_ptr, N, M, C, gA, dR,
-                           ld_dR, dmsg, ld_dmsg, dY, ld_dY, denv);
+        hipLaunchKernelGGL(cp_density_bwd_mfma_kernel<0>, dim3((unsigned)((N + kCpRowsPerBlock - 1) / kCpRowsPerBlock)),
+                           dim3(kCpRowsPerBlock * kWave), lds, (hipStream_t)stream, R, ld_R, env, msg, ld_msg, msg_row,
+                           Y, ld_Y, row_ptr, N, M, C, gA, dR, ld_dR, dmsg, ld_dmsg, dY, ld_dY, denv, nullptr, nullptr,
+                           0);
         FACE_LAUNCH_CHECK();
         return 0;
     }
@@ -749,6 +794,38 @@ extern "C" int face_cp_density_bwd(const float* R, int32_t ld_R, const float* en
     if ((int64_t)lds > 65536) return FACE_ERR_UNSUPPORTED;
     hipLaunchKernelGGL(cp_density_bwd_kernel, dim3((unsigned)N), dim3(nthr), lds, (hipStream_t)stream, R, ld_R, env,
                        msg, ld_msg, msg_row, Y, ld_Y, row_ptr, M, C, gA, dR, ld_dR, dmsg, ld_dmsg, dY, ld_dY, denv);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int face_cp_radial_bwd(const float* R, int32_t ld_R, const float* env, const float* msg, int32_t ld_msg,
+                                  const int32_t* msg_row, const float* Y, int32_t ld_Y, const int32_t* row_ptr,
+                                  int64_t N, int32_t M, int32_t C, const float* const* gA_ranks, int64_t atom_stride,
+                                  int64_t x_stride, const float* w_t, int32_t H, float* dh2, int32_t ld_dh2,
+                                  float* dmsg, int32_t ld_dmsg, float* dY, int32_t ld_dY, float* denv,
+                                  void* stream) {
+    if (N < 0 || C <= 0 || ld_R < 4 * C || ld_msg < C || ld_Y < 20 || (!row_ptr && M < 0)) return FACE_ERR_ARG;
+    if (H < 16 || H > 64 || H % 16 || !w_t || ((uintptr_t)w_t & 15) || !dh2 || ld_dh2 < H) return FACE_ERR_ARG;
+    if ((dmsg && ld_dmsg < C) || (dY && ld_dY < 20)) return FACE_ERR_ARG;
+    if (N == 0) return 0;
+    RankIn gA;
+    if (!R || !msg || !Y || !rank_in(gA_ranks, atom_stride, x_stride, 20, gA)) return FACE_ERR_ARG;
+    if (!mfma_layout_ok(R, ld_R, msg, ld_msg, Y, ld_Y, C, gA, nullptr, 0, dmsg, ld_dmsg, dY, ld_dY))
+        return FACE_ERR_UNSUPPORTED;
+    const size_t lds = (size_t)kCpRowsPerBlock * 20 * cp_mfma_stride(C) * sizeof(float);
+    if (lds > 65536) return FACE_ERR_UNSUPPORTED;
+    const dim3 grid((unsigned)((N + kCpRowsPerBlock - 1) / kCpRowsPerBlock)), block(kCpRowsPerBlock * kWave);
+    const hipStream_t st = (hipStream_t)stream;
+#define FACE_CPR(HB_)                                                                                           \
+    hipLaunchKernelGGL(cp_density_bwd_mfma_kernel<HB_>, grid, block, lds, st, R, ld_R, env, msg, ld_msg, msg_row, \
+                       Y, ld_Y, row_ptr, N, M, C, gA, nullptr, 0, dmsg, ld_dmsg, dY, ld_dY, denv, w_t, dh2, ld_dh2)
+    switch (H / 16) {
+        case 1: FACE_CPR(1); break;
+        case 2: FACE_CPR(2); break;
+        case 3: FACE_CPR(3); break;
+        default: FACE_CPR(4); break;
+    }
+#undef FACE_CPR
     FACE_LAUNCH_CHECK();
     return 0;
 }

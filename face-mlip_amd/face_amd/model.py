@@ -186,8 +186,12 @@ class FactorBlock(nn.Module):
             mj, gathered = msg_n, True
         s = self.elem_scale(zidx).view(N, 4, C) / avg_nb
         if self.cp:
-            R = F.linear(h2, W2[B:], b2[B:])                                      # (E, 4C), envelope in-kernel
-            Af = ops.cp_density(R, env, mj, Y, g, gathered)                       # 4 x (k_l, N, C)
+            # R = h2 W2[B:]^T + b2[B:] (E, 4C) feeds the pooling (envelope applied in-kernel); on the
+            # matrix-core shapes the pooling backward also applies W2[B:] and returns d h2 directly
+            if C % 32 == 0 and h2.shape[1] % 16 == 0 and h2.shape[1] <= 64:
+                Af = ops.cp_radial_density(h2, W2[B:].detach(), b2[B:].detach(), env, mj, Y, g, gathered)
+            else:
+                Af = ops.cp_density(F.linear(h2, W2[B:], b2[B:]), env, mj, Y, g, gathered)   # 4 x (k_l, N, C)
         else:
             Af = ops.density(phi, mj, Y, g, 20, gathered)                         # 4 x (k_l, N, B*K)
         A = [self.mix[l](Af[l]) * s[None, :, l, :] for l in range(4)]             # 4 x (k_l, N, C)
@@ -210,12 +214,14 @@ class FactorBlock(nn.Module):
                 W = W[:C]                                                         # only P0 is used
             elif l == 3:
                 W = W[:2 * C]                                                     # S3 is unused
-            # proj over the concatenated moment sets as a sum of per-set GEMMs (no concat copy)
+            # proj over the concatenated moment sets as a sum of per-set GEMMs (no concat copy); the
+            # GEMMs after the first accumulate in their epilogue (no separate add pass)
             y = None
             for si, S in enumerate(allsets):
                 Ws = W[:, si * C:(si + 1) * C]
-                y = F.linear(S[l], Ws) if y is None else y + F.linear(S[l], Ws)
-            ys.append(y)                                                          # (k_l, N, 3C | C | 2C)
+                x2 = S[l].reshape(-1, C)
+                y = x2 @ Ws.t() if y is None else torch.addmm(y, x2, Ws.t())
+            ys.append(y.view(S[l].shape[0], S[l].shape[1], -1))                   # (k_l, N, 3C | C | 2C)
         if self.eq_out:
             feats, V, Ms = ops.node_features(ys[0], ys[1], ys[2], ys[3], self.vpath, self.mpath, True, C)
         else:

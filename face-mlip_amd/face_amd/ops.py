@@ -359,6 +359,62 @@ def cp_density(R, env, msg, Y, graph, gathered=False):
     return CPDensity.apply(R, env, msg, Y, graph, gathered)
 
 
+class CPRadialDensity(torch.autograd.Function):
+    """CP pooling fed by the CP columns of the last radial layer: R = h2 W_cp^T + b_cp (E, 4C), then
+    A_l as in CPDensity (face/model.py:469-472, 496-502). The backward multiplies the pooling's dR by
+    W_cp on the matrix cores inside the pooling kernel and returns d h2 (E, H) without writing dR.
+    W_cp / b_cp receive no gradient (forces only)."""
+
+    @staticmethod
+    def forward(ctx, h2, w_cp, b_cp, env, msg, Y, graph, gathered):
+        _lib.require_gpu(h2, env, msg, Y)
+        C = msg.shape[1]
+        R = torch.addmm(b_cp.detach(), h2.detach(), w_cp.detach().t())                        # (E, 4C)
+        env_ = env.contiguous().float()
+        msg_, ld_msg = _rows(msg, C)
+        Y_, ld_Y = _rows(Y, 20)
+        outs = [torch.empty(k, graph.N, C, device=R.device) for k in RANK_K]
+        row = graph.col if gathered else None
+        call("face_cp_density_fwd", ptr(R), R.stride(0), ptr(env_), ptr(msg_), ld_msg, ptr(row), ptr(Y_), ld_Y,
+             ptr(graph.row_ptr), graph.N, 0, C, *_lib.ranks_of_blocks(outs), _lib.stream_of(R), label="cp_fwd")
+        ctx.save_for_backward(R, w_cp.detach(), env_, msg_, Y_)
+        ctx.graph, ctx.gathered, ctx.C = graph, gathered, C
+        return tuple(outs)
+
+    @staticmethod
+    def backward(ctx, *grads):
+        if ctx.needs_input_grad[1] or ctx.needs_input_grad[2]:
+            raise NotImplementedError("the fused CP radial backward gives no weight gradients (forces only)")
+        R, w_cp, env, msg, Y = ctx.saved_tensors
+        g, C = ctx.graph, ctx.C
+        dev = R.device
+        H = w_cp.shape[1]
+        Gs = [(t.contiguous().float() if t is not None else torch.zeros(k, g.N, C, device=dev))
+              for t, k in zip(grads, RANK_K)]
+        need_h2, need_env, need_msg, need_Y = (ctx.needs_input_grad[0], ctx.needs_input_grad[3],
+                                               ctx.needs_input_grad[4], ctx.needs_input_grad[5])
+        w_t = w_cp.t().contiguous()                                                          # (H, 4C)
+        dh2 = torch.empty(g.E, H, device=dev)
+        denv = torch.empty(g.E, device=dev) if need_env else None
+        dmsg = torch.empty(g.E, C, device=dev) if need_msg else None
+        dY = torch.empty(g.E, 20, device=dev) if need_Y else None
+        row = g.col if ctx.gathered else None
+        st = _lib.stream_of(R)
+        call("face_cp_radial_bwd", ptr(R), R.stride(0), ptr(env), ptr(msg), msg.stride(0), ptr(row), ptr(Y),
+             Y.stride(0), ptr(g.row_ptr), g.N, 0, C, *_lib.ranks_of_blocks(Gs), ptr(w_t), H, ptr(dh2), H, ptr(dmsg),
+             C, ptr(dY), 20, ptr(denv), st, label="cp_bwd")
+        if dmsg is not None and ctx.gathered:
+            dtab = torch.empty(g.N, C, device=dev)
+            call("face_gather_rows_bwd", ptr(dmsg), C, ptr(g.row_ptr), ptr(g.rev), g.N, C, ptr(dtab), C, st,
+                 label="gather_bwd")
+            dmsg = dtab
+        return (dh2 if need_h2 else None), None, None, denv, dmsg, dY, None, None
+
+
+def cp_radial_density(h2, w_cp, b_cp, env, msg, Y, graph, gathered=False):
+    return CPRadialDensity.apply(h2, w_cp, b_cp, env, msg, Y, graph, gathered)
+
+
 # ----------------------------------------------------------------------------- radial MLP
 class RadialMLP(torch.autograd.Function):
     """phi (E, B) = (silu(silu(rb W_in^T + b_in + pair_tab[pair]) W1^T + b1) W_phi^T + b_phi) * env and,

@@ -94,6 +94,17 @@ int face_cp_density_bwd(const float* R, int32_t ld_R, const float* env, const fl
                         int64_t x_stride, float* dR, int32_t ld_dR, float* dmsg, int32_t ld_dmsg, float* dY,
                         int32_t ld_dY, float* denv, void* stream);
 
+/* CP pooling backward fused with the CP columns of the last radial layer (face/model.py:469-472):
+ * with R = h2 W^T + b (W (4C, H)), returns dh2 (E, ld_dh2) = dR W instead of dR, computed on the
+ * matrix cores inside the pooling kernel. w_t = W^T (H, 4C) row-major, 16-byte aligned;
+ * H in {16, 32, 48, 64}; C a multiple of 32 and the layout conditions of the matrix-core
+ * path above. Other arguments as face_cp_density_bwd (dmsg, dY, denv may be NULL). */
+int face_cp_radial_bwd(const float* R, int32_t ld_R, const float* env, const float* msg, int32_t ld_msg,
+                       const int32_t* msg_row, const float* Y, int32_t ld_Y, const int32_t* row_ptr, int64_t N,
+                       int32_t M, int32_t C, const float* const* gA_ranks, int64_t atom_stride, int64_t x_stride,
+                       const float* w_t, int32_t H, float* dh2, int32_t ld_dh2, float* dmsg, int32_t ld_dmsg,
+                       float* dY, int32_t ld_dY, float* denv, void* stream);
+
 /* ---------------------------------------------------------------- node algebra
  * Per (atom n, channel c) invariants of symmetric Cartesian tensors
  *   inputs  P1,Q1,S1 (3 comps), P2,Q2,S2 (6, order xx,yy,zz,xy,xz,yz), P3,Q3 (10, face/cartesian.py:14-15)

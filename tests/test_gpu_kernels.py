@@ -152,6 +152,41 @@ def test_cp_density_ragged_rows(gathered, C):
     assert max(errs) < TOL, errs
 
 
+@pytest.mark.parametrize("gathered,C,H", [(False, 160, 64), (True, 160, 64), (True, 96, 32), (False, 64, 16),
+                                          (True, 32, 48)])
+def test_cp_radial_density_fused_backward(gathered, C, H):
+    """R = h2 W^T + b feeding the CP pooling, whose backward returns d h2 = dR W from inside the
+    pooling kernel: outputs and gradients (h2, env, msg, Y) vs the oracle in fp64."""
+    from face_amd import ops
+    say("cp radial density", gathered, C, H)
+    g = _G(41, 600, 5)
+    counts = g.counts
+    E = sum(counts)
+    torch.manual_seed(C + H)
+    h2 = torch.randn(E, H, device=DEV, requires_grad=True)
+    W = torch.randn(4 * C, H, device=DEV) / H ** 0.5
+    b = torch.randn(4 * C, device=DEV) * 0.1
+    env = torch.rand(E, device=DEV, requires_grad=True)
+    msg = torch.randn(41 if gathered else E, C, device=DEV, requires_grad=True)
+    Y = torch.randn(E, 20, device=DEV, requires_grad=True)
+    A = torch.cat(ops.cp_radial_density(h2, W, b, env, msg, Y, g.G, gathered), 0).permute(1, 0, 2)   # (N, 20, C)
+    G = torch.randn_like(A)
+    gr = torch.autograd.grad((A * G).sum(), (h2, env, msg, Y))
+    M = max(counts)
+    col = g.G.col.long().cpu()
+    pd = lambda t: _pad(t, counts, M)
+    hc = h2.detach().double().cpu().requires_grad_(True)
+    ec = env.detach().double().cpu().requires_grad_(True)
+    ms = msg.detach().double().cpu().requires_grad_(True)
+    Yc = Y.detach().double().cpu().requires_grad_(True)
+    Rc = hc @ W.double().cpu().T + b.double().cpu()
+    A2 = oops.cp_density(pd((Rc * ec[:, None]).view(E, 4, C)), pd(ms[col] if gathered else ms), pd(Yc))
+    gr2 = torch.autograd.grad((A2 * G.double().cpu()).sum(), (hc, ec, ms, Yc))
+    errs = [rel(A, A2)] + [rel(a, b) for a, b in zip(gr, gr2)]
+    say("   errs", errs)
+    assert max(errs) < TOL, errs
+
+
 # ----------------------------------------------------------------------------- node algebra
 @pytest.mark.parametrize("eq", [True, False])
 def test_node_algebra_dropin_matches_reference_spec(eq):
