@@ -426,9 +426,25 @@ __global__ __launch_bounds__(kCpRowsPerBlock * kWave) __attribute__((amdgpu_wave
     float* sg = lds + (size_t)w * 20 * GS;
     const int j = lane & 15, q = lane >> 4;
     const int nc4 = C >> 2;
-    for (int v = lane; v < 20 * nc4; v += kWave) {
-        const int x = v / nc4, c4 = v - x * nc4;
-        *reinterpret_cast<v4f*>(sg + x * GS + 4 * c4) = ld4(gA.at(i, x) + 4 * c4);
+    // stage gA[i]: up to 8 float4 per lane in flight per batch
+    for (int v0 = 0; v0 < 20 * nc4; v0 += 8 * kWave) {
+        v4f buf[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int v = v0 + u * kWave + lane;
+            if (v < 20 * nc4) {
+                const int x = v / nc4, c4 = v - x * nc4;
+                buf[u] = ld4(gA.at(i, x) + 4 * c4);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int v = v0 + u * kWave + lane;
+            if (v < 20 * nc4) {
+                const int x = v / nc4, c4 = v - x * nc4;
+                *reinterpret_cast<v4f*>(sg + x * GS + 4 * c4) = buf[u];
+            }
+        }
     }
     __builtin_amdgcn_wave_barrier();
     const int t_off = q * GS + j;                     // + kChunkX0[k] * GS + channel block start

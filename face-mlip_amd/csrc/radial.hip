@@ -20,7 +20,11 @@ struct RadialWeights {
     const float *w_in, *b_in, *pair_tab, *w1, *b1, *w_phi, *b_phi;
 };
 
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.f / (1.f + expf(-x)); }
+// sigmoid with the hardware exp2 and reciprocal (about 1 ulp each): the IEEE expf and divide
+// sequences dominated the instruction count of the radial kernels
+__device__ __forceinline__ float sigmoidf_(float x) {
+    return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.44269504088896341f * x));
+}
 __device__ __forceinline__ v4f silu4(v4f u) {
     v4f o;
 #pragma unroll
@@ -55,27 +59,43 @@ struct RadialLds {
     }
 };
 
+// dst[v] = src(v) for v < n over the workgroup, 8 loads per thread in flight per batch.
+template <typename Src>
+__device__ __forceinline__ void stage_lds(float* dst, int n, Src src) {
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    for (int v0 = 0; v0 < n; v0 += 8 * nthr) {
+        float b[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int v = v0 + u * nthr + tid;
+            b[u] = v < n ? src(v) : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int v = v0 + u * nthr + tid;
+            if (v < n) dst[v] = b[u];
+        }
+    }
+}
+
 __device__ void radial_stage(float* lds, const RadialLds& L, const RadialWeights& W, int H, int BB, int nbasis,
                              int n_pair, int B) {
-    const int tid = threadIdx.x, nthr = blockDim.x;
-    for (int v = tid; v < H * L.SI; v += nthr) {
+    stage_lds(lds, H * L.SI, [&](int v) {
         const int h = v / L.SI, k = v - h * L.SI;
-        lds[v] = k < nbasis ? W.w_in[h * nbasis + k] : 0.f;
-    }
-    for (int v = tid; v < H; v += nthr) {
-        lds[L.o_bin + v] = W.b_in[v];
-        lds[L.o_b1 + v] = W.b1[v];
-    }
-    for (int v = tid; v < n_pair * H; v += nthr) lds[L.o_pt + v] = W.pair_tab[v];
-    for (int v = tid; v < H * L.S1; v += nthr) {
+        return k < nbasis ? W.w_in[h * nbasis + k] : 0.f;
+    });
+    stage_lds(lds + L.o_bin, H, [&](int v) { return W.b_in[v]; });
+    stage_lds(lds + L.o_b1, H, [&](int v) { return W.b1[v]; });
+    stage_lds(lds + L.o_pt, n_pair * H, [&](int v) { return W.pair_tab[v]; });
+    stage_lds(lds + L.o_w1, H * L.S1, [&](int v) {
         const int h = v / L.S1, k = v - h * L.S1;
-        lds[L.o_w1 + v] = k < H ? W.w1[h * H + k] : 0.f;
-    }
-    for (int v = tid; v < 16 * BB * L.S1; v += nthr) {
+        return k < H ? W.w1[h * H + k] : 0.f;
+    });
+    stage_lds(lds + L.o_wp, 16 * BB * L.S1, [&](int v) {
         const int b = v / L.S1, k = v - b * L.S1;
-        lds[L.o_wp + v] = (b < B && k < H) ? W.w_phi[b * H + k] : 0.f;
-    }
-    for (int v = tid; v < 16 * BB; v += nthr) lds[L.o_bp + v] = v < B ? W.b_phi[v] : 0.f;
+        return (b < B && k < H) ? W.w_phi[b * H + k] : 0.f;
+    });
+    stage_lds(lds + L.o_bp, 16 * BB, [&](int v) { return v < B ? W.b_phi[v] : 0.f; });
 }
 
 __device__ __forceinline__ v4f lds4(const float* p) { return *reinterpret_cast<const v4f*>(p); }

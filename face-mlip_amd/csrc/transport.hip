@@ -141,8 +141,9 @@ __global__ __launch_bounds__(256) void transport_bwd_kernel(const float* __restr
     const int64_t i = blockIdx.x;
     const int tid = threadIdx.x, nthr = blockDim.x;
     const int64_t W = (int64_t)B * 2 * Kd;
+    // (channel fastest: each wave reads contiguous runs of the nine upstream component rows)
     for (int q = tid; q < B * Kd * kFP; q += nthr) {
-        const int o = q % kFP, r = q / kFP;
+        const int r = q % (B * Kd), o = q / (B * Kd);
         const int k = r % Kd, bb = r / Kd;
         const int64_t ch0 = (int64_t)bb * 2 * Kd + k;
         float v = 0.f;
@@ -150,7 +151,7 @@ __global__ __launch_bounds__(256) void transport_bwd_kernel(const float* __restr
         else if (o < 6) v = gD1[((o - 3) * N + i) * W + ch0 + Kd];
         else if (o < 12) v = gD2[((o - 6) * N + i) * W + ch0];
         else if (o < 18) v = gD2[((o - 12) * N + i) * W + ch0 + Kd];
-        s_g[q] = scale * v;
+        s_g[r * kFP + o] = scale * v;
     }
     __syncthreads();
     const int kd = tid & (KP - 1);
@@ -237,6 +238,149 @@ __global__ __launch_bounds__(256) void transport_bwd_kernel(const float* __restr
     }
 }
 
+// Matrix-core backward for B == 16, Kd == 16 (the flagship widths). One wave per atom row;
+// the row's upstream gradient G[o][b][kd] = scale * gD (18 x 16 x 16) sits in the wave's LDS
+// slice. Per tile of 16 edges, lane (j, q) owns edge j and channels kd = 4q + r (r = 0..3):
+//   dphi[b, e]   = sum_{o, kd} G[o][b][kd] F[e][kd][o]   M = b, N = e, K = kd (one o per chain step)
+//   dF[o][kd, e] = sum_b G[o][b][kd] phi[e][b]          M = kd, N = e, K = b
+// With v_mfma_f32_16x16x4f32 (A[i][k] in lane i + 16k, B[k][n] in lane n + 16k, D[4q + r][n] in
+// register r of lane n + 16q) the F operand of lane (j, q) for K index q is its own channel
+// 4q + kc, and the dF block of o lands in register r = kd - 4q of lane (j, q): every lane ends
+// with all 18 dF[o] of its 4 channels and forms the table and direction gradients locally.
+__global__ __launch_bounds__(2 * kWave) void transport_bwd_mfma_kernel(
+    const float* __restrict__ phi, int ld_phi, Tables T, const float* __restrict__ Y, int ld_Y,
+    const int32_t* __restrict__ col, const int32_t* __restrict__ row_ptr, int64_t N, float scale,
+    const float* __restrict__ gD1, const float* __restrict__ gD2, float* __restrict__ dphi, int ld_dphi,
+    float* __restrict__ dT_edge, float* __restrict__ gY) {
+    constexpr int Kd = 16, B = 16, W = 2 * B * Kd;
+    extern __shared__ float lds[];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int w = threadIdx.x / kWave;
+    const int64_t i = (int64_t)blockIdx.x * 2 + w;
+    if (i >= N) return;                               // uniform per wave
+    float* sG = lds + (size_t)w * 18 * B * Kd;
+    // channel (b, kd) fastest: contiguous reads; all 18 component rows of a lane in flight at once
+    for (int c0 = 0; c0 < B * Kd; c0 += kWave) {
+        const int r = c0 + lane;
+        const int kd = r % Kd, b = r / Kd;
+        const int64_t ch = (int64_t)b * 2 * Kd + kd;
+        float g[18];
+#pragma unroll
+        for (int o = 0; o < 18; ++o) {
+            if (o < 3) g[o] = gD1[(o * N + i) * W + ch];
+            else if (o < 6) g[o] = gD1[((o - 3) * N + i) * W + ch + Kd];
+            else if (o < 12) g[o] = gD2[((o - 6) * N + i) * W + ch];
+            else g[o] = gD2[((o - 12) * N + i) * W + ch + Kd];
+        }
+#pragma unroll
+        for (int o = 0; o < 18; ++o) sG[o * B * Kd + r] = scale * g[o];
+    }
+    __builtin_amdgcn_wave_barrier();
+    const int j = lane & 15, q = lane >> 4;
+    const v4f z4 = {0.f, 0.f, 0.f, 0.f};
+    const int64_t e0 = row_ptr[i], e1 = row_ptr[i + 1];
+    for (int64_t t0 = e0; t0 < e1; t0 += 16) {
+        const int64_t e = t0 + j;
+        const bool ok = e < e1;
+        float u[3] = {0.f, 0.f, 0.f}, ph[4] = {0.f, 0.f, 0.f, 0.f};
+        v4f V[3], Mt[6];
+        if (ok) {
+            const float* y = Y + e * ld_Y;
+            u[0] = y[1]; u[1] = y[2]; u[2] = y[3];
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) ph[kb] = phi[e * ld_phi + 4 * kb + q];
+            const int64_t n = col[e];
+#pragma unroll
+            for (int a = 0; a < 3; ++a) V[a] = ld4(T.V + a * T.v_sq + n * T.v_sn + 4 * q);
+#pragma unroll
+            for (int k = 0; k < 6; ++k) Mt[k] = ld4(T.M + k * T.m_sq + n * T.m_sn + 4 * q);
+        } else {
+#pragma unroll
+            for (int a = 0; a < 3; ++a) V[a] = z4;
+#pragma unroll
+            for (int k = 0; k < 6; ++k) Mt[k] = z4;
+        }
+        v4f acc_phi = z4;
+        v4f dV[3] = {z4, z4, z4}, dM[6] = {z4, z4, z4, z4, z4, z4};
+        float du[3] = {0.f, 0.f, 0.f};
+#pragma unroll
+        for (int o = 0; o < 18; ++o) {
+            // features F[o] of this lane's 4 channels
+            v4f F;
+            if (o < 3) {
+                F = V[o];
+            } else if (o < 6) {
+                const int a = o - 3;
+                F = Mt[s2(a, 0)] * u[0] + Mt[s2(a, 1)] * u[1] + Mt[s2(a, 2)] * u[2];
+            } else if (o < 12) {
+                F = Mt[o - 6];
+            } else if (o < 15) {
+                F = V[o - 12] * u[o - 12];
+            } else {
+                const int a = o == 17 ? 1 : 0, c = o == 15 ? 1 : 2;
+                F = 0.5f * (V[c] * u[a] + V[a] * u[c]);
+            }
+            const float* g = sG + o * B * Kd;
+            // dphi: K index q <-> channel 4q + kc; A = G[o][b = j][4q .. 4q + 3]
+            const v4f ga = *reinterpret_cast<const v4f*>(g + j * Kd + 4 * q);
+#pragma unroll
+            for (int kc = 0; kc < 4; ++kc) acc_phi = mfma_16x16x4(ga[kc], F[kc], acc_phi);
+            // dF[o]: register r <-> channel 4q + r; A = G[o][b = 4kb + q][kd = j]
+            v4f d = z4;
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) d = mfma_16x16x4(g[(4 * kb + q) * Kd + j], ph[kb], d);
+            if (o < 3) {
+                dV[o] += d;
+            } else if (o < 6) {
+                const int a = o - 3;
+#pragma unroll
+                for (int c = 0; c < 3; ++c) {
+                    dM[s2(a, c)] += u[c] * d;
+                    const v4f pm = Mt[s2(a, c)] * d;
+                    du[c] += pm[0] + pm[1] + pm[2] + pm[3];
+                }
+            } else if (o < 12) {
+                dM[o - 6] += d;
+            } else if (o < 15) {
+                const int a = o - 12;
+                const v4f pv = V[a] * d;
+                du[a] += pv[0] + pv[1] + pv[2] + pv[3];
+                dV[a] += u[a] * d;
+            } else {
+                const int a = o == 17 ? 1 : 0, c = o == 15 ? 1 : 2;
+                const v4f h = 0.5f * d;
+                const v4f pc = V[c] * h, pa = V[a] * h;
+                du[a] += pc[0] + pc[1] + pc[2] + pc[3];
+                du[c] += pa[0] + pa[1] + pa[2] + pa[3];
+                dV[c] += u[a] * h;
+                dV[a] += u[c] * h;
+            }
+            __builtin_amdgcn_sched_barrier(0);        // keep each o step's operands local
+        }
+        if (ok) {
+            if (dphi) st4(dphi + e * ld_dphi + 4 * q, acc_phi);       // register r <-> b = 4q + r
+            if (dT_edge) {
+                float* o = dT_edge + e * 9 * Kd + 4 * q;
+#pragma unroll
+                for (int a = 0; a < 3; ++a) st4(o + a * Kd, dV[a]);
+#pragma unroll
+                for (int k = 0; k < 6; ++k) st4(o + (3 + k) * Kd, dM[k]);
+            }
+        }
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            du[a] += __shfl_xor(du[a], 16, kWave);
+            du[a] += __shfl_xor(du[a], 32, kWave);
+        }
+        if (ok && q == 0 && gY) {
+            float* gy = gY + e * 20;
+            gy[1] += du[0];
+            gy[2] += du[1];
+            gy[3] += du[2];
+        }
+    }
+}
+
 // Node-table gradient of the transport tables: gV[a, n, kd] = sum_{e in row n} dT_edge[rev e, a, kd]
 // (the edges whose neighbour is n are the reverses of row n); same for gM.
 __global__ __launch_bounds__(256) void transport_table_grad_kernel(const float* __restrict__ dT_edge, int Kd,
@@ -297,8 +441,16 @@ extern "C" int face_transport_bwd(const float* phi, int32_t ld_phi, int32_t B, c
     if (lds > 65536) return FACE_ERR_UNSUPPORTED;
     Tables T{V, M, v_sn, v_sq, m_sn, m_sq};
     hipStream_t st = (hipStream_t)stream;
-    hipLaunchKernelGGL(transport_bwd_kernel, dim3((unsigned)N), dim3(nw * kWave), lds, st, phi, ld_phi, B, T, Kd, KP,
-                       Y, ld_Y, col, row_ptr, N, scale, gD1, gD2, dphi, ld_dphi, dT_edge, gY);
+    const bool a16 = !(((uintptr_t)V | (uintptr_t)M | (uintptr_t)(dphi ? dphi : V) | (uintptr_t)(dT_edge ? dT_edge : V)) & 15);
+    if (B == 16 && Kd == 16 && a16 && v_sn % 4 == 0 && v_sq % 4 == 0 && m_sn % 4 == 0 && m_sq % 4 == 0 &&
+        (!dphi || ld_dphi % 4 == 0)) {
+        const size_t lds2 = (size_t)2 * 18 * 16 * 16 * sizeof(float);
+        hipLaunchKernelGGL(transport_bwd_mfma_kernel, dim3((unsigned)((N + 1) / 2)), dim3(2 * kWave), lds2, st, phi,
+                           ld_phi, T, Y, ld_Y, col, row_ptr, N, scale, gD1, gD2, dphi, ld_dphi, dT_edge, gY);
+    } else {
+        hipLaunchKernelGGL(transport_bwd_kernel, dim3((unsigned)N), dim3(nw * kWave), lds, st, phi, ld_phi, B, T, Kd,
+                           KP, Y, ld_Y, col, row_ptr, N, scale, gD1, gD2, dphi, ld_dphi, dT_edge, gY);
+    }
     if (gV) {
         const int64_t total = N * 9 * Kd;
         hipLaunchKernelGGL(transport_table_grad_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
