@@ -181,7 +181,11 @@ class FactorBlock(nn.Module):
             Vb = self.pvt(src1)                                                  # (3, N, nt*Kd)
             Mb = self.pmt(src2)                                                  # (6, N, nt*Kd)
             d, D1, D2 = ops.dir_transport(Vb, Mb, phi, Y, g, Kd, self.transport)   # (E, 4Kd), transport sums
-            mj, gathered = ops.gather_neighbour(msg_n, g) + self.dir_mix(d), False
+            # gather(msg(h)) + dir_mix(d): the bias joins the node table before the gather and the
+            # dir_mix GEMM accumulates onto the gathered rows in its epilogue
+            Wd, bd = weight(self.dir_mix)
+            mj = ops.gather_neighbour(msg_n + bd, g).addmm_(d, Wd.t())
+            gathered = False
         else:
             mj, gathered = msg_n, True
         s = self.elem_scale(zidx).view(N, 4, C) / avg_nb
@@ -215,12 +219,12 @@ class FactorBlock(nn.Module):
             elif l == 3:
                 W = W[:2 * C]                                                     # S3 is unused
             # proj over the concatenated moment sets as a sum of per-set GEMMs (no concat copy); the
-            # GEMMs after the first accumulate in their epilogue (no separate add pass)
+            # GEMMs after the first accumulate in place in their epilogue (no add or copy pass)
             y = None
             for si, S in enumerate(allsets):
                 Ws = W[:, si * C:(si + 1) * C]
                 x2 = S[l].reshape(-1, C)
-                y = x2 @ Ws.t() if y is None else torch.addmm(y, x2, Ws.t())
+                y = x2 @ Ws.t() if y is None else y.addmm_(x2, Ws.t())
             ys.append(y.view(S[l].shape[0], S[l].shape[1], -1))                   # (k_l, N, 3C | C | 2C)
         if self.eq_out:
             feats, V, Ms = ops.node_features(ys[0], ys[1], ys[2], ys[3], self.vpath, self.mpath, True, C)
@@ -228,7 +232,9 @@ class FactorBlock(nn.Module):
             feats, V, Ms = ops.node_features(ys[0], ys[1], ys[2], ys[3], None, None, False, C)
         inv = self.norm(feats)
         W0, b0 = weight(self.out[0])
-        z = F.linear(torch.cat([inv, h], 1), W0[:, :-4], b0)   # the 4 trailing inputs are zeros
+        # out[0] on cat([inv, h, 0 (4)]) as two accumulating GEMMs (no concatenated copy)
+        nf = self.N_INV * C
+        z = F.linear(inv, W0[:, :nf], b0).addmm_(h, W0[:, nf:nf + C].t())
         o = run_mlp(self.out[2:], F.silu(z))
         eq_new = None
         if self.eq_out:
