@@ -426,11 +426,11 @@ __global__ __launch_bounds__(kCpRowsPerBlock * kWave) __attribute__((amdgpu_wave
     float* sg = lds + (size_t)w * 20 * GS;
     const int j = lane & 15, q = lane >> 4;
     const int nc4 = C >> 2;
-    // stage gA[i]: up to 8 float4 per lane in flight per batch
-    for (int v0 = 0; v0 < 20 * nc4; v0 += 8 * kWave) {
-        v4f buf[8];
+    // stage gA[i]: up to 4 float4 per lane in flight per batch
+    for (int v0 = 0; v0 < 20 * nc4; v0 += 4 * kWave) {
+        v4f buf[4];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < 4; ++u) {
             const int v = v0 + u * kWave + lane;
             if (v < 20 * nc4) {
                 const int x = v / nc4, c4 = v - x * nc4;
@@ -438,7 +438,7 @@ __global__ __launch_bounds__(kCpRowsPerBlock * kWave) __attribute__((amdgpu_wave
             }
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < 4; ++u) {
             const int v = v0 + u * kWave + lane;
             if (v < 20 * nc4) {
                 const int x = v / nc4, c4 = v - x * nc4;
