@@ -135,15 +135,17 @@ class GatherReceiver(torch.autograd.Function):
 
 
 def gather_neighbour(X, graph):
+    # 2-d tables come back as the operator's own output (not a view of it), so callers may
+    # accumulate into it in place without autograd copying the gradient
     shp = X.shape
     out = GatherNeighbour.apply(X.reshape(shp[0], -1), graph)
-    return out.view(graph.E, *shp[1:])
+    return out if X.dim() == 2 else out.view(graph.E, *shp[1:])
 
 
 def gather_receiver(X, graph):
     shp = X.shape
     out = GatherReceiver.apply(X.reshape(shp[0], -1), graph)
-    return out.view(graph.E, *shp[1:])
+    return out if X.dim() == 2 else out.view(graph.E, *shp[1:])
 
 
 class DirTransport(torch.autograd.Function):
