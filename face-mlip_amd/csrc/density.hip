@@ -406,17 +406,11 @@ constexpr int kCpRowsPerBlock = 2;                    // waves (= atom rows) per
 // LDS row stride of the staged gA (floats).
 __host__ __device__ constexpr int cp_mfma_stride(int C) { return C + 4; }
 
-// HB > 0: instead of writing dR, multiply it by the CP columns of the last radial layer on the
-// matrix cores: dh2[e, h] = sum_{l,c} dR[e, l, c] W[l C + c, h] for 16 HB hidden units, with
-// w_t = W^T (16 HB, 4C) row-major (M = edges, N = hidden units, K = (rank, channel): the t
-// registers, scaled to dR, are the A operand; D rows are edges 4q + r).
-template <int HB>
 __global__ __launch_bounds__(kCpRowsPerBlock * kWave) __attribute__((amdgpu_waves_per_eu(2))) void cp_density_bwd_mfma_kernel(
     const float* __restrict__ R, int ld_R, const float* __restrict__ env, const float* __restrict__ msg, int ld_msg,
     const int32_t* __restrict__ msg_row, const float* __restrict__ Y, int ld_Y, const int32_t* __restrict__ row_ptr,
     int64_t N, int M, int C, RankIn gA, float* __restrict__ dR, int ld_dR, float* __restrict__ dmsg, int ld_dmsg,
-    float* __restrict__ dY, int ld_dY, float* __restrict__ denv, const float* __restrict__ w_t,
-    float* __restrict__ dh2, int ld_dh2) {
+    float* __restrict__ dY, int ld_dY, float* __restrict__ denv) {
     extern __shared__ float lds[];
     const int lane = threadIdx.x & (kWave - 1);
     const int w = threadIdx.x / kWave;
@@ -466,9 +460,6 @@ __global__ __launch_bounds__(kCpRowsPerBlock * kWave) __attribute__((amdgpu_wave
         const float* Re = R + e * ld_R + own;
         const float* me = msg + mrow * ld_msg + own;
         v4f plo = z4, phi = z4;
-        v4f dacc[HB > 0 ? HB : 1];
-#pragma unroll
-        for (int hb = 0; hb < (HB > 0 ? HB : 1); ++hb) dacc[hb] = z4;
 #pragma unroll 1
         for (int cs = 0; cs < C; cs += kCpStep) {
             v4f r[2][4], m[2];
@@ -479,42 +470,17 @@ __global__ __launch_bounds__(kCpRowsPerBlock * kWave) __attribute__((amdgpu_wave
                 m[h] = ok ? ld4(me + cs + 16 * h) : z4;
             }
             v4f dm[2] = {z4, z4};
-            // W operands of (rank l, block h) pairs, one pair ahead of the MFMAs that use them
-            constexpr int NH = HB > 0 ? HB : 1;
-            const float* wrow = w_t + (int64_t)j * 4 * C + cs + own;
-            v4f wcur[NH], wnxt[NH];
-            if (HB > 0) {
-#pragma unroll
-                for (int hb = 0; hb < NH; ++hb) wcur[hb] = ld4(wrow + (int64_t)hb * 16 * 4 * C);
-            }
 #pragma unroll
             for (int l = 0; l < 4; ++l) {
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
-                    if (HB > 0 && (l < 3 || h == 0)) {
-                        const int ln = h == 1 ? l + 1 : l, hn = h == 1 ? 0 : 1;
-#pragma unroll
-                        for (int hb = 0; hb < NH; ++hb)
-                            wnxt[hb] = ld4(wrow + (int64_t)hb * 16 * 4 * C + ln * C + 16 * hn);
-                    }
                     v4f t = z4;
 #pragma unroll
                     for (int k = kRankChunk0[l]; k < kRankChunk1[l]; ++k) {
                         const float a = q < kChunkLen[k] ? sg[t_off + kChunkX0[k] * GS + cs + 16 * h] : 0.f;
                         t = mfma_16x16x4(a, yq[k], t);
                     }
-                    if (HB > 0) {
-                        const v4f g = (ev * m[h]) * t;
-#pragma unroll
-                        for (int rr = 0; rr < 4; ++rr) {
-#pragma unroll
-                            for (int hb = 0; hb < NH; ++hb) dacc[hb] = mfma_16x16x4(g[rr], wcur[hb][rr], dacc[hb]);
-                        }
-#pragma unroll
-                        for (int hb = 0; hb < NH; ++hb) wcur[hb] = wnxt[hb];
-                    } else if (ok && dR) {
-                        st4(dR + e * ld_dR + l * C + cs + own + 16 * h, (ev * m[h]) * t);
-                    }
+                    if (ok && dR) st4(dR + e * ld_dR + l * C + cs + own + 16 * h, (ev * m[h]) * t);
                     dm[h] += r[h][l] * t;
                 }
             }
@@ -548,14 +514,224 @@ __global__ __launch_bounds__(kCpRowsPerBlock * kWave) __attribute__((amdgpu_wave
         s += __shfl_xor(s, 16, kWave);
         s += __shfl_xor(s, 32, kWave);
         if (denv && ok && q == 0) denv[e] = s;
-        if (HB > 0) {
+    }
+}
+
+// ------------------------------------------------------------------ CP radial backward, shared W
+// The pooling backward of cp_density_bwd_mfma_kernel fused with the CP columns of the last radial
+// layer: instead of writing dR, multiply it by W on the matrix cores, dh2[e, h] = sum_{l,c}
+// dR[e, l, c] W[l C + c, h] for 16 HB hidden units, w_t = W^T (16 HB, 4C) row-major (M = edges,
+// N = hidden units, K = (rank, channel): the t registers scaled to dR are the A operand and D
+// rows are edges 4q + r). W is read from LDS:
+// persistent workgroups of kLdsWaves waves, each wave walking the 16-edge tiles of its own rows
+// (rows gw, gw + waves, ...), one tile per round; all waves of a workgroup step through the
+// 32-channel steps of their tiles in lockstep, and the step's slab of W^T (all hidden units x
+// 4 ranks x 32 channels, row stride 132 floats so that the float4 operand reads of 8
+// consecutive lanes hit distinct banks) is staged once per workgroup, the next slab being
+// fetched into registers while the current step computes. Every wave runs the workgroup's
+// largest round count, so every barrier is reached by all waves.
+constexpr int kLdsWaves = 8;
+constexpr int kSlabRS = 4 * kCpStep + 4;              // slab row stride (floats) per hidden unit
+
+template <int HB>
+__global__ __launch_bounds__(kLdsWaves * kWave) void cp_radial_bwd_lds_kernel(
+    const float* __restrict__ R, int ld_R, const float* __restrict__ env, const float* __restrict__ msg, int ld_msg,
+    const int32_t* __restrict__ msg_row, const float* __restrict__ Y, int ld_Y, const int32_t* __restrict__ row_ptr,
+    int64_t N, int M, int C, RankIn gA, float* __restrict__ dmsg, int ld_dmsg, float* __restrict__ dY, int ld_dY,
+    float* __restrict__ denv, const float* __restrict__ w_t, float* __restrict__ dh2, int ld_dh2) {
+    constexpr int H = 16 * HB;
+    extern __shared__ float lds[];
+    const int GS = cp_mfma_stride(C);
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int w = __builtin_amdgcn_readfirstlane(tid / kWave);
+    float* sW = lds;                                                  // H x kSlabRS
+    float* sg = lds + H * kSlabRS + (size_t)w * 20 * GS;             // this wave's gA row
+    int* s_cnt = reinterpret_cast<int*>(lds + H * kSlabRS + (size_t)kLdsWaves * 20 * GS);
+    const int64_t stride = (int64_t)gridDim.x * kLdsWaves;
+    const int64_t gw = (int64_t)blockIdx.x * kLdsWaves + w;
+    // rounds = the largest tile count over the workgroup's waves
+    int my_tiles = 0;
+    for (int64_t i = gw; i < N; i += stride) {
+        int64_t a, b;
+        row_range(row_ptr, i, M, a, b);
+        my_tiles += (int)((b - a + 15) / 16);
+    }
+    if (lane == 0) s_cnt[w] = my_tiles;
+    __syncthreads();
+    int rounds = 0;
+#pragma unroll
+    for (int k = 0; k < kLdsWaves; ++k) rounds = max(rounds, s_cnt[k]);
+    const int nsteps = C / kCpStep;
+    // W slab fetch: the slab is H x 4 ranks x 8 float4; thread tid owns float4 u * blockDim + tid
+    static_assert(HB * 16 * 4 * (kCpStep / 4) == HB * kLdsWaves * kWave, "slab float4s = HB per thread");
+    auto slab_load = [&](int cs, v4f (&buf)[HB]) {
+#pragma unroll
+        for (int u = 0; u < HB; ++u) {
+            const int f = u * kLdsWaves * kWave + tid;
+            const int h = f >> 5, l = (f >> 3) & 3, c4 = f & 7;
+            buf[u] = ld4(w_t + (int64_t)h * 4 * C + l * C + cs + 4 * c4);
+        }
+    };
+    auto slab_store = [&](const v4f (&buf)[HB]) {
+#pragma unroll
+        for (int u = 0; u < HB; ++u) {
+            const int f = u * kLdsWaves * kWave + tid;
+            const int h = f >> 5, l = (f >> 3) & 3, c4 = f & 7;
+            *reinterpret_cast<v4f*>(sW + h * kSlabRS + l * kCpStep + 4 * c4) = buf[u];
+        }
+    };
+    v4f wbuf[HB];
+    slab_load(0, wbuf);
+    const int j = lane & 15, q = lane >> 4;
+    const int nc4 = C >> 2;
+    const int t_off = q * GS + j, own = 4 * q;
+    const int plo_off = (j < 4 ? j : 0) * GS + own, phi_off = (4 + j) * GS + own;
+    const float sel0 = j == 0 ? 1.f : 0.f, sel1 = (j >= 1 && j < 4) ? 1.f : 0.f;
+    const float sel2 = j < 6 ? 1.f : 0.f, sel3 = j >= 6 ? 1.f : 0.f;
+    const v4f z4 = {0.f, 0.f, 0.f, 0.f};
+    int64_t row = gw - stride, t_next = 0, e_end = 0;   // tile cursor of this wave
+    for (int rd = 0; rd < rounds; ++rd) {
+        const bool active = rd < my_tiles;
+        int64_t t0 = 0, e1 = 0;
+        if (active) {
+            if (t_next >= e_end) {                        // next row with edges; stage its gA
+                int64_t a, b;
+                do {
+                    row += stride;
+                    row_range(row_ptr, row, M, a, b);
+                } while (b <= a);
+                t_next = a;
+                e_end = b;
+                for (int v0 = 0; v0 < 20 * nc4; v0 += 4 * kWave) {
+                    v4f buf[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int v = v0 + u * kWave + lane;
+                        if (v < 20 * nc4) {
+                            const int x = v / nc4, c4 = v - x * nc4;
+                            buf[u] = ld4(gA.at(row, x) + 4 * c4);
+                        }
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int v = v0 + u * kWave + lane;
+                        if (v < 20 * nc4) {
+                            const int x = v / nc4, c4 = v - x * nc4;
+                            *reinterpret_cast<v4f*>(sg + x * GS + 4 * c4) = buf[u];
+                        }
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
+            }
+            t0 = t_next;
+            e1 = e_end;
+            t_next += 16;
+        }
+        const int64_t e = t0 + j;
+        const bool ok = active && e < e1;
+        float yq[7];
+#pragma unroll
+        for (int k = 0; k < 7; ++k) yq[k] = (ok && q < kChunkLen[k]) ? Y[e * ld_Y + kChunkX0[k] + q] : 0.f;
+        const float ev = ok ? (env ? env[e] : 1.f) : 0.f;
+        const int64_t mrow = ok ? (msg_row ? (int64_t)msg_row[e] : e) : 0;
+        const float* Re = R + (ok ? e : 0) * ld_R + own;
+        const float* me = msg + mrow * ld_msg + own;
+        v4f plo = z4, phi = z4;
+        v4f dacc[HB];
+#pragma unroll
+        for (int hb = 0; hb < HB; ++hb) dacc[hb] = z4;
+        v4f rn[2][4], mn[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+#pragma unroll
+            for (int l = 0; l < 4; ++l) rn[h][l] = ok ? ld4(Re + l * C + 16 * h) : z4;
+            mn[h] = ok ? ld4(me + 16 * h) : z4;
+        }
+#pragma unroll 1
+        for (int st = 0; st < nsteps; ++st) {
+            const int cs = st * kCpStep;
+            __syncthreads();                              // every wave is done with the previous slab
+            slab_store(wbuf);
+            __syncthreads();
+            const bool more = st + 1 < nsteps || rd + 1 < rounds;
+            if (more) slab_load(st + 1 < nsteps ? cs + kCpStep : 0, wbuf);
+            v4f r[2][4], m[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                m[h] = mn[h];
+#pragma unroll
+                for (int l = 0; l < 4; ++l) r[h][l] = rn[h][l];
+            }
+            if (st + 1 < nsteps) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+#pragma unroll
+                    for (int l = 0; l < 4; ++l) rn[h][l] = ok ? ld4(Re + l * C + cs + kCpStep + 16 * h) : z4;
+                    mn[h] = ok ? ld4(me + cs + kCpStep + 16 * h) : z4;
+                }
+            }
+            if (active) {
+                v4f dm[2] = {z4, z4};
+#pragma unroll
+                for (int l = 0; l < 4; ++l) {
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        v4f t = z4;
+#pragma unroll
+                        for (int k = kRankChunk0[l]; k < kRankChunk1[l]; ++k) {
+                            const float a = q < kChunkLen[k] ? sg[t_off + kChunkX0[k] * GS + cs + 16 * h] : 0.f;
+                            t = mfma_16x16x4(a, yq[k], t);
+                        }
+                        const v4f g = (ev * m[h]) * t;
+                        const float* wl = sW + j * kSlabRS + l * kCpStep + 16 * h + own;
+#pragma unroll
+                        for (int hb = 0; hb < HB; ++hb) {
+                            const v4f wv = *reinterpret_cast<const v4f*>(wl + hb * 16 * kSlabRS);
+#pragma unroll
+                            for (int rr = 0; rr < 4; ++rr) dacc[hb] = mfma_16x16x4(g[rr], wv[rr], dacc[hb]);
+                        }
+                        dm[h] += r[h][l] * t;
+                    }
+                }
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    if (ok && dmsg) st4(dmsg + e * ld_dmsg + cs + own + 16 * h, ev * dm[h]);
+                    const v4f alo = *reinterpret_cast<const v4f*>(sg + plo_off + cs + 16 * h);
+                    const v4f ahi = *reinterpret_cast<const v4f*>(sg + phi_off + cs + 16 * h);
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) {
+                        const float mm = m[h][rr];
+                        plo = mfma_16x16x4(sel0 * alo[rr], r[h][0][rr] * mm, plo);
+                        phi = mfma_16x16x4(sel2 * ahi[rr], r[h][2][rr] * mm, phi);
+                        plo = mfma_16x16x4(sel1 * alo[rr], r[h][1][rr] * mm, plo);
+                        phi = mfma_16x16x4(sel3 * ahi[rr], r[h][3][rr] * mm, phi);
+                    }
+                }
+            }
+        }
+        if (active) {
+            // lane (j, q) holds P[x, e] for x = 4 + 4q + r (hi) and, in lanes q == 0, x = r (lo)
+            float s = 0.f;
+            if (ok) {
+                const v4f yhi = ld4(Y + e * ld_Y + 4 + 4 * q);
+                s = yhi[0] * phi[0] + yhi[1] * phi[1] + yhi[2] * phi[2] + yhi[3] * phi[3];
+                if (dY) st4(dY + e * ld_dY + 4 + 4 * q, ev * phi);
+                if (q == 0) {
+                    const v4f ylo = ld4(Y + e * ld_Y);
+                    s += ylo[0] * plo[0] + ylo[1] * plo[1] + ylo[2] * plo[2] + ylo[3] * plo[3];
+                    if (dY) st4(dY + e * ld_dY, ev * plo);
+                }
+            }
+            s += __shfl_xor(s, 16, kWave);
+            s += __shfl_xor(s, 32, kWave);
+            if (denv && ok && q == 0) denv[e] = s;
             // dacc[hb] register r of lane (j, q): edge t0 + 4q + r, hidden unit 16 hb + j
 #pragma unroll
             for (int rr = 0; rr < 4; ++rr) {
                 const int64_t er = t0 + 4 * q + rr;
                 if (er < e1) {
 #pragma unroll
-                    for (int hb = 0; hb < (HB > 0 ? HB : 1); ++hb) dh2[er * ld_dh2 + 16 * hb + j] = dacc[hb][rr];
+                    for (int hb = 0; hb < HB; ++hb) dh2[er * ld_dh2 + 16 * hb + j] = dacc[hb][rr];
                 }
             }
         }
@@ -796,10 +972,9 @@ extern "C" int face_cp_density_bwd(const float* R, int32_t ld_R, const float* en
         // one atom row per wave, kCpRowsPerBlock rows per workgroup, each with its gA slice in LDS
         const size_t lds = (size_t)kCpRowsPerBlock * 20 * cp_mfma_stride(C) * sizeof(float);
         if (lds > 65536) return FACE_ERR_UNSUPPORTED;
-        hipLaunchKernelGGL(cp_density_bwd_mfma_kernel<0>, dim3((unsigned)((N + kCpRowsPerBlock - 1) / kCpRowsPerBlock)),
+        hipLaunchKernelGGL(cp_density_bwd_mfma_kernel, dim3((unsigned)((N + kCpRowsPerBlock - 1) / kCpRowsPerBlock)),
                            dim3(kCpRowsPerBlock * kWave), lds, (hipStream_t)stream, R, ld_R, env, msg, ld_msg, msg_row,
-                           Y, ld_Y, row_ptr, N, M, C, gA, dR, ld_dR, dmsg, ld_dmsg, dY, ld_dY, denv, nullptr, nullptr,
-                           0);
+                           Y, ld_Y, row_ptr, N, M, C, gA, dR, ld_dR, dmsg, ld_dmsg, dY, ld_dY, denv);
         FACE_LAUNCH_CHECK();
         return 0;
     }
@@ -828,13 +1003,28 @@ extern "C" int face_cp_radial_bwd(const float* R, int32_t ld_R, const float* env
     if (!R || !msg || !Y || !rank_in(gA_ranks, atom_stride, x_stride, 20, gA)) return FACE_ERR_ARG;
     if (!mfma_layout_ok(R, ld_R, msg, ld_msg, Y, ld_Y, C, gA, nullptr, 0, dmsg, ld_dmsg, dY, ld_dY))
         return FACE_ERR_UNSUPPORTED;
-    const size_t lds = (size_t)kCpRowsPerBlock * 20 * cp_mfma_stride(C) * sizeof(float);
-    if (lds > 65536) return FACE_ERR_UNSUPPORTED;
-    const dim3 grid((unsigned)((N + kCpRowsPerBlock - 1) / kCpRowsPerBlock)), block(kCpRowsPerBlock * kWave);
+    // persistent workgroups, one per CU: W slab + one gA row per wave + per-wave tile counts
+    const size_t lds = ((size_t)H * kSlabRS + (size_t)kLdsWaves * 20 * cp_mfma_stride(C) + kLdsWaves) * sizeof(float);
+    if ((int64_t)lds > max_lds_bytes()) return FACE_ERR_UNSUPPORTED;
+    static int n_cu = 0;
+    if (n_cu <= 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
+            n_cu = 256;
+    }
+    const int64_t waves = N < (int64_t)n_cu * kLdsWaves ? N : (int64_t)n_cu * kLdsWaves;
+    const dim3 grid((unsigned)((waves + kLdsWaves - 1) / kLdsWaves)), block(kLdsWaves * kWave);
     const hipStream_t st = (hipStream_t)stream;
-#define FACE_CPR(HB_)                                                                                           \
-    hipLaunchKernelGGL(cp_density_bwd_mfma_kernel<HB_>, grid, block, lds, st, R, ld_R, env, msg, ld_msg, msg_row, \
-                       Y, ld_Y, row_ptr, N, M, C, gA, nullptr, 0, dmsg, ld_dmsg, dY, ld_dY, denv, w_t, dh2, ld_dh2)
+#define FACE_CPR(HB_)                                                                                            \
+    do {                                                                                                         \
+        auto kern = cp_radial_bwd_lds_kernel<HB_>;                                                               \
+        if (lds > 65536 &&                                                                                       \
+            hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) \
+            return FACE_ERR_UNSUPPORTED;                                                                         \
+        hipLaunchKernelGGL(kern, grid, block, lds, st, R, ld_R, env, msg, ld_msg, msg_row, Y, ld_Y, row_ptr, N, M, C, \
+                           gA, dmsg, ld_dmsg, dY, ld_dY, denv, w_t, dh2, ld_dh2);                                \
+    } while (0)
     switch (H / 16) {
         case 1: FACE_CPR(1); break;
         case 2: FACE_CPR(2); break;
