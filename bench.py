@@ -30,7 +30,7 @@ METRIC = "atom-steps/s (E+F, fp32) at 864 & 24k atoms; density-kernel HBM GB/s"
 HBM_PEAK_GBS = 8000.0
 TIMED = ["density_fwd20", "density_bwd20", "cp_fwd", "cp_bwd", "transport_fwd", "transport_bwd", "dir_fwd",
          "dir_bwd", "node_fwd", "node_bwd", "edge_fwd", "edge_bwd", "force_scatter", "gather_bwd", "radial_fwd",
-         "radial_bwd"]
+         "radial_bwd", "radial_head"]
 
 
 def log(*a):
@@ -71,6 +71,8 @@ def algorithmic_bytes(label, g, kw):
         return 4 * E * (nb + 2 + B + (H if kw.get("cp") else 0))
     if label == "radial_bwd":           # + upstream phi (and h2) gradients; d rb, d env out
         return 4 * E * (nb + 2 + B + (H if kw.get("cp") else 0) + nb + 1)
+    if label == "radial_head":          # h2 in, R (E, 4C) out
+        return 4 * E * (H + 4 * C)
     return None
 
 

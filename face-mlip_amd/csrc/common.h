@@ -48,4 +48,19 @@ __device__ __forceinline__ v4f mfma_16x16x4(float a, float b, v4f c) {
 __device__ __forceinline__ v4f ld4(const float* p) { return *reinterpret_cast<const v4f*>(p); }
 __device__ __forceinline__ void st4(float* p, v4f v) { *reinterpret_cast<v4f*>(p) = v; }
 
+// Attribute of the current device, cached per device and attribute slot (fallback if the
+// query fails).
+template <int Slot>
+static inline int device_attr(hipDeviceAttribute_t a, int fallback) {
+    constexpr int kMaxDev = 64;
+    static int cache[kMaxDev];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return fallback;
+    int& v = cache[dev];
+    if (v <= 0 && (hipDeviceGetAttribute(&v, a, dev) != hipSuccess || v <= 0)) v = fallback;
+    return v;
+}
+static inline int device_cu_count() { return device_attr<0>(hipDeviceAttributeMultiprocessorCount, 256); }
+static inline int device_max_lds() { return device_attr<1>(hipDeviceAttributeMaxSharedMemoryPerBlock, 65536); }
+
 }  // namespace face

@@ -739,16 +739,6 @@ __global__ __launch_bounds__(kLdsWaves * kWave) void cp_radial_bwd_lds_kernel(
 }
 
 // ------------------------------------------------------------------ launch helpers
-static int max_lds_bytes() {
-    static int v = -1;
-    if (v < 0) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess)
-            v = 65536;
-    }
-    return v;
-}
 
 template <int NX>
 static int launch_fwd_nx(int cpt, dim3 grid, size_t lds, hipStream_t st, const float* phi, int ld_phi,
@@ -776,7 +766,7 @@ static int launch_bwd3(int glog, int nthr, int64_t N, hipStream_t st, const floa
                        int ld_dmsg, float* dY, int ld_dY) {
     constexpr int KSP = (KS + 3) & ~3;
     const size_t lds = (size_t)NX * B * (1 << glog) * KSP * sizeof(float);
-    if ((int64_t)lds > max_lds_bytes()) return FACE_ERR_UNSUPPORTED;
+    if ((int64_t)lds > device_max_lds()) return FACE_ERR_UNSUPPORTED;
     auto kern = density_bwd_kernel<NX, B, KS>;
     if (lds > 65536 &&
         hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
@@ -1005,14 +995,8 @@ extern "C" int face_cp_radial_bwd(const float* R, int32_t ld_R, const float* env
         return FACE_ERR_UNSUPPORTED;
     // persistent workgroups, one per CU: W slab + one gA row per wave + per-wave tile counts
     const size_t lds = ((size_t)H * kSlabRS + (size_t)kLdsWaves * 20 * cp_mfma_stride(C) + kLdsWaves) * sizeof(float);
-    if ((int64_t)lds > max_lds_bytes()) return FACE_ERR_UNSUPPORTED;
-    static int n_cu = 0;
-    if (n_cu <= 0) {
-        int dev = 0;
-        if (hipGetDevice(&dev) != hipSuccess ||
-            hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n_cu <= 0)
-            n_cu = 256;
-    }
+    if ((int64_t)lds > device_max_lds()) return FACE_ERR_UNSUPPORTED;
+    const int n_cu = device_cu_count();
     const int64_t waves = N < (int64_t)n_cu * kLdsWaves ? N : (int64_t)n_cu * kLdsWaves;
     const dim3 grid((unsigned)((waves + kLdsWaves - 1) / kLdsWaves)), block(kLdsWaves * kWave);
     const hipStream_t st = (hipStream_t)stream;

@@ -22,7 +22,8 @@ runs:
 Supported configuration: factor=True (cp on or off), transport/eqmsg on or off, n_passes >= 1,
 norm="layer", terms=(), radial_hidden in {16, 32, 48, 64}, training toggles at their defaults;
 evaluation mode and first-order forces (create_graph=False), which is what the reference's fused
-kernels support (face/kernels.py:10-11).
+kernels support (face/kernels.py:10-11). Parameters enter the forward as constants (frozen()):
+energies and forces differentiate through positions only.
 """
 import math
 
@@ -76,11 +77,24 @@ def unit_parameterise(module):
     return module
 
 
-def weight(mod):
-    """Effective (weight, bias) of an nn.Linear or UnitLinear."""
-    if isinstance(mod, UnitLinear):
-        return mod.weight * mod.alpha, mod.bias
-    return mod.weight, mod.bias
+def _key(*ts):
+    return tuple((t._version, t.data_ptr(), t.device) for t in ts if t is not None)
+
+
+def frozen(mod):
+    """Effective (weight, bias) of an nn.Linear or UnitLinear as constants of the evaluation
+    graph: detached, the UnitLinear factor applied once and cached until a parameter is
+    changed in place (version counter) or replaced (storage pointer). Parameters therefore
+    take no gradient on this path, and a step reads no per-call weight-scaling kernels."""
+    w, b = mod.weight, mod.bias
+    key = _key(w, b)
+    c = mod.__dict__.get("_frozen")
+    if c is None or c[0] != key:
+        with torch.no_grad():
+            W = (w * mod.alpha) if isinstance(mod, UnitLinear) else w
+            c = (key, W.detach(), None if b is None else b.detach())
+        mod.__dict__["_frozen"] = c
+    return c[1], c[2]
 
 
 def mlp(sizes):
@@ -90,9 +104,10 @@ def mlp(sizes):
     return nn.Sequential(*layers[:-1])
 
 
-def run_mlp(seq, x):
+def run_frozen(seq, x):
+    """An mlp() stack (Linear / SiLU) on frozen weights."""
     for m in seq:
-        x = m(x)
+        x = F.silu(x) if isinstance(m, nn.SiLU) else F.linear(x, *frozen(m))
     return x
 
 
@@ -166,45 +181,63 @@ class FactorBlock(nn.Module):
         B, C, Kd = self.B, self.C, self.K
         # hidden layers and phi columns of the radial MLP in one HIP kernel; the CP columns of the
         # last layer are a GEMM on its h2 output
-        Wi, bi = weight(self.rad_in)
-        W1, b1 = weight(self.radial[0])
-        W2, b2 = weight(self.radial[2])
-        phi, h2 = ops.radial_mlp(rb, env, zp, Wi.detach(), bi.detach(), self.pair.weight.detach(), W1.detach(),
-                                 b1.detach(), W2[:B].detach(), b2[:B].detach(), self.cp)          # (E, B), (E, H)
-        msg_n = self.msg(h)                                                      # (N, K)
+        Wi, bi = frozen(self.rad_in)
+        W1, b1 = frozen(self.radial[0])
+        W2, b2 = frozen(self.radial[2])
+        phi, h2 = ops.radial_mlp(rb, env, zp, Wi, bi, self.pair.weight.detach(), W1, b1, W2[:B], b2[:B],
+                                 self.cp)                                        # (E, B), (E, H)
+        msg_n = F.linear(h, *frozen(self.msg))                                   # (N, K)
         if self.directional:
             if self.eq_in:
                 src1, src2 = eq                                                  # (3,N,C), (6,N,C)
             else:
                 src1 = torch.cat([S[1] for S in sets], -1)
                 src2 = torch.cat([S[2] for S in sets], -1)
-            Vb = self.pvt(src1)                                                  # (3, N, nt*Kd)
-            Mb = self.pmt(src2)                                                  # (6, N, nt*Kd)
+            Vb = F.linear(src1, frozen(self.pvt)[0])                             # (3, N, nt*Kd)
+            Mb = F.linear(src2, frozen(self.pmt)[0])                             # (6, N, nt*Kd)
             d, D1, D2 = ops.dir_transport(Vb, Mb, phi, Y, g, Kd, self.transport)   # (E, 4Kd), transport sums
             # gather(msg(h)) + dir_mix(d): the bias joins the node table before the gather and the
             # dir_mix GEMM accumulates onto the gathered rows in its epilogue
-            Wd, bd = weight(self.dir_mix)
+            Wd, bd = frozen(self.dir_mix)
             mj = ops.gather_neighbour(msg_n + bd, g).addmm_(d, Wd.t())
             gathered = False
         else:
             mj, gathered = msg_n, True
-        s = self.elem_scale(zidx).view(N, 4, C) / avg_nb
+        s = self._scale_table(avg_nb)[zidx].view(N, 4, C)                       # elem_scale / avg_nb per atom
         if self.cp:
             # R = h2 W2[B:]^T + b2[B:] (E, 4C) feeds the pooling (envelope applied in-kernel); on the
             # matrix-core shapes the pooling backward also applies W2[B:] and returns d h2 directly
             if C % 32 == 0 and h2.shape[1] % 16 == 0 and h2.shape[1] <= 64:
-                Af = ops.cp_radial_density(h2, W2[B:].detach(), b2[B:].detach(), env, mj, Y, g, gathered)
+                Af = ops.cp_radial_density(h2, W2[B:], b2[B:], env, mj, Y, g, gathered)
             else:
                 Af = ops.cp_density(F.linear(h2, W2[B:], b2[B:]), env, mj, Y, g, gathered)   # 4 x (k_l, N, C)
         else:
             Af = ops.density(phi, mj, Y, g, 20, gathered)                         # 4 x (k_l, N, B*K)
-        A = [self.mix[l](Af[l]) * s[None, :, l, :] for l in range(4)]             # 4 x (k_l, N, C)
-        if self.transport:
-            # D1/D2 are the raw sums; the reference's 1/avg_nb (face/model.py:522) and its avg_nb
-            # factor (:532-533) cancel through the linear tmix, leaving s = elem_scale / avg_nb
-            A[1] = A[1] + self.tmix1(D1) * s[None, :, 1, :]
-            A[2] = A[2] + self.tmix2(D2) * s[None, :, 2, :]
+        # A_l = (mix_l(Af_l) [+ tmix_l(D_l)]) * s: D1/D2 are the raw transport sums; the reference's
+        # 1/avg_nb (face/model.py:522) and its avg_nb factor (:532-533) cancel through the linear tmix,
+        # leaving the common factor s = elem_scale / avg_nb, so tmix accumulates into the mix GEMM's
+        # output in place and one scaling pass per rank remains
+        tm = {1: (self.tmix1, D1), 2: (self.tmix2, D2)} if self.transport else {}
+        A = []
+        for l in range(4):
+            x = Af[l]
+            y = x.reshape(-1, x.shape[-1]) @ frozen(self.mix[l])[0].t()
+            if l in tm:
+                mod, D = tm[l]
+                y.addmm_(D.reshape(-1, D.shape[-1]), frozen(mod)[0].t())
+            A.append(y.view(x.shape[0], N, C) * s[None, :, l, :])                 # (k_l, N, C)
         return A
+
+    def _scale_table(self, avg_nb):
+        """elem_scale / avg_nb per element (n_elem, 4C), cached like the frozen weights."""
+        w = self.elem_scale.weight
+        key = _key(w, avg_nb)
+        c = self.__dict__.get("_stab")
+        if c is None or c[0] != key:
+            with torch.no_grad():
+                c = (key, (w / avg_nb).detach())
+            self.__dict__["_stab"] = c
+        return c[1]
 
     # ------------------------------------------------------------------ invariants + readout
     def forward(self, h, rb, Y, env, zp, zidx, avg_nb, sets, eq, g):
@@ -213,7 +246,7 @@ class FactorBlock(nn.Module):
         allsets = sets + [A]
         ys = []
         for l in range(4):
-            W, _ = weight(self.proj[l])
+            W, _ = frozen(self.proj[l])
             if l == 0:
                 W = W[:C]                                                         # only P0 is used
             elif l == 3:
@@ -227,18 +260,19 @@ class FactorBlock(nn.Module):
                 y = x2 @ Ws.t() if y is None else y.addmm_(x2, Ws.t())
             ys.append(y.view(S[l].shape[0], S[l].shape[1], -1))                   # (k_l, N, 3C | C | 2C)
         if self.eq_out:
-            feats, V, Ms = ops.node_features(ys[0], ys[1], ys[2], ys[3], self.vpath, self.mpath, True, C)
+            feats, V, Ms = ops.node_features(ys[0], ys[1], ys[2], ys[3], self.vpath.detach(), self.mpath.detach(),
+                                             True, C)
         else:
             feats, V, Ms = ops.node_features(ys[0], ys[1], ys[2], ys[3], None, None, False, C)
-        inv = self.norm(feats)
-        W0, b0 = weight(self.out[0])
-        # out[0] on cat([inv, h, 0 (4)]) as two accumulating GEMMs (no concatenated copy)
         nf = self.N_INV * C
+        inv = F.layer_norm(feats, (nf,), self.norm.weight.detach(), self.norm.bias.detach(), self.norm.eps)
+        W0, b0 = frozen(self.out[0])
+        # out[0] on cat([inv, h, 0 (4)]) as two accumulating GEMMs (no concatenated copy)
         z = F.linear(inv, W0[:, :nf], b0).addmm_(h, W0[:, nf:nf + C].t())
-        o = run_mlp(self.out[2:], F.silu(z))
+        o = run_frozen(self.out[2:], F.silu(z))
         eq_new = None
         if self.eq_out:
-            gv, gm = self.gate(inv).chunk(2, dim=-1)
+            gv, gm = F.linear(inv, *frozen(self.gate)).chunk(2, dim=-1)
             eq_new = (V * gv[None], Ms * gm[None])                                # (3,N,C), (6,N,C)
         return o[:, :1], h + o[:, 1:], A, eq_new
 
@@ -305,7 +339,7 @@ class FACE(nn.Module):
         if zp is None:
             zp = (zidx[graph.recv.long()] * len(self.E0) + zidx[graph.col.long()]).to(torch.int32)
             graph.cache[zkey] = zp
-        h = self.embed(zidx)
+        h = F.embedding(zidx, self.embed.weight.detach())
         e_at = self.E0[zidx].clone()
         sets, eq = [], None
         for blk in self.blocks:

@@ -371,7 +371,7 @@ class CPRadialDensity(torch.autograd.Function):
     def forward(ctx, h2, w_cp, b_cp, env, msg, Y, graph, gathered):
         _lib.require_gpu(h2, env, msg, Y)
         C = msg.shape[1]
-        R = torch.addmm(b_cp.detach(), h2.detach(), w_cp.detach().t())                        # (E, 4C)
+        R = radial_head(h2.detach(), w_cp.detach(), b_cp.detach())                            # (E, 4C)
         env_ = env.contiguous().float()
         msg_, ld_msg = _rows(msg, C)
         Y_, ld_Y = _rows(Y, 20)
@@ -415,6 +415,24 @@ class CPRadialDensity(torch.autograd.Function):
 
 def cp_radial_density(h2, w_cp, b_cp, env, msg, Y, graph, gathered=False):
     return CPRadialDensity.apply(h2, w_cp, b_cp, env, msg, Y, graph, gathered)
+
+
+def _aligned16(t):
+    t = t.contiguous().float()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def radial_head(h2, w, b):
+    """R (E, F) = h2 w^T + b for the CP columns of the last radial layer (no gradient)."""
+    _lib.require_gpu(h2, w, b)
+    E, H = h2.shape
+    F_ = w.shape[0]
+    h2_ = h2 if (h2.stride(1) == 1 and h2.stride(0) % 4 == 0 and h2.data_ptr() % 16 == 0) else _aligned16(h2)
+    w_, b_ = _aligned16(w), _aligned16(b)
+    R = torch.empty(E, F_, device=h2.device)
+    call("face_radial_head_fwd", ptr(h2_), h2_.stride(0), E, H, ptr(w_), ptr(b_), F_, ptr(R), F_,
+         _lib.stream_of(R), label="radial_head")
+    return R
 
 
 # ----------------------------------------------------------------------------- radial MLP

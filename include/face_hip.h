@@ -216,6 +216,14 @@ int face_radial_bwd(const float* rb, int32_t ld_rb, int32_t n_basis, const int32
                     const float* gh2, int32_t ld_gh2, const float* gphi, int32_t ld_gphi, float* grb, int32_t ld_grb,
                     float* genv, void* stream);
 
+/* CP radial head, the 4C CP columns of the radial MLP's last layer (face/model.py:469 with the
+ * radial(...).split at :496-497): R (E, ld_R) = h2 (E, ld_h2) w^T + b, w (F, H) row-major,
+ * b (F). H in {16, 32, 48, 64}, F a multiple of 16; h2, w, b, R 16-byte aligned and ld_h2,
+ * ld_R multiples of 4 (else FACE_ERR_UNSUPPORTED). Replaces the GEMM the reference runs for
+ * the last nn.Linear of the radial MLP. */
+int face_radial_head_fwd(const float* h2, int32_t ld_h2, int64_t E, int32_t H, const float* w, const float* b,
+                         int32_t F, float* R, int32_t ld_R, void* stream);
+
 /* ---------------------------------------------------------------- directional edge features
  * Node tables of Kd channels: V element (component a, atom n, channel k) at
  * V[a*v_sq + n*v_sn + k] (3 components), M likewise (6 components, sym storage).

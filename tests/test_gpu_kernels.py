@@ -358,7 +358,30 @@ def test_dir_transport_and_gradients(Kd, B, transport):
 
 
 # ----------------------------------------------------------------------------- radial MLP
-@pytest.mark.parametrize("E,nb,H,B,n_pair,want_h2", [(20000, 8, 64, 16, 9, True), (20000, 8, 64, 16, 1, False),
+@pytest.mark.parametrize("E,H,F,offset", [(100000, 64, 640, 0), (1001, 16, 128, 0), (37, 48, 640, 0),
+                                          (5, 32, 1024, 0), (300, 64, 1280, 0), (4099, 64, 640, 4), (0, 64, 640, 0)])
+def test_radial_head_matches_torch(E, H, F, offset):
+    """R = h2 w^T + b for the CP columns of the last radial layer vs torch fp64: whole-LDS weight
+    images with the rotated (H = 64, F = 640) and padded row layouts, the feature-chunked grid
+    (H = 64, F = 1280), ragged edge tiles and a row stride / base offset that is not the width."""
+    from face_amd import ops
+    say("radial head", E, H, F, offset)
+    torch.manual_seed(E + F)
+    base = torch.randn(E * (H + offset) + offset, device=DEV)
+    h2 = base[offset:offset + E * (H + offset)].view(E, H + offset)[:, :H] if E else torch.empty(0, H, device=DEV)
+    w = torch.randn(F, H, device=DEV) / H ** 0.5
+    b = torch.randn(F, device=DEV)
+    R = ops.radial_head(h2, w, b)
+    assert R.shape == (E, F)
+    if E == 0:
+        return
+    ref = h2.double() @ w.double().T + b.double()
+    err = rel(R, ref)
+    say("   err", err)
+    assert err < 1e-5, err
+
+
+@pytest.mark.parametrize("E,nb,H,B,n_pair,want_h2",[(20000, 8, 64, 16, 9, True), (20000, 8, 64, 16, 1, False),
                                                       (1001, 8, 16, 8, 9, False), (37, 8, 32, 20, 4, True),
                                                       (5, 12, 48, 32, 9, True), (0, 8, 64, 16, 9, True)])
 def test_radial_mlp_matches_torch(E, nb, H, B, n_pair, want_h2):
