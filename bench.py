@@ -30,7 +30,7 @@ METRIC = "atom-steps/s (E+F, fp32) at 864 & 24k atoms; density-kernel HBM GB/s"
 HBM_PEAK_GBS = 8000.0
 TIMED = ["density_fwd20", "density_bwd20", "cp_fwd", "cp_bwd", "transport_fwd", "transport_bwd", "dir_fwd",
          "dir_bwd", "node_fwd", "node_bwd", "edge_fwd", "edge_bwd", "force_scatter", "gather_bwd", "radial_fwd",
-         "radial_bwd", "radial_head"]
+         "radial_bwd", "radial_head", "edge_msg_fwd", "edge_msg_bwd"]
 
 
 def log(*a):
@@ -73,6 +73,11 @@ def algorithmic_bytes(label, g, kw):
         return 4 * E * (nb + 2 + B + (H if kw.get("cp") else 0) + nb + 1)
     if label == "radial_head":          # h2 in, R (E, 4C) out
         return 4 * E * (H + 4 * C)
+    Kd4 = 4 * kw["K_dir"]
+    if label == "edge_msg_fwd":         # d, col in; message (E, K) out (the gathered node table: N rows)
+        return 4 * (E * (Kd4 + 1 + K) + N * K)
+    if label == "edge_msg_bwd":         # upstream (E, K), rev in; d d (E, 4Kd) and the table gradient out
+        return 4 * (E * (K + 1 + Kd4) + N * K)
     return None
 
 

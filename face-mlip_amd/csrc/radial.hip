@@ -2,8 +2,8 @@
 //   u1  = rb W_in^T + b_in + pair_tab[pair]     hid = silu(u1)        (E, H)
 //   u2  = hid W1^T + b1                         h2  = silu(u2)        (E, H)
 //   phi = (h2 W_phi^T + b_phi) * env                                  (E, B)
-// rb already carries the envelope (face/model.py:676). The last layer's 4C CP columns are a
-// plain GEMM on h2 outside this kernel.
+// rb already carries the envelope (face/model.py:676). The last layer's 4C CP columns are an
+// edge-linear launch on h2 (linear.hip).
 //
 // Work: one wave per tile of 16 edges, all layers in the transposed orientation (features x
 // edges): each layer is D = W . X^T with M = output features, N = edges, K = input features,
@@ -296,115 +296,6 @@ static bool radial_args_ok(const float* rb, int ld_rb, int nbasis, const int32_t
     return W.w_in && W.b_in && W.pair_tab && W.w1 && W.b1 && W.w_phi && W.b_phi;
 }
 
-// ------------------------------------------------------------------ CP radial head
-// R = h2 W^T + b (E, F): the F = 4C CP columns of the last radial layer (face/model.py:469,
-// :496-497). The (F, H) weight block sits whole in LDS (160 KB at F = 640, H = 64) as the A
-// operand; each wave loads the h2 rows of 16 BB edges once as B operands (K index q of
-// instruction r of chunk hb = hidden unit 16 hb + 4q + r) and walks all feature blocks, so R
-// streams out at the write rate: D = W . h2^T holds feature 4q + r of edge j in register r of
-// lane j + 16q, one float4 store of R[e][f .. f + 3] per lane and block.
-// LDS image: row f at f * S; with S = H (H = 32, 64) the float4 chunk c of row f is stored at
-// chunk (c + f) mod H/4, otherwise S = H + 4: both keep the 16 rows read by one instruction on
-// distinct banks.
-constexpr int kHeadWaves = 16;
-
-__device__ __forceinline__ int head_off(int f, int c4, int S, int nch, bool rot) {
-    return f * S + 4 * (rot ? ((c4 + f) & (nch - 1)) : c4);
-}
-
-template <int HB, int BB, int FB>
-__global__ __launch_bounds__(kHeadWaves * kWave) void radial_head_kernel(
-    const float* __restrict__ h2, int ld_h2, int64_t E, const float* __restrict__ w, const float* __restrict__ b,
-    int F, int f_chunk, int S, int rot, float* __restrict__ R, int ld_R) {
-    constexpr int H = 16 * HB, NCH = H / 4;
-    extern __shared__ float sW[];
-    const int tid = threadIdx.x, lane = tid & (kWave - 1);
-    const int f_beg = blockIdx.y * f_chunk;
-    const int nf = min(f_chunk, F - f_beg);                           // a multiple of 16
-    const bool rt = rot != 0;
-    for (int v0 = 0; v0 < nf * NCH; v0 += 4 * (int)blockDim.x) {
-        v4f buf[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int v = v0 + u * (int)blockDim.x + tid;
-            if (v < nf * NCH) buf[u] = ld4(w + (int64_t)(f_beg + v / NCH) * H + 4 * (v % NCH));
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int v = v0 + u * (int)blockDim.x + tid;
-            if (v < nf * NCH) st4(sW + head_off(v / NCH, v % NCH, S, NCH, rt), buf[u]);
-        }
-    }
-    __syncthreads();
-    const int j = lane & 15, q = lane >> 4;
-    const int wv_id = __builtin_amdgcn_readfirstlane(tid / kWave);
-    const int64_t ntile = (E + 16 * BB - 1) / (16 * BB);
-    const int64_t stride = (int64_t)gridDim.x * kHeadWaves;
-    const v4f z4 = {0.f, 0.f, 0.f, 0.f};
-    for (int64_t t = (int64_t)blockIdx.x * kHeadWaves + wv_id; t < ntile; t += stride) {
-        const int64_t e0 = t * 16 * BB;
-        v4f hv[BB][HB];
-#pragma unroll
-        for (int bb = 0; bb < BB; ++bb) {
-            const int64_t e = e0 + 16 * bb + j;
-#pragma unroll
-            for (int hb = 0; hb < HB; ++hb) hv[bb][hb] = e < E ? ld4(h2 + e * ld_h2 + 16 * hb + 4 * q) : z4;
-        }
-#pragma unroll 1
-        for (int fb0 = 0; fb0 < nf; fb0 += 16 * FB) {
-            v4f acc[FB][BB];
-#pragma unroll
-            for (int fb = 0; fb < FB; ++fb)
-#pragma unroll
-                for (int bb = 0; bb < BB; ++bb) acc[fb][bb] = z4;
-#pragma unroll
-            for (int hb = 0; hb < HB; ++hb) {
-                v4f wa[FB];
-#pragma unroll
-                for (int fb = 0; fb < FB; ++fb)
-                    wa[fb] = fb0 + 16 * fb < nf
-                                 ? *reinterpret_cast<const v4f*>(sW + head_off(fb0 + 16 * fb + j, 4 * hb + q, S, NCH, rt))
-                                 : z4;
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-#pragma unroll
-                    for (int fb = 0; fb < FB; ++fb)
-#pragma unroll
-                        for (int bb = 0; bb < BB; ++bb) acc[fb][bb] = mfma_16x16x4(wa[fb][r], hv[bb][hb][r], acc[fb][bb]);
-            }
-#pragma unroll
-            for (int fb = 0; fb < FB; ++fb) {
-                if (fb0 + 16 * fb < nf) {
-                    const int f = f_beg + fb0 + 16 * fb + 4 * q;
-                    const v4f bias = ld4(b + f);
-#pragma unroll
-                    for (int bb = 0; bb < BB; ++bb) {
-                        const int64_t e = e0 + 16 * bb + j;
-                        if (e < E) st4(R + e * ld_R + f, acc[fb][bb] + bias);
-                    }
-                }
-            }
-        }
-    }
-}
-
-// Row stride, swizzle and feature chunk of the radial-head LDS image for the LDS budget.
-static bool head_layout(int F, int H, int max_lds, int& S, int& rot, int& f_chunk) {
-    const int nch = H / 4;
-    if ((int64_t)F * (H + 4) * 4 <= max_lds) {
-        S = H + 4, rot = 0, f_chunk = F;
-    } else if ((nch & (nch - 1)) == 0 && nch >= 8 && (int64_t)F * H * 4 <= max_lds) {
-        S = H, rot = 1, f_chunk = F;
-    } else {
-        S = H + 4, rot = 0;
-        const int rows = (max_lds / (4 * S)) / 16 * 16;
-        if (rows < 16) return false;
-        const int nchunk = (F + rows - 1) / rows;
-        f_chunk = ((F / 16 + nchunk - 1) / nchunk) * 16;
-    }
-    return true;
-}
-
 }  // namespace face
 
 using namespace face;
@@ -465,44 +356,6 @@ extern "C" int face_radial_bwd(const float* rb, int32_t ld_rb, int32_t n_basis, 
     const int tpw = radial_tiles_per_wave(E);
     FACE_RADIAL_DISPATCH(radial_bwd_kernel, rb, ld_rb, n_basis, pair, env, E, W, n_pair, B, gh2, ld_gh2, gphi,
                          ld_gphi, grb, ld_grb, genv, tpw);
-    FACE_LAUNCH_CHECK();
-    return 0;
-}
-
-extern "C" int face_radial_head_fwd(const float* h2, int32_t ld_h2, int64_t E, int32_t H, const float* w,
-                                    const float* b, int32_t F, float* R, int32_t ld_R, void* stream) {
-    if (E < 0 || H < 16 || H > 64 || H % 16 || F < 16 || F % 16 || ld_h2 < H || ld_R < F) return FACE_ERR_ARG;
-    if (E == 0) return 0;
-    if (!h2 || !w || !b || !R) return FACE_ERR_ARG;
-    if (ld_h2 % 4 || ld_R % 4 || (((uintptr_t)h2 | (uintptr_t)w | (uintptr_t)b | (uintptr_t)R) & 15))
-        return FACE_ERR_UNSUPPORTED;
-    const int max_lds = device_max_lds();
-    int S = 0, rot = 0, f_chunk = 0;
-    if (!head_layout(F, H, max_lds, S, rot, f_chunk)) return FACE_ERR_UNSUPPORTED;
-    const size_t lds = (size_t)f_chunk * S * sizeof(float);
-    constexpr int BB = 2, FB = 2;
-    const int64_t ntile = (E + 16 * BB - 1) / (16 * BB);
-    int64_t wgs = device_cu_count();                  // persistent: one 16-wave workgroup per CU
-    const int64_t need = (ntile + kHeadWaves - 1) / kHeadWaves;
-    if (need < wgs) wgs = need;
-    const dim3 grid((unsigned)wgs, (unsigned)((F + f_chunk - 1) / f_chunk)), block(kHeadWaves * kWave);
-    const hipStream_t st = (hipStream_t)stream;
-#define FACE_HEAD(HB_)                                                                                        \
-    do {                                                                                                      \
-        auto kern = radial_head_kernel<HB_, BB, FB>;                                                          \
-        if (lds > 65536 &&                                                                                    \
-            hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=    \
-                hipSuccess)                                                                                   \
-            return FACE_ERR_UNSUPPORTED;                                                                      \
-        hipLaunchKernelGGL(kern, grid, block, lds, st, h2, ld_h2, E, w, b, F, f_chunk, S, rot, R, ld_R);      \
-    } while (0)
-    switch (H / 16) {
-        case 1: FACE_HEAD(1); break;
-        case 2: FACE_HEAD(2); break;
-        case 3: FACE_HEAD(3); break;
-        default: FACE_HEAD(4); break;
-    }
-#undef FACE_HEAD
     FACE_LAUNCH_CHECK();
     return 0;
 }

@@ -55,10 +55,11 @@ _SIGS = {
     "face_radial_fwd": (ctypes.c_int, [P, I32, I32, P, P, I64, P, P, P, I32, I32, P, P, P, P, I32, P, I32, P, I32, P]),
     "face_radial_bwd": (ctypes.c_int, [P, I32, I32, P, P, I64, P, P, P, I32, I32, P, P, P, P, I32, P, I32, P, I32, P,
                                        I32, P, P]),
-    "face_radial_head_fwd": (ctypes.c_int, [P, I32, I64, I32, P, P, I32, P, I32, P]),
+    "face_edge_linear_fwd": (ctypes.c_int, [P, I32, I64, I32, P, P, I32, P, I32, P, P, I32, P]),
+    "face_edge_linear_bwd": (ctypes.c_int, [P, I32, I32, P, I32, P, P, I64, P, I32, P, I32, P]),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 
 def lib():

@@ -196,10 +196,12 @@ class FactorBlock(nn.Module):
             Vb = F.linear(src1, frozen(self.pvt)[0])                             # (3, N, nt*Kd)
             Mb = F.linear(src2, frozen(self.pmt)[0])                             # (6, N, nt*Kd)
             d, D1, D2 = ops.dir_transport(Vb, Mb, phi, Y, g, Kd, self.transport)   # (E, 4Kd), transport sums
-            # gather(msg(h)) + dir_mix(d): the bias joins the node table before the gather and the
-            # dir_mix GEMM accumulates onto the gathered rows in its epilogue
+            # gather(msg(h)) + dir_mix(d) as one per-edge matrix-core launch (and one backward)
             Wd, bd = frozen(self.dir_mix)
-            mj = ops.gather_neighbour(msg_n + bd, g).addmm_(d, Wd.t())
+            if d.shape[1] % 16 == 0 and d.shape[1] <= 64 and msg_n.shape[1] % 16 == 0 and msg_n.shape[1] <= 256:
+                mj = ops.edge_message(msg_n, d, Wd, bd, g)
+            else:
+                mj = ops.gather_neighbour(msg_n + bd, g).addmm_(d, Wd.t())
             gathered = False
         else:
             mj, gathered = msg_n, True

@@ -422,17 +422,58 @@ def _aligned16(t):
     return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
+def edge_linear(x, w, b=None, tab=None, idx=None, label="edge_linear"):
+    """y (E, F) = x w^T + b + tab[idx] on the matrix cores, no gradient (x (E, K), w (F, K),
+    K in {16, 32, 48, 64}, F a multiple of 16)."""
+    _lib.require_gpu(x, w)
+    E, K = x.shape
+    F_ = w.shape[0]
+    x_ = x if (x.stride(1) == 1 and x.stride(0) % 4 == 0 and x.data_ptr() % 16 == 0) else _aligned16(x)
+    w_ = _aligned16(w)
+    b_ = None if b is None else _aligned16(b)
+    tab_ = None if tab is None else _aligned16(tab)
+    y = torch.empty(E, F_, device=x.device)
+    call("face_edge_linear_fwd", ptr(x_), x_.stride(0), E, K, ptr(w_), ptr(b_), F_, ptr(tab_),
+         0 if tab_ is None else tab_.stride(0), ptr(idx), ptr(y), F_, _lib.stream_of(y), label=label)
+    return y
+
+
 def radial_head(h2, w, b):
     """R (E, F) = h2 w^T + b for the CP columns of the last radial layer (no gradient)."""
-    _lib.require_gpu(h2, w, b)
-    E, H = h2.shape
-    F_ = w.shape[0]
-    h2_ = h2 if (h2.stride(1) == 1 and h2.stride(0) % 4 == 0 and h2.data_ptr() % 16 == 0) else _aligned16(h2)
-    w_, b_ = _aligned16(w), _aligned16(b)
-    R = torch.empty(E, F_, device=h2.device)
-    call("face_radial_head_fwd", ptr(h2_), h2_.stride(0), E, H, ptr(w_), ptr(b_), F_, ptr(R), F_,
-         _lib.stream_of(R), label="radial_head")
-    return R
+    return edge_linear(h2, w, b, label="radial_head")
+
+
+class EdgeMessage(torch.autograd.Function):
+    """Per-edge message of a directional pass, m[e] = msg_n[col e] + d[e] W_d^T + b_d
+    (face/model.py:488-493: gather(msg(h)) + dir_mix(d)), in one launch; the backward gives
+    d msg_n (reduction over each atom's reverse edges, no atomics) and d d = dm W_d in one launch.
+    W_d / b_d receive no gradient (forces only)."""
+
+    @staticmethod
+    def forward(ctx, msg_n, d, w, b, graph):
+        _lib.require_gpu(msg_n, d)
+        y = edge_linear(d.detach(), w.detach(), b.detach(), msg_n.detach(), graph.col, label="edge_msg_fwd")
+        ctx.save_for_backward(_aligned16(w.detach()))
+        ctx.graph, ctx.K = graph, d.shape[1]
+        return y
+
+    @staticmethod
+    def backward(ctx, gy):
+        if ctx.needs_input_grad[2] or ctx.needs_input_grad[3]:
+            raise NotImplementedError("the fused edge message gives no weight gradients (forces only)")
+        (w,) = ctx.saved_tensors
+        g = ctx.graph
+        gy = _aligned16(gy)
+        F_ = gy.shape[1]
+        dtab = torch.empty(g.N, F_, device=gy.device) if ctx.needs_input_grad[0] else None
+        dd = torch.empty(g.E, ctx.K, device=gy.device) if ctx.needs_input_grad[1] else None
+        call("face_edge_linear_bwd", ptr(gy), gy.stride(0), F_, ptr(w), ctx.K, ptr(g.row_ptr), ptr(g.rev), g.N,
+             ptr(dd), ctx.K, ptr(dtab), F_, _lib.stream_of(gy), label="edge_msg_bwd")
+        return dtab, dd, None, None, None
+
+
+def edge_message(msg_n, d, w, b, graph):
+    return EdgeMessage.apply(msg_n, d, w, b, graph)
 
 
 # ----------------------------------------------------------------------------- radial MLP

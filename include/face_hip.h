@@ -19,6 +19,8 @@
  *   face/neighbors.py:7-37       padded_graph (ASE neighbor_list) -> face_nbr_* (count, fill, rev, padded)
  *   face/model.py:670-677        edge geometry + Bessel basis     -> face_edge_geom_fwd / _bwd
  *   face/model.py:465-469        radial MLP (rad_in, pair, radial) -> face_radial_fwd / _bwd
+ *   face/model.py:469,488-493    CP radial columns; gather(msg(h)) + dir_mix(d)
+ *                                                                  -> face_edge_linear_fwd / _bwd
  *   face/model.py:474-493        directional edge features        -> face_dir_feats_fwd / _bwd
  *   face/model.py:514-533        transport sums + transport map   -> face_transport_fwd / _bwd
  *   face/model.py:670,464,692-694 index_select gathers and their index_add backward
@@ -216,13 +218,23 @@ int face_radial_bwd(const float* rb, int32_t ld_rb, int32_t n_basis, const int32
                     const float* gh2, int32_t ld_gh2, const float* gphi, int32_t ld_gphi, float* grb, int32_t ld_grb,
                     float* genv, void* stream);
 
-/* CP radial head, the 4C CP columns of the radial MLP's last layer (face/model.py:469 with the
- * radial(...).split at :496-497): R (E, ld_R) = h2 (E, ld_h2) w^T + b, w (F, H) row-major,
- * b (F). H in {16, 32, 48, 64}, F a multiple of 16; h2, w, b, R 16-byte aligned and ld_h2,
- * ld_R multiples of 4 (else FACE_ERR_UNSUPPORTED). Replaces the GEMM the reference runs for
- * the last nn.Linear of the radial MLP. */
-int face_radial_head_fwd(const float* h2, int32_t ld_h2, int64_t E, int32_t H, const float* w, const float* b,
-                         int32_t F, float* R, int32_t ld_R, void* stream);
+/* ---------------------------------------------------------------- per-edge linear layers
+ * Forward: y (E, ld_y) = x (E, ld_x) w^T + b + tab[idx[e]], w (F, K) row-major, b (F) and tab
+ * (N, ld_tab) optional (NULL), idx NULL = row e of tab. K in {16, 32, 48, 64}, F a multiple
+ * of 16; x, w, b, tab, y 16-byte aligned and ld_* multiples of 4 (else FACE_ERR_UNSUPPORTED).
+ * Replaces the last nn.Linear of the radial MLP for the CP columns (face/model.py:469 with the
+ * split at :496-497; tab NULL) and gather(msg(h)) + dir_mix(d) (face/model.py:488-493: x = d,
+ * w = dir_mix weight, b = its bias, tab = msg(h), idx = col). */
+int face_edge_linear_fwd(const float* x, int32_t ld_x, int64_t E, int32_t K, const float* w, const float* b,
+                         int32_t F, const float* tab, int32_t ld_tab, const int32_t* idx, float* y, int32_t ld_y,
+                         void* stream);
+/* Backward of face_edge_linear_fwd with idx = col of a CSR graph with reverse-edge map rev:
+ * dx (E, ld_dx) = dy w and dtab (N, ld_dtab) row n = sum of dy[e] over the edges with col = n
+ * (rev[e] for e in row n); either output may be NULL. F <= 256. The reduction has a fixed
+ * order (no atomics). */
+int face_edge_linear_bwd(const float* dy, int32_t ld_dy, int32_t F, const float* w, int32_t K,
+                         const int32_t* row_ptr, const int32_t* rev, int64_t N, float* dx, int32_t ld_dx, float* dtab,
+                         int32_t ld_dtab, void* stream);
 
 /* ---------------------------------------------------------------- directional edge features
  * Node tables of Kd channels: V element (component a, atom n, channel k) at
