@@ -1,0 +1,240 @@
+// Row-block linear layers of the node features on the fp32 matrix cores (gfx950):
+//
+//   y[m, :] = (beta y[m, :] + (x[m, :] * xs[m, :]) W^T + bias) * ys[m, :]    (per problem: x, W, y, beta)
+//
+// for the tall activations of a pass, (k_l N, C) blocks against weights of at most a few
+// hundred columns: mix, tmix and proj (face/model.py:498-533, :537-544) and their input
+// gradients. xs / ys are per-atom scale rows picked by the atom's element (the elem_scale
+// factor of face/model.py:530-533) and are optional, as are beta and bias. Up to four
+// problems (the four ranks) share one launch.
+//
+// Work: a workgroup of NW waves (16 on large problems, 8 or 4 on small ones) owns a slice of
+// NS = 16 NB output columns and 32 NW rows; the slice's weight block W[n0 : n0 + NS, 0 : K] sits in LDS (row stride
+// K + 4) as the A operand of v_mfma_f32_16x16x4f32, the rows of x stream through registers as
+// B operands (K index q of instruction r of chunk kc = input column 16 kc + 4q + r), one chunk
+// of 16 columns ahead, and the wave keeps its 32 x NS outputs in registers over the whole K
+// loop. D = W . x^T holds output column 4q + r of row j in register r of lane j + 16q, one
+// float4 store of y[m][n .. n + 3] per lane and block.
+#include "common.h"
+
+namespace face {
+
+constexpr int kGemmBB = 2;                 // 16-row blocks per wave
+constexpr int kGemmMaxProbs = 4;
+
+struct GemmProb {
+    const float* x;
+    int64_t ld_x, m;
+    const float* w;
+    int64_t ld_w;
+    float* y;
+    int64_t ld_y;
+    int n, k, s_off, tiles, slices;        // tiles of 32 NW rows, slices of NS columns
+    float beta;
+    int64_t first_block;                   // first workgroup index of this problem
+};
+
+struct GemmArgs {
+    GemmProb p[kGemmMaxProbs];
+    int n_probs, w_kn, NS;
+    const float *bias, *xs, *ys;
+    int ld_s;
+    const int32_t* group;
+    int64_t period;
+};
+
+template <int NB, int NW>
+__global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
+    extern __shared__ float sW[];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    // this workgroup's problem, column slice and row tile
+    int pi = 0;
+#pragma unroll
+    for (int k = 1; k < kGemmMaxProbs; ++k)
+        if (k < A.n_probs && (int64_t)blockIdx.x >= A.p[k].first_block) pi = k;
+    const GemmProb& P = A.p[pi];
+    const int64_t local = (int64_t)blockIdx.x - P.first_block;
+    const int slice = (int)(local % P.slices);
+    const int64_t tile = local / P.slices;
+    const int K = P.k, SK = K + 4;
+    const int n0 = slice * A.NS;
+    const int ns = min(A.NS, P.n - n0);                                 // a multiple of 16
+    // stage W[n0 : n0 + ns, :] as rows of K (+ 4 pad)
+    if (!A.w_kn) {
+        const int nk4 = K / 4;
+        for (int v = tid; v < ns * nk4; v += blockDim.x) {
+            const int r = v / nk4, c4 = v - r * nk4;
+            st4(sW + r * SK + 4 * c4, ld4(P.w + (int64_t)(n0 + r) * P.ld_w + 4 * c4));
+        }
+    } else {                                                             // W given as (K, n)
+        for (int v = tid; v < ns * K; v += blockDim.x) {
+            const int k = v / ns, r = v - k * ns;
+            sW[r * SK + k] = P.w[(int64_t)k * P.ld_w + n0 + r];
+        }
+    }
+    __syncthreads();
+    const int j = lane & 15, q = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int64_t m0 = (tile * NW + wv) * (16 * kGemmBB);
+    if (m0 >= P.m) return;                                               // no barrier follows
+    const v4f z4 = {0.f, 0.f, 0.f, 0.f};
+    int64_t rows[kGemmBB];
+    bool ok[kGemmBB];
+    const float* xr[kGemmBB];
+    const float* xsr[kGemmBB];
+    const float* ysr[kGemmBB];
+#pragma unroll
+    for (int bb = 0; bb < kGemmBB; ++bb) {
+        rows[bb] = m0 + 16 * bb + j;
+        ok[bb] = rows[bb] < P.m;
+        xr[bb] = P.x + (ok[bb] ? rows[bb] : 0) * P.ld_x + 4 * q;
+        const int64_t g = (A.group && ok[bb]) ? (int64_t)A.group[rows[bb] % A.period] : 0;
+        xsr[bb] = A.xs ? A.xs + g * A.ld_s + P.s_off + 4 * q : nullptr;
+        ysr[bb] = A.ys ? A.ys + g * A.ld_s + P.s_off : nullptr;
+    }
+    auto load_x = [&](int kc, v4f (&xv)[kGemmBB]) {
+#pragma unroll
+        for (int bb = 0; bb < kGemmBB; ++bb) {
+            xv[bb] = ok[bb] ? ld4(xr[bb] + 16 * kc) : z4;
+            if (A.xs) xv[bb] *= ld4(xsr[bb] + 16 * kc);
+        }
+    };
+    v4f acc[NB][kGemmBB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int bb = 0; bb < kGemmBB; ++bb) acc[nb][bb] = z4;
+    const int nkc = K / 16;
+    v4f xn[kGemmBB];
+    load_x(0, xn);
+#pragma unroll 1
+    for (int kc = 0; kc < nkc; ++kc) {
+        v4f xv[kGemmBB];
+#pragma unroll
+        for (int bb = 0; bb < kGemmBB; ++bb) xv[bb] = xn[bb];
+        if (kc + 1 < nkc) load_x(kc + 1, xn);
+        const float* wrow = sW + j * SK + 16 * kc + 4 * q;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            if (16 * nb < ns) {
+                const v4f wa = *reinterpret_cast<const v4f*>(wrow + 16 * nb * SK);
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int bb = 0; bb < kGemmBB; ++bb) acc[nb][bb] = mfma_16x16x4(wa[r], xv[bb][r], acc[nb][bb]);
+            }
+        }
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        if (16 * nb < ns) {
+            const int n = n0 + 16 * nb + 4 * q;
+            const v4f bias = A.bias ? ld4(A.bias + n) : z4;
+#pragma unroll
+            for (int bb = 0; bb < kGemmBB; ++bb) {
+                if (ok[bb]) {
+                    float* yp = P.y + rows[bb] * P.ld_y + n;
+                    v4f v = acc[nb][bb] + bias;
+                    if (P.beta != 0.f) v += P.beta * ld4(yp);
+                    if (A.ys) v *= ld4(ysr[bb] + n);
+                    st4(yp, v);
+                }
+            }
+        }
+    }
+}
+
+static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+}  // namespace face
+
+using namespace face;
+
+extern "C" int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, int32_t w_kn, const float* bias,
+                                const float* x_scale, const float* y_scale, int32_t ld_scale, const int32_t* group,
+                                int64_t period, void* stream) {
+    if (!probs || n_probs < 1 || n_probs > kGemmMaxProbs) return FACE_ERR_ARG;
+    int K = 16;
+    for (int i = 0; i < n_probs; ++i) {
+        if (probs[i].k < 16 || probs[i].k % 16) return FACE_ERR_ARG;
+        if (probs[i].k > K) K = probs[i].k;
+    }
+    const bool scaled = x_scale || y_scale;
+    if (scaled && (!group || period < 1 || ld_scale < 1)) return FACE_ERR_ARG;
+    if ((bias && !al16(bias)) || (x_scale && !al16(x_scale)) || (y_scale && !al16(y_scale)) || (scaled && ld_scale % 4))
+        return FACE_ERR_UNSUPPORTED;
+    // column slice: the weight slice (NS x (K + 4) floats) must fit in LDS, at most 160 columns,
+    // and the widest problem splits into slices of equal width (multiples of 16)
+    const int max_lds = device_max_lds();
+    int ns_max = (max_lds / (4 * (K + 4))) / 16 * 16;
+    if (ns_max > 160) ns_max = 160;
+    if (ns_max < 16) return FACE_ERR_UNSUPPORTED;
+    int n_widest = 16;
+    for (int i = 0; i < n_probs; ++i)
+        if (probs[i].n > n_widest) n_widest = probs[i].n;
+    const int n_sl = (n_widest + ns_max - 1) / ns_max;
+    const int NS = ((n_widest + n_sl - 1) / n_sl + 15) / 16 * 16;
+    GemmArgs A{};
+    A.n_probs = n_probs, A.w_kn = w_kn ? 1 : 0, A.bias = bias, A.xs = x_scale, A.ys = y_scale;
+    A.ld_s = ld_scale, A.group = group, A.period = period;
+    // 16-wave workgroups (4 waves per SIMD hide the row loads) unless that leaves CUs idle
+    auto wgs_for = [&](int nw) {
+        int64_t t = 0;
+        for (int i = 0; i < n_probs; ++i) t += (probs[i].m + 16 * kGemmBB * nw - 1) / (16 * kGemmBB * nw);
+        return t;
+    };
+    const int n_cu = device_cu_count();
+    const int NW = wgs_for(16) >= n_cu ? 16 : (wgs_for(8) >= n_cu ? 8 : 4);
+    int max_n = 16;
+    int64_t blocks = 0;
+    for (int i = 0; i < n_probs; ++i) {
+        const face_lin_problem& s = probs[i];
+        if (s.m < 0 || s.n < 16 || s.n % 16 || s.ld_x < s.k || s.ld_y < s.n || s.ld_w < (w_kn ? s.n : s.k))
+            return FACE_ERR_ARG;
+        if (scaled && (s.s_off < 0 || s.s_off % 4 || s.s_off + (x_scale ? s.k : 0) > ld_scale ||
+                       s.s_off + (y_scale ? s.n : 0) > ld_scale))
+            return FACE_ERR_ARG;
+        if (s.m > 0 && (!s.x || !s.w || !s.y)) return FACE_ERR_ARG;
+        if (s.ld_x % 4 || s.ld_y % 4 || !al16(s.x) || !al16(s.y) || (!w_kn && (!al16(s.w) || s.ld_w % 4)))
+            return FACE_ERR_UNSUPPORTED;
+        GemmProb& p = A.p[i];
+        p.x = s.x, p.ld_x = s.ld_x, p.m = s.m, p.w = s.w, p.ld_w = s.ld_w, p.y = s.y, p.ld_y = s.ld_y, p.n = s.n;
+        p.k = s.k, p.s_off = s.s_off, p.beta = s.beta;
+        p.tiles = (int)((s.m + 16 * kGemmBB * NW - 1) / (16 * kGemmBB * NW));
+        p.slices = (s.n + NS - 1) / NS;
+        p.first_block = blocks;
+        blocks += (int64_t)p.tiles * p.slices;
+        if (s.n > max_n) max_n = s.n;
+    }
+    for (int i = n_probs; i < kGemmMaxProbs; ++i) A.p[i].first_block = INT64_MAX;
+    if (blocks == 0) return 0;
+    A.NS = NS;
+    const int nb = (max_n < NS ? max_n : NS) / 16;
+    const size_t lds = (size_t)(nb * 16) * (K + 4) * sizeof(float);
+    const hipStream_t st = (hipStream_t)stream;
+#define FACE_GEMM(NB_)                                                                                      \
+    do {                                                                                                    \
+        auto kern = NW == 16 ? rows_gemm_kernel<NB_, 16>                                                    \
+                             : (NW == 8 ? rows_gemm_kernel<NB_, 8> : rows_gemm_kernel<NB_, 4>);             \
+        if (lds > 65536 &&                                                                                  \
+            hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != \
+                hipSuccess)                                                                                 \
+            return FACE_ERR_UNSUPPORTED;                                                                    \
+        hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(NW * kWave), lds, st, A);                    \
+    } while (0)
+    switch (nb) {
+        case 1: FACE_GEMM(1); break;
+        case 2: FACE_GEMM(2); break;
+        case 3: FACE_GEMM(3); break;
+        case 4: FACE_GEMM(4); break;
+        case 5: FACE_GEMM(5); break;
+        case 6: FACE_GEMM(6); break;
+        case 7: FACE_GEMM(7); break;
+        case 8: FACE_GEMM(8); break;
+        case 9: FACE_GEMM(9); break;
+        default: FACE_GEMM(10); break;
+    }
+#undef FACE_GEMM
+    FACE_LAUNCH_CHECK();
+    return 0;
+}

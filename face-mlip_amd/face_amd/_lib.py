@@ -57,9 +57,17 @@ _SIGS = {
                                        I32, P, P]),
     "face_edge_linear_fwd": (ctypes.c_int, [P, I32, I64, I32, P, P, I32, P, I32, P, P, I32, P]),
     "face_edge_linear_bwd": (ctypes.c_int, [P, I32, I32, P, I32, P, P, I64, P, I32, P, I32, P]),
+    "face_rows_linear": (ctypes.c_int, [P, I32, I32, P, P, P, I32, P, I64, P]),
 }
 
-ABI_VERSION = 6
+ABI_VERSION = 7
+
+
+class LinProblem(ctypes.Structure):
+    """face_lin_problem of include/face_hip.h."""
+    _fields_ = [("x", ctypes.c_void_p), ("ld_x", ctypes.c_int64), ("m", ctypes.c_int64), ("w", ctypes.c_void_p),
+                ("ld_w", ctypes.c_int64), ("y", ctypes.c_void_p), ("ld_y", ctypes.c_int64), ("n", ctypes.c_int32),
+                ("k", ctypes.c_int32), ("s_off", ctypes.c_int32), ("beta", ctypes.c_float)]
 
 
 def lib():

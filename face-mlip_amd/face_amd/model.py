@@ -175,7 +175,7 @@ class FactorBlock(nn.Module):
             self.tmix3 = nn.Linear(B * 2 * K_dir, C, bias=False)
 
     # ------------------------------------------------------------------ moments
-    def moments(self, h, rb, Y, env, zp, zidx, avg_nb, sets, eq, g):
+    def moments(self, h, rb, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g):
         """Moments A_l as monomial-major (k_l, N, C) blocks (face/model.py:460-534)."""
         N, E = g.N, g.E
         B, C, Kd = self.B, self.C, self.K
@@ -205,7 +205,7 @@ class FactorBlock(nn.Module):
             gathered = False
         else:
             mj, gathered = msg_n, True
-        s = self._scale_table(avg_nb)[zidx].view(N, 4, C)                       # elem_scale / avg_nb per atom
+        s_tab = self._scale_table(avg_nb)                                        # elem_scale / avg_nb (n_el, 4C)
         if self.cp:
             # R = h2 W2[B:]^T + b2[B:] (E, 4C) feeds the pooling (envelope applied in-kernel); on the
             # matrix-core shapes the pooling backward also applies W2[B:] and returns d h2 directly
@@ -217,16 +217,20 @@ class FactorBlock(nn.Module):
             Af = ops.density(phi, mj, Y, g, 20, gathered)                         # 4 x (k_l, N, B*K)
         # A_l = (mix_l(Af_l) [+ tmix_l(D_l)]) * s: D1/D2 are the raw transport sums; the reference's
         # 1/avg_nb (face/model.py:522) and its avg_nb factor (:532-533) cancel through the linear tmix,
-        # leaving the common factor s = elem_scale / avg_nb, so tmix accumulates into the mix GEMM's
-        # output in place and one scaling pass per rank remains
-        tm = {1: (self.tmix1, D1), 2: (self.tmix2, D2)} if self.transport else {}
+        # leaving the common factor s = elem_scale / avg_nb, applied in the mix GEMMs' epilogue
+        wm = [frozen(self.mix[l])[0] for l in range(4)]
+        wt = [frozen(self.tmix1)[0], frozen(self.tmix2)[0]] if self.transport else [None, None]
+        D1, D2 = (D1, D2) if self.transport else (None, None)
+        if C % 16 == 0 and Af[0].shape[-1] % 16 == 0:
+            return list(ops.scaled_mix(s_tab, zidx32, wm, wt, D1, D2, Af))         # 4 x (k_l, N, C)
+        s = s_tab[zidx].view(N, 4, C)
         A = []
         for l in range(4):
             x = Af[l]
-            y = x.reshape(-1, x.shape[-1]) @ frozen(self.mix[l])[0].t()
-            if l in tm:
-                mod, D = tm[l]
-                y.addmm_(D.reshape(-1, D.shape[-1]), frozen(mod)[0].t())
+            y = x.reshape(-1, x.shape[-1]) @ wm[l].t()
+            if l in (1, 2) and self.transport:
+                D = D1 if l == 1 else D2
+                y.addmm_(D.reshape(-1, D.shape[-1]), wt[l - 1].t())
             A.append(y.view(x.shape[0], N, C) * s[None, :, l, :])                 # (k_l, N, C)
         return A
 
@@ -242,9 +246,9 @@ class FactorBlock(nn.Module):
         return c[1]
 
     # ------------------------------------------------------------------ invariants + readout
-    def forward(self, h, rb, Y, env, zp, zidx, avg_nb, sets, eq, g):
+    def forward(self, h, rb, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g):
         C = self.C
-        A = self.moments(h, rb, Y, env, zp, zidx, avg_nb, sets, eq, g)
+        A = self.moments(h, rb, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g)
         allsets = sets + [A]
         ys = []
         for l in range(4):
@@ -336,16 +340,18 @@ class FACE(nn.Module):
             pos.requires_grad_(True)
         Y, rb, env = ops.edge_geometry(pos, graph, self.basis.freq, self.rc)
         zidx = self.zmap[graph.Z]
-        zkey = ("zp", len(self.E0))
+        zkey = ("zp", self.zmap.data_ptr(), len(self.E0))
         zp = graph.cache.get(zkey)
         if zp is None:
             zp = (zidx[graph.recv.long()] * len(self.E0) + zidx[graph.col.long()]).to(torch.int32)
             graph.cache[zkey] = zp
+            graph.cache[zkey + ("atoms",)] = zidx.to(torch.int32)
+        zidx32 = graph.cache[zkey + ("atoms",)]
         h = F.embedding(zidx, self.embed.weight.detach())
         e_at = self.E0[zidx].clone()
         sets, eq = [], None
         for blk in self.blocks:
-            e, h, A, eq = blk(h, rb, Y, env, zp, zidx, self.avg_nb, sets, eq, graph)
+            e, h, A, eq = blk(h, rb, Y, env, zp, zidx, zidx32, self.avg_nb, sets, eq, graph)
             sets.append(A)
             e_at = e_at + self.scale * e.squeeze(-1)
         E = ops.StructureSum.apply(e_at, graph.struct_ptr, graph.batch, graph.nstr)

@@ -611,3 +611,73 @@ class NodeFeatures(torch.autograd.Function):
 
 def node_features(y0, y1, y2, y3, a, b, eq, C):
     return NodeFeatures.apply(y0, y1, y2, y3, a, b, eq, C)
+
+
+# ----------------------------------------------------------------------------- row-block linear layers
+def rows_linear(probs, w_kn=False, bias=None, xs=None, ys=None, group=None, period=1, label="rows_linear"):
+    """One launch of up to four row-block linear problems (no autograd). probs: list of
+    (x (m, k), w, y (m, n), s_off, beta) with 2-d fp32 row-major views; w is (n, k) or, with
+    w_kn, (k, n). y[r] = (beta y[r] + (x[r] * xs[g(r), s_off:]) w^T + bias) * ys[g(r), s_off:],
+    g(r) = group[r % period]; xs / ys are (n_groups, ld) tables or None."""
+    arr = (_lib.LinProblem * len(probs))()
+    ref = None
+    for i, (x, w, y, s_off, beta) in enumerate(probs):
+        assert x.dim() == 2 and y.dim() == 2 and w.dim() == 2 and x.stride(1) == 1 and y.stride(1) == 1
+        assert w.stride(1) == 1 and x.shape[0] == y.shape[0]
+        arr[i] = _lib.LinProblem(x.data_ptr(), x.stride(0), x.shape[0], w.data_ptr(), w.stride(0), y.data_ptr(),
+                                 y.stride(0), y.shape[1], x.shape[1], int(s_off), float(beta))
+        ref = y
+    tab = xs if xs is not None else ys
+    call("face_rows_linear", arr, len(probs), 1 if w_kn else 0, ptr(bias), ptr(xs), ptr(ys),
+         0 if tab is None else tab.stride(0), ptr(group), int(period), _lib.stream_of(ref), label=label)
+
+
+class ScaledMix(torch.autograd.Function):
+    """A_l = (Af_l W_l^T [+ D_l T_l^T]) * s[z] for the four ranks l (face/model.py:498-501, the
+    transport terms of :530-533 for l = 1, 2): s = elem_scale / avg_nb per atom (s_tab (n_el, 4C),
+    group = element index per atom, int32). The four mix GEMMs run in one launch with the scale
+    (and the accumulation onto the tmix products) in their epilogue; the backward applies the
+    scale to the upstream rows as it loads them. Weights receive no gradient."""
+
+    @staticmethod
+    def forward(ctx, s_tab, group, wm, wt, D1, D2, *Af):
+        N = group.shape[0]
+        C = wm[0].shape[0]
+        dev = Af[0].device
+        outs = [torch.empty(a.shape[0], N, C, device=dev) for a in Af]
+        Ds = {1: D1, 2: D2}
+        for l, D in Ds.items():
+            if D is not None:
+                torch.mm(D.reshape(-1, D.shape[-1]), wt[l - 1].t(), out=outs[l].view(-1, C))
+        probs = [(a.reshape(-1, a.shape[-1]), wm[l], outs[l].view(-1, C), l * C,
+                  1.0 if Ds.get(l) is not None else 0.0) for l, a in enumerate(Af)]
+        rows_linear(probs, ys=s_tab, group=group, period=N, label="mix_fwd")
+        ctx.save_for_backward(s_tab, group)
+        ctx.wm, ctx.wt, ctx.has_D = wm, wt, (D1 is not None, D2 is not None)
+        ctx.shapes = [a.shape for a in Af]
+        return tuple(outs)
+
+    @staticmethod
+    def backward(ctx, *gA):
+        s_tab, group = ctx.saved_tensors
+        N = group.shape[0]
+        C = ctx.wm[0].shape[0]
+        dev = s_tab.device
+        gA = [(g.contiguous() if g is not None else torch.zeros(sh[0], N, C, device=dev))
+              for g, sh in zip(gA, ctx.shapes)]
+        dAf = [torch.empty(sh, device=dev) for sh in ctx.shapes]
+        probs = [(g.view(-1, C), ctx.wm[l], dAf[l].view(-1, dAf[l].shape[-1]), l * C, 0.0) for l, g in enumerate(gA)]
+        rows_linear(probs, w_kn=True, xs=s_tab, group=group, period=N, label="mix_bwd")
+        dD = [None, None]
+        s = None
+        for i, l in enumerate((1, 2)):
+            if ctx.has_D[i] and ctx.needs_input_grad[4 + i]:
+                if s is None:
+                    s = s_tab[group.long()].view(N, 4, C)
+                gs = (gA[l] * s[None, :, l, :]).view(-1, C)
+                dD[i] = (gs @ ctx.wt[i]).view(gA[l].shape[0], N, -1)
+        return (None, None, None, None, dD[0], dD[1], *dAf)
+
+
+def scaled_mix(s_tab, group, wm, wt, D1, D2, Af):
+    return ScaledMix.apply(s_tab, group, wm, wt, D1, D2, *Af)

@@ -21,6 +21,7 @@
  *   face/model.py:465-469        radial MLP (rad_in, pair, radial) -> face_radial_fwd / _bwd
  *   face/model.py:469,488-493    CP radial columns; gather(msg(h)) + dir_mix(d)
  *                                                                  -> face_edge_linear_fwd / _bwd
+ *   face/model.py:498-533,537-544 mix / tmix / proj (+ elem_scale)   -> face_rows_linear
  *   face/model.py:474-493        directional edge features        -> face_dir_feats_fwd / _bwd
  *   face/model.py:514-533        transport sums + transport map   -> face_transport_fwd / _bwd
  *   face/model.py:670,464,692-694 index_select gathers and their index_add backward
@@ -217,6 +218,30 @@ int face_radial_bwd(const float* rb, int32_t ld_rb, int32_t n_basis, const int32
                     int32_t H, const float* w1, const float* b1, const float* w_phi, const float* b_phi, int32_t B,
                     const float* gh2, int32_t ld_gh2, const float* gphi, int32_t ld_gphi, float* grb, int32_t ld_grb,
                     float* genv, void* stream);
+
+/* ---------------------------------------------------------------- row-block linear layers
+ * One problem: x (m, ld_x >= k) rows, w (n, k) row-major with row stride ld_w (w_kn = 0) or
+ * (k, n) with row stride ld_w (w_kn = 1), y (m, ld_y >= n); n and k multiples of 16. */
+typedef struct {
+    const float* x;
+    int64_t ld_x, m;
+    const float* w;
+    int64_t ld_w;
+    float* y;
+    int64_t ld_y;
+    int32_t n, k, s_off;
+    float beta;
+} face_lin_problem;
+/* For each problem (1..4 of them, host array):
+ *   y[r, :] = (beta y[r, :] + (x[r, :] * xs[r, :]) w^T + bias) * ys[r, :]
+ * with xs[r, k] = x_scale[group[r % period] * ld_scale + s_off + k] and ys likewise over the
+ * n output columns; x_scale, y_scale, bias may be NULL (beta = 0: y is not read). The linear
+ * layers of the node features: mix / tmix / proj and the readout input (face/model.py:498-533,
+ * :537-544) with the elem_scale factor, and their input gradients (w_kn = 1). x, y, bias and the
+ * scale tables 16-byte aligned, ld_x, ld_y (and ld_w, ld_scale, s_off) multiples of 4. */
+int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, int32_t w_kn, const float* bias,
+                     const float* x_scale, const float* y_scale, int32_t ld_scale, const int32_t* group, int64_t period,
+                     void* stream);
 
 /* ---------------------------------------------------------------- per-edge linear layers
  * Forward: y (E, ld_y) = x (E, ld_x) w^T + b + tab[idx[e]], w (F, K) row-major, b (F) and tab

@@ -446,3 +446,105 @@ def test_radial_mlp_matches_torch(E, nb, H, B, n_pair, want_h2):
     errs = [rel(a, b) for a, b in zip(outs, refs)] + [rel(a, b) for a, b in zip(grads, grads2)]
     say("   errs", errs)
     assert max(errs) < TOL, errs
+
+
+# ----------------------------------------------------------------------------- row-block linear layers
+def _lin_ref(x, w, w_kn, y0, beta, bias, xs, ys, grp, period, s_off):
+    x, w = x.double().cpu(), w.double().cpu()
+    g = grp.long().cpu()[torch.arange(x.shape[0]) % period] if grp is not None else None
+    if xs is not None:
+        x = x * xs.double().cpu()[g][:, s_off:s_off + x.shape[1]]
+    y = x @ (w if w_kn else w.T)
+    if beta:
+        y = y + beta * y0.double().cpu()
+    if bias is not None:
+        y = y + bias.double().cpu()
+    if ys is not None:
+        y = y * ys.double().cpu()[g][:, s_off:s_off + y.shape[1]]
+    return y
+
+
+@pytest.mark.parametrize("case", ["single", "ranks_proj", "ranks_scaled", "kn_xscale", "k512", "empty"])
+def test_rows_linear_matches_torch(case):
+    """y = (beta y + (x * xs) w^T + bias) * ys over up to four problems per launch (mix / tmix /
+    proj with the elem_scale factor and their input gradients) vs torch fp64: ragged row counts,
+    weight column slices (ld_w > k), (k, n) weights, K = 512, sliced outputs (n = 480), an empty
+    problem beside full ones."""
+    from face_amd import ops
+    say("rows_linear", case)
+    torch.manual_seed(len(case))
+    N, C = 1000, 160
+    grp = torch.randint(0, 3, (N,), device=DEV, dtype=torch.int32)
+    tab = torch.rand(3, 4 * C, device=DEV) + 0.5
+    bias = xs = ys = None
+    w_kn = False
+    probs, refs = [], []
+    if case == "single":
+        x = torch.randn(10007, C, device=DEV)
+        w = torch.randn(C, C, device=DEV) / C ** 0.5
+        probs = [(x, w, torch.empty(10007, C, device=DEV), 0, 0.0)]
+    elif case == "ranks_proj":
+        wide = torch.randn(3 * C, 2 * C, device=DEV) / C ** 0.5           # proj weight over two sets
+        for l, (k, n) in enumerate(((1, C), (3, 3 * C), (6, 3 * C), (10, 2 * C))):
+            x = torch.randn(k * N, C, device=DEV)
+            probs.append((x, wide[:n, C:], torch.randn(k * N, n, device=DEV), 0, 1.0 if l % 2 else 0.0))
+    elif case == "ranks_scaled":                                             # mix (+ tmix) * elem_scale
+        ys, bias = tab, torch.randn(C, device=DEV)
+        for l, k in enumerate((1, 3, 6, 10)):
+            x = torch.randn(k * N, C, device=DEV)
+            w = torch.randn(C, C, device=DEV) / C ** 0.5
+            probs.append((x, w, torch.randn(k * N, C, device=DEV), l * C, 1.0 if l in (1, 2) else 0.0))
+    elif case == "kn_xscale":
+        w_kn, xs = True, tab
+        for l, k in enumerate((1, 3, 6, 10)):
+            x = torch.randn(k * N, C, device=DEV)
+            w = torch.randn(C, 2 * C + 32, device=DEV)[:, 16:16 + 2 * C] / C ** 0.5   # (k, n), ld_w > n
+            probs.append((x, w, torch.empty(k * N, 2 * C, device=DEV), l * C, 0.0))
+    elif case == "k512":
+        x = torch.randn(6 * N, 512, device=DEV)
+        w = torch.randn(C, 512, device=DEV) / 512 ** 0.5
+        probs = [(x, w, torch.randn(6 * N, C, device=DEV), 0, 1.0)]
+    else:
+        x = torch.randn(0, C, device=DEV)
+        probs = [(x, torch.randn(C, C, device=DEV), torch.empty(0, C, device=DEV), 0, 0.0),
+                 (torch.randn(77, C, device=DEV), torch.randn(C, C, device=DEV), torch.empty(77, C, device=DEV), 0, 0.0)]
+    for (x, w, y, s, b) in probs:
+        refs.append(_lin_ref(x, w, w_kn, y, b, bias, xs, ys, grp if (xs is not None or ys is not None) else None, N, s))
+    ops.rows_linear(probs, w_kn=w_kn, bias=bias, xs=xs, ys=ys, group=grp, period=N)
+    errs = [rel(p[2], r) if r.numel() else 0.0 for p, r in zip(probs, refs)]
+    say("   errs", errs)
+    assert max(errs) < 1e-5, errs
+
+
+@pytest.mark.parametrize("transport,Cin", [(True, 160), (False, 160), (False, 512), (True, 32)])
+def test_scaled_mix_forward_backward(transport, Cin):
+    """A_l = (Af_l W_l^T [+ D_l T_l^T]) * s[z] for the four ranks (face/model.py:498-501, :530-533)
+    and the gradients of Af_l and D_l vs torch fp64 autograd."""
+    from face_amd import ops
+    say("scaled mix", transport, Cin)
+    torch.manual_seed(Cin + transport)
+    N, C, Dw = 517, 96 if Cin != 32 else 32, 64
+    grp = torch.randint(0, 3, (N,), device=DEV, dtype=torch.int32)
+    s_tab = torch.rand(3, 4 * C, device=DEV) + 0.5
+    Af = [torch.randn(k, N, Cin, device=DEV, requires_grad=True) for k in (1, 3, 6, 10)]
+    wm = [torch.randn(C, Cin, device=DEV) / Cin ** 0.5 for _ in range(4)]
+    D1 = torch.randn(3, N, Dw, device=DEV, requires_grad=True) if transport else None
+    D2 = torch.randn(6, N, Dw, device=DEV, requires_grad=True) if transport else None
+    wt = [torch.randn(C, Dw, device=DEV) / 8, torch.randn(C, Dw, device=DEV) / 8] if transport else [None, None]
+    A = ops.scaled_mix(s_tab, grp, wm, wt, D1, D2, Af)
+    G = [torch.randn_like(a) for a in A]
+    ins = Af + ([D1, D2] if transport else [])
+    gr = torch.autograd.grad(sum((a * g).sum() for a, g in zip(A, G)), ins)
+    c = lambda t: t.detach().double().cpu()
+    insc = [c(t).requires_grad_(True) for t in ins]
+    s = c(s_tab)[grp.long().cpu()].view(N, 4, C)
+    A2 = []
+    for l in range(4):
+        y = insc[l] @ c(wm[l]).T
+        if transport and l in (1, 2):
+            y = y + insc[3 + l] @ c(wt[l - 1]).T
+        A2.append(y * s[None, :, l, :])
+    gr2 = torch.autograd.grad(sum((a * c(g)).sum() for a, g in zip(A2, G)), insc)
+    errs = [rel(a, b) for a, b in zip(A, A2)] + [rel(a, b) for a, b in zip(gr, gr2)]
+    say("   errs", errs)
+    assert max(errs) < 1e-5, errs
