@@ -59,17 +59,19 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
     const int K = P.k, SK = K + 4;
     const int n0 = slice * A.NS;
     const int ns = min(A.NS, P.n - n0);                                 // a multiple of 16
-    // stage W[n0 : n0 + ns, :] as rows of K (+ 4 pad)
+    // stage W[n0 : n0 + ns, :] as rows of K (+ 4 pad); rows ns .. 16 NB - 1 are zero, so the
+    // MFMA loop below runs all NB blocks without branches
+    const v4f z4 = {0.f, 0.f, 0.f, 0.f};
     if (!A.w_kn) {
         const int nk4 = K / 4;
-        for (int v = tid; v < ns * nk4; v += blockDim.x) {
+        for (int v = tid; v < 16 * NB * nk4; v += blockDim.x) {
             const int r = v / nk4, c4 = v - r * nk4;
-            st4(sW + r * SK + 4 * c4, ld4(P.w + (int64_t)(n0 + r) * P.ld_w + 4 * c4));
+            st4(sW + r * SK + 4 * c4, r < ns ? ld4(P.w + (int64_t)(n0 + r) * P.ld_w + 4 * c4) : z4);
         }
     } else {                                                             // W given as (K, n)
-        for (int v = tid; v < ns * K; v += blockDim.x) {
-            const int k = v / ns, r = v - k * ns;
-            sW[r * SK + k] = P.w[(int64_t)k * P.ld_w + n0 + r];
+        for (int v = tid; v < 16 * NB * K; v += blockDim.x) {
+            const int k = v / (16 * NB), r = v - k * (16 * NB);
+            sW[r * SK + k] = r < ns ? P.w[(int64_t)k * P.ld_w + n0 + r] : 0.f;
         }
     }
     __syncthreads();
@@ -77,7 +79,6 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
     const int wv = __builtin_amdgcn_readfirstlane(tid / kWave);
     const int64_t m0 = (tile * NW + wv) * (16 * kGemmBB);
     if (m0 >= P.m) return;                                               // no barrier follows
-    const v4f z4 = {0.f, 0.f, 0.f, 0.f};
     int64_t rows[kGemmBB];
     bool ok[kGemmBB];
     const float* xr[kGemmBB];
@@ -113,16 +114,25 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
 #pragma unroll
         for (int bb = 0; bb < kGemmBB; ++bb) xv[bb] = xn[bb];
         if (kc + 1 < nkc) load_x(kc + 1, xn);
+        // weight blocks read one block ahead of their MFMAs (LDS latency under the MFMA chain)
         const float* wrow = sW + j * SK + 16 * kc + 4 * q;
+        v4f wa = *reinterpret_cast<const v4f*>(wrow);
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-            if (16 * nb < ns) {
-                const v4f wa = *reinterpret_cast<const v4f*>(wrow + 16 * nb * SK);
+            const v4f wn = nb + 1 < NB ? *reinterpret_cast<const v4f*>(wrow + 16 * (nb + 1) * SK) : wa;
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
+            for (int r = 0; r < 4; ++r)
 #pragma unroll
-                    for (int bb = 0; bb < kGemmBB; ++bb) acc[nb][bb] = mfma_16x16x4(wa[r], xv[bb][r], acc[nb][bb]);
-            }
+                for (int bb = 0; bb < kGemmBB; ++bb) acc[nb][bb] = mfma_16x16x4(wa[r], xv[bb][r], acc[nb][bb]);
+            wa = wn;
+        }
+        // issue order: reads of blocks 0 and 1, then per block its 4 kGemmBB MFMAs followed by
+        // the read of block nb + 2, so every read has a block of MFMAs to hide under
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+            if (nb == 0) __builtin_amdgcn_sched_group_barrier(0x100, NB > 1 ? 2 : 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4 * kGemmBB, 0);
+            if (nb + 2 < NB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
         }
     }
 #pragma unroll
