@@ -48,6 +48,32 @@ __device__ __forceinline__ v4f mfma_16x16x4(float a, float b, v4f c) {
 __device__ __forceinline__ v4f ld4(const float* p) { return *reinterpret_cast<const v4f*>(p); }
 __device__ __forceinline__ void st4(float* p, v4f v) { *reinterpret_cast<v4f*>(p) = v; }
 
+// LDS image of a (F, K) row-major weight block read as float4 chunks of 16 rows at a time:
+// row f at f * S; with S = K (K = 32, 64) the float4 chunk c of row f is stored at chunk
+// (c + f) mod K/4, otherwise S = K + 4: both keep the 16 rows read by one instruction on
+// distinct banks.
+__device__ __forceinline__ int lin_off(int f, int c4, int S, int nch, bool rot) {
+    return f * S + 4 * (rot ? ((c4 + f) & (nch - 1)) : c4);
+}
+
+// Row stride, swizzle and row chunk of that image for an LDS budget (f_chunk < F: the block is
+// split over several workgroups); false if not even 16 rows fit.
+static inline bool lin_layout(int F, int K, int max_lds, int& S, int& rot, int& f_chunk) {
+    const int nch = K / 4;
+    if ((int64_t)F * (K + 4) * 4 <= max_lds) {
+        S = K + 4, rot = 0, f_chunk = F;
+    } else if ((nch & (nch - 1)) == 0 && nch >= 8 && (int64_t)F * K * 4 <= max_lds) {
+        S = K, rot = 1, f_chunk = F;
+    } else {
+        S = K + 4, rot = 0;
+        const int rows = (max_lds / (4 * S)) / 16 * 16;
+        if (rows < 16) return false;
+        const int nchunk = (F + rows - 1) / rows;
+        f_chunk = ((F / 16 + nchunk - 1) / nchunk) * 16;
+    }
+    return true;
+}
+
 // Attribute of the current device, cached per device and attribute slot (fallback if the
 // query fails).
 template <int Slot>

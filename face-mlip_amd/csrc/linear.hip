@@ -20,14 +20,8 @@ namespace face {
 // q of instruction r of chunk kb = input feature 16 kb + 4q + r) and walks all output blocks, so
 // the output streams out at the write rate: D = W . X^T holds output feature 4q + r of edge j
 // in register r of lane j + 16q, one float4 store of Y[e][f .. f + 3] per lane and block.
-// LDS image: row f at f * S; with S = K (K = 32, 64) the float4 chunk c of row f is stored at
-// chunk (c + f) mod K/4, otherwise S = K + 4: both keep the 16 rows read by one instruction on
-// distinct banks.
+// LDS image: lin_off / lin_layout (common.h).
 constexpr int kLinWaves = 16;
-
-__device__ __forceinline__ int lin_off(int f, int c4, int S, int nch, bool rot) {
-    return f * S + 4 * (rot ? ((c4 + f) & (nch - 1)) : c4);
-}
 
 template <int KB, int BB, int FB>
 __global__ __launch_bounds__(kLinWaves * kWave) void edge_linear_fwd_kernel(
@@ -111,23 +105,6 @@ __global__ __launch_bounds__(kLinWaves * kWave) void edge_linear_fwd_kernel(
             }
         }
     }
-}
-
-// Row stride, swizzle and output chunk of the forward's LDS weight image for the LDS budget.
-static bool lin_layout(int F, int K, int max_lds, int& S, int& rot, int& f_chunk) {
-    const int nch = K / 4;
-    if ((int64_t)F * (K + 4) * 4 <= max_lds) {
-        S = K + 4, rot = 0, f_chunk = F;
-    } else if ((nch & (nch - 1)) == 0 && nch >= 8 && (int64_t)F * K * 4 <= max_lds) {
-        S = K, rot = 1, f_chunk = F;
-    } else {
-        S = K + 4, rot = 0;
-        const int rows = (max_lds / (4 * S)) / 16 * 16;
-        if (rows < 16) return false;
-        const int nchunk = (F + rows - 1) / rows;
-        f_chunk = ((F / 16 + nchunk - 1) / nchunk) * 16;
-    }
-    return true;
 }
 
 // ------------------------------------------------------------------ backward

@@ -60,7 +60,7 @@ _SIGS = {
     "face_rows_linear": (ctypes.c_int, [P, I32, I32, P, P, P, I32, P, I64, P]),
 }
 
-ABI_VERSION = 7
+ABI_VERSION = 9
 
 
 class LinProblem(ctypes.Structure):
@@ -128,6 +128,21 @@ def call(name, *args, label=None):
     if code != 0:
         msg = lib().face_hip_error_string(code).decode()
         raise RuntimeError(f"{name} failed: {msg} (code {code})")
+
+
+FACE_ERR_UNSUPPORTED = -2
+
+
+def call_status(name, *args, label=None):
+    """call(), except that FACE_ERR_UNSUPPORTED (a shape the entry point's kernels cannot serve;
+    nothing was launched) is returned instead of raised, for callers with another route."""
+    try:
+        call(name, *args, label=label)
+        return 0
+    except RuntimeError as err:
+        if f"(code {FACE_ERR_UNSUPPORTED})" in str(err):
+            return FACE_ERR_UNSUPPORTED
+        raise
 
 
 def ptr(t):

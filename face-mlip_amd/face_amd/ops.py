@@ -371,12 +371,12 @@ class CPRadialDensity(torch.autograd.Function):
     def forward(ctx, h2, w_cp, b_cp, env, msg, Y, graph, gathered):
         _lib.require_gpu(h2, env, msg, Y)
         C = msg.shape[1]
-        R = radial_head(h2.detach(), w_cp.detach(), b_cp.detach())                            # (E, 4C)
         env_ = env.contiguous().float()
         msg_, ld_msg = _rows(msg, C)
         Y_, ld_Y = _rows(Y, 20)
-        outs = [torch.empty(k, graph.N, C, device=R.device) for k in RANK_K]
+        outs = [torch.empty(k, graph.N, C, device=h2.device) for k in RANK_K]
         row = graph.col if gathered else None
+        R = radial_head(h2.detach(), w_cp.detach(), b_cp.detach())                            # (E, 4C)
         call("face_cp_density_fwd", ptr(R), R.stride(0), ptr(env_), ptr(msg_), ld_msg, ptr(row), ptr(Y_), ld_Y,
              ptr(graph.row_ptr), graph.N, 0, C, *_lib.ranks_of_blocks(outs), _lib.stream_of(R), label="cp_fwd")
         ctx.save_for_backward(R, w_cp.detach(), env_, msg_, Y_)
@@ -402,9 +402,17 @@ class CPRadialDensity(torch.autograd.Function):
         dY = torch.empty(g.E, 20, device=dev) if need_Y else None
         row = g.col if ctx.gathered else None
         st = _lib.stream_of(R)
-        call("face_cp_radial_bwd", ptr(R), R.stride(0), ptr(env), ptr(msg), msg.stride(0), ptr(row), ptr(Y),
-             Y.stride(0), ptr(g.row_ptr), g.N, 0, C, *_lib.ranks_of_blocks(Gs), ptr(w_t), H, ptr(dh2), H, ptr(dmsg),
-             C, ptr(dY), 20, ptr(denv), st, label="cp_bwd")
+        code = _lib.call_status("face_cp_radial_bwd", ptr(R), R.stride(0), ptr(env), ptr(msg), msg.stride(0), ptr(row),
+                                ptr(Y), Y.stride(0), ptr(g.row_ptr), g.N, 0, C, *_lib.ranks_of_blocks(Gs), ptr(w_t), H,
+                                ptr(dh2), H, ptr(dmsg), C, ptr(dY), 20, ptr(denv), st, label="cp_bwd")
+        if code == _lib.FACE_ERR_UNSUPPORTED:
+            # widths whose staging exceeds the fused kernel's LDS: the pooling backward writes dR
+            # and d h2 = dR W_cp is a separate GEMM
+            dR = torch.empty(g.E, 4 * C, device=dev)
+            call("face_cp_density_bwd", ptr(R), R.stride(0), ptr(env), ptr(msg), msg.stride(0), ptr(row), ptr(Y),
+                 Y.stride(0), ptr(g.row_ptr), g.N, 0, g.max_row, C, *_lib.ranks_of_blocks(Gs), ptr(dR), 4 * C,
+                 ptr(dmsg), C, ptr(dY), 20, ptr(denv), st, label="cp_bwd")
+            torch.mm(dR, w_cp, out=dh2)
         if dmsg is not None and ctx.gathered:
             dtab = torch.empty(g.N, C, device=dev)
             call("face_gather_rows_bwd", ptr(dmsg), C, ptr(g.row_ptr), ptr(g.rev), g.N, C, ptr(dtab), C, st,

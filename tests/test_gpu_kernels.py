@@ -153,10 +153,12 @@ def test_cp_density_ragged_rows(gathered, C):
 
 
 @pytest.mark.parametrize("gathered,C,H", [(False, 160, 64), (True, 160, 64), (True, 96, 32), (False, 64, 16),
-                                          (True, 32, 48)])
+                                          (True, 32, 48), (False, 320, 64)])
 def test_cp_radial_density_fused_backward(gathered, C, H):
-    """R = h2 W^T + b feeding the CP pooling, whose backward returns d h2 = dR W from inside the
-    pooling kernel: outputs and gradients (h2, env, msg, Y) vs the oracle in fp64."""
+    """R = h2 W^T + b feeding the CP pooling, computed with it in one pass (or, at C = 320 where
+    the weight block exceeds one workgroup's LDS, by the separate radial-head and pooling
+    launches), whose backward returns d h2 = dR W from inside the pooling kernel: outputs and
+    gradients (h2, env, msg, Y) vs the oracle in fp64."""
     from face_amd import ops
     say("cp radial density", gathered, C, H)
     g = _G(41, 600, 5)
