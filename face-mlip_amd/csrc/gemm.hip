@@ -182,7 +182,15 @@ extern "C" int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, 
     int n_widest = 16;
     for (int i = 0; i < n_probs; ++i)
         if (probs[i].n > n_widest) n_widest = probs[i].n;
-    const int n_sl = (n_widest + ns_max - 1) / ns_max;
+    int n_sl = (n_widest + ns_max - 1) / ns_max;
+    // small problems: narrower slices until there are two workgroups per CU (each slice re-reads
+    // its rows, from L2)
+    {
+        int64_t wg4 = 0;
+        for (int i = 0; i < n_probs; ++i) wg4 += (probs[i].m + 16 * kGemmBB * 4 - 1) / (16 * kGemmBB * 4);
+        const int n_cu = device_cu_count();
+        while (wg4 * n_sl < 2 * n_cu && (n_widest + n_sl) / (n_sl + 1) >= 16) ++n_sl;
+    }
     const int NS = ((n_widest + n_sl - 1) / n_sl + 15) / 16 * 16;
     GemmArgs A{};
     A.n_probs = n_probs, A.w_kn = w_kn ? 1 : 0, A.bias = bias, A.xs = x_scale, A.ys = y_scale;
