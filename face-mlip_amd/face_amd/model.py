@@ -250,21 +250,21 @@ class FactorBlock(nn.Module):
         C = self.C
         A = self.moments(h, rb, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g)
         allsets = sets + [A]
-        ys = []
-        for l in range(4):
-            W, _ = frozen(self.proj[l])
-            if l == 0:
-                W = W[:C]                                                         # only P0 is used
-            elif l == 3:
-                W = W[:2 * C]                                                     # S3 is unused
-            # proj over the concatenated moment sets as a sum of per-set GEMMs (no concat copy); the
-            # GEMMs after the first accumulate in place in their epilogue (no add or copy pass)
-            y = None
-            for si, S in enumerate(allsets):
-                Ws = W[:, si * C:(si + 1) * C]
-                x2 = S[l].reshape(-1, C)
-                y = x2 @ Ws.t() if y is None else y.addmm_(x2, Ws.t())
-            ys.append(y.view(S[l].shape[0], S[l].shape[1], -1))                   # (k_l, N, 3C | C | 2C)
+        # only P0 of rank 0 and P3, Q3 of rank 3 are used
+        ws = [frozen(self.proj[l])[0][:(C, 3 * C, 3 * C, 2 * C)[l]] for l in range(4)]
+        if C % 16 == 0:
+            # proj over the concatenated moment sets as a sum of per-set products (no concat copy),
+            # all four ranks per launch, later sets accumulating in the epilogue
+            ys = list(ops.rank_proj(ws, allsets))                                # (k_l, N, C | 3C | 3C | 2C)
+        else:
+            ys = []
+            for l in range(4):
+                y = None
+                for si, S in enumerate(allsets):
+                    Ws = ws[l][:, si * C:(si + 1) * C]
+                    x2 = S[l].reshape(-1, C)
+                    y = x2 @ Ws.t() if y is None else y.addmm_(x2, Ws.t())
+                ys.append(y.view(S[l].shape[0], S[l].shape[1], -1))
         if self.eq_out:
             feats, V, Ms = ops.node_features(ys[0], ys[1], ys[2], ys[3], self.vpath.detach(), self.mpath.detach(),
                                              True, C)

@@ -689,3 +689,46 @@ class ScaledMix(torch.autograd.Function):
 
 def scaled_mix(s_tab, group, wm, wt, D1, D2, Af):
     return ScaledMix.apply(s_tab, group, wm, wt, D1, D2, *Af)
+
+
+class RankProj(torch.autograd.Function):
+    """y_l = sum_s S_s,l W_l[:, s C:(s + 1) C]^T for the four ranks l over the moment sets s
+    (face/model.py:537-544, the proj of the concatenated sets as a sum of per-set products):
+    one launch per set, the sets after the first accumulating in the epilogue. The backward
+    gives each set's input gradient, again one launch per set. Weights receive no gradient."""
+
+    @staticmethod
+    def forward(ctx, ws, n_sets, *S):
+        C = S[0].shape[-1]
+        N = S[0].shape[1]
+        dev = S[0].device
+        sets = [S[4 * s:4 * s + 4] for s in range(n_sets)]
+        ys = [torch.empty(sets[0][l].shape[0], N, w.shape[0], device=dev) for l, w in enumerate(ws)]
+        for s, S_s in enumerate(sets):
+            rows_linear([(S_s[l].reshape(-1, C), ws[l][:, s * C:(s + 1) * C], ys[l].view(-1, ws[l].shape[0]), 0,
+                          1.0 if s else 0.0) for l in range(4)], label="proj_fwd")
+        ctx.ws, ctx.n_sets, ctx.C = ws, n_sets, C
+        ctx.shapes = [t.shape for t in S]
+        return tuple(ys)
+
+    @staticmethod
+    def backward(ctx, *gy):
+        C, ws = ctx.C, ctx.ws
+        dev = ws[0].device
+        gy = [(g.contiguous() if g is not None else torch.zeros(sh[0], sh[1], w.shape[0], device=dev))
+              for g, w, sh in zip(gy, ws, ctx.shapes[:4])]
+        grads = []
+        for s in range(ctx.n_sets):
+            need = [ctx.needs_input_grad[2 + 4 * s + l] for l in range(4)]
+            d = [torch.empty(ctx.shapes[4 * s + l], device=dev) if need[l] else None for l in range(4)]
+            probs = [(gy[l].view(-1, ws[l].shape[0]), ws[l][:, s * C:(s + 1) * C], d[l].view(-1, C), 0, 0.0)
+                     for l in range(4) if need[l]]
+            if probs:
+                rows_linear(probs, w_kn=True, label="proj_bwd")
+            grads += d
+        return (None, None, *grads)
+
+
+def rank_proj(ws, sets):
+    """ws: 4 frozen proj weights (n_l, n_sets C); sets: list of 4-tuples of (k_l, N, C) moments."""
+    return RankProj.apply(ws, len(sets), *[t for S in sets for t in S])

@@ -550,3 +550,28 @@ def test_scaled_mix_forward_backward(transport, Cin):
     errs = [rel(a, b) for a, b in zip(A, A2)] + [rel(a, b) for a, b in zip(gr, gr2)]
     say("   errs", errs)
     assert max(errs) < 1e-5, errs
+
+
+@pytest.mark.parametrize("n_sets,C", [(1, 160), (2, 160), (2, 96), (3, 32)])
+def test_rank_proj_forward_backward(n_sets, C):
+    """proj of the concatenated moment sets for the four ranks (face/model.py:537-544) as one launch
+    per set, with the row-sliced weights the node algebra uses (P0 | PQS | PQS | PQ), and the
+    sets' gradients, vs torch fp64 autograd."""
+    from face_amd import ops
+    say("rank proj", n_sets, C)
+    torch.manual_seed(n_sets * C)
+    N = 613
+    full = [torch.randn(3 * C, n_sets * C, device=DEV) / C ** 0.5 for _ in range(4)]
+    ws = [w[:n] for w, n in zip(full, (C, 3 * C, 3 * C, 2 * C))]
+    sets = [[torch.randn(k, N, C, device=DEV, requires_grad=True) for k in (1, 3, 6, 10)] for _ in range(n_sets)]
+    ys = ops.rank_proj(ws, sets)
+    G = [torch.randn_like(y) for y in ys]
+    flat = [t for S in sets for t in S]
+    gr = torch.autograd.grad(sum((y * g).sum() for y, g in zip(ys, G)), flat)
+    c = lambda t: t.detach().double().cpu()
+    flatc = [c(t).requires_grad_(True) for t in flat]
+    ys2 = [sum(flatc[4 * s + l] @ c(ws[l][:, s * C:(s + 1) * C]).T for s in range(n_sets)) for l in range(4)]
+    gr2 = torch.autograd.grad(sum((y * c(g)).sum() for y, g in zip(ys2, G)), flatc)
+    errs = [rel(a, b) for a, b in zip(ys, ys2)] + [rel(a, b) for a, b in zip(gr, gr2)]
+    say("   errs", max(errs))
+    assert max(errs) < 1e-5, errs
