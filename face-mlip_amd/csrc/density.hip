@@ -199,6 +199,158 @@ __global__ __launch_bounds__(kBlock) void density_bwd_kernel(
     }
 }
 
+// ------------------------------------------------------------------ factor backward on MFMA
+// B = 16 basis functions, NX = 20 monomials, K = 16 KB message channels: with the columns of
+// G[i] flattened as (x, b), the 16-column block x is monomial x. Tiles of 16 edges; per monomial
+// x two v_mfma_f32_16x16x4f32 chains:
+//   S[e, b]  = sum_k msg[e, k] G[x, b, k]       (A = msg rows, K index q of instruction r of chunk
+//                                                c = channel 16 c + 4q + r; B = G rows)
+//   dmsg[e, k] += sum_b Y[e, x] phi[e, b] G[x, b, k]   (A = Y[e, x] phi[e, :], K index q of
+//                                                instruction r = basis 4q + r; B = G columns)
+// both with edge 4q + r in register r of lane j + 16q (column j = basis b, resp. channel k).
+// From S: dphi[e, b] += S Y[e, x], and dY[e, x] = sum_b S phi[e, b], a sum over the 16 lanes
+// of a row group. WPA = 1: one wave per atom (kDbWaves atoms per workgroup). WPA > 1: one atom
+// per workgroup, its WPA waves split the monomials and sum their dphi / dmsg partials in LDS
+// (small systems, where one wave per atom leaves the SIMDs idle).
+constexpr int kDbWaves = 8;
+constexpr int kDbYS = 21;                                // Y tile row stride (floats)
+
+template <int KB, int WPA>
+__global__ __launch_bounds__((WPA > 1 ? WPA : kDbWaves) * kWave) void density_bwd_mfma_kernel(
+    const float* __restrict__ phi, int ld_phi, const float* __restrict__ msg, int ld_msg,
+    const int32_t* __restrict__ msg_row, const float* __restrict__ Y, int ld_Y, const int32_t* __restrict__ row_ptr,
+    int64_t N, int M, RankIn G, float* __restrict__ dphi, int ld_dphi, float* __restrict__ dmsg, int ld_dmsg,
+    float* __restrict__ dY, int ld_dY) {
+    constexpr int K = 16 * KB, NXW = 20 / WPA, NSLOT = (NXW + 15) / 16;
+    constexpr int YW = WPA > 1 ? 1 : kDbWaves;           // Y tiles: one per atom of the workgroup
+    constexpr int PW = WPA > 1 ? WPA : 1;
+    __shared__ float sY[YW][16 * kDbYS];
+    __shared__ float sP[PW][16 * (16 + K)];               // dphi | dmsg partials (WPA > 1)
+    const int lane = threadIdx.x & (kWave - 1), j = lane & 15, q = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int64_t n = WPA > 1 ? (int64_t)blockIdx.x : (int64_t)blockIdx.x * kDbWaves + wv;
+    if (n >= N) return;                                  // WPA = 1 only: no workgroup barrier there
+    const int x0 = WPA > 1 ? wv * NXW : 0;
+    float* ys = sY[WPA > 1 ? 0 : wv];
+    const v4f z4 = {0.f, 0.f, 0.f, 0.f};
+    int64_t a, bnd;
+    row_range(row_ptr, n, M, a, bnd);
+    for (int64_t e0 = a; e0 < bnd; e0 += 16) {
+        const int ne = (int)min((int64_t)16, bnd - e0);
+        // the tile's Y (16 x 20) into LDS, zero past the row end
+        if (WPA > 1) {
+            __syncthreads();                             // previous tile's Y and partials consumed
+            for (int v = threadIdx.x; v < 320; v += WPA * kWave) {
+                const int t = v / 20, x = v - t * 20;
+                ys[t * kDbYS + x] = t < ne ? Y[(e0 + t) * ld_Y + x] : 0.f;
+            }
+            __syncthreads();
+        } else {
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int u = 0; u < 5; ++u) {
+                const int v = u * kWave + lane, t = v / 20, x = v - t * 20;
+                ys[t * kDbYS + x] = t < ne ? Y[(e0 + t) * ld_Y + x] : 0.f;
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+        // edge e0 + j: message row and phi[4q .. 4q + 3] (A operands), zero past the row end
+        const bool oki = j < ne;
+        const int64_t ei = e0 + min(j, ne - 1);
+        const int64_t rowi = msg_row ? (int64_t)msg_row[ei] : ei;
+        v4f mA[KB];
+#pragma unroll
+        for (int c = 0; c < KB; ++c) mA[c] = oki ? ld4(msg + rowi * ld_msg + 16 * c + 4 * q) : z4;
+        const v4f ph4 = oki ? ld4(phi + ei * ld_phi + 4 * q) : z4;
+        // edges e0 + 4q + r at basis j (for dY)
+        float phT[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) phT[r] = phi[(e0 + min(4 * q + r, ne - 1)) * ld_phi + j];
+        v4f dph = z4, dm[KB];
+#pragma unroll
+        for (int c = 0; c < KB; ++c) dm[c] = z4;
+        float dyk[4][NSLOT];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int sl = 0; sl < NSLOT; ++sl) dyk[r][sl] = 0.f;
+#pragma unroll 2
+        for (int xx = 0; xx < NXW; ++xx) {
+            const int x = x0 + xx;
+            const float* gx = G.at(n, x);                // (16 b) x K
+            v4f sv = z4;
+#pragma unroll
+            for (int c = 0; c < KB; ++c) {
+                const v4f gv = ld4(gx + j * K + 16 * c + 4 * q);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sv = mfma_16x16x4(mA[c][r], gv[r], sv);
+            }
+            const float yi = ys[j * kDbYS + x];
+#pragma unroll
+            for (int c = 0; c < KB; ++c)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) dm[c] = mfma_16x16x4(yi * ph4[r], gx[(4 * q + r) * K + 16 * c + j], dm[c]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                dph[r] = fmaf(sv[r], ys[(4 * q + r) * kDbYS + x], dph[r]);
+                float v = sv[r] * phT[r];
+                v += __shfl_xor(v, 1, kWave);
+                v += __shfl_xor(v, 2, kWave);
+                v += __shfl_xor(v, 4, kWave);
+                v += __shfl_xor(v, 8, kWave);
+                if (j == (xx & 15)) dyk[r][xx >> 4] = v;
+            }
+        }
+        // dY of this wave's monomials
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = 4 * q + r;
+            if (dY && t < ne) {
+#pragma unroll
+                for (int sl = 0; sl < NSLOT; ++sl)
+                    if (16 * sl + j < NXW) dY[(e0 + t) * ld_dY + x0 + 16 * sl + j] = dyk[r][sl];
+            }
+        }
+        if (WPA > 1) {
+            // partials of the WPA waves summed by wave 0
+            float* mine = sP[wv];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                mine[(4 * q + r) * 16 + j] = dph[r];
+#pragma unroll
+                for (int c = 0; c < KB; ++c) mine[256 + (4 * q + r) * K + 16 * c + j] = dm[c][r];
+            }
+            __syncthreads();
+            if (wv == 0) {
+#pragma unroll
+                for (int w = 1; w < WPA; ++w) {
+                    const float* o = sP[w];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        dph[r] += o[(4 * q + r) * 16 + j];
+#pragma unroll
+                        for (int c = 0; c < KB; ++c) dm[c][r] += o[256 + (4 * q + r) * K + 16 * c + j];
+                    }
+                }
+            }
+        }
+        if (WPA == 1 || wv == 0) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = 4 * q + r;
+                if (t < ne) {
+                    const int64_t e = e0 + t;
+                    if (dphi) dphi[e * ld_dphi + j] = dph[r];
+                    if (dmsg) {
+#pragma unroll
+                        for (int c = 0; c < KB; ++c) dmsg[e * ld_dmsg + 16 * c + j] = dm[c][r];
+                    }
+                }
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------------ CP forward
 // Workgroup = (atom i, channel chunk); thread = channel c with 20 accumulators. Per edge it
 // streams R[e,0..3,c] and msg[m(e),c] (coalesced over c); Y and env are staged in LDS.
@@ -905,9 +1057,36 @@ extern "C" int face_density_bwd(const float* phi, int32_t ld_phi, const float* m
     if (N == 0 || max_row == 0) return 0;
     RankIn G;
     if (!phi || !msg || !Y || !rank_in(G_ranks, atom_stride, x_stride, NX, G)) return FACE_ERR_ARG;
+    hipStream_t st = (hipStream_t)stream;
+    // matrix cores: 20 monomials, B = 16, whole 16-channel blocks, 16-byte aligned rows
+    if (NX == 20 && B == 16 && K % 16 == 0 && K <= 64 && ld_phi % 4 == 0 && ld_msg % 4 == 0 && G.sa % 4 == 0 &&
+        G.sx % 4 == 0 && ((uintptr_t)phi & 15) == 0 && ((uintptr_t)msg & 15) == 0 && ((uintptr_t)G.p[0] & 15) == 0 &&
+        ((uintptr_t)G.p[1] & 15) == 0 && ((uintptr_t)G.p[2] & 15) == 0 && ((uintptr_t)G.p[3] & 15) == 0) {
+        // small systems: split each atom's monomials over 4 waves (one atom per workgroup)
+        const bool split = N < (int64_t)device_cu_count() * 16;
+        const dim3 grid(split ? (unsigned)N : (unsigned)((N + kDbWaves - 1) / kDbWaves));
+        const dim3 block(split ? 4 * kWave : kDbWaves * kWave);
+#define FACE_DBM(KB_)                                                                                           \
+    do {                                                                                                        \
+        if (split)                                                                                              \
+            hipLaunchKernelGGL((density_bwd_mfma_kernel<KB_, 4>), grid, block, 0, st, phi, ld_phi, msg, ld_msg,  \
+                               msg_row, Y, ld_Y, row_ptr, N, M, G, dphi, ld_dphi, dmsg, ld_dmsg, dY, ld_dY);     \
+        else                                                                                                    \
+            hipLaunchKernelGGL((density_bwd_mfma_kernel<KB_, 1>), grid, block, 0, st, phi, ld_phi, msg, ld_msg,  \
+                               msg_row, Y, ld_Y, row_ptr, N, M, G, dphi, ld_dphi, dmsg, ld_dmsg, dY, ld_dY);     \
+    } while (0)
+        switch (K / 16) {
+            case 1: FACE_DBM(1); break;
+            case 2: FACE_DBM(2); break;
+            case 3: FACE_DBM(3); break;
+            default: FACE_DBM(4); break;
+        }
+#undef FACE_DBM
+        FACE_LAUNCH_CHECK();
+        return 0;
+    }
     int ks = 8, glog = 2, nthr = 128;
     if (!plan_bwd(K, max_row, ks, glog, nthr)) return FACE_ERR_UNSUPPORTED;
-    hipStream_t st = (hipStream_t)stream;
     if (NX == 20)
         return launch_bwd_nx<20>(B, ks, glog, nthr, N, st, phi, ld_phi, msg, ld_msg, msg_row, Y, ld_Y, row_ptr, M, K,
                                  G, dphi, ld_dphi, dmsg, ld_dmsg, dY, ld_dY);
