@@ -107,6 +107,65 @@ __global__ __launch_bounds__(kBlock) void density_fwd_kernel(
     }
 }
 
+// ------------------------------------------------------------------ factor forward on MFMA
+// B = 16, NX = 20, K = 16 KB: for monomial x, D[x] (16 b x K) = sum_e U_x[e, :]^T msg[e, :] with
+// U_x[e, b] = Y[e, x] phi[e, b] -- per 16-edge tile a v_mfma_f32_16x16x4f32 chain with A = U_x^T
+// (basis j, K index q of instruction r = edge 4q + r) and B = msg rows, accumulating basis
+// 4q + r, channel j in register r of lane j + 16q. One atom per workgroup, its 4 waves own 5
+// monomials each (no cross-wave sums).
+constexpr int kDfWaves = 4;
+
+template <int KB>
+__global__ __launch_bounds__(kDfWaves * kWave) void density_fwd_mfma_kernel(
+    const float* __restrict__ phi, int ld_phi, const float* __restrict__ msg, int ld_msg,
+    const int32_t* __restrict__ msg_row, const float* __restrict__ Y, int ld_Y, const int32_t* __restrict__ row_ptr,
+    int M, RankOut D) {
+    constexpr int K = 16 * KB, NXW = 20 / kDfWaves;
+    const int lane = threadIdx.x & (kWave - 1), j = lane & 15, q = lane >> 4;
+    const int x0 = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave) * NXW;
+    const int64_t n = blockIdx.x;
+    const v4f z4 = {0.f, 0.f, 0.f, 0.f};
+    v4f acc[NXW][KB];
+#pragma unroll
+    for (int xx = 0; xx < NXW; ++xx)
+#pragma unroll
+        for (int c = 0; c < KB; ++c) acc[xx][c] = z4;
+    int64_t a, bnd;
+    row_range(row_ptr, n, M, a, bnd);
+    for (int64_t e0 = a; e0 < bnd; e0 += 16) {
+        const int ne = (int)min((int64_t)16, bnd - e0);
+        float phT[4], yv[NXW][4], mb[KB][4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = 4 * q + r;
+            const int64_t e = e0 + min(t, ne - 1);       // clamped: loads stay in the row
+            const float p = phi[e * ld_phi + j];
+            phT[r] = t < ne ? p : 0.f;                   // zero past the row end
+            const int64_t row = msg_row ? (int64_t)msg_row[e] : e;
+#pragma unroll
+            for (int c = 0; c < KB; ++c) mb[c][r] = msg[row * ld_msg + 16 * c + j];
+#pragma unroll
+            for (int xx = 0; xx < NXW; ++xx) yv[xx][r] = Y[e * ld_Y + x0 + xx];
+        }
+#pragma unroll
+        for (int xx = 0; xx < NXW; ++xx)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float u = yv[xx][r] * phT[r];
+#pragma unroll
+                for (int c = 0; c < KB; ++c) acc[xx][c] = mfma_16x16x4(u, mb[c][r], acc[xx][c]);
+            }
+    }
+#pragma unroll
+    for (int xx = 0; xx < NXW; ++xx) {
+        float* dx = D.at(n, x0 + xx);
+#pragma unroll
+        for (int c = 0; c < KB; ++c)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dx[(4 * q + r) * K + 16 * c + j] = acc[xx][c][r];
+    }
+}
+
 // ------------------------------------------------------------------ factor backward
 // Workgroup = atom i; G[i] (NX x B x K) is staged in LDS, split in GN k-slices of KS
 // columns (slice stride KSP, 16-byte aligned). A lane is (edge slot, k-slice g): it keeps
@@ -1025,6 +1084,20 @@ extern "C" int face_density_fwd(const float* phi, int32_t ld_phi, const float* m
     if (N == 0) return 0;
     RankOut D;
     if (!phi || !msg || !Y || !rank_out(D_ranks, atom_stride, x_stride, NX, D)) return FACE_ERR_ARG;
+    if (NX == 20 && B == 16 && K % 16 == 0 && K <= 64) {          // matrix cores
+#define FACE_DFM(KB_)                                                                                          \
+    hipLaunchKernelGGL(density_fwd_mfma_kernel<KB_>, dim3((unsigned)N), dim3(kDfWaves * kWave), 0,             \
+                       (hipStream_t)stream, phi, ld_phi, msg, ld_msg, msg_row, Y, ld_Y, row_ptr, M, D)
+        switch (K / 16) {
+            case 1: FACE_DFM(1); break;
+            case 2: FACE_DFM(2); break;
+            case 3: FACE_DFM(3); break;
+            default: FACE_DFM(4); break;
+        }
+#undef FACE_DFM
+        FACE_LAUNCH_CHECK();
+        return 0;
+    }
     const int BK = B * K;
     const int opts20[3] = {1, 2, 4}, opts4[4] = {1, 2, 4, 9};
     const int* opts = NX == 20 ? opts20 : opts4;
