@@ -30,7 +30,8 @@ METRIC = "atom-steps/s (E+F, fp32) at 864 & 24k atoms; density-kernel HBM GB/s"
 HBM_PEAK_GBS = 8000.0
 TIMED = ["density_fwd20", "density_bwd20", "cp_fwd", "cp_bwd", "transport_fwd", "transport_bwd", "dir_fwd",
          "dir_bwd", "node_fwd", "node_bwd", "edge_fwd", "edge_bwd", "force_scatter", "gather_bwd", "radial_fwd",
-         "radial_bwd", "radial_head", "edge_msg_fwd", "edge_msg_bwd"]
+         "radial_bwd", "radial_head", "edge_msg_fwd", "edge_msg_bwd", "mix_fwd", "mix_bwd", "proj_fwd", "proj_bwd"]
+MFMA_PEAK_TFS = 157.3                   # MI355X dense fp32 MFMA
 
 
 def log(*a):
@@ -78,6 +79,18 @@ def algorithmic_bytes(label, g, kw):
         return 4 * (E * (Kd4 + 1 + K) + N * K)
     if label == "edge_msg_bwd":         # upstream (E, K), rev in; d d (E, 4Kd) and the table gradient out
         return 4 * (E * (K + 1 + Kd4) + N * K)
+    return None
+
+
+def algorithmic_flops(label, g, kw):
+    """MFMA flops per launch of the row-GEMM labels: the four ranks (20 monomial rows per atom)
+    of one pass (mix) or of one moment set (proj: output widths C, 3C, 3C, 2C)."""
+    N, C = g.N, kw["C"]
+    cin = C if kw.get("cp") else kw["B"] * kw["K"]
+    if label in ("mix_fwd", "mix_bwd"):
+        return 2 * 20 * N * cin * C
+    if label in ("proj_fwd", "proj_bwd"):
+        return 2 * N * C * (C + 3 * 3 * C + 6 * 3 * C + 10 * 2 * C)
     return None
 
 
@@ -146,9 +159,11 @@ def run_gpu(k, steps, warmup, use_graph=True):
         ms = [s.elapsed_time(e) for s, e in evs]
         avg_us = 1e3 * float(np.mean(ms))
         byts = algorithmic_bytes(label, g, kw)
+        fl = algorithmic_flops(label, g, kw)
         kern[label] = {"launches_per_step": len(evs) / steps, "avg_us": avg_us,
                        "ms_per_step": float(np.sum(ms)) / steps,
-                       "alg_bytes": byts, "GBps": (byts / (avg_us * 1e-6) / 1e9) if byts else None}
+                       "alg_bytes": byts, "GBps": (byts / (avg_us * 1e-6) / 1e9) if byts else None,
+                       "TFLOPs": (fl / (avg_us * 1e-6) / 1e12) if fl else None}
     ms_step = 1e3 * dt / steps
     log(f"[bench]   {ms_step:.3f} ms/step, {g.N * steps / dt:.0f} atom-steps/s")
     return {"N": g.N, "E": g.E, "ms_per_step": ms_step, "atom_steps_per_s": g.N * steps / dt, "kernels": kern,
@@ -255,7 +270,7 @@ def main():
                                     "atom_steps_per_s": r["atom_steps_per_s"], "ms_per_step": r["ms_per_step"],
                                     "pairlist_ms": r["pairlist_ms"], "mode": r["mode"],
                                     "eager_ms_per_step": r["eager_ms_per_step"],
-                                    "kernels": {kk: {"avg_us": v["avg_us"], "GBps": v["GBps"]}
+                                    "kernels": {kk: {"avg_us": v["avg_us"], "GBps": v["GBps"], "TFLOPs": v["TFLOPs"]}
                                                 for kk, v in r["kernels"].items()}}
     kern = main_run["kernels"]
     hbm = {k: v for k, v in kern.items() if v["alg_bytes"]}
@@ -285,7 +300,9 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": {k: {"avg_us": v["avg_us"], "launches_per_step": v["launches_per_step"], "GBps": v["GBps"],
-                        "frac_hbm": (v["GBps"] / HBM_PEAK_GBS) if v["GBps"] else None} for k, v in kern.items()},
+                        "frac_hbm": (v["GBps"] / HBM_PEAK_GBS) if v["GBps"] else None,
+                        "TFLOPs": v["TFLOPs"], "frac_mfma": (v["TFLOPs"] / MFMA_PEAK_TFS) if v["TFLOPs"] else None}
+                    for k, v in kern.items()},
         "pairlist_ms": main_run["pairlist_ms"],
         "also": also,
     }
