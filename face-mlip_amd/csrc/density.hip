@@ -882,17 +882,29 @@ __global__ __launch_bounds__(kLdsWaves * kWave) void cp_radial_bwd_lds_kernel(
                 }
             }
             if (active) {
-                v4f dm[2] = {z4, z4};
+                // t for every (rank, half) first, so no MFMA result is read right after its issue;
+                // the chunk operands are read unmasked: yq is 0 on the lanes past a chunk's length
+                // (only the last chunk's rows run past monomial 19 and are clamped to it)
+                v4f tt[4][2];
 #pragma unroll
-                for (int l = 0; l < 4; ++l) {
+                for (int l = 0; l < 4; ++l)
 #pragma unroll
                     for (int h = 0; h < 2; ++h) {
                         v4f t = z4;
 #pragma unroll
                         for (int k = kRankChunk0[l]; k < kRankChunk1[l]; ++k) {
-                            const float a = q < kChunkLen[k] ? sg[t_off + kChunkX0[k] * GS + cs + 16 * h] : 0.f;
-                            t = mfma_16x16x4(a, yq[k], t);
+                            const int xr = kChunkX0[k] + 3 < 20 ? t_off + kChunkX0[k] * GS
+                                                                 : min(kChunkX0[k] + q, 19) * GS + j;
+                            t = mfma_16x16x4(sg[xr + cs + 16 * h], yq[k], t);
                         }
+                        tt[l][h] = t;
+                    }
+                v4f dm[2] = {z4, z4};
+#pragma unroll
+                for (int l = 0; l < 4; ++l) {
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const v4f t = tt[l][h];
                         const v4f g = (ev * m[h]) * t;
                         const float* wl = sW + j * kSlabRS + l * kCpStep + 16 * h + own;
 #pragma unroll
