@@ -69,9 +69,17 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
             st4(sW + r * SK + 4 * c4, r < ns ? ld4(P.w + (int64_t)(n0 + r) * P.ld_w + 4 * c4) : z4);
         }
     } else {                                                             // W given as (K, n)
-        for (int v = tid; v < 16 * NB * K; v += blockDim.x) {
-            const int k = v / (16 * NB), r = v - k * (16 * NB);
-            sW[r * SK + k] = r < ns ? P.w[(int64_t)k * P.ld_w + n0 + r] : 0.f;
+        // thread (k4, r): four coalesced reads down column n0 + r, one float4 into row r
+        const int nr = 16 * NB;
+        for (int v = tid; v < nr * (K / 4); v += blockDim.x) {
+            const int k4 = v / nr, r = v - k4 * nr;
+            v4f c4 = z4;
+            if (r < ns) {
+                const float* col = P.w + (int64_t)(4 * k4) * P.ld_w + n0 + r;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) c4[u] = col[(int64_t)u * P.ld_w];
+            }
+            st4(sW + r * SK + 4 * k4, c4);
         }
     }
     __syncthreads();
