@@ -28,7 +28,8 @@ import torch  # noqa: E402
 
 METRIC = "atom-steps/s (E+F, fp32) at 864 & 24k atoms; density-kernel HBM GB/s"
 HBM_PEAK_GBS = 8000.0
-TIMED = ["density_fwd20", "density_bwd20", "cp_fwd", "cp_bwd", "transport_fwd", "transport_bwd", "dir_fwd",
+TIMED = ["density_fwd20", "density_bwd20", "cp_fwd", "cp_fwd_tab", "cp_bwd", "cp_bwd_tab", "cp_radial_bwd",
+         "cp_radial_bwd_tab", "transport_fwd", "transport_bwd", "dir_fwd",
          "dir_bwd", "node_fwd", "node_bwd", "edge_fwd", "edge_bwd", "force_scatter", "gather_bwd", "radial_fwd",
          "radial_bwd", "radial_head", "edge_msg_fwd", "edge_msg_bwd", "mix_fwd", "mix_bwd", "proj_fwd", "proj_bwd"]
 MFMA_PEAK_TFS = 157.3                   # MI355X dense fp32 MFMA
@@ -53,10 +54,18 @@ def algorithmic_bytes(label, g, kw):
         return 4 * (E * (B + 3 + Kt // 2) + 18 * N * B * kw["K_dir"])
     if label == "transport_bwd":          # + upstream sums; dphi, du, per-edge table gradient out
         return 4 * (E * (B + 3 + Kt // 2) + 18 * N * B * kw["K_dir"] + E * (B + 3 + Kt // 2))
-    if label == "cp_fwd":
-        return 4 * (E * (5 * C + 20) + 20 * N * C)
-    if label == "cp_bwd":
-        return 4 * (2 * E * (5 * C + 20) + 20 * N * C)
+    if label.startswith("cp_"):
+        # R (4C), env, Y (20) per edge; messages per edge (E x C) or a node table gathered
+        # through col (N x C + E); 20 N C pooled sums out (forward) or upstream in (backward)
+        msg = N * C + E if label.endswith("_tab") else E * C
+        ins = E * (4 * C + 1 + 20) + msg + 20 * N * C
+        if label.startswith("cp_fwd"):
+            return 4 * ins
+        H = kw.get("radial_hidden", 64)
+        if label.startswith("cp_radial_bwd"):   # + W_cp; d h2 (H), d msg (C), dY (20), d env per edge out
+            return 4 * (ins + 4 * C * H + E * (H + C + 20 + 1))
+        if label.startswith("cp_bwd"):          # dR (4C), d msg, dY, d env per edge out
+            return 4 * (ins + E * (4 * C + C + 20 + 1))
     if label == "node_fwd":
         return 4 * 67 * N * C           # 47 in; 8 invariants + V (3) + full Mf (9) out
     if label == "node_bwd":
@@ -83,14 +92,21 @@ def algorithmic_bytes(label, g, kw):
 
 
 def algorithmic_flops(label, g, kw):
-    """MFMA flops per launch of the row-GEMM labels: the four ranks (20 monomial rows per atom)
-    of one pass (mix) or of one moment set (proj: output widths C, 3C, 3C, 2C)."""
-    N, C = g.N, kw["C"]
+    """Matrix-product flops per launch: the row GEMMs (the four ranks, 20 monomial rows per atom,
+    of one mix pass or of one moment set of the proj: output widths C, 3C, 3C, 2C), the radial
+    head (E x H by H x 4C), and the fused CP radial backward (d h2 = dR W_cp, E x 4C by 4C x H,
+    plus the two 20-monomial contractions per edge and channel)."""
+    N, E, C = g.N, g.E, kw["C"]
+    H = kw.get("radial_hidden", 64)
     cin = C if kw.get("cp") else kw["B"] * kw["K"]
     if label in ("mix_fwd", "mix_bwd"):
         return 2 * 20 * N * cin * C
     if label in ("proj_fwd", "proj_bwd"):
         return 2 * N * C * (C + 3 * 3 * C + 6 * 3 * C + 10 * 2 * C)
+    if label == "radial_head":
+        return 2 * E * H * 4 * C
+    if label.startswith("cp_radial_bwd"):
+        return 2 * E * (4 * C * H + 2 * 20 * C)
     return None
 
 
@@ -162,7 +178,7 @@ def run_gpu(k, steps, warmup, use_graph=True):
         fl = algorithmic_flops(label, g, kw)
         kern[label] = {"launches_per_step": len(evs) / steps, "avg_us": avg_us,
                        "ms_per_step": float(np.sum(ms)) / steps,
-                       "alg_bytes": byts, "GBps": (byts / (avg_us * 1e-6) / 1e9) if byts else None,
+                       "alg_bytes": byts, "alg_flops": fl, "GBps": (byts / (avg_us * 1e-6) / 1e9) if byts else None,
                        "TFLOPs": (fl / (avg_us * 1e-6) / 1e12) if fl else None}
     ms_step = 1e3 * dt / steps
     log(f"[bench]   {ms_step:.3f} ms/step, {g.N * steps / dt:.0f} atom-steps/s")
@@ -174,22 +190,27 @@ def run_gpu(k, steps, warmup, use_graph=True):
 def pmc_probe(k, steps=2, copy_floats=1 << 28):
     """Short run for hardware-counter passes: a few eager E+F steps of workload k, then a plain
     device-to-device copy of a known size, whose FETCH_SIZE / WRITE_SIZE readings calibrate the
-    counters (bytes known / counter reading)."""
+    counters (bytes known / counter reading). The JSON line lists the library calls in launch
+    order, which assigns the profiler's dispatches to call labels."""
     from face_amd import systems
     from face_amd.neighbors import build_graph
     sts, kw, el, desc = systems.workload(k)
     g = build_graph(sts, kw["rc"])
     m = model_for(kw, el)
+    from face_amd import _lib
+    order = _lib.record_order(True)
     for _ in range(steps):
         m(g.with_pos(g.pos.clone()))["forces"]
     torch.cuda.synchronize()
+    _lib.record_order(False)
     src = torch.ones(copy_floats, device="cuda")
     dst = torch.empty_like(src)
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
     out = {"probe": desc, "steps": steps, "copy_bytes_read": 4 * copy_floats, "copy_bytes_written": 4 * copy_floats,
-           "alg_bytes": {lab: algorithmic_bytes(lab, g, kw) for lab in TIMED}}
+           "alg_bytes": {lab: algorithmic_bytes(lab, g, kw) for lab in TIMED},
+           "alg_flops": {lab: algorithmic_flops(lab, g, kw) for lab in TIMED}, "order": order}
     print(json.dumps(out), flush=True)
 
 
@@ -273,15 +294,23 @@ def main():
                                     "kernels": {kk: {"avg_us": v["avg_us"], "GBps": v["GBps"], "TFLOPs": v["TFLOPs"]}
                                                 for kk, v in r["kernels"].items()}}
     kern = main_run["kernels"]
-    hbm = {k: v for k, v in kern.items() if v["alg_bytes"]}
-    dom = max(hbm, key=lambda k: hbm[k]["ms_per_step"]) if hbm else None
+    known = {k: v for k, v in kern.items() if v["alg_bytes"] or v["alg_flops"]}
+    dom = max(known, key=lambda k: known[k]["ms_per_step"]) if known else None
     roofline = None
     if dom:
-        ach = hbm[dom]["GBps"]
-        roofline = {"kernel": dom, "bound": "hbm", "achieved": ach, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": ach / HBM_PEAK_GBS,
-                    "traffic": measured_traffic(dom) if a.workload == 3 else None, "alg_bytes_per_launch": hbm[dom]["alg_bytes"],
-                    "avg_launch_us": hbm[dom]["avg_us"]}
+        # the bound is the larger of the two floors: algorithmic bytes at peak HBM bandwidth and
+        # algorithmic flops at the dense fp32 MFMA peak
+        v = known[dom]
+        t_hbm = (v["alg_bytes"] or 0) / (HBM_PEAK_GBS * 1e9)
+        t_mfma = (v["alg_flops"] or 0) / (MFMA_PEAK_TFS * 1e12)
+        if t_mfma > t_hbm:
+            bound, ach, peak, unit = "mfma", v["TFLOPs"], MFMA_PEAK_TFS, "TFLOP/s"
+        else:
+            bound, ach, peak, unit = "hbm", v["GBps"], HBM_PEAK_GBS, "GB/s"
+        roofline = {"kernel": dom, "bound": bound, "achieved": ach, "peak": peak, "unit": unit, "frac": ach / peak,
+                    "traffic": measured_traffic(dom) if a.workload == 3 else None,
+                    "alg_bytes_per_launch": v["alg_bytes"], "alg_flops_per_launch": v["alg_flops"],
+                    "GBps": v["GBps"], "TFLOPs": v["TFLOPs"], "avg_launch_us": v["avg_us"]}
     cpu = None
     if not a.no_cpu:
         log("[bench] cpu baseline ...")

@@ -961,6 +961,238 @@ __global__ __launch_bounds__(kLdsWaves * kWave) void cp_radial_bwd_lds_kernel(
     }
 }
 
+// ------------------------------------------------------------------ CP radial backward, resident W
+// The product of cp_radial_bwd_lds_kernel when all of W^T (H x 4C) fits in LDS: W^T is staged
+// once per workgroup (rows unpadded, float4 chunk c of row h stored at chunk c ^ (h & 15), so the
+// 16 rows read by one instruction fall on distinct banks) and every wave then works alone, with
+// no workgroup barrier: wave w owns the atom rows whose first edge lies in the w-th equal share
+// of the edges, walks their 16-edge tiles in 16-channel steps, reads gA straight from memory and
+// loads the next step's operands while the current step computes. Lane (j, q) holds channels
+// c0 + 4q .. c0 + 4q + 3 of edge j of the tile for R, m, t and dR; the dh2 accumulator D rows
+// are edges 4q + r, columns hidden units 16 hb + j.
+constexpr int kResStep = 16;                          // channels per step (C % kResStep == 0)
+// rank of the monomials of chunk k (kChunkX0 / kChunkLen)
+__device__ constexpr int kChunkRank[7] = {0, 1, 2, 2, 3, 3, 3};
+
+// Smallest r in [0, n] with a[r] >= target (a nondecreasing, a[n] >= target), the 64 lanes of
+// the wave probing 64 points per pass; the result is wave-uniform.
+__device__ __forceinline__ int64_t wave_lower_bound(const int32_t* __restrict__ a, int64_t n, int64_t target,
+                                                    int lane) {
+    int64_t lo = 0, hi = n;
+    while (lo < hi) {
+        const int64_t step = (hi - lo + kWave - 1) / kWave;
+        const int64_t p = min(lo + (int64_t)lane * step, hi);
+        const uint64_t m = __ballot(a[p] >= target);      // a[hi] >= target: clamped probes are true
+        if (m == 0) {
+            lo += (int64_t)(kWave - 1) * step + 1;
+        } else {
+            const int f = __ffsll((unsigned long long)m) - 1;
+            const int64_t pf = min(lo + (int64_t)f * step, hi);
+            if (f > 0) lo += (int64_t)(f - 1) * step + 1;
+            hi = pf;
+        }
+    }
+    return lo < n ? lo : n;
+}
+
+// A wave-uniform 64-bit value held in scalar registers.
+__device__ __forceinline__ int64_t uniform64(int64_t v) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)((uint64_t)v >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+template <int HB, int NW, bool PF>
+__global__ __launch_bounds__(NW * kWave) void cp_radial_bwd_res_kernel(
+    const float* __restrict__ R, int ld_R, const float* __restrict__ env, const float* __restrict__ msg, int ld_msg,
+    const int32_t* __restrict__ msg_row, const float* __restrict__ Y, int ld_Y, const int32_t* __restrict__ row_ptr,
+    int64_t N, int M, int C, RankIn gA, float* __restrict__ dmsg, int ld_dmsg, float* __restrict__ dY, int ld_dY,
+    float* __restrict__ denv, const float* __restrict__ w_t, float* __restrict__ dh2, int ld_dh2) {
+    constexpr int H = 16 * HB;
+    extern __shared__ float lds[];                    // W^T image, H rows of 4C floats
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int j = lane & 15, q = lane >> 4;
+    const int RS = 4 * C, nch = C;
+    for (int f = tid; f < H * nch; f += NW * kWave) {
+        const int h = f / nch, c = f - h * nch;
+        st4(lds + h * RS + 4 * (c ^ (h & 15)), ld4(w_t + (int64_t)h * RS + 4 * c));
+    }
+    __syncthreads();
+    // this wave's rows: those whose first edge lies in its share of the edges
+    const int64_t W = (int64_t)gridDim.x * NW;
+    const int64_t gw = (int64_t)blockIdx.x * NW + __builtin_amdgcn_readfirstlane(tid / kWave);
+    int64_t row, row_end;
+    if (row_ptr) {
+        const int64_t E = row_ptr[N];
+        row = wave_lower_bound(row_ptr, N, E * gw / W, lane);
+        row_end = wave_lower_bound(row_ptr, N, E * (gw + 1) / W, lane);
+    } else {
+        row = N * gw / W;
+        row_end = N * (gw + 1) / W;
+    }
+    row = uniform64(row);
+    row_end = uniform64(row_end);
+    const int nsteps = C / kResStep;
+    // per-lane monomial offsets (within the rank's block) of the t operands of the 7 chunks
+    // (lanes past a chunk's length read its first monomial; their Y factor is 0) and of the
+    // dY product rows x = j (j < 4, else 0) and x = 4 + j
+    // (32-bit element offsets from the rank block's row start: the host checks 19 sx + C < 2^31)
+    int toff[7];
+#pragma unroll
+    for (int k = 0; k < 7; ++k)
+        toff[k] = ((q < kChunkLen[k] ? q : 0) + kChunkX0[k] - rank_start(kChunkRank[k])) * (int)gA.sx + j;
+    const int xlo = j < 4 ? j : 0, xhi = 4 + j;
+    const float sel0 = j == 0 ? 1.f : 0.f, sel1 = (j >= 1 && j < 4) ? 1.f : 0.f;
+    const float sel2 = j < 6 ? 1.f : 0.f, sel3 = j >= 6 ? 1.f : 0.f;
+    const v4f z4 = {0.f, 0.f, 0.f, 0.f};
+    const int own = 4 * q;
+
+    // operands of one (tile, step): R of the 4 ranks, m, the 7 t operands, the dY product rows
+    struct Slot {
+        v4f r[4], m, alo, ahi;
+        float ta[7];
+    };
+    auto load_slot = [&](int64_t rw, int64_t eld, int64_t mr, int st, Slot& s) {
+        const int c0 = st * kResStep;
+        const float* Re = R + eld * ld_R + c0 + own;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) s.r[l] = ld4(Re + l * C);
+        s.m = ld4(msg + mr * ld_msg + c0 + own);
+#pragma unroll
+        for (int k = 0; k < 7; ++k) s.ta[k] = (gA.p[kChunkRank[k]] + rw * gA.sa + c0)[toff[k]];
+        s.alo = ld4(gA.at(rw, xlo) + c0 + own);
+        s.ahi = ld4(gA.at(rw, xhi) + c0 + own);
+    };
+    // per-tile values: Y factors of the chunks, Y rows x = 4 + 4q .. and x = 0 .. 3 for the dY
+    // product, envelope, message row
+    struct Head {
+        float yq[7], ev;
+        v4f yhi, ylo;
+        int64_t eld, mr;
+        bool ok;
+    };
+    auto load_head = [&](int64_t t0, int64_t e1, Head& h) {
+        const int64_t e = t0 + j;
+        h.ok = e < e1;
+        h.eld = h.ok ? e : e1 - 1;
+#pragma unroll
+        for (int k = 0; k < 7; ++k) h.yq[k] = (h.ok && q < kChunkLen[k]) ? Y[h.eld * ld_Y + kChunkX0[k] + q] : 0.f;
+        h.ev = h.ok ? (env ? env[h.eld] : 1.f) : 0.f;
+        h.mr = msg_row ? (int64_t)msg_row[h.eld] : h.eld;
+        h.yhi = ld4(Y + h.eld * ld_Y + 4 + 4 * q);
+        h.ylo = ld4(Y + h.eld * ld_Y);
+    };
+    // tile cursor: (rw, t0, e1) -> the next tile of this wave's rows; false when none is left
+    auto next_tile = [&](int64_t& rw, int64_t& t0, int64_t& e1) -> bool {
+        if (t0 + 16 < e1) {
+            t0 += 16;
+            return true;
+        }
+        while (++rw < row_end) {
+            int64_t a, b;
+            row_range(row_ptr, rw, M, a, b);
+            if (b > a) {
+                t0 = a;
+                e1 = b;
+                return true;
+            }
+        }
+        return false;
+    };
+
+    int64_t rw = row - 1, t0 = 0, e1 = 0;
+    if (!next_tile(rw, t0, e1)) return;
+    Head hd, hn;
+    Slot cur, nxt;
+    load_head(t0, e1, hd);
+    if (PF) load_slot(rw, hd.eld, hd.mr, 0, cur);
+    while (true) {
+        int64_t nrw = rw, nt0 = t0, ne1 = e1;
+        const bool more = next_tile(nrw, nt0, ne1);
+        if (PF && more) load_head(nt0, ne1, hn);
+        v4f dacc[HB];
+#pragma unroll
+        for (int hb = 0; hb < HB; ++hb) dacc[hb] = z4;
+        v4f plo = z4, phi = z4;
+        const int64_t e = t0 + j;
+#pragma unroll 1
+        for (int st = 0; st < nsteps; ++st) {
+            if (!PF) {
+                load_slot(rw, hd.eld, hd.mr, st, cur);
+            } else if (st + 1 < nsteps) {
+                load_slot(rw, hd.eld, hd.mr, st + 1, nxt);
+            } else if (more) {
+                load_slot(nrw, hn.eld, hn.mr, 0, nxt);
+            }
+            const int c0 = st * kResStep;
+            // P[x, e] = sum_c gA[x, c] R_{l(x)}[e, c] m[e, c] for the dY rows (first: it
+            // needs only loaded operands, and covers the latency of the t products below)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+                const float mm = cur.m[rr];
+                plo = mfma_16x16x4(sel0 * cur.alo[rr], cur.r[0][rr] * mm, plo);
+                phi = mfma_16x16x4(sel2 * cur.ahi[rr], cur.r[2][rr] * mm, phi);
+                plo = mfma_16x16x4(sel1 * cur.alo[rr], cur.r[1][rr] * mm, plo);
+                phi = mfma_16x16x4(sel3 * cur.ahi[rr], cur.r[3][rr] * mm, phi);
+            }
+            // t_l[c, e] = sum_{x in rank l} gA[x, c] Y[e, x]
+            v4f tt[4];
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                v4f t = z4;
+#pragma unroll
+                for (int k = kRankChunk0[l]; k < kRankChunk1[l]; ++k) t = mfma_16x16x4(cur.ta[k], hd.yq[k], t);
+                tt[l] = t;
+            }
+            // dR_l = ev m t_l; dh2 += dR_l W_l^T; dm = sum_l R_l t_l
+            v4f dm = z4;
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                const v4f g = (hd.ev * cur.m) * tt[l];
+                const int c4 = ((l * C + c0) >> 2) + q;
+#pragma unroll
+                for (int hb = 0; hb < HB; ++hb) {
+                    const v4f wv = ld4(lds + (16 * hb + j) * RS + 4 * (c4 ^ j));
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) dacc[hb] = mfma_16x16x4(g[rr], wv[rr], dacc[hb]);
+                }
+                dm += cur.r[l] * tt[l];
+            }
+            if (hd.ok && dmsg) st4(dmsg + e * ld_dmsg + c0 + own, hd.ev * dm);
+            if (PF) cur = nxt;
+        }
+        // lane (j, q) holds P[x, e] for x = 4 + 4q + r (hi) and, in lanes q == 0, x = r (lo)
+        float s = 0.f;
+        if (hd.ok) {
+            const v4f yhi = hd.yhi, ylo = hd.ylo;
+            s = yhi[0] * phi[0] + yhi[1] * phi[1] + yhi[2] * phi[2] + yhi[3] * phi[3];
+            if (dY) st4(dY + e * ld_dY + 4 + 4 * q, hd.ev * phi);
+            if (q == 0) {
+                s += ylo[0] * plo[0] + ylo[1] * plo[1] + ylo[2] * plo[2] + ylo[3] * plo[3];
+                if (dY) st4(dY + e * ld_dY, hd.ev * plo);
+            }
+        }
+        s += __shfl_xor(s, 16, kWave);
+        s += __shfl_xor(s, 32, kWave);
+        if (denv && hd.ok && q == 0) denv[e] = s;
+        // dacc[hb] register r of lane (j, q): edge t0 + 4q + r, hidden unit 16 hb + j
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const int64_t er = t0 + 4 * q + rr;
+            if (er < e1) {
+#pragma unroll
+                for (int hb = 0; hb < HB; ++hb) dh2[er * ld_dh2 + 16 * hb + j] = dacc[hb][rr];
+            }
+        }
+        if (!more) break;
+        rw = nrw, t0 = nt0, e1 = ne1;
+        if (PF)
+            hd = hn;
+        else
+            load_head(t0, e1, hd);
+    }
+}
+
 // ------------------------------------------------------------------ launch helpers
 
 template <int NX>
@@ -1184,8 +1416,8 @@ extern "C" int face_density_bwd(const float* phi, int32_t ld_phi, const float* m
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 static bool mfma_layout_ok(const float* R, int ld_R, const float* msg, int ld_msg, const float* Y, int ld_Y, int C,
                            const RankIn& gA, const float* dR, int ld_dR, const float* dmsg, int ld_dmsg,
-                           const float* dY, int ld_dY) {
-    if (C % kCpStep || ld_R % 4 || ld_msg % 4 || ld_Y % 4 || gA.sa % 4 || gA.sx % 4) return false;
+                           const float* dY, int ld_dY, int step = kCpStep) {
+    if (C % step || ld_R % 4 || ld_msg % 4 || ld_Y % 4 || gA.sa % 4 || gA.sx % 4) return false;
     if (!aligned16(R) || !aligned16(msg) || !aligned16(Y)) return false;
     for (int l = 0; l < 4; ++l)
         if (!aligned16(gA.p[l])) return false;
@@ -1255,15 +1487,40 @@ extern "C" int face_cp_radial_bwd(const float* R, int32_t ld_R, const float* env
     if (N == 0) return 0;
     RankIn gA;
     if (!R || !msg || !Y || !rank_in(gA_ranks, atom_stride, x_stride, 20, gA)) return FACE_ERR_ARG;
+    const hipStream_t st = (hipStream_t)stream;
+    const int n_cu = device_cu_count();
+    const size_t lds_res = (size_t)H * 4 * C * sizeof(float);
+    if ((int64_t)lds_res <= device_max_lds() && gA.sx * 19 + C < ((int64_t)1 << 31) &&
+        mfma_layout_ok(R, ld_R, msg, ld_msg, Y, ld_Y, C, gA, nullptr, 0, dmsg, ld_dmsg, dY, ld_dY, kResStep)) {
+        // all of W^T resident in LDS: one workgroup per CU, every wave on its own share of the edges
+        constexpr int kNW = 8;
+        constexpr bool kPF = true;
+#define FACE_CPRES(HB_)                                                                                          \
+    do {                                                                                                         \
+        auto kern = cp_radial_bwd_res_kernel<HB_, kNW, kPF>;                                                          \
+        if (lds_res > 65536 && hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, \
+                                                   (int)lds_res) != hipSuccess)                                  \
+            return FACE_ERR_UNSUPPORTED;                                                                         \
+        hipLaunchKernelGGL(kern, dim3((unsigned)n_cu), dim3(kNW * kWave), lds_res, st, R, ld_R, env, msg, ld_msg, \
+                           msg_row, Y, ld_Y, row_ptr, N, M, C, gA, dmsg, ld_dmsg, dY, ld_dY, denv, w_t, dh2, ld_dh2); \
+    } while (0)
+        switch (H / 16) {
+            case 1: FACE_CPRES(1); break;
+            case 2: FACE_CPRES(2); break;
+            case 3: FACE_CPRES(3); break;
+            default: FACE_CPRES(4); break;
+        }
+#undef FACE_CPRES
+        FACE_LAUNCH_CHECK();
+        return 0;
+    }
     if (!mfma_layout_ok(R, ld_R, msg, ld_msg, Y, ld_Y, C, gA, nullptr, 0, dmsg, ld_dmsg, dY, ld_dY))
         return FACE_ERR_UNSUPPORTED;
     // persistent workgroups, one per CU: W slab + one gA row per wave + per-wave tile counts
     const size_t lds = ((size_t)H * kSlabRS + (size_t)kLdsWaves * 20 * cp_mfma_stride(C) + kLdsWaves) * sizeof(float);
     if ((int64_t)lds > device_max_lds()) return FACE_ERR_UNSUPPORTED;
-    const int n_cu = device_cu_count();
     const int64_t waves = N < (int64_t)n_cu * kLdsWaves ? N : (int64_t)n_cu * kLdsWaves;
     const dim3 grid((unsigned)((waves + kLdsWaves - 1) / kLdsWaves)), block(kLdsWaves * kWave);
-    const hipStream_t st = (hipStream_t)stream;
 #define FACE_CPR(HB_)                                                                                            \
     do {                                                                                                         \
         auto kern = cp_radial_bwd_lds_kernel<HB_>;                                                               \

@@ -112,6 +112,18 @@ def stop_timing():
     return t
 
 
+# Optional call log: the label (or entry-point name) of every successful call, in call order,
+# for matching a profiler's dispatch list to the calls that launched it.
+_order = None
+
+
+def record_order(on=True):
+    """Start (on) or stop logging call labels; returns the list being filled (or None)."""
+    global _order
+    _order = [] if on else None
+    return _order
+
+
 def call(name, *args, label=None):
     """Call entry point `name`; raise RuntimeError on a non-zero status. `label` names the
     launch for time_calls (defaults to the entry-point name)."""
@@ -128,6 +140,8 @@ def call(name, *args, label=None):
     if code != 0:
         msg = lib().face_hip_error_string(code).decode()
         raise RuntimeError(f"{name} failed: {msg} (code {code})")
+    if _order is not None:
+        _order.append(key)
 
 
 FACE_ERR_UNSUPPORTED = -2

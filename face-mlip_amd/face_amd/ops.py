@@ -312,6 +312,12 @@ def density(phi, msg, Y, graph, nx=20, gathered=False):
     return Density.apply(phi, msg, Y, graph, nx, gathered)
 
 
+def _cp_label(base, gathered):
+    """Timing label of a CP pooling launch: "_tab" when the messages are node-table rows gathered
+    through col (N x C read) rather than per-edge rows (E x C)."""
+    return base + ("_tab" if gathered else "")
+
+
 class CPDensity(torch.autograd.Function):
     """CP pooling A_l (k_l, N, C) = sum over row i of env R[:, l, c] msg[:, c] Y[:, x in l]
     (face/model.py:496-502, envelope of face/model.py:469 folded in); four rank blocks."""
@@ -327,7 +333,8 @@ class CPDensity(torch.autograd.Function):
         outs = [torch.empty(k, graph.N, C, device=R.device) for k in RANK_K]
         row = graph.col if gathered else None
         call("face_cp_density_fwd", ptr(R_), ld_R, ptr(env_), ptr(msg_), ld_msg, ptr(row), ptr(Y_), ld_Y,
-             ptr(graph.row_ptr), graph.N, 0, C, *_lib.ranks_of_blocks(outs), _lib.stream_of(R), label="cp_fwd")
+             ptr(graph.row_ptr), graph.N, 0, C, *_lib.ranks_of_blocks(outs), _lib.stream_of(R),
+             label=_cp_label("cp_fwd", gathered))
         ctx.save_for_backward(R_, env_, msg_, Y_)
         ctx.graph, ctx.gathered, ctx.C = graph, gathered, C
         return tuple(outs)
@@ -348,7 +355,7 @@ class CPDensity(torch.autograd.Function):
         st = _lib.stream_of(R)
         call("face_cp_density_bwd", ptr(R), R.stride(0), ptr(env), ptr(msg), msg.stride(0), ptr(row), ptr(Y),
              Y.stride(0), ptr(g.row_ptr), g.N, 0, g.max_row, C, *_lib.ranks_of_blocks(Gs), ptr(dR), 4 * C, ptr(dmsg),
-             C, ptr(dY), 20, ptr(denv), st, label="cp_bwd")
+             C, ptr(dY), 20, ptr(denv), st, label=_cp_label("cp_bwd", ctx.gathered))
         if dmsg is not None and ctx.gathered:
             dtab = torch.empty(g.N, C, device=dev)
             call("face_gather_rows_bwd", ptr(dmsg), C, ptr(g.row_ptr), ptr(g.rev), g.N, C, ptr(dtab), C, st,
@@ -378,7 +385,8 @@ class CPRadialDensity(torch.autograd.Function):
         row = graph.col if gathered else None
         R = radial_head(h2.detach(), w_cp.detach(), b_cp.detach())                            # (E, 4C)
         call("face_cp_density_fwd", ptr(R), R.stride(0), ptr(env_), ptr(msg_), ld_msg, ptr(row), ptr(Y_), ld_Y,
-             ptr(graph.row_ptr), graph.N, 0, C, *_lib.ranks_of_blocks(outs), _lib.stream_of(R), label="cp_fwd")
+             ptr(graph.row_ptr), graph.N, 0, C, *_lib.ranks_of_blocks(outs), _lib.stream_of(R),
+             label=_cp_label("cp_fwd", gathered))
         ctx.save_for_backward(R, w_cp.detach(), env_, msg_, Y_)
         ctx.graph, ctx.gathered, ctx.C = graph, gathered, C
         return tuple(outs)
@@ -404,14 +412,15 @@ class CPRadialDensity(torch.autograd.Function):
         st = _lib.stream_of(R)
         code = _lib.call_status("face_cp_radial_bwd", ptr(R), R.stride(0), ptr(env), ptr(msg), msg.stride(0), ptr(row),
                                 ptr(Y), Y.stride(0), ptr(g.row_ptr), g.N, 0, C, *_lib.ranks_of_blocks(Gs), ptr(w_t), H,
-                                ptr(dh2), H, ptr(dmsg), C, ptr(dY), 20, ptr(denv), st, label="cp_bwd")
+                                ptr(dh2), H, ptr(dmsg), C, ptr(dY), 20, ptr(denv), st,
+                                label=_cp_label("cp_radial_bwd", ctx.gathered))
         if code == _lib.FACE_ERR_UNSUPPORTED:
             # widths whose staging exceeds the fused kernel's LDS: the pooling backward writes dR
             # and d h2 = dR W_cp is a separate GEMM
             dR = torch.empty(g.E, 4 * C, device=dev)
             call("face_cp_density_bwd", ptr(R), R.stride(0), ptr(env), ptr(msg), msg.stride(0), ptr(row), ptr(Y),
                  Y.stride(0), ptr(g.row_ptr), g.N, 0, g.max_row, C, *_lib.ranks_of_blocks(Gs), ptr(dR), 4 * C,
-                 ptr(dmsg), C, ptr(dY), 20, ptr(denv), st, label="cp_bwd")
+                 ptr(dmsg), C, ptr(dY), 20, ptr(denv), st, label=_cp_label("cp_bwd", ctx.gathered))
             torch.mm(dR, w_cp, out=dh2)
         if dmsg is not None and ctx.gathered:
             dtab = torch.empty(g.N, C, device=dev)

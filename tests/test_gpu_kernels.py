@@ -77,14 +77,18 @@ class _G:
 
 
 def _pad(x_edge, counts, M):
-    """(E, ...) edge tensor -> (N, M, ...) zero padded (for the padded oracle)."""
+    """(E, ...) edge tensor -> (N, M, ...) zero padded (for the padded oracle): one gather and a
+    mask, so that autograd through it stays linear in the size."""
     N = len(counts)
-    out = x_edge.new_zeros(N, M, *x_edge.shape[1:])
-    off = 0
-    for i, c in enumerate(counts):
-        out[i, :c] = x_edge[off:off + c]
-        off += c
-    return out
+    if x_edge.shape[0] == 0:
+        return x_edge.new_zeros(N, M, *x_edge.shape[1:])
+    cnt = torch.as_tensor(counts, dtype=torch.int64, device=x_edge.device)
+    start = torch.cumsum(cnt, 0) - cnt
+    slot = torch.arange(M, device=x_edge.device)
+    valid = slot[None, :] < cnt[:, None]
+    idx = (start[:, None] + slot[None, :]).clamp(max=x_edge.shape[0] - 1)
+    out = x_edge[idx.reshape(-1)].reshape(N, M, *x_edge.shape[1:])
+    return out * valid.reshape(N, M, *([1] * (x_edge.dim() - 1))).to(x_edge.dtype)
 
 
 @pytest.mark.parametrize("nx,gathered,B,K", [(20, False, 16, 32), (20, True, 16, 32), (4, True, 16, 144),
@@ -152,16 +156,19 @@ def test_cp_density_ragged_rows(gathered, C):
     assert max(errs) < TOL, errs
 
 
-@pytest.mark.parametrize("gathered,C,H", [(False, 160, 64), (True, 160, 64), (True, 96, 32), (False, 64, 16),
-                                          (True, 32, 48), (False, 320, 64)])
-def test_cp_radial_density_fused_backward(gathered, C, H):
-    """R = h2 W^T + b feeding the CP pooling, computed with it in one pass (or, at C = 320 where
-    the weight block exceeds one workgroup's LDS, by the separate radial-head and pooling
-    launches), whose backward returns d h2 = dR W from inside the pooling kernel: outputs and
-    gradients (h2, env, msg, Y) vs the oracle in fp64."""
+@pytest.mark.parametrize("gathered,C,H,N,pairs", [(False, 160, 64, 41, 600), (True, 160, 64, 41, 600),
+                                                  (True, 96, 32, 41, 600), (False, 64, 16, 41, 600),
+                                                  (True, 32, 48, 41, 600), (False, 160, 64, 3000, 20000),
+                                                  (True, 192, 64, 300, 3000), (False, 320, 64, 41, 600)])
+def test_cp_radial_density_fused_backward(gathered, C, H, N, pairs):
+    """R = h2 W^T + b feeding the CP pooling, whose backward returns d h2 = dR W from inside the
+    pooling kernel: with W^T resident in LDS (H x 4C fp32 up to 160 KB; the 3000-atom graph gives
+    every wave of the grid a share of rows), with W^T staged in channel slabs (C = 192, H = 64), or,
+    at C = 320 where neither fits, by the pooling backward writing dR and a separate product.
+    Outputs and gradients (h2, env, msg, Y) vs the oracle in fp64."""
     from face_amd import ops
-    say("cp radial density", gathered, C, H)
-    g = _G(41, 600, 5)
+    say("cp radial density", gathered, C, H, N, pairs)
+    g = _G(N, pairs, 5, hub=70 if N < 100 else 16)
     counts = g.counts
     E = sum(counts)
     torch.manual_seed(C + H)
@@ -169,7 +176,7 @@ def test_cp_radial_density_fused_backward(gathered, C, H):
     W = torch.randn(4 * C, H, device=DEV) / H ** 0.5
     b = torch.randn(4 * C, device=DEV) * 0.1
     env = torch.rand(E, device=DEV, requires_grad=True)
-    msg = torch.randn(41 if gathered else E, C, device=DEV, requires_grad=True)
+    msg = torch.randn(N if gathered else E, C, device=DEV, requires_grad=True)
     Y = torch.randn(E, 20, device=DEV, requires_grad=True)
     A = torch.cat(ops.cp_radial_density(h2, W, b, env, msg, Y, g.G, gathered), 0).permute(1, 0, 2)   # (N, 20, C)
     G = torch.randn_like(A)
