@@ -1002,7 +1002,7 @@ __device__ __forceinline__ int64_t uniform64(int64_t v) {
     return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
-template <int HB, int NW, bool PF>
+template <int HB, int NW>
 __global__ __launch_bounds__(NW * kWave) void cp_radial_bwd_res_kernel(
     const float* __restrict__ R, int ld_R, const float* __restrict__ env, const float* __restrict__ msg, int ld_msg,
     const int32_t* __restrict__ msg_row, const float* __restrict__ Y, int ld_Y, const int32_t* __restrict__ row_ptr,
@@ -1103,65 +1103,71 @@ __global__ __launch_bounds__(NW * kWave) void cp_radial_bwd_res_kernel(
     int64_t rw = row - 1, t0 = 0, e1 = 0;
     if (!next_tile(rw, t0, e1)) return;
     Head hd, hn;
-    Slot cur, nxt;
     load_head(t0, e1, hd);
-    if (PF) load_slot(rw, hd.eld, hd.mr, 0, cur);
-    while (true) {
-        int64_t nrw = rw, nt0 = t0, ne1 = e1;
-        const bool more = next_tile(nrw, nt0, ne1);
-        if (PF && more) load_head(nt0, ne1, hn);
-        v4f dacc[HB];
+    Slot sa, sb;
+    load_slot(rw, hd.eld, hd.mr, 0, sa);
+    int64_t nrw = rw, nt0 = t0, ne1 = e1;             // the tile after the current one
+    bool more = next_tile(nrw, nt0, ne1);
+    if (more)
+        load_head(nt0, ne1, hn);
+    else
+        hn = hd;
+    v4f dacc[HB];
 #pragma unroll
-        for (int hb = 0; hb < HB; ++hb) dacc[hb] = z4;
-        v4f plo = z4, phi = z4;
+    for (int hb = 0; hb < HB; ++hb) dacc[hb] = z4;
+    v4f plo = z4, phi = z4;
+    int st = 0;
+    // One (tile, step) computed on `cu` while the following one is loaded into `nx`: the next
+    // step of this tile, else step 0 of the next tile (this tile's step 0 again, unused, when
+    // none is left), so that the loads are issued on every path and the two buffers alternate
+    // without copies. False when this wave's last tile is done.
+    auto step = [&](Slot& cu, Slot& nx) __attribute__((always_inline)) -> bool {
+        const bool last = st + 1 == nsteps;
+        const bool to_next = last && more;
+        load_slot(to_next ? nrw : rw, to_next ? hn.eld : hd.eld, to_next ? hn.mr : hd.mr, last ? 0 : st + 1, nx);
+        __builtin_amdgcn_sched_barrier(0);           // keep the loads ahead of this step's work
+        const int c0 = st * kResStep;
         const int64_t e = t0 + j;
-#pragma unroll 1
-        for (int st = 0; st < nsteps; ++st) {
-            if (!PF) {
-                load_slot(rw, hd.eld, hd.mr, st, cur);
-            } else if (st + 1 < nsteps) {
-                load_slot(rw, hd.eld, hd.mr, st + 1, nxt);
-            } else if (more) {
-                load_slot(nrw, hn.eld, hn.mr, 0, nxt);
-            }
-            const int c0 = st * kResStep;
-            // P[x, e] = sum_c gA[x, c] R_{l(x)}[e, c] m[e, c] for the dY rows (first: it
-            // needs only loaded operands, and covers the latency of the t products below)
+        // P[x, e] = sum_c gA[x, c] R_{l(x)}[e, c] m[e, c] for the dY rows (first: it needs only
+        // loaded operands, and covers the latency of the t products below)
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr) {
-                const float mm = cur.m[rr];
-                plo = mfma_16x16x4(sel0 * cur.alo[rr], cur.r[0][rr] * mm, plo);
-                phi = mfma_16x16x4(sel2 * cur.ahi[rr], cur.r[2][rr] * mm, phi);
-                plo = mfma_16x16x4(sel1 * cur.alo[rr], cur.r[1][rr] * mm, plo);
-                phi = mfma_16x16x4(sel3 * cur.ahi[rr], cur.r[3][rr] * mm, phi);
-            }
-            // t_l[c, e] = sum_{x in rank l} gA[x, c] Y[e, x]
-            v4f tt[4];
-#pragma unroll
-            for (int l = 0; l < 4; ++l) {
-                v4f t = z4;
-#pragma unroll
-                for (int k = kRankChunk0[l]; k < kRankChunk1[l]; ++k) t = mfma_16x16x4(cur.ta[k], hd.yq[k], t);
-                tt[l] = t;
-            }
-            // dR_l = ev m t_l; dh2 += dR_l W_l^T; dm = sum_l R_l t_l
-            v4f dm = z4;
-#pragma unroll
-            for (int l = 0; l < 4; ++l) {
-                const v4f g = (hd.ev * cur.m) * tt[l];
-                const int c4 = ((l * C + c0) >> 2) + q;
-#pragma unroll
-                for (int hb = 0; hb < HB; ++hb) {
-                    const v4f wv = ld4(lds + (16 * hb + j) * RS + 4 * (c4 ^ j));
-#pragma unroll
-                    for (int rr = 0; rr < 4; ++rr) dacc[hb] = mfma_16x16x4(g[rr], wv[rr], dacc[hb]);
-                }
-                dm += cur.r[l] * tt[l];
-            }
-            if (hd.ok && dmsg) st4(dmsg + e * ld_dmsg + c0 + own, hd.ev * dm);
-            if (PF) cur = nxt;
+        for (int rr = 0; rr < 4; ++rr) {
+            const float mm = cu.m[rr];
+            plo = mfma_16x16x4(sel0 * cu.alo[rr], cu.r[0][rr] * mm, plo);
+            phi = mfma_16x16x4(sel2 * cu.ahi[rr], cu.r[2][rr] * mm, phi);
+            plo = mfma_16x16x4(sel1 * cu.alo[rr], cu.r[1][rr] * mm, plo);
+            phi = mfma_16x16x4(sel3 * cu.ahi[rr], cu.r[3][rr] * mm, phi);
         }
-        // lane (j, q) holds P[x, e] for x = 4 + 4q + r (hi) and, in lanes q == 0, x = r (lo)
+        // t_l[c, e] = sum_{x in rank l} gA[x, c] Y[e, x]
+        v4f tt[4];
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            v4f t = z4;
+#pragma unroll
+            for (int k = kRankChunk0[l]; k < kRankChunk1[l]; ++k) t = mfma_16x16x4(cu.ta[k], hd.yq[k], t);
+            tt[l] = t;
+        }
+        // dR_l = ev m t_l; dh2 += dR_l W_l^T; dm = sum_l R_l t_l
+        v4f dm = z4;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const v4f g = (hd.ev * cu.m) * tt[l];
+            const int c4 = ((l * C + c0) >> 2) + q;
+#pragma unroll
+            for (int hb = 0; hb < HB; ++hb) {
+                const v4f wv = ld4(lds + (16 * hb + j) * RS + 4 * (c4 ^ j));
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) dacc[hb] = mfma_16x16x4(g[rr], wv[rr], dacc[hb]);
+            }
+            dm += cu.r[l] * tt[l];
+        }
+        if (hd.ok && dmsg) st4(dmsg + e * ld_dmsg + c0 + own, hd.ev * dm);
+        if (!last) {
+            ++st;
+            return true;
+        }
+        // tile done: lane (j, q) holds P[x, e] for x = 4 + 4q + r (hi) and, in lanes q == 0,
+        // x = r (lo)
         float s = 0.f;
         if (hd.ok) {
             const v4f yhi = hd.yhi, ylo = hd.ylo;
@@ -1184,12 +1190,18 @@ __global__ __launch_bounds__(NW * kWave) void cp_radial_bwd_res_kernel(
                 for (int hb = 0; hb < HB; ++hb) dh2[er * ld_dh2 + 16 * hb + j] = dacc[hb][rr];
             }
         }
-        if (!more) break;
+        if (!more) return false;
         rw = nrw, t0 = nt0, e1 = ne1;
-        if (PF)
-            hd = hn;
-        else
-            load_head(t0, e1, hd);
+        hd = hn;
+        more = next_tile(nrw, nt0, ne1);
+        if (more) load_head(nt0, ne1, hn);
+#pragma unroll
+        for (int hb = 0; hb < HB; ++hb) dacc[hb] = z4;
+        plo = z4, phi = z4;
+        st = 0;
+        return true;
+    };
+    while (step(sa, sb) && step(sb, sa)) {
     }
 }
 
@@ -1494,10 +1506,9 @@ extern "C" int face_cp_radial_bwd(const float* R, int32_t ld_R, const float* env
         mfma_layout_ok(R, ld_R, msg, ld_msg, Y, ld_Y, C, gA, nullptr, 0, dmsg, ld_dmsg, dY, ld_dY, kResStep)) {
         // all of W^T resident in LDS: one workgroup per CU, every wave on its own share of the edges
         constexpr int kNW = 8;
-        constexpr bool kPF = true;
 #define FACE_CPRES(HB_)                                                                                          \
     do {                                                                                                         \
-        auto kern = cp_radial_bwd_res_kernel<HB_, kNW, kPF>;                                                          \
+        auto kern = cp_radial_bwd_res_kernel<HB_, kNW>;                                                          \
         if (lds_res > 65536 && hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, \
                                                    (int)lds_res) != hipSuccess)                                  \
             return FACE_ERR_UNSUPPORTED;                                                                         \
