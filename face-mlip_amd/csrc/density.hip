@@ -1147,18 +1147,25 @@ __global__ __launch_bounds__(NW * kWave) void cp_radial_bwd_res_kernel(
             for (int k = kRankChunk0[l]; k < kRankChunk1[l]; ++k) t = mfma_16x16x4(cu.ta[k], hd.yq[k], t);
             tt[l] = t;
         }
-        // dR_l = ev m t_l; dh2 += dR_l W_l^T; dm = sum_l R_l t_l
+        // dR_l = ev m t_l; dh2 += dR_l W_l^T; dm = sum_l R_l t_l (the W^T operands of rank l + 1
+        // are read while rank l's products issue)
         v4f dm = z4;
-#pragma unroll
-        for (int l = 0; l < 4; ++l) {
-            const v4f g = (hd.ev * cu.m) * tt[l];
+        v4f wv[2][HB];
+        auto read_w = [&](int l, v4f (&w)[HB]) __attribute__((always_inline)) {
             const int c4 = ((l * C + c0) >> 2) + q;
 #pragma unroll
-            for (int hb = 0; hb < HB; ++hb) {
-                const v4f wv = ld4(lds + (16 * hb + j) * RS + 4 * (c4 ^ j));
+            for (int hb = 0; hb < HB; ++hb) w[hb] = ld4(lds + (16 * hb + j) * RS + 4 * (c4 ^ j));
+        };
+        read_w(0, wv[0]);
 #pragma unroll
-                for (int rr = 0; rr < 4; ++rr) dacc[hb] = mfma_16x16x4(g[rr], wv[rr], dacc[hb]);
-            }
+        for (int l = 0; l < 4; ++l) {
+            if (l < 3) read_w(l + 1, wv[(l + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+            const v4f g = (hd.ev * cu.m) * tt[l];
+#pragma unroll
+            for (int hb = 0; hb < HB; ++hb)
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) dacc[hb] = mfma_16x16x4(g[rr], wv[l & 1][hb][rr], dacc[hb]);
             dm += cu.r[l] * tt[l];
         }
         if (hd.ok && dmsg) st4(dmsg + e * ld_dmsg + c0 + own, hd.ev * dm);
