@@ -23,7 +23,7 @@ namespace face {
 // LDS image: lin_off / lin_layout (common.h).
 constexpr int kLinWaves = 16;
 
-template <int KB, int BB, int FB>
+template <int KB, int BB, int FB, bool HAS_B, bool HAS_T>
 __global__ __launch_bounds__(kLinWaves * kWave) void edge_linear_fwd_kernel(
     const float* __restrict__ X, int ld_X, int64_t E, const float* __restrict__ w, const float* __restrict__ b,
     int F, int f_chunk, int S, int rot, const float* __restrict__ T, int ld_T, const int32_t* __restrict__ idx,
@@ -53,20 +53,59 @@ __global__ __launch_bounds__(kLinWaves * kWave) void edge_linear_fwd_kernel(
     const int64_t ntile = (E + 16 * BB - 1) / (16 * BB);
     const int64_t stride = (int64_t)gridDim.x * kLinWaves;
     const v4f z4 = {0.f, 0.f, 0.f, 0.f};
-    for (int64_t t = (int64_t)blockIdx.x * kLinWaves + wv_id; t < ntile; t += stride) {
+    int64_t t = (int64_t)blockIdx.x * kLinWaves + wv_id;
+    if (t >= ntile) return;
+    // X rows (B operands) and table rows of a tile's 16 BB edges; rows past E repeat edge E - 1
+    // (never stored). The next tile's rows are loaded while the current one computes, and moved
+    // in before its output blocks start, so that no load is outstanding inside the block loop:
+    // a wait there would also wait for the Y stores issued after it.
+    v4f xn[BB][KB];
+    int64_t trn[BB];
+    auto load_tile = [&](int64_t tt) __attribute__((always_inline)) {
+#pragma unroll
+        for (int bb = 0; bb < BB; ++bb) {
+            const int64_t e = tt * 16 * BB + 16 * bb + j;
+            const int64_t ec = e < E ? e : E - 1;
+#pragma unroll
+            for (int kb = 0; kb < KB; ++kb) xn[bb][kb] = ld4(X + ec * ld_X + 16 * kb + 4 * q);
+            trn[bb] = HAS_T ? (idx ? (int64_t)idx[ec] : ec) : 0;
+        }
+    };
+    load_tile(t);
+    for (; t < ntile; t += stride) {
         const int64_t e0 = t * 16 * BB;
         v4f xv[BB][KB];
         int64_t trow[BB];
 #pragma unroll
         for (int bb = 0; bb < BB; ++bb) {
-            const int64_t e = e0 + 16 * bb + j;
-            const bool ok = e < E;
+            trow[bb] = trn[bb];
 #pragma unroll
-            for (int kb = 0; kb < KB; ++kb) xv[bb][kb] = ok ? ld4(X + e * ld_X + 16 * kb + 4 * q) : z4;
-            trow[bb] = (T && ok) ? (idx ? (int64_t)idx[e] : e) : 0;
+            for (int kb = 0; kb < KB; ++kb) xv[bb][kb] = xn[bb][kb];
         }
+        if (t + stride < ntile) load_tile(t + stride);
 #pragma unroll 1
         for (int fb0 = 0; fb0 < nf; fb0 += 16 * FB) {
+            // epilogue operands, issued ahead of the products: the bias through scalar loads
+            // (16 features of a block are wave-uniform; lane (j, q) takes 4q .. 4q + 3), the
+            // table rows as vector loads
+            v4f bias[FB], tv[FB][BB];
+#pragma unroll
+            for (int fb = 0; fb < FB; ++fb) {
+                const int fc = min(fb0 + 16 * fb, nf - 16);
+                bias[fb] = z4;
+                if (HAS_B) {
+                    const float* bp = b + f_beg + fc;
+                    float bs[16];
+#pragma unroll
+                    for (int u = 0; u < 16; ++u)      // wave-uniform values: scalar loads
+                        bs[u] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(bp[u])));
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) bias[fb][r] = q == 0 ? bs[r] : (q == 1 ? bs[4 + r] : (q == 2 ? bs[8 + r] : bs[12 + r]));
+                }
+#pragma unroll
+                for (int bb = 0; bb < BB; ++bb)
+                    tv[fb][bb] = HAS_T ? ld4(T + trow[bb] * ld_T + f_beg + fc + 4 * q) : z4;
+            }
             v4f acc[FB][BB];
 #pragma unroll
             for (int fb = 0; fb < FB; ++fb)
@@ -91,15 +130,10 @@ __global__ __launch_bounds__(kLinWaves * kWave) void edge_linear_fwd_kernel(
             for (int fb = 0; fb < FB; ++fb) {
                 if (fb0 + 16 * fb < nf) {
                     const int f = f_beg + fb0 + 16 * fb + 4 * q;
-                    const v4f bias = b ? ld4(b + f) : z4;
 #pragma unroll
                     for (int bb = 0; bb < BB; ++bb) {
                         const int64_t e = e0 + 16 * bb + j;
-                        if (e < E) {
-                            v4f o = acc[fb][bb] + bias;
-                            if (T) o += ld4(T + trow[bb] * ld_T + f);
-                            st4(Y + e * ld_Y + f, o);
-                        }
+                        if (e < E) st4(Y + e * ld_Y + f, acc[fb][bb] + bias[fb] + tv[fb][bb]);
                     }
                 }
             }
@@ -224,7 +258,10 @@ extern "C" int face_edge_linear_fwd(const float* x, int32_t ld_x, int64_t E, int
     const hipStream_t st = (hipStream_t)stream;
 #define FACE_LINF(KB_)                                                                                        \
     do {                                                                                                      \
-        auto kern = edge_linear_fwd_kernel<KB_, BB, FB>;                                                      \
+        auto kern = b ? (tab ? edge_linear_fwd_kernel<KB_, BB, FB, true, true>                                \
+                             : edge_linear_fwd_kernel<KB_, BB, FB, true, false>)                              \
+                      : (tab ? edge_linear_fwd_kernel<KB_, BB, FB, false, true>                               \
+                             : edge_linear_fwd_kernel<KB_, BB, FB, false, false>);                            \
         if (lds > 65536 &&                                                                                    \
             hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=    \
                 hipSuccess)                                                                                   \
