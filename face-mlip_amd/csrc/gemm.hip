@@ -31,11 +31,15 @@ struct GemmProb {
     int64_t ld_y;
     int n, k, s_off, tiles, slices;        // tiles of 32 NW rows, slices of NS columns
     float beta;
-    int64_t first_block;                   // first workgroup index of this problem
+    int64_t first_block;                   // first work item of this problem
+    int64_t cost0;                         // summed cost of the items of the problems before it
+    int cost;                              // cost of one of its items (~ K + fixed per-item work)
 };
 
 struct GemmArgs {
     GemmProb p[kGemmMaxProbs];
+    int64_t items;                         // (problem, slice, tile) work items over all problems
+    int64_t total_cost;
     int n_probs, w_kn, NS;
     const float *bias, *xs, *ys;
     int ld_s;
@@ -43,122 +47,178 @@ struct GemmArgs {
     int64_t period;
 };
 
-template <int NB, int NW>
+template <int NB, int NW, bool PERSIST>
 __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
     extern __shared__ float sW[];
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
-    // this workgroup's problem, column slice and row tile
-    int pi = 0;
-#pragma unroll
-    for (int k = 1; k < kGemmMaxProbs; ++k)
-        if (k < A.n_probs && (int64_t)blockIdx.x >= A.p[k].first_block) pi = k;
-    const GemmProb& P = A.p[pi];
-    const int64_t local = (int64_t)blockIdx.x - P.first_block;
-    const int slice = (int)(local % P.slices);
-    const int64_t tile = local / P.slices;
-    const int K = P.k, SK = K + 4;
-    const int n0 = slice * A.NS;
-    const int ns = min(A.NS, P.n - n0);                                 // a multiple of 16
-    // stage W[n0 : n0 + ns, :] as rows of K (+ 4 pad); rows ns .. 16 NB - 1 are zero, so the
-    // MFMA loop below runs all NB blocks without branches
-    const v4f z4 = {0.f, 0.f, 0.f, 0.f};
-    if (!A.w_kn) {
-        const int nk4 = K / 4;
-        for (int v = tid; v < 16 * NB * nk4; v += blockDim.x) {
-            const int r = v / nk4, c4 = v - r * nk4;
-            st4(sW + r * SK + 4 * c4, r < ns ? ld4(P.w + (int64_t)(n0 + r) * P.ld_w + 4 * c4) : z4);
-        }
-    } else {                                                             // W given as (K, n)
-        // thread (k4, r): four coalesced reads down column n0 + r, one float4 into row r
-        const int nr = 16 * NB;
-        for (int v = tid; v < nr * (K / 4); v += blockDim.x) {
-            const int k4 = v / nr, r = v - k4 * nr;
-            v4f c4 = z4;
-            if (r < ns) {
-                const float* col = P.w + (int64_t)(4 * k4) * P.ld_w + n0 + r;
-#pragma unroll
-                for (int u = 0; u < 4; ++u) c4[u] = col[(int64_t)u * P.ld_w];
-            }
-            st4(sW + r * SK + 4 * k4, c4);
-        }
-    }
-    __syncthreads();
     const int j = lane & 15, q = lane >> 4;
     const int wv = __builtin_amdgcn_readfirstlane(tid / kWave);
-    const int64_t m0 = (tile * NW + wv) * (16 * kGemmBB);
-    if (m0 >= P.m) return;                                               // no barrier follows
-    int64_t rows[kGemmBB];
-    bool ok[kGemmBB];
-    const float* xr[kGemmBB];
-    const float* xsr[kGemmBB];
-    const float* ysr[kGemmBB];
+    const v4f z4 = {0.f, 0.f, 0.f, 0.f};
+    auto item_at = [&](int64_t target) -> int64_t {     // first item starting at or past target
+        int p = 0;
 #pragma unroll
-    for (int bb = 0; bb < kGemmBB; ++bb) {
-        rows[bb] = m0 + 16 * bb + j;
-        ok[bb] = rows[bb] < P.m;
-        xr[bb] = P.x + (ok[bb] ? rows[bb] : 0) * P.ld_x + 4 * q;
-        const int64_t g = (A.group && ok[bb]) ? (int64_t)A.group[rows[bb] % A.period] : 0;
-        xsr[bb] = A.xs ? A.xs + g * A.ld_s + P.s_off + 4 * q : nullptr;
-        ysr[bb] = A.ys ? A.ys + g * A.ld_s + P.s_off : nullptr;
-    }
-    auto load_x = [&](int kc, v4f (&xv)[kGemmBB]) {
+        for (int k = 1; k < kGemmMaxProbs; ++k)
+            if (k < A.n_probs && target >= A.p[k].cost0) p = k;
+        const int64_t i = A.p[p].first_block + (target - A.p[p].cost0 + A.p[p].cost - 1) / A.p[p].cost;
+        return min(i, A.items);
+    };
+    const bool one = !PERSIST || A.items <= gridDim.x;
+    const int64_t it_beg = one ? blockIdx.x : item_at(A.total_cost * (int64_t)blockIdx.x / gridDim.x);
+    const int64_t it_end = one ? min(A.items, (int64_t)blockIdx.x + 1) : item_at(A.total_cost * ((int64_t)blockIdx.x + 1) / gridDim.x);
+    int cur_pi = -1, cur_slice = -1;
+    auto run_item = [&](int64_t it) __attribute__((always_inline)) {
+        int pi = 0;
+#pragma unroll
+        for (int k = 1; k < kGemmMaxProbs; ++k)
+            if (k < A.n_probs && it >= A.p[k].first_block) pi = k;
+        const GemmProb& P = A.p[pi];
+        const int64_t local = it - P.first_block;
+        // persistent runs go slice by slice (the weight slice stays staged); one item per
+        // workgroup goes tile by tile (the slices of a row tile run side by side and share its
+        // rows in cache)
+        const int slice = PERSIST ? (int)(local / P.tiles) : (int)(local % P.slices);
+        const int64_t tile = PERSIST ? local - (int64_t)slice * P.tiles : local / P.slices;
+        const int K = P.k, SK = K + 4;
+        const int n0 = slice * A.NS;
+        const int ns = min(A.NS, P.n - n0);                             // a multiple of 16
+        if (pi != cur_pi || slice != cur_slice) {
+            // stage W[n0 : n0 + ns, :] as rows of K (+ 4 pad); rows ns .. 16 NB - 1 are zero, so
+            // the MFMA loop below runs all NB blocks without branches
+            if (PERSIST) __syncthreads();                                // every wave is done with the old slice
+            if (!A.w_kn) {
+                const int nk4 = K / 4;
+                for (int v = tid; v < 16 * NB * nk4; v += blockDim.x) {
+                    const int r = v / nk4, c4 = v - r * nk4;
+                    st4(sW + r * SK + 4 * c4, r < ns ? ld4(P.w + (int64_t)(n0 + r) * P.ld_w + 4 * c4) : z4);
+                }
+            } else {                                                     // W given as (K, n)
+                // thread (k4, r): four coalesced reads down column n0 + r, one float4 into row r
+                const int nr = 16 * NB;
+                for (int v = tid; v < nr * (K / 4); v += blockDim.x) {
+                    const int k4 = v / nr, r = v - k4 * nr;
+                    v4f c4 = z4;
+                    if (r < ns) {
+                        const float* col = P.w + (int64_t)(4 * k4) * P.ld_w + n0 + r;
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) c4[u] = col[(int64_t)u * P.ld_w];
+                    }
+                    st4(sW + r * SK + 4 * k4, c4);
+                }
+            }
+            __syncthreads();
+            cur_pi = pi, cur_slice = slice;
+        }
+        const int64_t m0 = (tile * NW + wv) * (16 * kGemmBB);
+        if (m0 >= P.m) return;
+        int64_t rows[kGemmBB];
+        bool ok[kGemmBB];
+        const float* xr[kGemmBB];
+        const float* xsr[kGemmBB];
+        const float* ysr[kGemmBB];
 #pragma unroll
         for (int bb = 0; bb < kGemmBB; ++bb) {
-            xv[bb] = ok[bb] ? ld4(xr[bb] + 16 * kc) : z4;
-            if (A.xs) xv[bb] *= ld4(xsr[bb] + 16 * kc);
+            rows[bb] = m0 + 16 * bb + j;
+            ok[bb] = rows[bb] < P.m;
+            const int64_t rc = ok[bb] ? rows[bb] : 0;
+            xr[bb] = P.x + rc * P.ld_x + 4 * q;
+            const int64_t g = A.group ? (int64_t)A.group[rc % A.period] : 0;
+            xsr[bb] = A.xs ? A.xs + g * A.ld_s + P.s_off + 4 * q : nullptr;
+            ysr[bb] = A.ys ? A.ys + g * A.ld_s + P.s_off + 4 * q : nullptr;
         }
-    };
-    v4f acc[NB][kGemmBB];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-        for (int bb = 0; bb < kGemmBB; ++bb) acc[nb][bb] = z4;
-    const int nkc = K / 16;
-    v4f xn[kGemmBB];
-    load_x(0, xn);
-#pragma unroll 1
-    for (int kc = 0; kc < nkc; ++kc) {
-        v4f xv[kGemmBB];
-#pragma unroll
-        for (int bb = 0; bb < kGemmBB; ++bb) xv[bb] = xn[bb];
-        if (kc + 1 < nkc) load_x(kc + 1, xn);
-        // weight blocks read one block ahead of their MFMAs (LDS latency under the MFMA chain)
-        const float* wrow = sW + j * SK + 16 * kc + 4 * q;
-        v4f wa = *reinterpret_cast<const v4f*>(wrow);
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            const v4f wn = nb + 1 < NB ? *reinterpret_cast<const v4f*>(wrow + 16 * (nb + 1) * SK) : wa;
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-#pragma unroll
-                for (int bb = 0; bb < kGemmBB; ++bb) acc[nb][bb] = mfma_16x16x4(wa[r], xv[bb][r], acc[nb][bb]);
-            wa = wn;
-        }
-        // issue order: reads of blocks 0 and 1, then per block its 4 kGemmBB MFMAs followed by
-        // the read of block nb + 2, so every read has a block of MFMAs to hide under
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            if (nb == 0) __builtin_amdgcn_sched_group_barrier(0x100, NB > 1 ? 2 : 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 4 * kGemmBB, 0);
-            if (nb + 2 < NB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        }
-    }
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-        if (16 * nb < ns) {
-            const int n = n0 + 16 * nb + 4 * q;
-            const v4f bias = A.bias ? ld4(A.bias + n) : z4;
+        auto load_x = [&](int kc, v4f (&xv)[kGemmBB]) {
 #pragma unroll
             for (int bb = 0; bb < kGemmBB; ++bb) {
-                if (ok[bb]) {
-                    float* yp = P.y + rows[bb] * P.ld_y + n;
+                xv[bb] = ok[bb] ? ld4(xr[bb] + 16 * kc) : z4;
+                if (A.xs) xv[bb] *= ld4(xsr[bb] + 16 * kc);
+            }
+        };
+        v4f acc[NB][kGemmBB];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int bb = 0; bb < kGemmBB; ++bb) acc[nb][bb] = z4;
+        const int nkc = K / 16;
+        v4f xn[kGemmBB];
+        load_x(0, xn);
+#pragma unroll 1
+        for (int kc = 0; kc < nkc; ++kc) {
+            v4f xv[kGemmBB];
+#pragma unroll
+            for (int bb = 0; bb < kGemmBB; ++bb) xv[bb] = xn[bb];
+            if (kc + 1 < nkc) load_x(kc + 1, xn);
+            // weight blocks read one block ahead of their MFMAs (LDS latency under the MFMA chain)
+            const float* wrow = sW + j * SK + 16 * kc + 4 * q;
+            v4f wa = *reinterpret_cast<const v4f*>(wrow);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                const v4f wn = nb + 1 < NB ? *reinterpret_cast<const v4f*>(wrow + 16 * (nb + 1) * SK) : wa;
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int bb = 0; bb < kGemmBB; ++bb) acc[nb][bb] = mfma_16x16x4(wa[r], xv[bb][r], acc[nb][bb]);
+                wa = wn;
+            }
+            // issue order: reads of blocks 0 and 1, then per block its 4 kGemmBB MFMAs followed by
+            // the read of block nb + 2, so every read has a block of MFMAs to hide under
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                if (nb == 0) __builtin_amdgcn_sched_group_barrier(0x100, NB > 1 ? 2 : 1, 0);
+                __builtin_amdgcn_sched_group_barrier(0x008, 4 * kGemmBB, 0);
+                if (nb + 2 < NB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            }
+        }
+        if (PERSIST) {
+            // epilogue, loads first: bias, beta y and the y scale folded into the accumulators
+            // (columns past the slice read its last block, rows past m read row 0; neither is
+            // stored), then the stores, so no wait for a load ever covers a store
+            float* yr[kGemmBB];
+#pragma unroll
+            for (int bb = 0; bb < kGemmBB; ++bb) yr[bb] = P.y + (ok[bb] ? rows[bb] : 0) * P.ld_y + 4 * q;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                const int nc = 16 * min(nb, ns / 16 - 1);
+                const v4f bias = A.bias ? ld4(A.bias + n0 + nc + 4 * q) : z4;
+#pragma unroll
+                for (int bb = 0; bb < kGemmBB; ++bb) {
                     v4f v = acc[nb][bb] + bias;
-                    if (P.beta != 0.f) v += P.beta * ld4(yp);
-                    if (A.ys) v *= ld4(ysr[bb] + n);
-                    st4(yp, v);
+                    if (P.beta != 0.f) v += P.beta * ld4(yr[bb] + n0 + nc);
+                    if (A.ys) v *= ld4(ysr[bb] + n0 + nc);
+                    acc[nb][bb] = v;
+                }
+            }
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                if (16 * nb < ns) {
+#pragma unroll
+                    for (int bb = 0; bb < kGemmBB; ++bb)
+                        if (ok[bb]) st4(yr[bb] + n0 + 16 * nb, acc[nb][bb]);
+                }
+            }
+        } else {
+            // one item per workgroup: each block's operands loaded next to its stores
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                if (16 * nb < ns) {
+                    const int n = n0 + 16 * nb;
+                    const v4f bias = A.bias ? ld4(A.bias + n + 4 * q) : z4;
+#pragma unroll
+                    for (int bb = 0; bb < kGemmBB; ++bb) {
+                        if (ok[bb]) {
+                            float* yp = P.y + rows[bb] * P.ld_y + n + 4 * q;
+                            v4f v = acc[nb][bb] + bias;
+                            if (P.beta != 0.f) v += P.beta * ld4(yp);
+                            if (A.ys) v *= ld4(ysr[bb] + n);
+                            st4(yp, v);
+                        }
+                    }
                 }
             }
         }
+    };
+    if (PERSIST) {
+        for (int64_t it = it_beg; it < it_end; ++it) run_item(it);
+    } else {
+        run_item(blockIdx.x);
     }
 }
 
@@ -212,7 +272,7 @@ extern "C" int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, 
     const int n_cu = device_cu_count();
     const int NW = wgs_for(16) >= n_cu ? 16 : (wgs_for(8) >= n_cu ? 8 : 4);
     int max_n = 16;
-    int64_t blocks = 0;
+    int64_t blocks = 0, total_cost = 0;
     for (int i = 0; i < n_probs; ++i) {
         const face_lin_problem& s = probs[i];
         if (s.m < 0 || s.n < 16 || s.n % 16 || s.ld_x < s.k || s.ld_y < s.n || s.ld_w < (w_kn ? s.n : s.k))
@@ -229,24 +289,51 @@ extern "C" int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, 
         p.tiles = (int)((s.m + 16 * kGemmBB * NW - 1) / (16 * kGemmBB * NW));
         p.slices = (s.n + NS - 1) / NS;
         p.first_block = blocks;
+        p.cost0 = total_cost;
+        p.cost = s.k + 64;
         blocks += (int64_t)p.tiles * p.slices;
+        total_cost += (int64_t)p.tiles * p.slices * p.cost;
         if (s.n > max_n) max_n = s.n;
     }
-    for (int i = n_probs; i < kGemmMaxProbs; ++i) A.p[i].first_block = INT64_MAX;
+    for (int i = n_probs; i < kGemmMaxProbs; ++i) A.p[i].first_block = A.p[i].cost0 = INT64_MAX;
     if (blocks == 0) return 0;
     A.NS = NS;
+    A.items = blocks;
+    A.total_cost = total_cost;
     const int nb = (max_n < NS ? max_n : NS) / 16;
     const size_t lds = (size_t)(nb * 16) * (K + 4) * sizeof(float);
+    // persistent grid: as many workgroups as fit on the device at once, each on a contiguous run
+    // of the work items
+    int64_t wg_cu = (int64_t)max_lds / (int64_t)lds;
+    if (wg_cu > 32 / NW) wg_cu = 32 / NW;
+    if (wg_cu < 1) wg_cu = 1;
+    // Persistent runs when the work outnumbers the resident workgroups and no weight slice has to
+    // be staged again per row tile: single-slice problems, or (n, K) weights whose slices stage
+    // from contiguous rows. Otherwise one work item per workgroup, tile by tile, so the slices of
+    // a row tile share its rows in cache (measured better for multi-slice (K, n) weights of
+    // large K and for launches that fit the device at once).
+    bool multi_slice = false;
+    for (int i = 0; i < n_probs; ++i)
+        if (A.p[i].slices > 1 && A.p[i].tiles > 0) multi_slice = true;
+    const bool persist = blocks > n_cu * wg_cu && (!w_kn || !multi_slice);
+    const int64_t grid = persist ? n_cu * wg_cu : blocks;
     const hipStream_t st = (hipStream_t)stream;
-#define FACE_GEMM(NB_)                                                                                      \
+#define FACE_GEMM_P(NB_, P_)                                                                                \
     do {                                                                                                    \
-        auto kern = NW == 16 ? rows_gemm_kernel<NB_, 16>                                                    \
-                             : (NW == 8 ? rows_gemm_kernel<NB_, 8> : rows_gemm_kernel<NB_, 4>);             \
+        auto kern = NW == 16 ? rows_gemm_kernel<NB_, 16, P_>                                                \
+                             : (NW == 8 ? rows_gemm_kernel<NB_, 8, P_> : rows_gemm_kernel<NB_, 4, P_>);     \
         if (lds > 65536 &&                                                                                  \
             hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != \
                 hipSuccess)                                                                                 \
             return FACE_ERR_UNSUPPORTED;                                                                    \
-        hipLaunchKernelGGL(kern, dim3((unsigned)blocks), dim3(NW * kWave), lds, st, A);                    \
+        hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NW * kWave), lds, st, A);                      \
+    } while (0)
+#define FACE_GEMM(NB_)               \
+    do {                             \
+        if (persist)                 \
+            FACE_GEMM_P(NB_, true);  \
+        else                         \
+            FACE_GEMM_P(NB_, false); \
     } while (0)
     switch (nb) {
         case 1: FACE_GEMM(1); break;
@@ -261,6 +348,7 @@ extern "C" int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, 
         default: FACE_GEMM(10); break;
     }
 #undef FACE_GEMM
+#undef FACE_GEMM_P
     FACE_LAUNCH_CHECK();
     return 0;
 }
