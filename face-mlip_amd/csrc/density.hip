@@ -464,6 +464,62 @@ __global__ __launch_bounds__(kBlock) void cp_density_fwd_kernel(
     }
 }
 
+// One wave per atom row, lane L owning channels 4L .. 4L + 3 (C <= 256): float4 loads of R and
+// the messages, the edge's Y row, envelope and message row through scalar loads (wave-uniform
+// addresses), no LDS and no barrier; the next edge's vector loads are issued before the current
+// edge's products.
+constexpr int kCpfWaves = 4;
+
+__global__ __launch_bounds__(kCpfWaves * kWave) void cp_density_fwd_wave_kernel(
+    const float* __restrict__ R, int ld_R, const float* __restrict__ env, const float* __restrict__ msg, int ld_msg,
+    const int32_t* __restrict__ msg_row, const float* __restrict__ Y, int ld_Y, const int32_t* __restrict__ row_ptr,
+    int64_t N, int M, int C, RankOut A) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t i = (int64_t)blockIdx.x * kCpfWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    if (i >= N) return;
+    const int c = 4 * (lane < C / 4 ? lane : C / 4 - 1);    // lanes past C / 4 repeat the last quad
+    const v4f z4 = {0.f, 0.f, 0.f, 0.f};
+    v4f acc[20];
+#pragma unroll
+    for (int x = 0; x < 20; ++x) acc[x] = z4;
+    int64_t e0, e1;
+    row_range(row_ptr, i, M, e0, e1);
+    if (e1 > e0) {
+        auto load = [&](int64_t e, v4f (&r)[4], v4f& m) __attribute__((always_inline)) {
+            const float* Re = R + e * ld_R + c;
+#pragma unroll
+            for (int l = 0; l < 4; ++l) r[l] = ld4(Re + l * C);
+            const int64_t row = msg_row ? (int64_t)msg_row[e] : e;
+            m = ld4(msg + row * ld_msg + c);
+        };
+        v4f r[4], m, rn[4], mn;
+        load(e0, r, m);
+        for (int64_t e = e0; e < e1; ++e) {
+            load(e + 1 < e1 ? e + 1 : e, rn, mn);
+            float y[20];
+#pragma unroll
+            for (int x = 0; x < 20; ++x) y[x] = Y[e * ld_Y + x];
+            const float ev = env ? env[e] : 1.f;
+            const v4f me = m * ev;
+            const v4f w0 = r[0] * me, w1 = r[1] * me, w2 = r[2] * me, w3 = r[3] * me;
+            acc[0] += w0 * y[0];
+#pragma unroll
+            for (int x = 1; x < 4; ++x) acc[x] += w1 * y[x];
+#pragma unroll
+            for (int x = 4; x < 10; ++x) acc[x] += w2 * y[x];
+#pragma unroll
+            for (int x = 10; x < 20; ++x) acc[x] += w3 * y[x];
+#pragma unroll
+            for (int l = 0; l < 4; ++l) r[l] = rn[l];
+            m = mn;
+        }
+    }
+    if (lane < C / 4) {
+#pragma unroll
+        for (int x = 0; x < 20; ++x) st4(A.at(i, x) + c, acc[x]);
+    }
+}
+
 // ------------------------------------------------------------------ CP backward
 // Workgroup = atom i, one thread per channel (C <= 256); gA[i] sits in registers (channel
 // view) and in LDS (monomial view). Per tile of edges:
@@ -1454,6 +1510,15 @@ extern "C" int face_cp_density_fwd(const float* R, int32_t ld_R, const float* en
     if (N == 0) return 0;
     RankOut A;
     if (!R || !msg || !Y || !rank_out(A_ranks, atom_stride, x_stride, 20, A)) return FACE_ERR_ARG;
+    const bool a16 = aligned16(R) && aligned16(msg) && ld_R % 4 == 0 && ld_msg % 4 == 0 && A.sa % 4 == 0 &&
+                     A.sx % 4 == 0 && aligned16(A.p[0]) && aligned16(A.p[1]) && aligned16(A.p[2]) && aligned16(A.p[3]);
+    if (a16 && C % 4 == 0 && C <= 4 * kWave) {
+        hipLaunchKernelGGL(cp_density_fwd_wave_kernel, dim3((unsigned)((N + kCpfWaves - 1) / kCpfWaves)),
+                           dim3(kCpfWaves * kWave), 0, (hipStream_t)stream, R, ld_R, env, msg, ld_msg, msg_row, Y,
+                           ld_Y, row_ptr, N, M, C, A);
+        FACE_LAUNCH_CHECK();
+        return 0;
+    }
     int nthr = ((C + kWave - 1) / kWave) * kWave;
     if (nthr > kBlock) nthr = kBlock;
     dim3 grid((unsigned)N, (unsigned)((C + nthr - 1) / nthr));
