@@ -154,19 +154,26 @@ class DirTransport(torch.autograd.Function):
 
     d (E, 4Kd) = [u.V_j | u^T M_j u | u.V_i | u^T M_i u]          (face/model.py:474-493)
     D1 (3, N, B*2Kd), D2 (6, N, B*2Kd): sum_e phi[e, b] F(u, V_j, M_j)  (face/model.py:514-528)
-    One autograd node for both, so the tables' gradient is assembled in place (no slices).
+    One autograd node for both, so the tables' gradient is assembled in place (no slices). The
+    kernels read the tables node-major, packed as P (N, nt, 9, Kd) ([node][directional |
+    transport][V0..V2, M0..M5][channel]): a neighbour's 9 component rows of one part are 36 Kd
+    contiguous bytes instead of 9 rows each in its own cache line.
     """
 
     @staticmethod
     def forward(ctx, Vb, Mb, phi, Y, graph, Kd, transport):
         _lib.require_gpu(Vb, Mb, phi, Y)
-        Vb, Mb = Vb.contiguous().float(), Mb.contiguous().float()
         Y = Y.contiguous().float()
         N, E = graph.N, graph.E
         dev = Vb.device
         st = _lib.stream_of(Vb)
+        nt = Vb.shape[2] // Kd
+        P = torch.empty(N, nt, 9, Kd, device=dev)
+        P[:, :, :3].copy_(Vb.float().view(3, N, nt, Kd).permute(1, 2, 0, 3))
+        P[:, :, 3:].copy_(Mb.float().view(6, N, nt, Kd).permute(1, 2, 0, 3))
+        sn = nt * 9 * Kd
         d = torch.empty(E, 4 * Kd, device=dev)
-        call("face_dir_feats_fwd", ptr(Vb), Vb.stride(1), Vb.stride(0), ptr(Mb), Mb.stride(1), Mb.stride(0), Kd,
+        call("face_dir_feats_fwd", ptr(P), sn, Kd, ptr(P) + 4 * 3 * Kd, sn, Kd, Kd,
              ptr(graph.recv), ptr(graph.col), ptr(Y), E, ptr(d), st, label="dir_fwd")
         D1 = D2 = None
         phi_ = phi
@@ -175,27 +182,27 @@ class DirTransport(torch.autograd.Function):
             B = phi.shape[1]
             D1 = torch.empty(3, N, B * 2 * Kd, device=dev)
             D2 = torch.empty(6, N, B * 2 * Kd, device=dev)
-            call("face_transport_fwd", ptr(phi_), ld_phi, B, ptr(Vb) + 4 * Kd, Vb.stride(1), Vb.stride(0),
-                 ptr(Mb) + 4 * Kd, Mb.stride(1), Mb.stride(0), Kd, ptr(Y), 20, ptr(graph.col), ptr(graph.row_ptr), N,
-                 1.0, ptr(D1), ptr(D2), st, label="transport_fwd")
-        ctx.save_for_backward(Vb, Mb, phi_ if transport else torch.empty(0), Y)
-        ctx.graph, ctx.Kd, ctx.transport = graph, Kd, transport
+            pt = ptr(P) + 4 * 9 * Kd
+            call("face_transport_fwd", ptr(phi_), ld_phi, B, pt, sn, Kd, pt + 4 * 3 * Kd, sn, Kd, Kd, ptr(Y), 20,
+                 ptr(graph.col), ptr(graph.row_ptr), N, 1.0, ptr(D1), ptr(D2), st, label="transport_fwd")
+        ctx.save_for_backward(P, phi_ if transport else torch.empty(0), Y)
+        ctx.graph, ctx.Kd, ctx.transport, ctx.nt = graph, Kd, transport, nt
         return d, D1, D2
 
     @staticmethod
     def backward(ctx, gd, gD1, gD2):
-        Vb, Mb, phi, Y = ctx.saved_tensors
-        g, Kd = ctx.graph, ctx.Kd
+        P, phi, Y = ctx.saved_tensors
+        g, Kd, nt = ctx.graph, ctx.Kd, ctx.nt
         N, E = g.N, g.E
-        dev = Vb.device
-        st = _lib.stream_of(Vb)
+        dev = P.device
+        st = _lib.stream_of(P)
+        sn = nt * 9 * Kd
         gd = torch.zeros(E, 4 * Kd, device=dev) if gd is None else gd.contiguous().float()
-        gVb = torch.empty_like(Vb)
-        gMb = torch.empty_like(Mb)
+        gP = torch.empty_like(P)
         gY = torch.empty_like(Y)
-        call("face_dir_feats_bwd", ptr(Vb), Vb.stride(1), Vb.stride(0), ptr(Mb), Mb.stride(1), Mb.stride(0), Kd,
-             ptr(g.row_ptr), ptr(g.recv), ptr(g.col), ptr(g.rev), ptr(Y), ptr(gd), N, E, ptr(gVb), ptr(gMb), ptr(gY),
-             st, label="dir_bwd")
+        call("face_dir_feats_bwd", ptr(P), sn, Kd, ptr(P) + 4 * 3 * Kd, sn, Kd, Kd,
+             ptr(g.row_ptr), ptr(g.recv), ptr(g.col), ptr(g.rev), ptr(Y), ptr(gd), N, E, ptr(gP),
+             ptr(gP) + 4 * 3 * Kd, ptr(gY), st, label="dir_bwd")
         dphi = None
         if ctx.transport:
             B = phi.shape[1]
@@ -204,10 +211,12 @@ class DirTransport(torch.autograd.Function):
             gD2 = torch.zeros(6, N, W, device=dev) if gD2 is None else gD2.contiguous().float()
             dphi = torch.empty(E, B, device=dev)
             dT = torch.empty(E, 9, Kd, device=dev)
-            call("face_transport_bwd", ptr(phi), phi.stride(0), B, ptr(Vb) + 4 * Kd, Vb.stride(1), Vb.stride(0),
-                 ptr(Mb) + 4 * Kd, Mb.stride(1), Mb.stride(0), Kd, ptr(Y), 20, ptr(g.col), ptr(g.row_ptr), ptr(g.rev),
-                 N, g.max_row, 1.0, ptr(gD1), ptr(gD2), ptr(dphi), B, ptr(dT), ptr(gVb) + 4 * Kd, ptr(gMb) + 4 * Kd,
-                 ptr(gY), st, label="transport_bwd")
+            pt, gt = ptr(P) + 4 * 9 * Kd, ptr(gP) + 4 * 9 * Kd
+            call("face_transport_bwd", ptr(phi), phi.stride(0), B, pt, sn, Kd, pt + 4 * 3 * Kd, sn, Kd, Kd, ptr(Y), 20,
+                 ptr(g.col), ptr(g.row_ptr), ptr(g.rev), N, g.max_row, 1.0, ptr(gD1), ptr(gD2), ptr(dphi), B, ptr(dT),
+                 gt, gt + 4 * 3 * Kd, ptr(gY), st, label="transport_bwd")
+        gVb = gP[:, :, :3].permute(2, 0, 1, 3).reshape(3, N, nt * Kd)
+        gMb = gP[:, :, 3:].permute(2, 0, 1, 3).reshape(6, N, nt * Kd)
         return gVb, gMb, dphi, gY, None, None, None
 
 
