@@ -398,3 +398,91 @@ extern "C" int face_node_bwd(const float* const* ins, const int64_t* in_strides,
     FACE_LAUNCH_CHECK();
     return 0;
 }
+
+// ------------------------------------------------------------------ gated equivariant outputs
+// Vo[a, n, c] = V[a, n, c] gv[n, c], Mo[k, n, c] = Ms[k, n, c] gm[n, c] with gvm = [gv | gm]
+// (N, 2C) the gate row (face/model.py:286-296); V (3, N, C), Ms (6, N, C) contiguous. Thread =
+// (atom, channel quad), float4 throughout (C % 4 == 0, 16-byte aligned arrays).
+__global__ __launch_bounds__(256) void eq_gate_fwd_kernel(const float* __restrict__ V, const float* __restrict__ Ms,
+                                                          const float* __restrict__ gvm, int64_t N, int C,
+                                                          float* __restrict__ Vo, float* __restrict__ Mo) {
+    const int C4 = C / 4;
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= N * C4) return;
+    const int64_t n = t / C4;
+    const int c = 4 * (int)(t - n * C4);
+    const int64_t NC = N * C, o = n * C + c;
+    const v4f gv = ld4(gvm + n * 2 * C + c), gm = ld4(gvm + n * 2 * C + C + c);
+#pragma unroll
+    for (int a = 0; a < 3; ++a) st4(Vo + a * NC + o, ld4(V + a * NC + o) * gv);
+#pragma unroll
+    for (int k = 0; k < 6; ++k) st4(Mo + k * NC + o, ld4(Ms + k * NC + o) * gm);
+}
+
+// Backward: dV = gVo gv, dMs = gMo gm, dgv = sum_a gVo[a] V[a], dgm = sum_k gMo[k] Ms[k].
+__global__ __launch_bounds__(256) void eq_gate_bwd_kernel(const float* __restrict__ V, const float* __restrict__ Ms,
+                                                          const float* __restrict__ gvm, const float* __restrict__ gVo,
+                                                          const float* __restrict__ gMo, int64_t N, int C,
+                                                          float* __restrict__ dV, float* __restrict__ dMs,
+                                                          float* __restrict__ dgvm) {
+    const int C4 = C / 4;
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= N * C4) return;
+    const int64_t n = t / C4;
+    const int c = 4 * (int)(t - n * C4);
+    const int64_t NC = N * C, o = n * C + c;
+    const v4f gv = ld4(gvm + n * 2 * C + c), gm = ld4(gvm + n * 2 * C + C + c);
+    v4f sv = {0.f, 0.f, 0.f, 0.f}, sm = sv;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        const v4f g = ld4(gVo + a * NC + o);
+        sv += g * ld4(V + a * NC + o);
+        st4(dV + a * NC + o, g * gv);
+    }
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+        const v4f g = ld4(gMo + k * NC + o);
+        sm += g * ld4(Ms + k * NC + o);
+        st4(dMs + k * NC + o, g * gm);
+    }
+    st4(dgvm + n * 2 * C + c, sv);
+    st4(dgvm + n * 2 * C + C + c, sm);
+}
+
+static bool eq_gate_ok(int64_t N, int C, std::initializer_list<const void*> ps) {
+    if (N < 0 || C <= 0) return false;
+    for (const void* p : ps)
+        if (!p) return false;
+    return true;
+}
+static bool eq_gate_aligned(int C, std::initializer_list<const void*> ps) {
+    if (C % 4) return false;
+    for (const void* p : ps)
+        if ((uintptr_t)p & 15) return false;
+    return true;
+}
+
+extern "C" int face_eq_gate_fwd(const float* V, const float* Ms, const float* gvm, int64_t N, int32_t C, float* Vo,
+                                float* Mo, void* stream) {
+    if (!eq_gate_ok(N, C, {V, Ms, gvm, Vo, Mo})) return FACE_ERR_ARG;
+    if (!eq_gate_aligned(C, {V, Ms, gvm, Vo, Mo})) return FACE_ERR_UNSUPPORTED;
+    if (N == 0) return 0;
+    const int64_t total = N * (C / 4);
+    hipLaunchKernelGGL(eq_gate_fwd_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       V, Ms, gvm, N, C, Vo, Mo);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int face_eq_gate_bwd(const float* V, const float* Ms, const float* gvm, const float* gVo,
+                                const float* gMo, int64_t N, int32_t C, float* dV, float* dMs, float* dgvm,
+                                void* stream) {
+    if (!eq_gate_ok(N, C, {V, Ms, gvm, gVo, gMo, dV, dMs, dgvm})) return FACE_ERR_ARG;
+    if (!eq_gate_aligned(C, {V, Ms, gvm, gVo, gMo, dV, dMs, dgvm})) return FACE_ERR_UNSUPPORTED;
+    if (N == 0) return 0;
+    const int64_t total = N * (C / 4);
+    hipLaunchKernelGGL(eq_gate_bwd_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       V, Ms, gvm, gVo, gMo, N, C, dV, dMs, dgvm);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}

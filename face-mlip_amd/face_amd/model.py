@@ -278,8 +278,12 @@ class FactorBlock(nn.Module):
         o = run_frozen(self.out[2:], F.silu(z))
         eq_new = None
         if self.eq_out:
-            gv, gm = F.linear(inv, *frozen(self.gate)).chunk(2, dim=-1)
-            eq_new = (V * gv[None], Ms * gm[None])                                # (3,N,C), (6,N,C)
+            gvm = F.linear(inv, *frozen(self.gate))                               # (N, 2C) = [gv | gm]
+            if C % 4 == 0:
+                eq_new = ops.eq_gate(V, Ms, gvm)                                  # (3,N,C), (6,N,C)
+            else:
+                gv, gm = gvm.chunk(2, dim=-1)
+                eq_new = (V * gv[None], Ms * gm[None])
         return o[:, :1], h + o[:, 1:], A, eq_new
 
 

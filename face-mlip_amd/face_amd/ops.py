@@ -220,6 +220,39 @@ class DirTransport(torch.autograd.Function):
         return gVb, gMb, dphi, gY, None, None, None
 
 
+class EqGate(torch.autograd.Function):
+    """Gated equivariant outputs of a pass, V * gv and Ms * gm per (atom, channel), with the gate
+    row gvm = [gv | gm] (N, 2C) (face/model.py:286-287, :295-296): one launch each way (the
+    backward also gives the gate row's gradient)."""
+
+    @staticmethod
+    def forward(ctx, V, Ms, gvm):
+        _lib.require_gpu(V, Ms, gvm)
+        V, Ms, gvm = V.contiguous().float(), Ms.contiguous().float(), gvm.contiguous().float()
+        N, C = gvm.shape[0], gvm.shape[1] // 2
+        Vo, Mo = torch.empty_like(V), torch.empty_like(Ms)
+        call("face_eq_gate_fwd", ptr(V), ptr(Ms), ptr(gvm), N, C, ptr(Vo), ptr(Mo), _lib.stream_of(V),
+             label="eq_gate_fwd")
+        ctx.save_for_backward(V, Ms, gvm)
+        return Vo, Mo
+
+    @staticmethod
+    def backward(ctx, gVo, gMo):
+        V, Ms, gvm = ctx.saved_tensors
+        N, C = gvm.shape[0], gvm.shape[1] // 2
+        gVo = torch.zeros_like(V) if gVo is None else gVo.contiguous().float()
+        gMo = torch.zeros_like(Ms) if gMo is None else gMo.contiguous().float()
+        dV, dMs, dgvm = torch.empty_like(V), torch.empty_like(Ms), torch.empty_like(gvm)
+        call("face_eq_gate_bwd", ptr(V), ptr(Ms), ptr(gvm), ptr(gVo), ptr(gMo), N, C, ptr(dV), ptr(dMs), ptr(dgvm),
+             _lib.stream_of(V), label="eq_gate_bwd")
+        return dV, dMs, dgvm
+
+
+def eq_gate(V, Ms, gvm):
+    """V (3, N, C), Ms (6, N, C), gvm (N, 2C) -> (V * gv, Ms * gm)."""
+    return EqGate.apply(V, Ms, gvm)
+
+
 def dir_transport(Vb, Mb, phi, Y, graph, Kd, transport):
     return DirTransport.apply(Vb, Mb, phi, Y, graph, Kd, transport)
 

@@ -16,6 +16,7 @@
  *   face/kernels.py:135-172      FactorDensity / factor_density   -> face_density_fwd / _bwd
  *   face/model.py:496-502        CP pooling bmm                   -> face_cp_density_fwd / _bwd
  *   face/node_kernel.py:164-209  NodeAlgebra / node_algebra       -> face_node_fwd / _bwd
+ *   face/model.py:286-296        gated equivariant outputs V*gv, Ms*gm -> face_eq_gate_fwd / _bwd
  *   face/neighbors.py:7-37       padded_graph (ASE neighbor_list) -> face_nbr_* (count, fill, rev, padded)
  *   face/model.py:670-677        edge geometry + Bessel basis     -> face_edge_geom_fwd / _bwd
  *   face/model.py:465-469        radial MLP (rad_in, pair, radial) -> face_radial_fwd / _bwd
@@ -131,6 +132,18 @@ int face_node_bwd(const float* const* ins, const int64_t* in_strides, const floa
                   const float* gI, const int64_t* gI_strides, const float* gV, const int64_t* gV_strides,
                   const float* gM, const int64_t* gM_strides, int32_t mf_mode, float* const* outs,
                   const int64_t* out_strides, float* da, float* db, int64_t N, int32_t C, int32_t eq, void* stream);
+
+/* Gated equivariant outputs of a pass: Vo = V * gv, Mo = Ms * gm per (atom, channel), with
+ * gvm = [gv | gm] (N, 2C) the gate row; V (3, N, C), Ms (6, N, C), Vo, Mo likewise, all
+ * contiguous (C % 4 == 0 and 16-byte aligned, else FACE_ERR_UNSUPPORTED).
+ * Replaces `V * gv[..., None], Ms * gm[..., None]` of face/model.py:286-287 and :295-296. */
+int face_eq_gate_fwd(const float* V, const float* Ms, const float* gvm, int64_t N, int32_t C, float* Vo, float* Mo,
+                     void* stream);
+
+/* Backward of face_eq_gate_fwd for upstream gVo (3, N, C), gMo (6, N, C): dV = gVo * gv,
+ * dMs = gMo * gm, dgvm = [sum_a gVo[a] V[a] | sum_k gMo[k] Ms[k]] (N, 2C). */
+int face_eq_gate_bwd(const float* V, const float* Ms, const float* gvm, const float* gVo, const float* gMo, int64_t N,
+                     int32_t C, float* dV, float* dMs, float* dgvm, void* stream);
 
 /* ---------------------------------------------------------------- neighbour build
  * Pair set of ASE neighbor_list("ijS", atoms, rc) as used by face/neighbors.py:12-15 and

@@ -196,6 +196,28 @@ def test_cp_radial_density_fused_backward(gathered, C, H, N, pairs):
     assert max(errs) < TOL, errs
 
 
+# ----------------------------------------------------------------------------- gated outputs
+@pytest.mark.parametrize("N,C", [(1000, 160), (37, 96), (1, 4)])
+def test_eq_gate_matches_torch(N, C):
+    """V * gv, Ms * gm (face/model.py:286-287): outputs bit-exact against torch fp32, gradients of
+    V, Ms and the gate row within fp32 rounding of torch's autograd."""
+    from face_amd import ops
+    say("eq_gate", N, C)
+    torch.manual_seed(N + C)
+    V = torch.randn(3, N, C, device=DEV, requires_grad=True)
+    Ms = torch.randn(6, N, C, device=DEV, requires_grad=True)
+    gvm = torch.randn(N, 2 * C, device=DEV, requires_grad=True)
+    Vo, Mo = ops.eq_gate(V, Ms, gvm)
+    gv, gm = gvm.chunk(2, dim=-1)
+    Vr, Mr = V * gv[None], Ms * gm[None]
+    assert torch.equal(Vo, Vr) and torch.equal(Mo, Mr)
+    gV, gM = torch.randn_like(Vo), torch.randn_like(Mo)
+    g1 = torch.autograd.grad((Vo * gV).sum() + (Mo * gM).sum(), (V, Ms, gvm))
+    g2 = torch.autograd.grad((Vr * gV).sum() + (Mr * gM).sum(), (V, Ms, gvm))
+    for a, b in zip(g1, g2):
+        assert (a - b).abs().max().item() <= 1e-6 * (1 + b.abs().max().item())
+
+
 # ----------------------------------------------------------------------------- node algebra
 @pytest.mark.parametrize("eq", [True, False])
 def test_node_algebra_dropin_matches_reference_spec(eq):
