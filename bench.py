@@ -31,7 +31,8 @@ HBM_PEAK_GBS = 8000.0
 TIMED = ["density_fwd20", "density_bwd20", "cp_fwd", "cp_fwd_tab", "cp_bwd", "cp_bwd_tab", "cp_radial_bwd",
          "cp_radial_bwd_tab", "transport_fwd", "transport_bwd", "dir_fwd",
          "dir_bwd", "node_fwd", "node_bwd", "edge_fwd", "edge_bwd", "force_scatter", "gather_bwd", "radial_fwd",
-         "radial_bwd", "radial_head", "edge_msg_fwd", "edge_msg_bwd", "mix_fwd", "mix_bwd", "proj_fwd", "proj_bwd"]
+         "radial_bwd", "radial_head", "edge_msg_fwd", "edge_msg_bwd", "mix_fwd", "mix_bwd", "tmix_bwd", "proj_fwd",
+         "proj_bwd", "eq_gate_fwd", "eq_gate_bwd"]
 MFMA_PEAK_TFS = 157.3                   # MI355X dense fp32 MFMA
 
 
@@ -103,6 +104,8 @@ def algorithmic_flops(label, g, kw):
         return 2 * 20 * N * cin * C
     if label in ("proj_fwd", "proj_bwd"):
         return 2 * N * C * (C + 3 * 3 * C + 6 * 3 * C + 10 * 2 * C)
+    if label == "tmix_bwd":             # (3 + 6) N rows of C -> B * 2 K_dir transport columns
+        return 2 * 9 * N * C * kw["B"] * 2 * kw["K_dir"]
     if label == "radial_head":
         return 2 * E * H * 4 * C
     if label.startswith("cp_radial_bwd"):

@@ -727,14 +727,16 @@ class ScaledMix(torch.autograd.Function):
         dAf = [torch.empty(sh, device=dev) for sh in ctx.shapes]
         probs = [(g.view(-1, C), ctx.wm[l], dAf[l].view(-1, dAf[l].shape[-1]), l * C, 0.0) for l, g in enumerate(gA)]
         rows_linear(probs, w_kn=True, xs=s_tab, group=group, period=N, label="mix_bwd")
+        # transport mix: dD_l = (gA_l * s_l) wt, the scale applied to the rows as they load
         dD = [None, None]
-        s = None
+        tp = []
         for i, l in enumerate((1, 2)):
             if ctx.has_D[i] and ctx.needs_input_grad[4 + i]:
-                if s is None:
-                    s = s_tab[group.long()].view(N, 4, C)
-                gs = (gA[l] * s[None, :, l, :]).view(-1, C)
-                dD[i] = (gs @ ctx.wt[i]).view(gA[l].shape[0], N, -1)
+                wt = ctx.wt[i]
+                dD[i] = torch.empty(gA[l].shape[0], N, wt.shape[1], device=dev)
+                tp.append((gA[l].view(-1, C), wt, dD[i].view(-1, wt.shape[1]), l * C, 0.0))
+        if tp:
+            rows_linear(tp, w_kn=True, xs=s_tab, group=group, period=N, label="tmix_bwd")
         return (None, None, None, None, dD[0], dD[1], *dAf)
 
 
