@@ -455,7 +455,7 @@ static bool eq_gate_ok(int64_t N, int C, std::initializer_list<const void*> ps) 
         if (!p) return false;
     return true;
 }
-static bool eq_gate_aligned(int C, std::initializer_list<const void*> ps) {
+static bool vec4_ok(int C, std::initializer_list<const void*> ps) {
     if (C % 4) return false;
     for (const void* p : ps)
         if ((uintptr_t)p & 15) return false;
@@ -465,7 +465,7 @@ static bool eq_gate_aligned(int C, std::initializer_list<const void*> ps) {
 extern "C" int face_eq_gate_fwd(const float* V, const float* Ms, const float* gvm, int64_t N, int32_t C, float* Vo,
                                 float* Mo, void* stream) {
     if (!eq_gate_ok(N, C, {V, Ms, gvm, Vo, Mo})) return FACE_ERR_ARG;
-    if (!eq_gate_aligned(C, {V, Ms, gvm, Vo, Mo})) return FACE_ERR_UNSUPPORTED;
+    if (!vec4_ok(C, {V, Ms, gvm, Vo, Mo})) return FACE_ERR_UNSUPPORTED;
     if (N == 0) return 0;
     const int64_t total = N * (C / 4);
     hipLaunchKernelGGL(eq_gate_fwd_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
@@ -478,11 +478,127 @@ extern "C" int face_eq_gate_bwd(const float* V, const float* Ms, const float* gv
                                 const float* gMo, int64_t N, int32_t C, float* dV, float* dMs, float* dgvm,
                                 void* stream) {
     if (!eq_gate_ok(N, C, {V, Ms, gvm, gVo, gMo, dV, dMs, dgvm})) return FACE_ERR_ARG;
-    if (!eq_gate_aligned(C, {V, Ms, gvm, gVo, gMo, dV, dMs, dgvm})) return FACE_ERR_UNSUPPORTED;
+    if (!vec4_ok(C, {V, Ms, gvm, gVo, gMo, dV, dMs, dgvm})) return FACE_ERR_UNSUPPORTED;
     if (N == 0) return 0;
     const int64_t total = N * (C / 4);
     hipLaunchKernelGGL(eq_gate_bwd_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
                        V, Ms, gvm, gVo, gMo, N, C, dV, dMs, dgvm);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+// ------------------------------------------------------------------ readout LayerNorm
+// y = (x - mean) rstd w + b over rows of F features (face/model.py:140, :332: nn.LayerNorm of the
+// invariant row, biased variance, rstd = 1 / sqrt(var + eps)). One wave per row, the row held in
+// registers as float4 (F % 4 == 0, F <= 2048); mean and rstd are kept for the backward.
+constexpr int kLnMaxU = 8;                            // float4 per lane: F <= 64 * 4 * 8
+
+template <int U>
+__global__ __launch_bounds__(256) void layer_norm_fwd_kernel(const float* __restrict__ x, int64_t N, int F,
+                                                             const float* __restrict__ w, const float* __restrict__ b,
+                                                             float eps, float* __restrict__ y,
+                                                             float* __restrict__ mean, float* __restrict__ rstd) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t n = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
+    if (n >= N) return;
+    const int F4 = F / 4;
+    const float* xr = x + n * F;
+    v4f v[U];
+    float s = 0.f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int c4 = lane + kWave * u;
+        v[u] = c4 < F4 ? ld4(xr + 4 * c4) : (v4f){0.f, 0.f, 0.f, 0.f};
+        s += (v[u][0] + v[u][1]) + (v[u][2] + v[u][3]);
+    }
+    const float mu = group_sum(s, kWave) / (float)F;
+    float ss = 0.f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int c4 = lane + kWave * u;
+        if (c4 < F4) {
+            const v4f d = v[u] - mu;
+            ss += (d[0] * d[0] + d[1] * d[1]) + (d[2] * d[2] + d[3] * d[3]);
+        }
+    }
+    const float rs = 1.f / sqrtf(group_sum(ss, kWave) / (float)F + eps);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int c4 = lane + kWave * u;
+        if (c4 < F4) st4(y + n * F + 4 * c4, (v[u] - mu) * rs * ld4(w + 4 * c4) + ld4(b + 4 * c4));
+    }
+    if (lane == 0) {
+        mean[n] = mu;
+        rstd[n] = rs;
+    }
+}
+
+// dx = rstd (g - mean(g) - xh mean(g xh)), g = dy w, xh = (x - mean) rstd (no weight gradients).
+template <int U>
+__global__ __launch_bounds__(256) void layer_norm_bwd_kernel(const float* __restrict__ x,
+                                                             const float* __restrict__ dy, int64_t N, int F,
+                                                             const float* __restrict__ w,
+                                                             const float* __restrict__ mean,
+                                                             const float* __restrict__ rstd, float* __restrict__ dx) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t n = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
+    if (n >= N) return;
+    const int F4 = F / 4;
+    const float mu = mean[n], rs = rstd[n];
+    v4f g[U], xh[U];
+    float sg = 0.f, sgx = 0.f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int c4 = lane + kWave * u;
+        const v4f z = {0.f, 0.f, 0.f, 0.f};
+        g[u] = c4 < F4 ? ld4(dy + n * F + 4 * c4) * ld4(w + 4 * c4) : z;
+        xh[u] = c4 < F4 ? (ld4(x + n * F + 4 * c4) - mu) * rs : z;
+        sg += (g[u][0] + g[u][1]) + (g[u][2] + g[u][3]);
+        const v4f p = g[u] * xh[u];
+        sgx += (p[0] + p[1]) + (p[2] + p[3]);
+    }
+    const float a = group_sum(sg, kWave) / (float)F, c = group_sum(sgx, kWave) / (float)F;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const int c4 = lane + kWave * u;
+        if (c4 < F4) st4(dx + n * F + 4 * c4, rs * (g[u] - a - xh[u] * c));
+    }
+}
+
+static int ln_units(int F) { return (F / 4 + kWave - 1) / kWave; }
+
+extern "C" int face_layer_norm_fwd(const float* x, int64_t N, int32_t F, const float* w, const float* b, float eps,
+                                   float* y, float* mean, float* rstd, void* stream) {
+    if (N < 0 || F <= 0 || !x || !w || !b || !y || !mean || !rstd) return FACE_ERR_ARG;
+    if (F % 4 || ln_units(F) > kLnMaxU || !vec4_ok(F, {x, w, b, y})) return FACE_ERR_UNSUPPORTED;
+    if (N == 0) return 0;
+    const dim3 grid((unsigned)((N + 3) / 4)), block(256);
+    const hipStream_t st = (hipStream_t)stream;
+    switch (ln_units(F)) {
+#define FACE_LNF(U_) \
+    case U_: hipLaunchKernelGGL(layer_norm_fwd_kernel<U_>, grid, block, 0, st, x, N, F, w, b, eps, y, mean, rstd); break
+        FACE_LNF(1); FACE_LNF(2); FACE_LNF(3); FACE_LNF(4); FACE_LNF(5); FACE_LNF(6); FACE_LNF(7); FACE_LNF(8);
+#undef FACE_LNF
+        default: return FACE_ERR_UNSUPPORTED;
+    }
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int face_layer_norm_bwd(const float* x, const float* dy, int64_t N, int32_t F, const float* w,
+                                   const float* mean, const float* rstd, float* dx, void* stream) {
+    if (N < 0 || F <= 0 || !x || !dy || !w || !mean || !rstd || !dx) return FACE_ERR_ARG;
+    if (F % 4 || ln_units(F) > kLnMaxU || !vec4_ok(F, {x, dy, w, dx})) return FACE_ERR_UNSUPPORTED;
+    if (N == 0) return 0;
+    const dim3 grid((unsigned)((N + 3) / 4)), block(256);
+    const hipStream_t st = (hipStream_t)stream;
+    switch (ln_units(F)) {
+#define FACE_LNB(U_) \
+    case U_: hipLaunchKernelGGL(layer_norm_bwd_kernel<U_>, grid, block, 0, st, x, dy, N, F, w, mean, rstd, dx); break
+        FACE_LNB(1); FACE_LNB(2); FACE_LNB(3); FACE_LNB(4); FACE_LNB(5); FACE_LNB(6); FACE_LNB(7); FACE_LNB(8);
+#undef FACE_LNB
+        default: return FACE_ERR_UNSUPPORTED;
+    }
     FACE_LAUNCH_CHECK();
     return 0;
 }

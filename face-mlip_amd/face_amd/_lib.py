@@ -60,9 +60,11 @@ _SIGS = {
     "face_rows_linear": (ctypes.c_int, [P, I32, I32, P, P, P, I32, P, I64, P]),
     "face_eq_gate_fwd": (ctypes.c_int, [P, P, P, I64, I32, P, P, P]),
     "face_eq_gate_bwd": (ctypes.c_int, [P, P, P, P, P, I64, I32, P, P, P, P]),
+    "face_layer_norm_fwd": (ctypes.c_int, [P, I64, I32, P, P, ctypes.c_float, P, P, P, P]),
+    "face_layer_norm_bwd": (ctypes.c_int, [P, P, I64, I32, P, P, P, P, P]),
 }
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 
 class LinProblem(ctypes.Structure):

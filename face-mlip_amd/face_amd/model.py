@@ -271,7 +271,10 @@ class FactorBlock(nn.Module):
         else:
             feats, V, Ms = ops.node_features(ys[0], ys[1], ys[2], ys[3], None, None, False, C)
         nf = self.N_INV * C
-        inv = F.layer_norm(feats, (nf,), self.norm.weight.detach(), self.norm.bias.detach(), self.norm.eps)
+        if nf % 4 == 0 and nf <= 2048:
+            inv = ops.layer_norm(feats, self.norm.weight.detach(), self.norm.bias.detach(), self.norm.eps)
+        else:
+            inv = F.layer_norm(feats, (nf,), self.norm.weight.detach(), self.norm.bias.detach(), self.norm.eps)
         W0, b0 = frozen(self.out[0])
         # out[0] on cat([inv, h, 0 (4)]) as two accumulating GEMMs (no concatenated copy)
         z = F.linear(inv, W0[:, :nf], b0).addmm_(h, W0[:, nf:nf + C].t())

@@ -253,6 +253,40 @@ def eq_gate(V, Ms, gvm):
     return EqGate.apply(V, Ms, gvm)
 
 
+class LayerNorm(torch.autograd.Function):
+    """nn.LayerNorm of the readout's invariant row with frozen weight and bias (face/model.py:140,
+    :332): one wave per row each way; the input gradient only."""
+
+    @staticmethod
+    def forward(ctx, x, w, b, eps):
+        _lib.require_gpu(x, w, b)
+        x = x.contiguous().float()
+        N, F_ = x.shape
+        y = torch.empty_like(x)
+        mean = torch.empty(N, device=x.device)
+        rstd = torch.empty(N, device=x.device)
+        call("face_layer_norm_fwd", ptr(x), N, F_, ptr(w), ptr(b), float(eps), ptr(y), ptr(mean), ptr(rstd),
+             _lib.stream_of(x), label="ln_fwd")
+        ctx.save_for_backward(x, w, mean, rstd)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        if ctx.needs_input_grad[1] or ctx.needs_input_grad[2]:
+            raise NotImplementedError("the readout LayerNorm gives no weight gradients (forces only)")
+        x, w, mean, rstd = ctx.saved_tensors
+        dy = dy.contiguous().float()
+        dx = torch.empty_like(x)
+        call("face_layer_norm_bwd", ptr(x), ptr(dy), x.shape[0], x.shape[1], ptr(w), ptr(mean), ptr(rstd), ptr(dx),
+             _lib.stream_of(x), label="ln_bwd")
+        return dx, None, None, None
+
+
+def layer_norm(x, w, b, eps):
+    """x (N, F) -> LayerNorm over F with frozen w, b (F % 4 == 0, F <= 2048)."""
+    return LayerNorm.apply(x, w.contiguous(), b.contiguous(), eps)
+
+
 def dir_transport(Vb, Mb, phi, Y, graph, Kd, transport):
     return DirTransport.apply(Vb, Mb, phi, Y, graph, Kd, transport)
 

@@ -17,6 +17,7 @@
  *   face/model.py:496-502        CP pooling bmm                   -> face_cp_density_fwd / _bwd
  *   face/node_kernel.py:164-209  NodeAlgebra / node_algebra       -> face_node_fwd / _bwd
  *   face/model.py:286-296        gated equivariant outputs V*gv, Ms*gm -> face_eq_gate_fwd / _bwd
+ *   face/model.py:140,332        readout nn.LayerNorm             -> face_layer_norm_fwd / _bwd
  *   face/neighbors.py:7-37       padded_graph (ASE neighbor_list) -> face_nbr_* (count, fill, rev, padded)
  *   face/model.py:670-677        edge geometry + Bessel basis     -> face_edge_geom_fwd / _bwd
  *   face/model.py:465-469        radial MLP (rad_in, pair, radial) -> face_radial_fwd / _bwd
@@ -144,6 +145,18 @@ int face_eq_gate_fwd(const float* V, const float* Ms, const float* gvm, int64_t 
  * dMs = gMo * gm, dgvm = [sum_a gVo[a] V[a] | sum_k gMo[k] Ms[k]] (N, 2C). */
 int face_eq_gate_bwd(const float* V, const float* Ms, const float* gvm, const float* gVo, const float* gMo, int64_t N,
                      int32_t C, float* dV, float* dMs, float* dgvm, void* stream);
+
+/* LayerNorm of the readout's invariant row (face/model.py:140, :332): y = (x - mean) * rstd * w + b
+ * over rows of F features, biased variance, rstd = 1 / sqrt(var + eps); mean, rstd (N) are
+ * written for the backward. x, y (N, F) contiguous, F % 4 == 0, F <= 2048, 16-byte aligned
+ * (else FACE_ERR_UNSUPPORTED). */
+int face_layer_norm_fwd(const float* x, int64_t N, int32_t F, const float* w, const float* b, float eps, float* y,
+                        float* mean, float* rstd, void* stream);
+
+/* Input gradient of face_layer_norm_fwd: dx = rstd (g - mean(g) - xh mean(g xh)), g = dy w,
+ * xh = (x - mean) rstd. No weight gradients. */
+int face_layer_norm_bwd(const float* x, const float* dy, int64_t N, int32_t F, const float* w, const float* mean,
+                        const float* rstd, float* dx, void* stream);
 
 /* ---------------------------------------------------------------- neighbour build
  * Pair set of ASE neighbor_list("ijS", atoms, rc) as used by face/neighbors.py:12-15 and

@@ -218,6 +218,25 @@ def test_eq_gate_matches_torch(N, C):
         assert (a - b).abs().max().item() <= 1e-6 * (1 + b.abs().max().item())
 
 
+@pytest.mark.parametrize("N,F", [(24000, 1440), (37, 864), (5, 4), (300, 2048)])
+def test_layer_norm_matches_torch(N, F):
+    """Readout LayerNorm (face/model.py:332) and its input gradient against torch's fp32
+    LayerNorm on the same device, within fp32 rounding."""
+    from face_amd import ops
+    say("layer_norm", N, F)
+    torch.manual_seed(N + F)
+    x = (torch.randn(N, F, device=DEV) * 3 + 1).requires_grad_(True)
+    w = torch.randn(F, device=DEV)
+    b = torch.randn(F, device=DEV)
+    y1 = ops.layer_norm(x, w, b, 1e-5)
+    y2 = torch.nn.functional.layer_norm(x, (F,), w, b, 1e-5)
+    assert (y1 - y2).abs().max().item() < 1e-5 * (1 + y2.abs().max().item())
+    dy = torch.randn_like(y1)
+    g1, = torch.autograd.grad((y1 * dy).sum(), x)
+    g2, = torch.autograd.grad((y2 * dy).sum(), x)
+    assert (g1 - g2).abs().max().item() < 1e-5 * (1 + g2.abs().max().item())
+
+
 # ----------------------------------------------------------------------------- node algebra
 @pytest.mark.parametrize("eq", [True, False])
 def test_node_algebra_dropin_matches_reference_spec(eq):
