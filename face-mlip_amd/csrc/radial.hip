@@ -25,22 +25,18 @@ struct RadialWeights {
 __device__ __forceinline__ float sigmoidf_(float x) {
     return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.44269504088896341f * x));
 }
-__device__ __forceinline__ v4f silu4(v4f u) {
-    v4f o;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) o[r] = u[r] * sigmoidf_(u[r]);
-    return o;
-}
-// d silu(u) / du = s (1 + u (1 - s)), s = sigmoid(u)
-__device__ __forceinline__ v4f dsilu4(v4f u) {
+// silu(u) = u s with s = sigmoid(u), kept for the derivative
+__device__ __forceinline__ v4f silu4_s(v4f u, v4f& s) {
     v4f o;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-        const float s = sigmoidf_(u[r]);
-        o[r] = s * (1.f + u[r] * (1.f - s));
+        s[r] = sigmoidf_(u[r]);
+        o[r] = u[r] * s[r];
     }
     return o;
 }
+// d silu(u) / du = s (1 + u (1 - s)) = s + h (1 - s) from s = sigmoid(u) and h = silu(u)
+__device__ __forceinline__ v4f dsilu4_sh(v4f s, v4f h) { return s + h * (1.f - s); }
 
 // LDS image of the weights (floats): w_in [H][SI] (zero beyond n_basis), b_in [H],
 // pair_tab [n_pair][H], w1 [H][S1], b1 [H], w_phi [16 BB][S1] (zero rows >= B), b_phi [16 BB].
@@ -100,22 +96,22 @@ __device__ void radial_stage(float* lds, const RadialLds& L, const RadialWeights
 
 __device__ __forceinline__ v4f lds4(const float* p) { return *reinterpret_cast<const v4f*>(p); }
 
-// Forward chain of one tile: pre-activations u1, u2 (D layout) and phi before the envelope.
+// Forward chain of one tile (D layout): the two hidden activations hid, hh, their sigmoids s1, s2
+// (for the backward's SiLU derivative) and phi before the envelope.
 template <int HB, int BB>
 __device__ __forceinline__ void radial_chain(const float* lds, const RadialLds& L, const float* xb, int nkb, int p,
-                                             int j, int q, v4f (&u1)[HB], v4f (&u2)[HB], v4f (&hh)[HB],
-                                             v4f (&pl)[BB]) {
+                                             int j, int q, v4f (&s1)[HB], v4f (&hid)[HB], v4f (&s2)[HB],
+                                             v4f (&hh)[HB], v4f (&pl)[BB]) {
     constexpr int H = 16 * HB;
     const v4f z4 = {0.f, 0.f, 0.f, 0.f};
-    v4f hid[HB];
 #pragma unroll
     for (int hb = 0; hb < HB; ++hb) {
         v4f acc = z4;
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
             if (kb < nkb) acc = mfma_16x16x4(lds[(16 * hb + j) * L.SI + 4 * kb + q], xb[kb], acc);
-        u1[hb] = acc + lds4(lds + L.o_bin + 16 * hb + 4 * q) + lds4(lds + L.o_pt + p * H + 16 * hb + 4 * q);
-        hid[hb] = silu4(u1[hb]);
+        const v4f u1 = acc + lds4(lds + L.o_bin + 16 * hb + 4 * q) + lds4(lds + L.o_pt + p * H + 16 * hb + 4 * q);
+        hid[hb] = silu4_s(u1, s1[hb]);
     }
 #pragma unroll
     for (int h2b = 0; h2b < HB; ++h2b) {
@@ -126,8 +122,7 @@ __device__ __forceinline__ void radial_chain(const float* lds, const RadialLds& 
 #pragma unroll
             for (int r = 0; r < 4; ++r) acc = mfma_16x16x4(a[r], hid[hb][r], acc);
         }
-        u2[h2b] = acc + lds4(lds + L.o_b1 + 16 * h2b + 4 * q);
-        hh[h2b] = silu4(u2[h2b]);
+        hh[h2b] = silu4_s(acc + lds4(lds + L.o_b1 + 16 * h2b + 4 * q), s2[h2b]);
     }
 #pragma unroll
     for (int bb = 0; bb < BB; ++bb) {
@@ -185,8 +180,8 @@ __global__ __launch_bounds__(kRadWaves * kWave) void radial_fwd_kernel(
         for (int kb = 0; kb < 4; ++kb) xb[kb] = (ok && 4 * kb + q < nbasis) ? rb[e * ld_rb + 4 * kb + q] : 0.f;
         int p = ok ? pair[e] : 0;
         p = p < 0 ? 0 : (p >= n_pair ? n_pair - 1 : p);
-        v4f u1[HB], u2[HB], hh[HB], pl[BB];
-        radial_chain<HB, BB>(lds, L, xb, nkb, p, j, q, u1, u2, hh, pl);
+        v4f s1[HB], hid[HB], s2[HB], hh[HB], pl[BB];
+        radial_chain<HB, BB>(lds, L, xb, nkb, p, j, q, s1, hid, s2, hh, pl);
         if (ok) {
             if (h2) {
 #pragma unroll
@@ -200,7 +195,7 @@ __global__ __launch_bounds__(kRadWaves * kWave) void radial_fwd_kernel(
 }
 
 template <int HB, int BB>
-__global__ __launch_bounds__(kRadWaves * kWave) void radial_bwd_kernel(
+__global__ __launch_bounds__(kRadWaves * kWave) __attribute__((amdgpu_waves_per_eu(3))) void radial_bwd_kernel(
     const float* __restrict__ rb, int ld_rb, int nbasis, const int32_t* __restrict__ pair,
     const float* __restrict__ env, int64_t E, RadialWeights W, int n_pair, int B, const float* __restrict__ gh2,
     int ld_gh2, const float* __restrict__ gphi, int ld_gphi, float* __restrict__ grb, int ld_grb,
@@ -225,8 +220,8 @@ __global__ __launch_bounds__(kRadWaves * kWave) void radial_bwd_kernel(
         for (int kb = 0; kb < 4; ++kb) xb[kb] = (ok && 4 * kb + q < nbasis) ? rb[e * ld_rb + 4 * kb + q] : 0.f;
         int p = ok ? pair[e] : 0;
         p = p < 0 ? 0 : (p >= n_pair ? n_pair - 1 : p);
-        v4f u1[HB], u2[HB], hh[HB], pl[BB];
-        radial_chain<HB, BB>(lds, L, xb, nkb, p, j, q, u1, u2, hh, pl);
+        v4f s1[HB], hid[HB], s2[HB], hh[HB], pl[BB];
+        radial_chain<HB, BB>(lds, L, xb, nkb, p, j, q, s1, hid, s2, hh, pl);
         const float ev = ok ? (env ? env[e] : 1.f) : 0.f;
         // phi = pl * env: d env = sum_b gphi pl; d pl = gphi * env
         v4f gp[BB];
@@ -251,7 +246,7 @@ __global__ __launch_bounds__(kRadWaves * kWave) void radial_bwd_kernel(
                 for (int r = 0; r < 4; ++r)
                     acc = mfma_16x16x4(lds[L.o_wp + (16 * bb + 4 * q + r) * L.S1 + 16 * hb + j], gp[bb][r], acc);
             }
-            du2[hb] = acc * dsilu4(u2[hb]);
+            du2[hb] = acc * dsilu4_sh(s2[hb], hh[hb]);
         }
         // d hid = W1^T d u2;  d u1 = d hid * silu'(u1)
         v4f du1[HB];
@@ -264,7 +259,7 @@ __global__ __launch_bounds__(kRadWaves * kWave) void radial_bwd_kernel(
                 for (int r = 0; r < 4; ++r)
                     acc = mfma_16x16x4(lds[L.o_w1 + (16 * h2b + 4 * q + r) * L.S1 + 16 * hb + j], du2[h2b][r], acc);
             }
-            du1[hb] = acc * dsilu4(u1[hb]);
+            du1[hb] = acc * dsilu4_sh(s1[hb], hid[hb]);
         }
         // d rb = W_in^T d u1 (M = basis functions, one block of 16)
         v4f acc = z4;
