@@ -263,14 +263,19 @@ extern "C" int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, 
     GemmArgs A{};
     A.n_probs = n_probs, A.w_kn = w_kn ? 1 : 0, A.bias = bias, A.xs = x_scale, A.ys = y_scale;
     A.ld_s = ld_scale, A.group = group, A.period = period;
-    // 16-wave workgroups (4 waves per SIMD hide the row loads) unless that leaves CUs idle
+    // 16-wave workgroups (4 waves per SIMD hide the row loads) unless that leaves CUs idle; else 8
+    // (the staged weight slice serves twice the rows of 4 waves), except for several column
+    // slices of a (K, n) weight, measured better with 4
     auto wgs_for = [&](int nw) {
         int64_t t = 0;
         for (int i = 0; i < n_probs; ++i) t += (probs[i].m + 16 * kGemmBB * nw - 1) / (16 * kGemmBB * nw);
         return t;
     };
     const int n_cu = device_cu_count();
-    const int NW = wgs_for(16) >= n_cu ? 16 : (wgs_for(8) >= n_cu ? 8 : 4);
+    bool kn_slices = false;
+    for (int i = 0; i < n_probs; ++i)
+        if (w_kn && probs[i].m > 0 && probs[i].n > NS) kn_slices = true;
+    const int NW = wgs_for(16) >= n_cu ? 16 : (!kn_slices || wgs_for(8) >= n_cu ? 8 : 4);
     int max_n = 16;
     int64_t blocks = 0, total_cost = 0;
     for (int i = 0; i < n_probs; ++i) {
