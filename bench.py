@@ -270,6 +270,8 @@ def main():
     ap.add_argument("--cpu-atoms", type=int, default=1500)
     ap.add_argument("--eager", action="store_true", help="time eager steps instead of HIP-graph replays")
     ap.add_argument("--pmc-probe", action="store_true", help="short run for rocprofv3 --pmc passes")
+    ap.add_argument("--no-tunable", action="store_true",
+                    help="library GEMMs with hipBLASLt's default solutions instead of PyTorch TunableOp")
     a = ap.parse_args()
     if a.gpus != 1:
         print("bench.py measures one GPU only: there is no multi-GPU path in this library (the pair list "
@@ -282,6 +284,15 @@ def main():
     torch.backends.cuda.matmul.allow_tf32 = False
     torch.backends.cudnn.allow_tf32 = False
     torch.set_float32_matmul_precision("highest")
+    tunable = not a.no_tunable and not a.pmc_probe
+    if tunable:
+        # the GEMMs left to the libraries (readout MLP, tmix, per-node linears): PyTorch's
+        # TunableOp times the fp32 hipBLASLt / rocBLAS solutions of each shape in the warm-up steps
+        # and keeps the fastest whose result matches the default one (atol = rtol = 1e-5)
+        import tempfile
+        torch.cuda.tunable.enable(True)
+        torch.cuda.tunable.set_filename(os.path.join(tempfile.mkdtemp(prefix="face_tunableop_"), "results.csv"))
+        torch.cuda.tunable.set_numerical_check_tolerances(True, 1e-5, 1e-5)
     if a.pmc_probe:
         pmc_probe(a.workload)
         return
@@ -327,6 +338,8 @@ def main():
         "config": {"workload": main_run["desc"], "atoms": main_run["N"], "pairs": main_run["E"],
                    "model": {k: kw[k] for k in ("C", "B", "K", "rc") if k in kw} | {"cp": bool(kw.get("cp"))},
                    "weights": "random init, torch.manual_seed(0) + unit_parameterise", "parallelism": "single GPU",
+                   "library_gemms": ("fp32 hipBLASLt/rocBLAS, solutions picked by PyTorch TunableOp in the warm-up"
+                                     if tunable else "fp32 hipBLASLt default solutions"),
                    "step": main_run["mode"], "eager_ms_per_step": main_run["eager_ms_per_step"],
                    "peak_mem_gb": main_run["peak_mem_gb"]},
         "roofline": roofline,

@@ -103,6 +103,30 @@ def test_workload_shapes_match_oracle(k, n_atoms, n_mol):
     say(f"  dE/E {dE:.2e}  max|dF|/rms {dF:.2e}")
 
 
+@pytest.mark.parametrize("k,n_atoms", [(3, 1500), (2, None)])
+def test_workload_matches_oracle_with_tuned_library_gemms(k, n_atoms, tmp_path):
+    """The benchmark's setting for the GEMMs left to the libraries (PyTorch TunableOp picking among
+    fp32 hipBLASLt / rocBLAS solutions, numerical check on): same parity bar as above."""
+    import torch.cuda.tunable as tun
+    from face_amd import systems
+    from face_amd.neighbors import build_graph
+    sts, kw, el, desc = systems.workload(k, n_atoms=n_atoms)
+    say("tuned library GEMMs", k, desc)
+    tun.enable(True)
+    tun.set_filename(str(tmp_path / "tunableop.csv"))
+    tun.set_numerical_check_tolerances(True, 1e-5, 1e-5)
+    try:
+        m = product_model(kw, el)
+        g = build_graph(sts, kw["rc"])
+        m(g)                                                     # tunes every GEMM shape
+        o = m(g)
+    finally:
+        tun.enable(False)
+    Eo, Fo = _oracle_EF(sts, kw, el)
+    dE, dF = check(o["energy"].detach().cpu(), o["forces"].detach().cpu(), Eo, Fo)
+    say(f"  dE/E {dE:.2e}  max|dF|/rms {dF:.2e}")
+
+
 def test_forces_are_minus_energy_gradient_fd():
     """Central differences of the GPU energy (fp32, h = 1e-2 A on a smooth small model)."""
     from face_amd.neighbors import build_graph
