@@ -286,13 +286,9 @@ def main():
     torch.set_float32_matmul_precision("highest")
     tunable = not a.no_tunable and not a.pmc_probe
     if tunable:
-        # the GEMMs left to the libraries (readout MLP, tmix, per-node linears): PyTorch's
-        # TunableOp times the fp32 hipBLASLt / rocBLAS solutions of each shape in the warm-up steps
-        # and keeps the fastest whose result matches the default one (atol = rtol = 1e-5)
-        import tempfile
-        torch.cuda.tunable.enable(True)
-        torch.cuda.tunable.set_filename(os.path.join(tempfile.mkdtemp(prefix="face_tunableop_"), "results.csv"))
-        torch.cuda.tunable.set_numerical_check_tolerances(True, 1e-5, 1e-5)
+        # the GEMMs left to the libraries: solutions timed in the warm-up steps (face_amd.runner)
+        from face_amd.runner import tune_library_gemms
+        tune_library_gemms()
     if a.pmc_probe:
         pmc_probe(a.workload)
         return

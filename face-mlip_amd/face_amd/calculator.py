@@ -29,7 +29,10 @@ class FACECalculator:
 
     implemented_properties = ("energy", "forces")
 
-    def __init__(self, model, skin=0.5, use_graph=True, e_shift=0.0, device="cuda"):
+    def __init__(self, model, skin=0.5, use_graph=True, e_shift=0.0, device="cuda", tune_gemms=False):
+        if tune_gemms:                     # library GEMM solutions timed on the first step
+            from .runner import tune_library_gemms
+            tune_library_gemms()
         if model.training:
             raise ValueError("FACECalculator needs the model in evaluation mode (model.eval())")
         if skin < 0:

@@ -10,7 +10,23 @@ tools/graph_bench.py:29-40).
 The captured step allocates from a private pool and never synchronises with the host; new
 positions are copied into the static input buffer before each replay.
 """
+import os
+import tempfile
+
 import torch
+
+
+def tune_library_gemms(results_file=None):
+    """Let PyTorch TunableOp pick the solutions of the GEMMs left to the libraries (readout MLP,
+    tmix forward, per-node linears): the first call of each shape times the fp32 hipBLASLt /
+    rocBLAS solutions and keeps the fastest whose result matches the default one within 1e-5.
+    Call before the first step (tuning runs eagerly, so before any graph capture). Process-wide;
+    results go to results_file (default: a fresh temporary directory)."""
+    if results_file is None:
+        results_file = os.path.join(tempfile.mkdtemp(prefix="face_tunableop_"), "results.csv")
+    torch.cuda.tunable.enable(True)
+    torch.cuda.tunable.set_filename(results_file)
+    torch.cuda.tunable.set_numerical_check_tolerances(True, 1e-5, 1e-5)
 
 
 class StepGraph:
