@@ -55,18 +55,10 @@ def algorithmic_bytes(label, g, kw):
         return 4 * (E * (B + 3 + Kt // 2) + 18 * N * B * kw["K_dir"])
     if label == "transport_bwd":          # + upstream sums; dphi, du, per-edge table gradient out
         return 4 * (E * (B + 3 + Kt // 2) + 18 * N * B * kw["K_dir"] + E * (B + 3 + Kt // 2))
-    if label.startswith("cp_"):
-        # R (4C), env, Y (20) per edge; messages per edge (E x C) or a node table gathered
-        # through col (N x C + E); 20 N C pooled sums out (forward) or upstream in (backward)
-        msg = N * C + E if label.endswith("_tab") else E * C
-        ins = E * (4 * C + 1 + 20) + msg + 20 * N * C
-        if label.startswith("cp_fwd"):
-            return 4 * ins
-        H = kw.get("radial_hidden", 64)
-        if label.startswith("cp_radial_bwd"):   # + W_cp; d h2 (H), d msg (C), dY (20), d env per edge out
-            return 4 * (ins + 4 * C * H + E * (H + C + 20 + 1))
-        if label.startswith("cp_bwd"):          # dR (4C), d msg, dY, d env per edge out
-            return 4 * (ins + E * (4 * C + C + 20 + 1))
+    if label.startswith("cp_fwd"):          # the CP pooling drop-in: R (4C), msg (C), Y (20) per edge in
+        return 4 * (E * (5 * C + 20) + 20 * N * C)
+    if label.startswith(("cp_bwd", "cp_radial_bwd")):   # + dR, dmsg, dY per edge out (fused or not)
+        return 4 * (2 * E * (5 * C + 20) + 20 * N * C)
     if label == "node_fwd":
         return 4 * 67 * N * C           # 47 in; 8 invariants + V (3) + full Mf (9) out
     if label == "node_bwd":
@@ -90,6 +82,24 @@ def algorithmic_bytes(label, g, kw):
     if label == "edge_msg_bwd":         # upstream (E, K), rev in; d d (E, 4Kd) and the table gradient out
         return 4 * (E * (K + 1 + Kd4) + N * K)
     return None
+
+
+def interface_bytes(label, g, kw):
+    """Bytes the CP launches' own interfaces move (each operand read once, each output written
+    once): the envelope, node-table messages gathered through col (N x C + E) under the "_tab"
+    labels, and for the fused backward W_cp in and d h2 (E x H) out instead of dR. None for the
+    other labels (their algorithmic figure is their interface)."""
+    E, N, C = g.E, g.N, kw["C"]
+    if not label.startswith("cp_"):
+        return None
+    msg = N * C + E if label.endswith("_tab") else E * C
+    ins = E * (4 * C + 1 + 20) + msg + 20 * N * C
+    if label.startswith("cp_fwd"):
+        return 4 * ins
+    H = kw.get("radial_hidden", 64)
+    if label.startswith("cp_radial_bwd"):
+        return 4 * (ins + 4 * C * H + E * (H + C + 20 + 1))
+    return 4 * (ins + E * (4 * C + C + 20 + 1))
 
 
 def algorithmic_flops(label, g, kw):
@@ -179,9 +189,11 @@ def run_gpu(k, steps, warmup, use_graph=True):
         avg_us = 1e3 * float(np.mean(ms))
         byts = algorithmic_bytes(label, g, kw)
         fl = algorithmic_flops(label, g, kw)
+        ib = interface_bytes(label, g, kw)
         kern[label] = {"launches_per_step": len(evs) / steps, "avg_us": avg_us,
                        "ms_per_step": float(np.sum(ms)) / steps,
                        "alg_bytes": byts, "alg_flops": fl, "GBps": (byts / (avg_us * 1e-6) / 1e9) if byts else None,
+                       "GBps_interface": (ib / (avg_us * 1e-6) / 1e9) if ib else None,
                        "TFLOPs": (fl / (avg_us * 1e-6) / 1e12) if fl else None}
     ms_step = 1e3 * dt / steps
     log(f"[bench]   {ms_step:.3f} ms/step, {g.N * steps / dt:.0f} atom-steps/s")
@@ -213,6 +225,7 @@ def pmc_probe(k, steps=2, copy_floats=1 << 28):
     torch.cuda.synchronize()
     out = {"probe": desc, "steps": steps, "copy_bytes_read": 4 * copy_floats, "copy_bytes_written": 4 * copy_floats,
            "alg_bytes": {lab: algorithmic_bytes(lab, g, kw) for lab in TIMED},
+           "interface_bytes": {lab: interface_bytes(lab, g, kw) for lab in TIMED},
            "alg_flops": {lab: algorithmic_flops(lab, g, kw) for lab in TIMED}, "order": order}
     print(json.dumps(out), flush=True)
 
@@ -341,6 +354,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "kernels": {k: {"avg_us": v["avg_us"], "launches_per_step": v["launches_per_step"], "GBps": v["GBps"],
+                        "GBps_interface": v["GBps_interface"],
                         "frac_hbm": (v["GBps"] / HBM_PEAK_GBS) if v["GBps"] else None,
                         "TFLOPs": v["TFLOPs"], "frac_mfma": (v["TFLOPs"] / MFMA_PEAK_TFS) if v["TFLOPs"] else None}
                     for k, v in kern.items()},

@@ -399,6 +399,8 @@ extern "C" int face_node_bwd(const float* const* ins, const int64_t* in_strides,
     return 0;
 }
 
+namespace face {
+
 // ------------------------------------------------------------------ gated equivariant outputs
 // Vo[a, n, c] = V[a, n, c] gv[n, c], Mo[k, n, c] = Ms[k, n, c] gm[n, c] with gvm = [gv | gm]
 // (N, 2C) the gate row (face/model.py:286-296); V (3, N, C), Ms (6, N, C) contiguous. Thread =
@@ -462,6 +464,8 @@ static bool vec4_ok(int C, std::initializer_list<const void*> ps) {
     return true;
 }
 
+}  // namespace face
+
 extern "C" int face_eq_gate_fwd(const float* V, const float* Ms, const float* gvm, int64_t N, int32_t C, float* Vo,
                                 float* Mo, void* stream) {
     if (!eq_gate_ok(N, C, {V, Ms, gvm, Vo, Mo})) return FACE_ERR_ARG;
@@ -486,6 +490,8 @@ extern "C" int face_eq_gate_bwd(const float* V, const float* Ms, const float* gv
     FACE_LAUNCH_CHECK();
     return 0;
 }
+
+namespace face {
 
 // ------------------------------------------------------------------ readout LayerNorm
 // y = (x - mean) rstd w + b over rows of F features (face/model.py:140, :332: nn.LayerNorm of the
@@ -566,6 +572,8 @@ __global__ __launch_bounds__(256) void layer_norm_bwd_kernel(const float* __rest
 }
 
 static int ln_units(int F) { return (F / 4 + kWave - 1) / kWave; }
+
+}  // namespace face
 
 extern "C" int face_layer_norm_fwd(const float* x, int64_t N, int32_t F, const float* w, const float* b, float eps,
                                    float* y, float* mean, float* rstd, void* stream) {
