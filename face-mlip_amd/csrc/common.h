@@ -48,6 +48,27 @@ __device__ __forceinline__ v4f mfma_16x16x4(float a, float b, v4f c) {
 __device__ __forceinline__ v4f ld4(const float* p) { return *reinterpret_cast<const v4f*>(p); }
 __device__ __forceinline__ void st4(float* p, v4f v) { *reinterpret_cast<v4f*>(p) = v; }
 
+// Workgroup copy of n float4 items, put(v, src(v)) for v < n, U loads per thread issued before
+// their U stores: a staging loop that stores each item before loading the next one waits a
+// full memory latency per round.
+template <int U, typename Src, typename Put>
+__device__ __forceinline__ void stage4(int n, Src src, Put put) {
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    for (int v0 = 0; v0 < n; v0 += U * nthr) {
+        v4f b[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int v = v0 + u * nthr + tid;
+            if (v < n) b[u] = src(v);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int v = v0 + u * nthr + tid;
+            if (v < n) put(v, b[u]);
+        }
+    }
+}
+
 // LDS image of a (F, K) row-major weight block read as float4 chunks of 16 rows at a time:
 // row f at f * S; with S = K (K = 32, 64) the float4 chunk c of row f is stored at chunk
 // (c + f) mod K/4, otherwise S = K + 4: both keep the 16 rows read by one instruction on

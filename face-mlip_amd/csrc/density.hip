@@ -1069,10 +1069,12 @@ __global__ __launch_bounds__(NW * kWave) void cp_radial_bwd_res_kernel(
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     const int j = lane & 15, q = lane >> 4;
     const int RS = 4 * C, nch = C;
-    for (int f = tid; f < H * nch; f += NW * kWave) {
-        const int h = f / nch, c = f - h * nch;
-        st4(lds + h * RS + 4 * (c ^ (h & 15)), ld4(w_t + (int64_t)h * RS + 4 * c));
-    }
+    stage4<8>(
+        H * nch, [&](int f) { return ld4(w_t + 4 * (int64_t)f); },
+        [&](int f, v4f x) {
+            const int h = f / nch, c = f - h * nch;
+            st4(lds + h * RS + 4 * (c ^ (h & 15)), x);
+        });
     __syncthreads();
     // this wave's rows: those whose first edge lies in its share of the edges
     const int64_t W = (int64_t)gridDim.x * NW;

@@ -158,22 +158,47 @@ __global__ __launch_bounds__(256) void segment_sum_kernel(const float* __restric
     out[k * ld_out + f] = s;
 }
 
+// grad[k] = sign * sum_{e in row k} (g[rev e] - g[e]). G lanes per atom (a power of two <= 64,
+// ~half the mean row length): lane l takes edges l, l + G, ... of the row two at a time, so
+// the row's own g and rev entries are read coalesced and every lane has two reverse-edge
+// gathers in flight; the G partial sums are then reduced by butterfly shuffles.
+template <int G>
 __global__ __launch_bounds__(256) void force_scatter_kernel(const float* __restrict__ gvec,
                                                             const int32_t* __restrict__ row_ptr,
                                                             const int32_t* __restrict__ rev, int64_t N, float sign,
                                                             float* __restrict__ grad) {
-    const int64_t k = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    if (k >= N) return;
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    const int l = threadIdx.x & (G - 1);
+    const int64_t k = t / G;
+    const bool live = k < N;                            // whole groups of G lanes share k
     float s0 = 0.f, s1 = 0.f, s2 = 0.f;
-    for (int64_t e = row_ptr[k]; e < row_ptr[k + 1]; ++e) {
-        const int64_t r = rev[e];
-        s0 += gvec[r * 3 + 0] - gvec[e * 3 + 0];
-        s1 += gvec[r * 3 + 1] - gvec[e * 3 + 1];
-        s2 += gvec[r * 3 + 2] - gvec[e * 3 + 2];
+    const int64_t e0 = live ? row_ptr[k] : 0, e1 = live ? row_ptr[k + 1] : 0;
+    for (int64_t e = e0 + l; e < e1; e += 2 * G) {
+        const int64_t f = e + G;
+        const bool two = f < e1;
+        const int64_t r = rev[e], rf = two ? (int64_t)rev[f] : r;
+        const float a0 = gvec[r * 3 + 0], a1 = gvec[r * 3 + 1], a2 = gvec[r * 3 + 2];
+        const float b0 = gvec[e * 3 + 0], b1 = gvec[e * 3 + 1], b2 = gvec[e * 3 + 2];
+        const float c0 = gvec[rf * 3 + 0], c1 = gvec[rf * 3 + 1], c2 = gvec[rf * 3 + 2];
+        const int64_t fe = two ? f : e;
+        const float d0 = gvec[fe * 3 + 0], d1 = gvec[fe * 3 + 1], d2 = gvec[fe * 3 + 2];
+        s0 += a0 - b0;
+        s1 += a1 - b1;
+        s2 += a2 - b2;
+        if (two) {
+            s0 += c0 - d0;
+            s1 += c1 - d1;
+            s2 += c2 - d2;
+        }
     }
-    grad[k * 3 + 0] = sign * s0;
-    grad[k * 3 + 1] = sign * s1;
-    grad[k * 3 + 2] = sign * s2;
+    s0 = group_sum(s0, G);
+    s1 = group_sum(s1, G);
+    s2 = group_sum(s2, G);
+    if (live && l == 0) {
+        grad[k * 3 + 0] = sign * s0;
+        grad[k * 3 + 1] = sign * s1;
+        grad[k * 3 + 2] = sign * s2;
+    }
 }
 
 // ---------------------------------------------------------------- directional edge features
@@ -388,8 +413,9 @@ extern "C" int face_force_scatter(const float* gvec, const int32_t* row_ptr, con
     if (N < 0) return FACE_ERR_ARG;
     if (N == 0) return 0;
     if (!gvec || !row_ptr || !rev || !grad) return FACE_ERR_ARG;
-    hipLaunchKernelGGL(force_scatter_kernel, dim3(blocks_for(N)), dim3(256), 0, (hipStream_t)stream, gvec, row_ptr,
-                       rev, N, sign, grad);
+    constexpr int G = 16;                               // rows of ~10-70 pairs: one or two sweeps
+    hipLaunchKernelGGL(force_scatter_kernel<G>, dim3(blocks_for(N * G)), dim3(256), 0, (hipStream_t)stream, gvec,
+                       row_ptr, rev, N, sign, grad);
     FACE_LAUNCH_CHECK();
     return 0;
 }

@@ -85,24 +85,46 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
             // stage W[n0 : n0 + ns, :] as rows of K (+ 4 pad); rows ns .. 16 NB - 1 are zero, so
             // the MFMA loop below runs all NB blocks without branches
             if (PERSIST) __syncthreads();                                // every wave is done with the old slice
+            // four loads per thread issued before their LDS stores (a loop that stores each
+            // float4 before loading the next waits a memory latency per round)
+            const float* __restrict__ wsrc = P.w;
+            const int64_t ldw = P.ld_w;
+            const int nthr = blockDim.x;
             if (!A.w_kn) {
-                const int nk4 = K / 4;
-                for (int v = tid; v < 16 * NB * nk4; v += blockDim.x) {
-                    const int r = v / nk4, c4 = v - r * nk4;
-                    st4(sW + r * SK + 4 * c4, r < ns ? ld4(P.w + (int64_t)(n0 + r) * P.ld_w + 4 * c4) : z4);
+                const int nk4 = K / 4, tot = 16 * NB * nk4;
+                for (int v0 = tid; v0 < tot; v0 += 4 * nthr) {
+                    v4f b[4];
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int v = v0 + u * nthr, r = v / nk4, c4 = v - r * nk4;
+                        b[u] = (v < tot && r < ns) ? ld4(wsrc + (int64_t)(n0 + r) * ldw + 4 * c4) : z4;
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) {
+                        const int v = v0 + u * nthr, r = v / nk4, c4 = v - r * nk4;
+                        if (v < tot) st4(sW + r * SK + 4 * c4, b[u]);
+                    }
                 }
             } else {                                                     // W given as (K, n)
-                // thread (k4, r): four coalesced reads down column n0 + r, one float4 into row r
-                const int nr = 16 * NB;
-                for (int v = tid; v < nr * (K / 4); v += blockDim.x) {
-                    const int k4 = v / nr, r = v - k4 * nr;
-                    v4f c4 = z4;
-                    if (r < ns) {
-                        const float* col = P.w + (int64_t)(4 * k4) * P.ld_w + n0 + r;
+                // item (k4, r): four coalesced reads down column n0 + r, one float4 into row r
+                const int nr = 16 * NB, tot = nr * (K / 4);
+                for (int v0 = tid; v0 < tot; v0 += 2 * nthr) {
+                    v4f b[2];
 #pragma unroll
-                        for (int u = 0; u < 4; ++u) c4[u] = col[(int64_t)u * P.ld_w];
+                    for (int u = 0; u < 2; ++u) {
+                        const int v = v0 + u * nthr, k4 = v / nr, r = v - k4 * nr;
+                        b[u] = z4;
+                        if (v < tot && r < ns) {
+                            const float* col = wsrc + (int64_t)(4 * k4) * ldw + n0 + r;
+#pragma unroll
+                            for (int c = 0; c < 4; ++c) b[u][c] = col[c * ldw];
+                        }
                     }
-                    st4(sW + r * SK + 4 * k4, c4);
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const int v = v0 + u * nthr, k4 = v / nr, r = v - k4 * nr;
+                        if (v < tot) st4(sW + r * SK + 4 * k4, b[u]);
+                    }
                 }
             }
             __syncthreads();
