@@ -1,6 +1,6 @@
 """Energy + forces throughput of the FACE hot path on one MI355X.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload 3] [--also 2] [--no-cpu]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload 3] [--also 2] [--compiled 2,3] [--no-cpu]
 
 A step is one energy + forces evaluation of the whole synthetic system with its pair list
 already resident in HBM (the pair-list build is timed separately, as the reference excludes
@@ -32,7 +32,7 @@ TIMED = ["density_fwd20", "density_bwd20", "cp_fwd", "cp_fwd_tab", "cp_bwd", "cp
          "cp_radial_bwd_tab", "transport_fwd", "transport_bwd", "dir_fwd",
          "dir_bwd", "node_fwd", "node_bwd", "edge_fwd", "edge_bwd", "force_scatter", "gather_bwd", "radial_fwd",
          "radial_bwd", "radial_head", "edge_msg_fwd", "edge_msg_bwd", "mix_fwd", "mix_bwd", "tmix_bwd", "proj_fwd",
-         "proj_bwd", "eq_gate_fwd", "eq_gate_bwd", "ln_fwd", "ln_bwd"]
+         "proj_bwd", "eq_gate_fwd", "eq_gate_bwd", "ln_fwd", "ln_bwd", "spline_fwd", "spline_bwd"]
 MFMA_PEAK_TFS = 157.3                   # MI355X dense fp32 MFMA
 
 
@@ -69,6 +69,11 @@ def algorithmic_bytes(label, g, kw):
         return 4 * E * (11 + 29 + 3)
     if label == "force_scatter":
         return 4 * (3 * E + E + 3 * N)
+    if label.startswith("spline_"):     # r, pair, env in, F columns out (in); both tables read once
+        F = kw.get("B", 16) + (4 * C if kw.get("cp") else 0)
+        n_el = kw.get("n_elem", 3)
+        tables = 8 * n_el * n_el * kw.get("n_grid", 4096) * F
+        return 4 * E * (3 + F) + tables + (8 * E if label == "spline_bwd" else 0)
     H, nb = kw.get("radial_hidden", 64), kw.get("n_basis", 8)
     if label == "radial_fwd":           # rb, pair, env in; phi (and h2 in CP mode) out
         return 4 * E * (nb + 2 + B + (H if kw.get("cp") else 0))
@@ -131,10 +136,12 @@ def model_for(kw, el):
     return m.cuda().eval()
 
 
-def run_gpu(k, steps, warmup, use_graph=True):
+def run_gpu(k, steps, warmup, use_graph=True, compiled_radial=False):
     from face_amd import _lib, systems
     from face_amd.neighbors import build_graph
     sts, kw, el, desc = systems.workload(k)
+    if compiled_radial:
+        desc += ", compiled radial (4096-point splines)"
     log(f"[bench] workload {k}: {desc}")
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -143,6 +150,9 @@ def run_gpu(k, steps, warmup, use_graph=True):
     t_nbr = time.perf_counter() - t0
     log(f"[bench]   pair list: N={g.N} E={g.E} max_row={g.max_row} ({t_nbr * 1e3:.1f} ms incl. host staging)")
     m = model_for(kw, el)
+    if compiled_radial:
+        m.compile_radial()
+        kw = dict(kw, n_elem=len(el), n_grid=4096)
 
     def step():
         return m(g.with_pos(g.pos.clone()))["forces"]
@@ -279,6 +289,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--workload", type=int, default=3)
     ap.add_argument("--also", default="2", help="comma list of extra workloads reported under 'also'")
+    ap.add_argument("--compiled", default="2,3",
+                    help="comma list of workloads also run with compile_radial() (the reference calculator's "
+                         "CUDA setting), reported under 'also'")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-atoms", type=int, default=1500)
     ap.add_argument("--eager", action="store_true", help="time eager steps instead of HIP-graph replays")
@@ -307,15 +320,16 @@ def main():
         return
     main_run = run_gpu(a.workload, a.steps, a.warmup, not a.eager)
     also = {}
-    for k in [int(x) for x in a.also.split(",") if x.strip()]:
-        if k != a.workload:
-            r = run_gpu(k, a.steps, a.warmup, not a.eager)
-            also[f"workload{k}"] = {"desc": r["desc"], "atoms": r["N"], "pairs": r["E"],
-                                    "atom_steps_per_s": r["atom_steps_per_s"], "ms_per_step": r["ms_per_step"],
-                                    "pairlist_ms": r["pairlist_ms"], "mode": r["mode"],
-                                    "eager_ms_per_step": r["eager_ms_per_step"],
-                                    "kernels": {kk: {"avg_us": v["avg_us"], "GBps": v["GBps"], "TFLOPs": v["TFLOPs"]}
-                                                for kk, v in r["kernels"].items()}}
+    runs = [(int(x), False) for x in a.also.split(",") if x.strip() and int(x) != a.workload]
+    runs += [(int(x), True) for x in a.compiled.split(",") if x.strip()]
+    for k, comp in runs:
+        r = run_gpu(k, a.steps, a.warmup, not a.eager, compiled_radial=comp)
+        also[f"workload{k}" + ("_compiled_radial" if comp else "")] = {
+            "desc": r["desc"], "atoms": r["N"], "pairs": r["E"], "atom_steps_per_s": r["atom_steps_per_s"],
+            "ms_per_step": r["ms_per_step"], "pairlist_ms": r["pairlist_ms"], "mode": r["mode"],
+            "eager_ms_per_step": r["eager_ms_per_step"],
+            "kernels": {kk: {"avg_us": v["avg_us"], "GBps": v["GBps"], "TFLOPs": v["TFLOPs"]}
+                        for kk, v in r["kernels"].items()}}
     kern = main_run["kernels"]
     known = {k: v for k, v in kern.items() if v["alg_bytes"] or v["alg_flops"]}
     dom = max(known, key=lambda k: known[k]["ms_per_step"]) if known else None

@@ -291,6 +291,120 @@ static bool radial_args_ok(const float* rb, int ld_rb, int nbasis, const int32_t
     return W.w_in && W.b_in && W.pair_tab && W.w1 && W.b1 && W.w_phi && W.b_phi;
 }
 
+
+// ------------------------------------------------------------------ compiled radial (splines)
+// phi(r; pair) from a table on a uniform grid r_g = g dr (face/model.py:383-418): values T and
+// exact derivatives dT, (P pairs, G points, F columns) row-major; cubic Hermite (C1) between
+// grid points, x = clamp(r / dr, 0, G - 1), i = min(floor x, G - 2), t = x - i:
+//   S = h00 T[i] + h10 dr dT[i] + h01 T[i+1] + h11 dr dT[i+1]
+//   h00 = 2t^3 - 3t^2 + 1, h10 = t^3 - 2t^2 + t, h01 = -2t^3 + 3t^2, h11 = t^3 - t^2,
+// evaluated as T[i] + h01 (T[i+1] - T[i]) + ... (h00 = 1 - h01): neighbouring table values differ
+// by ~dr |dS/dr|, and their fp32 difference is exact, whereas h00 T[i] + h01 T[i+1] rounds both
+// products before they cancel -- in the r-derivative 6t(1-t) (T[i+1] - T[i]) / dr that round-off
+// would be ~1e-4 of the slope at 4096 points.
+// Columns f < nb go to phi[e][f] times env[e], columns f >= nb to R[e][f - nb] as they are
+// (the CP columns: the pooling kernels apply the envelope). L lanes per edge (a power of two,
+// about the row width) walk the columns, so every table row is read coalesced; the backward
+// sums its column terms over those lanes.
+struct SplineTab {
+    const float *T, *dT;
+    int P, G, F;
+    float dr;
+};
+
+struct SplineCell {
+    int64_t row;                                       // offset of T[pair][i][0]
+    float t;
+    bool inside;                                       // r / dr within [0, G - 1] (clamp passes d/dr)
+};
+
+__device__ __forceinline__ SplineCell spline_cell(float r, int32_t pair, const SplineTab& S) {
+    SplineCell c;
+    const float x0 = r / S.dr, hi = (float)(S.G - 1);
+    c.inside = x0 >= 0.f && x0 <= hi;
+    const float x = fminf(fmaxf(x0, 0.f), hi);        // NaN -> 0: the cell stays inside the table
+    const int i = min((int)floorf(x), S.G - 2);
+    c.t = x - (float)i;
+    const int p = min(max((int)pair, 0), S.P - 1);
+    c.row = ((int64_t)p * S.G + i) * S.F;
+    return c;
+}
+
+template <int L>
+__global__ __launch_bounds__(256) void radial_spline_fwd_kernel(const float* __restrict__ r,
+                                                                const int32_t* __restrict__ pair, int64_t E,
+                                                                SplineTab S, const float* __restrict__ env, int nb,
+                                                                float* __restrict__ phi, int ld_phi,
+                                                                float* __restrict__ R, int ld_R) {
+    const int64_t tid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    const int64_t e = tid / L;
+    const int l = (int)(tid % L);
+    if (e >= E) return;
+    const SplineCell c = spline_cell(r[e], pair[e], S);
+    const float t = c.t, t2 = t * t, t3 = t2 * t;
+    const float h10 = t3 - 2.f * t2 + t, h01 = -2.f * t3 + 3.f * t2, h11 = t3 - t2;
+    const float ev = env ? env[e] : 1.f;
+    const float* T0 = S.T + c.row;
+    const float* D0 = S.dT + c.row;
+    for (int f = l; f < S.F; f += L) {
+        const float p0 = T0[f], p1 = T0[S.F + f];
+        const float m0 = D0[f] * S.dr, m1 = D0[S.F + f] * S.dr;
+        const float v = p0 + (h01 * (p1 - p0) + (h10 * m0 + h11 * m1));
+        if (f < nb)
+            phi[e * ld_phi + f] = v * ev;
+        else
+            R[e * ld_R + f - nb] = v;
+    }
+}
+
+template <int L>
+__global__ __launch_bounds__(256) void radial_spline_bwd_kernel(const float* __restrict__ r,
+                                                                const int32_t* __restrict__ pair, int64_t E,
+                                                                SplineTab S, const float* __restrict__ env, int nb,
+                                                                const float* __restrict__ gphi, int ld_gphi,
+                                                                const float* __restrict__ gR, int ld_gR,
+                                                                float* __restrict__ gr, float* __restrict__ genv) {
+    const int64_t tid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    const int64_t e = tid / L;
+    const int l = (int)(tid % L);
+    if (e >= E) return;                                // whole groups of L lanes share e
+    const SplineCell c = spline_cell(r[e], pair[e], S);
+    const float t = c.t, t2 = t * t, t3 = t2 * t;
+    const float h10 = t3 - 2.f * t2 + t, h01 = -2.f * t3 + 3.f * t2, h11 = t3 - t2;
+    const float d10 = 3.f * t2 - 4.f * t + 1.f, d01 = -6.f * t2 + 6.f * t, d11 = 3.f * t2 - 2.f * t;
+    const float ev = env ? env[e] : 1.f;
+    const float* T0 = S.T + c.row;
+    const float* D0 = S.dT + c.row;
+    float sr = 0.f, se = 0.f;                          // d/dt and d/denv partial sums
+    for (int f = l; f < S.F; f += L) {
+        const float gv = f < nb ? (gphi ? gphi[e * ld_gphi + f] : 0.f) : (gR ? gR[e * ld_gR + f - nb] : 0.f);
+        const float p0 = T0[f], p1 = T0[S.F + f];
+        const float m0 = D0[f] * S.dr, m1 = D0[S.F + f] * S.dr;
+        const float dp = p1 - p0;
+        const float dv = d01 * dp + (d10 * m0 + d11 * m1);
+        if (f < nb) {
+            se = fmaf(gv, p0 + (h01 * dp + (h10 * m0 + h11 * m1)), se);
+            sr = fmaf(gv * ev, dv, sr);
+        } else {
+            sr = fmaf(gv, dv, sr);
+        }
+    }
+    sr = group_sum(sr, L);
+    se = group_sum(se, L);
+    if (l == 0) {
+        gr[e] = c.inside ? sr / S.dr : 0.f;
+        if (genv) genv[e] = se;
+    }
+}
+
+static int spline_lanes(int F) { return F <= 8 ? 8 : (F <= 16 ? 16 : (F <= 32 ? 32 : 64)); }
+
+static bool spline_args_ok(const float* r, const int32_t* pair, int64_t E, const float* T, const float* dT, int P,
+                           int G, int F, float dr, int nb) {
+    if (E < 0 || P < 1 || G < 2 || F < 1 || !(dr > 0.f) || nb < 0 || nb > F) return false;
+    return E == 0 || (r && pair && T && dT);
+}
+
 }  // namespace face
 
 using namespace face;
@@ -351,6 +465,55 @@ extern "C" int face_radial_bwd(const float* rb, int32_t ld_rb, int32_t n_basis, 
     const int tpw = radial_tiles_per_wave(E);
     FACE_RADIAL_DISPATCH(radial_bwd_kernel, rb, ld_rb, n_basis, pair, env, E, W, n_pair, B, gh2, ld_gh2, gphi,
                          ld_gphi, grb, ld_grb, genv, tpw);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int face_radial_spline_fwd(const float* r, const int32_t* pair, int64_t E, const float* T, const float* dT,
+                                      int32_t P, int32_t G, int32_t F, float dr, const float* env, int32_t nb,
+                                      float* phi, int32_t ld_phi, float* R, int32_t ld_R, void* stream) {
+    if (!spline_args_ok(r, pair, E, T, dT, P, G, F, dr, nb) || (nb > 0 && (ld_phi < nb || (E > 0 && !phi))) ||
+        (nb < F && (ld_R < F - nb || (E > 0 && !R))))
+        return FACE_ERR_ARG;
+    if (E == 0) return 0;
+    const SplineTab tab{T, dT, P, G, F, dr};
+    const int L = spline_lanes(F);
+    const dim3 grid((unsigned)((E * L + 255) / 256)), block(256);
+    const hipStream_t st = (hipStream_t)stream;
+#define FACE_SPLINE(K_, L_) hipLaunchKernelGGL((K_<L_>), grid, block, 0, st, r, pair, E, tab, env, nb, ARGS_)
+#define ARGS_ phi, ld_phi, R, ld_R
+    switch (L) {
+        case 8: FACE_SPLINE(radial_spline_fwd_kernel, 8); break;
+        case 16: FACE_SPLINE(radial_spline_fwd_kernel, 16); break;
+        case 32: FACE_SPLINE(radial_spline_fwd_kernel, 32); break;
+        default: FACE_SPLINE(radial_spline_fwd_kernel, 64); break;
+    }
+#undef ARGS_
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int face_radial_spline_bwd(const float* r, const int32_t* pair, int64_t E, const float* T, const float* dT,
+                                      int32_t P, int32_t G, int32_t F, float dr, const float* env, int32_t nb,
+                                      const float* gphi, int32_t ld_gphi, const float* gR, int32_t ld_gR, float* gr,
+                                      float* genv, void* stream) {
+    if (!spline_args_ok(r, pair, E, T, dT, P, G, F, dr, nb) || (gphi && ld_gphi < nb) || (gR && ld_gR < F - nb) ||
+        (E > 0 && !gr))
+        return FACE_ERR_ARG;
+    if (E == 0) return 0;
+    const SplineTab tab{T, dT, P, G, F, dr};
+    const int L = spline_lanes(F);
+    const dim3 grid((unsigned)((E * L + 255) / 256)), block(256);
+    const hipStream_t st = (hipStream_t)stream;
+#define ARGS_ gphi, ld_gphi, gR, ld_gR, gr, genv
+    switch (L) {
+        case 8: FACE_SPLINE(radial_spline_bwd_kernel, 8); break;
+        case 16: FACE_SPLINE(radial_spline_bwd_kernel, 16); break;
+        case 32: FACE_SPLINE(radial_spline_bwd_kernel, 32); break;
+        default: FACE_SPLINE(radial_spline_bwd_kernel, 64); break;
+    }
+#undef ARGS_
+#undef FACE_SPLINE
     FACE_LAUNCH_CHECK();
     return 0;
 }

@@ -1,7 +1,9 @@
 """ASE-style calculator and an on-device molecular-dynamics loop over the MI355X path.
 
 FACECalculator follows face/calculator.py:35-56 (energy + forces of one structure from a
-FACE model in evaluation mode) with three differences that keep every step on the device:
+FACE model in evaluation mode; like the reference on CUDA, face/calculator.py:41-43, it
+tabulates the radial functions with model.compile_radial() unless the model already has
+tables or compile_radial=False) with three differences that keep every step on the device:
 
   * the pair list is built on the GPU with cutoff rc + skin and reused until some atom has
     moved more than skin / 2 since the build (the reference rebuilds the padded list on the
@@ -29,7 +31,8 @@ class FACECalculator:
 
     implemented_properties = ("energy", "forces")
 
-    def __init__(self, model, skin=0.5, use_graph=True, e_shift=0.0, device="cuda", tune_gemms=False):
+    def __init__(self, model, skin=0.5, use_graph=True, e_shift=0.0, device="cuda", tune_gemms=False,
+                 compile_radial=True):
         if tune_gemms:                     # library GEMM solutions timed on the first step
             from .runner import tune_library_gemms
             tune_library_gemms()
@@ -37,6 +40,8 @@ class FACECalculator:
             raise ValueError("FACECalculator needs the model in evaluation mode (model.eval())")
         if skin < 0:
             raise ValueError("skin must be >= 0")
+        if compile_radial and getattr(model.blocks[0], "spline", 1) is None:
+            model.compile_radial()
         self.model, self.skin, self.use_graph = model, float(skin), bool(use_graph)
         self.rc = float(model.rc)
         self.e_shift = float(e_shift)

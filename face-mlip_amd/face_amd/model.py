@@ -48,6 +48,50 @@ class BesselEnvelope(nn.Module):
         self.rc, self.p = rc, p
         self.register_buffer("freq", torch.arange(1, n + 1) * math.pi / rc)
 
+    def evaluate(self, r):
+        """(bessel (..., n), envelope (...)) in torch (face/model.py:32-40); used to tabulate the
+        radial functions, the edge kernel evaluates the same closed forms per edge."""
+        p, x = self.p, r / self.rc
+        env = 1 - (p + 1) * (p + 2) / 2 * x ** p + p * (p + 2) * x ** (p + 1) - p * (p + 1) / 2 * x ** (p + 2)
+        return torch.sin(self.freq * r[..., None]) / r[..., None] * math.sqrt(2 / self.rc), env * (x < 1)
+
+
+class RadialTables:
+    """Compiled radial functions of one pass (face/model.py:383-405): values T and exact
+    r-derivatives dT (P element pairs, G grid points, B [+ 4C] columns) on r_g = g * dr."""
+
+    def __init__(self, T, dT, dr):
+        self.T, self.dT, self.dr = T, dT, dr
+
+    @staticmethod
+    def build(block, basis, rc, n_grid):
+        """RadialSpline.build (face/model.py:392-405): the radial MLP on the grid r = linspace(0, rc,
+        n_grid) clamped to >= 1e-4, per element pair, and its exact r-derivative. Evaluated in
+        float64 and stored in float32 (the reference evaluates in the weights' float32): the
+        kernel's r-derivative rests on differences of neighbouring table values, so table entries
+        rounded once from exact values keep its round-off at the storage floor. dT by forward-mode
+        differentiation: each entry depends on its own grid radius only, so one Jacobian-vector
+        product with a unit tangent gives every column (the reference takes one reverse pass per
+        column)."""
+        f64 = torch.float64
+        def lin(m):
+            w = m.weight.detach().to(f64)
+            return (w * m.alpha) if isinstance(m, UnitLinear) else w, None if m.bias is None else m.bias.detach().to(f64)
+
+        (Wi, bi), (W1, b1), (W2, b2) = lin(block.rad_in), lin(block.radial[0]), lin(block.radial[2])
+        pair = block.pair.weight.detach().to(f64)[:, None, :]
+        r = torch.linspace(0, rc, n_grid, device=Wi.device, dtype=f64).clamp_min(1e-4)
+        rr = r[None].expand(pair.shape[0], -1).contiguous()
+
+        def table(x):
+            bes, env = basis.evaluate(x)
+            hid = F.silu(F.linear(bes * env[..., None], Wi, bi) + pair)
+            return F.linear(F.silu(F.linear(hid, W1, b1)), W2, b2)
+
+        T, dT = torch.func.jvp(table, (rr,), (torch.ones_like(rr),))
+        f32 = lambda t: t.detach().to(torch.float32).contiguous()
+        return RadialTables(f32(T), f32(dT), rc / (n_grid - 1))
+
 
 class UnitLinear(nn.Module):
     """Unit-variance stored weight with forward factor fan_in**-0.5 (face/model.py:43-55)."""
@@ -156,6 +200,7 @@ class FactorBlock(nn.Module):
             nn.init.ones_(self.gate.bias)
         # factorised pass
         self.cp = cp
+        self.spline = None              # RadialTables, set by FACE.compile_radial()
         if cp:
             K = C
         self.B, self.Km = B, K
@@ -175,17 +220,23 @@ class FactorBlock(nn.Module):
             self.tmix3 = nn.Linear(B * 2 * K_dir, C, bias=False)
 
     # ------------------------------------------------------------------ moments
-    def moments(self, h, rb, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g):
+    def moments(self, h, rb, r, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g):
         """Moments A_l as monomial-major (k_l, N, C) blocks (face/model.py:460-534)."""
         N, E = g.N, g.E
         B, C, Kd = self.B, self.C, self.K
-        # hidden layers and phi columns of the radial MLP in one HIP kernel; the CP columns of the
-        # last layer are a GEMM on its h2 output
-        Wi, bi = frozen(self.rad_in)
-        W1, b1 = frozen(self.radial[0])
         W2, b2 = frozen(self.radial[2])
-        phi, h2 = ops.radial_mlp(rb, env, zp, Wi, bi, self.pair.weight.detach(), W1, b1, W2[:B], b2[:B],
-                                 self.cp)                                        # (E, B), (E, H)
+        if self.spline is not None:
+            # compiled radial (face/model.py:466-467): phi = spline * env (E, B) and, in CP form,
+            # the raw CP radials (E, 4C) whose envelope the pooling kernels apply
+            sp = self.spline
+            phi, R_sp = ops.radial_spline(r, env, zp, sp.T, sp.dT, sp.dr, B)
+        else:
+            # hidden layers and phi columns of the radial MLP in one HIP kernel; the CP columns of
+            # the last layer are a GEMM on its h2 output
+            Wi, bi = frozen(self.rad_in)
+            W1, b1 = frozen(self.radial[0])
+            phi, h2 = ops.radial_mlp(rb, env, zp, Wi, bi, self.pair.weight.detach(), W1, b1, W2[:B], b2[:B],
+                                     self.cp)                                    # (E, B), (E, H)
         msg_n = F.linear(h, *frozen(self.msg))                                   # (N, K)
         if self.directional:
             if self.eq_in:
@@ -206,7 +257,9 @@ class FactorBlock(nn.Module):
         else:
             mj, gathered = msg_n, True
         s_tab = self._scale_table(avg_nb)                                        # elem_scale / avg_nb (n_el, 4C)
-        if self.cp:
+        if self.cp and self.spline is not None:
+            Af = ops.cp_density(R_sp, env, mj, Y, g, gathered)                    # 4 x (k_l, N, C)
+        elif self.cp:
             # R = h2 W2[B:]^T + b2[B:] (E, 4C) feeds the pooling (envelope applied in-kernel); on the
             # matrix-core shapes the pooling backward also applies W2[B:] and returns d h2 directly
             if C % 32 == 0 and h2.shape[1] % 16 == 0 and h2.shape[1] <= 64:
@@ -246,9 +299,9 @@ class FactorBlock(nn.Module):
         return c[1]
 
     # ------------------------------------------------------------------ invariants + readout
-    def forward(self, h, rb, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g):
+    def forward(self, h, rb, r, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g):
         C = self.C
-        A = self.moments(h, rb, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g)
+        A = self.moments(h, rb, r, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g)
         allsets = sets + [A]
         # only P0 of rank 0 and P3, Q3 of rank 3 are used
         ws = [frozen(self.proj[l])[0][:(C, 3 * C, 3 * C, 2 * C)[l]] for l in range(4)]
@@ -321,6 +374,16 @@ class FACE(nn.Module):
         """Kept for API compatibility (face/model.py:657-663): this path is always fused."""
         return self
 
+    @torch.no_grad()
+    def compile_radial(self, n_grid=4096, on=True):
+        """face/model.py:644-655: tabulate each pass's radial functions phi_b(r; Z_i, Z_j) (before the
+        envelope; B [+ 4C] columns) on n_grid points per element pair; the forward then evaluates
+        them by cubic Hermite interpolation (a HIP kernel) instead of the radial MLP. on=False
+        returns to the MLP. Build after moving the model to its device."""
+        for b in self.blocks:
+            b.spline = RadialTables.build(b, self.basis, self.rc, n_grid) if on else None
+        return self
+
     def _graph(self, g):
         if isinstance(g, Graph):
             return g
@@ -345,7 +408,9 @@ class FACE(nn.Module):
         pos = graph.pos
         if forces and not pos.requires_grad:
             pos.requires_grad_(True)
-        Y, rb, env = ops.edge_geometry(pos, graph, self.basis.freq, self.rc)
+        splines = [b.spline is not None for b in self.blocks]
+        Y, rb, env, r = ops.edge_geometry(pos, graph, self.basis.freq, self.rc, with_rb=not all(splines),
+                                          with_r=any(splines))
         zidx = self.zmap[graph.Z]
         zkey = ("zp", self.zmap.data_ptr(), len(self.E0))
         zp = graph.cache.get(zkey)
@@ -358,7 +423,7 @@ class FACE(nn.Module):
         e_at = self.E0[zidx].clone()
         sets, eq = [], None
         for blk in self.blocks:
-            e, h, A, eq = blk(h, rb, Y, env, zp, zidx, zidx32, self.avg_nb, sets, eq, graph)
+            e, h, A, eq = blk(h, rb, r, Y, env, zp, zidx, zidx32, self.avg_nb, sets, eq, graph)
             sets.append(A)
             e_at = e_at + self.scale * e.squeeze(-1)
         E = ops.StructureSum.apply(e_at, graph.struct_ptr, graph.batch, graph.nstr)

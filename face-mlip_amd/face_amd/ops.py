@@ -53,39 +53,45 @@ class Graph:
 
 # ----------------------------------------------------------------------------- edge geometry
 class EdgeGeometry(torch.autograd.Function):
-    """pos -> (Y (E,20), rb (E,nb), env (E)) for the edges of `graph` (face/model.py:670-677)."""
+    """pos -> (Y (E,20), rb (E,nb), env (E), r (E)) for the edges of `graph` (face/model.py:670-677).
+    With_r False: r is an empty tensor; with_rb False (compiled radial, which reads r instead of
+    the Bessel rows): rb is an empty tensor and is not computed."""
 
     @staticmethod
-    def forward(ctx, pos, graph, freq, rc, bes_scale):
+    def forward(ctx, pos, graph, freq, rc, bes_scale, with_rb, with_r):
         _lib.require_gpu(pos)
         pos = pos.contiguous().float()
         E, nb = graph.E, freq.numel()
         Y = torch.empty(E, 20, device=pos.device)
-        rb = torch.empty(E, nb, device=pos.device)
+        rb = torch.empty(E if with_rb else 0, nb, device=pos.device)
         env = torch.empty(E, device=pos.device)
+        r = torch.empty(E if with_r else 0, device=pos.device)
         call("face_edge_geom_fwd", ptr(pos), ptr(graph.recv), ptr(graph.col), ptr(graph.shift), None, E, ptr(freq),
-             nb, float(rc), float(bes_scale), ptr(Y), ptr(rb), ptr(env), None, _lib.stream_of(pos), label="edge_fwd")
+             nb, float(rc), float(bes_scale), ptr(Y), ptr(rb) if with_rb else None, ptr(env),
+             ptr(r) if with_r else None, _lib.stream_of(pos), label="edge_fwd")
         ctx.save_for_backward(pos, freq)
         ctx.graph, ctx.rc, ctx.bes_scale = graph, rc, bes_scale
-        return Y, rb, env
+        return Y, rb, env, r
 
     @staticmethod
-    def backward(ctx, gY, grb, genv):
+    def backward(ctx, gY, grb, genv, gr):
         pos, freq = ctx.saved_tensors
         g = ctx.graph
         gvec = torch.empty(g.E, 3, device=pos.device)
-        cont = lambda t: None if t is None else t.contiguous().float()
-        gY, grb, genv = cont(gY), cont(grb), cont(genv)
+        cont = lambda t: None if (t is None or t.numel() == 0) else t.contiguous().float()
+        gY, grb, genv, gr = cont(gY), cont(grb), cont(genv), cont(gr)
         st = _lib.stream_of(pos)
         call("face_edge_geom_bwd", ptr(pos), ptr(g.recv), ptr(g.col), ptr(g.shift), None, g.E, ptr(freq), freq.numel(),
-             float(ctx.rc), float(ctx.bes_scale), ptr(gY), ptr(grb), ptr(genv), None, ptr(gvec), st, label="edge_bwd")
+             float(ctx.rc), float(ctx.bes_scale), ptr(gY), ptr(grb), ptr(genv), ptr(gr), ptr(gvec), st,
+             label="edge_bwd")
         gpos = torch.empty_like(pos)
         call("face_force_scatter", ptr(gvec), ptr(g.row_ptr), ptr(g.rev), g.N, 1.0, ptr(gpos), st, label="force_scatter")
-        return gpos, None, None, None, None
+        return gpos, None, None, None, None, None, None
 
 
-def edge_geometry(pos, graph, freq, rc):
-    return EdgeGeometry.apply(pos, graph, freq, rc, math.sqrt(2.0 / rc))
+def edge_geometry(pos, graph, freq, rc, with_rb=True, with_r=False):
+    """(Y, rb, env, r); rb / r are empty tensors when not asked for."""
+    return EdgeGeometry.apply(pos, graph, freq, rc, math.sqrt(2.0 / rc), with_rb, with_r)
 
 
 # ----------------------------------------------------------------------------- gathers
@@ -611,6 +617,46 @@ class RadialMLP(torch.autograd.Function):
 
 def radial_mlp(rb, env, pair, w_in, b_in, pair_tab, w1, b1, w_phi, b_phi, want_h2):
     return RadialMLP.apply(rb, env, pair, w_in, b_in, pair_tab, w1, b1, w_phi, b_phi, want_h2)
+
+
+class RadialSpline(torch.autograd.Function):
+    """Compiled radial functions (face/model.py:407-418, :466-467): cubic Hermite interpolation of
+    the tables T, dT (P, G, F) at r (E) for element pair `pair` (E); returns phi (E, nb) = the
+    first nb columns times env, and R (E, F - nb) = the other columns as they are (the CP radials,
+    enveloped inside the pooling kernels). Gradients flow to r and env (the tables are constants
+    of the compiled model)."""
+
+    @staticmethod
+    def forward(ctx, r, env, pair, T, dT, dr, nb):
+        _lib.require_gpu(r, env, T)
+        P, G, F = T.shape
+        E = r.shape[0]
+        r_, env_ = r.contiguous().float(), env.contiguous().float()
+        phi = torch.empty(E, nb, device=r.device)
+        R = torch.empty(E, F - nb, device=r.device)
+        call("face_radial_spline_fwd", ptr(r_), ptr(pair), E, ptr(T), ptr(dT), P, G, F, float(dr), ptr(env_), nb,
+             ptr(phi), nb, ptr(R), F - nb, _lib.stream_of(r), label="spline_fwd")
+        ctx.save_for_backward(r_, env_, pair, T, dT)
+        ctx.dr, ctx.nb = dr, nb
+        return phi, R
+
+    @staticmethod
+    def backward(ctx, gphi, gR):
+        r, env, pair, T, dT = ctx.saved_tensors
+        P, G, F = T.shape
+        E, nb = r.shape[0], ctx.nb
+        gp, ldp = _rows(gphi, nb) if (gphi is not None and nb > 0) else (None, nb)
+        gq, ldq = _rows(gR, F - nb) if (gR is not None and F > nb) else (None, F - nb)
+        gr = torch.empty(E, device=r.device)
+        genv = torch.empty(E, device=r.device) if ctx.needs_input_grad[1] else None
+        call("face_radial_spline_bwd", ptr(r), ptr(pair), E, ptr(T), ptr(dT), P, G, F, float(ctx.dr), ptr(env), nb,
+             ptr(gp), ldp, ptr(gq), ldq, ptr(gr), ptr(genv), _lib.stream_of(r), label="spline_bwd")
+        return gr, genv, None, None, None, None, None
+
+
+def radial_spline(r, env, pair, T, dT, dr, nb):
+    """(phi (E, nb), R (E, F - nb)) from the compiled tables; see RadialSpline."""
+    return RadialSpline.apply(r, env, pair, T, dT, dr, nb)
 
 
 # ----------------------------------------------------------------------------- node algebra

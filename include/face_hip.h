@@ -21,6 +21,7 @@
  *   face/neighbors.py:7-37       padded_graph (ASE neighbor_list) -> face_nbr_* (count, fill, rev, padded)
  *   face/model.py:670-677        edge geometry + Bessel basis     -> face_edge_geom_fwd / _bwd
  *   face/model.py:465-469        radial MLP (rad_in, pair, radial) -> face_radial_fwd / _bwd
+ *   face/model.py:407-418,466-467 RadialSpline (compile_radial)   -> face_radial_spline_fwd / _bwd
  *   face/model.py:469,488-493    CP radial columns; gather(msg(h)) + dir_mix(d)
  *                                                                  -> face_edge_linear_fwd / _bwd
  *   face/model.py:498-533,537-544 mix / tmix / proj (+ elem_scale)   -> face_rows_linear
@@ -244,6 +245,26 @@ int face_radial_bwd(const float* rb, int32_t ld_rb, int32_t n_basis, const int32
                     int32_t H, const float* w1, const float* b1, const float* w_phi, const float* b_phi, int32_t B,
                     const float* gh2, int32_t ld_gh2, const float* gphi, int32_t ld_gphi, float* grb, int32_t ld_grb,
                     float* genv, void* stream);
+
+/* ---------------------------------------------------------------- compiled radial (splines)
+ * RadialSpline.forward (face/model.py:407-418), the table lookup that FACE.compile_radial
+ * (face/model.py:644-655) puts in place of the radial MLP: T, dT (P, G, F) row-major hold the
+ * values and exact r-derivatives of the radial functions of each element pair on the grid
+ * r_g = g * dr; for edge e, x = clamp(r[e] / dr, 0, G - 1), i = min(floor x, G - 2), t = x - i,
+ *   S[e, f] = h00 T[p][i][f] + h10 dr dT[p][i][f] + h01 T[p][i+1][f] + h11 dr dT[p][i+1][f]
+ * (cubic Hermite basis), p = pair[e] (clamped into [0, P)). Columns f < nb: phi[e][f] =
+ * S[e,f] * env[e] (face/model.py:467; env may be NULL: factor 1); columns f >= nb (the CP
+ * radials, enveloped inside the pooling kernels): R[e][f - nb] = S[e,f]. G >= 2, dr > 0,
+ * 0 <= nb <= F; phi is unused when nb = 0, R when nb = F. */
+int face_radial_spline_fwd(const float* r, const int32_t* pair, int64_t E, const float* T, const float* dT, int32_t P,
+                           int32_t G, int32_t F, float dr, const float* env, int32_t nb, float* phi, int32_t ld_phi,
+                           float* R, int32_t ld_R, void* stream);
+/* Its backward for upstream gphi (E, ld_gphi >= nb) and gR (E, ld_gR >= F - nb) (either may be
+ * NULL = 0): gr[e] = sum_f g[e,f] dphi_or_R[e,f]/dr (0 where r / dr lies outside [0, G - 1], as
+ * through the clamp), genv[e] = sum_{f < nb} gphi[e,f] S[e,f] (genv may be NULL). */
+int face_radial_spline_bwd(const float* r, const int32_t* pair, int64_t E, const float* T, const float* dT, int32_t P,
+                           int32_t G, int32_t F, float dr, const float* env, int32_t nb, const float* gphi,
+                           int32_t ld_gphi, const float* gR, int32_t ld_gR, float* gr, float* genv, void* stream);
 
 /* ---------------------------------------------------------------- row-block linear layers
  * One problem: x (m, ld_x >= k) rows, w (n, k) row-major with row stride ld_w (w_kn = 0) or

@@ -11,7 +11,9 @@ random-init weights; the state_dict keys match the reference's.
 
 Pinned by: tests/golden/*.npz, written by tests/golden/make_golden.py from the reference's
 own FACE.forward on the CPU (weights, energies and forces at seeded init), and by the
-invariance checks of tests/test_symmetry.py restated in tests/test_oracle.py.
+invariance checks of tests/test_symmetry.py restated in tests/test_oracle.py. RadialSpline /
+compile_radial: exactness for cubics, the tables against the MLP and its central differences,
+and compiled-vs-MLP agreement in fp64 (tests/test_oracle.py).
 """
 import math
 
@@ -40,6 +42,51 @@ class BesselEnvelope(nn.Module):
     def forward(self, r):
         rr = r[..., None]
         return torch.sin(self.freq * rr) / rr * math.sqrt(2 / self.rc), self.envelope(r)
+
+
+class RadialSpline(nn.Module):
+    """face/model.py:383-418: radial functions from a uniform-grid table of values T and exact
+    r-derivatives dT (P pairs, G points, columns), cubic Hermite (C1) between grid points."""
+
+    def __init__(self, T, dT, dr):
+        super().__init__()
+        self.register_buffer("T", T)
+        self.register_buffer("dT", dT)
+        self.dr = dr
+
+    @staticmethod
+    def build(block, basis, rc, n_grid, store_dtype=None):
+        """face/model.py:392-405: the radial MLP on r = linspace(0, rc, n_grid).clamp_min(1e-4) per
+        element pair; dT column by column by reverse-mode autograd, as the reference does.
+        store_dtype: round the tables to that type (and back), as a table stored in it."""
+        w = block.rad_in.weight
+        r = torch.linspace(0, rc, n_grid, dtype=w.dtype).clamp_min(1e-4)
+        P = block.pair.weight.shape[0]
+        with torch.enable_grad():
+            rr = r[None].expand(P, -1).clone().requires_grad_(True)
+            bes, env = basis(rr)
+            x = F.silu(block.rad_in(bes * env[..., None]) + block.pair.weight[:, None, :])
+            T = block.radial(x)
+            dT = torch.stack([torch.autograd.grad(T[..., b].sum(), rr, retain_graph=True)[0]
+                              for b in range(T.shape[-1])], -1)
+        T, dT = T.detach(), dT.detach()
+        if store_dtype is not None:
+            T, dT = T.to(store_dtype).to(T.dtype), dT.to(store_dtype).to(dT.dtype)
+        return RadialSpline(T, dT, rc / (n_grid - 1))
+
+    def forward(self, r, pair):
+        """face/model.py:407-418."""
+        P, G, B = self.T.shape
+        x = (r / self.dr).clamp(0, G - 1)
+        i = torch.floor(x).long().clamp(max=G - 2)
+        t = (x - i)[..., None]
+        flat = (pair * G + i).reshape(-1)
+        T, dT = self.T.reshape(P * G, B), self.dT.reshape(P * G, B)
+        sh = (*r.shape, B)
+        p0, p1 = T.index_select(0, flat).view(sh), T.index_select(0, flat + 1).view(sh)
+        m0, m1 = dT.index_select(0, flat).view(sh) * self.dr, dT.index_select(0, flat + 1).view(sh) * self.dr
+        t2, t3 = t * t, t * t * t
+        return (2 * t3 - 3 * t2 + 1) * p0 + (t3 - 2 * t2 + t) * m0 + (-2 * t3 + 3 * t2) * p1 + (t3 - t2) * m1
 
 
 class UnitLinear(nn.Module):
@@ -124,6 +171,8 @@ class FactorPass(nn.Module):
         if cp:
             K = C
         self.B, self.Km = B, K
+        self.spline = None              # RadialSpline, set by FACE.compile_radial()
+        self._r = None
         self.radial = mlp([radial_hidden, radial_hidden, B + (4 * C if cp else 0)])
         self.msg = nn.Linear(C, K)
         self.mix = nn.ModuleList([nn.Linear(C if cp else B * K, C, bias=False) for _ in range(4)])
@@ -145,7 +194,10 @@ class FactorPass(nn.Module):
         B, C, Kd = self.B, self.C, self.K
         at_j = lambda x: x[nbr]                                   # (N,M,...) neighbour gather
         zp = zidx[:, None] * self.n_elem + zidx[nbr]
-        phi = self.radial(F.silu(self.rad_in(rb) + self.pair(zp))) * env[..., None]
+        if self.spline is not None:                               # face/model.py:466-467
+            phi = self.spline(self._r, zp) * env[..., None]
+        else:
+            phi = self.radial(F.silu(self.rad_in(rb) + self.pair(zp))) * env[..., None]
         if self.cp:
             Rcp = phi[..., B:].reshape(N, M, 4, C)
             phi = phi[..., :B]
@@ -227,6 +279,13 @@ class FACE(nn.Module):
         self.register_buffer("avg_nb", torch.tensor(10.0))
         self.terms = nn.ModuleDict()
 
+    @torch.no_grad()
+    def compile_radial(self, n_grid=4096, on=True, store_dtype=None):
+        """face/model.py:644-655 (store_dtype: see RadialSpline.build)."""
+        for b in self.blocks:
+            b.spline = RadialSpline.build(b, self.basis, self.rc, n_grid, store_dtype) if on else None
+        return self
+
     def forward(self, g, forces=True):
         pos = g["pos"]
         if forces and not pos.requires_grad:
@@ -245,6 +304,7 @@ class FACE(nn.Module):
         e_at = self.E0[zidx].clone()
         sets, eq = [], None
         for blk in self.blocks:
+            blk._r = r
             e, h, A, eq = blk(h, rb, Y, nbr, env, zidx, self.avg_nb, sets, eq)
             sets.append(A)
             e_at = e_at + self.scale * e.squeeze(-1)

@@ -336,9 +336,12 @@ def test_edge_geometry_forward_and_backward():
     g = build_graph(st, rc)
     pos = g.pos.clone().requires_grad_(True)
     freq = (torch.arange(1, 9) * np.pi / rc).float().to(DEV)
-    Y, rb, env = ops.edge_geometry(pos, g, freq, rc)
-    wY, wr, we = torch.randn_like(Y), torch.randn_like(rb), torch.randn_like(env)
-    (gp,) = torch.autograd.grad((Y * wY).sum() + (rb * wr).sum() + (env * we).sum(), pos)
+    Y, rb, env, rr = ops.edge_geometry(pos, g, freq, rc, with_r=True)
+    wY, wr, we, wd = torch.randn_like(Y), torch.randn_like(rb), torch.randn_like(env), torch.randn_like(rr)
+    (gp,) = torch.autograd.grad((Y * wY).sum() + (rb * wr).sum() + (env * we).sum() + (rr * wd).sum(), pos)
+    # without the Bessel rows (compiled radial): rb is empty and the rest unchanged
+    Y3, rb3, env3, r3 = ops.edge_geometry(pos.detach(), g, freq, rc, with_rb=False, with_r=True)
+    assert rb3.numel() == 0 and torch.equal(Y3, Y.detach()) and torch.equal(r3, rr.detach())
     # oracle: the reference formulas in fp64 on the CPU (face/model.py:670-677, :28-40)
     pc = g.pos.detach().double().cpu().requires_grad_(True)
     col, recv = g.col.long().cpu(), g.recv.long().cpu()
@@ -350,9 +353,50 @@ def test_edge_geometry_forward_and_backward():
     bes = torch.sin(torch.arange(1, 9, dtype=torch.float64) * np.pi / rc * r[:, None]) / r[:, None] * np.sqrt(2 / rc)
     Y2, rb2 = cartesian.monomials(u), bes * e_ref[:, None]
     (gp2,) = torch.autograd.grad((Y2 * wY.double().cpu()).sum() + (rb2 * wr.double().cpu()).sum()
-                                 + (e_ref * we.double().cpu()).sum(), pc)
-    errs = [rel(Y, Y2), rel(rb, rb2), rel(env, e_ref), rel(gp, gp2)]
+                                 + (e_ref * we.double().cpu()).sum() + (r * wd.double().cpu()).sum(), pc)
+    errs = [rel(Y, Y2), rel(rb, rb2), rel(env, e_ref), rel(rr, r), rel(gp, gp2)]
     assert max(errs) < TOL, errs
+
+
+@pytest.mark.parametrize("P,G,F,nb", [(9, 4096, 16, 16), (9, 4096, 16 + 4 * 160, 16), (1, 300, 16, 16),
+                                       (4, 64, 37, 5), (2, 33, 6, 0)])
+def test_radial_spline_matches_oracle(P, G, F, nb):
+    """Compiled radial (face/model.py:407-418, :466-467): phi = S[:, :nb] * env and R = S[:, nb:]
+    with their r / env gradients, against the oracle's RadialSpline in fp64 (autograd), for radii
+    inside the grid, on grid points, and beyond its end (clamped, zero r-derivative). The tables
+    sample smooth functions, as compiled radial functions are: with random, non-smooth tables the
+    fp32 rounding of r / dr alone (2e-4 of a cell at 4096 points) moves the value by ~1e-4."""
+    from face_amd import ops
+    from oracle.model import RadialSpline
+    say("spline", P, G, F, nb)
+    gen = torch.Generator().manual_seed(G + F)
+    rc = 5.0
+    dr = rc / (G - 1)
+    rg = (torch.arange(G, dtype=torch.float64) * dr)[None, :, None]
+    amp, k, ph = (torch.randn(P, 1, F, generator=gen, dtype=torch.float64) for _ in range(3))
+    k = 0.3 + 2.5 * k.abs()
+    T = (amp * torch.sin(k * rg + ph) + 0.1 * amp * rg ** 2).float()
+    dT = (amp * k * torch.cos(k * rg + ph) + 0.2 * amp * rg).float()
+    E = 3000
+    rng = np.random.default_rng(F)
+    r = rng.uniform(1e-4, rc + 0.7, E)
+    r[:50] = np.arange(50) % G * dr                              # on grid points
+    r = torch.tensor(r, dtype=torch.float32)
+    pair = torch.tensor(rng.integers(0, P, E), dtype=torch.int32)
+    env = torch.rand(E, generator=gen)
+    rd, envd = r.to(DEV).requires_grad_(True), env.to(DEV).requires_grad_(True)
+    phi, R = ops.radial_spline(rd, envd, pair.to(DEV), T.to(DEV), dT.to(DEV), dr, nb)
+    assert phi.shape == (E, nb) and R.shape == (E, F - nb)
+    wp, wq = torch.randn(E, nb, generator=gen), torch.randn(E, F - nb, generator=gen)
+    gr, ge = torch.autograd.grad((phi * wp.to(DEV)).sum() + (R * wq.to(DEV)).sum(), (rd, envd))
+    sp = RadialSpline(T.double(), dT.double(), dr)
+    rc_, ec = r.double().requires_grad_(True), env.double().requires_grad_(True)
+    S = sp(rc_, pair.long())
+    phi2, R2 = S[:, :nb] * ec[:, None], S[:, nb:]
+    gr2, ge2 = torch.autograd.grad((phi2 * wp.double()).sum() + (R2 * wq.double()).sum(), (rc_, ec))
+    errs = [rel(phi, phi2) if nb else 0.0, rel(R, R2) if F > nb else 0.0, rel(gr, gr2), rel(ge, ge2) if nb else 0.0]
+    assert max(errs) < TOL, errs
+    assert float(gr[r.to(DEV) > rc + 1e-3].abs().max()) == 0.0   # clamped: no r-derivative
 
 
 @pytest.mark.parametrize("Kd,B,transport", [(16, 16, True), (4, 8, True), (5, 4, False), (16, 16, False)])

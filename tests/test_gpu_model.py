@@ -127,6 +127,58 @@ def test_workload_matches_oracle_with_tuned_library_gemms(k, n_atoms, tmp_path):
     say(f"  dE/E {dE:.2e}  max|dF|/rms {dF:.2e}")
 
 
+@pytest.mark.parametrize("name", ["small_flag_box", "small_cp_mol", "cfg2_flag_ag", "cfg3_cp_c160"])
+def test_compiled_radial_matches_oracle(name):
+    """FACE.compile_radial() (face/model.py:644-655; the reference calculator's CUDA setting): tables
+    built on the GPU (fp64, stored fp32), splines evaluated by the HIP kernel, against the oracle
+    model in fp64 with its own tables (reverse-mode derivatives as the reference builds them),
+    stored in fp32 as well: same hot-path bar as the MLP path."""
+    from oracle import model as om
+    kw, el, _ = (SMALL_CASES if name in SMALL_CASES else BIG_CASES)[name]
+    say("compiled radial", name)
+    d = np.load(os.path.join(GOLD, f"{name}_f32.npz"))
+    m = product_model(kw, el).compile_radial()
+    o = m(golden_graph(d))
+    torch.manual_seed(0)
+    mo = om.FACE(el, **kw)
+    om.unit_parameterise(mo)
+    mo = mo.double().eval().compile_radial(store_dtype=torch.float32)
+    t = lambda k, dt=None: torch.as_tensor(d[k], dtype=dt)
+    g = {"pos": t("pos", torch.float64), "Z": t("Z"), "nbr": t("nbr"), "shift": t("shift", torch.float64),
+         "mask": t("mask"), "batch": t("batch")}
+    oo = mo(g)
+    dE, dF = check(o["energy"].detach().cpu(), o["forces"].detach().cpu(), oo["energy"].detach().numpy(),
+                   oo["forces"].detach().numpy())
+    say(f"  dE/E {dE:.2e}  max|dF|/rms {dF:.2e}")
+    # back to the radial MLP: the golden reference values again
+    m.compile_radial(on=False)
+    o2 = m(golden_graph(d))
+    check(o2["energy"].detach().cpu(), o2["forces"].detach().cpu(), d["energy"], d["forces"])
+
+
+def test_compiled_radial_close_to_mlp_model():
+    """face/tests/test_kernels.py:38-54 (check_spline): perturbed flagship C32 model, compiled radial
+    against the radial MLP on the same structures: |dE| < 1e-5 eV/atom, rel ||dF|| < 1e-3."""
+    from face_amd import systems
+    from face_amd.neighbors import build_graph
+    say("compiled vs MLP")
+    kw = dict(C=32, transport=True, eqmsg=True, factor=True, B=16, K=32, rc=5.0)
+    m = product_model(kw, [1, 6, 8])
+    g0 = torch.Generator(device="cuda").manual_seed(0)
+    with torch.no_grad():
+        for p in m.parameters():
+            p.add_(0.05 * torch.randn(p.shape, generator=g0, device="cuda"))
+    sts, _, _, _ = systems.workload(3, n_atoms=400)
+    g = build_graph(sts, kw["rc"])
+    o1 = m(g)
+    o2 = m.compile_radial()(g)
+    m.compile_radial(on=False)
+    dE = (o1["energy"] - o2["energy"]).abs().item() / g.N
+    dF = ((o1["forces"] - o2["forces"]).norm() / o1["forces"].norm()).item()
+    say(f"  |dE| {dE:.1e} eV/atom  rel |dF| {dF:.1e}")
+    assert dE < 1e-5 and dF < 1e-3, (dE, dF)
+
+
 def test_forces_are_minus_energy_gradient_fd():
     """Central differences of the GPU energy (fp32, h = 1e-2 A on a smooth small model)."""
     from face_amd.neighbors import build_graph

@@ -297,3 +297,77 @@ def test_oracle_model_invariances_f64():
         pm[i, c] -= h
         fd = -(run(pp, False)["energy"].item() - run(pm, False)["energy"].item()) / (2 * h)
         assert abs(fd - F[i, c]) < 1e-6 * (1 + abs(fd))
+
+
+# ----------------------------------------------------------------------------- compiled radial
+def _cubic_spline(P, G, F, dr, seed):
+    """A RadialSpline whose tables sample per-(pair, column) cubics f(r) = a + b r + c r^2 + d r^3
+    exactly (values and derivatives), with the cubics themselves."""
+    g = torch.Generator().manual_seed(seed)
+    a, b, c, d = (torch.randn(P, 1, F, generator=g, dtype=torch.float64) for _ in range(4))
+    r = (torch.arange(G, dtype=torch.float64) * dr)[None, :, None]
+    T = a + b * r + c * r ** 2 + d * r ** 3
+    dT = b + 2 * c * r + 3 * d * r ** 2
+    f = lambda rr, p: a[p, 0] + b[p, 0] * rr[:, None] + c[p, 0] * rr[:, None] ** 2 + d[p, 0] * rr[:, None] ** 3
+    df = lambda rr, p: b[p, 0] + 2 * c[p, 0] * rr[:, None] + 3 * d[p, 0] * rr[:, None] ** 2
+    return omodel.RadialSpline(T, dT, dr), f, df
+
+
+def test_spline_reproduces_cubics_and_their_derivative():
+    """Cubic Hermite interpolation with exact end slopes is exact for cubics: a wrong basis
+    polynomial, a missing dr on the slopes or a shifted cell fails this."""
+    P, G, F, dr = 3, 50, 5, 0.1
+    sp, f, df = _cubic_spline(P, G, F, dr, 0)
+    rng = np.random.default_rng(0)
+    r = torch.tensor(rng.uniform(1e-3, (G - 1) * dr - 1e-9, 400), dtype=torch.float64, requires_grad=True)
+    pair = torch.tensor(rng.integers(0, P, 400))
+    S = sp(r, pair)
+    assert torch.allclose(S, f(r.detach(), pair), rtol=0, atol=1e-11)
+    g = torch.randn(S.shape, dtype=torch.float64)
+    (gr,) = torch.autograd.grad((S * g).sum(), r)
+    assert torch.allclose(gr, (df(r.detach(), pair) * g).sum(-1), rtol=0, atol=1e-9)
+    # grid points return the table rows; beyond the last point the clamp holds the last row
+    rg = torch.tensor([0.0, 7 * dr, (G - 1) * dr, (G - 1) * dr + 3.0], dtype=torch.float64)
+    pg = torch.tensor([0, 1, 2, 2])
+    Sg = sp(rg, pg)
+    assert torch.allclose(Sg[0], sp.T[0, 0]) and torch.allclose(Sg[1], sp.T[1, 7])
+    assert torch.allclose(Sg[2], sp.T[2, G - 1]) and torch.allclose(Sg[3], sp.T[2, G - 1])
+
+
+def test_spline_tables_match_the_radial_mlp_and_its_derivative():
+    """RadialSpline.build: T is the radial MLP on the grid and dT its r-derivative (central
+    differences of the MLP itself, fp64), per element pair."""
+    kw, el, _ = SMALL_CASES["small_cp_mol"]
+    m = build_oracle(kw, el, torch.float64).compile_radial(n_grid=257)
+    blk = m.blocks[0]
+    sp = blk.spline
+    G = sp.T.shape[1]
+    r = torch.linspace(0, m.rc, G, dtype=torch.float64).clamp_min(1e-4)
+
+    def mlp_at(rr):
+        bes, env = m.basis(rr[None].expand(sp.T.shape[0], -1))
+        return blk.radial(torch.nn.functional.silu(blk.rad_in(bes * env[..., None]) +
+                                                   blk.pair.weight[:, None, :]))
+
+    with torch.no_grad():
+        assert torch.allclose(sp.T, mlp_at(r), rtol=0, atol=1e-12)
+        h = 1e-5
+        inner = slice(1, G - 1)
+        fd = (mlp_at(r[inner] + h) - mlp_at(r[inner] - h)) / (2 * h)
+        assert (fd - sp.dT[:, inner]).abs().max() <= 1e-6 * sp.dT.abs().max()
+
+
+def test_compiled_radial_model_matches_mlp_model_f64():
+    """face/tests/test_kernels.py:38-54 (check_spline) in fp64: with 4096 grid points the
+    interpolation error is far below fp32 round-off, so compiled and MLP models agree tightly."""
+    for name in ("small_flag_box", "small_cp_mol"):
+        kw, el, _ = SMALL_CASES[name]
+        d = load(f"{name}_f64")
+        m = build_oracle(kw, el, torch.float64)
+        o1 = m(graph_of(d, torch.float64))
+        o2 = m.compile_radial()(graph_of(d, torch.float64))
+        m.compile_radial(on=False)
+        E1, E2 = o1["energy"].detach(), o2["energy"].detach()
+        F1, F2 = o1["forces"].detach(), o2["forces"].detach()
+        assert (E1 - E2).abs().max() <= 1e-9 * E1.abs().max(), name
+        assert (F1 - F2).abs().max() <= 1e-7 * F1.pow(2).mean().sqrt(), name
