@@ -32,7 +32,8 @@ TIMED = ["density_fwd20", "density_bwd20", "cp_fwd", "cp_fwd_tab", "cp_bwd", "cp
          "cp_radial_bwd_tab", "transport_fwd", "transport_bwd", "dir_fwd",
          "dir_bwd", "node_fwd", "node_bwd", "edge_fwd", "edge_bwd", "force_scatter", "gather_bwd", "radial_fwd",
          "radial_bwd", "radial_head", "edge_msg_fwd", "edge_msg_bwd", "mix_fwd", "mix_bwd", "tmix_bwd", "proj_fwd",
-         "proj_bwd", "eq_gate_fwd", "eq_gate_bwd", "ln_fwd", "ln_bwd", "spline_fwd", "spline_bwd"]
+         "proj_bwd", "eq_gate_fwd", "eq_gate_bwd", "ln_fwd", "ln_bwd", "spline_order",
+         "spline_fwd", "spline_bwd"]
 MFMA_PEAK_TFS = 157.3                   # MI355X dense fp32 MFMA
 
 

@@ -330,44 +330,68 @@ __device__ __forceinline__ SplineCell spline_cell(float r, int32_t pair, const S
     return c;
 }
 
-template <int L>
+// W columns per lane and load (1, or 4 when the rows are float4-aligned and nb % 4 == 0)
+template <int W>
+struct SplineVec;
+template <>
+struct SplineVec<1> {
+    typedef float T;
+    static __device__ __forceinline__ float ld(const float* p) { return *p; }
+    static __device__ __forceinline__ void st(float* p, float v) { *p = v; }
+    static __device__ __forceinline__ float sum(float v) { return v; }
+};
+template <>
+struct SplineVec<4> {
+    typedef v4f T;
+    static __device__ __forceinline__ v4f ld(const float* p) { return ld4(p); }
+    static __device__ __forceinline__ void st(float* p, v4f v) { st4(p, v); }
+    static __device__ __forceinline__ float sum(v4f v) { return (v[0] + v[1]) + (v[2] + v[3]); }
+};
+
+template <int L, int W>
 __global__ __launch_bounds__(256) void radial_spline_fwd_kernel(const float* __restrict__ r,
                                                                 const int32_t* __restrict__ pair, int64_t E,
                                                                 SplineTab S, const float* __restrict__ env, int nb,
+                                                                const int32_t* __restrict__ order,
                                                                 float* __restrict__ phi, int ld_phi,
                                                                 float* __restrict__ R, int ld_R) {
+    typedef SplineVec<W> V;
     const int64_t tid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    const int64_t e = tid / L;
+    const int64_t q = tid / L;
     const int l = (int)(tid % L);
-    if (e >= E) return;
+    if (q >= E) return;
+    const int64_t e = order ? (int64_t)order[q] : q;
     const SplineCell c = spline_cell(r[e], pair[e], S);
     const float t = c.t, t2 = t * t, t3 = t2 * t;
     const float h10 = t3 - 2.f * t2 + t, h01 = -2.f * t3 + 3.f * t2, h11 = t3 - t2;
     const float ev = env ? env[e] : 1.f;
     const float* T0 = S.T + c.row;
     const float* D0 = S.dT + c.row;
-    for (int f = l; f < S.F; f += L) {
-        const float p0 = T0[f], p1 = T0[S.F + f];
-        const float m0 = D0[f] * S.dr, m1 = D0[S.F + f] * S.dr;
-        const float v = p0 + (h01 * (p1 - p0) + (h10 * m0 + h11 * m1));
+    for (int f = W * l; f < S.F; f += W * L) {
+        const typename V::T p0 = V::ld(T0 + f), p1 = V::ld(T0 + S.F + f);
+        const typename V::T m0 = V::ld(D0 + f) * S.dr, m1 = V::ld(D0 + S.F + f) * S.dr;
+        const typename V::T v = p0 + (h01 * (p1 - p0) + (h10 * m0 + h11 * m1));
         if (f < nb)
-            phi[e * ld_phi + f] = v * ev;
+            V::st(phi + e * ld_phi + f, v * ev);
         else
-            R[e * ld_R + f - nb] = v;
+            V::st(R + e * ld_R + f - nb, v);
     }
 }
 
-template <int L>
+template <int L, int W>
 __global__ __launch_bounds__(256) void radial_spline_bwd_kernel(const float* __restrict__ r,
                                                                 const int32_t* __restrict__ pair, int64_t E,
                                                                 SplineTab S, const float* __restrict__ env, int nb,
+                                                                const int32_t* __restrict__ order,
                                                                 const float* __restrict__ gphi, int ld_gphi,
                                                                 const float* __restrict__ gR, int ld_gR,
                                                                 float* __restrict__ gr, float* __restrict__ genv) {
+    typedef SplineVec<W> V;
     const int64_t tid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    const int64_t e = tid / L;
+    const int64_t q = tid / L;
     const int l = (int)(tid % L);
-    if (e >= E) return;                                // whole groups of L lanes share e
+    if (q >= E) return;                                // whole groups of L lanes share q
+    const int64_t e = order ? (int64_t)order[q] : q;
     const SplineCell c = spline_cell(r[e], pair[e], S);
     const float t = c.t, t2 = t * t, t3 = t2 * t;
     const float h10 = t3 - 2.f * t2 + t, h01 = -2.f * t3 + 3.f * t2, h11 = t3 - t2;
@@ -375,29 +399,91 @@ __global__ __launch_bounds__(256) void radial_spline_bwd_kernel(const float* __r
     const float ev = env ? env[e] : 1.f;
     const float* T0 = S.T + c.row;
     const float* D0 = S.dT + c.row;
-    float sr = 0.f, se = 0.f;                          // d/dt and d/denv partial sums
-    for (int f = l; f < S.F; f += L) {
-        const float gv = f < nb ? (gphi ? gphi[e * ld_gphi + f] : 0.f) : (gR ? gR[e * ld_gR + f - nb] : 0.f);
-        const float p0 = T0[f], p1 = T0[S.F + f];
-        const float m0 = D0[f] * S.dr, m1 = D0[S.F + f] * S.dr;
-        const float dp = p1 - p0;
-        const float dv = d01 * dp + (d10 * m0 + d11 * m1);
-        if (f < nb) {
-            se = fmaf(gv, p0 + (h01 * dp + (h10 * m0 + h11 * m1)), se);
-            sr = fmaf(gv * ev, dv, sr);
+    typename V::T sr = {}, se = {};                    // d/dt and d/denv partial sums
+    for (int f = W * l; f < S.F; f += W * L) {
+        const bool lo = f < nb;
+        const float* gp = lo ? gphi : gR;
+        const typename V::T zero = {};
+        const typename V::T gv = gp ? V::ld(lo ? gphi + e * ld_gphi + f : gR + e * ld_gR + f - nb) : zero;
+        const typename V::T p0 = V::ld(T0 + f), p1 = V::ld(T0 + S.F + f);
+        const typename V::T m0 = V::ld(D0 + f) * S.dr, m1 = V::ld(D0 + S.F + f) * S.dr;
+        const typename V::T dp = p1 - p0;
+        const typename V::T dv = d01 * dp + (d10 * m0 + d11 * m1);
+        if (lo) {
+            se += gv * (p0 + (h01 * dp + (h10 * m0 + h11 * m1)));
+            sr += (gv * ev) * dv;
         } else {
-            sr = fmaf(gv, dv, sr);
+            sr += gv * dv;
         }
     }
-    sr = group_sum(sr, L);
-    se = group_sum(se, L);
+    float srs = group_sum(V::sum(sr), L);
+    float ses = group_sum(V::sum(se), L);
     if (l == 0) {
-        gr[e] = c.inside ? sr / S.dr : 0.f;
-        if (genv) genv[e] = se;
+        gr[e] = c.inside ? srs / S.dr : 0.f;
+        if (genv) genv[e] = ses;
     }
 }
 
-static int spline_lanes(int F) { return F <= 8 ? 8 : (F <= 16 ? 16 : (F <= 32 ? 32 : 64)); }
+static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// lanes per edge: a power of two about the number of column groups (W columns each), at most 64
+static int spline_lanes(int F, int W) {
+    const int g = (F + W - 1) / W;
+    return g <= 4 ? 4 : (g <= 8 ? 8 : (g <= 16 ? 16 : (g <= 32 ? 32 : 64)));
+}
+
+// Edge order by table cell (pair, grid interval): a counting sort, so that consecutive
+// workgroups of the spline kernels read the same table rows (from L2) instead of each edge
+// gathering its rows from HBM. Order within a cell is arbitrary (atomic cursors): every edge's
+// outputs are its own, so the results do not depend on it.
+__global__ __launch_bounds__(256) void spline_zero_kernel(int32_t* __restrict__ a, int64_t n) {
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (t < n) a[t] = 0;
+}
+
+__global__ __launch_bounds__(256) void spline_count_kernel(const float* __restrict__ r,
+                                                           const int32_t* __restrict__ pair, int64_t E, SplineTab S,
+                                                           int32_t* __restrict__ cnt) {
+    const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    const SplineCell c = spline_cell(r[e], pair[e], S);
+    atomicAdd(cnt + c.row / S.F, 1);
+}
+
+// exclusive scan of n counts in place, one workgroup of 1024 threads (n = P * G, tens of
+// thousands): per-thread chunk sums, a workgroup scan of the 1024 partials in LDS, then each
+// thread rewrites its chunk
+__global__ __launch_bounds__(1024) void spline_scan_kernel(int32_t* __restrict__ cnt, int n) {
+    __shared__ int32_t part[1024];
+    const int t = threadIdx.x, chunk = (n + 1023) / 1024;
+    const int b = min(n, t * chunk), e = min(n, b + chunk);
+    int32_t s = 0;
+    for (int k = b; k < e; ++k) s += cnt[k];
+    part[t] = s;
+    __syncthreads();
+    for (int o = 1; o < 1024; o <<= 1) {              // Hillis-Steele inclusive scan
+        const int32_t v = t >= o ? part[t - o] : 0;
+        __syncthreads();
+        part[t] += v;
+        __syncthreads();
+    }
+    int32_t run = t > 0 ? part[t - 1] : 0;
+    for (int k = b; k < e; ++k) {
+        const int32_t c = cnt[k];
+        cnt[k] = run;
+        run += c;
+    }
+}
+
+__global__ __launch_bounds__(256) void spline_place_kernel(const float* __restrict__ r,
+                                                           const int32_t* __restrict__ pair, int64_t E, SplineTab S,
+                                                           int32_t* __restrict__ cursor,
+                                                           int32_t* __restrict__ order) {
+    const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    const SplineCell c = spline_cell(r[e], pair[e], S);
+    order[atomicAdd(cursor + c.row / S.F, 1)] = (int32_t)e;
+}
 
 static bool spline_args_ok(const float* r, const int32_t* pair, int64_t E, const float* T, const float* dT, int P,
                            int G, int F, float dr, int nb) {
@@ -471,22 +557,33 @@ extern "C" int face_radial_bwd(const float* rb, int32_t ld_rb, int32_t n_basis, 
 
 extern "C" int face_radial_spline_fwd(const float* r, const int32_t* pair, int64_t E, const float* T, const float* dT,
                                       int32_t P, int32_t G, int32_t F, float dr, const float* env, int32_t nb,
-                                      float* phi, int32_t ld_phi, float* R, int32_t ld_R, void* stream) {
+                                      const int32_t* order, float* phi, int32_t ld_phi, float* R, int32_t ld_R,
+                                      void* stream) {
     if (!spline_args_ok(r, pair, E, T, dT, P, G, F, dr, nb) || (nb > 0 && (ld_phi < nb || (E > 0 && !phi))) ||
         (nb < F && (ld_R < F - nb || (E > 0 && !R))))
         return FACE_ERR_ARG;
     if (E == 0) return 0;
     const SplineTab tab{T, dT, P, G, F, dr};
-    const int L = spline_lanes(F);
+    const bool vec = F % 4 == 0 && nb % 4 == 0 && al16(T) && al16(dT) && (nb == 0 || (ld_phi % 4 == 0 && al16(phi))) &&
+                     (nb == F || (ld_R % 4 == 0 && al16(R)));
+    const int W = vec ? 4 : 1, L = spline_lanes(F, W);
     const dim3 grid((unsigned)((E * L + 255) / 256)), block(256);
     const hipStream_t st = (hipStream_t)stream;
-#define FACE_SPLINE(K_, L_) hipLaunchKernelGGL((K_<L_>), grid, block, 0, st, r, pair, E, tab, env, nb, ARGS_)
+#define FACE_SPLINE(K_, L_, W_) \
+    hipLaunchKernelGGL((K_<L_, W_>), grid, block, 0, st, r, pair, E, tab, env, nb, order, ARGS_)
+#define FACE_SPLINE_L(K_, W_)                           \
+    switch (L) {                                        \
+        case 4: FACE_SPLINE(K_, 4, W_); break;          \
+        case 8: FACE_SPLINE(K_, 8, W_); break;          \
+        case 16: FACE_SPLINE(K_, 16, W_); break;        \
+        case 32: FACE_SPLINE(K_, 32, W_); break;        \
+        default: FACE_SPLINE(K_, 64, W_); break;        \
+    }
 #define ARGS_ phi, ld_phi, R, ld_R
-    switch (L) {
-        case 8: FACE_SPLINE(radial_spline_fwd_kernel, 8); break;
-        case 16: FACE_SPLINE(radial_spline_fwd_kernel, 16); break;
-        case 32: FACE_SPLINE(radial_spline_fwd_kernel, 32); break;
-        default: FACE_SPLINE(radial_spline_fwd_kernel, 64); break;
+    if (vec) {
+        FACE_SPLINE_L(radial_spline_fwd_kernel, 4)
+    } else {
+        FACE_SPLINE_L(radial_spline_fwd_kernel, 1)
     }
 #undef ARGS_
     FACE_LAUNCH_CHECK();
@@ -495,25 +592,45 @@ extern "C" int face_radial_spline_fwd(const float* r, const int32_t* pair, int64
 
 extern "C" int face_radial_spline_bwd(const float* r, const int32_t* pair, int64_t E, const float* T, const float* dT,
                                       int32_t P, int32_t G, int32_t F, float dr, const float* env, int32_t nb,
-                                      const float* gphi, int32_t ld_gphi, const float* gR, int32_t ld_gR, float* gr,
-                                      float* genv, void* stream) {
+                                      const int32_t* order, const float* gphi, int32_t ld_gphi, const float* gR,
+                                      int32_t ld_gR, float* gr, float* genv, void* stream) {
     if (!spline_args_ok(r, pair, E, T, dT, P, G, F, dr, nb) || (gphi && ld_gphi < nb) || (gR && ld_gR < F - nb) ||
         (E > 0 && !gr))
         return FACE_ERR_ARG;
     if (E == 0) return 0;
     const SplineTab tab{T, dT, P, G, F, dr};
-    const int L = spline_lanes(F);
+    const bool vec = F % 4 == 0 && nb % 4 == 0 && al16(T) && al16(dT) &&
+                     (!gphi || (ld_gphi % 4 == 0 && al16(gphi))) && (!gR || (ld_gR % 4 == 0 && al16(gR)));
+    const int W = vec ? 4 : 1, L = spline_lanes(F, W);
     const dim3 grid((unsigned)((E * L + 255) / 256)), block(256);
     const hipStream_t st = (hipStream_t)stream;
 #define ARGS_ gphi, ld_gphi, gR, ld_gR, gr, genv
-    switch (L) {
-        case 8: FACE_SPLINE(radial_spline_bwd_kernel, 8); break;
-        case 16: FACE_SPLINE(radial_spline_bwd_kernel, 16); break;
-        case 32: FACE_SPLINE(radial_spline_bwd_kernel, 32); break;
-        default: FACE_SPLINE(radial_spline_bwd_kernel, 64); break;
+    if (vec) {
+        FACE_SPLINE_L(radial_spline_bwd_kernel, 4)
+    } else {
+        FACE_SPLINE_L(radial_spline_bwd_kernel, 1)
     }
 #undef ARGS_
+#undef FACE_SPLINE_L
 #undef FACE_SPLINE
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int face_radial_spline_order(const float* r, const int32_t* pair, int64_t E, int32_t P, int32_t G,
+                                        float dr, int32_t* work, int32_t* order, void* stream) {
+    if (E < 0 || P < 1 || G < 2 || !(dr > 0.f) || (int64_t)P * G > 0x7fffffff || E > 0x7fffffff) return FACE_ERR_ARG;
+    if (E == 0) return 0;
+    if (!r || !pair || !work || !order) return FACE_ERR_ARG;
+    const SplineTab tab{nullptr, nullptr, P, G, 1, dr};
+    const int64_t n = (int64_t)P * G;
+    const hipStream_t st = (hipStream_t)stream;
+    hipLaunchKernelGGL(spline_zero_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, work, n);
+    hipLaunchKernelGGL(spline_count_kernel, dim3((unsigned)((E + 255) / 256)), dim3(256), 0, st, r, pair, E, tab,
+                       work);
+    hipLaunchKernelGGL(spline_scan_kernel, dim3(1), dim3(1024), 0, st, work, (int)n);
+    hipLaunchKernelGGL(spline_place_kernel, dim3((unsigned)((E + 255) / 256)), dim3(256), 0, st, r, pair, E, tab,
+                       work, order);
     FACE_LAUNCH_CHECK();
     return 0;
 }

@@ -220,7 +220,7 @@ class FactorBlock(nn.Module):
             self.tmix3 = nn.Linear(B * 2 * K_dir, C, bias=False)
 
     # ------------------------------------------------------------------ moments
-    def moments(self, h, rb, r, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g):
+    def moments(self, h, rb, r, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g, order=None):
         """Moments A_l as monomial-major (k_l, N, C) blocks (face/model.py:460-534)."""
         N, E = g.N, g.E
         B, C, Kd = self.B, self.C, self.K
@@ -229,7 +229,7 @@ class FactorBlock(nn.Module):
             # compiled radial (face/model.py:466-467): phi = spline * env (E, B) and, in CP form,
             # the raw CP radials (E, 4C) whose envelope the pooling kernels apply
             sp = self.spline
-            phi, R_sp = ops.radial_spline(r, env, zp, sp.T, sp.dT, sp.dr, B)
+            phi, R_sp = ops.radial_spline(r, env, zp, sp.T, sp.dT, sp.dr, B, order)
         else:
             # hidden layers and phi columns of the radial MLP in one HIP kernel; the CP columns of
             # the last layer are a GEMM on its h2 output
@@ -299,9 +299,9 @@ class FactorBlock(nn.Module):
         return c[1]
 
     # ------------------------------------------------------------------ invariants + readout
-    def forward(self, h, rb, r, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g):
+    def forward(self, h, rb, r, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g, order=None):
         C = self.C
-        A = self.moments(h, rb, r, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g)
+        A = self.moments(h, rb, r, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g, order)
         allsets = sets + [A]
         # only P0 of rank 0 and P3, Q3 of rank 3 are used
         ws = [frozen(self.proj[l])[0][:(C, 3 * C, 3 * C, 2 * C)[l]] for l in range(4)]
@@ -421,9 +421,16 @@ class FACE(nn.Module):
         zidx32 = graph.cache[zkey + ("atoms",)]
         h = F.embedding(zidx, self.embed.weight.detach())
         e_at = self.E0[zidx].clone()
+        # table-cell edge order for large compiled tables: one sort per step, shared by the passes
+        order = None
+        big = [b.spline for b in self.blocks if b.spline is not None and ops.spline_wants_order(b.spline.T)]
+        if big:
+            P, G = big[0].T.shape[:2]
+            if all(s.T.shape[:2] == (P, G) and s.dr == big[0].dr for s in big):
+                order = ops.spline_order(r, zp, P, G, big[0].dr)
         sets, eq = [], None
         for blk in self.blocks:
-            e, h, A, eq = blk(h, rb, r, Y, env, zp, zidx, zidx32, self.avg_nb, sets, eq, graph)
+            e, h, A, eq = blk(h, rb, r, Y, env, zp, zidx, zidx32, self.avg_nb, sets, eq, graph, order)
             sets.append(A)
             e_at = e_at + self.scale * e.squeeze(-1)
         E = ops.StructureSum.apply(e_at, graph.struct_ptr, graph.batch, graph.nstr)

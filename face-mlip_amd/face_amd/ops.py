@@ -624,25 +624,29 @@ class RadialSpline(torch.autograd.Function):
     the tables T, dT (P, G, F) at r (E) for element pair `pair` (E); returns phi (E, nb) = the
     first nb columns times env, and R (E, F - nb) = the other columns as they are (the CP radials,
     enveloped inside the pooling kernels). Gradients flow to r and env (the tables are constants
-    of the compiled model)."""
+    of the compiled model). Tables far larger than L2 (the CP columns) are read in table-cell
+    order (spline_order)."""
 
     @staticmethod
-    def forward(ctx, r, env, pair, T, dT, dr, nb):
+    def forward(ctx, r, env, pair, T, dT, dr, nb, order):
         _lib.require_gpu(r, env, T)
         P, G, F = T.shape
         E = r.shape[0]
         r_, env_ = r.contiguous().float(), env.contiguous().float()
         phi = torch.empty(E, nb, device=r.device)
         R = torch.empty(E, F - nb, device=r.device)
+        st = _lib.stream_of(r)
+        if order is None and spline_wants_order(T):
+            order = spline_order(r_, pair, P, G, dr)
         call("face_radial_spline_fwd", ptr(r_), ptr(pair), E, ptr(T), ptr(dT), P, G, F, float(dr), ptr(env_), nb,
-             ptr(phi), nb, ptr(R), F - nb, _lib.stream_of(r), label="spline_fwd")
-        ctx.save_for_backward(r_, env_, pair, T, dT)
+             ptr(order), ptr(phi), nb, ptr(R), F - nb, st, label="spline_fwd")
+        ctx.save_for_backward(r_, env_, pair, T, dT, order)
         ctx.dr, ctx.nb = dr, nb
         return phi, R
 
     @staticmethod
     def backward(ctx, gphi, gR):
-        r, env, pair, T, dT = ctx.saved_tensors
+        r, env, pair, T, dT, order = ctx.saved_tensors
         P, G, F = T.shape
         E, nb = r.shape[0], ctx.nb
         gp, ldp = _rows(gphi, nb) if (gphi is not None and nb > 0) else (None, nb)
@@ -650,13 +654,35 @@ class RadialSpline(torch.autograd.Function):
         gr = torch.empty(E, device=r.device)
         genv = torch.empty(E, device=r.device) if ctx.needs_input_grad[1] else None
         call("face_radial_spline_bwd", ptr(r), ptr(pair), E, ptr(T), ptr(dT), P, G, F, float(ctx.dr), ptr(env), nb,
-             ptr(gp), ldp, ptr(gq), ldq, ptr(gr), ptr(genv), _lib.stream_of(r), label="spline_bwd")
-        return gr, genv, None, None, None, None, None
+             ptr(order), ptr(gp), ldp, ptr(gq), ldq, ptr(gr), ptr(genv), _lib.stream_of(r), label="spline_bwd")
+        return gr, genv, None, None, None, None, None, None
 
 
-def radial_spline(r, env, pair, T, dT, dr, nb):
-    """(phi (E, nb), R (E, F - nb)) from the compiled tables; see RadialSpline."""
-    return RadialSpline.apply(r, env, pair, T, dT, dr, nb)
+SPLINE_SORT_BYTES = 16 << 20                 # both tables above this: visit the edges cell by cell
+
+
+def spline_wants_order(T):
+    """Whether the spline kernels should visit the edges in table-cell order (tables of (P, G, F)
+    far larger than L2, e.g. with the CP columns)."""
+    return 8 * T.numel() > SPLINE_SORT_BYTES
+
+
+def spline_order(r, pair, P, G, dr):
+    """int32 (E,) permutation of the edges sorted by table cell (pair, grid interval of r); the
+    same for every pass of a step (they share r, the pair index and the grid)."""
+    E = r.shape[0]
+    order = torch.empty(E, dtype=torch.int32, device=r.device)
+    if E:
+        work = torch.empty(P * G, dtype=torch.int32, device=r.device)
+        call("face_radial_spline_order", ptr(r.detach().contiguous().float()), ptr(pair), E, P, G, float(dr),
+             ptr(work), ptr(order), _lib.stream_of(r), label="spline_order")
+    return order
+
+
+def radial_spline(r, env, pair, T, dT, dr, nb, order=None):
+    """(phi (E, nb), R (E, F - nb)) from the compiled tables; see RadialSpline. order: a
+    spline_order() permutation to reuse (computed here when the tables want one and it is None)."""
+    return RadialSpline.apply(r, env, pair, T, dT, dr, nb, order)
 
 
 # ----------------------------------------------------------------------------- node algebra

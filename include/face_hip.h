@@ -22,6 +22,7 @@
  *   face/model.py:670-677        edge geometry + Bessel basis     -> face_edge_geom_fwd / _bwd
  *   face/model.py:465-469        radial MLP (rad_in, pair, radial) -> face_radial_fwd / _bwd
  *   face/model.py:407-418,466-467 RadialSpline (compile_radial)   -> face_radial_spline_fwd / _bwd
+ *                                                                    (+ face_radial_spline_order)
  *   face/model.py:469,488-493    CP radial columns; gather(msg(h)) + dir_mix(d)
  *                                                                  -> face_edge_linear_fwd / _bwd
  *   face/model.py:498-533,537-544 mix / tmix / proj (+ elem_scale)   -> face_rows_linear
@@ -255,16 +256,25 @@ int face_radial_bwd(const float* rb, int32_t ld_rb, int32_t n_basis, const int32
  * (cubic Hermite basis), p = pair[e] (clamped into [0, P)). Columns f < nb: phi[e][f] =
  * S[e,f] * env[e] (face/model.py:467; env may be NULL: factor 1); columns f >= nb (the CP
  * radials, enveloped inside the pooling kernels): R[e][f - nb] = S[e,f]. G >= 2, dr > 0,
- * 0 <= nb <= F; phi is unused when nb = 0, R when nb = F. */
+ * 0 <= nb <= F; phi is unused when nb = 0, R when nb = F. order (E, may be NULL): the
+ * permutation of the edges in which to visit them (face_radial_spline_order), no effect on the
+ * results. */
 int face_radial_spline_fwd(const float* r, const int32_t* pair, int64_t E, const float* T, const float* dT, int32_t P,
-                           int32_t G, int32_t F, float dr, const float* env, int32_t nb, float* phi, int32_t ld_phi,
-                           float* R, int32_t ld_R, void* stream);
+                           int32_t G, int32_t F, float dr, const float* env, int32_t nb, const int32_t* order,
+                           float* phi, int32_t ld_phi, float* R, int32_t ld_R, void* stream);
 /* Its backward for upstream gphi (E, ld_gphi >= nb) and gR (E, ld_gR >= F - nb) (either may be
  * NULL = 0): gr[e] = sum_f g[e,f] dphi_or_R[e,f]/dr (0 where r / dr lies outside [0, G - 1], as
  * through the clamp), genv[e] = sum_{f < nb} gphi[e,f] S[e,f] (genv may be NULL). */
 int face_radial_spline_bwd(const float* r, const int32_t* pair, int64_t E, const float* T, const float* dT, int32_t P,
-                           int32_t G, int32_t F, float dr, const float* env, int32_t nb, const float* gphi,
-                           int32_t ld_gphi, const float* gR, int32_t ld_gR, float* gr, float* genv, void* stream);
+                           int32_t G, int32_t F, float dr, const float* env, int32_t nb, const int32_t* order,
+                           const float* gphi, int32_t ld_gphi, const float* gR, int32_t ld_gR, float* gr, float* genv,
+                           void* stream);
+/* No counterpart in the reference (its index_select gathers in edge order): the edges sorted by
+ * table cell (pair, grid interval) into order (E), a permutation, so that the spline kernels
+ * read each table row from L2 for the whole run of edges that needs it -- worth it when the
+ * tables (8 P G F bytes) are far larger than L2. work: P * G int32 of scratch. */
+int face_radial_spline_order(const float* r, const int32_t* pair, int64_t E, int32_t P, int32_t G, float dr,
+                             int32_t* work, int32_t* order, void* stream);
 
 /* ---------------------------------------------------------------- row-block linear layers
  * One problem: x (m, ld_x >= k) rows, w (n, k) row-major with row stride ld_w (w_kn = 0) or

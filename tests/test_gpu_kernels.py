@@ -399,6 +399,45 @@ def test_radial_spline_matches_oracle(P, G, F, nb):
     assert float(gr[r.to(DEV) > rc + 1e-3].abs().max()) == 0.0   # clamped: no r-derivative
 
 
+def test_radial_spline_order_is_a_cell_sorted_permutation():
+    """face_radial_spline_order: a permutation of the edges with non-decreasing table cell
+    (pair * G + grid interval, the same cell the spline kernels use), including radii past the
+    grid's end (last interval); the spline outputs in that order equal the unordered ones bitwise."""
+    from face_amd._lib import call, ptr, stream_of
+    say("spline order")
+    P, G, F, nb, E = 5, 700, 24, 8, 20000
+    rc = 4.0
+    dr = rc / (G - 1)
+    rng = np.random.default_rng(9)
+    r = torch.tensor(rng.uniform(1e-4, rc + 0.5, E), dtype=torch.float32, device=DEV)
+    pair = torch.tensor(rng.integers(0, P, E), dtype=torch.int32, device=DEV)
+    work = torch.empty(P * G, dtype=torch.int32, device=DEV)
+    order = torch.empty(E, dtype=torch.int32, device=DEV)
+    st = stream_of(r)
+    call("face_radial_spline_order", ptr(r), ptr(pair), E, P, G, dr, ptr(work), ptr(order), st)
+    o = order.long().cpu()
+    assert torch.equal(torch.sort(o).values, torch.arange(E))
+    x = (r.cpu() / dr).clamp(0, G - 1)
+    cell = pair.long().cpu() * G + torch.floor(x).long().clamp(max=G - 2)
+    assert bool((cell[o][1:] >= cell[o][:-1]).all())
+    T = torch.randn(P, G, F, device=DEV)
+    dT = torch.randn(P, G, F, device=DEV)
+    env = torch.rand(E, device=DEV)
+    outs = []
+    for od in (None, order):
+        phi = torch.empty(E, nb, device=DEV)
+        R = torch.empty(E, F - nb, device=DEV)
+        call("face_radial_spline_fwd", ptr(r), ptr(pair), E, ptr(T), ptr(dT), P, G, F, dr, ptr(env), nb, ptr(od),
+             ptr(phi), nb, ptr(R), F - nb, st)
+        gp, gq = torch.ones(E, nb, device=DEV), torch.ones(E, F - nb, device=DEV)
+        gr, ge = torch.empty(E, device=DEV), torch.empty(E, device=DEV)
+        call("face_radial_spline_bwd", ptr(r), ptr(pair), E, ptr(T), ptr(dT), P, G, F, dr, ptr(env), nb, ptr(od),
+             ptr(gp), nb, ptr(gq), F - nb, ptr(gr), ptr(ge), st)
+        outs.append((phi, R, gr, ge))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
 @pytest.mark.parametrize("Kd,B,transport", [(16, 16, True), (4, 8, True), (5, 4, False), (16, 16, False)])
 def test_dir_transport_and_gradients(Kd, B, transport):
     """Directional features d = [u.V_j, u^T M_j u, u.V_i, u^T M_i u] (face/model.py:474-493) and the
