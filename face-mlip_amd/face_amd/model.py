@@ -340,7 +340,8 @@ class FactorBlock(nn.Module):
             else:
                 gv, gm = gvm.chunk(2, dim=-1)
                 eq_new = (V * gv[None], Ms * gm[None])
-        return o[:, :1], h + o[:, 1:], A, eq_new
+        e, h_new = ops.readout_split(o, h)                                      # (N, 1), (N, C)
+        return e, h_new, A, eq_new
 
 
 class FACE(nn.Module):

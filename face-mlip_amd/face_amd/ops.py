@@ -297,6 +297,29 @@ def dir_transport(Vb, Mb, phi, Y, graph, Kd, transport):
     return DirTransport.apply(Vb, Mb, phi, Y, graph, Kd, transport)
 
 
+class ReadoutSplit(torch.autograd.Function):
+    """(o (N, 1 + C), h (N, C)) -> (e (N, 1) = o[:, :1], h + o[:, 1:]): the atom energy and the
+    residual update of face/model.py:336-339. Autograd of the two slices would zero-fill and copy
+    a full (N, 1 + C) gradient per slice and add them; here the backward is one concatenation."""
+
+    @staticmethod
+    def forward(ctx, o, h):
+        ctx.shape = h.shape
+        return o[:, :1].clone(), torch.add(h, o[:, 1:])
+
+    @staticmethod
+    def backward(ctx, ge, gh):
+        N, C = ctx.shape
+        like = gh if gh is not None else ge
+        ge = ge if ge is not None else like.new_zeros(N, 1)
+        gh = gh if gh is not None else like.new_zeros(N, C)
+        return torch.cat([ge, gh], 1), gh
+
+
+def readout_split(o, h):
+    return ReadoutSplit.apply(o, h)
+
+
 class StructureSum(torch.autograd.Function):
     """Per-structure sum of per-atom values (atoms of a structure are contiguous)."""
 
