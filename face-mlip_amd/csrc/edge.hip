@@ -132,7 +132,8 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(const float* __restric
     out[e * ld_out + f] = X[(int64_t)idx[e] * ld_X + f];
 }
 
-// dX[k, f] = sum_{e in row k} g[rev[e], f]; thread = (k, f), row walked in order.
+// dX[k, f] = sum_{e in row k} g[rev[e], f]; thread = (k, f), row walked in order, eight gathers
+// issued per round.
 __global__ __launch_bounds__(256) void gather_rows_bwd_kernel(const float* __restrict__ g, int ld_g,
                                                               const int32_t* __restrict__ row_ptr,
                                                               const int32_t* __restrict__ rev, int64_t N, int F,
@@ -141,8 +142,17 @@ __global__ __launch_bounds__(256) void gather_rows_bwd_kernel(const float* __res
     if (t >= N * F) return;
     const int64_t k = t / F;
     const int f = (int)(t - k * F);
+    const int64_t e1 = row_ptr[k + 1];
     float s = 0.f;
-    for (int64_t e = row_ptr[k]; e < row_ptr[k + 1]; ++e) s += g[(int64_t)rev[e] * ld_g + f];
+    int64_t e = row_ptr[k];
+    for (; e + 8 <= e1; e += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = g[(int64_t)rev[e + u] * ld_g + f];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; e < e1; ++e) s += g[(int64_t)rev[e] * ld_g + f];
     dX[k * ld_dX + f] = s;
 }
 

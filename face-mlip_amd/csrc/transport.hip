@@ -382,7 +382,9 @@ __global__ __launch_bounds__(2 * kWave) void transport_bwd_mfma_kernel(
 }
 
 // Node-table gradient of the transport tables: gV[a, n, kd] = sum_{e in row n} dT_edge[rev e, a, kd]
-// (the edges whose neighbour is n are the reverses of row n); same for gM.
+// (the edges whose neighbour is n are the reverses of row n); same for gM. Eight edges per
+// round, their gathers issued together (one dependent load after another per edge would leave
+// each thread a memory latency per edge), summed in row order.
 __global__ __launch_bounds__(256) void transport_table_grad_kernel(const float* __restrict__ dT_edge, int Kd,
                                                                     const int32_t* __restrict__ row_ptr,
                                                                     const int32_t* __restrict__ rev, int64_t N,
@@ -394,8 +396,18 @@ __global__ __launch_bounds__(256) void transport_table_grad_kernel(const float* 
     const int64_t n = t / (9 * Kd);
     const int r = (int)(t - n * 9 * Kd);
     const int q = r / Kd, kd = r - q * Kd;
+    const int64_t e1 = row_ptr[n + 1];
+    const int64_t st = 9 * (int64_t)Kd;
     float s = 0.f;
-    for (int64_t e = row_ptr[n]; e < row_ptr[n + 1]; ++e) s += dT_edge[(int64_t)rev[e] * 9 * Kd + r];
+    int64_t e = row_ptr[n];
+    for (; e + 8 <= e1; e += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = dT_edge[(int64_t)rev[e + u] * st + r];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; e < e1; ++e) s += dT_edge[(int64_t)rev[e] * st + r];
     if (q < 3) gV[q * v_sq + n * v_sn + kd] = s;
     else gM[(q - 3) * m_sq + n * m_sn + kd] = s;
 }
