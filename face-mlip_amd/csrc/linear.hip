@@ -185,10 +185,14 @@ __global__ __launch_bounds__(kLinBwdWaves * kWave) void edge_linear_bwd_kernel(
         v4f sums[FCB];
 #pragma unroll
         for (int fc = 0; fc < FCB; ++fc) sums[fc] = z4;
+        // the reverse-edge index of the next tile is loaded before this tile's stores: on gfx9 a
+        // wait for a load also waits for every store issued before it
+        int64_t ep_next = a + j < bnd ? (int64_t)rev[a + j] : 0;
         for (int64_t t0 = a; t0 < bnd; t0 += 16) {
             const int64_t er = t0 + j;
             const bool ok = er < bnd;
-            const int64_t ep = ok ? (int64_t)rev[er] : 0;
+            const int64_t ep = ep_next;
+            ep_next = t0 + 16 + j < bnd ? (int64_t)rev[t0 + 16 + j] : 0;
             v4f acc[KB];
 #pragma unroll
             for (int kb = 0; kb < KB; ++kb) acc[kb] = z4;
