@@ -55,6 +55,40 @@ def test_host_rejects_bad_shapes_before_launch():
     assert L.face_density_fwd(1, 16, 1, 32, None, 1, 20, 20, None, 5, 4, 16, 32, None, 1, 1, None) == -1
 
 
+def test_spline_entry_points_reject_bad_arguments():
+    from face_amd import _lib
+    L = _lib.lib()
+    # E, P, G, F, dr, nb out of range are refused before any launch; an empty edge list is a no-op
+    args = lambda E, P, G, F, dr, nb: (None, None, E, None, None, P, G, F, dr, None, nb, None, None, F, None, F, None)
+    assert L.face_radial_spline_fwd(*args(10, 3, 1, 16, 0.1, 16)) == -1          # G < 2
+    assert L.face_radial_spline_fwd(*args(10, 3, 64, 16, 0.0, 16)) == -1         # dr <= 0
+    assert L.face_radial_spline_fwd(*args(10, 3, 64, 16, 0.1, 17)) == -1         # nb > F
+    assert L.face_radial_spline_fwd(*args(-1, 3, 64, 16, 0.1, 16)) == -1
+    assert L.face_radial_spline_fwd(*args(10, 3, 64, 16, 0.1, 16)) == -1         # NULL operands
+    assert L.face_radial_spline_fwd(*args(0, 3, 64, 16, 0.1, 16)) == 0
+    assert L.face_radial_spline_order(None, None, 10, 1 << 16, 1 << 16, 0.1, None, None, None) == -1
+    assert L.face_radial_spline_order(None, None, 0, 3, 64, 0.1, None, None, None) == 0
+
+
+def test_compiled_tables_equal_the_oracle_build():
+    """FACE.compile_radial() on the CPU (float64 evaluation, float32 storage, forward-mode dT)
+    against the oracle's build (the reference's reverse-mode per-column dT, float64) rounded to
+    float32: T identical, dT within a float32 rounding step."""
+    from face_amd import model as fm
+    from oracle import model as om
+    kw, el, _ = SMALL_CASES["small_cp_mol"]
+    torch.manual_seed(0)
+    m = fm.unit_parameterise(fm.FACE(el, **kw)).eval().compile_radial(n_grid=300)
+    torch.manual_seed(0)
+    mo = om.unit_parameterise(om.FACE(el, **kw)).double().eval().compile_radial(n_grid=300,
+                                                                                 store_dtype=torch.float32)
+    for b, bo in zip(m.blocks, mo.blocks):
+        assert b.spline.T.dtype == torch.float32 and b.spline.dr == bo.spline.dr
+        assert torch.equal(b.spline.T.double(), bo.spline.T)
+        d = (b.spline.dT.double() - bo.spline.dT).abs()
+        assert bool((d <= 1.2e-7 * bo.spline.dT.abs() + 1e-30).all())
+
+
 def test_cpu_tensors_are_refused():
     from face_amd.kernels import factor_density
     with pytest.raises(RuntimeError, match="no CPU path"):
