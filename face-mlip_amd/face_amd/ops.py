@@ -653,6 +653,8 @@ class RadialSpline(torch.autograd.Function):
     @staticmethod
     def forward(ctx, r, env, pair, T, dT, dr, nb, order):
         _lib.require_gpu(r, env, T)
+        if pair.dtype != torch.int32 or T.dtype != torch.float32 or dT.dtype != torch.float32:
+            raise TypeError("radial_spline: pair must be int32 and the tables float32")
         P, G, F = T.shape
         E = r.shape[0]
         r_, env_ = r.contiguous().float(), env.contiguous().float()
@@ -693,6 +695,9 @@ def spline_wants_order(T):
 def spline_order(r, pair, P, G, dr):
     """int32 (E,) permutation of the edges sorted by table cell (pair, grid interval of r); the
     same for every pass of a step (they share r, the pair index and the grid)."""
+    _lib.require_gpu(r, pair)
+    if pair.dtype != torch.int32:
+        raise TypeError("spline_order: pair must be int32")
     E = r.shape[0]
     order = torch.empty(E, dtype=torch.int32, device=r.device)
     if E:

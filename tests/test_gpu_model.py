@@ -200,19 +200,27 @@ def test_forces_are_minus_energy_gradient_fd():
         assert abs(fd - F[i, c]) < 2e-3 * (1 + abs(F[i, c])), (fd, F[i, c])
 
 
-@pytest.mark.parametrize("case", ["small_flag_mol", "cfg2"])
+@pytest.mark.parametrize("case", ["small_flag_mol", "cfg2", "cfg3_compiled"])
 def test_graph_replay_matches_eager(case):
-    """HIP-graph replays with new positions, eager work in between, every replay checked."""
+    """HIP-graph replays with new positions, eager work in between, every replay checked.
+    cfg3_compiled: the CP liquid (cut to 1000 atoms) with compiled radial tables, whose size
+    (193 MB) makes each step sort the edges by table cell inside the captured graph."""
     from face_amd import systems
     from face_amd.neighbors import build_graph
     from face_amd.runner import StepGraph
     say("graph replay", case)
     if case == "cfg2":
         sts, kw, el, _ = systems.workload(2)
+    elif case == "cfg3_compiled":
+        sts, kw, el, _ = systems.workload(3, n_atoms=1000)
     else:
         kw, el, _ = SMALL_CASES[case]
         sts = systems.molecules(4, np.random.default_rng(3))
     m = product_model(kw, el)
+    if case == "cfg3_compiled":
+        from face_amd import ops
+        m.compile_radial()
+        assert ops.spline_wants_order(m.blocks[0].spline.T)
     g = build_graph(sts, kw["rc"])
     run = StepGraph(m, g)
     gen = torch.Generator(device="cuda").manual_seed(0)
