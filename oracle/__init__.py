@@ -2,7 +2,8 @@
 
 TEST INFRASTRUCTURE ONLY. Nothing in the product package may import, call or link
 anything under this directory; only ``tests/``, ``__graft_entry__.smoke()`` and the
-``cpu_baseline`` leg of ``bench.py`` use it, and only as the checker.
+``cpu_baseline`` leg of ``bench.py`` use it: as the reference the HIP results are compared
+against, and as the timed CPU baseline -- never as the measured or shipped path.
 
 Contents (each function cites the reference file:line it restates):
   cartesian.py   symmetric Cartesian storage, monomials, expansion  (face/cartesian.py)
