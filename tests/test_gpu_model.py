@@ -156,6 +156,36 @@ def test_compiled_radial_matches_oracle(name):
     check(o2["energy"].detach().cpu(), o2["forces"].detach().cpu(), d["energy"], d["forces"])
 
 
+@pytest.mark.parametrize("cp,compiled", [(False, False), (True, False), (False, True), (True, True)])
+def test_isolated_atoms_and_empty_rows(cp, compiled):
+    """Two molecules and two far-away single atoms (rows without pairs: their densities are zero,
+    their energies the readout of the embedding alone) in one batch, against the oracle."""
+    from face_amd import systems
+    from face_amd.neighbors import build_graph
+    from oracle import model as om
+    from oracle.neighbors import padded_graph as opad
+    say("isolated atoms", cp, compiled)
+    sts = systems.molecules(2, np.random.default_rng(11))
+    for z, p in ((8, (40.0, 0.0, 0.0)), (1, (0.0, 45.0, 3.0))):
+        sts.append({"pos": np.array([p]), "Z": np.array([z]), "cell": np.zeros((3, 3)), "pbc": np.zeros(3, bool)})
+    kw = dict(C=32, transport=True, eqmsg=True, factor=True, B=16, K=32, rc=4.5, cp=cp)
+    m = product_model(kw, [1, 6, 8])
+    if compiled:
+        m.compile_radial()
+    o = m(build_graph(sts, kw["rc"]))
+    torch.manual_seed(0)
+    mo = om.FACE([1, 6, 8], **kw)
+    om.unit_parameterise(mo)
+    mo = mo.double().eval()
+    if compiled:
+        mo.compile_radial(store_dtype=torch.float32)
+    g = opad(sts, kw["rc"], dtype=torch.float64)
+    oo = mo({k: g[k] for k in ("pos", "Z", "nbr", "shift", "mask", "batch")})
+    check(o["energy"].detach().cpu(), o["forces"].detach().cpu(), oo["energy"].detach().numpy(),
+          oo["forces"].detach().numpy())
+    assert float(o["forces"][-2:].abs().max()) == 0.0                 # no pairs: no force
+
+
 def test_compiled_radial_close_to_mlp_model():
     """face/tests/test_kernels.py:38-54 (check_spline): perturbed flagship C32 model, compiled radial
     against the radial MLP on the same structures: |dE| < 1e-5 eV/atom, rel ||dF|| < 1e-3."""
