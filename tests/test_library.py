@@ -137,3 +137,14 @@ def test_synthetic_workloads_follow_the_recipes():
     assert abs(3000 / L ** 3 - 0.10) < 1e-9
     assert systems.liquid_counts(24000) == [9143, 10286, 4571]
     assert systems.liquid_counts(100000) == [38095, 42857, 19048]
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus N > 1 exits with status 2 and says why, before any
+    device work."""
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, os.path.join(REPO, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=300, cwd=REPO)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr
