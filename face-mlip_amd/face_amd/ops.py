@@ -652,7 +652,7 @@ class RadialSpline(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, r, env, pair, T, dT, dr, nb, order):
-        _lib.require_gpu(r, env, T)
+        _lib.require_gpu(r, env, pair, T, dT)
         if pair.dtype != torch.int32 or T.dtype != torch.float32 or dT.dtype != torch.float32:
             raise TypeError("radial_spline: pair must be int32 and the tables float32")
         P, G, F = T.shape
