@@ -399,6 +399,39 @@ def test_radial_spline_matches_oracle(P, G, F, nb):
     assert float(gr[r.to(DEV) > rc + 1e-3].abs().max()) == 0.0   # clamped: no r-derivative
 
 
+def test_radial_spline_without_envelope_as_a_reference_binding():
+    """The call pattern of a binding inside the reference's RadialSpline.forward (padded (N, M)
+    radii and pair indices flattened, no envelope pointer, nb = F): values and r-gradient equal
+    the oracle's RadialSpline in fp64."""
+    from face_amd._lib import call, ptr, stream_of
+    from oracle.model import RadialSpline
+    say("spline binding")
+    P, G, F, N, M = 9, 4096, 16, 40, 23
+    dr = 4.5 / (G - 1)
+    gen = torch.Generator().manual_seed(4)
+    rg = (torch.arange(G, dtype=torch.float64) * dr)[None, :, None]
+    amp, k = torch.randn(P, 1, F, generator=gen, dtype=torch.float64), 0.5 + torch.rand(P, 1, F, generator=gen)
+    T, dT = (amp * torch.cos(k * rg)).float(), (-amp * k * torch.sin(k * rg)).float()
+    r = torch.rand(N, M, generator=gen) * 4.4 + 0.05
+    pair = torch.randint(0, P, (N, M), generator=gen)
+    rd, pd = r.reshape(-1).to(DEV), pair.reshape(-1).to(torch.int32).to(DEV)
+    E = N * M
+    S = torch.empty(E, F, device=DEV)
+    Td, dTd = T.to(DEV), dT.to(DEV)
+    st = stream_of(rd)
+    call("face_radial_spline_fwd", ptr(rd), ptr(pd), E, ptr(Td), ptr(dTd), P, G, F, dr, None, F, None, ptr(S), F,
+         None, 0, st)
+    w = torch.randn(E, F, generator=gen)
+    gr = torch.empty(E, device=DEV)
+    call("face_radial_spline_bwd", ptr(rd), ptr(pd), E, ptr(Td), ptr(dTd), P, G, F, dr, None, F, None,
+         ptr(w.to(DEV)), F, None, 0, ptr(gr), None, st)
+    sp = RadialSpline(T.double(), dT.double(), dr)
+    rc = r.double().requires_grad_(True)
+    S2 = sp(rc, pair)
+    (gr2,) = torch.autograd.grad((S2 * w.double().view(N, M, F)).sum(), rc)
+    assert max(rel(S, S2.reshape(E, F)), rel(gr, gr2.reshape(-1))) < TOL
+
+
 def test_radial_spline_order_is_a_cell_sorted_permutation():
     """face_radial_spline_order: a permutation of the edges with non-decreasing table cell
     (pair * G + grid interval, the same cell the spline kernels use), including radii past the
