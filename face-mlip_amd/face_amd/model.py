@@ -122,7 +122,17 @@ def unit_parameterise(module):
 
 
 def _key(*ts):
-    return tuple((t._version, t.data_ptr(), t.device) for t in ts if t is not None)
+    """Cache key of tensors: the tensor objects, an alias of their storage, their in-place version
+    counters, data pointers and devices. The entry holds the objects and the storage aliases, so
+    neither an object nor a storage the key names can be freed and recycled for another tensor
+    while the entry lives; a parameter whose .data is swapped (module.to()) or changed in place
+    no longer matches."""
+    return tuple((t, t.detach(), t._version, t.data_ptr(), t.device) for t in ts if t is not None)
+
+
+def _same(a, b):
+    return a is not None and len(a) == len(b) and all(
+        x[0] is y[0] and x[2:] == y[2:] for x, y in zip(a, b))
 
 
 def frozen(mod):
@@ -133,7 +143,7 @@ def frozen(mod):
     w, b = mod.weight, mod.bias
     key = _key(w, b)
     c = mod.__dict__.get("_frozen")
-    if c is None or c[0] != key:
+    if c is None or not _same(c[0], key):
         with torch.no_grad():
             W = (w * mod.alpha) if isinstance(mod, UnitLinear) else w
             c = (key, W.detach(), None if b is None else b.detach())
@@ -292,7 +302,7 @@ class FactorBlock(nn.Module):
         w = self.elem_scale.weight
         key = _key(w, avg_nb)
         c = self.__dict__.get("_stab")
-        if c is None or c[0] != key:
+        if c is None or not _same(c[0], key):
             with torch.no_grad():
                 c = (key, (w / avg_nb).detach())
             self.__dict__["_stab"] = c
@@ -369,7 +379,7 @@ class FACE(nn.Module):
         self.register_buffer("scale", torch.tensor(1.0))
         self.register_buffer("avg_nb", torch.tensor(10.0))
         self.terms = nn.ModuleDict()
-        self._padded_cache = {}
+        self._padded_cache = None          # (topology tensors, their versions, CSR Graph)
 
     def fuse(self, on=True):
         """Kept for API compatibility (face/model.py:657-663): this path is always fused."""
@@ -391,13 +401,19 @@ class FACE(nn.Module):
         if "csr" in g:
             gr = g["csr"]
             return gr if gr.pos is g["pos"] else gr.with_pos(g["pos"])
-        key = (g["nbr"].data_ptr(), g["mask"].data_ptr(), g["shift"].data_ptr(), tuple(g["nbr"].shape))
-        gr = self._padded_cache.get(key)
-        if gr is None:
-            self._padded_cache.clear()
-            gr = graph_from_padded(g)
-            self._padded_cache[key] = gr
-        return gr.with_pos(g["pos"])
+        # The CSR graph of a padded dict is reused only for the very same topology tensors, unchanged
+        # since (identity and in-place version counter). The entry holds strong references to them,
+        # so a freed dict's storage cannot be handed to a new dict of the same shape while its graph
+        # is cached: a fresh dict on every call (the reference calculator's pattern,
+        # face/calculator.py:52) always rebuilds.
+        src = tuple(g[k] for k in ("nbr", "mask", "shift", "Z", "batch"))
+        ver = tuple(t._version for t in src) + (g.get("nstr"),)
+        c = self._padded_cache
+        if c is None or c[1] != ver or any(a is not b for a, b in zip(c[0], src)):
+            self._padded_cache = None                  # drop the old entry before building the new one
+            c = (src, ver, graph_from_padded(g))
+            self._padded_cache = c
+        return c[2].with_pos(g["pos"])
 
     def forward(self, g, forces=True, create_graph=False):
         if create_graph:
@@ -413,13 +429,15 @@ class FACE(nn.Module):
         Y, rb, env, r = ops.edge_geometry(pos, graph, self.basis.freq, self.rc, with_rb=not all(splines),
                                           with_r=any(splines))
         zidx = self.zmap[graph.Z]
-        zkey = ("zp", self.zmap.data_ptr(), len(self.E0))
-        zp = graph.cache.get(zkey)
-        if zp is None:
+        # element-pair row of every edge and element of every atom, cached on the graph per element
+        # map (the entry holds the map tensor itself, so its key cannot be recycled by another model)
+        zkey = ("zp", id(self.zmap), len(self.E0))
+        ent = graph.cache.get(zkey)
+        if ent is None or ent[0] is not self.zmap or ent[1] != self.zmap._version:
             zp = (zidx[graph.recv.long()] * len(self.E0) + zidx[graph.col.long()]).to(torch.int32)
-            graph.cache[zkey] = zp
-            graph.cache[zkey + ("atoms",)] = zidx.to(torch.int32)
-        zidx32 = graph.cache[zkey + ("atoms",)]
+            ent = (self.zmap, self.zmap._version, zp, zidx.to(torch.int32))
+            graph.cache[zkey] = ent
+        zp, zidx32 = ent[2], ent[3]
         h = F.embedding(zidx, self.embed.weight.detach())
         e_at = self.E0[zidx].clone()
         # table-cell edge order for large compiled tables: one sort per step, shared by the passes

@@ -234,9 +234,16 @@ def graph_from_padded(g):
     rev = torch.empty(E, **i32)
     missing = torch.zeros(1, **i32)
     call("face_nbr_rev_shift", ptr(row_ptr), ptr(col), ptr(sh), N, ptr(rev), ptr(missing), _lib.stream_of(sh))
-    if int(missing.item()) != 0:
-        raise RuntimeError("padded graph is not symmetric: the force scatter needs every reverse pair")
     batch = g["batch"]
+    # per-structure energies are sums over contiguous atom ranges (struct_ptr), so the atoms of
+    # each structure must be contiguous and in structure order: checked with the same host read
+    unsorted = (batch[1:] < batch[:-1]).sum().to(torch.int32).view(1) if N > 1 else torch.zeros_like(missing)
+    flags = torch.cat([missing, unsorted]).tolist()
+    if flags[0] != 0:
+        raise RuntimeError("padded graph is not symmetric: the force scatter needs every reverse pair")
+    if flags[1] != 0:
+        raise ValueError("padded graph: 'batch' must be non-decreasing (the atoms of each structure contiguous, "
+                         "structures in order)")
     nstr = int(g["nstr"]) if "nstr" in g else int(batch.max()) + 1
     sizes = torch.bincount(batch, minlength=nstr)
     struct_ptr = torch.zeros(nstr + 1, **i32)

@@ -52,8 +52,8 @@ def test_energy_forces_match_reference_golden(name):
     o = m(golden_graph(d))
     dE, dF = check(o["energy"].detach().cpu(), o["forces"].detach().cpu(), d["energy"], d["forces"])
     say(f"  dE/E {dE:.2e}  max|dF|/rms {dF:.2e}")
-    # the same structures through the GPU pair-list build give the same E/F
-    from face_amd.neighbors import graph_from_padded
+    # a second, freshly built dict of the same structures (its CSR graph built again): the same
+    # forces bit for bit (fixed summation order, no atomics)
     o2 = m(golden_graph(d))
     assert torch.equal(o["forces"], o2["forces"])               # bitwise reproducible
 
@@ -262,3 +262,99 @@ def test_graph_replay_matches_eager(case):
         torch.cuda.synchronize()
         assert torch.allclose(E1, o["energy"], rtol=1e-6, atol=0), (k, E1, o["energy"])
         assert (F1 - o["forces"]).abs().max() <= 1e-5 * o["forces"].abs().max(), k
+
+
+def _repad(g, M):
+    """A padded dict (oracle layout) widened to M slots: extra slots masked, pointing at the
+    structure's first atom with zero shift (face/neighbors.py:27-32), moved to the GPU."""
+    N, M0 = g["nbr"].shape
+    nbr = torch.empty(N, M, dtype=torch.long)
+    starts = torch.cat([torch.zeros(1, dtype=torch.long), torch.cumsum(torch.bincount(g["batch"]), 0)[:-1]])
+    first = starts[g["batch"]]
+    nbr[:] = first[:, None]
+    nbr[:, :M0] = g["nbr"]
+    sh = torch.zeros(N, M, 3)
+    sh[:, :M0] = g["shift"]
+    mk = torch.zeros(N, M, dtype=torch.bool)
+    mk[:, :M0] = g["mask"]
+    c = lambda t: t.to("cuda")
+    return {"pos": c(g["pos"]), "Z": c(g["Z"]), "nbr": c(nbr), "shift": c(sh), "mask": c(mk), "batch": c(g["batch"])}
+
+
+def _crossing_variant(sts, rc, rng):
+    """A copy of the structures in which one pair of molecule 0 moves from just inside rc to just
+    outside it, and one hydrogen becomes an oxygen."""
+    s2 = [dict(s, pos=s["pos"].copy(), Z=s["Z"].copy()) for s in sts]
+    p = s2[0]["pos"]
+    d = np.linalg.norm(p[:, None] - p[None], axis=-1)
+    i, j = np.argwhere((d > rc - 0.6) & (d < rc))[0]
+    u = (p[j] - p[i]) / d[i, j]
+    p[j] += (rc + 0.02 - d[i, j]) * u
+    h = np.nonzero(s2[1]["Z"] == 1)[0][0]
+    s2[1]["Z"][h] = 8
+    return s2
+
+
+def test_fresh_same_shape_padded_dicts_are_not_confused():
+    """The reference calculator builds a new padded dict on every call (face/calculator.py:52). Two
+    same-shape dicts built one after the other, the first freed in between, that differ in one pair
+    crossing rc and in one species, each match the oracle; then a short MD-like loop of fresh dicts
+    with moving atoms."""
+    from face_amd import systems
+    from oracle.neighbors import padded_graph as opad
+    say("fresh padded dicts")
+    kw = dict(C=32, transport=True, eqmsg=True, factor=True, B=16, K=32, rc=4.5)
+    el = [1, 6, 8]
+    rng = np.random.default_rng(21)
+    sts_a = systems.molecules(2, rng)
+    sts_b = _crossing_variant(sts_a, kw["rc"], rng)
+    ga, gb = opad(sts_a, kw["rc"]), opad(sts_b, kw["rc"])
+    M = max(ga["nbr"].shape[1], gb["nbr"].shape[1]) + 1
+    assert int(ga["mask"].sum()) != int(gb["mask"].sum())             # a pair crossed rc
+    m = product_model(kw, el)
+    da = _repad(ga, M)
+    oa = m(da)
+    check(oa["energy"].detach().cpu(), oa["forces"].detach().cpu(), *_oracle_EF(sts_a, kw, el))
+    shapes = {k: tuple(v.shape) for k, v in da.items()}
+    del da
+    db = _repad(gb, M)
+    assert {k: tuple(v.shape) for k, v in db.items()} == shapes
+    ob = m(db)
+    Eb, Fb = _oracle_EF(sts_b, kw, el)
+    dE, dF = check(ob["energy"].detach().cpu(), ob["forces"].detach().cpu(), Eb, Fb)
+    say(f"  second dict: dE/E {dE:.2e}  max|dF|/rms {dF:.2e}")
+    del db
+    # MD-like loop: fresh dict per step, atoms moving by up to 0.15 A per step
+    sts = sts_b
+    for step in range(4):
+        sts = [dict(s, pos=s["pos"] + rng.normal(0, 0.08, s["pos"].shape)) for s in sts]
+        gs = opad(sts, kw["rc"])
+        if gs["nbr"].shape[1] > M:
+            M = gs["nbr"].shape[1]
+        o = m(_repad(gs, M))
+        dE, dF = check(o["energy"].detach().cpu(), o["forces"].detach().cpu(), *_oracle_EF(sts, kw, el))
+        say(f"  step {step}: dE/E {dE:.2e}  max|dF|/rms {dF:.2e}")
+
+
+def test_padded_dict_changed_in_place_is_rebuilt():
+    """The same dict object with its topology edited in place (mask cleared for a pair and its
+    reverse): the graph is rebuilt (version counters), matching a fresh dict."""
+    from face_amd import systems
+    from oracle.neighbors import padded_graph as opad
+    say("in-place edited padded dict")
+    kw = dict(C=32, transport=True, eqmsg=True, factor=True, B=16, K=32, rc=4.5)
+    m = product_model(kw, [1, 6, 8])
+    sts = systems.molecules(2, np.random.default_rng(5))
+    g = opad(sts, kw["rc"])
+    d = _repad(g, g["nbr"].shape[1])
+    m(d)
+    mk = g["mask"].clone()
+    i, s = map(int, torch.nonzero(mk)[0])
+    j = int(g["nbr"][i, s])
+    mk[i, s] = False
+    s2 = int(torch.nonzero((g["nbr"][j] == i) & mk[j])[0])
+    mk[j, s2] = False
+    d["mask"].copy_(mk.cuda())
+    o1 = m(d)
+    o2 = m(dict(d, mask=d["mask"].clone()))
+    assert torch.equal(o1["forces"], o2["forces"])

@@ -371,3 +371,32 @@ def test_compiled_radial_model_matches_mlp_model_f64():
         F1, F2 = o1["forces"].detach(), o2["forces"].detach()
         assert (E1 - E2).abs().max() <= 1e-9 * E1.abs().max(), name
         assert (F1 - F2).abs().max() <= 1e-7 * F1.pow(2).mean().sqrt(), name
+
+
+def test_padded_layout_hand_worked_case():
+    """The padded-dense layout of face/neighbors.py:20-33 worked out by hand for a tiny batch:
+    rows sorted by receiver, slot = rank within the row, M = longest row of the batch, padding
+    slots pointing at the first atom of the atom's own structure with zero shift and mask False;
+    shift = S . cell (rows of cell = lattice vectors)."""
+    from oracle.neighbors import padded_graph
+    rc = 1.5
+    # structure 0: three atoms on a line 1 A apart (0-1 and 1-2 within rc, 0-2 at 2 A is not)
+    s0 = {"pos": np.array([[0.0, 0, 0], [1.0, 0, 0], [2.0, 0, 0]]), "Z": np.array([1, 6, 8]),
+          "cell": np.zeros((3, 3)), "pbc": np.zeros(3, bool)}
+    # structure 1: one atom in a box periodic along x only, a = 1.2 A: its own images at S = -1, +1
+    s1 = {"pos": np.array([[0.3, 0.4, 0.5]]), "Z": np.array([6]),
+          "cell": np.diag([1.2, 5.0, 5.0]), "pbc": np.array([True, False, False])}
+    # structure 2: two atoms 0.5 A apart, non-periodic
+    s2 = {"pos": np.array([[0.0, 0, 0], [0.0, 0.5, 0]]), "Z": np.array([1, 1]),
+          "cell": np.zeros((3, 3)), "pbc": np.zeros(3, bool)}
+    g = padded_graph([s0, s1, s2], rc, dtype=torch.float64)
+    nbr = np.array([[1, 0], [0, 2], [1, 0], [3, 3], [5, 4], [4, 4]])
+    mask = np.array([[1, 0], [1, 1], [1, 0], [1, 1], [1, 0], [1, 0]], bool)
+    shift = np.zeros((6, 2, 3))
+    shift[3, 0] = [-1.2, 0, 0]
+    shift[3, 1] = [1.2, 0, 0]
+    assert g["nbr"].tolist() == nbr.tolist()
+    assert g["mask"].tolist() == mask.tolist()
+    assert np.array_equal(g["shift"].numpy(), shift)
+    assert g["batch"].tolist() == [0, 0, 0, 1, 2, 2]
+    assert g["Z"].tolist() == [1, 6, 8, 6, 1, 1]
