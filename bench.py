@@ -1,20 +1,31 @@
 """Energy + forces throughput of the FACE hot path on one MI355X.
 
-python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload 3] [--also 2] [--compiled 2,3] [--no-cpu]
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload 3] [--also 0,1,2,4] [--compiled 2,3]
+                [--no-cpu] [--cpu-budget S]
 
 A step is one energy + forces evaluation of the whole synthetic system with its pair list
 already resident in HBM (the pair-list build is timed separately, as the reference excludes
-it from its timings). Workloads (face_amd.systems.workload):
+it from its timings, tools/bench.py:4). Workloads (face_amd.systems.workload):
   0  64 x C9H8O4 molecules, FACE C96 B16 K32 rc 4.5
   1  512 x C9H8O4 molecules, FACE-CP C160 rc 4.5
   2  FCC Ag 6x6x6 = 864 atoms, FACE C96 B16 K32 rc 4.5
   3  24,000-atom H:C:O liquid, FACE-CP C160 rc 5.0            (headline `value`)
   4  100,000-atom H:C:O liquid, FACE C256 B16 K64 rc 5.5
+Timing follows the reference's protocol (tools/bench_review.py:53-69): W warm-up steps, then
+rounds of 5 calls, each round bracketed by torch.cuda.synchronize(); ms/step is the median
+over the rounds (min and max reported beside it). K = 35 steps = 7 rounds by default.
 Prints ONE JSON line; progress goes to stderr.
+
+Profile summaries (text under profiles/) are written by the summary modes from rocprofv3 output:
+  --pmc-probe                       short eager run for `rocprofv3 --pmc` passes (one counter each)
+  --pmc-summary FETCH_DIR WRITE_DIR  HBM traffic per call label / kernel family from the two passes
+  --trace-summary STATS_CSV          kernel-time summary of a `rocprofv3 --kernel-trace --stats` run
 """
 import argparse
 import json
+import math
 import os
+import statistics
 import sys
 import time
 
@@ -28,19 +39,57 @@ import torch  # noqa: E402
 
 METRIC = "atom-steps/s (E+F, fp32) at 864 & 24k atoms; density-kernel HBM GB/s"
 HBM_PEAK_GBS = 8000.0
-TIMED = ["density_fwd20", "density_bwd20", "cp_fwd", "cp_fwd_tab", "cp_bwd", "cp_bwd_tab", "cp_radial_bwd",
-         "cp_radial_bwd_tab", "transport_fwd", "transport_bwd", "dir_fwd",
-         "dir_bwd", "node_fwd", "node_bwd", "edge_fwd", "edge_bwd", "force_scatter", "gather_bwd", "radial_fwd",
-         "radial_bwd", "radial_head", "edge_msg_fwd", "edge_msg_bwd", "mix_fwd", "mix_bwd", "tmix_bwd", "proj_fwd",
-         "proj_bwd", "eq_gate_fwd", "eq_gate_bwd", "ln_fwd", "ln_bwd", "spline_order",
-         "spline_fwd", "spline_bwd"]
 MFMA_PEAK_TFS = 157.3                   # MI355X dense fp32 MFMA
+CALLS_PER_ROUND = 5
+TAGS = {0: "mol64_c96", 1: "mol512_cp160", 2: "fcc864_c96", 3: "liquid24k_cp160", 4: "liquid100k_c256"}
+
+# call label -> kernel family (the kernel function the label's entry point launches; labels that
+# launch the same kernel are summed when the dominant kernel is chosen)
+KERNEL_FAMILY = {
+    "density_fwd20": "density_fwd", "density_bwd20": "density_bwd",
+    "cp_fwd": "cp_density_fwd", "cp_fwd_tab": "cp_density_fwd",
+    "cp_bwd": "cp_density_bwd", "cp_bwd_tab": "cp_density_bwd",
+    "cp_radial_bwd": "cp_radial_bwd", "cp_radial_bwd_tab": "cp_radial_bwd",
+    "transport_fwd": "transport_fwd", "transport_bwd": "transport_bwd",
+    "dir_fwd": "dir_feats_fwd", "dir_bwd": "dir_feats_bwd",
+    "node_fwd": "node_fwd", "node_bwd": "node_bwd",
+    "edge_fwd": "edge_geom_fwd", "edge_bwd": "edge_geom_bwd", "force_scatter": "force_scatter",
+    "gather_bwd": "gather_rows_bwd", "radial_fwd": "radial_fwd", "radial_bwd": "radial_bwd",
+    "radial_head": "edge_linear_fwd", "edge_msg_fwd": "edge_linear_fwd", "edge_msg_bwd": "edge_linear_bwd",
+    "mix_fwd": "rows_gemm", "mix_bwd": "rows_gemm", "tmix_bwd": "rows_gemm", "proj_fwd": "rows_gemm",
+    "proj_bwd": "rows_gemm", "eq_gate_fwd": "eq_gate_fwd", "eq_gate_bwd": "eq_gate_bwd",
+    "ln_fwd": "layer_norm_fwd", "ln_bwd": "layer_norm_bwd", "spline_order": "spline_order",
+    "spline_fwd": "radial_spline_fwd", "spline_bwd": "radial_spline_bwd",
+}
+# kernel family -> kernel functions of libface_hip.so it stands for (rocprofv3 names, namespace face)
+FAMILY_KERNELS = {
+    "density_fwd": ["density_fwd_mfma_kernel", "density_fwd_kernel"],
+    "density_bwd": ["density_bwd_mfma_kernel", "density_bwd_kernel"],
+    "cp_density_fwd": ["cp_density_fwd_wave_kernel", "cp_density_fwd_kernel"],
+    "cp_density_bwd": ["cp_density_bwd_mfma_kernel", "cp_density_bwd_kernel"],
+    "cp_radial_bwd": ["cp_radial_bwd_res_kernel", "cp_radial_bwd_lds_kernel"],
+    "transport_fwd": ["transport_fwd_kernel"],
+    "transport_bwd": ["transport_bwd_mfma_kernel", "transport_bwd_kernel", "transport_table_grad_kernel"],
+    "dir_feats_fwd": ["dir_feats_fwd_kernel"], "dir_feats_bwd": ["dir_feats_bwd_edge_kernel",
+                                                                 "dir_feats_bwd_node_kernel"],
+    "node_fwd": ["node_fwd_kernel"], "node_bwd": ["node_bwd_kernel"],
+    "edge_geom_fwd": ["edge_geom_fwd_kernel"], "edge_geom_bwd": ["edge_geom_bwd_kernel"],
+    "force_scatter": ["force_scatter_kernel"], "gather_rows_bwd": ["gather_rows_bwd_kernel"],
+    "radial_fwd": ["radial_fwd_kernel"], "radial_bwd": ["radial_bwd_kernel"],
+    "edge_linear_fwd": ["edge_linear_fwd_kernel"], "edge_linear_bwd": ["edge_linear_bwd_kernel"],
+    "rows_gemm": ["rows_gemm_kernel"], "eq_gate_fwd": ["eq_gate_fwd_kernel"], "eq_gate_bwd": ["eq_gate_bwd_kernel"],
+    "layer_norm_fwd": ["layer_norm_fwd_kernel"], "layer_norm_bwd": ["layer_norm_bwd_kernel"],
+    "spline_order": ["spline_zero_kernel", "spline_count_kernel", "spline_scan_kernel", "spline_place_kernel"],
+    "radial_spline_fwd": ["radial_spline_fwd_kernel"], "radial_spline_bwd": ["radial_spline_bwd_kernel"],
+}
+TIMED = list(KERNEL_FAMILY)
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+# ----------------------------------------------------------------------------- algorithmic figures
 def algorithmic_bytes(label, g, kw):
     """Bytes per launch: every operand of the kernel's interface read once, every output written
     once, fp32 / int32 (valid pairs E only)."""
@@ -70,7 +119,7 @@ def algorithmic_bytes(label, g, kw):
         return 4 * E * (11 + 29 + 3)
     if label == "force_scatter":
         return 4 * (3 * E + E + 3 * N)
-    if label.startswith("spline_"):     # r, pair, env in, F columns out (in); both tables read once
+    if label.startswith("spline_") and label != "spline_order":   # r, pair, env in, F columns out; tables once
         F = kw.get("B", 16) + (4 * C if kw.get("cp") else 0)
         n_el = kw.get("n_elem", 3)
         tables = 8 * n_el * n_el * kw.get("n_grid", 4096) * F
@@ -87,6 +136,14 @@ def algorithmic_bytes(label, g, kw):
         return 4 * (E * (Kd4 + 1 + K) + N * K)
     if label == "edge_msg_bwd":         # upstream (E, K), rev in; d d (E, 4Kd) and the table gradient out
         return 4 * (E * (K + 1 + Kd4) + N * K)
+    if label == "eq_gate_fwd":          # V (3), Ms (6), gate row (2) in; Vo, Mo (9) out per (atom, channel)
+        return 4 * 20 * N * C
+    if label == "eq_gate_bwd":          # + upstream (9); dV, dMs (9), gate-row gradient (2) out
+        return 4 * 31 * N * C
+    if label == "ln_fwd":               # row of 9C in and out (+ mean, rstd)
+        return 4 * (2 * 9 * C + 2) * N
+    if label == "ln_bwd":
+        return 4 * (3 * 9 * C + 2) * N
     return None
 
 
@@ -111,11 +168,14 @@ def interface_bytes(label, g, kw):
 def algorithmic_flops(label, g, kw):
     """Matrix-product flops per launch: the row GEMMs (the four ranks, 20 monomial rows per atom,
     of one mix pass or of one moment set of the proj: output widths C, 3C, 3C, 2C), the radial
-    head (E x H by H x 4C), and the fused CP radial backward (d h2 = dR W_cp, E x 4C by 4C x H,
-    plus the two 20-monomial contractions per edge and channel)."""
+    head (E x H by H x 4C), the pass message's d W_d^T (E x 4Kd by 4Kd x K) and its input
+    gradient, the fused CP radial backward (d h2 = dR W_cp, E x 4C by 4C x H, plus the two
+    20-monomial contractions per edge and channel), and the factor density's per-monomial
+    products (2 E 20 B K each way; 3 of them in the backward)."""
     N, E, C = g.N, g.E, kw["C"]
     H = kw.get("radial_hidden", 64)
     cin = C if kw.get("cp") else kw["B"] * kw["K"]
+    K = C if kw.get("cp") else kw["K"]
     if label in ("mix_fwd", "mix_bwd"):
         return 2 * 20 * N * cin * C
     if label in ("proj_fwd", "proj_bwd"):
@@ -124,17 +184,121 @@ def algorithmic_flops(label, g, kw):
         return 2 * 9 * N * C * kw["B"] * 2 * kw["K_dir"]
     if label == "radial_head":
         return 2 * E * H * 4 * C
+    if label in ("edge_msg_fwd", "edge_msg_bwd"):
+        return 2 * E * 4 * kw["K_dir"] * K
     if label.startswith("cp_radial_bwd"):
         return 2 * E * (4 * C * H + 2 * 20 * C)
+    if label == "density_fwd20":
+        return 2 * E * 20 * kw["B"] * kw["K"]
+    if label == "density_bwd20":
+        return 3 * 2 * E * 20 * kw["B"] * kw["K"]
     return None
 
 
+def floor_us(byts, fl):
+    """(time floor in us, binding bound) of one launch: bytes at peak HBM, flops at the fp32 MFMA peak."""
+    t_hbm = (byts or 0) / (HBM_PEAK_GBS * 1e9) * 1e6
+    t_mfma = (fl or 0) / (MFMA_PEAK_TFS * 1e12) * 1e6
+    return (t_mfma, "mfma") if t_mfma > t_hbm else (t_hbm, "hbm")
+
+
+# ----------------------------------------------------------------------------- GPU runs
 def model_for(kw, el):
     from face_amd import model as fm
     torch.manual_seed(0)
     m = fm.FACE(el, **kw)
     fm.unit_parameterise(m)
     return m.cuda().eval()
+
+
+def timed_rounds(fn, steps, calls=CALLS_PER_ROUND):
+    """Per-step seconds of each round of `calls` calls (the last round shorter when steps is not a
+    multiple), every round bracketed by torch.cuda.synchronize()."""
+    out, left = [], steps
+    while left > 0:
+        c = min(calls, left)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(c):
+            fn()
+        torch.cuda.synchronize()
+        out.append((time.perf_counter() - t0) / c)
+        left -= c
+    return out
+
+
+def label_stats(timers, steps, g, kw):
+    kern = {}
+    for label, evs in timers.items():
+        if not evs:
+            continue
+        ms = [s.elapsed_time(e) for s, e in evs]
+        avg_us = 1e3 * float(np.mean(ms))
+        byts = algorithmic_bytes(label, g, kw)
+        fl = algorithmic_flops(label, g, kw)
+        ib = interface_bytes(label, g, kw)
+        fus, bound = floor_us(byts, fl)
+        kern[label] = {"family": KERNEL_FAMILY.get(label), "launches_per_step": len(evs) / steps, "avg_us": avg_us,
+                       "ms_per_step": float(np.sum(ms)) / steps, "alg_bytes": byts, "alg_flops": fl,
+                       "GBps": (byts / (avg_us * 1e-6) / 1e9) if byts else None,
+                       "GBps_interface": (ib / (avg_us * 1e-6) / 1e9) if ib else None,
+                       "TFLOPs": (fl / (avg_us * 1e-6) / 1e12) if fl else None,
+                       "bound": bound if (byts or fl) else None,
+                       "frac": (fus / avg_us) if (byts or fl) else None}
+    return kern
+
+
+def family_stats(kern):
+    """Per kernel family: launches, time, algorithmic bytes / flops per launch, and the roofline
+    fraction = sum of the launches' floors / their measured time."""
+    fam = {}
+    for label, v in kern.items():
+        f = fam.setdefault(v["family"] or label, {"labels": [], "launches_per_step": 0.0, "ms_per_step": 0.0,
+                                                  "bytes_per_step": 0.0, "flops_per_step": 0.0,
+                                                  "floor_ms_per_step": 0.0, "floor_hbm": 0.0, "floor_mfma": 0.0,
+                                                  "known": False})
+        f["labels"].append(label)
+        n = v["launches_per_step"]
+        f["launches_per_step"] += n
+        f["ms_per_step"] += v["ms_per_step"]
+        f["bytes_per_step"] += n * (v["alg_bytes"] or 0)
+        f["flops_per_step"] += n * (v["alg_flops"] or 0)
+        if v["alg_bytes"] or v["alg_flops"]:
+            fus, bound = floor_us(v["alg_bytes"], v["alg_flops"])
+            f["floor_ms_per_step"] += n * fus * 1e-3
+            f["floor_" + bound] += n * fus * 1e-3
+            f["known"] = True
+    for k, f in fam.items():
+        n = f["launches_per_step"]
+        f["avg_us"] = 1e3 * f["ms_per_step"] / n
+        f["alg_bytes_per_launch"] = f["bytes_per_step"] / n if f["bytes_per_step"] else None
+        f["alg_flops_per_launch"] = f["flops_per_step"] / n if f["flops_per_step"] else None
+        f["frac"] = f["floor_ms_per_step"] / f["ms_per_step"] if f["known"] else None
+        f["bound"] = ("mfma" if f["floor_mfma"] > f["floor_hbm"] else "hbm") if f["known"] else None
+        f["kernels"] = FAMILY_KERNELS.get(k, [k])
+    return fam
+
+
+def roofline_of(fam, tag):
+    """The roofline object of the kernel family with the largest time per step (families without
+    an algorithmic figure are skipped): achieved = frac x peak of its binding bound."""
+    known = {k: v for k, v in fam.items() if v["known"]}
+    if not known:
+        return None
+    dom = max(known, key=lambda k: known[k]["ms_per_step"])
+    v = known[dom]
+    if v["bound"] == "mfma":
+        peak, unit = MFMA_PEAK_TFS, "TFLOP/s"
+    else:
+        peak, unit = HBM_PEAK_GBS, "GB/s"
+    return {"kernel": dom, "kernels": v["kernels"], "labels": v["labels"], "bound": v["bound"],
+            "achieved": v["frac"] * peak, "peak": peak, "unit": unit, "frac": v["frac"],
+            "traffic": measured_traffic(tag, v["labels"]),
+            "alg_bytes_per_launch": v["alg_bytes_per_launch"], "alg_flops_per_launch": v["alg_flops_per_launch"],
+            "avg_launch_us": v["avg_us"], "launches_per_step": v["launches_per_step"],
+            "GBps": (v["alg_bytes_per_launch"] / (v["avg_us"] * 1e-6) / 1e9) if v["alg_bytes_per_launch"] else None,
+            "TFLOPs": (v["alg_flops_per_launch"] / (v["avg_us"] * 1e-6) / 1e12) if v["alg_flops_per_launch"]
+            else None}
 
 
 def run_gpu(k, steps, warmup, use_graph=True, compiled_radial=False):
@@ -163,67 +327,101 @@ def run_gpu(k, steps, warmup, use_graph=True, compiled_radial=False):
     torch.cuda.synchronize()
     log(f"[bench]   warm-up done ({warmup} steps)")
     torch.cuda.reset_peak_memory_stats()
-    # eager pass: HIP events around every hot-kernel launch (kernel durations)
+    # eager steps with HIP events around every hot-kernel launch (kernel durations), recorded on
+    # torch's current stream, the stream every entry point launches on
     timers = _lib.time_calls(TIMED)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        step()
-    torch.cuda.synchronize()
-    dt_eager = time.perf_counter() - t0
+    eager = timed_rounds(step, steps)
     _lib.stop_timing()
     peak_gb = torch.cuda.max_memory_allocated() / 1e9
-    log(f"[bench]   eager: {1e3 * dt_eager / steps:.3f} ms/step, peak device memory {peak_gb:.2f} GB")
-    dt = dt_eager
-    mode = "eager"
+    log(f"[bench]   eager (instrumented): {1e3 * statistics.median(eager):.3f} ms/step, peak device memory "
+        f"{peak_gb:.2f} GB")
+    rounds, mode, nodes = eager, "eager", None
     if use_graph:
         # HIP-graph replay of the whole E+F step, positions copied into the static input
         from face_amd.runner import StepGraph
         run = StepGraph(m, g)
+        nodes = run.node_counts()
         pos = g.pos.clone()
         for _ in range(warmup):
             run(pos)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            run(pos)
-        torch.cuda.synchronize()
-        dt = time.perf_counter() - t0
+        rounds = timed_rounds(lambda: run(pos), steps)
         mode = "hipgraph"
-        log(f"[bench]   graph replay: {1e3 * dt / steps:.3f} ms/step")
         del run
-    kern = {}
-    for label, evs in timers.items():
-        if not evs:
-            continue
-        ms = [s.elapsed_time(e) for s, e in evs]
-        avg_us = 1e3 * float(np.mean(ms))
-        byts = algorithmic_bytes(label, g, kw)
-        fl = algorithmic_flops(label, g, kw)
-        ib = interface_bytes(label, g, kw)
-        kern[label] = {"launches_per_step": len(evs) / steps, "avg_us": avg_us,
-                       "ms_per_step": float(np.sum(ms)) / steps,
-                       "alg_bytes": byts, "alg_flops": fl, "GBps": (byts / (avg_us * 1e-6) / 1e9) if byts else None,
-                       "GBps_interface": (ib / (avg_us * 1e-6) / 1e9) if ib else None,
-                       "TFLOPs": (fl / (avg_us * 1e-6) / 1e12) if fl else None}
-    ms_step = 1e3 * dt / steps
-    log(f"[bench]   {ms_step:.3f} ms/step, {g.N * steps / dt:.0f} atom-steps/s")
-    return {"N": g.N, "E": g.E, "ms_per_step": ms_step, "atom_steps_per_s": g.N * steps / dt, "kernels": kern,
-            "pairlist_ms": 1e3 * t_nbr, "desc": desc, "kw": kw, "mode": mode,
-            "eager_ms_per_step": 1e3 * dt_eager / steps, "peak_mem_gb": peak_gb}
+    ms = [1e3 * x for x in rounds]
+    ms_step = statistics.median(ms)
+    log(f"[bench]   {mode}: {ms_step:.3f} ms/step (median of {len(ms)} rounds; {min(ms):.3f}-{max(ms):.3f}), "
+        f"{g.N / ms_step * 1e3:.0f} atom-steps/s; graph nodes {nodes}")
+    kern = label_stats(timers, steps, g, kw)
+    fam = family_stats(kern)
+    tag = TAGS[k] + ("_compiled" if compiled_radial else "")
+    out = {"N": g.N, "E": g.E, "max_row": g.max_row, "ms_per_step": ms_step, "ms_min": min(ms), "ms_max": max(ms),
+           "rounds": len(ms), "atom_steps_per_s": g.N / ms_step * 1e3, "kernels": kern, "families": fam,
+           "roofline": roofline_of(fam, tag), "pairlist_ms": 1e3 * t_nbr, "desc": desc, "kw": kw, "mode": mode,
+           "graph_nodes": nodes, "eager_ms_per_step": 1e3 * statistics.median(eager), "peak_mem_gb": peak_gb}
+    del m, g
+    torch.cuda.empty_cache()
+    return out
 
 
+# ----------------------------------------------------------------------------- CPU baseline
+# CPU samples of the default run: None = the whole system, otherwise the atom count of a sample of
+# the same recipe. The whole 100,000-atom C256 K64 box is not run: the unfused torch path
+# materialises phi (x) msg of 100,000 x 101 x 1024 floats (41 GB) plus its autograd buffers and one
+# call takes minutes; a 10,000-atom box of the same recipe stands for it (reported per atom).
+# --cpu-full runs it whole.
+CPU_SAMPLE = {0: None, 1: None, 2: None, 3: None, 4: 10000}
+
+
+def run_cpu(k, budget_s=10.0, full=False):
+    """The CPU oracle (the pure-torch restatement of the reference's torch path, unfused density
+    bmm and broadcast node algebra, autograd forces) on the workload's system or a bounded
+    sample of it: one warm-up call, then as many single-call rounds as fit the budget (2..7),
+    median reported. The padded pair list comes from the GPU build (bit-exact with the oracle's
+    pair list); like the reference's timings it is outside the timed region."""
+    from face_amd import systems
+    from face_amd.neighbors import build_graph, padded_view
+    from oracle import model as om
+    cores = min(16, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(cores)
+    n_atoms = None if full else CPU_SAMPLE.get(k)
+    sts, kw, el, desc = systems.workload(k, n_atoms=n_atoms)
+    g = build_graph(sts, kw["rc"])
+    nbr, sh, mask = padded_view(g)
+    gg = {"pos": g.pos.cpu(), "Z": g.Z.cpu(), "nbr": nbr.cpu(), "shift": sh.cpu(), "mask": mask.cpu(),
+          "batch": g.batch.cpu()}
+    N = g.N
+    del g, nbr, sh, mask
+    torch.manual_seed(0)
+    m = om.unit_parameterise(om.FACE(el, **kw)).eval()
+
+    def call():
+        t0 = time.perf_counter()
+        m(dict(gg, pos=gg["pos"].clone()))
+        return time.perf_counter() - t0
+
+    t_warm = call()
+    rounds = int(max(2, min(7, budget_s // max(t_warm, 1e-3))))
+    ts = [call() for _ in range(rounds)]
+    med = statistics.median(ts)
+    what = "the whole system" if n_atoms is None else f"a {N}-atom sample of the same recipe"
+    return {"value": N / med, "unit": "atom-steps/s", "cores": cores, "kind": "port",
+            "ms_per_step": 1e3 * med, "ms_min": 1e3 * min(ts), "ms_max": 1e3 * max(ts),
+            "sample": f"{what} ({N} atoms, {desc.split(',')[-1].strip()}), oracle torch path (unfused, as the "
+                      f"reference's torch path), fp32, median of {rounds} single E+F calls after 1 warm-up "
+                      f"({t_warm:.1f} s), torch.set_num_threads({cores})"}
+
+
+# ----------------------------------------------------------------------------- profiler helpers
 def pmc_probe(k, steps=2, copy_floats=1 << 28):
     """Short run for hardware-counter passes: a few eager E+F steps of workload k, then a plain
     device-to-device copy of a known size, whose FETCH_SIZE / WRITE_SIZE readings calibrate the
     counters (bytes known / counter reading). The JSON line lists the library calls in launch
     order, which assigns the profiler's dispatches to call labels."""
-    from face_amd import systems
+    from face_amd import _lib, systems
     from face_amd.neighbors import build_graph
     sts, kw, el, desc = systems.workload(k)
     g = build_graph(sts, kw["rc"])
     m = model_for(kw, el)
-    from face_amd import _lib
     order = _lib.record_order(True)
     for _ in range(steps):
         m(g.with_pos(g.pos.clone()))["forces"]
@@ -234,72 +432,205 @@ def pmc_probe(k, steps=2, copy_floats=1 << 28):
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
-    out = {"probe": desc, "steps": steps, "copy_bytes_read": 4 * copy_floats, "copy_bytes_written": 4 * copy_floats,
+    out = {"probe": desc, "workload": k, "steps": steps, "copy_bytes_read": 4 * copy_floats,
+           "copy_bytes_written": 4 * copy_floats,
            "alg_bytes": {lab: algorithmic_bytes(lab, g, kw) for lab in TIMED},
            "interface_bytes": {lab: interface_bytes(lab, g, kw) for lab in TIMED},
            "alg_flops": {lab: algorithmic_flops(lab, g, kw) for lab in TIMED}, "order": order}
     print(json.dumps(out), flush=True)
 
 
-def measured_traffic(label):
-    """HBM bytes per launch of a labelled kernel from the committed counter summary, or None."""
-    path = os.path.join(REPO, "profiles", "traffic_liquid24k_cp160.md")
+def _kernel_base(name):
+    """Kernel function name of a profiler kernel name ("void face::foo<...>(...)" -> "foo")."""
+    n = name.replace("void ", "")
+    if "face::" in n:
+        n = n.split("face::", 1)[1]
+    for stop in "<( ":
+        n = n.split(stop, 1)[0]
+    return n
+
+
+def pmc_summary(fetch_dir, write_dir, probe_log, out_path):
+    """HBM traffic per call label and per kernel family from two `rocprofv3 --pmc` passes over
+    `bench.py --pmc-probe` (FETCH_SIZE, WRITE_SIZE; counter CSVs in the two directories), scaled by
+    what the same counters read for the probe's 1 GiB device copy. Writes a markdown summary."""
+    import collections
+    import csv
+    import glob
+    rows = {}
+    for C, d in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        f = sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True))
+        if not f:
+            sys.exit(f"no counter_collection.csv under {d}")
+        rows[C] = sorted(csv.DictReader(open(f[0])), key=lambda r: int(r["Dispatch_Id"]))
+    probe = [json.loads(x) for x in open(probe_log) if x.startswith('{"probe"')][0]
+    cb = probe["copy_bytes_read"]
+    scale = {}
+    for C in rows:
+        cp = sorted((r for r in rows[C] if "copyBuffer" in r["Kernel_Name"]), key=lambda r: -float(r["Counter_Value"]))
+        scale[C] = cb / (1024 * sum(float(r["Counter_Value"]) for r in cp[:3]) / 3)
+    by_base = collections.defaultdict(list)
+    for lab, fam in KERNEL_FAMILY.items():
+        for kname in FAMILY_KERNELS[fam]:
+            by_base[kname].append(lab)
+    order = probe["order"]
+    seq = {b: [lab for lab in order if lab in labs] for b, labs in by_base.items()}
+    acc = {C: collections.defaultdict(float) for C in rows}
+    names = collections.defaultdict(set)
+    calls = collections.Counter(lab for lab in order)
+    for C, rs in rows.items():
+        pos = collections.Counter()
+        for r in rs:
+            if "face::" not in r["Kernel_Name"]:
+                continue
+            b = _kernel_base(r["Kernel_Name"])
+            if b not in seq or not seq[b]:
+                continue
+            i = pos[b]
+            pos[b] += 1
+            if i >= len(seq[b]):
+                sys.exit(f"{C}: more dispatches of {b} than calls that launch it")
+            acc[C][seq[b][i]] += float(r["Counter_Value"])
+            names[seq[b][i]].add(r["Kernel_Name"].replace("void ", "").split("(")[0].replace("face::", ""))
+    k = probe.get("workload", 3)
+    out = [f"# HBM traffic per launch: {probe['probe']}\n\n",
+           "Commands (repo root, MI355X, ROCm 7.2), one counter per pass, then the summary:\n\n```\n"]
+    for C in ("FETCH_SIZE", "WRITE_SIZE"):
+        out.append(f"rocprofv3 --pmc {C} --kernel-include-regex 'face::|copy' --output-format csv "
+                   f"-d gpurun_out/pmc_{C}_w{k} -o p -- python -u bench.py --pmc-probe --workload {k} "
+                   f"> gpurun_out/pmc_{C}_w{k}.log\n")
+    out.append(f"python bench.py --pmc-summary gpurun_out/pmc_FETCH_SIZE_w{k} gpurun_out/pmc_WRITE_SIZE_w{k} "
+               f"gpurun_out/pmc_FETCH_SIZE_w{k}.log {out_path}\n```\n\n")
+    out.append("`bench.py --pmc-probe` runs 2 eager E+F steps, then three device-to-device copies of 1 GiB; "
+               "its JSON line lists the library calls in launch order, which "
+               "assigns each dispatch of a kernel shared by several call labels to its label.\n\n")
+    out.append(f"Calibration on the 1 GiB copy: bytes = FETCH_SIZE x 1024 x {scale['FETCH_SIZE']:.4f} and "
+               f"WRITE_SIZE x 1024 x {scale['WRITE_SIZE']:.4f}.\n\n")
+    out.append("traffic = scaled FETCH + scaled WRITE per call (kernels of one call summed); alg = algorithmic "
+               "bytes of the label (operands of the drop-in read once, outputs written once).\n\n")
+    out.append("| label | family | kernels | calls | traffic bytes/call | alg bytes/call | traffic/alg |\n"
+               "|---|---|---|---:|---:|---:|---:|\n")
+    tracked = [lab for lab in KERNEL_FAMILY if calls.get(lab)]
+    fam_t = collections.defaultdict(lambda: [0.0, 0.0, 0])
+    for lab in tracked:
+        n = calls[lab]
+        t = (acc["FETCH_SIZE"][lab] * 1024 * scale["FETCH_SIZE"] + acc["WRITE_SIZE"][lab] * 1024 *
+             scale["WRITE_SIZE"]) / n
+        alg = probe["alg_bytes"].get(lab)
+        fam = KERNEL_FAMILY[lab]
+        fam_t[fam][0] += t * n
+        fam_t[fam][1] += (alg or 0) * n
+        fam_t[fam][2] += n
+        out.append(f"| {lab} | {fam} | {' + '.join(sorted(names[lab])) or '-'} | {n} | {t:.0f} | "
+                   f"{alg if alg else '-'} | {f'{t / alg:.3f}' if alg else '-'} |\n")
+    out.append("\nPer kernel family (the bench's roofline unit):\n\n| family | calls | traffic bytes/launch | "
+               "alg bytes/launch | traffic/alg |\n|---|---:|---:|---:|---:|\n")
+    for fam, (t, a, n) in fam_t.items():
+        out.append(f"| {fam} | {n} | {t / n:.0f} | {a / n if a else '-'} | {f'{t / a:.3f}' if a else '-'} |\n")
+    open(out_path, "w").write("".join(out))
+    print("".join(out))
+
+
+def measured_traffic(tag, labels):
+    """HBM bytes per launch of a kernel family (its labels' calls) from the committed counter
+    summary of the workload (profiles/traffic_<tag>.md), or None."""
+    path = os.path.join(REPO, "profiles", f"traffic_{tag}.md")
     if not os.path.exists(path):
         return None
+    tot = n = 0.0
     for line in open(path):
         parts = [x.strip() for x in line.strip().strip("|").split("|")]
-        if len(parts) >= 6 and parts[0] == label:
+        if len(parts) == 7 and parts[0] in labels:
             try:
-                return float(parts[5])
+                tot += float(parts[4]) * int(parts[3])
+                n += int(parts[3])
             except ValueError:
                 return None
-    return None
+    return tot / n if n else None
 
 
-def run_cpu(k, n_atoms, rounds=5, warm=2):
-    """The CPU oracle (pure-torch restatement of the reference path) on a bounded sample."""
-    from face_amd import systems
-    from oracle import model as om
-    from oracle.neighbors import padded_graph as opad
-    cores = min(16, len(os.sched_getaffinity(0)))
-    torch.set_num_threads(cores)
-    sts, kw, el, desc = systems.workload(k, n_atoms=n_atoms)
-    if n_atoms and k in (0, 1):
-        sts = sts[:max(1, n_atoms // 21)]
-    torch.manual_seed(0)
-    m = om.unit_parameterise(om.FACE(el, **kw)).eval()
-    g = opad(sts, kw["rc"])
-    gg = {kk: g[kk] for kk in ("pos", "Z", "nbr", "shift", "mask", "batch")}
-    N = gg["pos"].shape[0]
-    for _ in range(warm):
-        m(dict(gg, pos=gg["pos"].clone()))
-    t0 = time.perf_counter()
-    for _ in range(rounds):
-        m(dict(gg, pos=gg["pos"].clone()))
-    dt = time.perf_counter() - t0
-    return {"value": N * rounds / dt, "unit": "atom-steps/s", "cores": cores, "kind": "port",
-            "sample": f"{N}-atom sample of the same recipe and model ({desc.split(',')[-1].strip()}), "
-                      f"oracle torch path, {rounds} timed E+F calls after {warm} warm-ups, "
-                      f"torch.set_num_threads({cores})"}
+def trace_summary(stats_csv, bench_log, out_path, title):
+    """Kernel-time summary of a `rocprofv3 --kernel-trace --stats` run of bench.py (its kernel
+    stats CSV and the run's JSON line): the kernel families of the library with their trace
+    averages, then the top kernels."""
+    import csv
+    rows = list(csv.DictReader(open(stats_csv)))
+    d = [json.loads(x) for x in open(bench_log) if x.startswith('{"metric"')][0]
+    tot = sum(float(r["TotalDurationNs"]) for r in rows)
+    base_fam = {kn: fam for fam, kns in FAMILY_KERNELS.items() for kn in kns}
+    out = [f"# Kernel-time summary: {title}\n\nCommand (repo root, MI355X, ROCm 7.2):\n\n```\n"
+           f"rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof -o bench -- python -u bench.py "
+           f"{d.get('_argv', '')}\npython bench.py --trace-summary {stats_csv} <bench stdout> {out_path}\n```\n\n"]
+    out.append(f"Bench line of the same run: value {d['value']:.0f} atom-steps/s, {d['ms_per_step']:.3f} ms/step "
+               f"({d['config']['workload']}).\n\n")
+    r = d.get("roofline")
+    if r:
+        out.append(f"Bench roofline kernel family `{r['kernel']}` ({', '.join(r['labels'])}): HIP-event average "
+                   f"{r['avg_launch_us']:.1f} us/launch, {r['achieved']:.1f} {r['unit']} of {r['peak']} "
+                   f"({100 * r['frac']:.1f} %).\n\n")
+    out.append("Library kernel families in the trace (all workloads of the run, warm-up, eager and replayed "
+               "steps; sizes differ between workloads, so averages mix them):\n\n"
+               "| family | calls | total ms | avg us |\n|---|---:|---:|---:|\n")
+    fam = {}
+    for x in rows:
+        b = _kernel_base(x["Name"])
+        if "face::" in x["Name"] and b in base_fam:
+            f = fam.setdefault(base_fam[b], [0, 0.0])
+            f[0] += int(x["Calls"])
+            f[1] += float(x["TotalDurationNs"])
+    for f, (c, t) in sorted(fam.items(), key=lambda kv: -kv[1][1]):
+        out.append(f"| {f} | {c} | {t / 1e6:.2f} | {t / c / 1e3:.1f} |\n")
+    out.append(f"\nAll kernels of the run: {tot / 1e6:.1f} ms total. Top 30:\n\n"
+               "| total ms | calls | avg us | % | kernel |\n|---:|---:|---:|---:|---|\n")
+    for x in sorted(rows, key=lambda r: -float(r["TotalDurationNs"]))[:30]:
+        nm = x["Name"].replace("|", "/")[:110]
+        out.append(f"| {float(x['TotalDurationNs']) / 1e6:.2f} | {x['Calls']} | {float(x['AverageNs']) / 1e3:.1f} | "
+                   f"{float(x['Percentage']):.1f} | `{nm}` |\n")
+    open(out_path, "w").write("".join(out))
+    print("".join(out)[:3000])
+
+
+# ----------------------------------------------------------------------------- main
+def workload_record(r, cpu=None):
+    return {"desc": r["desc"], "atoms": r["N"], "pairs": r["E"], "max_row": r["max_row"],
+            "atom_steps_per_s": r["atom_steps_per_s"], "ms_per_step": r["ms_per_step"], "ms_min": r["ms_min"],
+            "ms_max": r["ms_max"], "rounds": r["rounds"], "pairlist_ms": r["pairlist_ms"], "mode": r["mode"],
+            "eager_ms_per_step": r["eager_ms_per_step"], "peak_mem_gb": r["peak_mem_gb"],
+            "graph_nodes": r["graph_nodes"], "roofline": r["roofline"], "cpu_baseline": cpu,
+            "kernels": {k: {"avg_us": v["avg_us"], "launches_per_step": v["launches_per_step"], "GBps": v["GBps"],
+                            "TFLOPs": v["TFLOPs"], "bound": v["bound"], "frac": v["frac"]}
+                        for k, v in r["kernels"].items()},
+            "families": {k: {"ms_per_step": v["ms_per_step"], "launches_per_step": v["launches_per_step"],
+                             "avg_us": v["avg_us"], "bound": v["bound"], "frac": v["frac"]}
+                         for k, v in r["families"].items()}}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=35, help="timed steps (rounds of 5 calls)")
+    ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", type=int, default=3)
-    ap.add_argument("--also", default="2", help="comma list of extra workloads reported under 'also'")
+    ap.add_argument("--also", default="0,1,2,4", help="comma list of extra workloads reported under 'also'")
     ap.add_argument("--compiled", default="2,3",
                     help="comma list of workloads also run with compile_radial() (the reference calculator's "
                          "CUDA setting), reported under 'also'")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-atoms", type=int, default=1500)
+    ap.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of timed CPU calls per workload")
+    ap.add_argument("--cpu-full", action="store_true", help="CPU baselines on the whole systems (slow)")
     ap.add_argument("--eager", action="store_true", help="time eager steps instead of HIP-graph replays")
     ap.add_argument("--pmc-probe", action="store_true", help="short run for rocprofv3 --pmc passes")
+    ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "PROBE_LOG", "OUT"))
+    ap.add_argument("--trace-summary", nargs=4, metavar=("STATS_CSV", "BENCH_LOG", "OUT", "TITLE"))
     ap.add_argument("--no-tunable", action="store_true",
                     help="library GEMMs with hipBLASLt's default solutions instead of PyTorch TunableOp")
     a = ap.parse_args()
+    if a.pmc_summary:
+        pmc_summary(*a.pmc_summary)
+        return
+    if a.trace_summary:
+        trace_summary(*a.trace_summary)
+        return
     if a.gpus != 1:
         print("bench.py measures one GPU only: there is no multi-GPU path in this library (the pair list "
               "would shard by spatial domain with halo atoms; nothing here runs it). Run with --gpus 1.",
@@ -320,41 +651,22 @@ def main():
         pmc_probe(a.workload)
         return
     main_run = run_gpu(a.workload, a.steps, a.warmup, not a.eager)
-    also = {}
     runs = [(int(x), False) for x in a.also.split(",") if x.strip() and int(x) != a.workload]
     runs += [(int(x), True) for x in a.compiled.split(",") if x.strip()]
+    results = {}
     for k, comp in runs:
-        r = run_gpu(k, a.steps, a.warmup, not a.eager, compiled_radial=comp)
-        also[f"workload{k}" + ("_compiled_radial" if comp else "")] = {
-            "desc": r["desc"], "atoms": r["N"], "pairs": r["E"], "atom_steps_per_s": r["atom_steps_per_s"],
-            "ms_per_step": r["ms_per_step"], "pairlist_ms": r["pairlist_ms"], "mode": r["mode"],
-            "eager_ms_per_step": r["eager_ms_per_step"],
-            "kernels": {kk: {"avg_us": v["avg_us"], "GBps": v["GBps"], "TFLOPs": v["TFLOPs"]}
-                        for kk, v in r["kernels"].items()}}
-    kern = main_run["kernels"]
-    known = {k: v for k, v in kern.items() if v["alg_bytes"] or v["alg_flops"]}
-    dom = max(known, key=lambda k: known[k]["ms_per_step"]) if known else None
-    roofline = None
-    if dom:
-        # the bound is the larger of the two floors: algorithmic bytes at peak HBM bandwidth and
-        # algorithmic flops at the dense fp32 MFMA peak
-        v = known[dom]
-        t_hbm = (v["alg_bytes"] or 0) / (HBM_PEAK_GBS * 1e9)
-        t_mfma = (v["alg_flops"] or 0) / (MFMA_PEAK_TFS * 1e12)
-        if t_mfma > t_hbm:
-            bound, ach, peak, unit = "mfma", v["TFLOPs"], MFMA_PEAK_TFS, "TFLOP/s"
-        else:
-            bound, ach, peak, unit = "hbm", v["GBps"], HBM_PEAK_GBS, "GB/s"
-        roofline = {"kernel": dom, "bound": bound, "achieved": ach, "peak": peak, "unit": unit, "frac": ach / peak,
-                    "traffic": measured_traffic(dom) if a.workload == 3 else None,
-                    "alg_bytes_per_launch": v["alg_bytes"], "alg_flops_per_launch": v["alg_flops"],
-                    "GBps": v["GBps"], "TFLOPs": v["TFLOPs"], "avg_launch_us": v["avg_us"]}
-    cpu = None
+        results[(k, comp)] = run_gpu(k, a.steps, a.warmup, not a.eager, compiled_radial=comp)
+    cpu = {}
     if not a.no_cpu:
-        log("[bench] cpu baseline ...")
-        cpu = run_cpu(a.workload, a.cpu_atoms)
-        log(f"[bench]   cpu {cpu['value']:.1f} atom-steps/s on {cpu['cores']} cores")
+        for k in [a.workload] + [k for k, comp in runs if not comp]:
+            log(f"[bench] cpu baseline, workload {k} ...")
+            cpu[k] = run_cpu(k, a.cpu_budget, a.cpu_full)
+            log(f"[bench]   cpu {cpu[k]['value']:.1f} atom-steps/s on {cpu[k]['cores']} cores ({cpu[k]['sample']})")
+    also = {}
+    for (k, comp), r in results.items():
+        also[f"workload{k}" + ("_compiled_radial" if comp else "")] = workload_record(r, None if comp else cpu.get(k))
     kw = main_run["kw"]
+    rec = workload_record(main_run)
     out = {
         "metric": METRIC, "value": main_run["atom_steps_per_s"], "unit": "atom-steps/s", "n_gpus": 1,
         "steps": a.steps, "warmup": a.warmup, "ms_per_step": main_run["ms_per_step"], "higher_is_better": True,
@@ -364,17 +676,18 @@ def main():
                    "weights": "random init, torch.manual_seed(0) + unit_parameterise", "parallelism": "single GPU",
                    "library_gemms": ("fp32 hipBLASLt/rocBLAS, solutions picked by PyTorch TunableOp in the warm-up"
                                      if tunable else "fp32 hipBLASLt default solutions"),
-                   "step": main_run["mode"], "eager_ms_per_step": main_run["eager_ms_per_step"],
-                   "peak_mem_gb": main_run["peak_mem_gb"]},
-        "roofline": roofline,
-        "cpu_baseline": cpu,
-        "kernels": {k: {"avg_us": v["avg_us"], "launches_per_step": v["launches_per_step"], "GBps": v["GBps"],
-                        "GBps_interface": v["GBps_interface"],
-                        "frac_hbm": (v["GBps"] / HBM_PEAK_GBS) if v["GBps"] else None,
-                        "TFLOPs": v["TFLOPs"], "frac_mfma": (v["TFLOPs"] / MFMA_PEAK_TFS) if v["TFLOPs"] else None}
-                    for k, v in kern.items()},
+                   "step": main_run["mode"], "timing": f"median of {main_run['rounds']} rounds of "
+                   f"{CALLS_PER_ROUND} calls after {a.warmup} warm-ups (tools/bench_review.py:53-69)",
+                   "ms_min": main_run["ms_min"], "ms_max": main_run["ms_max"],
+                   "eager_ms_per_step": main_run["eager_ms_per_step"], "peak_mem_gb": main_run["peak_mem_gb"],
+                   "graph_nodes": main_run["graph_nodes"]},
+        "roofline": main_run["roofline"],
+        "cpu_baseline": cpu.get(a.workload),
+        "kernels": rec["kernels"],
+        "families": rec["families"],
         "pairlist_ms": main_run["pairlist_ms"],
         "also": also,
+        "_argv": " ".join(sys.argv[1:]),
     }
     print(json.dumps(out), flush=True)
 

@@ -10,10 +10,30 @@ tools/graph_bench.py:29-40).
 The captured step allocates from a private pool and never synchronises with the host; new
 positions are copied into the static input buffer before each replay.
 """
+import ctypes
 import os
 import tempfile
 
 import torch
+
+_HIP = None
+
+
+def _hip_runtime():
+    """ctypes handle of the libamdhip64 that this process already loaded (torch's), found by path
+    in the process maps so that no second HIP runtime is loaded."""
+    global _HIP
+    if _HIP is None:
+        path = None
+        with open("/proc/self/maps") as f:
+            for line in f:
+                if "libamdhip64.so" in line:
+                    path = line.split()[-1]
+                    break
+        _HIP = ctypes.CDLL(path or "libamdhip64.so")
+        _HIP.hipGraphGetNodes.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.POINTER(ctypes.c_size_t)]
+        _HIP.hipGraphNodeGetType.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int)]
+    return _HIP
 
 
 def tune_library_gemms(results_file=None):
@@ -41,9 +61,33 @@ class StepGraph:
                 self._step()
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
-        self.cg = torch.cuda.CUDAGraph()
+        # the captured graph is kept (instantiated on the first replay) so that its nodes can be counted
+        self.cg = torch.cuda.CUDAGraph(keep_graph=True)
         with torch.cuda.graph(self.cg):
             self.energy, self.forces = self._step()
+        self.cg.instantiate()
+
+    def node_counts(self):
+        """{node type: count} of the captured step graph (hipGraphGetNodes / hipGraphNodeGetType of
+        the HIP runtime torch loaded): "kernel" is the number of kernel launches per replayed step."""
+        hip = _hip_runtime()
+        g = ctypes.c_void_p(self.cg.raw_cuda_graph())
+        n = ctypes.c_size_t(0)
+        if hip.hipGraphGetNodes(g, None, ctypes.byref(n)) != 0:
+            return None
+        nodes = (ctypes.c_void_p * n.value)()
+        if hip.hipGraphGetNodes(g, nodes, ctypes.byref(n)) != 0:
+            return None
+        names = {0: "kernel", 1: "memcpy", 2: "memset", 3: "host", 4: "graph", 5: "empty", 6: "wait_event",
+                 7: "event_record"}
+        out = {}
+        t = ctypes.c_int(0)
+        for k in range(n.value):
+            if hip.hipGraphNodeGetType(ctypes.c_void_p(nodes[k]), ctypes.byref(t)) != 0:
+                return None
+            key = names.get(t.value, f"type{t.value}")
+            out[key] = out.get(key, 0) + 1
+        return out
 
     def _step(self):
         p = self.pos.detach().requires_grad_(True)

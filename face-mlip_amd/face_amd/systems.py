@@ -100,14 +100,18 @@ FLAGSHIP = dict(n_basis=8, n_passes=2, radial_hidden=64, K_dir=16, norm="layer",
 def workload(k, n_atoms=None):
     """(structures, model kwargs, elements, description) of benchmark workload k (0..4).
 
-    n_atoms overrides the atom count of the liquid workloads (3, 4) for bounded samples."""
+    n_atoms overrides the size for bounded samples: the atom count of the liquids (3, 4), or
+    n_atoms // 21 molecules of the molecule batches (0, 1; the first molecules of the full batch)."""
     rng = stream(k)
-    if k == 0:
-        return molecules(64, rng), dict(FLAGSHIP, C=96, B=16, K=32, rc=4.5), [1, 6, 8], \
-            "64 x C9H8O4 molecules, FACE C96 B16 K32 rc4.5"
-    if k == 1:
-        return molecules(512, rng), dict(FLAGSHIP, C=160, B=16, K=32, rc=4.5, cp=True), [1, 6, 8], \
-            "512 x C9H8O4 molecules, FACE-CP C160 B16 rc4.5"
+    if k in (0, 1):
+        n_full = 64 if k == 0 else 512
+        n_mol = n_full if n_atoms is None else max(1, min(n_full, n_atoms // len(ASPIRIN_Z)))
+        mols = molecules(n_mol, rng)
+        if k == 0:
+            return mols, dict(FLAGSHIP, C=96, B=16, K=32, rc=4.5), [1, 6, 8], \
+                f"{n_mol} x C9H8O4 molecules, FACE C96 B16 K32 rc4.5"
+        return mols, dict(FLAGSHIP, C=160, B=16, K=32, rc=4.5, cp=True), [1, 6, 8], \
+            f"{n_mol} x C9H8O4 molecules, FACE-CP C160 B16 rc4.5"
     if k == 2:
         return [fcc(4.09, 6, 0.1, rng)], dict(FLAGSHIP, C=96, B=16, K=32, rc=4.5), [47], \
             "FCC Ag 6x6x6 (864 atoms), FACE C96 B16 K32 rc4.5"

@@ -358,3 +358,33 @@ def test_padded_dict_changed_in_place_is_rebuilt():
     o1 = m(d)
     o2 = m(dict(d, mask=d["mask"].clone()))
     assert torch.equal(o1["forces"], o2["forces"])
+
+
+def test_workload4_full_size_properties():
+    """The 100,000-atom C256 B16 K64 box at full size (6.9 M pairs): finite energy and forces, net
+    force zero to rounding (translation invariance: every pair term enters two atoms with
+    opposite signs), and HIP-graph replay equal to the eager step."""
+    from face_amd import systems
+    from face_amd.neighbors import build_graph
+    from face_amd.runner import StepGraph
+    sts, kw, el, desc = systems.workload(4)
+    say("full size", desc)
+    g = build_graph(sts, kw["rc"])
+    say(f"  N {g.N} E {g.E} max_row {g.max_row}")
+    assert g.N == 100000 and g.E > 6_000_000
+    m = product_model(kw, el)
+    o = m(g.with_pos(g.pos.clone()))
+    E, F = o["energy"].detach(), o["forces"].detach()
+    assert torch.isfinite(E).all() and torch.isfinite(F).all()
+    rms = F.double().pow(2).mean().sqrt()
+    net = F.double().sum(0).abs().max()
+    say(f"  E {E.item():.6e}  rms(F) {rms.item():.4e}  max|sum F| {net.item():.3e}")
+    assert net <= 1e-3 * rms, (net, rms)
+    run = StepGraph(m, g)
+    E1, F1 = run(g.pos)
+    torch.cuda.synchronize()
+    assert torch.allclose(E1, E, rtol=1e-6, atol=0), (E1, E)
+    assert (F1 - F).abs().max() <= 1e-5 * F.abs().max()
+    nodes = run.node_counts()
+    say(f"  graph nodes {nodes}")
+    assert nodes and nodes.get("kernel", 0) > 0 and nodes.get("memset", 0) == 0

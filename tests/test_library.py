@@ -148,3 +148,31 @@ def test_bench_refuses_more_than_one_gpu():
                        text=True, timeout=300, cwd=REPO)
     assert r.returncode == 2
     assert "one GPU" in r.stderr
+
+
+def test_bench_roofline_sums_labels_of_one_kernel():
+    """The bench's roofline kernel is chosen per kernel family (labels that launch the same kernel
+    summed), and its fraction is the sum of the launches' floors (bytes at 8 TB/s or flops at the
+    fp32 MFMA peak, whichever binds) over their measured time."""
+    import bench
+    kern = {
+        "cp_radial_bwd": {"family": "cp_radial_bwd", "launches_per_step": 1.0, "ms_per_step": 1.0,
+                          "alg_bytes": 4.0e9, "alg_flops": None},
+        "cp_radial_bwd_tab": {"family": "cp_radial_bwd", "launches_per_step": 1.0, "ms_per_step": 1.0,
+                              "alg_bytes": 4.0e9, "alg_flops": None},
+        "radial_head": {"family": "edge_linear_fwd", "launches_per_step": 1.0, "ms_per_step": 1.5,
+                        "alg_bytes": 1.0e9, "alg_flops": 1.573e11},
+    }
+    fam = bench.family_stats(kern)
+    assert fam["cp_radial_bwd"]["launches_per_step"] == 2.0 and fam["cp_radial_bwd"]["ms_per_step"] == 2.0
+    r = bench.roofline_of(fam, "none")
+    assert r["kernel"] == "cp_radial_bwd" and r["bound"] == "hbm" and r["unit"] == "GB/s"
+    assert abs(r["frac"] - 0.5) < 1e-12 and abs(r["achieved"] - 4000.0) < 1e-6      # 4 GB per 1 ms launch
+    assert abs(fam["edge_linear_fwd"]["frac"] - 1.0 / 1.5) < 1e-12                   # 1 ms MFMA floor
+    assert fam["edge_linear_fwd"]["bound"] == "mfma"
+
+
+def test_bench_labels_map_to_kernel_families():
+    import bench
+    for lab, fam in bench.KERNEL_FAMILY.items():
+        assert fam in bench.FAMILY_KERNELS, lab
