@@ -11,4 +11,4 @@ extern "C" const char* face_hip_error_string(int code) {
     }
 }
 
-extern "C" int face_hip_abi_version(void) { return 12; }
+extern "C" int face_hip_abi_version(void) { return 13; }

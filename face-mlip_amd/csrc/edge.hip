@@ -73,14 +73,11 @@ __global__ __launch_bounds__(256) void edge_geom_fwd_kernel(const float* __restr
     }
 }
 
-__global__ __launch_bounds__(256) void edge_geom_bwd_kernel(
-    const float* __restrict__ pos, const int32_t* __restrict__ recv, const int32_t* __restrict__ col,
-    const float* __restrict__ shift, const uint8_t* __restrict__ mask, int64_t E, const float* __restrict__ freq,
-    int nb, float rc, float bes_scale, const float* __restrict__ gY, const float* __restrict__ grb,
-    const float* __restrict__ genv, const float* __restrict__ gr, float* __restrict__ gvec) {
-    const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    if (e >= E) return;
-    const EdgeGeom g = edge_geom(pos, recv, col, shift, mask, e, rc);
+// dL/dvec of one edge from the upstream gradients of its outputs (Y, rb, env, r).
+__device__ __forceinline__ void edge_dvec(const EdgeGeom& g, int64_t e, const float* __restrict__ freq, int nb, float rc,
+                                          float bes_scale, const float* __restrict__ gY,
+                                          const float* __restrict__ grb, const float* __restrict__ genv,
+                                          const float* __restrict__ gr, float* out) {
     // d/du of the monomials contracted with gY
     float gu[3] = {0.f, 0.f, 0.f};
     if (gY) {
@@ -93,7 +90,6 @@ __global__ __launch_bounds__(256) void edge_geom_bwd_kernel(
         gu[2] = q[3] + 2.f * z * q[6] + x * q[8] + y * q[9] + 3.f * z * z * q[12] + x * x * q[14] +
                 y * y * q[16] + 2.f * x * z * q[17] + 2.f * y * z * q[18] + x * y * q[19];
     }
-    float out[3];
     if (g.valid) {
         const float ev = envelope(g);
         float genv_t = genv ? genv[e] : 0.f;
@@ -118,8 +114,68 @@ __global__ __launch_bounds__(256) void edge_geom_bwd_kernel(
 #pragma unroll
         for (int a = 0; a < 3; ++a) out[a] = gu[a];   // r := 1 is a constant on masked slots
     }
+}
+
+__global__ __launch_bounds__(256) void edge_geom_bwd_kernel(
+    const float* __restrict__ pos, const int32_t* __restrict__ recv, const int32_t* __restrict__ col,
+    const float* __restrict__ shift, const uint8_t* __restrict__ mask, int64_t E, const float* __restrict__ freq,
+    int nb, float rc, float bes_scale, const float* __restrict__ gY, const float* __restrict__ grb,
+    const float* __restrict__ genv, const float* __restrict__ gr, float* __restrict__ gvec) {
+    const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    const EdgeGeom g = edge_geom(pos, recv, col, shift, mask, e, rc);
+    float out[3];
+    edge_dvec(g, e, freq, nb, rc, bes_scale, gY, grb, genv, gr, out);
 #pragma unroll
     for (int a = 0; a < 3; ++a) gvec[e * 3 + a] = out[a];
+}
+
+// Edge backward with the own-row half of the force scatter folded in (CSR lists, no mask). One
+// thread per edge computes dL/dvec_e as edge_geom_bwd_kernel does and writes it to the slot of
+// the edge's REVERSE, gvec_rev[rev e], so that row k of gvec_rev holds the dL/dvec of the edges
+// whose neighbour is k, contiguous for the scatter that follows. The row's own sum is reduced
+// inside the wave: rows are contiguous edge ranges, so a segmented scan over the wave's 64 edges
+// (segments = receiver atoms) leaves, at the last edge of each row inside a 64-edge window, the sum
+// of the row's edges in that window; it is written to wsum at that edge's index (the other wsum
+// slots are never written or read). Every sum has a fixed order: no atomics.
+__global__ __launch_bounds__(256) void edge_geom_bwd_seg_kernel(
+    const float* __restrict__ pos, const int32_t* __restrict__ recv, const int32_t* __restrict__ col,
+    const float* __restrict__ shift, const int32_t* __restrict__ rev, int64_t E, const float* __restrict__ freq,
+    int nb, float rc, float bes_scale, const float* __restrict__ gY, const float* __restrict__ grb,
+    const float* __restrict__ genv, const float* __restrict__ gr, float* __restrict__ gvec_rev,
+    float* __restrict__ wsum) {
+    const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;   // windows of 64 edges = one wave
+    const int lane = threadIdx.x & (kWave - 1);
+    const bool valid = e < E;
+    float out[3] = {0.f, 0.f, 0.f};
+    int key = -1;
+    if (valid) {
+        const EdgeGeom g = edge_geom(pos, recv, col, shift, nullptr, e, rc);
+        edge_dvec(g, e, freq, nb, rc, bes_scale, gY, grb, genv, gr, out);
+        const int64_t r = rev[e];
+        gvec_rev[r * 3 + 0] = out[0];
+        gvec_rev[r * 3 + 1] = out[1];
+        gvec_rev[r * 3 + 2] = out[2];
+        key = recv[e];
+    }
+    // segmented inclusive scan: keys are non-decreasing along the wave, so equal keys d lanes
+    // apart bound a run of one row
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const float p0 = __shfl_up(out[0], d, kWave), p1 = __shfl_up(out[1], d, kWave), p2 = __shfl_up(out[2], d, kWave);
+        const int kp = __shfl_up(key, d, kWave);
+        if (lane >= d && kp == key) {
+            out[0] += p0;
+            out[1] += p1;
+            out[2] += p2;
+        }
+    }
+    const int kn = __shfl_down(key, 1, kWave);
+    if (valid && (lane == kWave - 1 || kn != key)) {
+        wsum[e * 3 + 0] = out[0];
+        wsum[e * 3 + 1] = out[1];
+        wsum[e * 3 + 2] = out[2];
+    }
 }
 
 __global__ __launch_bounds__(256) void gather_rows_kernel(const float* __restrict__ X, int ld_X,
@@ -199,6 +255,41 @@ __global__ __launch_bounds__(256) void force_scatter_kernel(const float* __restr
             s0 += c0 - d0;
             s1 += c1 - d1;
             s2 += c2 - d2;
+        }
+    }
+    s0 = group_sum(s0, G);
+    s1 = group_sum(s1, G);
+    s2 = group_sum(s2, G);
+    if (live && l == 0) {
+        grad[k * 3 + 0] = sign * s0;
+        grad[k * 3 + 1] = sign * s1;
+        grad[k * 3 + 2] = sign * s2;
+    }
+}
+
+// grad[k] = sign * sum_{e in row k} (gvec_rev[e] - own_e), own_e = wsum[e] at the last edge of the
+// row in each 64-edge window (e % 64 == 63 or e == end of row) and 0 elsewhere: the force scatter
+// as one contiguous pass over each row (gvec_rev and wsum from edge_geom_bwd_seg_kernel). G lanes
+// per atom read the row's 12-byte entries coalesced; partial sums reduced by butterfly shuffles.
+template <int G>
+__global__ __launch_bounds__(256) void force_scatter_rows_kernel(const float* __restrict__ gvec_rev,
+                                                                 const float* __restrict__ wsum,
+                                                                 const int32_t* __restrict__ row_ptr, int64_t N,
+                                                                 float sign, float* __restrict__ grad) {
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    const int l = threadIdx.x & (G - 1);
+    const int64_t k = t / G;
+    const bool live = k < N;                            // whole groups of G lanes share k
+    const int64_t e0 = live ? row_ptr[k] : 0, e1 = live ? row_ptr[k + 1] : 0;
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f;
+    for (int64_t e = e0 + l; e < e1; e += G) {
+        s0 += gvec_rev[e * 3 + 0];
+        s1 += gvec_rev[e * 3 + 1];
+        s2 += gvec_rev[e * 3 + 2];
+        if ((e & (kWave - 1)) == kWave - 1 || e == e1 - 1) {
+            s0 -= wsum[e * 3 + 0];
+            s1 -= wsum[e * 3 + 1];
+            s2 -= wsum[e * 3 + 2];
         }
     }
     s0 = group_sum(s0, G);
@@ -377,6 +468,37 @@ extern "C" int face_edge_geom_bwd(const float* pos, const int32_t* recv, const i
     if (!pos || !recv || !col || !shift || !gvec) return FACE_ERR_ARG;
     hipLaunchKernelGGL(edge_geom_bwd_kernel, dim3(blocks_for(E)), dim3(256), 0, (hipStream_t)stream, pos, recv, col,
                        shift, mask, E, freq, n_basis, rc, bes_scale, gY, grb, genv, gr, gvec);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int face_edge_geom_bwd_seg(const float* pos, const int32_t* recv, const int32_t* col, const float* shift,
+                                      const int32_t* rev, int64_t E, const float* freq, int32_t n_basis, float rc,
+                                      float bes_scale, const float* gY, const float* grb, const float* genv,
+                                      const float* gr, float* gvec_rev, float* wsum, void* stream) {
+    if (E < 0 || n_basis < 0 || !(rc > 0.f) || (grb && (!freq || n_basis == 0))) return FACE_ERR_ARG;
+    if (E == 0) return 0;
+    if (!pos || !recv || !col || !shift || !rev || !gvec_rev || !wsum) return FACE_ERR_ARG;
+    hipLaunchKernelGGL(edge_geom_bwd_seg_kernel, dim3(blocks_for(E)), dim3(256), 0, (hipStream_t)stream, pos, recv,
+                       col, shift, rev, E, freq, n_basis, rc, bes_scale, gY, grb, genv, gr, gvec_rev, wsum);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int face_force_scatter_rows(const float* gvec_rev, const float* wsum, const int32_t* row_ptr, int64_t N,
+                                       int32_t mean_row, float sign, float* grad, void* stream) {
+    if (N < 0) return FACE_ERR_ARG;
+    if (N == 0) return 0;
+    if (!gvec_rev || !wsum || !row_ptr || !grad) return FACE_ERR_ARG;
+    const hipStream_t st = (hipStream_t)stream;
+    // lanes per row ~ a third of the mean row length: two or three edges per lane
+    if (mean_row <= 24) {
+        hipLaunchKernelGGL(force_scatter_rows_kernel<8>, dim3(blocks_for(N * 8)), dim3(256), 0, st, gvec_rev, wsum,
+                           row_ptr, N, sign, grad);
+    } else {
+        hipLaunchKernelGGL(force_scatter_rows_kernel<16>, dim3(blocks_for(N * 16)), dim3(256), 0, st, gvec_rev, wsum,
+                           row_ptr, N, sign, grad);
+    }
     FACE_LAUNCH_CHECK();
     return 0;
 }

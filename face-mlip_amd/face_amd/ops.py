@@ -81,11 +81,17 @@ class EdgeGeometry(torch.autograd.Function):
         cont = lambda t: None if (t is None or t.numel() == 0) else t.contiguous().float()
         gY, grb, genv, gr = cont(gY), cont(grb), cont(genv), cont(gr)
         st = _lib.stream_of(pos)
-        call("face_edge_geom_bwd", ptr(pos), ptr(g.recv), ptr(g.col), ptr(g.shift), None, g.E, ptr(freq), freq.numel(),
-             float(ctx.rc), float(ctx.bes_scale), ptr(gY), ptr(grb), ptr(genv), ptr(gr), ptr(gvec), st,
-             label="edge_bwd")
+        # edge backward: each edge's dL/dvec lands in its reverse edge's slot and the own-row sums are
+        # reduced per 64-edge window in the same pass (wsum), so the scatter reads one contiguous row
+        # per atom, no reverse-edge gathers: grad_k = sum_{e in row k} gvec[rev e] - gvec[e]
+        wsum = torch.empty(g.E, 3, device=pos.device)
+        call("face_edge_geom_bwd_seg", ptr(pos), ptr(g.recv), ptr(g.col), ptr(g.shift), ptr(g.rev), g.E, ptr(freq),
+             freq.numel(), float(ctx.rc), float(ctx.bes_scale), ptr(gY), ptr(grb), ptr(genv), ptr(gr), ptr(gvec),
+             ptr(wsum), st, label="edge_bwd")
         gpos = torch.empty_like(pos)
-        call("face_force_scatter", ptr(gvec), ptr(g.row_ptr), ptr(g.rev), g.N, 1.0, ptr(gpos), st, label="force_scatter")
+        mean_row = (g.E + max(g.N, 1) - 1) // max(g.N, 1)
+        call("face_force_scatter_rows", ptr(gvec), ptr(wsum), ptr(g.row_ptr), g.N, mean_row, 1.0, ptr(gpos), st,
+             label="force_scatter")
         return gpos, None, None, None, None, None, None
 
 

@@ -371,6 +371,21 @@ int face_segment_sum(const float* g, int32_t ld_g, const int32_t* row_ptr, int64
  * Writes grad (N,3) (forces are its negative: sign = -1 writes -grad). */
 int face_force_scatter(const float* gvec, const int32_t* row_ptr, const int32_t* rev, int64_t N, float sign,
                        float* grad, void* stream);
+/* The same force scatter without reverse-edge gathers, in two passes over a CSR list (no mask):
+ * face_edge_geom_bwd_seg computes dL/dvec of every edge as face_edge_geom_bwd does and writes it
+ * to the slot of the edge's reverse, gvec_rev[rev e] (E,3); its own-row sums are reduced per
+ * window of 64 consecutive edges (e / 64) and written to wsum (E,3) at the last edge of the row
+ * in the window (wsum's other rows are left unwritten). face_force_scatter_rows then writes
+ * grad[k] = sign * sum_{e in row k} (gvec_rev[e] - [e is the row's last edge in its window] wsum[e]),
+ * reading each row contiguously. mean_row (~E/N) picks the lanes per row. Fixed summation
+ * order, no atomics. Replaces the index_add backward of pos[nbr] - pos[i] (face/model.py:670;
+ * forces = -grad at :692-694). */
+int face_edge_geom_bwd_seg(const float* pos, const int32_t* recv, const int32_t* col, const float* shift,
+                           const int32_t* rev, int64_t E, const float* freq, int32_t n_basis, float rc, float bes_scale,
+                           const float* gY, const float* grb, const float* genv, const float* gr, float* gvec_rev,
+                           float* wsum, void* stream);
+int face_force_scatter_rows(const float* gvec_rev, const float* wsum, const int32_t* row_ptr, int64_t N,
+                            int32_t mean_row, float sign, float* grad, void* stream);
 
 #ifdef __cplusplus
 }

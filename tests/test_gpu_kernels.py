@@ -323,16 +323,37 @@ def test_gathers_and_force_scatter_match_index_add():
     call("face_force_scatter", ptr(gvec), ptr(g.row_ptr), ptr(g.rev), g.N, 1.0, ptr(grad), stream_of(gvec))
     ref = torch.zeros(g.N, 3, device=DEV).index_add(0, col, gvec).index_add(0, recv, -gvec)
     assert rel(grad, ref) < 1e-5
+    # the contiguous row form: reverse slots and per-window own-row sums laid out as the edge backward
+    # (face_edge_geom_bwd_seg) writes them, wsum filled only at the last edge of each row in each
+    # 64-edge window (NaN elsewhere: never read), then the row pass (both lane widths)
+    gvec_rev = gvec[g.rev.long()].contiguous()
+    e_idx = torch.arange(g.E, device=DEV)
+    seg = recv * ((g.E + 63) // 64) + e_idx // 64
+    _, inv, cnt = torch.unique_consecutive(seg, return_inverse=True, return_counts=True)
+    sums = torch.zeros(cnt.numel(), 3, device=DEV).index_add(0, inv, gvec)
+    wsum = torch.full((g.E, 3), float("nan"), device=DEV)
+    wsum[torch.cumsum(cnt, 0) - 1] = sums
+    for mean_row in (16, 40):
+        grad2 = torch.full((g.N, 3), float("nan"), device=DEV)
+        call("face_force_scatter_rows", ptr(gvec_rev), ptr(wsum), ptr(g.row_ptr), g.N, mean_row, -1.0, ptr(grad2),
+             stream_of(gvec))
+        assert rel(-grad2, ref) < 1e-5
 
 
 # ----------------------------------------------------------------------------- edge geometry
-def test_edge_geometry_forward_and_backward():
+@pytest.mark.parametrize("system", ["molecules", "liquid"])
+def test_edge_geometry_forward_and_backward(system):
+    """Edge geometry, basis and envelope and their backward into dE/dpos (the row-organised edge
+    backward and the contiguous force scatter; short molecule rows and ~40-pair periodic rows)."""
     from face_amd import ops
     from face_amd.neighbors import build_graph
     from face_amd import systems
-    say("edge geometry")
-    st = systems.molecules(6, np.random.default_rng(2))
+    say("edge geometry", system)
     rc = 4.5
+    if system == "molecules":
+        st = systems.molecules(6, np.random.default_rng(2))
+    else:
+        st = [systems.liquid(400, np.random.default_rng(4), rho=0.1, dmin=0.9)]
     g = build_graph(st, rc)
     pos = g.pos.clone().requires_grad_(True)
     freq = (torch.arange(1, 9) * np.pi / rc).float().to(DEV)
