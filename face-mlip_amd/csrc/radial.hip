@@ -12,6 +12,8 @@
 // is input feature 4q + r of the block. Weights, biases and the pair table sit in LDS.
 #include "common.h"
 
+#include <mutex>
+
 namespace face {
 
 constexpr int kRadWaves = 4;                           // waves per workgroup
@@ -615,6 +617,63 @@ extern "C" int face_radial_spline_bwd(const float* r, const int32_t* pair, int64
 #undef FACE_SPLINE
     FACE_LAUNCH_CHECK();
     return 0;
+}
+
+// ---------------------------------------------------------------- allocation-free edge order
+// face_radial_spline_order with its counting-sort counters in a file-scope device array instead of a
+// caller workspace, for callers that cannot allocate. Each GPU the library runs on holds its own copy
+// of the array (4 MiB) until the process ends. In host code `spline_order_scratch` names a host-side
+// stand-in, not device memory: its device address is taken once per device with
+// hipGetSymbolAddress (that device current) and only that address is passed to kernels.
+static __device__ __align__(256) int32_t spline_order_scratch[FACE_SPLINE_ORDER_SCRATCH];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+int32_t* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of this device's copy of spline_order_scratch (looked up on the first call on the
+// device, with that device current); nullptr and the HIP status on failure.
+int32_t* spline_scratch_for(int dev, int* status) {
+    *status = 0;
+    if (dev < 0 || dev >= kMaxDevices) {
+        *status = FACE_ERR_ARG;
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        int cur = -1;
+        hipError_t e = hipGetDevice(&cur);
+        if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+        void* p = nullptr;
+        if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(spline_order_scratch));
+        if (cur >= 0 && cur != dev) {
+            const hipError_t e2 = hipSetDevice(cur);
+            if (e == hipSuccess) e = e2;
+        }
+        if (e != hipSuccess || !p) {
+            *status = e != hipSuccess ? (int)e : FACE_ERR_ARG;
+            return nullptr;
+        }
+        g_scratch_ptr[dev] = static_cast<int32_t*>(p);
+    }
+    return g_scratch_ptr[dev];
+}
+}  // namespace
+
+extern "C" int face_radial_spline_order_noalloc(const float* r, const int32_t* pair, int64_t E, int32_t P, int32_t G,
+                                                float dr, int32_t* order, void* stream) {
+    if (E < 0 || P < 1 || G < 2 || !(dr > 0.f) || E > 0x7fffffff) return FACE_ERR_ARG;
+    if ((int64_t)P * G > FACE_SPLINE_ORDER_SCRATCH) return FACE_ERR_SCRATCH;
+    if (E == 0) return 0;
+    if (!r || !pair || !order) return FACE_ERR_ARG;
+    int dev = -1;
+    hipError_t e = stream ? hipStreamGetDevice((hipStream_t)stream, &dev) : hipGetDevice(&dev);
+    if (e != hipSuccess) return (int)e;
+    int status = 0;
+    int32_t* work = spline_scratch_for(dev, &status);
+    if (!work) return status;
+    return face_radial_spline_order(r, pair, E, P, G, dr, work, order, stream);
 }
 
 extern "C" int face_radial_spline_order(const float* r, const int32_t* pair, int64_t E, int32_t P, int32_t G,

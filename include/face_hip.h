@@ -44,6 +44,7 @@ extern "C" {
 #define FACE_ERR_ARG (-1)         /* invalid shape, stride or null pointer */
 #define FACE_ERR_UNSUPPORTED (-2) /* shape outside the instantiated kernel variants */
 #define FACE_ERR_CAPACITY (-3)    /* a row or bin exceeds the kernel's capacity */
+#define FACE_ERR_SCRATCH (-4)     /* input exceeds the fixed scratch of an allocation-free entry point */
 
 const char* face_hip_error_string(int code);
 /* ABI version of this header (bumped on any signature change). */
@@ -275,6 +276,16 @@ int face_radial_spline_bwd(const float* r, const int32_t* pair, int64_t E, const
  * tables (8 P G F bytes) are far larger than L2. work: P * G int32 of scratch. */
 int face_radial_spline_order(const float* r, const int32_t* pair, int64_t E, int32_t P, int32_t G, float dr,
                              int32_t* work, int32_t* order, void* stream);
+/* No counterpart in the reference. For callers that cannot allocate device memory (code under
+ * HIP-graph capture, tight serving loops, harnesses that forbid hipMalloc): face_radial_spline_order
+ * without the `work` argument. Its P * G sort counters live in a fixed device array of the library,
+ * FACE_SPLINE_ORDER_SCRATCH int32 (4 MiB) per GPU, held until the process ends; P * G above that
+ * returns FACE_ERR_SCRATCH before any launch. The entry point allocates nothing (no hipMalloc /
+ * hipFree); the counters are cleared by a kernel at the start of every call. Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (e.g. on two streams) race. */
+#define FACE_SPLINE_ORDER_SCRATCH (1 << 20)
+int face_radial_spline_order_noalloc(const float* r, const int32_t* pair, int64_t E, int32_t P, int32_t G, float dr,
+                                     int32_t* order, void* stream);
 
 /* ---------------------------------------------------------------- row-block linear layers
  * One problem: x (m, ld_x >= k) rows, w (n, k) row-major with row stride ld_w (w_kn = 0) or
