@@ -47,6 +47,7 @@ TAGS = {0: "mol64_c96", 1: "mol512_cp160", 2: "fcc864_c96", 3: "liquid24k_cp160"
 # launch the same kernel are summed when the dominant kernel is chosen)
 KERNEL_FAMILY = {
     "density_fwd20": "density_fwd", "density_bwd20": "density_bwd",
+    "density_mix_fwd": "density_mix_fwd", "density_mix_bwd": "density_mix_bwd",
     "cp_fwd": "cp_density_fwd", "cp_fwd_tab": "cp_density_fwd",
     "cp_bwd": "cp_density_bwd", "cp_bwd_tab": "cp_density_bwd",
     "cp_radial_bwd": "cp_radial_bwd", "cp_radial_bwd_tab": "cp_radial_bwd",
@@ -65,6 +66,7 @@ KERNEL_FAMILY = {
 FAMILY_KERNELS = {
     "density_fwd": ["density_fwd_mfma_kernel", "density_fwd_kernel"],
     "density_bwd": ["density_bwd_mfma_kernel", "density_bwd_kernel"],
+    "density_mix_fwd": ["density_mix_fwd_kernel"], "density_mix_bwd": ["density_mix_bwd_kernel"],
     "cp_density_fwd": ["cp_density_fwd_wave_kernel", "cp_density_fwd_kernel"],
     "cp_density_bwd": ["cp_density_bwd_mfma_kernel", "cp_density_bwd_kernel"],
     "cp_radial_bwd": ["cp_radial_bwd_res_kernel", "cp_radial_bwd_lds_kernel"],
@@ -100,6 +102,10 @@ def algorithmic_bytes(label, g, kw):
     if label == "density_fwd20":
         return 4 * (E * (B + K + 20) + 20 * N * B * K)
     if label == "density_bwd20":
+        return 4 * (2 * E * (B + K + 20) + 20 * N * B * K)
+    if label == "density_mix_fwd":        # the density's drop-in figure (D counted as if written)
+        return 4 * (E * (B + K + 20) + 20 * N * B * K)
+    if label == "density_mix_bwd":
         return 4 * (2 * E * (B + K + 20) + 20 * N * B * K)
     if label == "transport_fwd":          # phi, u, gathered V|M of Kd channels in; 18 sums per (b, kd) out
         return 4 * (E * (B + 3 + Kt // 2) + 18 * N * B * kw["K_dir"])
@@ -192,6 +198,10 @@ def algorithmic_flops(label, g, kw):
         return 2 * E * 20 * kw["B"] * kw["K"]
     if label == "density_bwd20":
         return 3 * 2 * E * 20 * kw["B"] * kw["K"]
+    if label == "density_mix_fwd":        # density products + the four mixes (20 rows per atom)
+        return 2 * E * 20 * kw["B"] * kw["K"] + 2 * 20 * N * cin * C
+    if label == "density_mix_bwd":
+        return 3 * 2 * E * 20 * kw["B"] * kw["K"] + 2 * 20 * N * cin * C
     return None
 
 
@@ -531,6 +541,59 @@ def pmc_summary(fetch_dir, write_dir, probe_log, out_path):
     print("".join(out))
 
 
+SQ_PASSES = [
+    "SQ_WAVES SQ_WAVE_CYCLES SQ_BUSY_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY SQ_ACTIVE_INST_ANY SQ_LEVEL_WAVES "
+    "SQ_VALU_MFMA_BUSY_CYCLES",
+    "SQ_INSTS_MFMA SQ_INSTS_VALU SQ_INSTS_LDS SQ_INSTS_VMEM_RD SQ_INSTS_VMEM_WR SQ_ACTIVE_INST_VALU "
+    "SQ_ACTIVE_INST_VMEM SQ_ACTIVE_INST_LDS",
+    "SQ_LDS_BANK_CONFLICT SQ_WAIT_INST_LDS SQ_INST_LEVEL_VMEM SQ_INSTS_SALU SQ_INST_CYCLES_VMEM_RD "
+    "SQ_INST_CYCLES_VMEM_WR SQ_LDS_IDX_ACTIVE SQ_CYCLES",
+]
+
+
+def sq_summary(out_path, title, probe_args, *dirs):
+    """Per-kernel SQ counter summary of `rocprofv3 --pmc` passes (SQ_PASSES, one directory each) over
+    `bench.py --pmc-probe ...`: wave occupancy and wait fractions, instruction mix and MFMA busy
+    cycles per dispatch. mfma_util = SQ_VALU_MFMA_BUSY_CYCLES (= MFMA instructions x their busy
+    cycles, summed over SIMDs) / (1024 SIMDs x the dispatch's duration x 2.4 GHz): the share of the
+    matrix-core cycles of the whole device the kernel kept busy."""
+    import collections
+    import csv
+    import glob
+    data = collections.defaultdict(lambda: collections.defaultdict(list))
+    for d in dirs:
+        f = sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True))
+        if not f:
+            sys.exit(f"no counter_collection.csv under {d}")
+        for r in csv.DictReader(open(f[0])):
+            k = r["Kernel_Name"].split("(")[0].replace("void ", "").replace("face::", "")
+            data[k][r["Counter_Name"]].append(float(r["Counter_Value"]))
+            data[k]["_dur_ns"].append(float(r["End_Timestamp"]) - float(r["Start_Timestamp"]))
+    out = [f"# SQ counters: {title}\n\nCommands (repo root, MI355X, ROCm 7.2), one pass per counter group:\n\n```\n"]
+    for i, P in enumerate(SQ_PASSES):
+        out.append(f"rocprofv3 --pmc {P} --kernel-include-regex 'face::' --output-format csv "
+                   f"-d gpurun_out/sq{i + 1} -o p -- python -u bench.py --pmc-probe {probe_args}\n")
+    out.append(f"python bench.py --sq-summary {out_path} '{title}' '{probe_args}' "
+               + " ".join(f"gpurun_out/sq{i + 1}" for i in range(len(dirs))) + "\n```\n\n")
+    out.append("Per dispatch averages. wave-cycle fractions: time a wave spends waiting on anything / on "
+               "s_waitcnt / issuing. mfma_util: SQ_VALU_MFMA_BUSY_CYCLES over (1024 SIMDs x duration x 2.4 GHz).\n\n"
+               "| kernel | dispatches | waves | us | wait_any | wait_inst | active | mfma insts | "
+               "mfma_util | valu insts | lds insts | vmem rd | vmem wr | lds bank conflicts |\n"
+               "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|\n")
+    for k, d in sorted(data.items(), key=lambda kv: -sum(kv[1].get("_dur_ns", [0]))):
+        m = {c: sum(v) / len(v) for c, v in d.items()}
+        wc = m.get("SQ_WAVE_CYCLES", 0) or 1
+        dur = m.get("_dur_ns", 0) or 1
+        g = lambda c: m.get(c, float("nan"))
+        out.append(f"| `{k[:70]}` | {len(d.get('SQ_WAVES', []))} | {g('SQ_WAVES'):.0f} | {dur / 1e3:.1f} | "
+                   f"{g('SQ_WAIT_ANY') / wc:.2f} | {g('SQ_WAIT_INST_ANY') / wc:.2f} | {g('SQ_ACTIVE_INST_ANY') / wc:.2f} | "
+                   f"{g('SQ_INSTS_MFMA'):.3g} | {g('SQ_VALU_MFMA_BUSY_CYCLES') / (1024 * 2.4 * dur):.3f} | "
+                   f"{g('SQ_INSTS_VALU'):.3g} | {g('SQ_INSTS_LDS'):.3g} | {g('SQ_INSTS_VMEM_RD'):.3g} | "
+                   f"{g('SQ_INSTS_VMEM_WR'):.3g} | {g('SQ_LDS_BANK_CONFLICT'):.3g} |\n")
+    open(out_path, "w").write("".join(out))
+    print("".join(out))
+
+
 def measured_traffic(tag, labels):
     """HBM bytes per launch of a kernel family (its labels' calls) from the committed counter
     summary of the workload (profiles/traffic_<tag>.md), or None."""
@@ -622,6 +685,8 @@ def main():
     ap.add_argument("--pmc-probe", action="store_true", help="short run for rocprofv3 --pmc passes")
     ap.add_argument("--pmc-summary", nargs=4, metavar=("FETCH_DIR", "WRITE_DIR", "PROBE_LOG", "OUT"))
     ap.add_argument("--trace-summary", nargs=4, metavar=("STATS_CSV", "BENCH_LOG", "OUT", "TITLE"))
+    ap.add_argument("--sq-summary", nargs="+", metavar="OUT TITLE PROBE_ARGS DIR",
+                    help="OUT TITLE PROBE_ARGS DIR1 [DIR2 DIR3]: SQ counter summary of rocprofv3 --pmc passes")
     ap.add_argument("--no-tunable", action="store_true",
                     help="library GEMMs with hipBLASLt's default solutions instead of PyTorch TunableOp")
     a = ap.parse_args()
@@ -630,6 +695,9 @@ def main():
         return
     if a.trace_summary:
         trace_summary(*a.trace_summary)
+        return
+    if a.sq_summary:
+        sq_summary(*a.sq_summary)
         return
     if a.gpus != 1:
         print("bench.py measures one GPU only: there is no multi-GPU path in this library (the pair list "

@@ -21,7 +21,7 @@ FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-ta
 # graph.hip evaluates the pair-acceptance test in fp64 with a fixed operation order: no contraction.
 SOURCES = {"capi.hip": "fast", "density.hip": "fast", "node.hip": "fast", "edge.hip": "fast", "graph.hip": "off",
            "transport.hip": "fast", "radial.hip": "fast", "linear.hip": "fast",
-           "gemm.hip": "fast"}
+           "gemm.hip": "fast", "densmix.hip": "fast"}
 
 
 def compile_one(src):

@@ -27,6 +27,10 @@ _SIGS = {
     "face_density_fwd": (ctypes.c_int, [P, I32, P, I32, P, P, I32, I32, P, I64, I32, I32, I32, P, I64, I64, P]),
     "face_density_bwd": (ctypes.c_int, [P, I32, P, I32, P, P, I32, I32, P, I64, I32, I32, I32, I32, P, I64, I64, P,
                                         I32, P, I32, P, I32, P]),
+    "face_density_mix_fwd": (ctypes.c_int, [P, I32, P, I32, P, P, I32, P, I64, I32, I32, I32, P, I64, P, I64, I64, P,
+                                            I32, P, I32, P]),
+    "face_density_mix_bwd": (ctypes.c_int, [P, I32, P, I32, P, P, I32, P, I64, I32, I32, I32, P, I64, P, I64, I64, P,
+                                            I32, P, P, I32, P, I32, P, I32, P]),
     "face_cp_density_fwd": (ctypes.c_int, [P, I32, P, P, I32, P, P, I32, P, I64, I32, I32, P, I64, I64, P]),
     "face_cp_density_bwd": (ctypes.c_int, [P, I32, P, P, I32, P, P, I32, P, I64, I32, I32, I32, P, I64, I64, P, I32,
                                            P, I32, P, I32, P, P]),
@@ -71,7 +75,7 @@ _SIGS = {
     "face_layer_norm_bwd": (ctypes.c_int, [P, P, I64, I32, P, P, P, P, P]),
 }
 
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 
 class LinProblem(ctypes.Structure):

@@ -276,14 +276,18 @@ class FactorBlock(nn.Module):
                 Af = ops.cp_radial_density(h2, W2[B:], b2[B:], env, mj, Y, g, gathered)
             else:
                 Af = ops.cp_density(F.linear(h2, W2[B:], b2[B:]), env, mj, Y, g, gathered)   # 4 x (k_l, N, C)
-        else:
-            Af = ops.density(phi, mj, Y, g, 20, gathered)                         # 4 x (k_l, N, B*K)
         # A_l = (mix_l(Af_l) [+ tmix_l(D_l)]) * s: D1/D2 are the raw transport sums; the reference's
         # 1/avg_nb (face/model.py:522) and its avg_nb factor (:532-533) cancel through the linear tmix,
         # leaving the common factor s = elem_scale / avg_nb, applied in the mix GEMMs' epilogue
         wm = [frozen(self.mix[l])[0] for l in range(4)]
         wt = [frozen(self.tmix1)[0], frozen(self.tmix2)[0]] if self.transport else [None, None]
         D1, D2 = (D1, D2) if self.transport else (None, None)
+        if not self.cp:
+            if ops.density_mix_fits(B, mj.shape[1], C, N):
+                # factor density and mix in one launch each way: D stays on chip
+                return list(ops.density_mix(s_tab, zidx32, wm, self._mix_t(wm), wt, D1, D2, phi, mj, Y, g,
+                                            gathered))
+            Af = ops.density(phi, mj, Y, g, 20, gathered)                         # 4 x (k_l, N, B*K)
         if C % 16 == 0 and Af[0].shape[-1] % 16 == 0:
             return list(ops.scaled_mix(s_tab, zidx32, wm, wt, D1, D2, Af))         # 4 x (k_l, N, C)
         s = s_tab[zidx].view(N, 4, C)
@@ -296,6 +300,16 @@ class FactorBlock(nn.Module):
                 y.addmm_(D.reshape(-1, D.shape[-1]), wt[l - 1].t())
             A.append(y.view(x.shape[0], N, C) * s[None, :, l, :])                 # (k_l, N, C)
         return A
+
+    def _mix_t(self, wm):
+        """Contiguous transposes (B K, C) of the four frozen mix weights, cached with them."""
+        key = _key(*wm)
+        c = self.__dict__.get("_mixT")
+        if c is None or not _same(c[0], key):
+            with torch.no_grad():
+                c = (key, [w.t().contiguous() for w in wm])
+            self.__dict__["_mixT"] = c
+        return c[1]
 
     def _scale_table(self, avg_nb):
         """elem_scale / avg_nb per element (n_elem, 4C), cached like the frozen weights."""

@@ -6,6 +6,7 @@ the backward of every neighbour gather is a row reduction through the reverse-ed
 (`rev`) instead of an atomic scatter, so forces are bitwise reproducible.
 """
 import math
+import os
 
 import torch
 
@@ -421,6 +422,99 @@ class Density(torch.autograd.Function):
 
 def density(phi, msg, Y, graph, nx=20, gathered=False):
     return Density.apply(phi, msg, Y, graph, nx, gathered)
+
+
+class DensityMix(torch.autograd.Function):
+    """Factor density fused with the per-rank mix and the element scale (face/kernels.py:170-178,
+    face/model.py:503-506, the scale of :530-533): A_l = (Af_l W_l^T [+ D_l T_l^T]) * s[z] with
+    Af = the factor density of phi, msg, Y, in one launch each way (the density D never leaves the
+    chip). The transport mix (D1, D2 with weights wt) is a separate GEMM written first and
+    accumulated in the fused epilogue. wm: 4 mix weights (C, B K); wmt: their transposes (B K, C),
+    contiguous. Weights receive no gradient."""
+
+    @staticmethod
+    def forward(ctx, s_tab, group, wm, wmt, wt, D1, D2, phi, msg, Y, graph, gathered):
+        _lib.require_gpu(phi, msg, Y)
+        B, K = phi.shape[1], msg.shape[1]
+        C = wm[0].shape[0]
+        N = graph.N
+        # dense rows (16-byte aligned row strides for the backward's vector loads; a no-op in the model)
+        phi_, msg_, Y_ = phi.float().contiguous(), msg.float().contiguous(), Y.float().contiguous()
+        ld_phi, ld_msg, ld_Y = B, K, Y_.shape[1]
+        dev = phi.device
+        outs = [torch.empty(k, N, C, device=dev) for k in RANK_K]
+        beta = 0
+        for l, D in ((1, D1), (2, D2)):
+            if D is not None:
+                torch.mm(D.reshape(-1, D.shape[-1]), wt[l - 1].t(), out=outs[l].view(-1, C))
+                beta |= 1 << l
+        row = graph.col if gathered else None
+        call("face_density_mix_fwd", ptr(phi_), ld_phi, ptr(msg_), ld_msg, ptr(row), ptr(Y_), ld_Y,
+             ptr(graph.row_ptr), N, B, K, C, _lib.ptr_array(wm), wm[0].stride(0), _lib.ptr_array(outs), C, N * C,
+             ptr(s_tab), s_tab.stride(0), ptr(group), beta, _lib.stream_of(phi), label="density_mix_fwd")
+        ctx.save_for_backward(s_tab, group, phi_, msg_, Y_)
+        ctx.graph, ctx.gathered, ctx.wmt, ctx.wt = graph, gathered, wmt, wt
+        ctx.has_D = (D1 is not None, D2 is not None)
+        ctx.ywidth = Y.shape[1]
+        return tuple(outs)
+
+    @staticmethod
+    def backward(ctx, *gA):
+        s_tab, group, phi, msg, Y = ctx.saved_tensors
+        g = ctx.graph
+        N, B, K = g.N, phi.shape[1], msg.shape[1]
+        C = ctx.wmt[0].shape[1]
+        dev = phi.device
+        gA = [(t.contiguous() if t is not None else torch.zeros(k, N, C, device=dev)) for t, k in zip(gA, RANK_K)]
+        need_D1, need_D2, need_phi, need_msg, need_Y = ctx.needs_input_grad[5:10]
+        dphi = torch.empty(g.E, B, device=dev) if need_phi else None
+        dmsg = torch.empty(g.E, K, device=dev) if need_msg else None
+        dY = torch.empty(g.E, 20, device=dev) if need_Y else None
+        st = _lib.stream_of(phi)
+        row = g.col if ctx.gathered else None
+        call("face_density_mix_bwd", ptr(phi), phi.stride(0), ptr(msg), msg.stride(0), ptr(row), ptr(Y), Y.stride(0),
+             ptr(g.row_ptr), N, B, K, C, _lib.ptr_array(ctx.wmt), ctx.wmt[0].stride(0), _lib.ptr_array(gA), C, N * C,
+             ptr(s_tab), s_tab.stride(0), ptr(group), ptr(dphi), B, ptr(dmsg), K, ptr(dY), 20, st,
+             label="density_mix_bwd")
+        if dmsg is not None and ctx.gathered:
+            dtab = torch.empty(N, K, device=dev)
+            call("face_gather_rows_bwd", ptr(dmsg), K, ptr(g.row_ptr), ptr(g.rev), N, K, ptr(dtab), K, st,
+                 label="gather_bwd")
+            dmsg = dtab
+        if dY is not None and ctx.ywidth != 20:
+            dY = torch.nn.functional.pad(dY, (0, ctx.ywidth - 20))
+        # transport mix: dD_l = (gA_l * s_l) wt, the scale applied to the rows as they load
+        dD = [None, None]
+        tp = []
+        for i, (l, need) in enumerate(((1, need_D1), (2, need_D2))):
+            if ctx.has_D[i] and need:
+                w = ctx.wt[i]
+                dD[i] = torch.empty(gA[l].shape[0], N, w.shape[1], device=dev)
+                tp.append((gA[l].view(-1, C), w, dD[i].view(-1, w.shape[1]), l * C, 0.0))
+        if tp:
+            rows_linear(tp, w_kn=True, xs=s_tab, group=group, period=N, label="tmix_bwd")
+        return (None, None, None, None, None, dD[0], dD[1], dphi, dmsg, dY, None, None)
+
+
+def density_mix(s_tab, group, wm, wmt, wt, D1, D2, phi, msg, Y, graph, gathered=False):
+    """4 x (k_l, N, C) moments of a factorised pass from the fused density + mix kernels."""
+    return DensityMix.apply(s_tab, group, wm, wmt, wt, D1, D2, phi, msg, Y, graph, gathered)
+
+
+def density_mix_fits(B, K, C, N, nx=20):
+    """Whether the model takes the fused density + mix route for this shape: the kernels serve
+    B = 16, K <= 64 and C <= 256 (multiples of 16), and the route is taken for systems of at most
+    DENSITY_MIX_MAX_ATOMS atoms. Measured on the flagship workloads (864-atom FCC, 1,344-atom
+    molecule batch) the fused kernels are slower than the density kernel + row GEMM pair they
+    replace (fwd 65 / 114 us against 54 / 74 us, bwd 121 / 227 us against 80 / 95 us): every
+    4-atom workgroup streams all four mix weights from L2 and pads its rank blocks to 16 rows
+    (71 % useful), and these launches are latency-bound single rounds. The default therefore
+    keeps D in memory (DENSITY_MIX_MAX_ATOMS = 0); set it to use the fused route."""
+    return (nx == 20 and B == 16 and K % 16 == 0 and K <= 64 and C % 16 == 0 and C <= 256
+            and N <= DENSITY_MIX_MAX_ATOMS)
+
+
+DENSITY_MIX_MAX_ATOMS = int(os.environ.get("FACE_DENSITY_MIX_MAX_ATOMS", "0"))
 
 
 def _cp_label(base, gathered):

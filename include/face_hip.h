@@ -14,6 +14,8 @@
  *
  * Reference interfaces replaced (albert-hzbn/face-mlip):
  *   face/kernels.py:135-172      FactorDensity / factor_density   -> face_density_fwd / _bwd
+ *   face/kernels.py:135-172 + face/model.py:503-506  factor density + mix[l]
+ *                                                                  -> face_density_mix_fwd / _bwd
  *   face/model.py:496-502        CP pooling bmm                   -> face_cp_density_fwd / _bwd
  *   face/node_kernel.py:164-209  NodeAlgebra / node_algebra       -> face_node_fwd / _bwd
  *   face/model.py:286-296        gated equivariant outputs V*gv, Ms*gm -> face_eq_gate_fwd / _bwd
@@ -81,6 +83,33 @@ int face_density_bwd(const float* phi, int32_t ld_phi, const float* msg, int32_t
                      int32_t max_row, int32_t B, int32_t K, const float* const* G_ranks, int64_t atom_stride,
                      int64_t x_stride, float* dphi, int32_t ld_dphi, float* dmsg, int32_t ld_dmsg, float* dY,
                      int32_t ld_dY, void* stream);
+
+/* ---------------------------------------------------------------- factor density fused with mix
+ * The factor density above (B = 16, NX = 20, CSR rows) followed by the per-rank channel mixing
+ * and element scale, with D kept on chip (LDS, one chunk of 16 basis functions x 16 channels at a
+ * time) instead of written:
+ *   A_l[i, x, c] = (beta_l A_l[i, x, c] + sum_{b,k} D[i, x, b, k] W_l[c, b K + k]) * ys[group[i], l C + c]
+ * w_ranks: 4 device pointers to W_l (C, ld_w >= B K) row-major (face/model.py:445 mix[l].weight);
+ * A_ranks: 4 output rank blocks (k_l, N, C)-addressed by atom_stride / x_stride (multiples of 4,
+ * 16-byte aligned); beta_l = bit l of beta_mask (the block already holds the transport mix of
+ * face/model.py:530-533); y_scale (n_el, ld_scale >= 4C) the elem_scale / avg_nb table, group (N)
+ * int32 element index, or NULL (no scale). K a multiple of 16 up to 64, C a multiple of 16 up to
+ * 256. Replaces FactorDensity.forward (face/kernels.py:137-149) + mix (face/model.py:503-506). */
+int face_density_mix_fwd(const float* phi, int32_t ld_phi, const float* msg, int32_t ld_msg, const int32_t* msg_row,
+                         const float* Y, int32_t ld_Y, const int32_t* row_ptr, int64_t N, int32_t B, int32_t K,
+                         int32_t C, const float* const* w_ranks, int64_t ld_w, float* const* A_ranks,
+                         int64_t atom_stride, int64_t x_stride, const float* y_scale, int32_t ld_scale,
+                         const int32_t* group, int32_t beta_mask, void* stream);
+/* Its backward for gA (rank blocks): dD = (gA * x_scale) W_l recomputed on chip per chunk, then
+ * dphi (E, ld_dphi), dmsg (E, ld_dmsg) per edge and dY (E, ld_dY) as face_density_bwd (any may be
+ * NULL). wt_ranks: W_l^T (B K, ld_wt >= C) row-major. Replaces FactorDensity.backward
+ * (face/kernels.py:151-167) + the mix backward. */
+int face_density_mix_bwd(const float* phi, int32_t ld_phi, const float* msg, int32_t ld_msg, const int32_t* msg_row,
+                         const float* Y, int32_t ld_Y, const int32_t* row_ptr, int64_t N, int32_t B, int32_t K,
+                         int32_t C, const float* const* wt_ranks, int64_t ld_wt, const float* const* gA_ranks,
+                         int64_t atom_stride, int64_t x_stride, const float* x_scale, int32_t ld_scale,
+                         const int32_t* group, float* dphi, int32_t ld_dphi, float* dmsg, int32_t ld_dmsg, float* dY,
+                         int32_t ld_dY, void* stream);
 
 /* ---------------------------------------------------------------- CP density
  * A[i, x, c] = sum_{e in row i} env[e] * R[e, l(x), c] * msg[m(e), c] * Y[e, x],  l(x) = rank of x

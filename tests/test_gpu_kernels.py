@@ -760,3 +760,57 @@ def test_rank_proj_forward_backward(n_sets, C):
     errs = [rel(a, b) for a, b in zip(ys, ys2)] + [rel(a, b) for a, b in zip(gr, gr2)]
     say("   errs", max(errs))
     assert max(errs) < 1e-5, errs
+
+
+@pytest.mark.parametrize("gathered,K,C,transport", [(False, 32, 96, True), (True, 32, 96, False),
+                                                    (False, 64, 256, True), (True, 16, 160, True),
+                                                    (False, 48, 32, False)])
+def test_density_mix_fused_matches_reference(gathered, K, C, transport):
+    """Factor density fused with the per-rank mix and element scale (face/kernels.py:170-178 then
+    face/model.py:503-506, :530-533), forward and the gradients of phi, msg, Y and the transport
+    sums, against the oracle's factor density + F.linear + scale in fp64 autograd. Ragged rows:
+    a hub row, isolated atoms, N not a multiple of the 4-atom tile."""
+    from face_amd import ops
+    say("density+mix fused", gathered, K, C, transport)
+    B, N, Dw = 16, 57, 64
+    g = _G(N, 500, 5)
+    counts = g.counts
+    E = sum(counts)
+    torch.manual_seed(K + C)
+    phi = torch.randn(E, B, device=DEV, requires_grad=True)
+    msg = torch.randn(N if gathered else E, K, device=DEV, requires_grad=True)
+    Y = torch.randn(E, 20, device=DEV, requires_grad=True)
+    grp = torch.randint(0, 3, (N,), device=DEV, dtype=torch.int32)
+    s_tab = torch.rand(3, 4 * C, device=DEV) + 0.5
+    wm = [torch.randn(C, B * K, device=DEV) / (B * K) ** 0.5 for _ in range(4)]
+    wmt = [w.t().contiguous() for w in wm]
+    D1 = torch.randn(3, N, Dw, device=DEV, requires_grad=True) if transport else None
+    D2 = torch.randn(6, N, Dw, device=DEV, requires_grad=True) if transport else None
+    wt = [torch.randn(C, Dw, device=DEV) / 8, torch.randn(C, Dw, device=DEV) / 8] if transport else [None, None]
+    A = ops.density_mix(s_tab, grp, wm, wmt, wt, D1, D2, phi, msg, Y, g.G, gathered)
+    assert [tuple(a.shape) for a in A] == [(k, N, C) for k in (1, 3, 6, 10)]
+    Gs = [torch.randn_like(a) for a in A]
+    ins = [phi, msg, Y] + ([D1, D2] if transport else [])
+    gr = torch.autograd.grad(sum((a * gg).sum() for a, gg in zip(A, Gs)), ins)
+    # oracle: padded factor density, then the four mixes with the scale
+    c = lambda t: t.detach().double().cpu()
+    insc = [c(t).requires_grad_(True) for t in ins]
+    M = max(counts)
+    col = g.G.col.long().cpu()
+    pd = lambda t: _pad(t, counts, M)
+    msg_e = insc[1][col] if gathered else insc[1]
+    Dd = oops.factor_density(pd(insc[0]), pd(msg_e), pd(insc[2]))             # (N, 20, B K)
+    s = c(s_tab)[grp.long().cpu()].view(N, 4, C)
+    A2 = []
+    for l, (x0, x1) in enumerate(((0, 1), (1, 4), (4, 10), (10, 20))):
+        y = Dd[:, x0:x1, :].permute(1, 0, 2) @ c(wm[l]).T                      # (k_l, N, C)
+        if transport and l in (1, 2):
+            y = y + insc[2 + l] @ c(wt[l - 1]).T
+        A2.append(y * s[None, :, l, :])
+    gr2 = torch.autograd.grad(sum((a * c(gg)).sum() for a, gg in zip(A2, Gs)), insc)
+    errs = [rel(a, b) for a, b in zip(A, A2)] + [rel(a, b) for a, b in zip(gr, gr2)]
+    say("   errs", [f"{e:.1e}" for e in errs])
+    assert max(errs) < TOL, errs
+    # bitwise reproducible (fixed summation order)
+    A3 = ops.density_mix(s_tab, grp, wm, wmt, wt, D1, D2, phi, msg, Y, g.G, gathered)
+    assert all(torch.equal(a, b) for a, b in zip(A, A3))

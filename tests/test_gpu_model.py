@@ -388,3 +388,21 @@ def test_workload4_full_size_properties():
     nodes = run.node_counts()
     say(f"  graph nodes {nodes}")
     assert nodes and nodes.get("kernel", 0) > 0 and nodes.get("memset", 0) == 0
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_factor_density_mix_routes_match_oracle(fused, monkeypatch):
+    """The factorised passes with the fused density + mix kernels and with the unfused route
+    (density written, row GEMM), on the 64-molecule flagship workload cut to 16 molecules,
+    against the oracle."""
+    from face_amd import ops, systems
+    from face_amd.neighbors import build_graph
+    monkeypatch.setattr(ops, "DENSITY_MIX_MAX_ATOMS", 1 << 30 if fused else 0)
+    sts, kw, el, desc = systems.workload(0)
+    sts = sts[:16]
+    say("density+mix route", fused, desc)
+    m = product_model(kw, el)
+    o = m(build_graph(sts, kw["rc"]))
+    Eo, Fo = _oracle_EF(sts, kw, el)
+    dE, dF = check(o["energy"].detach().cpu(), o["forces"].detach().cpu(), Eo, Fo)
+    say(f"  dE/E {dE:.2e}  max|dF|/rms {dF:.2e}")
