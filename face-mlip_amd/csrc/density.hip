@@ -12,6 +12,8 @@
 // tensor (p[l] = D_l, sa = W, sx = N*W) so the channel-mixing GEMMs read contiguous blocks.
 #include "common.h"
 
+#include <cstdlib>
+
 namespace face {
 
 constexpr int kBlock = 256;
@@ -404,6 +406,137 @@ __global__ __launch_bounds__((WPA > 1 ? WPA : kDbWaves) * kWave) void density_bw
 #pragma unroll
                         for (int c = 0; c < KB; ++c) dmsg[e * ld_dmsg + 16 * c + j] = dm[c][r];
                     }
+                }
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------ factor backward, G in LDS
+// Large systems (long rows, K up to 64): one workgroup of 4 waves per atom stages the atom's G
+// (20 x 16 x K) in LDS in two halves of 10 monomials (row stride K + 4: the 16 rows one
+// instruction reads sit on distinct banks), so that G is read from memory once per group of 4
+// edge tiles of the atom instead of once per tile and monomial. Wave w takes tile w of each
+// group and keeps its operands (msg, phi) and accumulators (dphi, dmsg) in registers over both
+// halves; per monomial the two MFMA chains of density_bwd_mfma_kernel run against the LDS copy,
+// and dY[e, x] is complete per monomial.
+constexpr int kDbLWaves = 4;
+
+template <int KB>
+__global__ __launch_bounds__(kDbLWaves * kWave) void density_bwd_lds_kernel(
+    const float* __restrict__ phi, int ld_phi, const float* __restrict__ msg, int ld_msg,
+    const int32_t* __restrict__ msg_row, const float* __restrict__ Y, int ld_Y, const int32_t* __restrict__ row_ptr,
+    RankIn G, float* __restrict__ dphi, int ld_dphi, float* __restrict__ dmsg, int ld_dmsg, float* __restrict__ dY,
+    int ld_dY) {
+    constexpr int K = 16 * KB, GS = K + 4, XH = 10;
+    __shared__ float sG[XH * 16 * GS];
+    __shared__ float sY[kDbLWaves][16 * kDbYS];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), j = lane & 15, q = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int64_t n = blockIdx.x;
+    const v4f z4 = {0.f, 0.f, 0.f, 0.f};
+    const int64_t a = row_ptr[n], bnd = row_ptr[n + 1];
+    const int ntile = (int)((bnd - a + 15) / 16);
+    float* ys = sY[wv];
+#pragma unroll 1
+    for (int g0 = 0; g0 < ntile; g0 += kDbLWaves) {
+        // this wave's tile of the group: operands and accumulators
+        const int t = g0 + wv;
+        const int64_t e0 = a + 16 * (int64_t)t;
+        const int ne = t < ntile ? (int)min((int64_t)16, bnd - e0) : 0;
+        v4f mA[KB], ph4 = z4, dph = z4, dm[KB];
+        float phT[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int c = 0; c < KB; ++c) dm[c] = mA[c] = z4;
+        if (ne > 0) {
+#pragma unroll
+            for (int u = 0; u < 5; ++u) {
+                const int v = u * kWave + lane, tt = v / 20, x = v - tt * 20;
+                ys[tt * kDbYS + x] = tt < ne ? Y[(e0 + tt) * ld_Y + x] : 0.f;
+            }
+            const bool oki = j < ne;
+            const int64_t ei = e0 + min(j, ne - 1);
+            const int64_t rowi = msg_row ? (int64_t)msg_row[ei] : ei;
+#pragma unroll
+            for (int c = 0; c < KB; ++c) mA[c] = oki ? ld4(msg + rowi * ld_msg + 16 * c + 4 * q) : z4;
+            ph4 = oki ? ld4(phi + ei * ld_phi + 4 * q) : z4;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) phT[r] = phi[(e0 + min(4 * q + r, ne - 1)) * ld_phi + j];
+        }
+#pragma unroll 1
+        for (int h = 0; h < 2; ++h) {
+            // stage G[x0 .. x0 + 9] of the atom: 16 rows of K per monomial, row stride GS
+            __syncthreads();                                   // previous half (or group) consumed
+            const int x0 = XH * h;
+            constexpr int NV = XH * 16 * K / 4;
+            for (int v0 = 0; v0 < NV; v0 += 4 * kDbLWaves * kWave) {
+                v4f b4[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int v = v0 + u * kDbLWaves * kWave + tid;
+                    if (v < NV) {
+                        const int xl = v / (4 * K), rem = v - xl * 4 * K;        // rem: float4 index in (16, K)
+                        b4[u] = ld4(G.at(n, x0 + xl) + 4 * rem);
+                    }
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int v = v0 + u * kDbLWaves * kWave + tid;
+                    if (v < NV) {
+                        const int xl = v / (4 * K), rem = v - xl * 4 * K, b = rem / (K / 4), k4 = rem - b * (K / 4);
+                        st4(sG + (xl * 16 + b) * GS + 4 * k4, b4[u]);
+                    }
+                }
+            }
+            __syncthreads();
+            if (ne > 0) {
+                float dyk[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+                for (int xl = 0; xl < XH; ++xl) {
+                    const int x = x0 + xl;
+                    const float* gx = sG + xl * 16 * GS;
+                    v4f sv = z4;
+#pragma unroll
+                    for (int c = 0; c < KB; ++c) {
+                        const v4f gv = *reinterpret_cast<const v4f*>(gx + j * GS + 16 * c + 4 * q);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) sv = mfma_16x16x4(mA[c][r], gv[r], sv);
+                    }
+                    const float yi = ys[j * kDbYS + x];
+#pragma unroll
+                    for (int c = 0; c < KB; ++c)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            dm[c] = mfma_16x16x4(yi * ph4[r], gx[(4 * q + r) * GS + 16 * c + j], dm[c]);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        dph[r] = fmaf(sv[r], ys[(4 * q + r) * kDbYS + x], dph[r]);
+                        float v = sv[r] * phT[r];
+                        v += __shfl_xor(v, 1, kWave);
+                        v += __shfl_xor(v, 2, kWave);
+                        v += __shfl_xor(v, 4, kWave);
+                        v += __shfl_xor(v, 8, kWave);
+                        if (j == xl) dyk[r] = v;
+                    }
+                }
+                if (dY && j < XH) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int te = 4 * q + r;
+                        if (te < ne) dY[(e0 + te) * ld_dY + x0 + j] = dyk[r];
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int te = 4 * q + r;
+            if (te < ne) {
+                const int64_t e = e0 + te;
+                if (dphi) dphi[e * ld_dphi + j] = dph[r];
+                if (dmsg) {
+#pragma unroll
+                    for (int c = 0; c < KB; ++c) dmsg[e * ld_dmsg + 16 * c + j] = dm[c][r];
                 }
             }
         }
@@ -1439,6 +1572,15 @@ extern "C" int face_density_fwd(const float* phi, int32_t ld_phi, const float* m
     return launch_fwd_nx<4>(cpt, grid, lds, st, phi, ld_phi, msg, ld_msg, msg_row, Y, ld_Y, row_ptr, M, B, K, D);
 }
 
+// Route of the factor backward for CSR rows: G staged in LDS per atom for systems of at least 64
+// atoms per CU (density_bwd_lds_kernel), the per-wave kernel below that. FACE_DENSITY_BWD_LDS=0 / 1
+// in the environment forces either (read on every call).
+static bool use_lds_bwd(int64_t N) {
+    const char* e = getenv("FACE_DENSITY_BWD_LDS");
+    if (e && (e[0] == '0' || e[0] == '1')) return e[0] == '1';
+    return N >= (int64_t)device_cu_count() * 64;
+}
+
 extern "C" int face_density_bwd(const float* phi, int32_t ld_phi, const float* msg, int32_t ld_msg,
                                 const int32_t* msg_row, const float* Y, int32_t ld_Y, int32_t NX,
                                 const int32_t* row_ptr, int64_t N, int32_t M, int32_t max_row, int32_t B, int32_t K,
@@ -1456,6 +1598,21 @@ extern "C" int face_density_bwd(const float* phi, int32_t ld_phi, const float* m
     if (NX == 20 && B == 16 && K % 16 == 0 && K <= 64 && ld_phi % 4 == 0 && ld_msg % 4 == 0 && G.sa % 4 == 0 &&
         G.sx % 4 == 0 && ((uintptr_t)phi & 15) == 0 && ((uintptr_t)msg & 15) == 0 && ((uintptr_t)G.p[0] & 15) == 0 &&
         ((uintptr_t)G.p[1] & 15) == 0 && ((uintptr_t)G.p[2] & 15) == 0 && ((uintptr_t)G.p[3] & 15) == 0) {
+        // CSR rows of large systems: G staged in LDS per atom (read once), see density_bwd_lds_kernel
+        if (row_ptr && use_lds_bwd(N)) {
+#define FACE_DBL(KB_)                                                                                          \
+    hipLaunchKernelGGL((density_bwd_lds_kernel<KB_>), dim3((unsigned)N), dim3(kDbLWaves * kWave), 0, st, phi,   \
+                       ld_phi, msg, ld_msg, msg_row, Y, ld_Y, row_ptr, G, dphi, ld_dphi, dmsg, ld_dmsg, dY, ld_dY)
+            switch (K / 16) {
+                case 1: FACE_DBL(1); break;
+                case 2: FACE_DBL(2); break;
+                case 3: FACE_DBL(3); break;
+                default: FACE_DBL(4); break;
+            }
+#undef FACE_DBL
+            FACE_LAUNCH_CHECK();
+            return 0;
+        }
         // small systems: split each atom's monomials over 4 waves (one atom per workgroup)
         const bool split = N < (int64_t)device_cu_count() * 16;
         const dim3 grid(split ? (unsigned)N : (unsigned)((N + kDbWaves - 1) / kDbWaves));

@@ -253,7 +253,10 @@ extern "C" int face_edge_linear_fwd(const float* x, int32_t ld_x, int64_t E, int
     int S = 0, rot = 0, f_chunk = 0;
     if (!lin_layout(F, K, max_lds, S, rot, f_chunk)) return FACE_ERR_UNSUPPORTED;
     const size_t lds = (size_t)f_chunk * S * sizeof(float);
-    constexpr int BB = 2, FB = 2;
+    // 32 edges per tile (BB = 2) for the plain head; the gathered-table form keeps 16 (BB = 1): its
+    // table rows (FB x BB float4 per lane) on top of the 32-edge operands spill at 16 waves
+    const int BB = tab ? 1 : 2;
+    constexpr int FB = 2;
     const int64_t ntile = (E + 16 * BB - 1) / (16 * BB);
     int64_t wgs = device_cu_count();                  // persistent: one 16-wave workgroup per CU
     const int64_t need = (ntile + kLinWaves - 1) / kLinWaves;
@@ -262,10 +265,10 @@ extern "C" int face_edge_linear_fwd(const float* x, int32_t ld_x, int64_t E, int
     const hipStream_t st = (hipStream_t)stream;
 #define FACE_LINF(KB_)                                                                                        \
     do {                                                                                                      \
-        auto kern = b ? (tab ? edge_linear_fwd_kernel<KB_, BB, FB, true, true>                                \
-                             : edge_linear_fwd_kernel<KB_, BB, FB, true, false>)                              \
-                      : (tab ? edge_linear_fwd_kernel<KB_, BB, FB, false, true>                               \
-                             : edge_linear_fwd_kernel<KB_, BB, FB, false, false>);                            \
+        auto kern = b ? (tab ? edge_linear_fwd_kernel<KB_, 1, FB, true, true>                                 \
+                             : edge_linear_fwd_kernel<KB_, 2, FB, true, false>)                               \
+                      : (tab ? edge_linear_fwd_kernel<KB_, 1, FB, false, true>                                \
+                             : edge_linear_fwd_kernel<KB_, 2, FB, false, false>);                             \
         if (lds > 65536 &&                                                                                    \
             hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) !=    \
                 hipSuccess)                                                                                   \

@@ -91,11 +91,18 @@ def _pad(x_edge, counts, M):
     return out * valid.reshape(N, M, *([1] * (x_edge.dim() - 1))).to(x_edge.dtype)
 
 
-@pytest.mark.parametrize("nx,gathered,B,K", [(20, False, 16, 32), (20, True, 16, 32), (4, True, 16, 144),
-                                             (20, False, 8, 16), (4, True, 8, 36)])
-def test_csr_density_ragged_rows(nx, gathered, B, K):
+@pytest.mark.parametrize("nx,gathered,B,K,lds", [(20, False, 16, 32, None), (20, True, 16, 32, None),
+                                                 (4, True, 16, 144, None), (20, False, 8, 16, None),
+                                                 (4, True, 8, 36, None), (20, False, 16, 64, "1"),
+                                                 (20, True, 16, 32, "1"), (20, False, 16, 48, "1")])
+def test_csr_density_ragged_rows(nx, gathered, B, K, lds, monkeypatch):
+    """Factor density forward / backward on ragged CSR rows (a 70-edge hub row, isolated atoms)
+    against the oracle; lds = "1" forces the backward that stages each atom's G in LDS (the route
+    of large systems)."""
     from face_amd import ops
-    say("csr density", nx, gathered, B, K)
+    if lds is not None:
+        monkeypatch.setenv("FACE_DENSITY_BWD_LDS", lds)
+    say("csr density", nx, gathered, B, K, lds)
     g = _G(57, 500, 2)
     counts = g.counts
     E = sum(counts)

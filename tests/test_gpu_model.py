@@ -406,3 +406,19 @@ def test_factor_density_mix_routes_match_oracle(fused, monkeypatch):
     Eo, Fo = _oracle_EF(sts, kw, el)
     dE, dF = check(o["energy"].detach().cpu(), o["forces"].detach().cpu(), Eo, Fo)
     say(f"  dE/E {dE:.2e}  max|dF|/rms {dF:.2e}")
+
+
+def test_workload4_lds_backward_matches_oracle(monkeypatch):
+    """The C256 B16 K64 model with the factor-density backward that stages each atom's G in LDS (the
+    route taken above 64 atoms per CU, forced here on a 1,200-atom box of the same recipe) against
+    the oracle."""
+    from face_amd import systems
+    from face_amd.neighbors import build_graph
+    monkeypatch.setenv("FACE_DENSITY_BWD_LDS", "1")
+    sts, kw, el, desc = systems.workload(4, n_atoms=1200)
+    say("lds backward", desc)
+    m = product_model(kw, el)
+    o = m(build_graph(sts, kw["rc"]))
+    Eo, Fo = _oracle_EF(sts, kw, el)
+    dE, dF = check(o["energy"].detach().cpu(), o["forces"].detach().cpu(), Eo, Fo)
+    say(f"  dE/E {dE:.2e}  max|dF|/rms {dF:.2e}")
