@@ -17,6 +17,8 @@
 // float4 store of y[m][n .. n + 3] per lane and block.
 #include "common.h"
 
+#include <cstdlib>
+
 namespace face {
 
 constexpr int kGemmBB = 2;                 // 16-row blocks per wave
@@ -244,7 +246,186 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
     }
 }
 
+// ------------------------------------------------------------------ K-chunked row GEMM
+// The whole-K weight slice of rows_gemm_kernel leaves narrow column slices once K grows (K = 1024:
+// 32 columns), and every slice re-reads its x rows. Here the weight slice of NS = 16 NB columns
+// (up to 256) is streamed through LDS in chunks of 32 k (row stride 36 floats: the 16 rows one
+// instruction reads sit on distinct banks), double-buffered: the next chunk's loads are issued
+// before the current chunk's products and written to the other buffer after them, one barrier
+// per chunk. As in rows_gemm_kernel each of the 8 waves streams 32 x rows as B operands (two
+// 16-column steps ahead) and keeps its 32 x NS outputs in registers over the whole K loop.
+// Workgroups take the items (problem, 256-row tile, column slice), slice fastest, in an
+// XCD-aware order (workgroup b runs on XCD b % 8, each XCD a contiguous range of items) so that
+// the slices of a row tile read its rows from one L2. The epilogue (bias, beta y, y scale)
+// loads all its operands before its stores.
+constexpr int kKcWaves = 8, kKcK = 32, kKcS = 36;
+
+template <int NB>
+__global__ __launch_bounds__(kKcWaves * kWave) void rows_gemm_kc_kernel(GemmArgs A) {
+    constexpr int NSB = 16 * NB;                              // columns of the slice buffer
+    constexpr int WI = (NSB * (kKcK / 4) + kKcWaves * kWave - 1) / (kKcWaves * kWave);   // float4 items per thread
+    __shared__ float sW[2][NSB * kKcS];
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), j = lane & 15, q = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const v4f z4 = {0.f, 0.f, 0.f, 0.f};
+    const int64_t nbk = gridDim.x, bx = blockIdx.x, xcd = bx & 7, kx = bx >> 3;
+    const int64_t per = nbk >> 3, rem = nbk & 7;
+    const int64_t it = xcd * per + (xcd < rem ? xcd : rem) + kx;
+    int pi = 0;
+#pragma unroll
+    for (int k = 1; k < kGemmMaxProbs; ++k)
+        if (k < A.n_probs && it >= A.p[k].first_block) pi = k;
+    const GemmProb& P = A.p[pi];
+    const int64_t local = it - P.first_block;
+    const int64_t tile = local / P.slices;
+    const int slice = (int)(local - tile * P.slices);
+    const int n0 = slice * A.NS, K = P.k;
+    const int ns = min(A.NS, P.n - n0);
+    // weight chunk staging: item v = col * 8 + k4 (w as (n, k)) or k * (NSB / 4) + c4 (w as (k, n))
+    auto load_w = [&](int k0, v4f (&bw)[WI]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < WI; ++u) {
+            const int v = u * kKcWaves * kWave + tid;
+            v4f t = z4;
+            if (v < NSB * (kKcK / 4)) {
+                if (!A.w_kn) {
+                    const int col = v >> 3, k = k0 + 4 * (v & 7);
+                    if (col < ns && k < K) t = ld4(P.w + (int64_t)(n0 + col) * P.ld_w + k);
+                } else {
+                    const int k = k0 + v / (NSB / 4), c4 = v % (NSB / 4);
+                    if (k < K && 4 * c4 < ns) t = ld4(P.w + (int64_t)k * P.ld_w + n0 + 4 * c4);
+                }
+            }
+            bw[u] = t;
+        }
+    };
+    auto store_w = [&](int buf, const v4f (&bw)[WI]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < WI; ++u) {
+            const int v = u * kKcWaves * kWave + tid;
+            if (v < NSB * (kKcK / 4)) {
+                if (!A.w_kn) {
+                    st4(&sW[buf][(v >> 3) * kKcS + 4 * (v & 7)], bw[u]);
+                } else {
+                    const int kk = v / (NSB / 4), c4 = v % (NSB / 4);
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) sW[buf][(4 * c4 + c) * kKcS + kk] = bw[u][c];
+                }
+            }
+        }
+    };
+    const int64_t m0 = (tile * kKcWaves + wv) * (16 * kGemmBB);
+    int64_t rows[kGemmBB];
+    bool ok[kGemmBB];
+    const float* xr[kGemmBB];
+    const float* xsr[kGemmBB];
+    const float* ysr[kGemmBB];
+#pragma unroll
+    for (int bb = 0; bb < kGemmBB; ++bb) {
+        rows[bb] = m0 + 16 * bb + j;
+        ok[bb] = rows[bb] < P.m;
+        const int64_t rc = ok[bb] ? rows[bb] : 0;
+        xr[bb] = P.x + rc * P.ld_x + 4 * q;
+        const int64_t g = A.group ? (int64_t)A.group[rc % A.period] : 0;
+        xsr[bb] = A.xs ? A.xs + g * A.ld_s + P.s_off + 4 * q : nullptr;
+        ysr[bb] = A.ys ? A.ys + g * A.ld_s + P.s_off + 4 * q : nullptr;
+    }
+    const int nks = K / 16;                                    // 16-column steps of x
+    auto load_x = [&](int ks, v4f (&xv)[kGemmBB]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int bb = 0; bb < kGemmBB; ++bb) {
+            xv[bb] = (ok[bb] && ks < nks) ? ld4(xr[bb] + 16 * ks) : z4;
+            if (A.xs && ok[bb] && ks < nks) xv[bb] *= ld4(xsr[bb] + 16 * ks);
+        }
+    };
+    v4f acc[NB][kGemmBB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int bb = 0; bb < kGemmBB; ++bb) acc[nb][bb] = z4;
+    {
+        v4f bw[WI];
+        load_w(0, bw);
+        store_w(0, bw);
+    }
+    v4f x0[kGemmBB], x1[kGemmBB];
+    load_x(0, x0);
+    load_x(1, x1);
+    __syncthreads();
+    const int nchunk = (K + kKcK - 1) / kKcK;
+#pragma unroll 1
+    for (int c = 0; c < nchunk; ++c) {
+        const int buf = c & 1;
+        const bool more = c + 1 < nchunk;
+        v4f bw[WI];
+        if (more) load_w((c + 1) * kKcK, bw);
+#pragma unroll
+        for (int s2 = 0; s2 < kKcK / 16; ++s2) {
+            const int ks = 2 * c + s2;
+            if (ks >= nks) break;
+            v4f xv[kGemmBB];
+#pragma unroll
+            for (int bb = 0; bb < kGemmBB; ++bb) {
+                xv[bb] = x0[bb];
+                x0[bb] = x1[bb];
+            }
+            load_x(ks + 2, x1);                               // two 16-column steps ahead
+            const float* wrow = sW[buf] + j * kKcS + 16 * s2 + 4 * q;
+            v4f wa = *reinterpret_cast<const v4f*>(wrow);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                const v4f wn = nb + 1 < NB ? *reinterpret_cast<const v4f*>(wrow + 16 * (nb + 1) * kKcS) : wa;
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int bb = 0; bb < kGemmBB; ++bb) acc[nb][bb] = mfma_16x16x4(wa[r], xv[bb][r], acc[nb][bb]);
+                wa = wn;
+            }
+        }
+        if (more) store_w(buf ^ 1, bw);
+        __syncthreads();
+    }
+    // epilogue, loads first (columns past the slice read its last block, rows past m read row 0;
+    // neither is stored)
+    float* yr[kGemmBB];
+#pragma unroll
+    for (int bb = 0; bb < kGemmBB; ++bb) yr[bb] = P.y + (ok[bb] ? rows[bb] : 0) * P.ld_y + 4 * q;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        const int nc = 16 * min(nb, ns / 16 - 1);
+        const v4f bias = A.bias ? ld4(A.bias + n0 + nc + 4 * q) : z4;
+#pragma unroll
+        for (int bb = 0; bb < kGemmBB; ++bb) {
+            v4f v = acc[nb][bb] + bias;
+            if (P.beta != 0.f) v += P.beta * ld4(yr[bb] + n0 + nc);
+            if (A.ys) v *= ld4(ysr[bb] + n0 + nc);
+            acc[nb][bb] = v;
+        }
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+        if (16 * nb < ns) {
+#pragma unroll
+            for (int bb = 0; bb < kGemmBB; ++bb)
+                if (ok[bb]) st4(yr[bb] + n0 + 16 * nb, acc[nb][bb]);
+        }
+    }
+}
+
 static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// Route of a launch: the K-chunked kernel for K >= 1024 with at least two 256-row tiles per CU
+// (whole-K slices are then at most 32 columns wide, and every slice re-reads the x rows);
+// measured on 2M-row problems: K = 1024, n = 256 9.18 against 10.0 ms (in the 100k-atom step's
+// mix forward 9.7 against 11.8 ms); at K = 512 (64-column slices, n = 768) the whole-K kernel
+// stays faster (12.9 against 13.9 ms), at K = 768 with (k, n) weights too (the 100k-atom proj
+// backward 6.3 against 7.7 ms), and so it does for small row counts. FACE_ROWS_GEMM_KC=0 / 1 in
+// the environment forces either kernel.
+static bool use_kc_gemm(int K, int ns_max, int n_widest, int64_t rows) {
+    const char* e = getenv("FACE_ROWS_GEMM_KC");
+    if (e && (e[0] == '0' || e[0] == '1')) return e[0] == '1';
+    return K >= 1024 && n_widest > ns_max && rows >= (int64_t)device_cu_count() * 512;
+}
 
 }  // namespace face
 
@@ -268,23 +449,65 @@ extern "C" int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, 
     const int max_lds = device_max_lds();
     int ns_max = (max_lds / (4 * (K + 4))) / 16 * 16;
     if (ns_max > 160) ns_max = 160;
-    if (ns_max < 16) return FACE_ERR_UNSUPPORTED;
     int n_widest = 16;
     for (int i = 0; i < n_probs; ++i)
         if (probs[i].n > n_widest) n_widest = probs[i].n;
-    int n_sl = (n_widest + ns_max - 1) / ns_max;
+    int n_sl = ns_max >= 16 ? (n_widest + ns_max - 1) / ns_max : 1;
     // small problems: narrower slices until there are two workgroups per CU (each slice re-reads
     // its rows, from L2)
     {
         int64_t wg4 = 0;
         for (int i = 0; i < n_probs; ++i) wg4 += (probs[i].m + 16 * kGemmBB * 4 - 1) / (16 * kGemmBB * 4);
         const int n_cu = device_cu_count();
-        while (wg4 * n_sl < 2 * n_cu && (n_widest + n_sl) / (n_sl + 1) >= 16) ++n_sl;
+        while (ns_max >= 16 && wg4 * n_sl < 2 * n_cu && (n_widest + n_sl) / (n_sl + 1) >= 16) ++n_sl;
     }
     const int NS = ((n_widest + n_sl - 1) / n_sl + 15) / 16 * 16;
     GemmArgs A{};
     A.n_probs = n_probs, A.w_kn = w_kn ? 1 : 0, A.bias = bias, A.xs = x_scale, A.ys = y_scale;
     A.ld_s = ld_scale, A.group = group, A.period = period;
+    int64_t rows_total = 0;
+    for (int i = 0; i < n_probs; ++i) rows_total += probs[i].m > 0 ? probs[i].m : 0;
+    if (use_kc_gemm(K, ns_max, n_widest, rows_total)) {
+        // K-chunked weight slices of up to 256 columns (rows_gemm_kc_kernel)
+        const int nsl = (n_widest + 255) / 256;
+        const int NSk = ((n_widest + nsl - 1) / nsl + 15) / 16 * 16;
+        int64_t blocks = 0;
+        for (int i = 0; i < n_probs; ++i) {
+            const face_lin_problem& s = probs[i];
+            if (s.m < 0 || s.n < 16 || s.n % 16 || s.ld_x < s.k || s.ld_y < s.n || s.ld_w < (w_kn ? s.n : s.k))
+                return FACE_ERR_ARG;
+            if (scaled && (s.s_off < 0 || s.s_off % 4 || s.s_off + (x_scale ? s.k : 0) > ld_scale ||
+                           s.s_off + (y_scale ? s.n : 0) > ld_scale))
+                return FACE_ERR_ARG;
+            if (s.m > 0 && (!s.x || !s.w || !s.y)) return FACE_ERR_ARG;
+            if (s.ld_x % 4 || s.ld_y % 4 || !al16(s.x) || !al16(s.y) || !al16(s.w) || s.ld_w % 4)
+                return FACE_ERR_UNSUPPORTED;
+            GemmProb& p = A.p[i];
+            p.x = s.x, p.ld_x = s.ld_x, p.m = s.m, p.w = s.w, p.ld_w = s.ld_w, p.y = s.y, p.ld_y = s.ld_y;
+            p.n = s.n, p.k = s.k, p.s_off = s.s_off, p.beta = s.beta;
+            p.tiles = (int)((s.m + 16 * kGemmBB * kKcWaves - 1) / (16 * kGemmBB * kKcWaves));
+            p.slices = (s.n + NSk - 1) / NSk;
+            p.first_block = blocks;
+            blocks += (int64_t)p.tiles * p.slices;
+        }
+        for (int i = n_probs; i < kGemmMaxProbs; ++i) A.p[i].first_block = INT64_MAX;
+        if (blocks == 0) return 0;
+        A.NS = NSk;
+        A.items = blocks;
+        const hipStream_t stk = (hipStream_t)stream;
+#define FACE_GEMM_KC(NB_) \
+    hipLaunchKernelGGL(rows_gemm_kc_kernel<NB_>, dim3((unsigned)blocks), dim3(kKcWaves * kWave), 0, stk, A)
+        switch (NSk / 16) {
+            case 1: case 2: case 3: case 4: FACE_GEMM_KC(4); break;
+            case 5: case 6: case 7: case 8: FACE_GEMM_KC(8); break;
+            case 9: case 10: case 11: case 12: FACE_GEMM_KC(12); break;
+            default: FACE_GEMM_KC(16); break;
+        }
+#undef FACE_GEMM_KC
+        FACE_LAUNCH_CHECK();
+        return 0;
+    }
+    if (ns_max < 16) return FACE_ERR_UNSUPPORTED;
     // 16-wave workgroups (4 waves per SIMD hide the row loads) unless that leaves CUs idle; else 8
     // (the staged weight slice serves twice the rows of 4 waves), except for several column
     // slices of a (K, n) weight, measured better with 4

@@ -658,14 +658,19 @@ def _lin_ref(x, w, w_kn, y0, beta, bias, xs, ys, grp, period, s_off):
     return y
 
 
-@pytest.mark.parametrize("case", ["single", "ranks_proj", "ranks_scaled", "kn_xscale", "k512", "empty"])
-def test_rows_linear_matches_torch(case):
+@pytest.mark.parametrize("case,kc", [("single", None), ("ranks_proj", None), ("ranks_scaled", None),
+                                     ("kn_xscale", None), ("k512", None), ("empty", None), ("k1024", None),
+                                     ("ranks_proj", "1"), ("ranks_scaled", "1"), ("kn_xscale", "1"),
+                                     ("k512", "1"), ("empty", "1")])
+def test_rows_linear_matches_torch(case, kc, monkeypatch):
     """y = (beta y + (x * xs) w^T + bias) * ys over up to four problems per launch (mix / tmix /
     proj with the elem_scale factor and their input gradients) vs torch fp64: ragged row counts,
-    weight column slices (ld_w > k), (k, n) weights, K = 512, sliced outputs (n = 480), an empty
-    problem beside full ones."""
+    weight column slices (ld_w > k), (k, n) weights, K = 512 and 1024, sliced outputs (n = 480), an
+    empty problem beside full ones. kc = "1" forces the K-chunked kernel (the route of long K)."""
     from face_amd import ops
-    say("rows_linear", case)
+    if kc is not None:
+        monkeypatch.setenv("FACE_ROWS_GEMM_KC", kc)
+    say("rows_linear", case, kc)
     torch.manual_seed(len(case))
     N, C = 1000, 160
     grp = torch.randint(0, 3, (N,), device=DEV, dtype=torch.int32)
@@ -698,6 +703,11 @@ def test_rows_linear_matches_torch(case):
         x = torch.randn(6 * N, 512, device=DEV)
         w = torch.randn(C, 512, device=DEV) / 512 ** 0.5
         probs = [(x, w, torch.randn(6 * N, C, device=DEV), 0, 1.0)]
+    elif case == "k1024":                                                    # the mix of a K = 64 model
+        ys = tab
+        x = torch.randn(40 * N, 1024, device=DEV)
+        w = torch.randn(C, 1024, device=DEV) / 32
+        probs = [(x, w, torch.randn(40 * N, C, device=DEV), C, 1.0)]
     else:
         x = torch.randn(0, C, device=DEV)
         probs = [(x, torch.randn(C, C, device=DEV), torch.empty(0, C, device=DEV), 0, 0.0),
