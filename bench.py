@@ -65,7 +65,7 @@ KERNEL_FAMILY = {
 # kernel family -> kernel functions of libface_hip.so it stands for (rocprofv3 names, namespace face)
 FAMILY_KERNELS = {
     "density_fwd": ["density_fwd_mfma_kernel", "density_fwd_kernel"],
-    "density_bwd": ["density_bwd_mfma_kernel", "density_bwd_kernel"],
+    "density_bwd": ["density_bwd_mfma_kernel", "density_bwd_lds_kernel", "density_bwd_kernel"],
     "density_mix_fwd": ["density_mix_fwd_kernel"], "density_mix_bwd": ["density_mix_bwd_kernel"],
     "cp_density_fwd": ["cp_density_fwd_wave_kernel", "cp_density_fwd_kernel"],
     "cp_density_bwd": ["cp_density_bwd_mfma_kernel", "cp_density_bwd_kernel"],
@@ -75,11 +75,12 @@ FAMILY_KERNELS = {
     "dir_feats_fwd": ["dir_feats_fwd_kernel"], "dir_feats_bwd": ["dir_feats_bwd_edge_kernel",
                                                                  "dir_feats_bwd_node_kernel"],
     "node_fwd": ["node_fwd_kernel"], "node_bwd": ["node_bwd_kernel"],
-    "edge_geom_fwd": ["edge_geom_fwd_kernel"], "edge_geom_bwd": ["edge_geom_bwd_kernel"],
-    "force_scatter": ["force_scatter_kernel"], "gather_rows_bwd": ["gather_rows_bwd_kernel"],
+    "edge_geom_fwd": ["edge_geom_fwd_kernel"], "edge_geom_bwd": ["edge_geom_bwd_seg_kernel", "edge_geom_bwd_kernel"],
+    "force_scatter": ["force_scatter_rows_kernel", "force_scatter_kernel"],
+    "gather_rows_bwd": ["gather_rows_bwd_kernel"],
     "radial_fwd": ["radial_fwd_kernel"], "radial_bwd": ["radial_bwd_kernel"],
     "edge_linear_fwd": ["edge_linear_fwd_kernel"], "edge_linear_bwd": ["edge_linear_bwd_kernel"],
-    "rows_gemm": ["rows_gemm_kernel"], "eq_gate_fwd": ["eq_gate_fwd_kernel"], "eq_gate_bwd": ["eq_gate_bwd_kernel"],
+    "rows_gemm": ["rows_gemm_kernel", "rows_gemm_kc_kernel"], "eq_gate_fwd": ["eq_gate_fwd_kernel"], "eq_gate_bwd": ["eq_gate_bwd_kernel"],
     "layer_norm_fwd": ["layer_norm_fwd_kernel"], "layer_norm_bwd": ["layer_norm_bwd_kernel"],
     "spline_order": ["spline_zero_kernel", "spline_count_kernel", "spline_scan_kernel", "spline_place_kernel"],
     "radial_spline_fwd": ["radial_spline_fwd_kernel"], "radial_spline_bwd": ["radial_spline_bwd_kernel"],
@@ -537,6 +538,19 @@ def pmc_summary(fetch_dir, write_dir, probe_log, out_path):
                "alg bytes/launch | traffic/alg |\n|---|---:|---:|---:|---:|\n")
     for fam, (t, a, n) in fam_t.items():
         out.append(f"| {fam} | {n} | {t / n:.0f} | {a / n if a else '-'} | {f'{t / a:.3f}' if a else '-'} |\n")
+    # register / scratch footprint of every library kernel of the run (same dispatch records):
+    # Scratch_Size is the per-lane private segment, non-zero when registers spill
+    res = {}
+    for r in rows["FETCH_SIZE"]:
+        if "face::" in r["Kernel_Name"]:
+            nm = r["Kernel_Name"].replace("void ", "").split("(")[0].replace("face::", "")
+            res[nm] = (r.get("VGPR_Count"), r.get("Accum_VGPR_Count"), r.get("SGPR_Count"), r.get("LDS_Block_Size"),
+                       r.get("Scratch_Size"), r.get("Workgroup_Size"))
+    out.append("\nKernel resources (dispatch records of the same run; scratch = per-lane private segment "
+               "bytes, non-zero when registers spill):\n\n| kernel | VGPR | AGPR | SGPR | LDS bytes | scratch | "
+               "workgroup |\n|---|---:|---:|---:|---:|---:|---:|\n")
+    for nm, v in sorted(res.items()):
+        out.append(f"| `{nm}` | " + " | ".join(str(x) for x in v) + " |\n")
     open(out_path, "w").write("".join(out))
     print("".join(out))
 
@@ -570,11 +584,10 @@ def sq_summary(out_path, title, probe_args, *dirs):
             data[k][r["Counter_Name"]].append(float(r["Counter_Value"]))
             data[k]["_dur_ns"].append(float(r["End_Timestamp"]) - float(r["Start_Timestamp"]))
     out = [f"# SQ counters: {title}\n\nCommands (repo root, MI355X, ROCm 7.2), one pass per counter group:\n\n```\n"]
-    for i, P in enumerate(SQ_PASSES):
+    for P, d in zip(SQ_PASSES, dirs):
         out.append(f"rocprofv3 --pmc {P} --kernel-include-regex 'face::' --output-format csv "
-                   f"-d gpurun_out/sq{i + 1} -o p -- python -u bench.py --pmc-probe {probe_args}\n")
-    out.append(f"python bench.py --sq-summary {out_path} '{title}' '{probe_args}' "
-               + " ".join(f"gpurun_out/sq{i + 1}" for i in range(len(dirs))) + "\n```\n\n")
+                   f"-d {d} -o p -- python -u bench.py --pmc-probe {probe_args}\n")
+    out.append(f"python bench.py --sq-summary {out_path} '{title}' '{probe_args}' " + " ".join(dirs) + "\n```\n\n")
     out.append("Per dispatch averages. wave-cycle fractions: time a wave spends waiting on anything / on "
                "s_waitcnt / issuing. mfma_util: SQ_VALU_MFMA_BUSY_CYCLES over (1024 SIMDs x duration x 2.4 GHz).\n\n"
                "| kernel | dispatches | waves | us | wait_any | wait_inst | active | mfma insts | "
