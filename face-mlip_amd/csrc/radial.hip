@@ -350,6 +350,26 @@ struct SplineVec<4> {
     static __device__ __forceinline__ float sum(v4f v) { return (v[0] + v[1]) + (v[2] + v[3]); }
 };
 
+// The Hermite terms with their products fused in one fixed order (every kernel evaluating a spline
+// rounds the same way):  herm = a dp + (b m0 + c m1),  with dp = p1 - p0 the table difference.
+__device__ __forceinline__ float herm(float a, float dp, float b, float m0, float c, float m1) {
+    return __builtin_fmaf(a, dp, __builtin_fmaf(b, m0, c * m1));
+}
+__device__ __forceinline__ v4f herm(float a, v4f dp, float b, v4f m0, float c, v4f m1) {
+    v4f o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = herm(a, dp[k], b, m0[k], c, m1[k]);
+    return o;
+}
+// acc + x y, fused per component
+__device__ __forceinline__ float fma_acc(float acc, float x, float y) { return __builtin_fmaf(x, y, acc); }
+__device__ __forceinline__ v4f fma_acc(v4f acc, v4f x, v4f y) {
+    v4f o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) o[k] = __builtin_fmaf(x[k], y[k], acc[k]);
+    return o;
+}
+
 template <int L, int W>
 __global__ __launch_bounds__(256) void radial_spline_fwd_kernel(const float* __restrict__ r,
                                                                 const int32_t* __restrict__ pair, int64_t E,
@@ -372,7 +392,7 @@ __global__ __launch_bounds__(256) void radial_spline_fwd_kernel(const float* __r
     for (int f = W * l; f < S.F; f += W * L) {
         const typename V::T p0 = V::ld(T0 + f), p1 = V::ld(T0 + S.F + f);
         const typename V::T m0 = V::ld(D0 + f) * S.dr, m1 = V::ld(D0 + S.F + f) * S.dr;
-        const typename V::T v = p0 + (h01 * (p1 - p0) + (h10 * m0 + h11 * m1));
+        const typename V::T v = p0 + herm(h01, p1 - p0, h10, m0, h11, m1);
         if (f < nb)
             V::st(phi + e * ld_phi + f, v * ev);
         else
@@ -410,12 +430,12 @@ __global__ __launch_bounds__(256) void radial_spline_bwd_kernel(const float* __r
         const typename V::T p0 = V::ld(T0 + f), p1 = V::ld(T0 + S.F + f);
         const typename V::T m0 = V::ld(D0 + f) * S.dr, m1 = V::ld(D0 + S.F + f) * S.dr;
         const typename V::T dp = p1 - p0;
-        const typename V::T dv = d01 * dp + (d10 * m0 + d11 * m1);
+        const typename V::T dv = herm(d01, dp, d10, m0, d11, m1);
         if (lo) {
-            se += gv * (p0 + (h01 * dp + (h10 * m0 + h11 * m1)));
-            sr += (gv * ev) * dv;
+            se = fma_acc(se, gv, p0 + herm(h01, dp, h10, m0, h11, m1));
+            sr = fma_acc(sr, gv * ev, dv);
         } else {
-            sr += gv * dv;
+            sr = fma_acc(sr, gv, dv);
         }
     }
     float srs = group_sum(V::sum(sr), L);
@@ -426,7 +446,176 @@ __global__ __launch_bounds__(256) void radial_spline_bwd_kernel(const float* __r
     }
 }
 
+// Cell-run form of the two kernels above, for edges visited in table-cell order (`order` from
+// the counting sort below; ~E / (P G) consecutive edges share one cell): a wave walks 64
+// consecutive positions of the order, lane l owning column quads l + 64 s (s < NS, rows
+// float4-aligned), and keeps the current cell's four table rows (T, dT at grid points i, i + 1)
+// in registers, reloading them only where the cell changes. Each edge's phi / R row (forward) or
+// upstream-gradient row (backward) is one coalesced row access; the per-edge quantities (edge,
+// cell, t, env) are loaded once per wave and read back with v_readlane. Lane l's columns and the
+// order of its partial sums are those of the L = 64 kernels above, so the results are the same.
+constexpr int kRunLen = 64;                            // positions of the order per wave
+
+struct RunEdges {                                      // this lane's edge of the wave's run
+    int32_t e, cell;
+    float t, ev;
+    int inside;
+};
+
+__device__ __forceinline__ RunEdges run_edges(const float* __restrict__ r, const int32_t* __restrict__ pair,
+                                              const float* __restrict__ env, const int32_t* __restrict__ order,
+                                              int64_t q0, int n, int lane, const SplineTab& S) {
+    RunEdges u{0, 0, 0.f, 0.f, 0};
+    if (lane < n) {
+        u.e = order[q0 + lane];
+        const SplineCell c = spline_cell(r[u.e], pair[u.e], S);
+        u.cell = (int32_t)(c.row / S.F);
+        u.t = c.t;
+        u.inside = c.inside;
+        u.ev = env ? env[u.e] : 1.f;
+    }
+    return u;
+}
+
+template <int NS>
+__global__ __launch_bounds__(256) void radial_spline_run_fwd_kernel(const float* __restrict__ r,
+                                                                    const int32_t* __restrict__ pair, int64_t E,
+                                                                    SplineTab S, const float* __restrict__ env, int nb,
+                                                                    const int32_t* __restrict__ order,
+                                                                    float* __restrict__ phi, int ld_phi,
+                                                                    float* __restrict__ R, int ld_R) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t q0 = ((int64_t)blockIdx.x * (blockDim.x / kWave) +
+                        __builtin_amdgcn_readfirstlane(threadIdx.x / kWave)) * kRunLen;
+    if (q0 >= E) return;                               // uniform per wave
+    const int n = (int)min((int64_t)kRunLen, E - q0);
+    const RunEdges u = run_edges(r, pair, env, order, q0, n, lane, S);
+    v4f p0[NS], p1[NS], m0[NS], m1[NS];
+    int32_t cur = -1;
+    for (int k = 0; k < n; ++k) {
+        const int32_t cell = __builtin_amdgcn_readlane(u.cell, k);
+        const int64_t e = __builtin_amdgcn_readlane(u.e, k);
+        if (cell != cur) {                             // uniform: reload the cell's rows
+            cur = cell;
+            const float* T0 = S.T + (int64_t)cell * S.F;
+            const float* D0 = S.dT + (int64_t)cell * S.F;
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                const int f = 4 * (lane + kWave * s);
+                if (f < S.F) {
+                    p0[s] = ld4(T0 + f), p1[s] = ld4(T0 + S.F + f);
+                    m0[s] = ld4(D0 + f) * S.dr, m1[s] = ld4(D0 + S.F + f) * S.dr;
+                }
+            }
+        }
+        const float t = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(u.t), k));
+        const float ev = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(u.ev), k));
+        const float t2 = t * t, t3 = t2 * t;
+        const float h10 = t3 - 2.f * t2 + t, h01 = -2.f * t3 + 3.f * t2, h11 = t3 - t2;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const int f = 4 * (lane + kWave * s);
+            if (f < S.F) {
+                const v4f v = p0[s] + herm(h01, p1[s] - p0[s], h10, m0[s], h11, m1[s]);
+                if (f < nb)
+                    st4(phi + e * ld_phi + f, v * ev);
+                else
+                    st4(R + e * ld_R + f - nb, v);
+            }
+        }
+    }
+}
+
+template <int NS>
+__global__ __launch_bounds__(256) void radial_spline_run_bwd_kernel(const float* __restrict__ r,
+                                                                    const int32_t* __restrict__ pair, int64_t E,
+                                                                    SplineTab S, const float* __restrict__ env, int nb,
+                                                                    const int32_t* __restrict__ order,
+                                                                    const float* __restrict__ gphi, int ld_gphi,
+                                                                    const float* __restrict__ gR, int ld_gR,
+                                                                    float* __restrict__ gr, float* __restrict__ genv) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t q0 = ((int64_t)blockIdx.x * (blockDim.x / kWave) +
+                        __builtin_amdgcn_readfirstlane(threadIdx.x / kWave)) * kRunLen;
+    if (q0 >= E) return;                               // uniform per wave
+    const int n = (int)min((int64_t)kRunLen, E - q0);
+    const RunEdges u = run_edges(r, pair, env, order, q0, n, lane, S);
+    const v4f z4 = {0.f, 0.f, 0.f, 0.f};
+    // upstream gradient of column quad s of edge e (zero where its operand is absent)
+    auto load_g = [&](int64_t e, v4f (&g)[NS]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const int f = 4 * (lane + kWave * s);
+            g[s] = z4;
+            if (f < S.F) {
+                if (f < nb) {
+                    if (gphi) g[s] = ld4(gphi + e * ld_gphi + f);
+                } else if (gR) {
+                    g[s] = ld4(gR + e * ld_gR + f - nb);
+                }
+            }
+        }
+    };
+    v4f p0[NS], p1[NS], m0[NS], m1[NS], g[NS], gn[NS];
+    load_g(__builtin_amdgcn_readlane(u.e, 0), gn);
+    int32_t cur = -1;
+    for (int k = 0; k < n; ++k) {
+        const int32_t cell = __builtin_amdgcn_readlane(u.cell, k);
+        const int64_t e = __builtin_amdgcn_readlane(u.e, k);
+#pragma unroll
+        for (int s = 0; s < NS; ++s) g[s] = gn[s];
+        if (k + 1 < n) load_g(__builtin_amdgcn_readlane(u.e, k + 1), gn);   // next edge's row in flight
+        if (cell != cur) {
+            cur = cell;
+            const float* T0 = S.T + (int64_t)cell * S.F;
+            const float* D0 = S.dT + (int64_t)cell * S.F;
+#pragma unroll
+            for (int s = 0; s < NS; ++s) {
+                const int f = 4 * (lane + kWave * s);
+                if (f < S.F) {
+                    p0[s] = ld4(T0 + f), p1[s] = ld4(T0 + S.F + f);
+                    m0[s] = ld4(D0 + f) * S.dr, m1[s] = ld4(D0 + S.F + f) * S.dr;
+                }
+            }
+        }
+        const float t = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(u.t), k));
+        const float ev = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(u.ev), k));
+        const int inside = __builtin_amdgcn_readlane(u.inside, k);
+        const float t2 = t * t, t3 = t2 * t;
+        const float h10 = t3 - 2.f * t2 + t, h01 = -2.f * t3 + 3.f * t2, h11 = t3 - t2;
+        const float d10 = 3.f * t2 - 4.f * t + 1.f, d01 = -6.f * t2 + 6.f * t, d11 = 3.f * t2 - 2.f * t;
+        v4f sr = z4, se = z4;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+            const int f = 4 * (lane + kWave * s);
+            if (f < S.F) {
+                const v4f dp = p1[s] - p0[s];
+                const v4f dv = herm(d01, dp, d10, m0[s], d11, m1[s]);
+                if (f < nb) {
+                    se = fma_acc(se, g[s], p0[s] + herm(h01, dp, h10, m0[s], h11, m1[s]));
+                    sr = fma_acc(sr, g[s] * ev, dv);
+                } else {
+                    sr = fma_acc(sr, g[s], dv);
+                }
+            }
+        }
+        const float srs = group_sum(SplineVec<4>::sum(sr), kWave);
+        const float ses = group_sum(SplineVec<4>::sum(se), kWave);
+        if (lane == 0) {
+            gr[e] = inside ? srs / S.dr : 0.f;
+            if (genv) genv[e] = ses;
+        }
+    }
+}
+
 static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+// column-quad slots per lane of the cell-run kernels (edges given in table-cell order, float4
+// rows, up to 5 x 64 quads), or 0 for the per-edge kernels
+static int run_slots(const int32_t* order, bool vec, int F) {
+    const int ns = (F / 4 + kWave - 1) / kWave;
+    return (order && vec && ns <= 5) ? ns : 0;
+}
 
 // lanes per edge: a power of two about the number of column groups (W columns each), at most 64
 static int spline_lanes(int F, int W) {
@@ -573,6 +762,17 @@ extern "C" int face_radial_spline_fwd(const float* r, const int32_t* pair, int64
     const hipStream_t st = (hipStream_t)stream;
 #define FACE_SPLINE(K_, L_, W_) \
     hipLaunchKernelGGL((K_<L_, W_>), grid, block, 0, st, r, pair, E, tab, env, nb, order, ARGS_)
+#define FACE_SPLINE_RUN(K_, NS_)                                                               \
+    do {                                                                                       \
+        const dim3 rgrid((unsigned)(((E + kRunLen - 1) / kRunLen + 3) / 4)), rblock(4 * kWave); \
+        switch (NS_) {                                                                         \
+            case 1: hipLaunchKernelGGL((K_<1>), rgrid, rblock, 0, st, r, pair, E, tab, env, nb, order, ARGS_); break; \
+            case 2: hipLaunchKernelGGL((K_<2>), rgrid, rblock, 0, st, r, pair, E, tab, env, nb, order, ARGS_); break; \
+            case 3: hipLaunchKernelGGL((K_<3>), rgrid, rblock, 0, st, r, pair, E, tab, env, nb, order, ARGS_); break; \
+            case 4: hipLaunchKernelGGL((K_<4>), rgrid, rblock, 0, st, r, pair, E, tab, env, nb, order, ARGS_); break; \
+            default: hipLaunchKernelGGL((K_<5>), rgrid, rblock, 0, st, r, pair, E, tab, env, nb, order, ARGS_); break; \
+        }                                                                                      \
+    } while (0)
 #define FACE_SPLINE_L(K_, W_)                           \
     switch (L) {                                        \
         case 4: FACE_SPLINE(K_, 4, W_); break;          \
@@ -582,7 +782,10 @@ extern "C" int face_radial_spline_fwd(const float* r, const int32_t* pair, int64
         default: FACE_SPLINE(K_, 64, W_); break;        \
     }
 #define ARGS_ phi, ld_phi, R, ld_R
-    if (vec) {
+    const int ns = run_slots(order, vec, F);
+    if (ns > 0) {
+        FACE_SPLINE_RUN(radial_spline_run_fwd_kernel, ns);
+    } else if (vec) {
         FACE_SPLINE_L(radial_spline_fwd_kernel, 4)
     } else {
         FACE_SPLINE_L(radial_spline_fwd_kernel, 1)
@@ -607,13 +810,17 @@ extern "C" int face_radial_spline_bwd(const float* r, const int32_t* pair, int64
     const dim3 grid((unsigned)((E * L + 255) / 256)), block(256);
     const hipStream_t st = (hipStream_t)stream;
 #define ARGS_ gphi, ld_gphi, gR, ld_gR, gr, genv
-    if (vec) {
+    const int ns = run_slots(order, vec, F);
+    if (ns > 0) {
+        FACE_SPLINE_RUN(radial_spline_run_bwd_kernel, ns);
+    } else if (vec) {
         FACE_SPLINE_L(radial_spline_bwd_kernel, 4)
     } else {
         FACE_SPLINE_L(radial_spline_bwd_kernel, 1)
     }
 #undef ARGS_
 #undef FACE_SPLINE_L
+#undef FACE_SPLINE_RUN
 #undef FACE_SPLINE
     FACE_LAUNCH_CHECK();
     return 0;

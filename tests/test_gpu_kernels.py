@@ -460,13 +460,16 @@ def test_radial_spline_without_envelope_as_a_reference_binding():
     assert max(rel(S, S2.reshape(E, F)), rel(gr, gr2.reshape(-1))) < TOL
 
 
-def test_radial_spline_order_is_a_cell_sorted_permutation():
+@pytest.mark.parametrize("P,G,F,nb,E", [(5, 700, 24, 8, 20000), (9, 4096, 16 + 4 * 160, 16, 150000),
+                                         (4, 4096, 16 + 4 * 256, 16, 40000), (2, 40, 8 + 4 * 32, 8, 3001)])
+def test_radial_spline_order_is_a_cell_sorted_permutation(P, G, F, nb, E):
     """face_radial_spline_order: a permutation of the edges with non-decreasing table cell
     (pair * G + grid interval, the same cell the spline kernels use), including radii past the
-    grid's end (last interval); the spline outputs in that order equal the unordered ones bitwise."""
+    grid's end (last interval); the spline outputs in that order (the cell-run kernels, which
+    keep each cell's table rows in registers over its run of edges) equal the unordered per-edge
+    kernels' bitwise, at the CP widths (16 + 4C columns, C = 160 and 256) too."""
     from face_amd._lib import call, ptr, stream_of
-    say("spline order")
-    P, G, F, nb, E = 5, 700, 24, 8, 20000
+    say("spline order", P, G, F, nb, E)
     rc = 4.0
     dr = rc / (G - 1)
     rng = np.random.default_rng(9)
