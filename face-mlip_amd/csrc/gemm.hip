@@ -15,6 +15,13 @@
 // of 16 columns ahead, and the wave keeps its 32 x NS outputs in registers over the whole K
 // loop. D = W . x^T holds output column 4q + r of row j in register r of lane j + 16q, one
 // float4 store of y[m][n .. n + 3] per lane and block.
+//
+// Side operands never wait on memory inside or after the K loop: the scale rows of every group
+// (the ys columns of the slice, the xs columns of the problem) and the slice's bias are staged
+// in LDS with the weight slice, and beta y is loaded into the accumulators before the K loop
+// (its loads complete under the first x rows'). The epilogue therefore reads LDS only, then
+// stores. (Epilogue loads from memory cost one full memory latency each: with 80 accumulator
+// registers held, the compiler could not keep them in flight together.)
 #include "common.h"
 
 #include <cstdlib>
@@ -23,6 +30,7 @@ namespace face {
 
 constexpr int kGemmBB = 2;                 // 16-row blocks per wave
 constexpr int kGemmMaxProbs = 4;
+constexpr int kGemmMaxGroups = 64;         // scale-table rows (elements) staged in LDS
 
 struct GemmProb {
     const float* x;
@@ -44,12 +52,47 @@ struct GemmArgs {
     int64_t total_cost;
     int n_probs, w_kn, NS;
     const float *bias, *xs, *ys;
-    int ld_s;
+    int ld_s, n_groups;
     const int32_t* group;
     int64_t period;
+    int side_off, kmax;                    // LDS offset (floats) of the side tables; largest K
 };
 
-template <int NB, int NW, bool PERSIST>
+// LDS side tables of a launch, after the weight slice (floats): ys [n_groups][16 NB] (slice
+// columns), xs [n_groups][kmax] (problem columns), bias [16 NB] -- each present only when its
+// operand is.
+struct GemmSide {
+    float *ys, *xs, *bias;
+    __device__ __forceinline__ GemmSide(float* base, const GemmArgs& A, int nsb) {
+        ys = base;
+        xs = ys + (A.ys ? A.n_groups * nsb : 0);
+        bias = xs + (A.xs ? A.n_groups * A.kmax : 0);
+    }
+};
+
+// Stage the side tables of (problem P, slice n0 .. n0 + ns) into LDS (callers synchronise);
+// columns past ns are zero. The xs rows are restaged only with a new problem.
+__device__ __forceinline__ void gemm_stage_side(const GemmArgs& A, const GemmProb& P, const GemmSide& S, int nsb, int n0,
+                                                int ns, bool new_prob) {
+    const int tid = threadIdx.x, nthr = blockDim.x;
+    if (A.ys) {
+        for (int v = tid; v < A.n_groups * nsb; v += nthr) {
+            const int g = v / nsb, c = v - g * nsb;
+            S.ys[v] = c < ns ? A.ys[(int64_t)g * A.ld_s + P.s_off + n0 + c] : 0.f;
+        }
+    }
+    if (A.xs && new_prob) {
+        for (int v = tid; v < A.n_groups * P.k; v += nthr) {
+            const int g = v / P.k, k = v - g * P.k;
+            S.xs[g * A.kmax + k] = A.xs[(int64_t)g * A.ld_s + P.s_off + k];
+        }
+    }
+    if (A.bias) {
+        for (int c = tid; c < nsb; c += nthr) S.bias[c] = c < ns ? A.bias[n0 + c] : 0.f;
+    }
+}
+
+template <int NB, int NW, bool PERSIST, bool XS>
 __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
     extern __shared__ float sW[];
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
@@ -83,6 +126,7 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
         const int K = P.k, SK = K + 4;
         const int n0 = slice * A.NS;
         const int ns = min(A.NS, P.n - n0);                             // a multiple of 16
+        const GemmSide side(sW + A.side_off, A, 16 * NB);
         if (pi != cur_pi || slice != cur_slice) {
             // stage W[n0 : n0 + ns, :] as rows of K (+ 4 pad); rows ns .. 16 NB - 1 are zero, so
             // the MFMA loop below runs all NB blocks without branches
@@ -129,38 +173,43 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
                     }
                 }
             }
+            gemm_stage_side(A, P, side, 16 * NB, n0, ns, pi != cur_pi);
             __syncthreads();
             cur_pi = pi, cur_slice = slice;
         }
         const int64_t m0 = (tile * NW + wv) * (16 * kGemmBB);
         if (m0 >= P.m) return;
-        int64_t rows[kGemmBB];
         bool ok[kGemmBB];
         const float* xr[kGemmBB];
-        const float* xsr[kGemmBB];
-        const float* ysr[kGemmBB];
+        float* yr[kGemmBB];
+        int xso[kGemmBB], yso[kGemmBB];                                  // LDS offsets of the row's scale rows
 #pragma unroll
         for (int bb = 0; bb < kGemmBB; ++bb) {
-            rows[bb] = m0 + 16 * bb + j;
-            ok[bb] = rows[bb] < P.m;
-            const int64_t rc = ok[bb] ? rows[bb] : 0;
+            const int64_t row = m0 + 16 * bb + j;
+            ok[bb] = row < P.m;
+            const int64_t rc = ok[bb] ? row : 0;
             xr[bb] = P.x + rc * P.ld_x + 4 * q;
-            const int64_t g = A.group ? (int64_t)A.group[rc % A.period] : 0;
-            xsr[bb] = A.xs ? A.xs + g * A.ld_s + P.s_off + 4 * q : nullptr;
-            ysr[bb] = A.ys ? A.ys + g * A.ld_s + P.s_off + 4 * q : nullptr;
+            yr[bb] = P.y + rc * P.ld_y + 4 * q;
+            const int g = A.group ? A.group[rc % A.period] : 0;
+            xso[bb] = g * A.kmax + 4 * q;
+            yso[bb] = g * (16 * NB) + 4 * q;
         }
         auto load_x = [&](int kc, v4f (&xv)[kGemmBB]) {
 #pragma unroll
-            for (int bb = 0; bb < kGemmBB; ++bb) {
-                xv[bb] = ok[bb] ? ld4(xr[bb] + 16 * kc) : z4;
-                if (A.xs) xv[bb] *= ld4(xsr[bb] + 16 * kc);
-            }
+            for (int bb = 0; bb < kGemmBB; ++bb) xv[bb] = ok[bb] ? ld4(xr[bb] + 16 * kc) : z4;
         };
+        // accumulators start at beta y (loads in flight with the first x rows), else zero
         v4f acc[NB][kGemmBB];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-            for (int bb = 0; bb < kGemmBB; ++bb) acc[nb][bb] = z4;
+            for (int bb = 0; bb < kGemmBB; ++bb) {
+                acc[nb][bb] = z4;
+                if (P.beta != 0.f && ok[bb] && 16 * nb < ns) {
+                    acc[nb][bb] = ld4(yr[bb] + n0 + 16 * nb);
+                    if (P.beta != 1.f) acc[nb][bb] *= P.beta;
+                }
+            }
         const int nkc = K / 16;
         v4f xn[kGemmBB];
         load_x(0, xn);
@@ -168,7 +217,10 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
         for (int kc = 0; kc < nkc; ++kc) {
             v4f xv[kGemmBB];
 #pragma unroll
-            for (int bb = 0; bb < kGemmBB; ++bb) xv[bb] = xn[bb];
+            for (int bb = 0; bb < kGemmBB; ++bb) {
+                xv[bb] = xn[bb];
+                if (XS) xv[bb] *= *reinterpret_cast<const v4f*>(side.xs + xso[bb] + 16 * kc);
+            }
             if (kc + 1 < nkc) load_x(kc + 1, xn);
             // weight blocks read one block ahead of their MFMAs (LDS latency under the MFMA chain)
             const float* wrow = sW + j * SK + 16 * kc + 4 * q;
@@ -186,55 +238,21 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
             // the read of block nb + 2, so every read has a block of MFMAs to hide under
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
-                if (nb == 0) __builtin_amdgcn_sched_group_barrier(0x100, NB > 1 ? 2 : 1, 0);
+                if (nb == 0) __builtin_amdgcn_sched_group_barrier(0x100, (NB > 1 ? 2 : 1) + (XS ? kGemmBB : 0), 0);
                 __builtin_amdgcn_sched_group_barrier(0x008, 4 * kGemmBB, 0);
                 if (nb + 2 < NB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             }
         }
-        if (PERSIST) {
-            // epilogue, loads first: bias, beta y and the y scale folded into the accumulators
-            // (columns past the slice read its last block, rows past m read row 0; neither is
-            // stored), then the stores, so no wait for a load ever covers a store
-            float* yr[kGemmBB];
+        // epilogue: bias and y scale from LDS, then the stores
 #pragma unroll
-            for (int bb = 0; bb < kGemmBB; ++bb) yr[bb] = P.y + (ok[bb] ? rows[bb] : 0) * P.ld_y + 4 * q;
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-                const int nc = 16 * min(nb, ns / 16 - 1);
-                const v4f bias = A.bias ? ld4(A.bias + n0 + nc + 4 * q) : z4;
+        for (int nb = 0; nb < NB; ++nb) {
+            if (16 * nb < ns) {
+                const v4f bias = A.bias ? *reinterpret_cast<const v4f*>(side.bias + 16 * nb + 4 * q) : z4;
 #pragma unroll
                 for (int bb = 0; bb < kGemmBB; ++bb) {
                     v4f v = acc[nb][bb] + bias;
-                    if (P.beta != 0.f) v += P.beta * ld4(yr[bb] + n0 + nc);
-                    if (A.ys) v *= ld4(ysr[bb] + n0 + nc);
-                    acc[nb][bb] = v;
-                }
-            }
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-                if (16 * nb < ns) {
-#pragma unroll
-                    for (int bb = 0; bb < kGemmBB; ++bb)
-                        if (ok[bb]) st4(yr[bb] + n0 + 16 * nb, acc[nb][bb]);
-                }
-            }
-        } else {
-            // one item per workgroup: each block's operands loaded next to its stores
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-                if (16 * nb < ns) {
-                    const int n = n0 + 16 * nb;
-                    const v4f bias = A.bias ? ld4(A.bias + n + 4 * q) : z4;
-#pragma unroll
-                    for (int bb = 0; bb < kGemmBB; ++bb) {
-                        if (ok[bb]) {
-                            float* yp = P.y + rows[bb] * P.ld_y + n + 4 * q;
-                            v4f v = acc[nb][bb] + bias;
-                            if (P.beta != 0.f) v += P.beta * ld4(yp);
-                            if (A.ys) v *= ld4(ysr[bb] + n);
-                            st4(yp, v);
-                        }
-                    }
+                    if (A.ys) v *= *reinterpret_cast<const v4f*>(side.ys + yso[bb] + 16 * nb);
+                    if (ok[bb]) st4(yr[bb] + n0 + 16 * nb, v);
                 }
             }
         }
@@ -265,6 +283,7 @@ __global__ __launch_bounds__(kKcWaves * kWave) void rows_gemm_kc_kernel(GemmArgs
     constexpr int NSB = 16 * NB;                              // columns of the slice buffer
     constexpr int WI = (NSB * (kKcK / 4) + kKcWaves * kWave - 1) / (kKcWaves * kWave);   // float4 items per thread
     __shared__ float sW[2][NSB * kKcS];
+    extern __shared__ float sSide[];                          // side tables (GemmSide), dynamic
     const int tid = threadIdx.x, lane = tid & (kWave - 1), j = lane & 15, q = lane >> 4;
     const int wv = __builtin_amdgcn_readfirstlane(tid / kWave);
     const v4f z4 = {0.f, 0.f, 0.f, 0.f};
@@ -315,39 +334,45 @@ __global__ __launch_bounds__(kKcWaves * kWave) void rows_gemm_kc_kernel(GemmArgs
         }
     };
     const int64_t m0 = (tile * kKcWaves + wv) * (16 * kGemmBB);
-    int64_t rows[kGemmBB];
+    const GemmSide side(sSide, A, NSB);
     bool ok[kGemmBB];
     const float* xr[kGemmBB];
-    const float* xsr[kGemmBB];
-    const float* ysr[kGemmBB];
+    float* yr[kGemmBB];
+    int xso[kGemmBB], yso[kGemmBB];                            // LDS offsets of the row's scale rows
 #pragma unroll
     for (int bb = 0; bb < kGemmBB; ++bb) {
-        rows[bb] = m0 + 16 * bb + j;
-        ok[bb] = rows[bb] < P.m;
-        const int64_t rc = ok[bb] ? rows[bb] : 0;
+        const int64_t row = m0 + 16 * bb + j;
+        ok[bb] = row < P.m;
+        const int64_t rc = ok[bb] ? row : 0;
         xr[bb] = P.x + rc * P.ld_x + 4 * q;
-        const int64_t g = A.group ? (int64_t)A.group[rc % A.period] : 0;
-        xsr[bb] = A.xs ? A.xs + g * A.ld_s + P.s_off + 4 * q : nullptr;
-        ysr[bb] = A.ys ? A.ys + g * A.ld_s + P.s_off + 4 * q : nullptr;
+        yr[bb] = P.y + rc * P.ld_y + 4 * q;
+        const int g = A.group ? A.group[rc % A.period] : 0;
+        xso[bb] = g * A.kmax + 4 * q;
+        yso[bb] = g * NSB + 4 * q;
     }
     const int nks = K / 16;                                    // 16-column steps of x
     auto load_x = [&](int ks, v4f (&xv)[kGemmBB]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int bb = 0; bb < kGemmBB; ++bb) {
-            xv[bb] = (ok[bb] && ks < nks) ? ld4(xr[bb] + 16 * ks) : z4;
-            if (A.xs && ok[bb] && ks < nks) xv[bb] *= ld4(xsr[bb] + 16 * ks);
-        }
+        for (int bb = 0; bb < kGemmBB; ++bb) xv[bb] = (ok[bb] && ks < nks) ? ld4(xr[bb] + 16 * ks) : z4;
     };
-    v4f acc[NB][kGemmBB];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-        for (int bb = 0; bb < kGemmBB; ++bb) acc[nb][bb] = z4;
     {
         v4f bw[WI];
         load_w(0, bw);
         store_w(0, bw);
     }
+    gemm_stage_side(A, P, side, NSB, n0, ns, true);
+    // accumulators start at beta y (loads in flight with the first x rows), else zero
+    v4f acc[NB][kGemmBB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int bb = 0; bb < kGemmBB; ++bb) {
+            acc[nb][bb] = z4;
+            if (P.beta != 0.f && ok[bb] && 16 * nb < ns) {
+                acc[nb][bb] = ld4(yr[bb] + n0 + 16 * nb);
+                if (P.beta != 1.f) acc[nb][bb] *= P.beta;
+            }
+        }
     v4f x0[kGemmBB], x1[kGemmBB];
     load_x(0, x0);
     load_x(1, x1);
@@ -367,6 +392,7 @@ __global__ __launch_bounds__(kKcWaves * kWave) void rows_gemm_kc_kernel(GemmArgs
 #pragma unroll
             for (int bb = 0; bb < kGemmBB; ++bb) {
                 xv[bb] = x0[bb];
+                if (A.xs) xv[bb] *= *reinterpret_cast<const v4f*>(side.xs + xso[bb] + 16 * ks);
                 x0[bb] = x1[bb];
             }
             load_x(ks + 2, x1);                               // two 16-column steps ahead
@@ -385,29 +411,17 @@ __global__ __launch_bounds__(kKcWaves * kWave) void rows_gemm_kc_kernel(GemmArgs
         if (more) store_w(buf ^ 1, bw);
         __syncthreads();
     }
-    // epilogue, loads first (columns past the slice read its last block, rows past m read row 0;
-    // neither is stored)
-    float* yr[kGemmBB];
-#pragma unroll
-    for (int bb = 0; bb < kGemmBB; ++bb) yr[bb] = P.y + (ok[bb] ? rows[bb] : 0) * P.ld_y + 4 * q;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-        const int nc = 16 * min(nb, ns / 16 - 1);
-        const v4f bias = A.bias ? ld4(A.bias + n0 + nc + 4 * q) : z4;
-#pragma unroll
-        for (int bb = 0; bb < kGemmBB; ++bb) {
-            v4f v = acc[nb][bb] + bias;
-            if (P.beta != 0.f) v += P.beta * ld4(yr[bb] + n0 + nc);
-            if (A.ys) v *= ld4(ysr[bb] + n0 + nc);
-            acc[nb][bb] = v;
-        }
-    }
+    // epilogue: bias and y scale from LDS, then the stores
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
         if (16 * nb < ns) {
+            const v4f bias = A.bias ? *reinterpret_cast<const v4f*>(side.bias + 16 * nb + 4 * q) : z4;
 #pragma unroll
-            for (int bb = 0; bb < kGemmBB; ++bb)
-                if (ok[bb]) st4(yr[bb] + n0 + 16 * nb, acc[nb][bb]);
+            for (int bb = 0; bb < kGemmBB; ++bb) {
+                v4f v = acc[nb][bb] + bias;
+                if (A.ys) v *= *reinterpret_cast<const v4f*>(side.ys + yso[bb] + 16 * nb);
+                if (ok[bb]) st4(yr[bb] + n0 + 16 * nb, v);
+            }
         }
     }
 }
@@ -432,8 +446,8 @@ static bool use_kc_gemm(int K, int ns_max, int n_widest, int64_t rows) {
 using namespace face;
 
 extern "C" int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, int32_t w_kn, const float* bias,
-                                const float* x_scale, const float* y_scale, int32_t ld_scale, const int32_t* group,
-                                int64_t period, void* stream) {
+                                const float* x_scale, const float* y_scale, int32_t ld_scale, int32_t n_groups,
+                                const int32_t* group, int64_t period, void* stream) {
     if (!probs || n_probs < 1 || n_probs > kGemmMaxProbs) return FACE_ERR_ARG;
     int K = 16;
     for (int i = 0; i < n_probs; ++i) {
@@ -441,14 +455,20 @@ extern "C" int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, 
         if (probs[i].k > K) K = probs[i].k;
     }
     const bool scaled = x_scale || y_scale;
-    if (scaled && (!group || period < 1 || ld_scale < 1)) return FACE_ERR_ARG;
+    if (scaled && (!group || period < 1 || ld_scale < 1 || n_groups < 1 || n_groups > kGemmMaxGroups))
+        return FACE_ERR_ARG;
+    if (!scaled) n_groups = 1;
     if ((bias && !al16(bias)) || (x_scale && !al16(x_scale)) || (y_scale && !al16(y_scale)) || (scaled && ld_scale % 4))
         return FACE_ERR_UNSUPPORTED;
-    // column slice: the weight slice (NS x (K + 4) floats) must fit in LDS, at most 160 columns,
-    // and the widest problem splits into slices of equal width (multiples of 16)
+    // LDS floats of the side tables for a slice of ns columns (GemmSide)
+    auto side_floats = [&](int ns) {
+        return (y_scale ? n_groups * ns : 0) + (x_scale ? n_groups * K : 0) + (bias ? ns : 0);
+    };
+    // column slice: the weight slice (NS x (K + 4) floats) and the side tables must fit in LDS, at
+    // most 160 columns, and the widest problem splits into slices of equal width (multiples of 16)
     const int max_lds = device_max_lds();
-    int ns_max = (max_lds / (4 * (K + 4))) / 16 * 16;
-    if (ns_max > 160) ns_max = 160;
+    int ns_max = 160;
+    while (ns_max >= 16 && 4 * ((int64_t)ns_max * (K + 4) + side_floats(ns_max)) > max_lds) ns_max -= 16;
     int n_widest = 16;
     for (int i = 0; i < n_probs; ++i)
         if (probs[i].n > n_widest) n_widest = probs[i].n;
@@ -464,7 +484,7 @@ extern "C" int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, 
     const int NS = ((n_widest + n_sl - 1) / n_sl + 15) / 16 * 16;
     GemmArgs A{};
     A.n_probs = n_probs, A.w_kn = w_kn ? 1 : 0, A.bias = bias, A.xs = x_scale, A.ys = y_scale;
-    A.ld_s = ld_scale, A.group = group, A.period = period;
+    A.ld_s = ld_scale, A.n_groups = n_groups, A.group = group, A.period = period, A.kmax = K;
     int64_t rows_total = 0;
     for (int i = 0; i < n_probs; ++i) rows_total += probs[i].m > 0 ? probs[i].m : 0;
     if (use_kc_gemm(K, ns_max, n_widest, rows_total)) {
@@ -494,13 +514,25 @@ extern "C" int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, 
         if (blocks == 0) return 0;
         A.NS = NSk;
         A.items = blocks;
+        A.side_off = 0;
         const hipStream_t stk = (hipStream_t)stream;
-#define FACE_GEMM_KC(NB_) \
-    hipLaunchKernelGGL(rows_gemm_kc_kernel<NB_>, dim3((unsigned)blocks), dim3(kKcWaves * kWave), 0, stk, A)
-        switch (NSk / 16) {
-            case 1: case 2: case 3: case 4: FACE_GEMM_KC(4); break;
-            case 5: case 6: case 7: case 8: FACE_GEMM_KC(8); break;
-            case 9: case 10: case 11: case 12: FACE_GEMM_KC(12); break;
+        const int nbk = NSk <= 64 ? 4 : (NSk <= 128 ? 8 : (NSk <= 192 ? 12 : 16));
+        const size_t side_lds = 4 * (size_t)side_floats(16 * nbk);
+        const size_t static_lds = 2 * (size_t)(16 * nbk) * kKcS * sizeof(float);
+        if ((int64_t)(side_lds + static_lds) > max_lds) return FACE_ERR_UNSUPPORTED;
+#define FACE_GEMM_KC(NB_)                                                                                          \
+    do {                                                                                                           \
+        if (side_lds + static_lds > 65536 &&                                                                       \
+            hipFuncSetAttribute((const void*)rows_gemm_kc_kernel<NB_>, hipFuncAttributeMaxDynamicSharedMemorySize, \
+                                (int)side_lds) != hipSuccess)                                                      \
+            return FACE_ERR_UNSUPPORTED;                                                                           \
+        hipLaunchKernelGGL(rows_gemm_kc_kernel<NB_>, dim3((unsigned)blocks), dim3(kKcWaves * kWave), side_lds, stk, \
+                           A);                                                                                     \
+    } while (0)
+        switch (nbk) {
+            case 4: FACE_GEMM_KC(4); break;
+            case 8: FACE_GEMM_KC(8); break;
+            case 12: FACE_GEMM_KC(12); break;
             default: FACE_GEMM_KC(16); break;
         }
 #undef FACE_GEMM_KC
@@ -551,7 +583,8 @@ extern "C" int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, 
     A.items = blocks;
     A.total_cost = total_cost;
     const int nb = (max_n < NS ? max_n : NS) / 16;
-    const size_t lds = (size_t)(nb * 16) * (K + 4) * sizeof(float);
+    A.side_off = nb * 16 * (K + 4);
+    const size_t lds = ((size_t)A.side_off + side_floats(nb * 16)) * sizeof(float);
     // persistent grid: as many workgroups as fit on the device at once, each on a contiguous run
     // of the work items
     int64_t wg_cu = (int64_t)max_lds / (int64_t)lds;
@@ -568,22 +601,26 @@ extern "C" int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, 
     const bool persist = blocks > n_cu * wg_cu && (!w_kn || !multi_slice);
     const int64_t grid = persist ? n_cu * wg_cu : blocks;
     const hipStream_t st = (hipStream_t)stream;
-#define FACE_GEMM_P(NB_, P_)                                                                                \
+#define FACE_GEMM_P(NB_, P_, X_)                                                                            \
     do {                                                                                                    \
-        auto kern = NW == 16 ? rows_gemm_kernel<NB_, 16, P_>                                                \
-                             : (NW == 8 ? rows_gemm_kernel<NB_, 8, P_> : rows_gemm_kernel<NB_, 4, P_>);     \
+        auto kern = NW == 16 ? rows_gemm_kernel<NB_, 16, P_, X_>                                            \
+                             : (NW == 8 ? rows_gemm_kernel<NB_, 8, P_, X_> : rows_gemm_kernel<NB_, 4, P_, X_>); \
         if (lds > 65536 &&                                                                                  \
             hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != \
                 hipSuccess)                                                                                 \
             return FACE_ERR_UNSUPPORTED;                                                                    \
         hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NW * kWave), lds, st, A);                      \
     } while (0)
-#define FACE_GEMM(NB_)               \
-    do {                             \
-        if (persist)                 \
-            FACE_GEMM_P(NB_, true);  \
-        else                         \
-            FACE_GEMM_P(NB_, false); \
+#define FACE_GEMM(NB_)                      \
+    do {                                    \
+        if (persist && x_scale)             \
+            FACE_GEMM_P(NB_, true, true);   \
+        else if (persist)                   \
+            FACE_GEMM_P(NB_, true, false);  \
+        else if (x_scale)                   \
+            FACE_GEMM_P(NB_, false, true);  \
+        else                                \
+            FACE_GEMM_P(NB_, false, false); \
     } while (0)
     switch (nb) {
         case 1: FACE_GEMM(1); break;

@@ -68,14 +68,14 @@ _SIGS = {
     "face_radial_spline_order_noalloc": (ctypes.c_int, [P, P, I64, I32, I32, F32, P, P]),
     "face_edge_linear_fwd": (ctypes.c_int, [P, I32, I64, I32, P, P, I32, P, I32, P, P, I32, P]),
     "face_edge_linear_bwd": (ctypes.c_int, [P, I32, I32, P, I32, P, P, I64, P, I32, P, I32, P]),
-    "face_rows_linear": (ctypes.c_int, [P, I32, I32, P, P, P, I32, P, I64, P]),
+    "face_rows_linear": (ctypes.c_int, [P, I32, I32, P, P, P, I32, I32, P, I64, P]),
     "face_eq_gate_fwd": (ctypes.c_int, [P, P, P, I64, I32, P, P, P]),
     "face_eq_gate_bwd": (ctypes.c_int, [P, P, P, P, P, I64, I32, P, P, P, P]),
     "face_layer_norm_fwd": (ctypes.c_int, [P, I64, I32, P, P, ctypes.c_float, P, P, P, P]),
     "face_layer_norm_bwd": (ctypes.c_int, [P, P, I64, I32, P, P, P, P, P]),
 }
 
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 
 class LinProblem(ctypes.Structure):

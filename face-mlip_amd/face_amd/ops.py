@@ -921,8 +921,11 @@ def rows_linear(probs, w_kn=False, bias=None, xs=None, ys=None, group=None, peri
                                  y.stride(0), y.shape[1], x.shape[1], int(s_off), float(beta))
         ref = y
     tab = xs if xs is not None else ys
+    if xs is not None and ys is not None and xs.shape[0] != ys.shape[0]:
+        raise ValueError("rows_linear: xs and ys must have the same number of groups")
     call("face_rows_linear", arr, len(probs), 1 if w_kn else 0, ptr(bias), ptr(xs), ptr(ys),
-         0 if tab is None else tab.stride(0), ptr(group), int(period), _lib.stream_of(ref), label=label)
+         0 if tab is None else tab.stride(0), 0 if tab is None else tab.shape[0], ptr(group), int(period),
+         _lib.stream_of(ref), label=label)
 
 
 class ScaledMix(torch.autograd.Function):

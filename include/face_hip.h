@@ -332,13 +332,14 @@ typedef struct {
 /* For each problem (1..4 of them, host array):
  *   y[r, :] = (beta y[r, :] + (x[r, :] * xs[r, :]) w^T + bias) * ys[r, :]
  * with xs[r, k] = x_scale[group[r % period] * ld_scale + s_off + k] and ys likewise over the
- * n output columns; x_scale, y_scale, bias may be NULL (beta = 0: y is not read). The linear
+ * n output columns, group values in [0, n_groups) (n_groups <= 64: the scale tables' rows, staged
+ * in LDS); x_scale, y_scale, bias may be NULL (beta = 0: y is not read). The linear
  * layers of the node features: mix / tmix / proj and the readout input (face/model.py:498-533,
  * :537-544) with the elem_scale factor, and their input gradients (w_kn = 1). x, y, bias and the
  * scale tables 16-byte aligned, ld_x, ld_y (and ld_w, ld_scale, s_off) multiples of 4. */
 int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, int32_t w_kn, const float* bias,
-                     const float* x_scale, const float* y_scale, int32_t ld_scale, const int32_t* group, int64_t period,
-                     void* stream);
+                     const float* x_scale, const float* y_scale, int32_t ld_scale, int32_t n_groups,
+                     const int32_t* group, int64_t period, void* stream);
 
 /* ---------------------------------------------------------------- per-edge linear layers
  * Forward: y (E, ld_y) = x (E, ld_x) w^T + b + tab[idx[e]], w (F, K) row-major, b (F) and tab
