@@ -46,6 +46,13 @@ __device__ __forceinline__ v4f mfma_16x16x4(float a, float b, v4f c) {
 }
 
 __device__ __forceinline__ v4f ld4(const float* p) { return *reinterpret_cast<const v4f*>(p); }
+
+// float4 read of an LDS image (16-byte aligned base) at a float offset that is a multiple of 4:
+// one ds_read_b128. A plain pointer cast at a runtime offset leaves the alignment unknown to
+// the compiler, which then splits the read into 32-bit pairs (ds_read2_b32).
+__device__ __forceinline__ v4f lds4_at(const float* base, int off) {
+    return reinterpret_cast<const v4f*>(__builtin_assume_aligned(base, 16))[off >> 2];
+}
 __device__ __forceinline__ void st4(float* p, v4f v) { *reinterpret_cast<v4f*>(p) = v; }
 
 // Workgroup copy of n float4 items, put(v, src(v)) for v < n, U loads per thread issued before

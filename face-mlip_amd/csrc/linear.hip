@@ -117,7 +117,7 @@ __global__ __launch_bounds__(kLinWaves * kWave) void edge_linear_fwd_kernel(
 #pragma unroll
                 for (int fb = 0; fb < FB; ++fb)
                     wa[fb] = fb0 + 16 * fb < nf
-                                 ? *reinterpret_cast<const v4f*>(sW + lin_off(fb0 + 16 * fb + j, 4 * kb + q, S, NCH, rt))
+                                 ? lds4_at(sW, lin_off(fb0 + 16 * fb + j, 4 * kb + q, S, NCH, rt))
                                  : z4;
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
@@ -204,7 +204,7 @@ __global__ __launch_bounds__(kLinBwdWaves * kWave) void edge_linear_bwd_kernel(
                     if (dX) {
 #pragma unroll
                         for (int kb = 0; kb < KB; ++kb) {
-                            const v4f wa = *reinterpret_cast<const v4f*>(sWT + (16 * kb + j) * SW + 16 * fc + 4 * q);
+                            const v4f wa = lds4_at(sWT, (16 * kb + j) * SW + 16 * fc + 4 * q);
 #pragma unroll
                             for (int r = 0; r < 4; ++r) acc[kb] = mfma_16x16x4(wa[r], g[r], acc[kb]);
                         }
