@@ -58,7 +58,9 @@ KERNEL_FAMILY = {
     "gather_bwd": "gather_rows_bwd", "radial_fwd": "radial_fwd", "radial_bwd": "radial_bwd",
     "radial_head": "edge_linear_fwd", "edge_msg_fwd": "edge_linear_fwd", "edge_msg_bwd": "edge_linear_bwd",
     "mix_fwd": "rows_gemm", "mix_bwd": "rows_gemm", "tmix_bwd": "rows_gemm", "proj_fwd": "rows_gemm",
-    "proj_bwd": "rows_gemm", "eq_gate_fwd": "eq_gate_fwd", "eq_gate_bwd": "eq_gate_bwd",
+    "proj_bwd": "rows_gemm", "readout_in": "rows_gemm", "readout_hid": "rows_gemm", "readout_out": "rows_gemm",
+    "readout_in_bwd": "rows_gemm", "readout_hid_bwd": "rows_gemm", "readout_out_bwd": "rows_gemm",
+    "eq_gate_fwd": "eq_gate_fwd", "eq_gate_bwd": "eq_gate_bwd",
     "ln_fwd": "layer_norm_fwd", "ln_bwd": "layer_norm_bwd", "spline_order": "spline_order",
     "spline_fwd": "radial_spline_fwd", "spline_bwd": "radial_spline_bwd",
 }
@@ -195,6 +197,17 @@ def algorithmic_flops(label, g, kw):
         return 2 * E * 4 * kw["K_dir"] * K
     if label.startswith("cp_radial_bwd"):
         return 2 * E * (4 * C * H + 2 * 20 * C)
+    # readout (per launch, averaged over the passes: the gate row only where a pass has
+    # equivariant outputs, i.e. all passes but the last with eqmsg)
+    gate = (kw.get("n_passes", 2) - 1) / kw.get("n_passes", 2) if kw.get("eqmsg") else 0.0
+    if label == "readout_in":
+        return 2 * N * 10 * C * 2 * C + gate * 2 * N * 9 * C * 2 * C
+    if label in ("readout_hid", "readout_hid_bwd"):
+        return 2 * N * 2 * C * 2 * C
+    if label in ("readout_out", "readout_out_bwd"):
+        return 2 * N * 2 * C * (C + 16)
+    if label == "readout_in_bwd":
+        return 2 * N * 2 * C * 10 * C + gate * 2 * N * 2 * C * 9 * C
     if label == "density_fwd20":
         return 2 * E * 20 * kw["B"] * kw["K"]
     if label == "density_bwd20":

@@ -41,17 +41,47 @@ struct GemmProb {
     int64_t ld_y;
     int n, k, s_off, tiles, slices;        // tiles of 32 NW rows, slices of NS columns
     float beta;
+    const float* x2;                       // input columns k >= k1 (column k - k1), or null
+    int64_t ld_x2;
+    int k1, x_op;                          // x_op on columns < k1: 0 none, 1 silu, 2 * silu'(xz)
+    const float* xz;
+    int64_t ld_xz;
+    const float* bias;
+    const float* y0;                       // initial sum beta * y0 (columns < n_y0), null: y
+    int64_t ld_y0;
+    int n_y0;
     int64_t first_block;                   // first work item of this problem
     int64_t cost0;                         // summed cost of the items of the problems before it
     int cost;                              // cost of one of its items (~ K + fixed per-item work)
 };
+
+// silu and its derivative with the hardware exp2 and reciprocal (about 1 ulp each)
+__device__ __forceinline__ float gemm_sigmoid(float x) {
+    return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-1.44269504088896341f * x));
+}
+__device__ __forceinline__ v4f gemm_silu(v4f x) {
+    v4f o;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) o[r] = x[r] * gemm_sigmoid(x[r]);
+    return o;
+}
+__device__ __forceinline__ v4f gemm_dsilu(v4f g, v4f z) {       // g * d silu(z) / dz
+    v4f o;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const float sg = gemm_sigmoid(z[r]);
+        o[r] = g[r] * (sg * (1.f + z[r] * (1.f - sg)));
+    }
+    return o;
+}
 
 struct GemmArgs {
     GemmProb p[kGemmMaxProbs];
     int64_t items;                         // (problem, slice, tile) work items over all problems
     int64_t total_cost;
     int n_probs, w_kn, NS;
-    const float *bias, *xs, *ys;
+    const float *xs, *ys;
+    int any_bias;                          // some problem has a bias (side table present)
     int ld_s, n_groups;
     const int32_t* group;
     int64_t period;
@@ -66,7 +96,7 @@ struct GemmSide {
     __device__ __forceinline__ GemmSide(float* base, const GemmArgs& A, int nsb) {
         ys = base;
         xs = ys + (A.ys ? A.n_groups * nsb : 0);
-        bias = xs + (A.xs ? A.n_groups * A.kmax : 0);
+        bias = xs + (A.xs ? A.n_groups * A.kmax : 0);       // present when A.any_bias
     }
 };
 
@@ -87,13 +117,15 @@ __device__ __forceinline__ void gemm_stage_side(const GemmArgs& A, const GemmPro
             S.xs[g * A.kmax + k] = A.xs[(int64_t)g * A.ld_s + P.s_off + k];
         }
     }
-    if (A.bias) {
-        for (int c = tid; c < nsb; c += nthr) S.bias[c] = c < ns ? A.bias[n0 + c] : 0.f;
+    if (A.any_bias) {
+        for (int c = tid; c < nsb; c += nthr) S.bias[c] = (c < ns && P.bias) ? P.bias[n0 + c] : 0.f;
     }
 }
 
-template <int NB, int NW, bool PERSIST, bool XS>
+// XM: input mode -- 0 plain, 1 the per-group x scale (xs), 2 the per-problem transform x_op
+template <int NB, int NW, bool PERSIST, int XM>
 __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
+    constexpr bool XS = XM == 1, XO = XM == 2;
     extern __shared__ float sW[];
     const int tid = threadIdx.x, lane = tid & (kWave - 1);
     const int j = lane & 15, q = lane >> 4;
@@ -180,6 +212,7 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
         const int64_t m0 = (tile * NW + wv) * (16 * kGemmBB);
         if (m0 >= P.m) return;
         bool ok[kGemmBB];
+        int64_t rcs[kGemmBB];
         const float* xr[kGemmBB];
         float* yr[kGemmBB];
         int xso[kGemmBB], yso[kGemmBB];                                  // LDS offsets of the row's scale rows
@@ -187,18 +220,30 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
         for (int bb = 0; bb < kGemmBB; ++bb) {
             const int64_t row = m0 + 16 * bb + j;
             ok[bb] = row < P.m;
-            const int64_t rc = ok[bb] ? row : 0;
-            xr[bb] = P.x + rc * P.ld_x + 4 * q;
-            yr[bb] = P.y + rc * P.ld_y + 4 * q;
-            const int g = A.group ? A.group[rc % A.period] : 0;
+            rcs[bb] = ok[bb] ? row : 0;
+            xr[bb] = P.x + rcs[bb] * P.ld_x + 4 * q;
+            yr[bb] = P.y + rcs[bb] * P.ld_y + 4 * q;
+            const int g = A.group ? A.group[rcs[bb] % A.period] : 0;
             xso[bb] = g * A.kmax + 4 * q;
             yso[bb] = g * (16 * NB) + 4 * q;
         }
-        auto load_x = [&](int kc, v4f (&xv)[kGemmBB]) {
-#pragma unroll
-            for (int bb = 0; bb < kGemmBB; ++bb) xv[bb] = ok[bb] ? ld4(xr[bb] + 16 * kc) : z4;
+        // input column block kc of row bb: x for columns < k1, x2 beyond (the second range only in
+        // the XM = 2 kernels; k1 is a multiple of 16)
+        auto x_at = [&](int bb, int kc) -> const float* {
+            const int c0 = 16 * kc;
+            if (!XO) return xr[bb] + c0;
+            return c0 < P.k1 ? xr[bb] + c0 : P.x2 + rcs[bb] * P.ld_x2 + (c0 - P.k1) + 4 * q;
         };
-        // accumulators start at beta y (loads in flight with the first x rows), else zero
+        auto load_x = [&](int kc, v4f (&xv)[kGemmBB], v4f (&zv)[kGemmBB]) {
+#pragma unroll
+            for (int bb = 0; bb < kGemmBB; ++bb) {
+                xv[bb] = ok[bb] ? ld4(x_at(bb, kc)) : z4;
+                if (XO && P.x_op == 2 && 16 * kc < P.k1)
+                    zv[bb] = ok[bb] ? ld4(P.xz + rcs[bb] * P.ld_xz + 16 * kc + 4 * q) : z4;
+            }
+        };
+        // accumulators start at beta y (XM = 2: beta y0 over its first n_y0 columns), the loads
+        // in flight with the first x rows, else zero
         v4f acc[NB][kGemmBB];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
@@ -206,13 +251,18 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
             for (int bb = 0; bb < kGemmBB; ++bb) {
                 acc[nb][bb] = z4;
                 if (P.beta != 0.f && ok[bb] && 16 * nb < ns) {
-                    acc[nb][bb] = ld4(yr[bb] + n0 + 16 * nb);
+                    if (!XO) {
+                        acc[nb][bb] = ld4(yr[bb] + n0 + 16 * nb);
+                    } else if (n0 + 16 * nb + 4 * q < P.n_y0) {
+                        acc[nb][bb] = P.y0 ? ld4(P.y0 + rcs[bb] * P.ld_y0 + n0 + 16 * nb + 4 * q)
+                                           : ld4(yr[bb] + n0 + 16 * nb);
+                    }
                     if (P.beta != 1.f) acc[nb][bb] *= P.beta;
                 }
             }
         const int nkc = K / 16;
-        v4f xn[kGemmBB];
-        load_x(0, xn);
+        v4f xn[kGemmBB], zn[kGemmBB];
+        load_x(0, xn, zn);
 #pragma unroll 1
         for (int kc = 0; kc < nkc; ++kc) {
             v4f xv[kGemmBB];
@@ -220,8 +270,12 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
             for (int bb = 0; bb < kGemmBB; ++bb) {
                 xv[bb] = xn[bb];
                 if (XS) xv[bb] *= *reinterpret_cast<const v4f*>(side.xs + xso[bb] + 16 * kc);
+                if (XO && 16 * kc < P.k1) {
+                    if (P.x_op == 1) xv[bb] = gemm_silu(xv[bb]);
+                    else if (P.x_op == 2) xv[bb] = gemm_dsilu(xv[bb], zn[bb]);
+                }
             }
-            if (kc + 1 < nkc) load_x(kc + 1, xn);
+            if (kc + 1 < nkc) load_x(kc + 1, xn, zn);
             // weight blocks read one block ahead of their MFMAs (LDS latency under the MFMA chain)
             const float* wrow = sW + j * SK + 16 * kc + 4 * q;
             v4f wa = *reinterpret_cast<const v4f*>(wrow);
@@ -247,7 +301,7 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
             if (16 * nb < ns) {
-                const v4f bias = A.bias ? *reinterpret_cast<const v4f*>(side.bias + 16 * nb + 4 * q) : z4;
+                const v4f bias = A.any_bias ? *reinterpret_cast<const v4f*>(side.bias + 16 * nb + 4 * q) : z4;
 #pragma unroll
                 for (int bb = 0; bb < kGemmBB; ++bb) {
                     v4f v = acc[nb][bb] + bias;
@@ -337,6 +391,7 @@ __global__ __launch_bounds__(kKcWaves * kWave) void rows_gemm_kc_kernel(GemmArgs
     const GemmSide side(sSide, A, NSB);
     bool ok[kGemmBB];
     const float* xr[kGemmBB];
+    const float* x2r[kGemmBB];
     float* yr[kGemmBB];
     int xso[kGemmBB], yso[kGemmBB];                            // LDS offsets of the row's scale rows
 #pragma unroll
@@ -345,15 +400,22 @@ __global__ __launch_bounds__(kKcWaves * kWave) void rows_gemm_kc_kernel(GemmArgs
         ok[bb] = row < P.m;
         const int64_t rc = ok[bb] ? row : 0;
         xr[bb] = P.x + rc * P.ld_x + 4 * q;
+        x2r[bb] = P.x2 + rc * P.ld_x2 + 4 * q;
         yr[bb] = P.y + rc * P.ld_y + 4 * q;
         const int g = A.group ? A.group[rc % A.period] : 0;
         xso[bb] = g * A.kmax + 4 * q;
         yso[bb] = g * NSB + 4 * q;
     }
     const int nks = K / 16;                                    // 16-column steps of x
-    auto load_x = [&](int ks, v4f (&xv)[kGemmBB]) __attribute__((always_inline)) {
+    // x rows of 16-column step ks (columns >= k1 from x2, k1 % 16 == 0) and, for x_op 2, the
+    // matching pre-activation rows
+    auto load_x = [&](int ks, v4f (&xv)[kGemmBB], v4f (&zv)[kGemmBB]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int bb = 0; bb < kGemmBB; ++bb) xv[bb] = (ok[bb] && ks < nks) ? ld4(xr[bb] + 16 * ks) : z4;
+        for (int bb = 0; bb < kGemmBB; ++bb) {
+            xv[bb] = (ok[bb] && ks < nks) ? ld4(16 * ks < P.k1 ? xr[bb] + 16 * ks : x2r[bb] + (16 * ks - P.k1)) : z4;
+            if (P.x_op == 2 && 16 * ks < P.k1)
+                zv[bb] = (ok[bb] && ks < nks) ? ld4(P.xz + (m0 + 16 * bb + j) * P.ld_xz + 16 * ks + 4 * q) : z4;
+        }
     };
     {
         v4f bw[WI];
@@ -368,14 +430,15 @@ __global__ __launch_bounds__(kKcWaves * kWave) void rows_gemm_kc_kernel(GemmArgs
 #pragma unroll
         for (int bb = 0; bb < kGemmBB; ++bb) {
             acc[nb][bb] = z4;
-            if (P.beta != 0.f && ok[bb] && 16 * nb < ns) {
-                acc[nb][bb] = ld4(yr[bb] + n0 + 16 * nb);
+            const int c = n0 + 16 * nb + 4 * q;
+            if (P.beta != 0.f && ok[bb] && 16 * nb < ns && c < P.n_y0) {
+                acc[nb][bb] = P.y0 ? ld4(P.y0 + (m0 + 16 * bb + j) * P.ld_y0 + c) : ld4(yr[bb] + n0 + 16 * nb);
                 if (P.beta != 1.f) acc[nb][bb] *= P.beta;
             }
         }
-    v4f x0[kGemmBB], x1[kGemmBB];
-    load_x(0, x0);
-    load_x(1, x1);
+    v4f x0[kGemmBB], x1[kGemmBB], z0[kGemmBB], z1[kGemmBB];
+    load_x(0, x0, z0);
+    load_x(1, x1, z1);
     __syncthreads();
     const int nchunk = (K + kKcK - 1) / kKcK;
 #pragma unroll 1
@@ -393,9 +456,12 @@ __global__ __launch_bounds__(kKcWaves * kWave) void rows_gemm_kc_kernel(GemmArgs
             for (int bb = 0; bb < kGemmBB; ++bb) {
                 xv[bb] = x0[bb];
                 if (A.xs) xv[bb] *= *reinterpret_cast<const v4f*>(side.xs + xso[bb] + 16 * ks);
+                if (P.x_op == 1 && 16 * ks < P.k1) xv[bb] = gemm_silu(xv[bb]);
+                if (P.x_op == 2 && 16 * ks < P.k1) xv[bb] = gemm_dsilu(xv[bb], z0[bb]);
                 x0[bb] = x1[bb];
+                z0[bb] = z1[bb];
             }
-            load_x(ks + 2, x1);                               // two 16-column steps ahead
+            load_x(ks + 2, x1, z1);                           // two 16-column steps ahead
             const float* wrow = sW[buf] + j * kKcS + 16 * s2 + 4 * q;
             v4f wa = *reinterpret_cast<const v4f*>(wrow);
 #pragma unroll
@@ -415,7 +481,7 @@ __global__ __launch_bounds__(kKcWaves * kWave) void rows_gemm_kc_kernel(GemmArgs
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
         if (16 * nb < ns) {
-            const v4f bias = A.bias ? *reinterpret_cast<const v4f*>(side.bias + 16 * nb + 4 * q) : z4;
+            const v4f bias = A.any_bias ? *reinterpret_cast<const v4f*>(side.bias + 16 * nb + 4 * q) : z4;
 #pragma unroll
             for (int bb = 0; bb < kGemmBB; ++bb) {
                 v4f v = acc[nb][bb] + bias;
@@ -435,34 +501,75 @@ static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 // stays faster (12.9 against 13.9 ms), at K = 768 with (k, n) weights too (the 100k-atom proj
 // backward 6.3 against 7.7 ms), and so it does for small row counts. FACE_ROWS_GEMM_KC=0 / 1 in
 // the environment forces either kernel.
+// Whole-K slices narrower than 64 columns (K >= ~600) re-read every x row once per 16-32 columns:
+// the K-chunked kernel also serves those (the readout input layer, K = 10 C) once there are a
+// few of its 256-row tiles per CU.
 static bool use_kc_gemm(int K, int ns_max, int n_widest, int64_t rows) {
     const char* e = getenv("FACE_ROWS_GEMM_KC");
     if (e && (e[0] == '0' || e[0] == '1')) return e[0] == '1';
-    return K >= 1024 && n_widest > ns_max && rows >= (int64_t)device_cu_count() * 512;
+    const int64_t n_cu = device_cu_count();
+    return K >= 1024 && n_widest > ns_max && (rows >= n_cu * 512 || (ns_max < 64 && rows >= n_cu * 32));
 }
 
 }  // namespace face
 
 using namespace face;
 
-extern "C" int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, int32_t w_kn, const float* bias,
-                                const float* x_scale, const float* y_scale, int32_t ld_scale, int32_t n_groups,
-                                const int32_t* group, int64_t period, void* stream) {
+// Validate problem s and fill p (everything but the tiling); 0 or a FACE_ERR_* status.
+static int fill_prob(const face_lin_problem& s, int w_kn, bool scaled, const float* x_scale, const float* y_scale,
+                     int ld_scale, GemmProb& p) {
+    if (s.m < 0 || s.n < 16 || s.n % 16 || s.k < 16 || s.k % 16 || s.ld_y < s.n || s.ld_w < (w_kn ? s.n : s.k))
+        return FACE_ERR_ARG;
+    const int k1 = s.x2 ? s.k1 : s.k;
+    if (k1 < 0 || k1 > s.k || k1 % 16 || s.ld_x < k1 || (s.x2 && s.ld_x2 < s.k - k1)) return FACE_ERR_ARG;
+    if (s.x_op < 0 || s.x_op > 2 || (s.x_op == 2 && (!s.xz || s.ld_xz < k1)) || (s.x_op && x_scale)) return FACE_ERR_ARG;
+    if (s.y0 && (s.n_y0 < 0 || s.n_y0 > s.n || s.n_y0 % 4 || s.ld_y0 < s.n_y0)) return FACE_ERR_ARG;
+    if (scaled && (s.s_off < 0 || s.s_off % 4 || s.s_off + (x_scale ? s.k : 0) > ld_scale ||
+                   s.s_off + (y_scale ? s.n : 0) > ld_scale))
+        return FACE_ERR_ARG;
+    if (s.m > 0 && (!s.x || !s.w || !s.y)) return FACE_ERR_ARG;
+    if (s.ld_x % 4 || s.ld_y % 4 || !al16(s.x) || !al16(s.y) || (!w_kn && (!al16(s.w) || s.ld_w % 4)) ||
+        (s.x2 && (!al16(s.x2) || s.ld_x2 % 4)) || (s.x_op == 2 && (!al16(s.xz) || s.ld_xz % 4)) ||
+        (s.bias && !al16(s.bias)) || (s.y0 && (!al16(s.y0) || s.ld_y0 % 4)))
+        return FACE_ERR_UNSUPPORTED;
+    p.x = s.x, p.ld_x = s.ld_x, p.m = s.m, p.w = s.w, p.ld_w = s.ld_w, p.y = s.y, p.ld_y = s.ld_y, p.n = s.n;
+    p.k = s.k, p.s_off = s.s_off, p.beta = s.beta;
+    p.x2 = s.x2 ? s.x2 : s.x, p.ld_x2 = s.x2 ? s.ld_x2 : s.ld_x, p.k1 = k1;
+    p.x_op = s.x_op, p.xz = s.x_op == 2 ? s.xz : s.x, p.ld_xz = s.x_op == 2 ? s.ld_xz : s.ld_x;
+    p.bias = s.bias;
+    p.y0 = s.y0, p.ld_y0 = s.y0 ? s.ld_y0 : 0, p.n_y0 = s.y0 ? s.n_y0 : s.n;
+    return 0;
+}
+
+extern "C" int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, int32_t w_kn, const float* x_scale,
+                                const float* y_scale, int32_t ld_scale, int32_t n_groups, const int32_t* group,
+                                int64_t period, void* stream) {
     if (!probs || n_probs < 1 || n_probs > kGemmMaxProbs) return FACE_ERR_ARG;
     int K = 16;
+    bool any_bias = false, any_op = false, any_ext = false;
     for (int i = 0; i < n_probs; ++i) {
         if (probs[i].k < 16 || probs[i].k % 16) return FACE_ERR_ARG;
         if (probs[i].k > K) K = probs[i].k;
+        if (probs[i].bias) any_bias = true;
+        if (probs[i].x_op) any_op = true;
+        if (probs[i].x_op || probs[i].x2 || probs[i].y0) any_ext = true;     // the XM = 2 kernels
     }
     const bool scaled = x_scale || y_scale;
     if (scaled && (!group || period < 1 || ld_scale < 1 || n_groups < 1 || n_groups > kGemmMaxGroups))
         return FACE_ERR_ARG;
     if (!scaled) n_groups = 1;
-    if ((bias && !al16(bias)) || (x_scale && !al16(x_scale)) || (y_scale && !al16(y_scale)) || (scaled && ld_scale % 4))
+    if ((x_scale && !al16(x_scale)) || (y_scale && !al16(y_scale)) || (scaled && ld_scale % 4))
         return FACE_ERR_UNSUPPORTED;
+    GemmArgs A{};
+    A.n_probs = n_probs, A.w_kn = w_kn ? 1 : 0, A.any_bias = any_bias ? 1 : 0, A.xs = x_scale, A.ys = y_scale;
+    A.ld_s = ld_scale, A.n_groups = n_groups, A.group = group, A.period = period, A.kmax = K;
+    for (int i = 0; i < n_probs; ++i) {
+        const int st = fill_prob(probs[i], A.w_kn, scaled, x_scale, y_scale, ld_scale, A.p[i]);
+        if (st) return st;
+    }
     // LDS floats of the side tables for a slice of ns columns (GemmSide)
     auto side_floats = [&](int ns) {
-        return (y_scale ? n_groups * ns : 0) + (x_scale ? n_groups * K : 0) + (bias ? ns : 0);
+        return (y_scale ? n_groups * ns : 0) + (x_scale ? n_groups * K : 0) + (any_bias ? ns : 0);
     };
     // column slice: the weight slice (NS x (K + 4) floats) and the side tables must fit in LDS, at
     // most 160 columns, and the widest problem splits into slices of equal width (multiples of 16)
@@ -482,29 +589,19 @@ extern "C" int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, 
         while (ns_max >= 16 && wg4 * n_sl < 2 * n_cu && (n_widest + n_sl) / (n_sl + 1) >= 16) ++n_sl;
     }
     const int NS = ((n_widest + n_sl - 1) / n_sl + 15) / 16 * 16;
-    GemmArgs A{};
-    A.n_probs = n_probs, A.w_kn = w_kn ? 1 : 0, A.bias = bias, A.xs = x_scale, A.ys = y_scale;
-    A.ld_s = ld_scale, A.n_groups = n_groups, A.group = group, A.period = period, A.kmax = K;
     int64_t rows_total = 0;
     for (int i = 0; i < n_probs; ++i) rows_total += probs[i].m > 0 ? probs[i].m : 0;
     if (use_kc_gemm(K, ns_max, n_widest, rows_total)) {
-        // K-chunked weight slices of up to 256 columns (rows_gemm_kc_kernel)
-        const int nsl = (n_widest + 255) / 256;
+        // K-chunked weight slices of up to 256 columns (rows_gemm_kc_kernel; 192 with an input
+        // transform, whose pre-activation rows take registers too)
+        const int ns_cap = any_op ? 192 : 256;
+        const int nsl = (n_widest + ns_cap - 1) / ns_cap;
         const int NSk = ((n_widest + nsl - 1) / nsl + 15) / 16 * 16;
         int64_t blocks = 0;
         for (int i = 0; i < n_probs; ++i) {
             const face_lin_problem& s = probs[i];
-            if (s.m < 0 || s.n < 16 || s.n % 16 || s.ld_x < s.k || s.ld_y < s.n || s.ld_w < (w_kn ? s.n : s.k))
-                return FACE_ERR_ARG;
-            if (scaled && (s.s_off < 0 || s.s_off % 4 || s.s_off + (x_scale ? s.k : 0) > ld_scale ||
-                           s.s_off + (y_scale ? s.n : 0) > ld_scale))
-                return FACE_ERR_ARG;
-            if (s.m > 0 && (!s.x || !s.w || !s.y)) return FACE_ERR_ARG;
-            if (s.ld_x % 4 || s.ld_y % 4 || !al16(s.x) || !al16(s.y) || !al16(s.w) || s.ld_w % 4)
-                return FACE_ERR_UNSUPPORTED;
+            if (!al16(s.w) || s.ld_w % 4) return FACE_ERR_UNSUPPORTED;
             GemmProb& p = A.p[i];
-            p.x = s.x, p.ld_x = s.ld_x, p.m = s.m, p.w = s.w, p.ld_w = s.ld_w, p.y = s.y, p.ld_y = s.ld_y;
-            p.n = s.n, p.k = s.k, p.s_off = s.s_off, p.beta = s.beta;
             p.tiles = (int)((s.m + 16 * kGemmBB * kKcWaves - 1) / (16 * kGemmBB * kKcWaves));
             p.slices = (s.n + NSk - 1) / NSk;
             p.first_block = blocks;
@@ -557,17 +654,7 @@ extern "C" int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, 
     int64_t blocks = 0, total_cost = 0;
     for (int i = 0; i < n_probs; ++i) {
         const face_lin_problem& s = probs[i];
-        if (s.m < 0 || s.n < 16 || s.n % 16 || s.ld_x < s.k || s.ld_y < s.n || s.ld_w < (w_kn ? s.n : s.k))
-            return FACE_ERR_ARG;
-        if (scaled && (s.s_off < 0 || s.s_off % 4 || s.s_off + (x_scale ? s.k : 0) > ld_scale ||
-                       s.s_off + (y_scale ? s.n : 0) > ld_scale))
-            return FACE_ERR_ARG;
-        if (s.m > 0 && (!s.x || !s.w || !s.y)) return FACE_ERR_ARG;
-        if (s.ld_x % 4 || s.ld_y % 4 || !al16(s.x) || !al16(s.y) || (!w_kn && (!al16(s.w) || s.ld_w % 4)))
-            return FACE_ERR_UNSUPPORTED;
         GemmProb& p = A.p[i];
-        p.x = s.x, p.ld_x = s.ld_x, p.m = s.m, p.w = s.w, p.ld_w = s.ld_w, p.y = s.y, p.ld_y = s.ld_y, p.n = s.n;
-        p.k = s.k, p.s_off = s.s_off, p.beta = s.beta;
         p.tiles = (int)((s.m + 16 * kGemmBB * NW - 1) / (16 * kGemmBB * NW));
         p.slices = (s.n + NS - 1) / NS;
         p.first_block = blocks;
@@ -611,16 +698,22 @@ extern "C" int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, 
             return FACE_ERR_UNSUPPORTED;                                                                    \
         hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NW * kWave), lds, st, A);                      \
     } while (0)
-#define FACE_GEMM(NB_)                      \
-    do {                                    \
-        if (persist && x_scale)             \
-            FACE_GEMM_P(NB_, true, true);   \
-        else if (persist)                   \
-            FACE_GEMM_P(NB_, true, false);  \
-        else if (x_scale)                   \
-            FACE_GEMM_P(NB_, false, true);  \
-        else                                \
-            FACE_GEMM_P(NB_, false, false); \
+    if (x_scale && any_ext) return FACE_ERR_UNSUPPORTED;                 // x scale with split / op / y0
+    const int xm = x_scale ? 1 : (any_ext ? 2 : 0);
+#define FACE_GEMM(NB_)                     \
+    do {                                   \
+        if (persist && xm == 1)            \
+            FACE_GEMM_P(NB_, true, 1);     \
+        else if (persist && xm == 2)       \
+            FACE_GEMM_P(NB_, true, 2);     \
+        else if (persist)                  \
+            FACE_GEMM_P(NB_, true, 0);     \
+        else if (xm == 1)                  \
+            FACE_GEMM_P(NB_, false, 1);    \
+        else if (xm == 2)                  \
+            FACE_GEMM_P(NB_, false, 2);    \
+        else                               \
+            FACE_GEMM_P(NB_, false, 0);    \
     } while (0)
     switch (nb) {
         case 1: FACE_GEMM(1); break;

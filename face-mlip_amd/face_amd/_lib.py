@@ -68,21 +68,24 @@ _SIGS = {
     "face_radial_spline_order_noalloc": (ctypes.c_int, [P, P, I64, I32, I32, F32, P, P]),
     "face_edge_linear_fwd": (ctypes.c_int, [P, I32, I64, I32, P, P, I32, P, I32, P, P, I32, P]),
     "face_edge_linear_bwd": (ctypes.c_int, [P, I32, I32, P, I32, P, P, I64, P, I32, P, I32, P]),
-    "face_rows_linear": (ctypes.c_int, [P, I32, I32, P, P, P, I32, I32, P, I64, P]),
+    "face_rows_linear": (ctypes.c_int, [P, I32, I32, P, P, I32, I32, P, I64, P]),
     "face_eq_gate_fwd": (ctypes.c_int, [P, P, P, I64, I32, P, P, P]),
     "face_eq_gate_bwd": (ctypes.c_int, [P, P, P, P, P, I64, I32, P, P, P, P]),
     "face_layer_norm_fwd": (ctypes.c_int, [P, I64, I32, P, P, ctypes.c_float, P, P, P, P]),
     "face_layer_norm_bwd": (ctypes.c_int, [P, P, I64, I32, P, P, P, P, P]),
 }
 
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 
 class LinProblem(ctypes.Structure):
     """face_lin_problem of include/face_hip.h."""
     _fields_ = [("x", ctypes.c_void_p), ("ld_x", ctypes.c_int64), ("m", ctypes.c_int64), ("w", ctypes.c_void_p),
                 ("ld_w", ctypes.c_int64), ("y", ctypes.c_void_p), ("ld_y", ctypes.c_int64), ("n", ctypes.c_int32),
-                ("k", ctypes.c_int32), ("s_off", ctypes.c_int32), ("beta", ctypes.c_float)]
+                ("k", ctypes.c_int32), ("s_off", ctypes.c_int32), ("beta", ctypes.c_float),
+                ("x2", ctypes.c_void_p), ("ld_x2", ctypes.c_int64), ("k1", ctypes.c_int32), ("x_op", ctypes.c_int32),
+                ("xz", ctypes.c_void_p), ("ld_xz", ctypes.c_int64), ("bias", ctypes.c_void_p),
+                ("y0", ctypes.c_void_p), ("ld_y0", ctypes.c_int64), ("n_y0", ctypes.c_int32), ("pad_", ctypes.c_int32)]
 
 
 def lib():

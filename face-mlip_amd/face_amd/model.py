@@ -26,6 +26,7 @@ kernels support (face/kernels.py:10-11). Parameters enter the forward as constan
 energies and forces differentiate through positions only.
 """
 import math
+import os
 
 import torch
 import torch.nn as nn
@@ -36,6 +37,12 @@ from .neighbors import graph_from_padded
 from .ops import Graph
 
 RANKS = [(0, 1), (1, 4), (4, 10), (10, 20)]   # monomial range of each rank (face/cartesian.py:18)
+# The readout chain on the row GEMM (ops.readout: 4 launches forward, 5 backward) instead of
+# LayerNorm + library GEMMs + elementwise SiLU / residual: measured slower at the benchmark widths
+# (24,000-atom C160 step 19.1 -> 21.4 ms, 864-atom C96 0.84 -> 0.96 ms: the whole-K weight
+# slices leave the N x 10C -> 2C input layer and its gradient under-occupied, and the small
+# 2C-wide layers pay a weight-slice staging per workgroup), so it is opt-in.
+READOUT_ROW_GEMM = os.environ.get("FACE_READOUT_ROW_GEMM", "0") == "1"
 
 
 class BesselEnvelope(nn.Module):
@@ -301,6 +308,39 @@ class FactorBlock(nn.Module):
             A.append(y.view(x.shape[0], N, C) * s[None, :, l, :])                 # (k_l, N, C)
         return A
 
+    def _readout_weights(self):
+        """Frozen readout weights in the row GEMM's forms, cached with the parameters:
+        (W0 (2C, 10C + 4), b0, W1, b1, W2p (n_pad, 2C), b2p, Wg, bg, Wstack): W2p / b2p hold W2's
+        channel rows first, its energy row at C and zero rows up to n_pad = C + 16 (the layer
+        writes [h_new | e | 0]); Wstack = [W0[:, :9C]; Wg] (4C, 9C) for the backward of the
+        invariant row through both the out MLP and the gate (W0[:, :9C] alone without a gate)."""
+        C, nf = self.C, self.N_INV * self.C
+        mods = [self.out[0], self.out[2], self.out[4]] + ([self.gate] if self.eq_out else [])
+        fr = [frozen(m) for m in mods]
+        key = _key(*[t for wb in fr for t in wb])
+        c = self.__dict__.get("_rw")
+        if c is None or not _same(c[0], key):
+            with torch.no_grad():
+                (W0, b0), (W1, b1), (W2, b2) = fr[:3]
+                n_pad = C + 16
+                W2p = W2.new_zeros(n_pad, W2.shape[1])
+                W2p[:C] = W2[1:]
+                W2p[C] = W2[0]
+                b2p = b2.new_zeros(n_pad)
+                b2p[:C] = b2[1:]
+                b2p[C] = b2[0]
+                W0c = W0.contiguous()
+                if self.eq_out:
+                    Wg, bg = fr[3]
+                    Wg, bg = Wg.contiguous(), bg.contiguous()
+                    Wst = torch.cat([W0c[:, :nf], Wg], 0).contiguous()
+                else:
+                    Wg = bg = Wst = None
+                vals = (W0c, b0.contiguous(), W1.contiguous(), b1.contiguous(), W2p, b2p, Wg, bg, Wst)
+            c = (key, vals)
+            self.__dict__["_rw"] = c
+        return c[1]
+
     def _mix_t(self, wm):
         """Contiguous transposes (B K, C) of the four frozen mix weights, cached with them."""
         key = _key(*wm)
@@ -348,6 +388,16 @@ class FactorBlock(nn.Module):
         else:
             feats, V, Ms = ops.node_features(ys[0], ys[1], ys[2], ys[3], None, None, False, C)
         nf = self.N_INV * C
+        if READOUT_ROW_GEMM and C % 16 == 0 and nf <= 2048:
+            # LayerNorm, the out MLP and the residual split on the row GEMM (four launches forward;
+            # opt-in: slower than the library GEMMs at the benchmark widths)
+            rw = self._readout_weights()
+            e, h_new, gvm = ops.readout(feats, h, self.norm.weight.detach(), self.norm.bias.detach(), self.norm.eps,
+                                        *rw)
+            eq_new = None
+            if self.eq_out:
+                eq_new = ops.eq_gate(V, Ms, gvm)                                  # (3,N,C), (6,N,C)
+            return e, h_new, A, eq_new
         if nf % 4 == 0 and nf <= 2048:
             inv = ops.layer_norm(feats, self.norm.weight.detach(), self.norm.bias.detach(), self.norm.eps)
         else:

@@ -327,6 +327,80 @@ def readout_split(o, h):
     return ReadoutSplit.apply(o, h)
 
 
+class Readout(torch.autograd.Function):
+    """The readout of a pass (face/model.py:331-339, with the gate row of an eq_out pass,
+    face/model.py:286-287), forward and input gradients on the row GEMM:
+        inv = LayerNorm(feats);  z1 = [inv | h] W0^T + b0;  z2 = silu(z1) W1^T + b1;
+        o = silu(z2) W2^T + b2;  e = o[:, 0];  h_new = h + o[:, 1:];  gvm = inv Wg^T + bg.
+    The SiLUs are applied to the GEMM inputs as they load and their derivatives likewise in the
+    backward chain, [inv | h] and [dz1 | dgvm] are read as two column ranges without copies, and
+    the residual h enters the last layer as its initial sum: W2p = W2 with the energy row moved
+    last and zero rows to a multiple of 16 (n_pad), so one launch writes [h_new | e | 0] (N, n_pad).
+    Four launches forward (LayerNorm and three GEMMs), five backward. Weights receive no
+    gradient. Returns (e (N, 1), h_new (N, C), gvm (N, 2C) or an empty tensor)."""
+
+    @staticmethod
+    def forward(ctx, feats, h, ln_w, ln_b, eps, w0, b0, w1, b1, w2p, b2p, wg, bg, wstack):
+        _lib.require_gpu(feats, h)
+        dev = feats.device
+        N, nf = feats.shape
+        C = h.shape[1]
+        H1, H2, n_pad = w0.shape[0], w1.shape[0], w2p.shape[0]
+        feats = feats.contiguous().float()
+        inv = torch.empty_like(feats)
+        mean = torch.empty(N, device=dev)
+        rstd = torch.empty(N, device=dev)
+        st = _lib.stream_of(feats)
+        call("face_layer_norm_fwd", ptr(feats), N, nf, ptr(ln_w), ptr(ln_b), float(eps), ptr(inv), ptr(mean),
+             ptr(rstd), st, label="ln_fwd")
+        z1 = torch.empty(N, H1, device=dev)
+        probs = [lin(inv, w0, z1, x2=h, bias=b0)]
+        gvm = torch.empty(0, device=dev)
+        if wg is not None:
+            gvm = torch.empty(N, wg.shape[0], device=dev)
+            probs.append(lin(inv, wg, gvm, bias=bg))
+        rows_linear(probs, label="readout_in")
+        z2 = torch.empty(N, H2, device=dev)
+        rows_linear([lin(z1, w1, z2, x_op=1, bias=b1)], label="readout_hid")
+        out = torch.empty(N, n_pad, device=dev)
+        rows_linear([lin(z2, w2p, out, x_op=1, bias=b2p, beta=1.0, y0=h, n_y0=C)], label="readout_out")
+        ctx.save_for_backward(feats, ln_w, mean, rstd, z1, z2)
+        ctx.w = (w0, w1, w2p, wstack)
+        ctx.dims = (N, nf, C, n_pad, wg is not None)
+        return out[:, C:C + 1], out[:, :C], gvm
+
+    @staticmethod
+    def backward(ctx, ge, gh, dgvm):
+        feats, ln_w, mean, rstd, z1, z2 = ctx.saved_tensors
+        w0, w1, w2p, wstack = ctx.w
+        N, nf, C, n_pad, gate = ctx.dims
+        dev = feats.device
+        gh = gh if gh is not None else feats.new_zeros(N, C)
+        ge = ge if ge is not None else feats.new_zeros(N, 1)
+        do = torch.cat([gh, ge, feats.new_zeros(N, n_pad - C - 1)], 1)          # (N, n_pad): [gh | ge | 0]
+        gh = do[:, :C]
+        da2 = torch.empty(N, w1.shape[0], device=dev)
+        rows_linear([lin(do, w2p, da2)], w_kn=True, label="readout_out_bwd")
+        da1 = torch.empty(N, w0.shape[0], device=dev)
+        rows_linear([lin(da2, w1, da1, x_op=2, xz=z2)], w_kn=True, label="readout_hid_bwd")
+        dinv = torch.empty(N, nf, device=dev)
+        dh = torch.empty(N, C, device=dev)
+        use_gate = gate and dgvm is not None and dgvm.numel() > 0
+        pa = lin(da1, wstack if use_gate else w0[:, :nf], dinv, x_op=2, xz=z1,
+                 x2=dgvm.contiguous() if use_gate else None)
+        pb = lin(da1, w0[:, nf:nf + C], dh, x_op=2, xz=z1, beta=1.0, y0=gh)
+        rows_linear([pa, pb], w_kn=True, label="readout_in_bwd")
+        dfeats = torch.empty_like(feats)
+        call("face_layer_norm_bwd", ptr(feats), ptr(dinv), N, nf, ptr(ln_w), ptr(mean), ptr(rstd), ptr(dfeats),
+             _lib.stream_of(feats), label="ln_bwd")
+        return dfeats, dh, None, None, None, None, None, None, None, None, None, None, None, None
+
+
+def readout(feats, h, ln_w, ln_b, eps, w0, b0, w1, b1, w2p, b2p, wg=None, bg=None, wstack=None):
+    """(e (N, 1), h_new (N, C), gvm (N, 2C) | empty); see Readout."""
+    return Readout.apply(feats, h, ln_w, ln_b, eps, w0, b0, w1, b1, w2p, b2p, wg, bg, wstack)
+
+
 class StructureSum(torch.autograd.Function):
     """Per-structure sum of per-atom values (atoms of a structure are contiguous)."""
 
@@ -907,23 +981,44 @@ def node_features(y0, y1, y2, y3, a, b, eq, C):
 
 
 # ----------------------------------------------------------------------------- row-block linear layers
+def lin(x, w, y, s_off=0, beta=0.0, x2=None, x_op=0, xz=None, bias=None, y0=None, n_y0=None):
+    """One problem of rows_linear: y = (beta y0 + op(x | x2) w^T + bias) [* scales]; x (m, k1),
+    x2 (m, k - k1) the rest of the input columns (no concatenated copy), x_op on the x columns:
+    0 none, 1 silu, 2 x * silu'(xz); y0 the initial sum (default y) over its first n_y0 columns.
+    2-d fp32 views with unit column stride."""
+    return dict(x=x, w=w, y=y, s_off=s_off, beta=beta, x2=x2, x_op=x_op, xz=xz, bias=bias, y0=y0, n_y0=n_y0)
+
+
 def rows_linear(probs, w_kn=False, bias=None, xs=None, ys=None, group=None, period=1, label="rows_linear"):
-    """One launch of up to four row-block linear problems (no autograd). probs: list of
-    (x (m, k), w, y (m, n), s_off, beta) with 2-d fp32 row-major views; w is (n, k) or, with
-    w_kn, (k, n). y[r] = (beta y[r] + (x[r] * xs[g(r), s_off:]) w^T + bias) * ys[g(r), s_off:],
-    g(r) = group[r % period]; xs / ys are (n_groups, ld) tables or None."""
+    """One launch of up to four row-block linear problems (no autograd). probs: lin() dicts or
+    (x (m, k), w, y (m, n), s_off, beta) tuples; w is (n, k) or, with w_kn, (k, n).
+    y[r] = (beta y0[r] + (op(x)[r] * xs[g(r), s_off:]) w^T + bias) * ys[g(r), s_off:],
+    g(r) = group[r % period]; xs / ys are (n_groups, ld) tables or None; `bias` applies to the
+    problems without their own."""
     arr = (_lib.LinProblem * len(probs))()
     ref = None
-    for i, (x, w, y, s_off, beta) in enumerate(probs):
+    for i, pr in enumerate(probs):
+        if not isinstance(pr, dict):
+            pr = lin(*pr)
+        x, w, y, x2, xz, y0 = pr["x"], pr["w"], pr["y"], pr["x2"], pr["xz"], pr["y0"]
+        b = pr["bias"] if pr["bias"] is not None else bias
         assert x.dim() == 2 and y.dim() == 2 and w.dim() == 2 and x.stride(1) == 1 and y.stride(1) == 1
         assert w.stride(1) == 1 and x.shape[0] == y.shape[0]
+        k1 = x.shape[1]
+        k = k1 + (x2.shape[1] if x2 is not None else 0)
+        for t in (x2, xz, y0):
+            assert t is None or (t.dim() == 2 and t.stride(1) == 1 and t.shape[0] == x.shape[0])
+        n_y0 = pr["n_y0"] if pr["n_y0"] is not None else (y0.shape[1] if y0 is not None else y.shape[1])
         arr[i] = _lib.LinProblem(x.data_ptr(), x.stride(0), x.shape[0], w.data_ptr(), w.stride(0), y.data_ptr(),
-                                 y.stride(0), y.shape[1], x.shape[1], int(s_off), float(beta))
+                                 y.stride(0), y.shape[1], k, int(pr["s_off"]), float(pr["beta"]),
+                                 ptr(x2), 0 if x2 is None else x2.stride(0), k1, int(pr["x_op"]),
+                                 ptr(xz), 0 if xz is None else xz.stride(0), ptr(b),
+                                 ptr(y0), 0 if y0 is None else y0.stride(0), int(n_y0), 0)
         ref = y
     tab = xs if xs is not None else ys
     if xs is not None and ys is not None and xs.shape[0] != ys.shape[0]:
         raise ValueError("rows_linear: xs and ys must have the same number of groups")
-    call("face_rows_linear", arr, len(probs), 1 if w_kn else 0, ptr(bias), ptr(xs), ptr(ys),
+    call("face_rows_linear", arr, len(probs), 1 if w_kn else 0, ptr(xs), ptr(ys),
          0 if tab is None else tab.stride(0), 0 if tab is None else tab.shape[0], ptr(group), int(period),
          _lib.stream_of(ref), label=label)
 

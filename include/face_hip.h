@@ -318,7 +318,17 @@ int face_radial_spline_order_noalloc(const float* r, const int32_t* pair, int64_
 
 /* ---------------------------------------------------------------- row-block linear layers
  * One problem: x (m, ld_x >= k) rows, w (n, k) row-major with row stride ld_w (w_kn = 0) or
- * (k, n) with row stride ld_w (w_kn = 1), y (m, ld_y >= n); n and k multiples of 16. */
+ * (k, n) with row stride ld_w (w_kn = 1), y (m, ld_y >= n); n and k multiples of 16.
+ * Optional per problem (NULL / 0 = absent):
+ *   x2, ld_x2, k1   input columns k >= k1 are read from x2 (column k - k1): x = [x | x2], the
+ *                   concatenation of two activations without a copy (k1 a multiple of 16; k1 = k
+ *                   when x2 is NULL);
+ *   x_op, xz, ld_xz transform of the input columns k < k1 as they load: 0 none, 1 silu(x),
+ *                   2 x * silu'(xz) (xz (m, ld_xz) the pre-activation, for backward chains);
+ *   bias            (n) added to every row;
+ *   y0, ld_y0, n_y0 initial value of the sum: beta * y0[r, c] for columns c < n_y0 (a multiple
+ *                   of 4), 0 beyond; y0 NULL: beta * y[r, :] (y0 may be another tensor, e.g. a
+ *                   residual). */
 typedef struct {
     const float* x;
     int64_t ld_x, m;
@@ -328,18 +338,28 @@ typedef struct {
     int64_t ld_y;
     int32_t n, k, s_off;
     float beta;
+    const float* x2;
+    int64_t ld_x2;
+    int32_t k1, x_op;
+    const float* xz;
+    int64_t ld_xz;
+    const float* bias;
+    const float* y0;
+    int64_t ld_y0;
+    int32_t n_y0, pad_;
 } face_lin_problem;
 /* For each problem (1..4 of them, host array):
- *   y[r, :] = (beta y[r, :] + (x[r, :] * xs[r, :]) w^T + bias) * ys[r, :]
+ *   y[r, :] = (beta y0[r, :] + (op(x)[r, :] * xs[r, :]) w^T + bias) * ys[r, :]
  * with xs[r, k] = x_scale[group[r % period] * ld_scale + s_off + k] and ys likewise over the
  * n output columns, group values in [0, n_groups) (n_groups <= 64: the scale tables' rows, staged
- * in LDS); x_scale, y_scale, bias may be NULL (beta = 0: y is not read). The linear
- * layers of the node features: mix / tmix / proj and the readout input (face/model.py:498-533,
- * :537-544) with the elem_scale factor, and their input gradients (w_kn = 1). x, y, bias and the
- * scale tables 16-byte aligned, ld_x, ld_y (and ld_w, ld_scale, s_off) multiples of 4. */
-int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, int32_t w_kn, const float* bias,
-                     const float* x_scale, const float* y_scale, int32_t ld_scale, int32_t n_groups,
-                     const int32_t* group, int64_t period, void* stream);
+ * in LDS); x_scale, y_scale may be NULL (beta = 0: y0 / y is not read). The linear layers of the
+ * node features: mix / tmix / proj (face/model.py:498-533, :537-544) with the elem_scale factor,
+ * the readout MLP (face/model.py:331-339: [inv | h] W0^T + b0, then SiLU-on-load layers, the
+ * residual as y0) and their input gradients (w_kn = 1). x, x2, xz, y, y0, bias and the scale
+ * tables 16-byte aligned, every ld and s_off a multiple of 4. */
+int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, int32_t w_kn, const float* x_scale,
+                     const float* y_scale, int32_t ld_scale, int32_t n_groups, const int32_t* group, int64_t period,
+                     void* stream);
 
 /* ---------------------------------------------------------------- per-edge linear layers
  * Forward: y (E, ld_y) = x (E, ld_x) w^T + b + tab[idx[e]], w (F, K) row-major, b (F) and tab

@@ -723,6 +723,102 @@ def test_rows_linear_matches_torch(case, kc, monkeypatch):
     assert max(errs) < 1e-5, errs
 
 
+@pytest.mark.parametrize("kc", [None, "1"])
+@pytest.mark.parametrize("w_kn", [False, True])
+def test_rows_linear_split_input_transforms_and_initial_sum(w_kn, kc, monkeypatch):
+    """The readout forms of face_rows_linear vs torch fp64: input columns from two tensors
+    ([x | x2], the split at k1), silu(x) and x * silu'(xz) applied to the x columns as they load,
+    a bias per problem, and the sum started at beta * y0 over the first n_y0 columns of another
+    tensor (a residual); four problems of different K in one launch, ragged rows, strided views.
+    kc = "1" forces the K-chunked kernel."""
+    from face_amd import ops
+    if kc is not None:
+        monkeypatch.setenv("FACE_ROWS_GEMM_KC", kc)
+    say("rows_linear split/ops", w_kn, kc)
+    torch.manual_seed(7)
+    m = 1203
+    silu = lambda t: t * torch.sigmoid(t)
+    dsilu = lambda g, z: g * torch.sigmoid(z) * (1 + z * (1 - torch.sigmoid(z)))
+    base = torch.randn(m, 400, device=DEV)
+    cases = []
+    # (x cols k1, x2 cols, n, x_op, bias, y0 cols)
+    for k1, k2, n, op, has_b, ny0 in ((144, 16, 64, 0, True, 0), (96, 0, 48, 1, True, 32), (64, 32, 80, 2, False, 80),
+                                      (32, 0, 16, 1, True, 16)):
+        x = base[:, :k1] if op != 2 else torch.randn(m, k1, device=DEV)          # a strided view
+        x2 = torch.randn(m, k2 + 8, device=DEV)[:, :k2] if k2 else None
+        xz = torch.randn(m, k1, device=DEV) if op == 2 else None
+        k = k1 + k2
+        w = torch.randn(k, n, device=DEV) / k ** 0.5 if w_kn else torch.randn(n, k + 4, device=DEV)[:, :k] / k ** 0.5
+        bias = torch.randn(n, device=DEV) if has_b else None
+        y0 = torch.randn(m, ny0 + 4, device=DEV)[:, :ny0] if ny0 else None
+        y = torch.empty(m, n, device=DEV)
+        cases.append((ops.lin(x, w, y, x2=x2, x_op=op, xz=xz, bias=bias, y0=y0, beta=1.0 if ny0 else 0.0,
+                              n_y0=ny0 if ny0 else None), (x, x2, xz, w, bias, y0, op, ny0)))
+    ops.rows_linear([c[0] for c in cases], w_kn=w_kn)
+    errs = []
+    for pr, (x, x2, xz, w, bias, y0, op, ny0) in cases:
+        d = lambda t: None if t is None else t.double().cpu()
+        xi = d(x)
+        xi = silu(xi) if op == 1 else (dsilu(xi, d(xz)) if op == 2 else xi)
+        if x2 is not None:
+            xi = torch.cat([xi, d(x2)], 1)
+        ref = xi @ (d(w) if w_kn else d(w).T)
+        if bias is not None:
+            ref = ref + d(bias)
+        if ny0:
+            ref[:, :ny0] += d(y0)
+        errs.append(rel(pr["y"], ref))
+    say("   errs", errs)
+    assert max(errs) < 1e-5, errs
+
+
+@pytest.mark.parametrize("C,gate", [(160, True), (160, False), (96, True), (32, False)])
+def test_readout_matches_torch(C, gate):
+    """The pass readout on the row GEMM (face/model.py:331-339, the gate row of :286-287):
+    LayerNorm -> [inv | h] W0^T + b0 -> SiLU -> W1 -> SiLU -> W2 with the energy column and the
+    residual h + o[:, 1:], and gvm = inv Wg^T + bg; values and the gradients of feats and h (with
+    the gate row's gradient entering the backward) vs torch fp64 autograd."""
+    from face_amd import ops
+    say("readout", C, gate)
+    torch.manual_seed(C + gate)
+    N, nf = 777, 9 * C
+    feats = torch.randn(N, nf, device=DEV) * 2 + 0.3
+    h = torch.randn(N, C + 16, device=DEV)[:, :C]                  # a strided residual, like a previous h_new
+    lnw, lnb = torch.rand(nf, device=DEV) + 0.5, torch.randn(nf, device=DEV) * 0.1
+    W0 = torch.randn(2 * C, 10 * C + 4, device=DEV) / (10 * C) ** 0.5
+    b0 = torch.randn(2 * C, device=DEV) * 0.1
+    W1, b1 = torch.randn(2 * C, 2 * C, device=DEV) / (2 * C) ** 0.5, torch.randn(2 * C, device=DEV) * 0.1
+    W2, b2 = torch.randn(C + 1, 2 * C, device=DEV) / (2 * C) ** 0.5, torch.randn(C + 1, device=DEV) * 0.1
+    Wg, bg = torch.randn(2 * C, nf, device=DEV) / nf ** 0.5, torch.randn(2 * C, device=DEV)
+    n_pad = C + 16
+    W2p = W2.new_zeros(n_pad, 2 * C)
+    W2p[:C], W2p[C] = W2[1:], W2[0]
+    b2p = b2.new_zeros(n_pad)
+    b2p[:C], b2p[C] = b2[1:], b2[0]
+    Wst = torch.cat([W0[:, :nf], Wg], 0).contiguous()
+    fd, hd = feats.clone().requires_grad_(True), h.clone().requires_grad_(True)
+    e, hn, gvm = ops.readout(fd, hd, lnw, lnb, 1e-5, W0, b0, W1, b1, W2p, b2p, *((Wg, bg, Wst) if gate else (None, None, None)))
+    ge, gh = torch.randn(N, 1, device=DEV), torch.randn(N, C, device=DEV)
+    gg = torch.randn(N, 2 * C, device=DEV)
+    loss = (e * ge).sum() + (hn * gh).sum() + ((gvm * gg).sum() if gate else 0.0)
+    gf, ghh = torch.autograd.grad(loss, (fd, hd))
+    c = lambda t: t.detach().double().cpu()
+    f2, h2 = c(feats).requires_grad_(True), c(h).requires_grad_(True)
+    inv = torch.nn.functional.layer_norm(f2, (nf,), c(lnw), c(lnb), 1e-5)
+    z = torch.cat([inv, h2, torch.zeros(N, 4, dtype=torch.float64)], 1) @ c(W0).T + c(b0)
+    z = torch.nn.functional.silu(z) @ c(W1).T + c(b1)
+    o = torch.nn.functional.silu(z) @ c(W2).T + c(b2)
+    e2, hn2 = o[:, :1], h2 + o[:, 1:]
+    loss2 = (e2 * c(ge)).sum() + (hn2 * c(gh)).sum()
+    if gate:
+        gvm2 = inv @ c(Wg).T + c(bg)
+        loss2 = loss2 + (gvm2 * c(gg)).sum()
+    gf2, gh2 = torch.autograd.grad(loss2, (f2, h2))
+    errs = [rel(e, e2), rel(hn, hn2), rel(gf, gf2), rel(ghh, gh2)] + ([rel(gvm, gvm2)] if gate else [])
+    say("   errs", errs)
+    assert max(errs) < 1e-5, errs
+
+
 @pytest.mark.parametrize("transport,Cin", [(True, 160), (False, 160), (False, 512), (True, 32)])
 def test_scaled_mix_forward_backward(transport, Cin):
     """A_l = (Af_l W_l^T [+ D_l T_l^T]) * s[z] for the four ranks (face/model.py:498-501, :530-533)

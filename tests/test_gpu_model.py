@@ -408,6 +408,24 @@ def test_factor_density_mix_routes_match_oracle(fused, monkeypatch):
     say(f"  dE/E {dE:.2e}  max|dF|/rms {dF:.2e}")
 
 
+@pytest.mark.parametrize("k,n_atoms,n_mol", [(0, None, 16), (3, 1500, None)])
+def test_row_gemm_readout_route_matches_oracle(k, n_atoms, n_mol, monkeypatch):
+    """The opt-in readout on the row GEMM (LayerNorm and the out MLP with SiLU on load, the gate
+    row and the residual in the same launches) against the oracle, flagship and CP workloads."""
+    from face_amd import model as fm, systems
+    from face_amd.neighbors import build_graph
+    monkeypatch.setattr(fm, "READOUT_ROW_GEMM", True)
+    sts, kw, el, desc = systems.workload(k, n_atoms=n_atoms)
+    if n_mol:
+        sts = sts[:n_mol]
+    say("row-GEMM readout", desc)
+    m = product_model(kw, el)
+    o = m(build_graph(sts, kw["rc"]))
+    Eo, Fo = _oracle_EF(sts, kw, el)
+    dE, dF = check(o["energy"].detach().cpu(), o["forces"].detach().cpu(), Eo, Fo)
+    say(f"  dE/E {dE:.2e}  max|dF|/rms {dF:.2e}")
+
+
 def test_workload4_lds_backward_matches_oracle(monkeypatch):
     """The C256 B16 K64 model with the factor-density backward that stages each atom's G in LDS (the
     route taken above 64 atoms per CU, forced here on a 1,200-atom box of the same recipe) against
