@@ -669,6 +669,20 @@ def trace_summary(stats_csv, bench_log, out_path, title):
             f[1] += float(x["TotalDurationNs"])
     for f, (c, t) in sorted(fam.items(), key=lambda kv: -kv[1][1]):
         out.append(f"| {f} | {c} | {t / 1e6:.2f} | {t / c / 1e3:.1f} |\n")
+    # register / scratch footprint per library kernel from the dispatch records beside the stats
+    trace_csv = stats_csv.replace("kernel_stats.csv", "kernel_trace.csv")
+    if trace_csv != stats_csv and os.path.exists(trace_csv):
+        res = {}
+        for x in csv.DictReader(open(trace_csv)):
+            if "face::" in x["Kernel_Name"]:
+                nm = x["Kernel_Name"].replace("void ", "").split("(")[0].replace("face::", "")
+                res[nm] = (x.get("VGPR_Count"), x.get("Accum_VGPR_Count"), x.get("SGPR_Count"),
+                           x.get("LDS_Block_Size"), x.get("Scratch_Size"))
+        out.append("\nLibrary kernels' resources (dispatch records of the same run; scratch = per-lane private "
+                   "segment bytes, non-zero when registers spill):\n\n| kernel | VGPR | AGPR | SGPR | LDS bytes | "
+                   "scratch |\n|---|---:|---:|---:|---:|---:|\n")
+        for nm, v in sorted(res.items()):
+            out.append(f"| `{nm}` | " + " | ".join(str(t) for t in v) + " |\n")
     out.append(f"\nAll kernels of the run: {tot / 1e6:.1f} ms total. Top 30:\n\n"
                "| total ms | calls | avg us | % | kernel |\n|---:|---:|---:|---:|---|\n")
     for x in sorted(rows, key=lambda r: -float(r["TotalDurationNs"]))[:30]:

@@ -143,18 +143,22 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
     const int64_t it_beg = one ? blockIdx.x : item_at(A.total_cost * (int64_t)blockIdx.x / gridDim.x);
     const int64_t it_end = one ? min(A.items, (int64_t)blockIdx.x + 1) : item_at(A.total_cost * ((int64_t)blockIdx.x + 1) / gridDim.x);
     int cur_pi = -1, cur_slice = -1;
-    auto run_item = [&](int64_t it) __attribute__((always_inline)) {
-        int pi = 0;
+    // Work items: (problem, column slice, row tile). Persistent runs walk 32-row wave tiles,
+    // slice by slice: the workgroup stages a slice once, then its waves take the run's tiles of
+    // that slice round robin (at most one tile of imbalance per wave); one item per workgroup is a
+    // tile of 32 NW rows.
+    auto locate = [&](int64_t it, int& pi, int& slice, int64_t& tile) {
+        pi = 0;
 #pragma unroll
         for (int k = 1; k < kGemmMaxProbs; ++k)
             if (k < A.n_probs && it >= A.p[k].first_block) pi = k;
+        const int64_t local = it - A.p[pi].first_block;
+        slice = PERSIST ? (int)(local / A.p[pi].tiles) : (int)(local % A.p[pi].slices);
+        tile = PERSIST ? local - (int64_t)slice * A.p[pi].tiles : local / A.p[pi].slices;
+    };
+    // stage the weight slice and the side tables of (pi, slice) unless they are staged
+    auto stage = [&](int pi, int slice) __attribute__((always_inline)) {
         const GemmProb& P = A.p[pi];
-        const int64_t local = it - P.first_block;
-        // persistent runs go slice by slice (the weight slice stays staged); one item per
-        // workgroup goes tile by tile (the slices of a row tile run side by side and share its
-        // rows in cache)
-        const int slice = PERSIST ? (int)(local / P.tiles) : (int)(local % P.slices);
-        const int64_t tile = PERSIST ? local - (int64_t)slice * P.tiles : local / P.slices;
         const int K = P.k, SK = K + 4;
         const int n0 = slice * A.NS;
         const int ns = min(A.NS, P.n - n0);                             // a multiple of 16
@@ -209,7 +213,14 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
             __syncthreads();
             cur_pi = pi, cur_slice = slice;
         }
-        const int64_t m0 = (tile * NW + wv) * (16 * kGemmBB);
+    };
+    // rows m0 .. m0 + 31 of problem pi against the staged slice
+    auto compute = [&](int pi, int slice, int64_t m0) __attribute__((always_inline)) {
+        const GemmProb& P = A.p[pi];
+        const int K = P.k, SK = K + 4;
+        const int n0 = slice * A.NS;
+        const int ns = min(A.NS, P.n - n0);
+        const GemmSide side(sW + A.side_off, A, 16 * NB);
         if (m0 >= P.m) return;
         bool ok[kGemmBB];
         int64_t rcs[kGemmBB];
@@ -312,9 +323,24 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
         }
     };
     if (PERSIST) {
-        for (int64_t it = it_beg; it < it_end; ++it) run_item(it);
+        int64_t it = it_beg;
+        while (it < it_end) {                                            // uniform over the workgroup
+            int pi, slice;
+            int64_t t;
+            locate(it, pi, slice, t);
+            const GemmProb& P = A.p[pi];
+            const int64_t seg_end = min(it_end, P.first_block + (int64_t)(slice + 1) * P.tiles);
+            stage(pi, slice);
+            for (int64_t w = it + wv; w < seg_end; w += NW)
+                compute(pi, slice, (w - P.first_block - (int64_t)slice * P.tiles) * (16 * kGemmBB));
+            it = seg_end;
+        }
     } else {
-        run_item(blockIdx.x);
+        int pi, slice;
+        int64_t t;
+        locate(blockIdx.x, pi, slice, t);
+        stage(pi, slice);
+        compute(pi, slice, (t * NW + wv) * (16 * kGemmBB));
     }
 }
 
@@ -686,6 +712,21 @@ extern "C" int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, 
     for (int i = 0; i < n_probs; ++i)
         if (A.p[i].slices > 1 && A.p[i].tiles > 0) multi_slice = true;
     const bool persist = blocks > n_cu * wg_cu && (!w_kn || !multi_slice);
+    if (persist) {
+        // persistent runs count 32-row wave tiles as items (the cost split can then end a run
+        // inside a workgroup tile; the run's waves share its tiles)
+        blocks = total_cost = 0;
+        for (int i = 0; i < n_probs; ++i) {
+            GemmProb& p = A.p[i];
+            p.tiles = (int)((probs[i].m + 16 * kGemmBB - 1) / (16 * kGemmBB));
+            p.first_block = blocks;
+            p.cost0 = total_cost;
+            blocks += (int64_t)p.tiles * p.slices;
+            total_cost += (int64_t)p.tiles * p.slices * p.cost;
+        }
+        A.items = blocks;
+        A.total_cost = total_cost;
+    }
     const int64_t grid = persist ? n_cu * wg_cu : blocks;
     const hipStream_t st = (hipStream_t)stream;
 #define FACE_GEMM_P(NB_, P_, X_)                                                                            \
