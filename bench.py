@@ -648,7 +648,8 @@ def trace_summary(stats_csv, bench_log, out_path, title):
     tot = sum(float(r["TotalDurationNs"]) for r in rows)
     base_fam = {kn: fam for fam, kns in FAMILY_KERNELS.items() for kn in kns}
     out = [f"# Kernel-time summary: {title}\n\nCommand (repo root, MI355X, ROCm 7.2):\n\n```\n"
-           f"rocprofv3 --kernel-trace --stats --output-format csv -d gpurun_out/prof -o bench -- python -u bench.py "
+           f"rocprofv3 --kernel-trace --stats --output-format csv -d {os.path.dirname(stats_csv)} -o bench -- "
+           f"python -u bench.py "
            f"{d.get('_argv', '')}\npython bench.py --trace-summary {stats_csv} <bench stdout> {out_path}\n```\n\n"]
     out.append(f"Bench line of the same run: value {d['value']:.0f} atom-steps/s, {d['ms_per_step']:.3f} ms/step "
                f"({d['config']['workload']}).\n\n")
