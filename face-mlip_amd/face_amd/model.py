@@ -165,13 +165,6 @@ def mlp(sizes):
     return nn.Sequential(*layers[:-1])
 
 
-def run_frozen(seq, x):
-    """An mlp() stack (Linear / SiLU) on frozen weights."""
-    for m in seq:
-        x = F.silu(x) if isinstance(m, nn.SiLU) else F.linear(x, *frozen(m))
-    return x
-
-
 class FactorBlock(nn.Module):
     """One factorised interaction pass; registrations follow MomentBlock then FactorBlock."""
     N_INV = 9
@@ -363,7 +356,10 @@ class FactorBlock(nn.Module):
         return c[1]
 
     # ------------------------------------------------------------------ invariants + readout
-    def forward(self, h, rb, r, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g, order=None):
+    def forward(self, h, rb, r, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g, order=None, acc=None, last=False):
+        """(e (N, 1), h_new (N, C) | None, A, eq_new) of one pass. acc: the per-forward dict of
+        shared moment-set gradients (ops.rank_proj) or None; last: the final pass, whose h_new is
+        not computed."""
         C = self.C
         A = self.moments(h, rb, r, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g, order)
         allsets = sets + [A]
@@ -372,7 +368,7 @@ class FactorBlock(nn.Module):
         if C % 16 == 0:
             # proj over the concatenated moment sets as a sum of per-set products (no concat copy),
             # all four ranks per launch, later sets accumulating in the epilogue
-            ys = list(ops.rank_proj(ws, allsets))                                # (k_l, N, C | 3C | 3C | 2C)
+            ys = list(ops.rank_proj(ws, allsets, acc))                           # (k_l, N, C | 3C | 3C | 2C)
         else:
             ys = []
             for l in range(4):
@@ -403,18 +399,19 @@ class FactorBlock(nn.Module):
         else:
             inv = F.layer_norm(feats, (nf,), self.norm.weight.detach(), self.norm.bias.detach(), self.norm.eps)
         W0, b0 = frozen(self.out[0])
-        # out[0] on cat([inv, h, 0 (4)]) as two accumulating GEMMs (no concatenated copy)
-        z = F.linear(inv, W0[:, :nf], b0).addmm_(h, W0[:, nf:nf + C].t())
-        o = run_frozen(self.out[2:], F.silu(z))
+        W1, b1 = frozen(self.out[2])
+        W2, b2 = frozen(self.out[4])
+        Wg, bg = frozen(self.gate) if self.eq_out else (None, None)
+        # out MLP on cat([inv, h, 0 (4)]) (two accumulating GEMMs, no concatenated copy), residual
+        # and gate row as one autograd node; the last pass computes the energy row only
+        e, h_new, gvm = ops.readout_mlp(inv, h, W0[:, :nf], W0[:, nf:nf + C], b0, W1, b1, W2, b2, Wg, bg, last)
         eq_new = None
         if self.eq_out:
-            gvm = F.linear(inv, *frozen(self.gate))                               # (N, 2C) = [gv | gm]
             if C % 4 == 0:
                 eq_new = ops.eq_gate(V, Ms, gvm)                                  # (3,N,C), (6,N,C)
             else:
                 gv, gm = gvm.chunk(2, dim=-1)
                 eq_new = (V * gv[None], Ms * gm[None])
-        e, h_new = ops.readout_split(o, h)                                      # (N, 1), (N, C)
         return e, h_new, A, eq_new
 
 
@@ -492,18 +489,21 @@ class FACE(nn.Module):
         splines = [b.spline is not None for b in self.blocks]
         Y, rb, env, r = ops.edge_geometry(pos, graph, self.basis.freq, self.rc, with_rb=not all(splines),
                                           with_r=any(splines))
-        zidx = self.zmap[graph.Z]
-        # element-pair row of every edge and element of every atom, cached on the graph per element
-        # map (the entry holds the map tensor itself, so its key cannot be recycled by another model)
-        zkey = ("zp", id(self.zmap), len(self.E0))
-        ent = graph.cache.get(zkey)
-        if ent is None or ent[0] is not self.zmap or ent[1] != self.zmap._version:
-            zp = (zidx[graph.recv.long()] * len(self.E0) + zidx[graph.col.long()]).to(torch.int32)
-            ent = (self.zmap, self.zmap._version, zp, zidx.to(torch.int32))
-            graph.cache[zkey] = ent
-        zp, zidx32 = ent[2], ent[3]
-        h = F.embedding(zidx, self.embed.weight.detach())
-        e_at = self.E0[zidx].clone()
+        # per-atom element index, element-pair row of every edge, the embedding rows and the energy
+        # offsets: functions of the graph's species and of constants only, cached on the graph per
+        # model (the entry holds the tensors it depends on and their in-place versions, so it can
+        # be neither recycled by another model nor outlive a change of the weights)
+        w, E0 = self.embed.weight, self.E0
+        dep = (self.zmap, w, E0)
+        ver = tuple(t._version for t in dep)
+        akey = ("atoms", id(self))
+        ent = graph.cache.get(akey)
+        if ent is None or any(a is not b for a, b in zip(ent[0], dep)) or ent[1] != ver:
+            zidx = self.zmap[graph.Z]
+            zp = (zidx[graph.recv.long()] * len(E0) + zidx[graph.col.long()]).to(torch.int32)
+            ent = (dep, ver, (zidx, zidx.to(torch.int32), zp, F.embedding(zidx, w.detach()), E0[zidx]))
+            graph.cache[akey] = ent
+        zidx, zidx32, zp, h, e0 = ent[2]
         # table-cell edge order for large compiled tables: one sort per step, shared by the passes
         order = None
         big = [b.spline for b in self.blocks if b.spline is not None and ops.spline_wants_order(b.spline.T)]
@@ -511,14 +511,24 @@ class FACE(nn.Module):
             P, G = big[0].T.shape[:2]
             if all(s.T.shape[:2] == (P, G) and s.dr == big[0].dr for s in big):
                 order = ops.spline_order(r, zp, P, G, big[0].dr)
-        sets, eq = [], None
-        for blk in self.blocks:
-            e, h, A, eq = blk(h, rb, r, Y, env, zp, zidx, zidx32, self.avg_nb, sets, eq, graph, order)
+        # moment sets read only by the projections (every directional pass takes its tables from
+        # the previous pass's gated outputs): their gradients accumulate in place across passes
+        acc = {} if all(b.eq_in or not b.directional for b in self.blocks) else None
+        sets, eq, es = [], None, []
+        nb = len(self.blocks)
+        for t, blk in enumerate(self.blocks):
+            e, h, A, eq = blk(h, rb, r, Y, env, zp, zidx, zidx32, self.avg_nb, sets, eq, graph, order, acc,
+                              last=t == nb - 1)
             sets.append(A)
-            e_at = e_at + self.scale * e.squeeze(-1)
-        E = ops.StructureSum.apply(e_at, graph.struct_ptr, graph.batch, graph.nstr)
+            es.append(e)
+        E, e_at = ops.atom_energy(e0, self.scale, graph.struct_ptr, graph.batch, graph.nstr, es)
         out = {"energy": E, "atom_energy": e_at}
         if forces:
-            (grad,) = torch.autograd.grad(E.sum(), pos)
-            out["forces"] = -grad
+            # forces = -dE/dpos directly: the backward is seeded with -1 per structure
+            key = ("neg_ones", graph.nstr)
+            seed = graph.cache.get(key)
+            if seed is None or seed.device != E.device:
+                seed = torch.full((graph.nstr,), -1.0, device=E.device)
+                graph.cache[key] = seed
+            (out["forces"],) = torch.autograd.grad(E, pos, grad_outputs=seed)
         return out

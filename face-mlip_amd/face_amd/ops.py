@@ -304,27 +304,93 @@ def dir_transport(Vb, Mb, phi, Y, graph, Kd, transport):
     return DirTransport.apply(Vb, Mb, phi, Y, graph, Kd, transport)
 
 
-class ReadoutSplit(torch.autograd.Function):
-    """(o (N, 1 + C), h (N, C)) -> (e (N, 1) = o[:, :1], h + o[:, 1:]): the atom energy and the
-    residual update of face/model.py:336-339. Autograd of the two slices would zero-fill and copy
-    a full (N, 1 + C) gradient per slice and add them; here the backward is one concatenation."""
+class ReadoutMLP(torch.autograd.Function):
+    """The readout after the LayerNorm on the library GEMMs (face/model.py:331-339, the gate of
+    :286-287): z0 = [inv | h] W0^T + b0 (two accumulating GEMMs, no concatenated copy),
+    o = W2 silu(W1 silu(z0) + b1) + b2, e = o[:, :1], h_new = h + o[:, 1:], gvm = inv Wg^T + bg.
+    As one autograd node its backward accumulates where autograd would add: d inv takes the gate
+    term in the second GEMM's epilogue, d h = gh + dz0 W0[:, 9C:10C] in one GEMM. last (the final
+    pass, whose h_new nobody reads): only the energy row of the last layer is computed and its
+    input gradient is the outer product ge W2[0]. W0a / W0b are the inv / h column blocks of W0.
+    Weights receive no gradient."""
 
     @staticmethod
-    def forward(ctx, o, h):
-        ctx.shape = h.shape
-        return o[:, :1].clone(), torch.add(h, o[:, 1:])
+    def forward(ctx, inv, h, W0a, W0b, b0, W1, b1, W2, b2, Wg, bg, last):
+        z0 = torch.addmm(b0, inv, W0a.t())
+        z0.addmm_(h, W0b.t())
+        z1 = torch.addmm(b1, torch.nn.functional.silu(z0), W1.t())
+        a1 = torch.nn.functional.silu(z1)
+        if last:
+            e = torch.addmm(b2[:1], a1, W2[:1].t())                               # (N, 1)
+            h_new = None
+        else:
+            o = torch.addmm(b2, a1, W2.t())                                       # (N, 1 + C)
+            e = o[:, :1]
+            h_new = torch.add(h, o[:, 1:])
+        gvm = torch.addmm(bg, inv, Wg.t()) if Wg is not None else None
+        ctx.save_for_backward(z0, z1)
+        ctx.w = (W0a, W0b, W1, W2, Wg)
+        ctx.last = last
+        return e, h_new, gvm
 
     @staticmethod
-    def backward(ctx, ge, gh):
-        N, C = ctx.shape
-        like = gh if gh is not None else ge
-        ge = ge if ge is not None else like.new_zeros(N, 1)
-        gh = gh if gh is not None else like.new_zeros(N, C)
-        return torch.cat([ge, gh], 1), gh
+    def backward(ctx, ge, gh, ggvm):
+        z0, z1 = ctx.saved_tensors
+        W0a, W0b, W1, W2, Wg = ctx.w
+        N = z0.shape[0]
+        C = W0b.shape[1]
+        if ge is None:
+            ge = z0.new_zeros(N, 1)
+        if ctx.last:
+            da1 = ge * W2[:1]                                                     # (N, 2C)
+        else:
+            if gh is None:
+                gh = z0.new_zeros(N, C)
+            da1 = torch.cat([ge, gh], 1) @ W2
+        da0 = torch.ops.aten.silu_backward(da1, z1) @ W1
+        dz0 = torch.ops.aten.silu_backward(da0, z0)
+        dinv = dz0 @ W0a
+        if ggvm is not None and Wg is not None:
+            dinv.addmm_(ggvm, Wg)
+        dh = torch.addmm(gh, dz0, W0b) if (not ctx.last) else dz0 @ W0b
+        return dinv, dh, None, None, None, None, None, None, None, None, None, None
 
 
-def readout_split(o, h):
-    return ReadoutSplit.apply(o, h)
+def readout_mlp(inv, h, W0a, W0b, b0, W1, b1, W2, b2, Wg=None, bg=None, last=False):
+    """(e (N, 1), h_new (N, C) | None when last, gvm (N, 2C) | None); see ReadoutMLP."""
+    return ReadoutMLP.apply(inv, h, W0a, W0b, b0, W1, b1, W2, b2, Wg, bg, last)
+
+
+class AtomEnergy(torch.autograd.Function):
+    """Atom energies e_at = e0 + scale * sum_p e_p (N,) and their per-structure sums E (nstr,)
+    (face/model.py:689-690): one fused multiply-add per pass and one segment-sum launch (atoms of
+    a structure are contiguous); the backward gives every pass the same gradient scale * gE[batch].
+    e_p may be strided (N, 1) column views."""
+
+    @staticmethod
+    def forward(ctx, e0, scale, struct_ptr, batch, nstr, *es):
+        e_at = torch.addcmul(e0, scale, es[0].squeeze(-1))
+        for e in es[1:]:
+            e_at.addcmul_(scale, e.squeeze(-1))
+        E = torch.empty(nstr, 1, device=e_at.device)
+        call("face_segment_sum", ptr(e_at), 1, ptr(struct_ptr), nstr, 1, ptr(E), 1, _lib.stream_of(e_at))
+        ctx.save_for_backward(batch, scale)
+        ctx.n = len(es)
+        return E.view(nstr), e_at
+
+    @staticmethod
+    def backward(ctx, gE, g_at):
+        batch, scale = ctx.saved_tensors
+        g = gE[batch] if gE is not None else None
+        if g_at is not None:
+            g = g_at if g is None else g + g_at
+        ge = (g * scale).view(-1, 1)
+        return (None, None, None, None, None) + (ge,) * ctx.n
+
+
+def atom_energy(e0, scale, struct_ptr, batch, nstr, es):
+    """(E (nstr,), e_at (N,)); see AtomEnergy."""
+    return AtomEnergy.apply(e0, scale, struct_ptr, batch, nstr, *es)
 
 
 class Readout(torch.autograd.Function):
@@ -399,23 +465,6 @@ class Readout(torch.autograd.Function):
 def readout(feats, h, ln_w, ln_b, eps, w0, b0, w1, b1, w2p, b2p, wg=None, bg=None, wstack=None):
     """(e (N, 1), h_new (N, C), gvm (N, 2C) | empty); see Readout."""
     return Readout.apply(feats, h, ln_w, ln_b, eps, w0, b0, w1, b1, w2p, b2p, wg, bg, wstack)
-
-
-class StructureSum(torch.autograd.Function):
-    """Per-structure sum of per-atom values (atoms of a structure are contiguous)."""
-
-    @staticmethod
-    def forward(ctx, e_at, struct_ptr, batch, nstr):
-        e = e_at.contiguous().float().view(-1, 1)
-        out = torch.empty(nstr, 1, device=e.device)
-        call("face_segment_sum", ptr(e), 1, ptr(struct_ptr), nstr, 1, ptr(out), 1, _lib.stream_of(e))
-        ctx.save_for_backward(batch)
-        return out.view(nstr)
-
-    @staticmethod
-    def backward(ctx, g):
-        (batch,) = ctx.saved_tensors
-        return g[batch], None, None, None
 
 
 # ----------------------------------------------------------------------------- densities
@@ -945,7 +994,6 @@ class NodeFeatures(torch.autograd.Function):
         dev = y1.device
         ins = _pqs_views(y1, y2, y3, C)
         st = sum((_s3(t) for t in ins), [])
-        dy0 = torch.zeros_like(y0)
         dy1 = torch.empty_like(y1)
         dy2 = torch.empty_like(y2)
         dy3 = torch.empty_like(y3)
@@ -956,8 +1004,16 @@ class NodeFeatures(torch.autograd.Function):
         z3 = [0, 0, 0]
         if gfeats is not None:
             gfeats = gfeats.contiguous().float()
-            dy0[0, :, :C] = gfeats[:, :C]
             gI = gfeats[:, C:].view(N, 8, C).transpose(1, 2)
+        # P0 was copied into the readout row: its gradient is that row's first C columns, handed
+        # on as a strided view when y0 has exactly C channels (the projection backward reads rows
+        # at any stride)
+        if gfeats is not None and y0.shape[2] == C:
+            dy0 = gfeats[:, :C].unsqueeze(0)
+        else:
+            dy0 = torch.zeros_like(y0)
+            if gfeats is not None:
+                dy0[0, :, :C] = gfeats[:, :C]
         need_ab = eq and (ctx.needs_input_grad[4] or ctx.needs_input_grad[5])
         da = torch.empty(N, C, 4, device=dev) if need_ab else None
         db = torch.empty(N, C, 4, device=dev) if need_ab else None
@@ -1076,14 +1132,35 @@ def scaled_mix(s_tab, group, wm, wt, D1, D2, Af):
     return ScaledMix.apply(s_tab, group, wm, wt, D1, D2, *Af)
 
 
+def _row_view(t, n):
+    """(k, N, n) -> (k N, n) rows with unit column stride: a view where the strides allow one
+    (e.g. a column block of a wider row-major tensor), else a contiguous copy."""
+    if t.stride(-1) == 1 and t.stride(1) >= n and (t.shape[0] == 1 or t.stride(0) == t.shape[1] * t.stride(1)):
+        return t.as_strided((t.shape[0] * t.shape[1], n), (t.stride(1), 1))
+    return t.contiguous().view(-1, n)
+
+
+class SetGrad:
+    """The input gradient of one moment set read by several RankProj nodes (the set of pass p is
+    projected again by every later pass): the first backward to run writes it, the later ones
+    accumulate onto it in the GEMM epilogue (beta = 1) and hand autograd None, so no separate
+    accumulation add runs. Valid only when RankProj nodes are the set's only readers; reset once
+    all of them have run (a second backward through the same graph starts again)."""
+    __slots__ = ("readers", "arrived", "g")
+
+    def __init__(self):
+        self.readers, self.arrived, self.g = 0, 0, None
+
+
 class RankProj(torch.autograd.Function):
     """y_l = sum_s S_s,l W_l[:, s C:(s + 1) C]^T for the four ranks l over the moment sets s
     (face/model.py:537-544, the proj of the concatenated sets as a sum of per-set products):
     one launch per set, the sets after the first accumulating in the epilogue. The backward
-    gives each set's input gradient, again one launch per set. Weights receive no gradient."""
+    gives each set's input gradient, again one launch per set (accumulated across the nodes
+    that share a set through its SetGrad, when given). Weights receive no gradient."""
 
     @staticmethod
-    def forward(ctx, ws, n_sets, *S):
+    def forward(ctx, ws, n_sets, acc, *S):
         C = S[0].shape[-1]
         N = S[0].shape[1]
         dev = S[0].device
@@ -1092,7 +1169,19 @@ class RankProj(torch.autograd.Function):
         for s, S_s in enumerate(sets):
             rows_linear([(S_s[l].reshape(-1, C), ws[l][:, s * C:(s + 1) * C], ys[l].view(-1, ws[l].shape[0]), 0,
                           1.0 if s else 0.0) for l in range(4)], label="proj_fwd")
-        ctx.ws, ctx.n_sets, ctx.C = ws, n_sets, C
+        slots = None
+        if acc is not None:
+            # one SetGrad per set, keyed by its rank-0 tensor (the entry holds the tensor itself, so
+            # the key cannot be recycled while the dict lives)
+            slots = []
+            for S_s in sets:
+                ent = acc.get(id(S_s[0]))
+                if ent is None or ent[0] is not S_s[0]:
+                    ent = (S_s[0], SetGrad())
+                    acc[id(S_s[0])] = ent
+                ent[1].readers += 1
+                slots.append(ent[1])
+        ctx.ws, ctx.n_sets, ctx.C, ctx.slots = ws, n_sets, C, slots
         ctx.shapes = [t.shape for t in S]
         return tuple(ys)
 
@@ -1100,20 +1189,32 @@ class RankProj(torch.autograd.Function):
     def backward(ctx, *gy):
         C, ws = ctx.C, ctx.ws
         dev = ws[0].device
-        gy = [(g.contiguous() if g is not None else torch.zeros(sh[0], sh[1], w.shape[0], device=dev))
+        gy = [(_row_view(g, w.shape[0]) if g is not None else torch.zeros(sh[0] * sh[1], w.shape[0], device=dev))
               for g, w, sh in zip(gy, ws, ctx.shapes[:4])]
         grads = []
         for s in range(ctx.n_sets):
-            need = [ctx.needs_input_grad[2 + 4 * s + l] for l in range(4)]
-            d = [torch.empty(ctx.shapes[4 * s + l], device=dev) if need[l] else None for l in range(4)]
-            probs = [(gy[l].view(-1, ws[l].shape[0]), ws[l][:, s * C:(s + 1) * C], d[l].view(-1, C), 0, 0.0)
-                     for l in range(4) if need[l]]
+            need = [ctx.needs_input_grad[3 + 4 * s + l] for l in range(4)]
+            slot = ctx.slots[s] if ctx.slots is not None else None
+            if slot is not None and slot.g is not None:
+                d, beta, out = slot.g, 1.0, [None] * 4
+            else:
+                d = [torch.empty(ctx.shapes[4 * s + l], device=dev) if need[l] else None for l in range(4)]
+                beta, out = 0.0, d
+                if slot is not None:
+                    slot.g = d
+            probs = [(gy[l], ws[l][:, s * C:(s + 1) * C], d[l].view(-1, C), 0, beta) for l in range(4) if need[l]]
             if probs:
                 rows_linear(probs, w_kn=True, label="proj_bwd")
-            grads += d
-        return (None, None, *grads)
+            if slot is not None:
+                slot.arrived += 1
+                if slot.arrived == slot.readers:
+                    slot.g, slot.arrived = None, 0
+            grads += out
+        return (None, None, None, *grads)
 
 
-def rank_proj(ws, sets):
-    """ws: 4 frozen proj weights (n_l, n_sets C); sets: list of 4-tuples of (k_l, N, C) moments."""
-    return RankProj.apply(ws, len(sets), *[t for S in sets for t in S])
+def rank_proj(ws, sets, acc=None):
+    """ws: 4 frozen proj weights (n_l, n_sets C); sets: list of 4-tuples of (k_l, N, C) moments;
+    acc: a dict shared by the rank_proj calls of one forward whose sets nothing else reads (their
+    gradients then accumulate in place, see SetGrad), or None."""
+    return RankProj.apply(ws, len(sets), acc, *[t for S in sets for t in S])
