@@ -24,7 +24,11 @@
 // registers held, the compiler could not keep them in flight together.)
 #include "common.h"
 
+#include <algorithm>
 #include <cstdlib>
+#include <map>
+#include <mutex>
+#include <vector>
 
 namespace face {
 
@@ -567,6 +571,231 @@ static int fill_prob(const face_lin_problem& s, int w_kn, bool scaled, const flo
     return 0;
 }
 
+// Everything a sliced launch needs but its shape (waves per workgroup, column slices).
+struct RowsCtx {
+    GemmArgs A;                                  // problems filled, tiling not yet
+    const face_lin_problem* probs;
+    int n_probs, K, n_widest, ns_max, max_lds, n_cu, n_groups;
+    bool w_kn, x_scale, y_scale, any_bias, any_ext;
+    hipStream_t st;
+    // LDS floats of the side tables for a slice of ns columns (GemmSide)
+    int side_floats(int ns) const {
+        return (y_scale ? n_groups * ns : 0) + (x_scale ? n_groups * K : 0) + (any_bias ? ns : 0);
+    }
+};
+
+// 16-wave workgroups (4 waves per SIMD hide the row loads) unless that leaves CUs idle; else 8
+// (the staged weight slice serves twice the rows of 4 waves), except for several column slices
+// of a (K, n) weight, measured better with 4.
+static int default_nw(const RowsCtx& c, int NS) {
+    auto wgs_for = [&](int nw) {
+        int64_t t = 0;
+        for (int i = 0; i < c.n_probs; ++i) t += (c.probs[i].m + 16 * kGemmBB * nw - 1) / (16 * kGemmBB * nw);
+        return t;
+    };
+    bool kn_slices = false;
+    for (int i = 0; i < c.n_probs; ++i)
+        if (c.w_kn && c.probs[i].m > 0 && c.probs[i].n > NS) kn_slices = true;
+    return wgs_for(16) >= c.n_cu ? 16 : (!kn_slices || wgs_for(8) >= c.n_cu ? 8 : 4);
+}
+
+// One launch of rows_gemm_kernel with NW waves per workgroup and the widest problem split into
+// n_sl column slices (NS = its width rounded up to 16 columns); FACE_ERR_UNSUPPORTED, before
+// anything is launched, if that shape does not fit.
+static int launch_rows(const RowsCtx& c, int NW, int n_sl) {
+    if (n_sl < 1 || (NW != 4 && NW != 8 && NW != 16)) return FACE_ERR_UNSUPPORTED;
+    const int NS = ((c.n_widest + n_sl - 1) / n_sl + 15) / 16 * 16;
+    if (NS > c.ns_max || NS > 160) return FACE_ERR_UNSUPPORTED;
+    GemmArgs A = c.A;
+    int max_n = 16;
+    int64_t blocks = 0, total_cost = 0;
+    for (int i = 0; i < c.n_probs; ++i) {
+        const face_lin_problem& s = c.probs[i];
+        GemmProb& p = A.p[i];
+        p.tiles = (int)((s.m + 16 * kGemmBB * NW - 1) / (16 * kGemmBB * NW));
+        p.slices = (s.n + NS - 1) / NS;
+        p.first_block = blocks;
+        p.cost0 = total_cost;
+        p.cost = s.k + 64;
+        blocks += (int64_t)p.tiles * p.slices;
+        total_cost += (int64_t)p.tiles * p.slices * p.cost;
+        if (s.n > max_n) max_n = s.n;
+    }
+    for (int i = c.n_probs; i < kGemmMaxProbs; ++i) A.p[i].first_block = A.p[i].cost0 = INT64_MAX;
+    if (blocks == 0) return 0;
+    A.NS = NS;
+    A.items = blocks;
+    A.total_cost = total_cost;
+    const int nb = (max_n < NS ? max_n : NS) / 16;
+    A.side_off = nb * 16 * (c.K + 4);
+    const size_t lds = ((size_t)A.side_off + c.side_floats(nb * 16)) * sizeof(float);
+    // persistent grid: as many workgroups as fit on the device at once, each on a contiguous run
+    // of the work items
+    int64_t wg_cu = (int64_t)c.max_lds / (int64_t)lds;
+    if (wg_cu > 32 / NW) wg_cu = 32 / NW;
+    if (wg_cu < 1) wg_cu = 1;
+    // Persistent runs when the work outnumbers the resident workgroups and no weight slice has to
+    // be staged again per row tile: single-slice problems, or (n, K) weights whose slices stage
+    // from contiguous rows. Otherwise one work item per workgroup, tile by tile, so the slices of
+    // a row tile share its rows in cache (measured better for multi-slice (K, n) weights of
+    // large K and for launches that fit the device at once).
+    bool multi_slice = false;
+    for (int i = 0; i < c.n_probs; ++i)
+        if (A.p[i].slices > 1 && A.p[i].tiles > 0) multi_slice = true;
+    const bool persist = blocks > c.n_cu * wg_cu && (!c.w_kn || !multi_slice);
+    if (persist) {
+        // persistent runs count 32-row wave tiles as items (the cost split can then end a run
+        // inside a workgroup tile; the run's waves share its tiles)
+        blocks = total_cost = 0;
+        for (int i = 0; i < c.n_probs; ++i) {
+            GemmProb& p = A.p[i];
+            p.tiles = (int)((c.probs[i].m + 16 * kGemmBB - 1) / (16 * kGemmBB));
+            p.first_block = blocks;
+            p.cost0 = total_cost;
+            blocks += (int64_t)p.tiles * p.slices;
+            total_cost += (int64_t)p.tiles * p.slices * p.cost;
+        }
+        A.items = blocks;
+        A.total_cost = total_cost;
+    }
+    const int64_t grid = persist ? c.n_cu * wg_cu : blocks;
+    const hipStream_t st = c.st;
+#define FACE_GEMM_P(NB_, P_, X_)                                                                            \
+    do {                                                                                                    \
+        auto kern = NW == 16 ? rows_gemm_kernel<NB_, 16, P_, X_>                                            \
+                             : (NW == 8 ? rows_gemm_kernel<NB_, 8, P_, X_> : rows_gemm_kernel<NB_, 4, P_, X_>); \
+        if (lds > 65536 &&                                                                                  \
+            hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != \
+                hipSuccess)                                                                                 \
+            return FACE_ERR_UNSUPPORTED;                                                                    \
+        hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NW * kWave), lds, st, A);                      \
+    } while (0)
+    const int xm = c.x_scale ? 1 : (c.any_ext ? 2 : 0);
+#define FACE_GEMM(NB_)                     \
+    do {                                   \
+        if (persist && xm == 1)            \
+            FACE_GEMM_P(NB_, true, 1);     \
+        else if (persist && xm == 2)       \
+            FACE_GEMM_P(NB_, true, 2);     \
+        else if (persist)                  \
+            FACE_GEMM_P(NB_, true, 0);     \
+        else if (xm == 1)                  \
+            FACE_GEMM_P(NB_, false, 1);    \
+        else if (xm == 2)                  \
+            FACE_GEMM_P(NB_, false, 2);    \
+        else                               \
+            FACE_GEMM_P(NB_, false, 0);    \
+    } while (0)
+    switch (nb) {
+        case 1: FACE_GEMM(1); break;
+        case 2: FACE_GEMM(2); break;
+        case 3: FACE_GEMM(3); break;
+        case 4: FACE_GEMM(4); break;
+        case 5: FACE_GEMM(5); break;
+        case 6: FACE_GEMM(6); break;
+        case 7: FACE_GEMM(7); break;
+        case 8: FACE_GEMM(8); break;
+        case 9: FACE_GEMM(9); break;
+        default: FACE_GEMM(10); break;
+    }
+#undef FACE_GEMM
+#undef FACE_GEMM_P
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+// Launch shapes picked per problem signature by timing. The shape that the rules above pick is
+// near the best on most launches, but measured 20-30 % off on some small ones (e.g. 17,280 rows
+// of 96 -> 512 columns with an input scale: 32 against 26 us; 26,880 rows of 512 -> 96: 48 against
+// 33 us), and the best shape moves irregularly with the row count. So the first call of a
+// signature (device, problem shapes, transposition, scales, kernel form) times every shape of
+// 4, 8 or 16 waves and distinct slice widths (three launches each, then the three fastest and the
+// rule's own five times more) and keeps the fastest unless it beats the rule's by less than 2 %.
+// Every shape computes each output with the same instructions in the same order, so results are
+// bitwise the same whatever the shape. Timing needs launches that can run again with the same
+// result: only calls whose problems all have beta = 0 (or read beta y0 from another tensor), on a
+// stream that is not being captured, are timed; others use a shape timed earlier for the same
+// signature, else the rules. FACE_GEMM_TUNE=0 in the environment keeps the rules.
+struct ShapePlan {
+    int nw, n_sl;
+};
+static std::mutex g_plan_mu;
+static std::map<std::vector<int64_t>, ShapePlan> g_plans;
+
+static void pick_shape(const RowsCtx& c, int& NW, int& n_sl) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return;
+    std::vector<int64_t> key = {dev, c.n_probs, c.w_kn, c.x_scale, c.y_scale, c.n_groups, c.any_ext, c.any_bias};
+    for (int i = 0; i < c.n_probs; ++i) {
+        key.push_back(c.probs[i].m);
+        key.push_back(c.probs[i].n);
+        key.push_back(c.probs[i].k);
+    }
+    {
+        std::lock_guard<std::mutex> lk(g_plan_mu);
+        auto it = g_plans.find(key);
+        if (it != g_plans.end()) {
+            NW = it->second.nw, n_sl = it->second.n_sl;
+            return;
+        }
+    }
+    const char* env = getenv("FACE_GEMM_TUNE");
+    if (env && env[0] == '0') return;
+    for (int i = 0; i < c.n_probs; ++i) {
+        const face_lin_problem& s = c.probs[i];
+        if (s.beta != 0.f && (!s.y0 || s.y0 == s.y)) return;          // accumulating: not re-runnable
+    }
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(c.st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return;
+    std::vector<ShapePlan> cand = {{NW, n_sl}};
+    for (int nw : {16, 8, 4})
+        for (int ns = 16; ns <= c.ns_max && ns <= 160; ns += 16) {
+            const int k = (c.n_widest + ns - 1) / ns;
+            if (k > 32) continue;
+            bool seen = false;
+            for (const ShapePlan& p : cand) seen = seen || (p.nw == nw && p.n_sl == k);
+            if (!seen) cand.push_back({nw, k});
+        }
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
+        if (e0) hipEventDestroy(e0);
+        return;
+    }
+    auto time_it = [&](const ShapePlan& p, int reps) -> float {   // us per launch, < 0 if it does not run
+        if (launch_rows(c, p.nw, p.n_sl) != 0) return -1.f;
+        if (hipEventRecord(e0, c.st) != hipSuccess) return -1.f;
+        for (int r = 0; r < reps; ++r)
+            if (launch_rows(c, p.nw, p.n_sl) != 0) return -1.f;
+        float ms = 0.f;
+        if (hipEventRecord(e1, c.st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
+            hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
+            return -1.f;
+        return 1000.f * ms / reps;
+    };
+    std::vector<std::pair<float, int>> t1;
+    for (int i = 0; i < (int)cand.size(); ++i) {
+        const float t = time_it(cand[i], 3);
+        if (t >= 0.f) t1.push_back({t, i});
+    }
+    ShapePlan best = cand[0];
+    if (!t1.empty()) {
+        std::sort(t1.begin(), t1.end());
+        const float t_rule = time_it(cand[0], 5);
+        float t_best = t_rule;
+        for (int r = 0; r < 3 && r < (int)t1.size(); ++r) {
+            if (t1[r].second == 0) continue;
+            const float t = time_it(cand[t1[r].second], 5);
+            if (t >= 0.f && (t_best < 0.f || t < t_best)) t_best = t, best = cand[t1[r].second];
+        }
+        if (t_rule >= 0.f && !(t_best < 0.98f * t_rule)) best = cand[0];
+    }
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    NW = best.nw, n_sl = best.n_sl;
+    std::lock_guard<std::mutex> lk(g_plan_mu);
+    g_plans[key] = best;
+}
+
 extern "C" int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, int32_t w_kn, const float* x_scale,
                                 const float* y_scale, int32_t ld_scale, int32_t n_groups, const int32_t* group,
                                 int64_t period, void* stream) {
@@ -663,113 +892,13 @@ extern "C" int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, 
         return 0;
     }
     if (ns_max < 16) return FACE_ERR_UNSUPPORTED;
-    // 16-wave workgroups (4 waves per SIMD hide the row loads) unless that leaves CUs idle; else 8
-    // (the staged weight slice serves twice the rows of 4 waves), except for several column
-    // slices of a (K, n) weight, measured better with 4
-    auto wgs_for = [&](int nw) {
-        int64_t t = 0;
-        for (int i = 0; i < n_probs; ++i) t += (probs[i].m + 16 * kGemmBB * nw - 1) / (16 * kGemmBB * nw);
-        return t;
-    };
-    const int n_cu = device_cu_count();
-    bool kn_slices = false;
-    for (int i = 0; i < n_probs; ++i)
-        if (w_kn && probs[i].m > 0 && probs[i].n > NS) kn_slices = true;
-    const int NW = wgs_for(16) >= n_cu ? 16 : (!kn_slices || wgs_for(8) >= n_cu ? 8 : 4);
-    int max_n = 16;
-    int64_t blocks = 0, total_cost = 0;
-    for (int i = 0; i < n_probs; ++i) {
-        const face_lin_problem& s = probs[i];
-        GemmProb& p = A.p[i];
-        p.tiles = (int)((s.m + 16 * kGemmBB * NW - 1) / (16 * kGemmBB * NW));
-        p.slices = (s.n + NS - 1) / NS;
-        p.first_block = blocks;
-        p.cost0 = total_cost;
-        p.cost = s.k + 64;
-        blocks += (int64_t)p.tiles * p.slices;
-        total_cost += (int64_t)p.tiles * p.slices * p.cost;
-        if (s.n > max_n) max_n = s.n;
-    }
-    for (int i = n_probs; i < kGemmMaxProbs; ++i) A.p[i].first_block = A.p[i].cost0 = INT64_MAX;
-    if (blocks == 0) return 0;
-    A.NS = NS;
-    A.items = blocks;
-    A.total_cost = total_cost;
-    const int nb = (max_n < NS ? max_n : NS) / 16;
-    A.side_off = nb * 16 * (K + 4);
-    const size_t lds = ((size_t)A.side_off + side_floats(nb * 16)) * sizeof(float);
-    // persistent grid: as many workgroups as fit on the device at once, each on a contiguous run
-    // of the work items
-    int64_t wg_cu = (int64_t)max_lds / (int64_t)lds;
-    if (wg_cu > 32 / NW) wg_cu = 32 / NW;
-    if (wg_cu < 1) wg_cu = 1;
-    // Persistent runs when the work outnumbers the resident workgroups and no weight slice has to
-    // be staged again per row tile: single-slice problems, or (n, K) weights whose slices stage
-    // from contiguous rows. Otherwise one work item per workgroup, tile by tile, so the slices of
-    // a row tile share its rows in cache (measured better for multi-slice (K, n) weights of
-    // large K and for launches that fit the device at once).
-    bool multi_slice = false;
-    for (int i = 0; i < n_probs; ++i)
-        if (A.p[i].slices > 1 && A.p[i].tiles > 0) multi_slice = true;
-    const bool persist = blocks > n_cu * wg_cu && (!w_kn || !multi_slice);
-    if (persist) {
-        // persistent runs count 32-row wave tiles as items (the cost split can then end a run
-        // inside a workgroup tile; the run's waves share its tiles)
-        blocks = total_cost = 0;
-        for (int i = 0; i < n_probs; ++i) {
-            GemmProb& p = A.p[i];
-            p.tiles = (int)((probs[i].m + 16 * kGemmBB - 1) / (16 * kGemmBB));
-            p.first_block = blocks;
-            p.cost0 = total_cost;
-            blocks += (int64_t)p.tiles * p.slices;
-            total_cost += (int64_t)p.tiles * p.slices * p.cost;
-        }
-        A.items = blocks;
-        A.total_cost = total_cost;
-    }
-    const int64_t grid = persist ? n_cu * wg_cu : blocks;
-    const hipStream_t st = (hipStream_t)stream;
-#define FACE_GEMM_P(NB_, P_, X_)                                                                            \
-    do {                                                                                                    \
-        auto kern = NW == 16 ? rows_gemm_kernel<NB_, 16, P_, X_>                                            \
-                             : (NW == 8 ? rows_gemm_kernel<NB_, 8, P_, X_> : rows_gemm_kernel<NB_, 4, P_, X_>); \
-        if (lds > 65536 &&                                                                                  \
-            hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != \
-                hipSuccess)                                                                                 \
-            return FACE_ERR_UNSUPPORTED;                                                                    \
-        hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(NW * kWave), lds, st, A);                      \
-    } while (0)
+    RowsCtx c;
+    c.A = A, c.probs = probs, c.n_probs = n_probs, c.K = K, c.n_widest = n_widest, c.ns_max = ns_max;
+    c.max_lds = max_lds, c.n_cu = device_cu_count(), c.w_kn = w_kn != 0, c.x_scale = x_scale != nullptr;
+    c.y_scale = y_scale != nullptr, c.any_bias = any_bias, c.any_ext = any_ext, c.n_groups = n_groups;
+    c.st = (hipStream_t)stream;
     if (x_scale && any_ext) return FACE_ERR_UNSUPPORTED;                 // x scale with split / op / y0
-    const int xm = x_scale ? 1 : (any_ext ? 2 : 0);
-#define FACE_GEMM(NB_)                     \
-    do {                                   \
-        if (persist && xm == 1)            \
-            FACE_GEMM_P(NB_, true, 1);     \
-        else if (persist && xm == 2)       \
-            FACE_GEMM_P(NB_, true, 2);     \
-        else if (persist)                  \
-            FACE_GEMM_P(NB_, true, 0);     \
-        else if (xm == 1)                  \
-            FACE_GEMM_P(NB_, false, 1);    \
-        else if (xm == 2)                  \
-            FACE_GEMM_P(NB_, false, 2);    \
-        else                               \
-            FACE_GEMM_P(NB_, false, 0);    \
-    } while (0)
-    switch (nb) {
-        case 1: FACE_GEMM(1); break;
-        case 2: FACE_GEMM(2); break;
-        case 3: FACE_GEMM(3); break;
-        case 4: FACE_GEMM(4); break;
-        case 5: FACE_GEMM(5); break;
-        case 6: FACE_GEMM(6); break;
-        case 7: FACE_GEMM(7); break;
-        case 8: FACE_GEMM(8); break;
-        case 9: FACE_GEMM(9); break;
-        default: FACE_GEMM(10); break;
-    }
-#undef FACE_GEMM
-#undef FACE_GEMM_P
-    FACE_LAUNCH_CHECK();
-    return 0;
+    int NW = default_nw(c, NS), nsl = n_sl;
+    pick_shape(c, NW, nsl);
+    return launch_rows(c, NW, nsl);
 }

@@ -723,6 +723,39 @@ def test_rows_linear_matches_torch(case, kc, monkeypatch):
     assert max(errs) < 1e-5, errs
 
 
+def test_rows_linear_launch_shapes_give_bitwise_equal_rows(monkeypatch):
+    """face_rows_linear times launch shapes (waves per workgroup, column slices) on the first call of
+    a problem signature and keeps the fastest. Every shape must give the same bits: the 864-atom
+    factor mix backward (17,280 rows of 96 -> 512 columns, (k, n) weight, input scale; the shape
+    the timing changes there) against its first 2,000 rows as a separate call (another signature,
+    timed again) and against 17,279 rows with the timing off (the rules' shape), plus torch fp64."""
+    from face_amd import ops
+    say("rows_linear launch shapes")
+    torch.manual_seed(11)
+    N, C, BK = 864, 96, 512
+    tab = torch.rand(1, 4 * C, device=DEV) + 0.5
+    grp = torch.zeros(N, device=DEV, dtype=torch.int32)
+    xs = [torch.randn(k * N, C, device=DEV) for k in (1, 3, 6, 10)]
+    ws = [torch.randn(C, BK, device=DEV) / C ** 0.5 for _ in range(4)]
+
+    def run(rows):
+        ys = [torch.empty(min(rows, x.shape[0]), BK, device=DEV) for x in xs]
+        ops.rows_linear([(x[:y.shape[0]], w, y, l * C, 0.0) for l, (x, w, y) in enumerate(zip(xs, ws, ys))],
+                        w_kn=True, xs=tab, group=grp, period=N)
+        torch.cuda.synchronize()
+        return ys
+
+    full = run(10 * N)                                   # timed shapes
+    part = run(2000)                                     # another signature, timed separately
+    monkeypatch.setenv("FACE_GEMM_TUNE", "0")
+    rule = run(10 * N - 1)                               # the rules' shape
+    for l, (x, w) in enumerate(zip(xs, ws)):
+        ref = (x.double() * tab.double()[0, l * C:(l + 1) * C]) @ w.double()
+        assert (full[l].double() - ref).abs().max() <= 1e-5 * ref.abs().max()
+        assert torch.equal(part[l], full[l][:part[l].shape[0]])
+        assert torch.equal(rule[l], full[l][:rule[l].shape[0]])
+
+
 @pytest.mark.parametrize("kc", [None, "1"])
 @pytest.mark.parametrize("w_kn", [False, True])
 def test_rows_linear_split_input_transforms_and_initial_sum(w_kn, kc, monkeypatch):
