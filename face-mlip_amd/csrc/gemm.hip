@@ -758,7 +758,7 @@ static void pick_shape(const RowsCtx& c, int& NW, int& n_sl) {
         }
     hipEvent_t e0 = nullptr, e1 = nullptr;
     if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
-        if (e0) hipEventDestroy(e0);
+        if (e0) (void)hipEventDestroy(e0);
         return;
     }
     auto time_it = [&](const ShapePlan& p, int reps) -> float {   // us per launch, < 0 if it does not run
@@ -789,8 +789,8 @@ static void pick_shape(const RowsCtx& c, int& NW, int& n_sl) {
         }
         if (t_rule >= 0.f && !(t_best < 0.98f * t_rule)) best = cand[0];
     }
-    hipEventDestroy(e0);
-    hipEventDestroy(e1);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
     NW = best.nw, n_sl = best.n_sl;
     std::lock_guard<std::mutex> lk(g_plan_mu);
     g_plans[key] = best;
