@@ -134,21 +134,33 @@ __global__ __launch_bounds__(kDfWaves * kWave) void density_fwd_mfma_kernel(
         for (int c = 0; c < KB; ++c) acc[xx][c] = z4;
     int64_t a, bnd;
     row_range(row_ptr, n, M, a, bnd);
-    for (int64_t e0 = a; e0 < bnd; e0 += 16) {
+    // tile rows (phi at basis j, msg channels, Y of the wave's monomials) of edges e0 + 4q + r,
+    // clamped into the row (phi zero past its end). K <= 32: the next tile's rows load while this
+    // one's MFMAs run (864-atom FCC 15.0 -> 14.1 us, 2,000 atoms of 70 neighbours 51 -> 49 us);
+    // at K = 64 the second set of rows costs occupancy (184 registers) and the loads stay in order
+    // (833 against 855 us on a 20,000-atom liquid).
+    constexpr bool PF = KB <= 2;
+    auto load_tile = [&](int64_t e0, float (&phT)[4], float (&yv)[NXW][4], float (&mb)[KB][4]) {
         const int ne = (int)min((int64_t)16, bnd - e0);
-        float phT[4], yv[NXW][4], mb[KB][4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int t = 4 * q + r;
-            const int64_t e = e0 + min(t, ne - 1);       // clamped: loads stay in the row
+            const int64_t e = e0 + min(t, ne - 1);
             const float p = phi[e * ld_phi + j];
-            phT[r] = t < ne ? p : 0.f;                   // zero past the row end
+            phT[r] = t < ne ? p : 0.f;
             const int64_t row = msg_row ? (int64_t)msg_row[e] : e;
 #pragma unroll
             for (int c = 0; c < KB; ++c) mb[c][r] = msg[row * ld_msg + 16 * c + j];
 #pragma unroll
             for (int xx = 0; xx < NXW; ++xx) yv[xx][r] = Y[e * ld_Y + x0 + xx];
         }
+    };
+    float phT[4], yv[NXW][4], mb[KB][4];
+    if (PF && a < bnd) load_tile(a, phT, yv, mb);
+    for (int64_t e0 = a; e0 < bnd; e0 += 16) {
+        if (!PF) load_tile(e0, phT, yv, mb);
+        float phN[4], yN[NXW][4], mN[KB][4];
+        if (PF && e0 + 16 < bnd) load_tile(e0 + 16, phN, yN, mN);
 #pragma unroll
         for (int xx = 0; xx < NXW; ++xx)
 #pragma unroll
@@ -157,6 +169,16 @@ __global__ __launch_bounds__(kDfWaves * kWave) void density_fwd_mfma_kernel(
 #pragma unroll
                 for (int c = 0; c < KB; ++c) acc[xx][c] = mfma_16x16x4(u, mb[c][r], acc[xx][c]);
             }
+        if (PF && e0 + 16 < bnd) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                phT[r] = phN[r];
+#pragma unroll
+                for (int c = 0; c < KB; ++c) mb[c][r] = mN[c][r];
+#pragma unroll
+                for (int xx = 0; xx < NXW; ++xx) yv[xx][r] = yN[xx][r];
+            }
+        }
     }
 #pragma unroll
     for (int xx = 0; xx < NXW; ++xx) {
@@ -396,6 +418,148 @@ __global__ __launch_bounds__((WPA > 1 ? WPA : kDbWaves) * kWave) void density_bw
             }
         }
         if (WPA == 1 || wv == 0) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = 4 * q + r;
+                if (t < ne) {
+                    const int64_t e = e0 + t;
+                    if (dphi) dphi[e * ld_dphi + j] = dph[r];
+                    if (dmsg) {
+#pragma unroll
+                        for (int c = 0; c < KB; ++c) dmsg[e * ld_dmsg + 16 * c + j] = dm[c][r];
+                    }
+                }
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------ factor backward, small systems
+// One atom per workgroup of 4 waves, wave w on monomials 5w .. 5w + 4 (the per-monomial MFMA
+// chains of density_bwd_mfma_kernel), for K <= 32. The wave's G operands (5 monomials x 16 b x K,
+// both operand layouts: 80 registers at K = 32) are read once per atom, while the first tile's
+// rows load, and stay in registers over the atom's tiles; per 16-edge tile the Y tile, the message
+// rows and phi are issued together before the workgroup barrier. A tile then costs one memory
+// latency instead of one per pair of monomials (the G reads of density_bwd_mfma_kernel). The
+// four waves' dphi / dmsg partials are summed by wave 0 through LDS. At K = 32 the kernel holds
+// ~230 registers (two waves per SIMD); capped at four waves per SIMD it spills 312 bytes and runs
+// 1.8x slower. Measured against density_bwd_mfma_kernel<2, 4>: 35.5 -> 27.3 us (864-atom FCC),
+// 37.6 -> 32.3 us (1,344 atoms), 153 -> 113 us (2,000 atoms of 70 neighbours), same bits.
+constexpr int kDsWaves = 4;
+
+template <int KB>
+__global__ __launch_bounds__(kDsWaves * kWave) void density_bwd_split_kernel(
+    const float* __restrict__ phi, int ld_phi, const float* __restrict__ msg, int ld_msg,
+    const int32_t* __restrict__ msg_row, const float* __restrict__ Y, int ld_Y, const int32_t* __restrict__ row_ptr,
+    int M, RankIn G, float* __restrict__ dphi, int ld_dphi, float* __restrict__ dmsg, int ld_dmsg,
+    float* __restrict__ dY, int ld_dY) {
+    constexpr int K = 16 * KB, NXW = 20 / kDsWaves;
+    __shared__ float sY[16 * kDbYS];
+    __shared__ float sP[kDsWaves][16 * (16 + K)];        // dphi | dmsg partials
+    const int tid = threadIdx.x, lane = tid & (kWave - 1), j = lane & 15, q = lane >> 4;
+    const int wv = __builtin_amdgcn_readfirstlane(tid / kWave);
+    const int64_t n = blockIdx.x;
+    const int x0 = wv * NXW;
+    const v4f z4 = {0.f, 0.f, 0.f, 0.f};
+    // G_x operands: gv = G[x][b = j][16c + 4q .. + 3] (S chain), gs = G[x][b = 4q + r][16c + j] (dmsg chain)
+    v4f gv[NXW][KB];
+    float gs[NXW][KB][4];
+#pragma unroll
+    for (int xx = 0; xx < NXW; ++xx) {
+        const float* gx = G.at(n, x0 + xx);
+#pragma unroll
+        for (int c = 0; c < KB; ++c) {
+            gv[xx][c] = ld4(gx + j * K + 16 * c + 4 * q);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) gs[xx][c][r] = gx[(4 * q + r) * K + 16 * c + j];
+        }
+    }
+    int64_t a, bnd;
+    row_range(row_ptr, n, M, a, bnd);
+    for (int64_t e0 = a; e0 < bnd; e0 += 16) {
+        const int ne = (int)min((int64_t)16, bnd - e0);
+        // this tile's loads, all issued before the barrier: the Y tile (16 x 20, zero past the row
+        // end; 320 values over 256 threads), the message row and phi of edge e0 + j, phi of edges
+        // e0 + 4q + r at basis j
+        float yl[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int v = u * kDsWaves * kWave + tid, t = v / 20, x = v - t * 20;
+            yl[u] = (v < 320 && t < ne) ? Y[(e0 + t) * ld_Y + x] : 0.f;
+        }
+        const bool oki = j < ne;
+        const int64_t ei = e0 + min(j, ne - 1);
+        const int64_t rowi = msg_row ? (int64_t)msg_row[ei] : ei;
+        v4f mA[KB];
+#pragma unroll
+        for (int c = 0; c < KB; ++c) mA[c] = oki ? ld4(msg + rowi * ld_msg + 16 * c + 4 * q) : z4;
+        const v4f ph4 = oki ? ld4(phi + ei * ld_phi + 4 * q) : z4;
+        float phT[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) phT[r] = phi[(e0 + min(4 * q + r, ne - 1)) * ld_phi + j];
+        __syncthreads();                                 // previous tile's Y and partials consumed
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int v = u * kDsWaves * kWave + tid, t = v / 20, x = v - t * 20;
+            if (v < 320) sY[t * kDbYS + x] = yl[u];
+        }
+        __syncthreads();
+        v4f dph = z4, dm[KB];
+#pragma unroll
+        for (int c = 0; c < KB; ++c) dm[c] = z4;
+        float dyk[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dyk[r] = 0.f;
+#pragma unroll
+        for (int xx = 0; xx < NXW; ++xx) {
+            const int x = x0 + xx;
+            v4f sv = z4;
+#pragma unroll
+            for (int c = 0; c < KB; ++c)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) sv = mfma_16x16x4(mA[c][r], gv[xx][c][r], sv);
+            const float yi = sY[j * kDbYS + x];
+#pragma unroll
+            for (int c = 0; c < KB; ++c)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) dm[c] = mfma_16x16x4(yi * ph4[r], gs[xx][c][r], dm[c]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                dph[r] = fmaf(sv[r], sY[(4 * q + r) * kDbYS + x], dph[r]);
+                float v = sv[r] * phT[r];
+                v += __shfl_xor(v, 1, kWave);
+                v += __shfl_xor(v, 2, kWave);
+                v += __shfl_xor(v, 4, kWave);
+                v += __shfl_xor(v, 8, kWave);
+                if (j == xx) dyk[r] = v;
+            }
+        }
+        // dY of this wave's monomials: lane j < 5 holds monomial x0 + j of edge e0 + 4q + r
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = 4 * q + r;
+            if (dY && t < ne && j < NXW) dY[(e0 + t) * ld_dY + x0 + j] = dyk[r];
+        }
+        // partials of the four waves summed by wave 0
+        float* mine = sP[wv];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            mine[(4 * q + r) * 16 + j] = dph[r];
+#pragma unroll
+            for (int c = 0; c < KB; ++c) mine[256 + (4 * q + r) * K + 16 * c + j] = dm[c][r];
+        }
+        __syncthreads();
+        if (wv == 0) {
+#pragma unroll
+            for (int w = 1; w < kDsWaves; ++w) {
+                const float* o = sP[w];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    dph[r] += o[(4 * q + r) * 16 + j];
+#pragma unroll
+                    for (int c = 0; c < KB; ++c) dm[c][r] += o[256 + (4 * q + r) * K + 16 * c + j];
+                }
+            }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int t = 4 * q + r;
@@ -1619,7 +1783,11 @@ extern "C" int face_density_bwd(const float* phi, int32_t ld_phi, const float* m
         const dim3 block(split ? 4 * kWave : kDbWaves * kWave);
 #define FACE_DBM(KB_)                                                                                           \
     do {                                                                                                        \
-        if (split)                                                                                              \
+        if (split && KB_ <= 2)                                                                                  \
+            hipLaunchKernelGGL((density_bwd_split_kernel<(KB_ <= 2 ? KB_ : 2)>), grid, block, 0, st, phi, ld_phi, \
+                               msg, ld_msg, msg_row, Y, ld_Y, row_ptr, M, G, dphi, ld_dphi, dmsg, ld_dmsg, dY,   \
+                               ld_dY);                                                                          \
+        else if (split)                                                                                         \
             hipLaunchKernelGGL((density_bwd_mfma_kernel<KB_, 4>), grid, block, 0, st, phi, ld_phi, msg, ld_msg,  \
                                msg_row, Y, ld_Y, row_ptr, N, M, G, dphi, ld_dphi, dmsg, ld_dmsg, dY, ld_dY);     \
         else                                                                                                    \
