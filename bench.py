@@ -67,7 +67,8 @@ KERNEL_FAMILY = {
 # kernel family -> kernel functions of libface_hip.so it stands for (rocprofv3 names, namespace face)
 FAMILY_KERNELS = {
     "density_fwd": ["density_fwd_mfma_kernel", "density_fwd_kernel"],
-    "density_bwd": ["density_bwd_mfma_kernel", "density_bwd_lds_kernel", "density_bwd_kernel"],
+    "density_bwd": ["density_bwd_split_kernel", "density_bwd_mfma_kernel", "density_bwd_lds_kernel",
+                    "density_bwd_kernel"],
     "density_mix_fwd": ["density_mix_fwd_kernel"], "density_mix_bwd": ["density_mix_bwd_kernel"],
     "cp_density_fwd": ["cp_density_fwd_wave_kernel", "cp_density_fwd_kernel"],
     "cp_density_bwd": ["cp_density_bwd_mfma_kernel", "cp_density_bwd_kernel"],
@@ -85,7 +86,8 @@ FAMILY_KERNELS = {
     "rows_gemm": ["rows_gemm_kernel", "rows_gemm_kc_kernel"], "eq_gate_fwd": ["eq_gate_fwd_kernel"], "eq_gate_bwd": ["eq_gate_bwd_kernel"],
     "layer_norm_fwd": ["layer_norm_fwd_kernel"], "layer_norm_bwd": ["layer_norm_bwd_kernel"],
     "spline_order": ["spline_zero_kernel", "spline_count_kernel", "spline_scan_kernel", "spline_place_kernel"],
-    "radial_spline_fwd": ["radial_spline_fwd_kernel"], "radial_spline_bwd": ["radial_spline_bwd_kernel"],
+    "radial_spline_fwd": ["radial_spline_fwd_kernel", "radial_spline_run_fwd_kernel"],
+    "radial_spline_bwd": ["radial_spline_bwd_kernel", "radial_spline_run_bwd_kernel"],
 }
 TIMED = list(KERNEL_FAMILY)
 
@@ -446,6 +448,16 @@ def pmc_probe(k, steps=2, copy_floats=1 << 28):
     sts, kw, el, desc = systems.workload(k)
     g = build_graph(sts, kw["rc"])
     m = model_for(kw, el)
+    # one step first, so that the row GEMM's launch shapes are timed and cached; then a marker
+    # launch (the gather form of the force scatter, which the model does not use) whose dispatch
+    # separates that step's (and the shape timing's) dispatches from the recorded steps'
+    m(g.with_pos(g.pos.clone()))["forces"]
+    torch.cuda.synchronize()
+    z = torch.zeros(2, dtype=torch.int32, device="cuda")
+    mark = torch.empty(1, 3, device="cuda")
+    _lib.call("face_force_scatter", _lib.ptr(mark), _lib.ptr(z), _lib.ptr(z), 1, 1.0, _lib.ptr(mark),
+              _lib.stream_of(mark))
+    torch.cuda.synchronize()
     order = _lib.record_order(True)
     for _ in range(steps):
         m(g.with_pos(g.pos.clone()))["forces"]
@@ -462,6 +474,42 @@ def pmc_probe(k, steps=2, copy_floats=1 << 28):
            "interface_bytes": {lab: interface_bytes(lab, g, kw) for lab in TIMED},
            "alg_flops": {lab: algorithmic_flops(lab, g, kw) for lab in TIMED}, "order": order}
     print(json.dumps(out), flush=True)
+
+
+PROBE_MARK = "force_scatter_kernel"
+
+
+def _after_mark(rows):
+    """Dispatch records (sorted by Dispatch_Id) after the probe's marker launch."""
+    ids = [i for i, r in enumerate(rows) if _kernel_base(r["Kernel_Name"]) == PROBE_MARK]
+    return rows[ids[-1] + 1:] if ids else rows
+
+
+def _label_dispatches(rows, order, what):
+    """(label, record) for the library dispatches of a probe run, in order: a dispatch of a kernel
+    that serves call labels (KERNEL_FAMILY) takes the next of those labels in the probe's call order;
+    other library kernels get label None."""
+    import collections
+    by_base = collections.defaultdict(list)
+    for lab, fam in KERNEL_FAMILY.items():
+        for kname in FAMILY_KERNELS[fam]:
+            by_base[kname].append(lab)
+    seq = {b: [lab for lab in order if lab in labs] for b, labs in by_base.items()}
+    pos = collections.Counter()
+    out = []
+    for r in rows:
+        if "face::" not in r["Kernel_Name"]:
+            continue
+        b = _kernel_base(r["Kernel_Name"])
+        if b not in seq or not seq[b]:
+            out.append((None, r))
+            continue
+        i = pos[b]
+        pos[b] += 1
+        if i >= len(seq[b]):
+            sys.exit(f"{what}: more dispatches of {b} than calls that launch it")
+        out.append((seq[b][i], r))
+    return out
 
 
 def _kernel_base(name):
@@ -486,36 +534,23 @@ def pmc_summary(fetch_dir, write_dir, probe_log, out_path):
         f = sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True))
         if not f:
             sys.exit(f"no counter_collection.csv under {d}")
-        rows[C] = sorted(csv.DictReader(open(f[0])), key=lambda r: int(r["Dispatch_Id"]))
+        rows[C] = _after_mark(sorted(csv.DictReader(open(f[0])), key=lambda r: int(r["Dispatch_Id"])))
     probe = [json.loads(x) for x in open(probe_log) if x.startswith('{"probe"')][0]
     cb = probe["copy_bytes_read"]
     scale = {}
     for C in rows:
         cp = sorted((r for r in rows[C] if "copyBuffer" in r["Kernel_Name"]), key=lambda r: -float(r["Counter_Value"]))
         scale[C] = cb / (1024 * sum(float(r["Counter_Value"]) for r in cp[:3]) / 3)
-    by_base = collections.defaultdict(list)
-    for lab, fam in KERNEL_FAMILY.items():
-        for kname in FAMILY_KERNELS[fam]:
-            by_base[kname].append(lab)
     order = probe["order"]
-    seq = {b: [lab for lab in order if lab in labs] for b, labs in by_base.items()}
     acc = {C: collections.defaultdict(float) for C in rows}
     names = collections.defaultdict(set)
     calls = collections.Counter(lab for lab in order)
     for C, rs in rows.items():
-        pos = collections.Counter()
-        for r in rs:
-            if "face::" not in r["Kernel_Name"]:
+        for lab, r in _label_dispatches(rs, order, C):
+            if lab is None:
                 continue
-            b = _kernel_base(r["Kernel_Name"])
-            if b not in seq or not seq[b]:
-                continue
-            i = pos[b]
-            pos[b] += 1
-            if i >= len(seq[b]):
-                sys.exit(f"{C}: more dispatches of {b} than calls that launch it")
-            acc[C][seq[b][i]] += float(r["Counter_Value"])
-            names[seq[b][i]].add(r["Kernel_Name"].replace("void ", "").split("(")[0].replace("face::", ""))
+            acc[C][lab] += float(r["Counter_Value"])
+            names[lab].add(r["Kernel_Name"].replace("void ", "").split("(")[0].replace("face::", ""))
     k = probe.get("workload", 3)
     out = [f"# HBM traffic per launch: {probe['probe']}\n\n",
            "Commands (repo root, MI355X, ROCm 7.2), one counter per pass, then the summary:\n\n```\n"]
@@ -525,9 +560,11 @@ def pmc_summary(fetch_dir, write_dir, probe_log, out_path):
                    f"> gpurun_out/pmc_{C}_w{k}.log\n")
     out.append(f"python bench.py --pmc-summary gpurun_out/pmc_FETCH_SIZE_w{k} gpurun_out/pmc_WRITE_SIZE_w{k} "
                f"gpurun_out/pmc_FETCH_SIZE_w{k}.log {out_path}\n```\n\n")
-    out.append("`bench.py --pmc-probe` runs 2 eager E+F steps, then three device-to-device copies of 1 GiB; "
-               "its JSON line lists the library calls in launch order, which "
-               "assigns each dispatch of a kernel shared by several call labels to its label.\n\n")
+    out.append("`bench.py --pmc-probe` runs one eager E+F step (the row GEMM's launch shapes are timed there) "
+               "and a marker launch, then 2 recorded eager E+F steps, then three device-to-device copies of 1 GiB; "
+               "only dispatches after the marker are counted. Its JSON line lists the library calls of the "
+               "recorded steps in launch order, which assigns each dispatch of a kernel shared by several call "
+               "labels to its label.\n\n")
     out.append(f"Calibration on the 1 GiB copy: bytes = FETCH_SIZE x 1024 x {scale['FETCH_SIZE']:.4f} and "
                f"WRITE_SIZE x 1024 x {scale['WRITE_SIZE']:.4f}.\n\n")
     out.append("traffic = scaled FETCH + scaled WRITE per call (kernels of one call summed); alg = algorithmic "
@@ -587,13 +624,28 @@ def sq_summary(out_path, title, probe_args, *dirs):
     import collections
     import csv
     import glob
+    # rows keyed by call label for the kernels that serve labels (each pass is its own process, whose
+    # row GEMM may pick other launch shapes, i.e. other kernel instances, for the same call), else by
+    # kernel; each pass's probe JSON line (the .log beside its directory) gives the call order
     data = collections.defaultdict(lambda: collections.defaultdict(list))
     for d in dirs:
         f = sorted(glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True))
         if not f:
             sys.exit(f"no counter_collection.csv under {d}")
-        for r in csv.DictReader(open(f[0])):
-            k = r["Kernel_Name"].split("(")[0].replace("void ", "").replace("face::", "")
+        recs = _after_mark(sorted(csv.DictReader(open(f[0])), key=lambda r: int(r["Dispatch_Id"])))
+        log = d.rstrip("/") + ".log"
+        order = []
+        if os.path.exists(log):
+            order = [json.loads(x) for x in open(log) if x.startswith('{"probe"')][0]["order"]
+        # a dispatch carries one record per counter: label the dispatches, then their records
+        disp = {}
+        for r in recs:
+            disp.setdefault(r["Dispatch_Id"], r)
+        labels = {r["Dispatch_Id"]: lab for lab, r in _label_dispatches(list(disp.values()), order, d)}
+        for r in recs:
+            lab = labels.get(r["Dispatch_Id"])
+            k = f"{lab} ({_kernel_base(r['Kernel_Name'])})" if lab else \
+                r["Kernel_Name"].split("(")[0].replace("void ", "").replace("face::", "")
             data[k][r["Counter_Name"]].append(float(r["Counter_Value"]))
             data[k]["_dur_ns"].append(float(r["End_Timestamp"]) - float(r["Start_Timestamp"]))
     out = [f"# SQ counters: {title}\n\nCommands (repo root, MI355X, ROCm 7.2), one pass per counter group:\n\n```\n"]
