@@ -376,6 +376,7 @@ class AtomEnergy(torch.autograd.Function):
         call("face_segment_sum", ptr(e_at), 1, ptr(struct_ptr), nstr, 1, ptr(E), 1, _lib.stream_of(e_at))
         ctx.save_for_backward(batch, scale)
         ctx.n = len(es)
+        ctx.set_materialize_grads(False)                 # e_at is usually not differentiated
         return E.view(nstr), e_at
 
     @staticmethod
@@ -384,6 +385,8 @@ class AtomEnergy(torch.autograd.Function):
         g = gE[batch] if gE is not None else None
         if g_at is not None:
             g = g_at if g is None else g + g_at
+        if g is None:
+            return (None,) * (5 + ctx.n)
         ge = (g * scale).view(-1, 1)
         return (None, None, None, None, None) + (ge,) * ctx.n
 
