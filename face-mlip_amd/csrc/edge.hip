@@ -116,6 +116,103 @@ __device__ __forceinline__ void edge_dvec(const EdgeGeom& g, int64_t e, const fl
     }
 }
 
+// Up to kEdgeGradSlots gradient buffers per edge input (Y, rb, envelope, r), null where absent:
+// one per reader of the input in the forward (each reader gets its own view of the same tensor), so
+// that their gradients are summed here, in a fixed order, instead of by separate addition launches.
+constexpr int kEdgeGradSlots = 4;
+struct EdgeGrads {
+    const float* y[kEdgeGradSlots];
+    const float* rb[kEdgeGradSlots];
+    const float* env[kEdgeGradSlots];
+    const float* r[kEdgeGradSlots];
+};
+__device__ __forceinline__ float slot_sum(const float* const (&p)[kEdgeGradSlots], int64_t i) {
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < kEdgeGradSlots; ++k)
+        if (p[k]) s += p[k][i];
+    return s;
+}
+__device__ __forceinline__ bool any_slot(const float* const (&p)[kEdgeGradSlots]) {
+    bool a = false;
+#pragma unroll
+    for (int k = 0; k < kEdgeGradSlots; ++k) a = a || p[k] != nullptr;
+    return a;
+}
+
+// edge_dvec with the gradients of each input summed over its slots. Each slot's values are read
+// in one batch (float4 rows) under a uniform branch before they are added: loads split over
+// separate branches would each wait for the one before.
+__device__ __forceinline__ void edge_dvec_slots(const EdgeGeom& g, int64_t e, const float* __restrict__ freq, int nb,
+                                                float rc, float bes_scale, const EdgeGrads& G, float* out) {
+    float gu[3] = {0.f, 0.f, 0.f};
+    if (any_slot(G.y)) {
+        float q[20];
+#pragma unroll
+        for (int k = 0; k < 20; ++k) q[k] = 0.f;
+#pragma unroll
+        for (int s = 0; s < kEdgeGradSlots; ++s) {
+            if (G.y[s]) {
+                const v4f* src = reinterpret_cast<const v4f*>(G.y[s] + e * 20);
+                v4f t[5];
+#pragma unroll
+                for (int c = 0; c < 5; ++c) t[c] = src[c];
+#pragma unroll
+                for (int c = 0; c < 5; ++c)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) q[4 * c + r] += t[c][r];
+            }
+        }
+        const float x = g.u[0], y = g.u[1], z = g.u[2];
+        gu[0] = q[1] + 2.f * x * q[4] + y * q[7] + z * q[8] + 3.f * x * x * q[10] + 2.f * x * y * q[13] +
+                2.f * x * z * q[14] + y * y * q[15] + z * z * q[17] + y * z * q[19];
+        gu[1] = q[2] + 2.f * y * q[5] + x * q[7] + z * q[9] + 3.f * y * y * q[11] + x * x * q[13] +
+                2.f * x * y * q[15] + 2.f * y * z * q[16] + z * z * q[18] + x * z * q[19];
+        gu[2] = q[3] + 2.f * z * q[6] + x * q[8] + y * q[9] + 3.f * z * z * q[12] + x * x * q[14] +
+                y * y * q[16] + 2.f * x * z * q[17] + 2.f * y * z * q[18] + x * y * q[19];
+    }
+    if (g.valid) {
+        const float ev = envelope(g);
+        float genv_t = slot_sum(G.env, e);
+        float g_r = slot_sum(G.r, e);
+        if (any_slot(G.rb)) {
+            // rb gradient rows (nb <= 16), summed over the slots, each slot read in one batch
+            float qb[16];
+#pragma unroll
+            for (int n = 0; n < 16; ++n) qb[n] = 0.f;
+#pragma unroll
+            for (int s = 0; s < kEdgeGradSlots; ++s) {
+                if (G.rb[s]) {
+                    float t[16];
+#pragma unroll
+                    for (int n = 0; n < 16; ++n) t[n] = n < nb ? G.rb[s][e * nb + n] : 0.f;
+#pragma unroll
+                    for (int n = 0; n < 16; ++n) qb[n] += t[n];
+                }
+            }
+            const float inv_r = 1.f / g.r;
+#pragma unroll
+            for (int n = 0; n < 16; ++n) {
+                if (n < nb) {
+                    const float fr = freq[n] * g.r;
+                    const float sn = sinf(fr), c = cosf(fr);
+                    const float bes = sn * inv_r * bes_scale;
+                    const float dbes = bes_scale * (freq[n] * c * inv_r - sn * inv_r * inv_r);
+                    genv_t = fmaf(qb[n], bes, genv_t);
+                    g_r = fmaf(qb[n] * ev, dbes, g_r);
+                }
+            }
+        }
+        g_r = fmaf(genv_t, envelope_dr(g, rc), g_r);
+        const float gdotu = gu[0] * g.u[0] + gu[1] * g.u[1] + gu[2] * g.u[2];
+#pragma unroll
+        for (int a = 0; a < 3; ++a) out[a] = (gu[a] - gdotu * g.u[a]) / g.r + g_r * g.u[a];
+    } else {
+#pragma unroll
+        for (int a = 0; a < 3; ++a) out[a] = gu[a];   // r := 1 is a constant on masked slots
+    }
+}
+
 __global__ __launch_bounds__(256) void edge_geom_bwd_kernel(
     const float* __restrict__ pos, const int32_t* __restrict__ recv, const int32_t* __restrict__ col,
     const float* __restrict__ shift, const uint8_t* __restrict__ mask, int64_t E, const float* __restrict__ freq,
@@ -141,9 +238,7 @@ __global__ __launch_bounds__(256) void edge_geom_bwd_kernel(
 __global__ __launch_bounds__(256) void edge_geom_bwd_seg_kernel(
     const float* __restrict__ pos, const int32_t* __restrict__ recv, const int32_t* __restrict__ col,
     const float* __restrict__ shift, const int32_t* __restrict__ rev, int64_t E, const float* __restrict__ freq,
-    int nb, float rc, float bes_scale, const float* __restrict__ gY, const float* __restrict__ grb,
-    const float* __restrict__ genv, const float* __restrict__ gr, float* __restrict__ gvec_rev,
-    float* __restrict__ wsum) {
+    int nb, float rc, float bes_scale, EdgeGrads G, float* __restrict__ gvec_rev, float* __restrict__ wsum) {
     const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;   // windows of 64 edges = one wave
     const int lane = threadIdx.x & (kWave - 1);
     const bool valid = e < E;
@@ -151,7 +246,7 @@ __global__ __launch_bounds__(256) void edge_geom_bwd_seg_kernel(
     int key = -1;
     if (valid) {
         const EdgeGeom g = edge_geom(pos, recv, col, shift, nullptr, e, rc);
-        edge_dvec(g, e, freq, nb, rc, bes_scale, gY, grb, genv, gr, out);
+        edge_dvec_slots(g, e, freq, nb, rc, bes_scale, G, out);
         const int64_t r = rev[e];
         gvec_rev[r * 3 + 0] = out[0];
         gvec_rev[r * 3 + 1] = out[1];
@@ -474,13 +569,23 @@ extern "C" int face_edge_geom_bwd(const float* pos, const int32_t* recv, const i
 
 extern "C" int face_edge_geom_bwd_seg(const float* pos, const int32_t* recv, const int32_t* col, const float* shift,
                                       const int32_t* rev, int64_t E, const float* freq, int32_t n_basis, float rc,
-                                      float bes_scale, const float* gY, const float* grb, const float* genv,
-                                      const float* gr, float* gvec_rev, float* wsum, void* stream) {
-    if (E < 0 || n_basis < 0 || !(rc > 0.f) || (grb && (!freq || n_basis == 0))) return FACE_ERR_ARG;
+                                      float bes_scale, const float* const* gY, const float* const* grb,
+                                      const float* const* genv, const float* const* gr, float* gvec_rev, float* wsum,
+                                      void* stream) {
+    if (E < 0 || n_basis < 0 || !(rc > 0.f)) return FACE_ERR_ARG;
+    EdgeGrads G{};
+    for (int k = 0; k < kEdgeGradSlots; ++k) {
+        G.y[k] = gY ? gY[k] : nullptr;
+        G.rb[k] = grb ? grb[k] : nullptr;
+        G.env[k] = genv ? genv[k] : nullptr;
+        G.r[k] = gr ? gr[k] : nullptr;
+        if (G.rb[k] && (!freq || n_basis == 0 || n_basis > 16)) return FACE_ERR_ARG;
+        if (G.y[k] && ((uintptr_t)G.y[k] & 15)) return FACE_ERR_UNSUPPORTED;     // float4 rows of 20
+    }
     if (E == 0) return 0;
     if (!pos || !recv || !col || !shift || !rev || !gvec_rev || !wsum) return FACE_ERR_ARG;
     hipLaunchKernelGGL(edge_geom_bwd_seg_kernel, dim3(blocks_for(E)), dim3(256), 0, (hipStream_t)stream, pos, recv,
-                       col, shift, rev, E, freq, n_basis, rc, bes_scale, gY, grb, genv, gr, gvec_rev, wsum);
+                       col, shift, rev, E, freq, n_basis, rc, bes_scale, G, gvec_rev, wsum);
     FACE_LAUNCH_CHECK();
     return 0;
 }

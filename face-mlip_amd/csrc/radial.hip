@@ -200,8 +200,8 @@ template <int HB, int BB>
 __global__ __launch_bounds__(kRadWaves * kWave) __attribute__((amdgpu_waves_per_eu(3))) void radial_bwd_kernel(
     const float* __restrict__ rb, int ld_rb, int nbasis, const int32_t* __restrict__ pair,
     const float* __restrict__ env, int64_t E, RadialWeights W, int n_pair, int B, const float* __restrict__ gh2,
-    int ld_gh2, const float* __restrict__ gphi, int ld_gphi, float* __restrict__ grb, int ld_grb,
-    float* __restrict__ genv, int tiles_per_wave) {
+    int ld_gh2, const float* __restrict__ gphi, const float* __restrict__ gphi2, int ld_gphi,
+    float* __restrict__ grb, int ld_grb, float* __restrict__ genv, int tiles_per_wave) {
     extern __shared__ float lds[];
     constexpr int H = 16 * HB;
     const RadialLds L(H, BB, n_pair);
@@ -231,6 +231,7 @@ __global__ __launch_bounds__(kRadWaves * kWave) __attribute__((amdgpu_waves_per_
 #pragma unroll
         for (int bb = 0; bb < BB; ++bb) {
             gp[bb] = ok ? load_cols(gphi + e * ld_gphi, 16 * bb + 4 * q, B) : z4;
+            if (gphi2 && ok) gp[bb] += load_cols(gphi2 + e * ld_gphi, 16 * bb + 4 * q, B);
             sden += gp[bb][0] * pl[bb][0] + gp[bb][1] * pl[bb][1] + gp[bb][2] * pl[bb][2] + gp[bb][3] * pl[bb][3];
             gp[bb] = gp[bb] * ev;
         }
@@ -730,8 +731,8 @@ extern "C" int face_radial_bwd(const float* rb, int32_t ld_rb, int32_t n_basis, 
                                const float* env, int64_t E, const float* w_in, const float* b_in,
                                const float* pair_tab, int32_t n_pair, int32_t H, const float* w1, const float* b1,
                                const float* w_phi, const float* b_phi, int32_t B, const float* gh2, int32_t ld_gh2,
-                               const float* gphi, int32_t ld_gphi, float* grb, int32_t ld_grb, float* genv,
-                               void* stream) {
+                               const float* gphi, const float* gphi2, int32_t ld_gphi, float* grb, int32_t ld_grb,
+                               float* genv, void* stream) {
     const RadialWeights W{w_in, b_in, pair_tab, w1, b1, w_phi, b_phi};
     if (!radial_args_ok(rb, ld_rb, n_basis, pair, E, W, n_pair, H, B) || (E > 0 && !gphi) || ld_gphi < B ||
         (gh2 && (ld_gh2 < H || ld_gh2 % 4 || ((uintptr_t)gh2 & 15))) || (grb && ld_grb < n_basis))
@@ -741,7 +742,7 @@ extern "C" int face_radial_bwd(const float* rb, int32_t ld_rb, int32_t n_basis, 
     if (lds > 65536) return FACE_ERR_UNSUPPORTED;
     const int tpw = radial_tiles_per_wave(E);
     FACE_RADIAL_DISPATCH(radial_bwd_kernel, rb, ld_rb, n_basis, pair, env, E, W, n_pair, B, gh2, ld_gh2, gphi,
-                         ld_gphi, grb, ld_grb, genv, tpw);
+                         gphi2, ld_gphi, grb, ld_grb, genv, tpw);
     FACE_LAUNCH_CHECK();
     return 0;
 }

@@ -59,8 +59,8 @@ _SIGS = {
     "face_cp_radial_bwd": (ctypes.c_int, [P, I32, P, P, I32, P, P, I32, P, I64, I32, I32, P, I64, I64, P, I32, P, I32,
                                           P, I32, P, I32, P, P]),
     "face_radial_fwd": (ctypes.c_int, [P, I32, I32, P, P, I64, P, P, P, I32, I32, P, P, P, P, I32, P, I32, P, I32, P]),
-    "face_radial_bwd": (ctypes.c_int, [P, I32, I32, P, P, I64, P, P, P, I32, I32, P, P, P, P, I32, P, I32, P, I32, P,
-                                       I32, P, P]),
+    "face_radial_bwd": (ctypes.c_int, [P, I32, I32, P, P, I64, P, P, P, I32, I32, P, P, P, P, I32, P, I32, P, P, I32,
+                                       P, I32, P, P]),
     "face_radial_spline_fwd": (ctypes.c_int, [P, P, I64, P, P, I32, I32, I32, F32, P, I32, P, P, I32, P, I32, P]),
     "face_radial_spline_bwd": (ctypes.c_int, [P, P, I64, P, P, I32, I32, I32, F32, P, I32, P, P, I32, P, I32, P,
                                               P, P]),
@@ -75,7 +75,7 @@ _SIGS = {
     "face_layer_norm_bwd": (ctypes.c_int, [P, P, I64, I32, P, P, P, P, P]),
 }
 
-ABI_VERSION = 17
+ABI_VERSION = 18
 
 
 class LinProblem(ctypes.Structure):

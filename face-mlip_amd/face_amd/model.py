@@ -231,22 +231,27 @@ class FactorBlock(nn.Module):
 
     # ------------------------------------------------------------------ moments
     def moments(self, h, rb, r, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g, order=None):
-        """Moments A_l as monomial-major (k_l, N, C) blocks (face/model.py:460-534)."""
+        """Moments A_l as monomial-major (k_l, N, C) blocks (face/model.py:460-534). Y and env may be
+        pairs of views of one tensor, (density reader, directional / radial reader), so that their
+        gradients reach the edge backward separately (FACE.forward)."""
         N, E = g.N, g.E
         B, C, Kd = self.B, self.C, self.K
+        Y, Y_dir = Y if isinstance(Y, tuple) else (Y, Y)
+        env, env_rad = env if isinstance(env, tuple) else (env, env)
         W2, b2 = frozen(self.radial[2])
         if self.spline is not None:
             # compiled radial (face/model.py:466-467): phi = spline * env (E, B) and, in CP form,
             # the raw CP radials (E, 4C) whose envelope the pooling kernels apply
             sp = self.spline
-            phi, R_sp = ops.radial_spline(r, env, zp, sp.T, sp.dT, sp.dr, B, order)
+            phi, R_sp = ops.radial_spline(r, env_rad, zp, sp.T, sp.dT, sp.dr, B, order)
+            phi_dir = phi
         else:
             # hidden layers and phi columns of the radial MLP in one HIP kernel; the CP columns of
-            # the last layer are a GEMM on its h2 output
+            # the last layer are a GEMM on its h2 output; phi once per reader (density, transport)
             Wi, bi = frozen(self.rad_in)
             W1, b1 = frozen(self.radial[0])
-            phi, h2 = ops.radial_mlp(rb, env, zp, Wi, bi, self.pair.weight.detach(), W1, b1, W2[:B], b2[:B],
-                                     self.cp)                                    # (E, B), (E, H)
+            phi, phi_dir, h2 = ops.radial_mlp(rb, env_rad, zp, Wi, bi, self.pair.weight.detach(), W1, b1, W2[:B],
+                                              b2[:B], self.cp)                   # (E, B) twice, (E, H)
         msg_n = F.linear(h, *frozen(self.msg))                                   # (N, K)
         if self.directional:
             if self.eq_in:
@@ -256,7 +261,7 @@ class FactorBlock(nn.Module):
                 src2 = torch.cat([S[2] for S in sets], -1)
             Vb = F.linear(src1, frozen(self.pvt)[0])                             # (3, N, nt*Kd)
             Mb = F.linear(src2, frozen(self.pmt)[0])                             # (6, N, nt*Kd)
-            d, D1, D2 = ops.dir_transport(Vb, Mb, phi, Y, g, Kd, self.transport)   # (E, 4Kd), transport sums
+            d, D1, D2 = ops.dir_transport(Vb, Mb, phi_dir, Y_dir, g, Kd, self.transport)   # (E, 4Kd), sums
             # gather(msg(h)) + dir_mix(d) as one per-edge matrix-core launch (and one backward)
             Wd, bd = frozen(self.dir_mix)
             if d.shape[1] % 16 == 0 and d.shape[1] <= 64 and msg_n.shape[1] % 16 == 0 and msg_n.shape[1] <= 256:
@@ -487,8 +492,25 @@ class FACE(nn.Module):
         if forces and not pos.requires_grad:
             pos.requires_grad_(True)
         splines = [b.spline is not None for b in self.blocks]
-        Y, rb, env, r = ops.edge_geometry(pos, graph, self.basis.freq, self.rc, with_rb=not all(splines),
-                                          with_r=any(splines))
+        # each reader of Y, rb, the envelope and r gets its own view, so that the edge backward sums
+        # their gradients (no addition launches): per pass, Y is read by the density and the
+        # directional features, the envelope by the radial functions and the CP pooling
+        readers = [(1 + b.directional, int(b.spline is None), 1 + int(b.cp), int(b.spline is not None))
+                   for b in self.blocks]
+        counts = [sum(x[i] for x in readers) for i in range(4)]
+        geo = ops.edge_geometry(pos, graph, self.basis.freq, self.rc, with_rb=not all(splines), with_r=any(splines),
+                                counts=counts)
+        views, k = [], 0
+        for c in counts:
+            c = max(1, min(ops.EDGE_GRAD_SLOTS, c))
+            views.append(list(geo[k:k + c]))
+            k += c
+
+        def take(i):
+            """The next view of input i (the last one is shared once the slots run out)."""
+            v = views[i]
+            return v.pop(0) if len(v) > 1 else v[0]
+        r = views[3][0]                  # the spline order (no gradient) reads the first r view
         # per-atom element index, element-pair row of every edge, the embedding rows and the energy
         # offsets: functions of the graph's species and of constants only, cached on the graph per
         # model (the entry holds the tensors it depends on and their in-place versions, so it can
@@ -516,9 +538,16 @@ class FACE(nn.Module):
         acc = {} if all(b.eq_in or not b.directional for b in self.blocks) else None
         sets, eq, es = [], None, []
         nb = len(self.blocks)
+        rb0, r0 = views[1][0], views[3][0]
         for t, blk in enumerate(self.blocks):
-            e, h, A, eq = blk(h, rb, r, Y, env, zp, zidx, zidx32, self.avg_nb, sets, eq, graph, order, acc,
-                              last=t == nb - 1)
+            y_d = take(0)
+            y_t = take(0) if blk.directional else y_d
+            rb_b = take(1) if blk.spline is None else rb0
+            env_r = take(2)
+            env_d = take(2) if blk.cp else env_r
+            r_b = take(3) if blk.spline is not None else r0
+            e, h, A, eq = blk(h, rb_b, r_b, (y_d, y_t), (env_d, env_r), zp, zidx, zidx32, self.avg_nb, sets, eq, graph,
+                              order, acc, last=t == nb - 1)
             sets.append(A)
             es.append(e)
         E, e_at = ops.atom_energy(e0, self.scale, graph.struct_ptr, graph.batch, graph.nstr, es)

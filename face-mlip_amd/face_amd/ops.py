@@ -53,13 +53,18 @@ class Graph:
 
 
 # ----------------------------------------------------------------------------- edge geometry
+EDGE_GRAD_SLOTS = 4                 # gradient buffers per edge input the edge backward sums
+
+
 class EdgeGeometry(torch.autograd.Function):
     """pos -> (Y (E,20), rb (E,nb), env (E), r (E)) for the edges of `graph` (face/model.py:670-677).
     With_r False: r is an empty tensor; with_rb False (compiled radial, which reads r instead of
-    the Bessel rows): rb is an empty tensor and is not computed."""
+    the Bessel rows): rb is an empty tensor and is not computed. counts = (n_y, n_rb, n_env, n_r):
+    each input is returned that many times, as views of one tensor, one per reader, so that the
+    readers' gradients arrive separately and the edge backward sums them (no addition launches)."""
 
     @staticmethod
-    def forward(ctx, pos, graph, freq, rc, bes_scale, with_rb, with_r):
+    def forward(ctx, pos, graph, freq, rc, bes_scale, with_rb, with_r, counts):
         _lib.require_gpu(pos)
         pos = pos.contiguous().float()
         E, nb = graph.E, freq.numel()
@@ -71,34 +76,50 @@ class EdgeGeometry(torch.autograd.Function):
              nb, float(rc), float(bes_scale), ptr(Y), ptr(rb) if with_rb else None, ptr(env),
              ptr(r) if with_r else None, _lib.stream_of(pos), label="edge_fwd")
         ctx.save_for_backward(pos, freq)
-        ctx.graph, ctx.rc, ctx.bes_scale = graph, rc, bes_scale
-        return Y, rb, env, r
+        ctx.graph, ctx.rc, ctx.bes_scale, ctx.counts = graph, rc, bes_scale, counts
+        ctx.set_materialize_grads(False)
+        out = []
+        for t, n in zip((Y, rb, env, r), counts):
+            out += [t] + [t.view(t.shape) for _ in range(n - 1)]
+        return tuple(out)
 
     @staticmethod
-    def backward(ctx, gY, grb, genv, gr):
+    def backward(ctx, *grads):
         pos, freq = ctx.saved_tensors
         g = ctx.graph
         gvec = torch.empty(g.E, 3, device=pos.device)
-        cont = lambda t: None if (t is None or t.numel() == 0) else t.contiguous().float()
-        gY, grb, genv, gr = cont(gY), cont(grb), cont(genv), cont(gr)
+        keep = []
+
+        def slots(gs):
+            ts = [t.contiguous().float() for t in gs if t is not None and t.numel() > 0]
+            if not ts:
+                return None
+            keep.extend(ts)
+            return _lib.ptr_array(ts + [None] * (EDGE_GRAD_SLOTS - len(ts)))
+
+        groups, i = [], 0
+        for n in ctx.counts:
+            groups.append(slots(grads[i:i + n]))
+            i += n
         st = _lib.stream_of(pos)
         # edge backward: each edge's dL/dvec lands in its reverse edge's slot and the own-row sums are
         # reduced per 64-edge window in the same pass (wsum), so the scatter reads one contiguous row
         # per atom, no reverse-edge gathers: grad_k = sum_{e in row k} gvec[rev e] - gvec[e]
         wsum = torch.empty(g.E, 3, device=pos.device)
         call("face_edge_geom_bwd_seg", ptr(pos), ptr(g.recv), ptr(g.col), ptr(g.shift), ptr(g.rev), g.E, ptr(freq),
-             freq.numel(), float(ctx.rc), float(ctx.bes_scale), ptr(gY), ptr(grb), ptr(genv), ptr(gr), ptr(gvec),
-             ptr(wsum), st, label="edge_bwd")
+             freq.numel(), float(ctx.rc), float(ctx.bes_scale), *groups, ptr(gvec), ptr(wsum), st, label="edge_bwd")
         gpos = torch.empty_like(pos)
         mean_row = (g.E + max(g.N, 1) - 1) // max(g.N, 1)
         call("face_force_scatter_rows", ptr(gvec), ptr(wsum), ptr(g.row_ptr), g.N, mean_row, 1.0, ptr(gpos), st,
              label="force_scatter")
-        return gpos, None, None, None, None, None, None
+        return gpos, None, None, None, None, None, None, None
 
 
-def edge_geometry(pos, graph, freq, rc, with_rb=True, with_r=False):
-    """(Y, rb, env, r); rb / r are empty tensors when not asked for."""
-    return EdgeGeometry.apply(pos, graph, freq, rc, math.sqrt(2.0 / rc), with_rb, with_r)
+def edge_geometry(pos, graph, freq, rc, with_rb=True, with_r=False, counts=(1, 1, 1, 1)):
+    """(Y..., rb..., env..., r...): each input counts[i] times (views, one per reader; at most
+    EDGE_GRAD_SLOTS each); rb / r are empty tensors when not asked for."""
+    counts = tuple(max(1, min(EDGE_GRAD_SLOTS, int(c))) for c in counts)
+    return EdgeGeometry.apply(pos, graph, freq, rc, math.sqrt(2.0 / rc), with_rb, with_r, counts)
 
 
 # ----------------------------------------------------------------------------- gathers
@@ -845,26 +866,31 @@ class RadialMLP(torch.autograd.Function):
              ptr(phi), B, _lib.stream_of(rb), label="radial_fwd")
         ctx.save_for_backward(rb_, env_, pair, *ws)
         ctx.dims = (E, nb, H, B)
-        return phi, h2
+        ctx.set_materialize_grads(False)
+        return phi, phi.view(phi.shape), h2
 
     @staticmethod
-    def backward(ctx, gphi, gh2):
+    def backward(ctx, gphi, gphi2, gh2):
         if any(ctx.needs_input_grad[2:]):
             raise NotImplementedError("the fused radial MLP gives no weight gradients (forces only)")
         rb, env, pair, *ws = ctx.saved_tensors
         E, nb, H, B = ctx.dims
         dev = rb.device
-        gphi = torch.zeros(E, B, device=dev) if gphi is None else gphi.contiguous().float()
+        gp = [t.contiguous().float() for t in (gphi, gphi2) if t is not None]
+        if not gp:
+            gp = [torch.zeros(E, B, device=dev)]
         gh2 = gh2.contiguous().float() if (gh2 is not None and gh2.numel()) else None
         grb = torch.empty(E, nb, device=dev) if ctx.needs_input_grad[0] else None
         genv = torch.empty(E, device=dev) if ctx.needs_input_grad[1] else None
         call("face_radial_bwd", ptr(rb), rb.stride(0), nb, ptr(pair), ptr(env), E, ptr(ws[0]), ptr(ws[1]), ptr(ws[2]),
-             ws[2].shape[0], H, ptr(ws[3]), ptr(ws[4]), ptr(ws[5]), ptr(ws[6]), B, ptr(gh2), H, ptr(gphi), B,
-             ptr(grb), nb, ptr(genv), _lib.stream_of(rb), label="radial_bwd")
+             ws[2].shape[0], H, ptr(ws[3]), ptr(ws[4]), ptr(ws[5]), ptr(ws[6]), B, ptr(gh2), H, ptr(gp[0]),
+             ptr(gp[1]) if len(gp) > 1 else None, B, ptr(grb), nb, ptr(genv), _lib.stream_of(rb), label="radial_bwd")
         return grb, genv, None, None, None, None, None, None, None, None, None
 
 
 def radial_mlp(rb, env, pair, w_in, b_in, pair_tab, w1, b1, w_phi, b_phi, want_h2):
+    """(phi, phi again as a view for a second reader (its gradient is summed in the backward
+    kernel), h2)."""
     return RadialMLP.apply(rb, env, pair, w_in, b_in, pair_tab, w1, b1, w_phi, b_phi, want_h2)
 
 

@@ -268,14 +268,15 @@ int face_radial_fwd(const float* rb, int32_t ld_rb, int32_t n_basis, const int32
                     int64_t E, const float* w_in, const float* b_in, const float* pair_tab, int32_t n_pair,
                     int32_t H, const float* w1, const float* b1, const float* w_phi, const float* b_phi, int32_t B,
                     float* h2, int32_t ld_h2, float* phi, int32_t ld_phi, void* stream);
-/* Backward for gh2 = dL/dh2 (may be NULL = 0; 16-byte aligned rows) and gphi = dL/dphi:
+/* Backward for gh2 = dL/dh2 (may be NULL = 0; 16-byte aligned rows) and gphi = dL/dphi
+ * (plus gphi2, same layout, when phi has a second reader; may be NULL):
  * grb (E, ld_grb) = dL/drb, genv (E) = dL/denv through phi (either may be NULL). The
  * weights receive no gradient (forces only). */
 int face_radial_bwd(const float* rb, int32_t ld_rb, int32_t n_basis, const int32_t* pair, const float* env,
                     int64_t E, const float* w_in, const float* b_in, const float* pair_tab, int32_t n_pair,
                     int32_t H, const float* w1, const float* b1, const float* w_phi, const float* b_phi, int32_t B,
-                    const float* gh2, int32_t ld_gh2, const float* gphi, int32_t ld_gphi, float* grb, int32_t ld_grb,
-                    float* genv, void* stream);
+                    const float* gh2, int32_t ld_gh2, const float* gphi, const float* gphi2, int32_t ld_gphi,
+                    float* grb, int32_t ld_grb, float* genv, void* stream);
 
 /* ---------------------------------------------------------------- compiled radial (splines)
  * RadialSpline.forward (face/model.py:407-418), the table lookup that FACE.compile_radial
@@ -440,11 +441,13 @@ int face_force_scatter(const float* gvec, const int32_t* row_ptr, const int32_t*
  * grad[k] = sign * sum_{e in row k} (gvec_rev[e] - [e is the row's last edge in its window] wsum[e]),
  * reading each row contiguously. mean_row (~E/N) picks the lanes per row. Fixed summation
  * order, no atomics. Replaces the index_add backward of pos[nbr] - pos[i] (face/model.py:670;
- * forces = -grad at :692-694). */
+ * forces = -grad at :692-694). gY, grb, genv, gr each point to 4 gradient buffers of that input
+ * (entries may be null; a null array means none), summed in slot order: one per reader of the
+ * input in the forward, so no separate accumulation of the readers' gradients is needed. */
 int face_edge_geom_bwd_seg(const float* pos, const int32_t* recv, const int32_t* col, const float* shift,
                            const int32_t* rev, int64_t E, const float* freq, int32_t n_basis, float rc, float bes_scale,
-                           const float* gY, const float* grb, const float* genv, const float* gr, float* gvec_rev,
-                           float* wsum, void* stream);
+                           const float* const* gY, const float* const* grb, const float* const* genv,
+                           const float* const* gr, float* gvec_rev, float* wsum, void* stream);
 int face_force_scatter_rows(const float* gvec_rev, const float* wsum, const int32_t* row_ptr, int64_t N,
                             int32_t mean_row, float sign, float* grad, void* stream);
 

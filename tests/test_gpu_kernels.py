@@ -367,6 +367,14 @@ def test_edge_geometry_forward_and_backward(system):
     Y, rb, env, rr = ops.edge_geometry(pos, g, freq, rc, with_r=True)
     wY, wr, we, wd = torch.randn_like(Y), torch.randn_like(rb), torch.randn_like(env), torch.randn_like(rr)
     (gp,) = torch.autograd.grad((Y * wY).sum() + (rb * wr).sum() + (env * we).sum() + (rr * wd).sum(), pos)
+    # each input handed to several readers as views of one tensor: their gradients, summed in the
+    # edge backward, give the same forces as one reader with the summed upstream gradient
+    outs = ops.edge_geometry(pos, g, freq, rc, with_r=True, counts=(3, 2, 4, 2))
+    assert len(outs) == 11 and all(torch.equal(t, Y) for t in outs[:3]) and torch.equal(outs[3], rb)
+    parts = [(outs[0], 0.5 * wY), (outs[1], 0.25 * wY), (outs[2], 0.25 * wY), (outs[3], 0.5 * wr), (outs[4], 0.5 * wr),
+             (outs[5], we), (outs[6], 0 * we), (outs[9], 0.5 * wd), (outs[10], 0.5 * wd)]   # one env view unread
+    (gp_v,) = torch.autograd.grad(sum((t * w).sum() for t, w in parts), pos)
+    assert (gp_v - gp).abs().max() <= 1e-5 * gp.abs().max()
     # without the Bessel rows (compiled radial): rb is empty and the rest unchanged
     Y3, rb3, env3, r3 = ops.edge_geometry(pos.detach(), g, freq, rc, with_rb=False, with_r=True)
     assert rb3.numel() == 0 and torch.equal(Y3, Y.detach()) and torch.equal(r3, rr.detach())
@@ -620,12 +628,14 @@ def test_radial_mlp_matches_torch(E, nb, H, B, n_pair, want_h2):
     ws = [torch.randn(H, nb) / nb ** 0.5, torch.randn(H) * 0.1, torch.randn(n_pair, H) * 0.3,
           torch.randn(H, H) / H ** 0.5, torch.randn(H) * 0.1, torch.randn(B, H) / H ** 0.5, torch.randn(B) * 0.1]
     ws = [w.to(DEV) for w in ws]
-    phi, h2 = ops.radial_mlp(rb, env, pair, *ws, want_h2)
+    phi, phi_b, h2 = ops.radial_mlp(rb, env, pair, *ws, want_h2)
     assert phi.shape == (E, B) and h2.shape == ((E, H) if want_h2 else (0, H))
+    assert torch.equal(phi, phi_b)
     if E == 0:
         return
     gp = torch.randn_like(phi)
-    L = (phi * gp).sum()
+    # the upstream gradient split over the two readers' views (summed in the backward kernel)
+    L = (phi * (0.25 * gp)).sum() + (phi_b * (0.75 * gp)).sum()
     gh = torch.randn(E, H, device=DEV)
     if want_h2:
         L = L + (h2 * gh).sum()
