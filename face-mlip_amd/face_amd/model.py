@@ -559,5 +559,8 @@ class FACE(nn.Module):
             if seed is None or seed.device != E.device:
                 seed = torch.full((graph.nstr,), -1.0, device=E.device)
                 graph.cache[key] = seed
-            (out["forces"],) = torch.autograd.grad(E, pos, grad_outputs=seed)
+            # the backward runs on this thread: handing it to autograd's device thread cost ~1.4 ms
+            # per eager 864-atom step (4.1 -> 2.7 ms) in cross-thread scheduling of ~90 small launches
+            with torch.autograd.set_multithreading_enabled(False):
+                (out["forces"],) = torch.autograd.grad(E, pos, grad_outputs=seed)
         return out
