@@ -90,6 +90,7 @@ struct GemmArgs {
     const int32_t* group;
     int64_t period;
     int side_off, kmax;                    // LDS offset (floats) of the side tables; largest K
+    int xcd_order;                         // one-item launches: items in XCD-contiguous ranges
 };
 
 // LDS side tables of a launch, after the weight slice (floats): ys [n_groups][16 NB] (slice
@@ -342,7 +343,14 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
     } else {
         int pi, slice;
         int64_t t;
-        locate(blockIdx.x, pi, slice, t);
+        // XCD-aware item order (xcd_order): workgroup b runs on XCD b % 8, so each XCD takes a
+        // contiguous range of items and the column slices of a row tile share its L2 for the rows
+        int64_t item = blockIdx.x;
+        if (A.xcd_order) {
+            const int64_t nbk = gridDim.x, bx = blockIdx.x, xcd = bx & 7, per = nbk >> 3, rem = nbk & 7;
+            item = xcd * per + (xcd < rem ? xcd : rem) + (bx >> 3);
+        }
+        locate(item, pi, slice, t);
         stage(pi, slice);
         compute(pi, slice, (t * NW + wv) * (16 * kGemmBB));
     }
@@ -602,11 +610,12 @@ static int default_nw(const RowsCtx& c, int NS) {
 // One launch of rows_gemm_kernel with NW waves per workgroup and the widest problem split into
 // n_sl column slices (NS = its width rounded up to 16 columns); FACE_ERR_UNSUPPORTED, before
 // anything is launched, if that shape does not fit.
-static int launch_rows(const RowsCtx& c, int NW, int n_sl) {
+static int launch_rows(const RowsCtx& c, int NW, int n_sl, int xcd_order = 0) {
     if (n_sl < 1 || (NW != 4 && NW != 8 && NW != 16)) return FACE_ERR_UNSUPPORTED;
     const int NS = ((c.n_widest + n_sl - 1) / n_sl + 15) / 16 * 16;
     if (NS > c.ns_max || NS > 160) return FACE_ERR_UNSUPPORTED;
     GemmArgs A = c.A;
+    A.xcd_order = xcd_order;
     int max_n = 16;
     int64_t blocks = 0, total_cost = 0;
     for (int i = 0; i < c.n_probs; ++i) {
@@ -710,19 +719,21 @@ static int launch_rows(const RowsCtx& c, int NW, int n_sl) {
 // 33 us), and the best shape moves irregularly with the row count. So the first call of a
 // signature (device, problem shapes, transposition, scales, kernel form) times every shape of
 // 4, 8 or 16 waves and distinct slice widths (three launches each, then the three fastest and the
-// rule's own five times more) and keeps the fastest unless it beats the rule's by less than 2 %.
+// rule's own five times more, also with an XCD-aware item order for one-item launches) and keeps
+// the fastest unless it beats the rule's by less than 2 %.
 // Every shape computes each output with the same instructions in the same order, so results are
 // bitwise the same whatever the shape. Timing needs launches that can run again with the same
 // result: only calls whose problems all have beta = 0 (or read beta y0 from another tensor), on a
 // stream that is not being captured, are timed; others use a shape timed earlier for the same
 // signature, else the rules. FACE_GEMM_TUNE=0 in the environment keeps the rules.
 struct ShapePlan {
-    int nw, n_sl;
+    int nw, n_sl, xcd;
 };
 static std::mutex g_plan_mu;
 static std::map<std::vector<int64_t>, ShapePlan> g_plans;
 
-static void pick_shape(const RowsCtx& c, int& NW, int& n_sl) {
+static void pick_shape(const RowsCtx& c, ShapePlan& plan) {
+    const int NW = plan.nw, n_sl = plan.n_sl;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return;
     std::vector<int64_t> key = {dev, c.n_probs, c.w_kn, c.x_scale, c.y_scale, c.n_groups, c.any_ext, c.any_bias};
@@ -735,7 +746,7 @@ static void pick_shape(const RowsCtx& c, int& NW, int& n_sl) {
         std::lock_guard<std::mutex> lk(g_plan_mu);
         auto it = g_plans.find(key);
         if (it != g_plans.end()) {
-            NW = it->second.nw, n_sl = it->second.n_sl;
+            plan = it->second;
             return;
         }
     }
@@ -747,14 +758,14 @@ static void pick_shape(const RowsCtx& c, int& NW, int& n_sl) {
     }
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(c.st, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return;
-    std::vector<ShapePlan> cand = {{NW, n_sl}};
+    std::vector<ShapePlan> cand = {{NW, n_sl, 0}};
     for (int nw : {16, 8, 4})
         for (int ns = 16; ns <= c.ns_max && ns <= 160; ns += 16) {
             const int k = (c.n_widest + ns - 1) / ns;
             if (k > 32) continue;
             bool seen = false;
             for (const ShapePlan& p : cand) seen = seen || (p.nw == nw && p.n_sl == k);
-            if (!seen) cand.push_back({nw, k});
+            if (!seen) cand.push_back({nw, k, 0});
         }
     hipEvent_t e0 = nullptr, e1 = nullptr;
     if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) {
@@ -762,10 +773,10 @@ static void pick_shape(const RowsCtx& c, int& NW, int& n_sl) {
         return;
     }
     auto time_it = [&](const ShapePlan& p, int reps) -> float {   // us per launch, < 0 if it does not run
-        if (launch_rows(c, p.nw, p.n_sl) != 0) return -1.f;
+        if (launch_rows(c, p.nw, p.n_sl, p.xcd) != 0) return -1.f;
         if (hipEventRecord(e0, c.st) != hipSuccess) return -1.f;
         for (int r = 0; r < reps; ++r)
-            if (launch_rows(c, p.nw, p.n_sl) != 0) return -1.f;
+            if (launch_rows(c, p.nw, p.n_sl, p.xcd) != 0) return -1.f;
         float ms = 0.f;
         if (hipEventRecord(e1, c.st) != hipSuccess || hipEventSynchronize(e1) != hipSuccess ||
             hipEventElapsedTime(&ms, e0, e1) != hipSuccess)
@@ -782,16 +793,24 @@ static void pick_shape(const RowsCtx& c, int& NW, int& n_sl) {
         std::sort(t1.begin(), t1.end());
         const float t_rule = time_it(cand[0], 5);
         float t_best = t_rule;
+        // the three fastest and the rule's shape again, each also with the XCD-aware item order
         for (int r = 0; r < 3 && r < (int)t1.size(); ++r) {
             if (t1[r].second == 0) continue;
             const float t = time_it(cand[t1[r].second], 5);
             if (t >= 0.f && (t_best < 0.f || t < t_best)) t_best = t, best = cand[t1[r].second];
         }
+        for (int r = -1; r < 3 && r < (int)t1.size(); ++r) {
+            if (r >= 0 && t1[r].second == 0) continue;
+            ShapePlan p = r < 0 ? cand[0] : cand[t1[r].second];
+            p.xcd = 1;
+            const float t = time_it(p, 5);
+            if (t >= 0.f && (t_best < 0.f || t < t_best)) t_best = t, best = p;
+        }
         if (t_rule >= 0.f && !(t_best < 0.98f * t_rule)) best = cand[0];
     }
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
-    NW = best.nw, n_sl = best.n_sl;
+    plan = best;
     std::lock_guard<std::mutex> lk(g_plan_mu);
     g_plans[key] = best;
 }
@@ -898,7 +917,7 @@ extern "C" int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, 
     c.y_scale = y_scale != nullptr, c.any_bias = any_bias, c.any_ext = any_ext, c.n_groups = n_groups;
     c.st = (hipStream_t)stream;
     if (x_scale && any_ext) return FACE_ERR_UNSUPPORTED;                 // x scale with split / op / y0
-    int NW = default_nw(c, NS), nsl = n_sl;
-    pick_shape(c, NW, nsl);
-    return launch_rows(c, NW, nsl);
+    ShapePlan plan{default_nw(c, NS), n_sl, 0};
+    pick_shape(c, plan);
+    return launch_rows(c, plan.nw, plan.n_sl, plan.xcd);
 }

@@ -182,8 +182,15 @@ def ptr(t):
     return None if t is None else t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t=None):
-    """Raw HIP stream handle of torch's current stream on the tensor's device."""
+    """Raw HIP stream handle of torch's current stream on the tensor's device (the raw-handle
+    query skips building a Stream object on every launch)."""
+    if _raw_stream is not None:
+        idx = t.device.index if (t is not None and t.device.index is not None) else torch.cuda.current_device()
+        return _raw_stream(idx)
     dev = t.device if t is not None else torch.device("cuda")
     return torch.cuda.current_stream(dev).cuda_stream
 
