@@ -28,6 +28,8 @@ def _lib():
         lib.oracle_pair_list.argtypes = [ctypes.c_void_p, ctypes.c_int32, ctypes.c_void_p, ctypes.c_void_p,
                                          ctypes.c_double, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                          ctypes.c_int64]
+        lib.oracle_pair_list_cells.restype = ctypes.c_int64
+        lib.oracle_pair_list_cells.argtypes = lib.oracle_pair_list.argtypes
         _LIB = lib
     return _LIB
 
@@ -38,19 +40,40 @@ def pair_list(pos, cell, pbc, rc):
     pos (n,3) float64, cell (3,3) float64 (rows = lattice vectors), pbc (3,) bool.
     Returns i (E,), j (E,), S (E,3) as int64 numpy arrays.
     """
+    return _pairs("oracle_pair_list", pos, cell, pbc, rc)
+
+
+def pair_list_cells(pos, cell, pbc, rc):
+    """pair_list for cells periodic on all three axes in about O(n) time: the same per-pair image
+    loop and arithmetic, the j loop narrowed to the atoms of adjacent bins of the fractional
+    coordinates (bins no narrower than rc / face distance, so no pair within rc is skipped).
+    Raises ValueError unless all three axes are periodic."""
+    if not all(bool(b) for b in np.asarray(pbc).reshape(3)):
+        raise ValueError("pair_list_cells needs a cell periodic on all three axes")
+    return _pairs("oracle_pair_list_cells", pos, cell, pbc, rc)
+
+
+def _pairs(fn, pos, cell, pbc, rc):
     pos = np.ascontiguousarray(pos, dtype=np.float64)
     cell = np.ascontiguousarray(cell, dtype=np.float64)
     pbc_a = np.ascontiguousarray(np.asarray(pbc, dtype=np.int32).reshape(3))
     n = len(pos)
-    lib = _lib()
+    f = getattr(_lib(), fn)
     args = (pos.ctypes.data, n, cell.ctypes.data, pbc_a.ctypes.data, float(rc))
-    E = lib.oracle_pair_list(*args, None, None, None, 0)
-    oi = np.zeros(E, np.int32)
-    oj = np.zeros(E, np.int32)
-    oS = np.zeros((E, 3), np.int32)
-    E2 = lib.oracle_pair_list(*args, oi.ctypes.data, oj.ctypes.data, oS.ctypes.data, E)
-    assert E2 == E
-    return oi.astype(np.int64), oj.astype(np.int64), oS.astype(np.int64)
+    # one pass into a buffer of 96 pairs per atom, a second one sized to the count if that is short
+    cap = 0 if fn == "oracle_pair_list" else 96 * n + 1024
+    while True:
+        oi = np.zeros(cap, np.int32)
+        oj = np.zeros(cap, np.int32)
+        oS = np.zeros((cap, 3), np.int32)
+        E = f(*args, oi.ctypes.data if cap else None, oj.ctypes.data if cap else None,
+              oS.ctypes.data if cap else None, cap)
+        if E < 0:
+            raise RuntimeError(f"{fn} failed ({E})")
+        if E <= cap:
+            break
+        cap = E
+    return oi[:E].astype(np.int64), oj[:E].astype(np.int64), oS[:E].astype(np.int64)
 
 
 def padded_graph(structures, rc, device="cpu", dtype=torch.float32):

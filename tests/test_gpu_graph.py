@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 import torch
 
-from oracle.neighbors import pair_list, padded_graph as oracle_padded
+from oracle.neighbors import pair_list, pair_list_cells, padded_graph as oracle_padded
 
 pytestmark = pytest.mark.gpu
 
@@ -16,19 +16,19 @@ def say(*a):
     sys.stdout.flush()
 
 
-def oracle_csr(structures, rc):
+def oracle_csr(structures, rc, pairs=pair_list):
     I, J, S, off = [], [], [], 0
     for st in structures:
-        i, j, s = pair_list(st["pos"], st["cell"], st["pbc"], rc)
+        i, j, s = pairs(st["pos"], st["cell"], st["pbc"], rc)
         I.append(i + off); J.append(j + off); S.append(s)
         off += len(st["pos"])
     return np.concatenate(I), np.concatenate(J), np.concatenate(S)
 
 
-def check_graph(structures, rc, method="auto"):
+def check_graph(structures, rc, method="auto", pairs=pair_list):
     from face_amd.neighbors import build_graph
     g = build_graph(structures, rc, method=method)
-    i, j, S = oracle_csr(structures, rc)
+    i, j, S = oracle_csr(structures, rc, pairs)
     recv, col, Sg = g.recv.cpu().numpy(), g.col.cpu().numpy(), g.S.cpu().numpy()
     assert len(col) == len(j), (len(col), len(j))
     assert np.array_equal(recv, i) and np.array_equal(col, j) and np.array_equal(Sg, S)
@@ -62,6 +62,18 @@ def test_liquid_3000_exact(method):
     say("liquid 3000", method)
     st = systems.liquid(3000, np.random.default_rng(5))
     check_graph([st], 5.0, method=method)
+
+
+@pytest.mark.parametrize("k", [3, 4])
+def test_liquid_full_size_exact(k):
+    """The 24,000-atom (1.25 M pairs) and 100,000-atom (6.9 M pairs) liquids at full size against
+    the bin-candidate fp64 oracle (equal to the brute-force one, pinned on the CPU)."""
+    from face_amd import systems
+    sts, kw, el, desc = systems.workload(k)
+    say("full-size pair list", desc)
+    g = check_graph(sts, kw["rc"], pairs=pair_list_cells)
+    say(f"  N {g.N} E {g.E} max_row {g.max_row}")
+    assert g.N == len(sts[0]["pos"]) and g.E > (1_000_000 if k == 3 else 6_000_000)
 
 
 @pytest.mark.parametrize("method", ["cell", "small"])

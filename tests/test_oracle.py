@@ -9,7 +9,7 @@ import torch
 
 from oracle import cartesian, ops
 from oracle import model as omodel
-from oracle.neighbors import pair_list, padded_graph
+from oracle.neighbors import pair_list, pair_list_cells, padded_graph
 from golden.cases import BIG_CASES, SMALL_CASES
 
 GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
@@ -204,6 +204,48 @@ def test_fcc_shell_counts():
     st = systems.fcc(4.09, 3, 0.0, np.random.default_rng(0))
     i, _, _ = pair_list(st["pos"], st["cell"], st["pbc"], 4.5)
     assert (np.bincount(i) == 18).all()          # 12 nearest (2.89 A) + 6 second shell (4.09 A)
+
+
+def _cell_cases():
+    from face_amd import systems
+    rng = np.random.default_rng(11)
+    tri = np.array([[9.0, 0.7, 0.0], [1.1, 8.4, 0.3], [-0.6, 0.9, 13.5]])
+    yield "liquid 1500", systems.liquid(1500, np.random.default_rng(5)), 5.0
+    yield "fcc 864 jittered", systems.fcc(4.09, 6, 0.1, np.random.default_rng(2)), 4.5
+    # exact lattice, rc on the second shell: every boundary decision is a tie of rounding
+    yield "fcc 500 exact, rc = a", systems.fcc(4.09, 5, 0.0, np.random.default_rng(0)), 4.09
+    yield "fcc 500 exact, rc = a / sqrt 2", systems.fcc(4.09, 5, 0.0, np.random.default_rng(0)), 4.09 / np.sqrt(2)
+    # triclinic, positions not wrapped (outside the cell, negative), 1 / 1 / 3 bins
+    pos = rng.random((300, 3)) @ tri + rng.normal(0, 6.0, (300, 3))
+    yield "triclinic unwrapped", {"pos": pos, "cell": tri, "pbc": np.ones(3, bool)}, 4.2
+    # thin cell: one axis shorter than rc (one bin, several images of the same pair)
+    thin = np.diag([14.0, 13.0, 3.1])
+    yield "thin", {"pos": rng.random((200, 3)) @ thin, "cell": thin, "pbc": np.ones(3, bool)}, 4.5
+    # atoms on bin edges and on the cell faces (fractional k / 6, 0, just under 1, just under 0)
+    L = 30.0
+    f = rng.integers(0, 6, (400, 3)) / 6.0
+    f[:20] = 0.0
+    f[20:40] = np.nextafter(1.0, 0.0)
+    f[40:60] = -np.nextafter(0.0, 1.0)
+    f += np.where(rng.random((400, 3)) < 0.5, 0.0, rng.normal(0, 0.02, (400, 3)))
+    yield "bin edges", {"pos": f * L, "cell": np.eye(3) * L, "pbc": np.ones(3, bool)}, 4.9
+
+
+@pytest.mark.parametrize("case", [c[0] for c in _cell_cases()])
+def test_cell_pair_list_equals_brute_force(case):
+    """The bin-candidate oracle (used for the 24k / 100k pair lists) gives exactly the
+    brute-force pairs, order and shifts."""
+    st, rc = {c[0]: c[1:] for c in _cell_cases()}[case]
+    a = pair_list(st["pos"], st["cell"], st["pbc"], rc)
+    b = pair_list_cells(st["pos"], st["cell"], st["pbc"], rc)
+    assert len(a[0]) > 0
+    for x, y in zip(a, b):
+        assert np.array_equal(x, y)
+
+
+def test_cell_pair_list_needs_full_pbc():
+    with pytest.raises(ValueError):
+        pair_list_cells(np.zeros((2, 3)), np.eye(3) * 10, (1, 0, 1), 4.0)
 
 
 # ----------------------------------------------------------------------------- model vs golden
