@@ -536,6 +536,86 @@ __global__ __launch_bounds__(256) void row_sum_kernel(const float* __restrict__ 
     if (tid == 0) out[k * ld_out] = part[0];
 }
 
+// ------------------------------------------------------------------ atom energies
+// e_at[a] = e0[a] + scale (e_1[a] + ...) added pass by pass, and E[s] = the sum of e_at over the
+// atoms of structure s (contiguous, [struct_ptr[s], struct_ptr[s+1])): one workgroup of 1024
+// threads per structure, each thread issuing the loads of 4 atoms and all passes before using
+// them (a single structure of 10^4-10^5 atoms is a few such rounds), then a fixed-order sum
+// (face/model.py:680-690).
+constexpr int kMaxEnergyTerms = 8;
+constexpr int kEnergyThreads = 1024, kEnergyUnroll = 4;
+struct EnergyTerms {
+    const float* e[kMaxEnergyTerms];
+    int64_t ld[kMaxEnergyTerms];
+    int n;
+};
+
+__global__ __launch_bounds__(kEnergyThreads) void atom_energy_fwd_kernel(const float* __restrict__ e0,
+                                                                         const float* __restrict__ scale,
+                                                                         EnergyTerms T,
+                                                                         const int32_t* __restrict__ struct_ptr,
+                                                                         float* __restrict__ e_at,
+                                                                         float* __restrict__ E) {
+    __shared__ float part[kEnergyThreads / kWave];
+    const int64_t k = blockIdx.x, beg = struct_ptr[k], end = struct_ptr[k + 1];
+    const int tid = threadIdx.x;
+    const float sc = *scale;
+    float s = 0.f;
+    for (int64_t a0 = beg + tid; a0 < end; a0 += kEnergyThreads * kEnergyUnroll) {
+        float v[kEnergyUnroll], x[kMaxEnergyTerms][kEnergyUnroll];
+#pragma unroll
+        for (int u = 0; u < kEnergyUnroll; ++u) {
+            const int64_t a = a0 + u * kEnergyThreads;
+            v[u] = a < end ? e0[a] : 0.f;
+#pragma unroll
+            for (int p = 0; p < kMaxEnergyTerms; ++p) x[p][u] = (p < T.n && a < end) ? T.e[p][a * T.ld[p]] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < kEnergyUnroll; ++u) {
+            const int64_t a = a0 + u * kEnergyThreads;
+#pragma unroll
+            for (int p = 0; p < kMaxEnergyTerms; ++p)
+                if (p < T.n) v[u] += sc * x[p][u];
+            if (a < end) {
+                e_at[a] = v[u];
+                s += v[u];
+            }
+        }
+    }
+#pragma unroll
+    for (int o = kWave / 2; o > 0; o >>= 1) s += __shfl_xor(s, o, kWave);
+    if ((tid & (kWave - 1)) == 0) part[tid / kWave] = s;
+    __syncthreads();
+    if (tid == 0) {
+        float t = 0.f;
+        for (int w = 0; w < kEnergyThreads / kWave; ++w) t += part[w];
+        E[k] = t;
+    }
+}
+
+// ge[a] = scale (gE[s] + g_at[a]) for the atoms a of structure s (either term may be absent)
+__global__ __launch_bounds__(kEnergyThreads) void atom_energy_bwd_kernel(const float* __restrict__ gE,
+                                                                         const float* __restrict__ g_at,
+                                                                         const float* __restrict__ scale,
+                                                                         const int32_t* __restrict__ struct_ptr,
+                                                                         float* __restrict__ ge) {
+    const int64_t k = blockIdx.x, beg = struct_ptr[k], end = struct_ptr[k + 1];
+    const float sc = *scale, gs = gE ? gE[k] : 0.f;
+    for (int64_t a0 = beg + threadIdx.x; a0 < end; a0 += kEnergyThreads * kEnergyUnroll) {
+        float x[kEnergyUnroll];
+#pragma unroll
+        for (int u = 0; u < kEnergyUnroll; ++u) {
+            const int64_t a = a0 + u * kEnergyThreads;
+            x[u] = (g_at && a < end) ? g_at[a] : 0.f;
+        }
+#pragma unroll
+        for (int u = 0; u < kEnergyUnroll; ++u) {
+            const int64_t a = a0 + u * kEnergyThreads;
+            if (a < end) ge[a] = sc * (gs + x[u]);
+        }
+    }
+}
+
 static unsigned blocks_for(int64_t n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace face
@@ -641,6 +721,36 @@ extern "C" int face_segment_sum(const float* g, int32_t ld_g, const int32_t* row
     else
         hipLaunchKernelGGL(segment_sum_kernel, dim3(blocks_for(N * F)), dim3(256), 0, (hipStream_t)stream, g, ld_g,
                            row_ptr, N, F, out, ld_out);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int face_atom_energy_fwd(const float* e0, const float* scale, const float* const* e, const int64_t* ld_e,
+                                    int32_t n_e, const int32_t* struct_ptr, int64_t nstr, float* e_at, float* E,
+                                    void* stream) {
+    if (nstr < 0 || n_e < 0 || n_e > kMaxEnergyTerms || (n_e > 0 && (!e || !ld_e))) return FACE_ERR_ARG;
+    if (nstr == 0) return 0;
+    if (!e0 || !scale || !struct_ptr || !e_at || !E) return FACE_ERR_ARG;
+    EnergyTerms T{};
+    T.n = n_e;
+    for (int p = 0; p < n_e; ++p) {
+        if (!e[p] || ld_e[p] < 1) return FACE_ERR_ARG;
+        T.e[p] = e[p];
+        T.ld[p] = ld_e[p];
+    }
+    hipLaunchKernelGGL(atom_energy_fwd_kernel, dim3((unsigned)nstr), dim3(kEnergyThreads), 0, (hipStream_t)stream, e0,
+                       scale, T, struct_ptr, e_at, E);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int face_atom_energy_bwd(const float* gE, const float* g_at, const float* scale, const int32_t* struct_ptr,
+                                    int64_t nstr, float* ge, void* stream) {
+    if (nstr < 0) return FACE_ERR_ARG;
+    if (nstr == 0) return 0;
+    if (!scale || !struct_ptr || !ge) return FACE_ERR_ARG;
+    hipLaunchKernelGGL(atom_energy_bwd_kernel, dim3((unsigned)nstr), dim3(kEnergyThreads), 0, (hipStream_t)stream, gE,
+                       g_at, scale, struct_ptr, ge);
     FACE_LAUNCH_CHECK();
     return 0;
 }

@@ -53,6 +53,8 @@ _SIGS = {
     "face_gather_rows": (ctypes.c_int, [P, I32, P, I64, I32, P, I32, P]),
     "face_gather_rows_bwd": (ctypes.c_int, [P, I32, P, P, I64, I32, P, I32, P]),
     "face_segment_sum": (ctypes.c_int, [P, I32, P, I64, I32, P, I32, P]),
+    "face_atom_energy_fwd": (ctypes.c_int, [P, P, P, P, I32, P, I64, P, P, P]),
+    "face_atom_energy_bwd": (ctypes.c_int, [P, P, P, P, I64, P, P]),
     "face_force_scatter": (ctypes.c_int, [P, P, P, I64, F32, P, P]),
     "face_edge_geom_bwd_seg": (ctypes.c_int, [P, P, P, P, P, I64, P, I32, F32, F32, P, P, P, P, P, P, P]),
     "face_force_scatter_rows": (ctypes.c_int, [P, P, P, I64, I32, F32, P, P]),
@@ -75,7 +77,7 @@ _SIGS = {
     "face_layer_norm_bwd": (ctypes.c_int, [P, P, I64, I32, P, P, P, P, P]),
 }
 
-ABI_VERSION = 18
+ABI_VERSION = 19
 
 
 class LinProblem(ctypes.Structure):

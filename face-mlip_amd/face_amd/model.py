@@ -370,10 +370,13 @@ class FactorBlock(nn.Module):
         allsets = sets + [A]
         # only P0 of rank 0 and P3, Q3 of rank 3 are used
         ws = [frozen(self.proj[l])[0][:(C, 3 * C, 3 * C, 2 * C)[l]] for l in range(4)]
+        feats_buf = None
         if C % 16 == 0:
             # proj over the concatenated moment sets as a sum of per-set products (no concat copy),
-            # all four ranks per launch, later sets accumulating in the epilogue
-            ys = list(ops.rank_proj(ws, allsets, acc))                           # (k_l, N, C | 3C | 3C | 2C)
+            # all four ranks per launch, later sets accumulating in the epilogue; P0 (rank 0) is
+            # written straight into the first C columns of the readout row
+            feats_buf = torch.empty(g.N, self.N_INV * C, device=h.device)
+            ys = list(ops.rank_proj(ws, allsets, acc, out0=feats_buf[:, :C]))   # (k_l, N, C | 3C | 3C | 2C)
         else:
             ys = []
             for l in range(4):
@@ -385,9 +388,9 @@ class FactorBlock(nn.Module):
                 ys.append(y.view(S[l].shape[0], S[l].shape[1], -1))
         if self.eq_out:
             feats, V, Ms = ops.node_features(ys[0], ys[1], ys[2], ys[3], self.vpath.detach(), self.mpath.detach(),
-                                             True, C)
+                                             True, C, feats_buf)
         else:
-            feats, V, Ms = ops.node_features(ys[0], ys[1], ys[2], ys[3], None, None, False, C)
+            feats, V, Ms = ops.node_features(ys[0], ys[1], ys[2], ys[3], None, None, False, C, feats_buf)
         nf = self.N_INV * C
         if READOUT_ROW_GEMM and C % 16 == 0 and nf <= 2048:
             # LayerNorm, the out MLP and the residual split on the row GEMM (four launches forward;
@@ -550,7 +553,7 @@ class FACE(nn.Module):
                               order, acc, last=t == nb - 1)
             sets.append(A)
             es.append(e)
-        E, e_at = ops.atom_energy(e0, self.scale, graph.struct_ptr, graph.batch, graph.nstr, es)
+        E, e_at = ops.atom_energy(e0, self.scale, graph.struct_ptr, graph.nstr, es)
         out = {"energy": E, "atom_energy": e_at}
         if forces:
             # forces = -dE/dpos directly: the backward is seeded with -1 per structure

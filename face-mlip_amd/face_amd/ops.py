@@ -182,17 +182,33 @@ def gather_receiver(X, graph):
     return out if X.dim() == 2 else out.view(graph.E, *shp[1:])
 
 
+# directional tables of at most this many bytes are read in place by the edge kernels
+DIR_PACK_MIN_BYTES = 4 << 20
+
+
 class DirTransport(torch.autograd.Function):
     """Directional edge features and transport moments from the node tables Vb (3, N, nt*Kd),
     Mb (6, N, nt*Kd) (component-major; channels [0, Kd) directional, [Kd, 2Kd) transport).
 
     d (E, 4Kd) = [u.V_j | u^T M_j u | u.V_i | u^T M_i u]          (face/model.py:474-493)
     D1 (3, N, B*2Kd), D2 (6, N, B*2Kd): sum_e phi[e, b] F(u, V_j, M_j)  (face/model.py:514-528)
-    One autograd node for both, so the tables' gradient is assembled in place (no slices). The
-    kernels read the tables node-major, packed as P (N, nt, 9, Kd) ([node][directional |
-    transport][V0..V2, M0..M5][channel]): a neighbour's 9 component rows of one part are 36 Kd
-    contiguous bytes instead of 9 rows each in its own cache line.
+    One autograd node for both, so the tables' gradient is assembled in place (no slices). Tables
+    larger than an L2 (DIR_PACK_MIN_BYTES) are read node-major, packed as P (N, nt, 9, Kd)
+    ([node][directional | transport][V0..V2, M0..M5][channel]): a neighbour's 9 component rows of
+    one part are 36 Kd contiguous bytes instead of 9 rows each in its own cache line; smaller ones
+    (held in L2 whatever the layout) are read where the linears wrote them, with no packing
+    copies either way.
     """
+
+    @staticmethod
+    def _tables(V, M, N, nt, Kd, packed, t):
+        """(V, v_sn, v_sq, M, m_sn, m_sq) pointers and strides of part t (0 directional, 1
+        transport): in the packed P (V is P, M unused) or in place in the (3|6, N, nt*Kd) tables."""
+        if packed:
+            base = ptr(V) + 4 * t * 9 * Kd
+            sn = nt * 9 * Kd
+            return base, sn, Kd, base + 4 * 3 * Kd, sn, Kd
+        return ptr(V) + 4 * t * Kd, nt * Kd, N * nt * Kd, ptr(M) + 4 * t * Kd, nt * Kd, N * nt * Kd
 
     @staticmethod
     def forward(ctx, Vb, Mb, phi, Y, graph, Kd, transport):
@@ -202,13 +218,19 @@ class DirTransport(torch.autograd.Function):
         dev = Vb.device
         st = _lib.stream_of(Vb)
         nt = Vb.shape[2] // Kd
-        P = torch.empty(N, nt, 9, Kd, device=dev)
-        P[:, :, :3].copy_(Vb.float().view(3, N, nt, Kd).permute(1, 2, 0, 3))
-        P[:, :, 3:].copy_(Mb.float().view(6, N, nt, Kd).permute(1, 2, 0, 3))
-        sn = nt * 9 * Kd
+        # tables that fit in an L2 are read in place (no packing copies); larger ones are packed
+        packed = 9 * N * nt * Kd * 4 > DIR_PACK_MIN_BYTES
+        if packed:
+            P = torch.empty(N, nt, 9, Kd, device=dev)
+            P[:, :, :3].copy_(Vb.float().view(3, N, nt, Kd).permute(1, 2, 0, 3))
+            P[:, :, 3:].copy_(Mb.float().view(6, N, nt, Kd).permute(1, 2, 0, 3))
+            tabs = (P, P)
+        else:
+            tabs = (Vb.contiguous().float(), Mb.contiguous().float())
+        tab = lambda t: DirTransport._tables(tabs[0], tabs[1], N, nt, Kd, packed, t)
         d = torch.empty(E, 4 * Kd, device=dev)
-        call("face_dir_feats_fwd", ptr(P), sn, Kd, ptr(P) + 4 * 3 * Kd, sn, Kd, Kd,
-             ptr(graph.recv), ptr(graph.col), ptr(Y), E, ptr(d), st, label="dir_fwd")
+        call("face_dir_feats_fwd", *tab(0), Kd, ptr(graph.recv), ptr(graph.col), ptr(Y), E, ptr(d), st,
+             label="dir_fwd")
         D1 = D2 = None
         phi_ = phi
         if transport:
@@ -216,27 +238,29 @@ class DirTransport(torch.autograd.Function):
             B = phi.shape[1]
             D1 = torch.empty(3, N, B * 2 * Kd, device=dev)
             D2 = torch.empty(6, N, B * 2 * Kd, device=dev)
-            pt = ptr(P) + 4 * 9 * Kd
-            call("face_transport_fwd", ptr(phi_), ld_phi, B, pt, sn, Kd, pt + 4 * 3 * Kd, sn, Kd, Kd, ptr(Y), 20,
+            call("face_transport_fwd", ptr(phi_), ld_phi, B, *tab(1), Kd, ptr(Y), 20,
                  ptr(graph.col), ptr(graph.row_ptr), N, 1.0, ptr(D1), ptr(D2), st, label="transport_fwd")
-        ctx.save_for_backward(P, phi_ if transport else torch.empty(0), Y)
-        ctx.graph, ctx.Kd, ctx.transport, ctx.nt = graph, Kd, transport, nt
+        ctx.save_for_backward(tabs[0], tabs[1] if not packed else torch.empty(0),
+                              phi_ if transport else torch.empty(0), Y)
+        ctx.graph, ctx.Kd, ctx.transport, ctx.nt, ctx.packed = graph, Kd, transport, nt, packed
         return d, D1, D2
 
     @staticmethod
     def backward(ctx, gd, gD1, gD2):
-        P, phi, Y = ctx.saved_tensors
-        g, Kd, nt = ctx.graph, ctx.Kd, ctx.nt
+        T0, T1, phi, Y = ctx.saved_tensors
+        g, Kd, nt, packed = ctx.graph, ctx.Kd, ctx.nt, ctx.packed
         N, E = g.N, g.E
-        dev = P.device
-        st = _lib.stream_of(P)
-        sn = nt * 9 * Kd
+        dev = T0.device
+        st = _lib.stream_of(T0)
+        tabs = (T0, T0) if packed else (T0, T1)
+        gtabs = (torch.empty_like(T0),) * 2 if packed else (torch.empty_like(T0), torch.empty_like(T1))
+        tab = lambda t: DirTransport._tables(tabs[0], tabs[1], N, nt, Kd, packed, t)
+        gtab = lambda t: DirTransport._tables(gtabs[0], gtabs[1], N, nt, Kd, packed, t)
         gd = torch.zeros(E, 4 * Kd, device=dev) if gd is None else gd.contiguous().float()
-        gP = torch.empty_like(P)
         gY = torch.empty_like(Y)
-        call("face_dir_feats_bwd", ptr(P), sn, Kd, ptr(P) + 4 * 3 * Kd, sn, Kd, Kd,
-             ptr(g.row_ptr), ptr(g.recv), ptr(g.col), ptr(g.rev), ptr(Y), ptr(gd), N, E, ptr(gP),
-             ptr(gP) + 4 * 3 * Kd, ptr(gY), st, label="dir_bwd")
+        g0 = gtab(0)
+        call("face_dir_feats_bwd", *tab(0), Kd, ptr(g.row_ptr), ptr(g.recv), ptr(g.col), ptr(g.rev), ptr(Y),
+             ptr(gd), N, E, g0[0], g0[3], ptr(gY), st, label="dir_bwd")
         dphi = None
         if ctx.transport:
             B = phi.shape[1]
@@ -245,10 +269,13 @@ class DirTransport(torch.autograd.Function):
             gD2 = torch.zeros(6, N, W, device=dev) if gD2 is None else gD2.contiguous().float()
             dphi = torch.empty(E, B, device=dev)
             dT = torch.empty(E, 9, Kd, device=dev)
-            pt, gt = ptr(P) + 4 * 9 * Kd, ptr(gP) + 4 * 9 * Kd
-            call("face_transport_bwd", ptr(phi), phi.stride(0), B, pt, sn, Kd, pt + 4 * 3 * Kd, sn, Kd, Kd, ptr(Y), 20,
+            g1 = gtab(1)
+            call("face_transport_bwd", ptr(phi), phi.stride(0), B, *tab(1), Kd, ptr(Y), 20,
                  ptr(g.col), ptr(g.row_ptr), ptr(g.rev), N, g.max_row, 1.0, ptr(gD1), ptr(gD2), ptr(dphi), B, ptr(dT),
-                 gt, gt + 4 * 3 * Kd, ptr(gY), st, label="transport_bwd")
+                 g1[0], g1[3], ptr(gY), st, label="transport_bwd")
+        if not packed:
+            return gtabs[0], gtabs[1], dphi, gY, None, None, None
+        gP = gtabs[0]
         gVb = gP[:, :, :3].permute(2, 0, 1, 3).reshape(3, N, nt * Kd)
         gMb = gP[:, :, 3:].permute(2, 0, 1, 3).reshape(6, N, nt * Kd)
         return gVb, gMb, dphi, gY, None, None, None
@@ -383,38 +410,45 @@ def readout_mlp(inv, h, W0a, W0b, b0, W1, b1, W2, b2, Wg=None, bg=None, last=Fal
 
 
 class AtomEnergy(torch.autograd.Function):
-    """Atom energies e_at = e0 + scale * sum_p e_p (N,) and their per-structure sums E (nstr,)
-    (face/model.py:689-690): one fused multiply-add per pass and one segment-sum launch (atoms of
-    a structure are contiguous); the backward gives every pass the same gradient scale * gE[batch].
-    e_p may be strided (N, 1) column views."""
+    """Atom energies e_at = e0 + scale * e_1 + scale * e_2 + ... (N,) and their per-structure sums
+    E (nstr,) (face/model.py:680-690) in one launch (atoms of a structure contiguous, ranges
+    struct_ptr); the backward gives every pass the same gradient scale * (gE[structure] + g_at),
+    again one launch. e_p may be strided (N, 1) column views."""
 
     @staticmethod
-    def forward(ctx, e0, scale, struct_ptr, batch, nstr, *es):
-        e_at = torch.addcmul(e0, scale, es[0].squeeze(-1))
-        for e in es[1:]:
-            e_at.addcmul_(scale, e.squeeze(-1))
-        E = torch.empty(nstr, 1, device=e_at.device)
-        call("face_segment_sum", ptr(e_at), 1, ptr(struct_ptr), nstr, 1, ptr(E), 1, _lib.stream_of(e_at))
-        ctx.save_for_backward(batch, scale)
-        ctx.n = len(es)
+    def forward(ctx, e0, scale, struct_ptr, nstr, *es):
+        _lib.require_gpu(e0, scale, *es)
+        N = e0.shape[0]
+        dev = e0.device
+        e0_ = e0.contiguous().float()
+        sc = scale.detach().float().contiguous().view(1)
+        cols = [e if (e.dtype == torch.float32 and e.dim() == 2 and e.stride(1) == 1) else e.float().view(N, 1)
+                for e in es]
+        e_at = torch.empty(N, device=dev)
+        E = torch.empty(nstr, device=dev)
+        call("face_atom_energy_fwd", ptr(e0_), ptr(sc), _lib.ptr_array(cols), _lib.i64_array([c.stride(0) for c in cols]),
+             len(cols), ptr(struct_ptr), nstr, ptr(e_at), ptr(E), _lib.stream_of(e0_), label="atom_energy")
+        ctx.save_for_backward(struct_ptr, sc)
+        ctx.n, ctx.N, ctx.nstr = len(es), N, nstr
         ctx.set_materialize_grads(False)                 # e_at is usually not differentiated
-        return E.view(nstr), e_at
+        return E, e_at
 
     @staticmethod
     def backward(ctx, gE, g_at):
-        batch, scale = ctx.saved_tensors
-        g = gE[batch] if gE is not None else None
-        if g_at is not None:
-            g = g_at if g is None else g + g_at
-        if g is None:
-            return (None,) * (5 + ctx.n)
-        ge = (g * scale).view(-1, 1)
-        return (None, None, None, None, None) + (ge,) * ctx.n
+        if gE is None and g_at is None:
+            return (None,) * (4 + ctx.n)
+        struct_ptr, sc = ctx.saved_tensors
+        gE_ = gE.contiguous().float() if gE is not None else None
+        ga_ = g_at.contiguous().float() if g_at is not None else None
+        ge = torch.empty(ctx.N, 1, device=sc.device)
+        call("face_atom_energy_bwd", ptr(gE_), ptr(ga_), ptr(sc), ptr(struct_ptr), ctx.nstr, ptr(ge),
+             _lib.stream_of(sc), label="atom_energy_bwd")
+        return (None, None, None, None) + (ge,) * ctx.n
 
 
-def atom_energy(e0, scale, struct_ptr, batch, nstr, es):
+def atom_energy(e0, scale, struct_ptr, nstr, es):
     """(E (nstr,), e_at (N,)); see AtomEnergy."""
-    return AtomEnergy.apply(e0, scale, struct_ptr, batch, nstr, *es)
+    return AtomEnergy.apply(e0, scale, struct_ptr, nstr, *es)
 
 
 class Readout(torch.autograd.Function):
@@ -987,14 +1021,15 @@ class NodeFeatures(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, y0, y1, y2, y3, a, b, eq, C):
+    def forward(ctx, y0, y1, y2, y3, a, b, eq, C, out):
         _lib.require_gpu(y0, y1, y2, y3)
         N = y1.shape[1]
         dev = y1.device
-        y0, y1, y2, y3 = [y.contiguous().float() for y in (y0, y1, y2, y3)]
+        y1, y2, y3 = [y.contiguous().float() for y in (y1, y2, y3)]
         ins = _pqs_views(y1, y2, y3, C)
-        feats = torch.empty(N, 9 * C, device=dev)
-        feats[:, :C] = y0[0, :, :C]
+        feats = out[0] if out else torch.empty(N, 9 * C, device=dev)
+        if not (y0.data_ptr() == feats.data_ptr() and y0.stride(1) == feats.stride(0) and y0.shape[2] == C):
+            feats[:, :C] = y0[0, :, :C]                 # P0 not already written in place
         inv_view = feats[:, C:].view(N, 8, C).transpose(1, 2)                   # (N,C,8)
         st = sum((_s3(t) for t in ins), [])
         V = Ms = None
@@ -1009,16 +1044,16 @@ class NodeFeatures(torch.autograd.Function):
              _lib.i64_array(_s3(inv_view)), ptr(V), _lib.i64_array(_s3(V.permute(1, 2, 0)) if eq else z3),
              ptr(Ms), _lib.i64_array(_s3(Ms.permute(1, 2, 0)) if eq else z3), 1, N, C, int(bool(eq)),
              _lib.stream_of(y1), label="node_fwd")
-        ctx.save_for_backward(y0, y1, y2, y3, a_ if eq else torch.empty(0), b_ if eq else torch.empty(0))
-        ctx.eq, ctx.C = eq, C
+        ctx.save_for_backward(y1, y2, y3, a_ if eq else torch.empty(0), b_ if eq else torch.empty(0))
+        ctx.eq, ctx.C, ctx.y0_shape = eq, C, y0.shape
         if eq:
             return feats, V, Ms
         return feats, None, None
 
     @staticmethod
     def backward(ctx, gfeats, gV, gMs):
-        y0, y1, y2, y3, a, b = ctx.saved_tensors
-        C, eq = ctx.C, ctx.eq
+        y1, y2, y3, a, b = ctx.saved_tensors
+        C, eq, y0_shape = ctx.C, ctx.eq, ctx.y0_shape
         N = y1.shape[1]
         dev = y1.device
         ins = _pqs_views(y1, y2, y3, C)
@@ -1037,10 +1072,10 @@ class NodeFeatures(torch.autograd.Function):
         # P0 was copied into the readout row: its gradient is that row's first C columns, handed
         # on as a strided view when y0 has exactly C channels (the projection backward reads rows
         # at any stride)
-        if gfeats is not None and y0.shape[2] == C:
+        if gfeats is not None and y0_shape[2] == C:
             dy0 = gfeats[:, :C].unsqueeze(0)
         else:
-            dy0 = torch.zeros_like(y0)
+            dy0 = torch.zeros(y0_shape, device=dev)
             if gfeats is not None:
                 dy0[0, :, :C] = gfeats[:, :C]
         need_ab = eq and (ctx.needs_input_grad[4] or ctx.needs_input_grad[5])
@@ -1058,11 +1093,13 @@ class NodeFeatures(torch.autograd.Function):
              int(bool(eq)), _lib.stream_of(y1), label="node_bwd")
         ga = da.sum(0).t() if need_ab else None
         gb = db.sum(0).t() if need_ab else None
-        return dy0, dy1, dy2, dy3, ga, gb, None, None
+        return dy0, dy1, dy2, dy3, ga, gb, None, None, None
 
 
-def node_features(y0, y1, y2, y3, a, b, eq, C):
-    return NodeFeatures.apply(y0, y1, y2, y3, a, b, eq, C)
+def node_features(y0, y1, y2, y3, a, b, eq, C, out=None):
+    """(feats, V | None, Ms | None); out: an (N, 9C) buffer for feats, whose first C columns may
+    already hold P0 (y0 a view of them, as rank_proj writes it with out0)."""
+    return NodeFeatures.apply(y0, y1, y2, y3, a, b, eq, C, (out,) if out is not None else ())
 
 
 # ----------------------------------------------------------------------------- row-block linear layers
@@ -1189,14 +1226,16 @@ class RankProj(torch.autograd.Function):
     that share a set through its SetGrad, when given). Weights receive no gradient."""
 
     @staticmethod
-    def forward(ctx, ws, n_sets, acc, *S):
+    def forward(ctx, ws, n_sets, acc, out0, *S):
         C = S[0].shape[-1]
         N = S[0].shape[1]
         dev = S[0].device
         sets = [S[4 * s:4 * s + 4] for s in range(n_sets)]
         ys = [torch.empty(sets[0][l].shape[0], N, w.shape[0], device=dev) for l, w in enumerate(ws)]
+        if out0:
+            ys[0] = out0[0].unsqueeze(0)                 # rank 0 (one monomial) into the caller's rows
         for s, S_s in enumerate(sets):
-            rows_linear([(S_s[l].reshape(-1, C), ws[l][:, s * C:(s + 1) * C], ys[l].view(-1, ws[l].shape[0]), 0,
+            rows_linear([(S_s[l].reshape(-1, C), ws[l][:, s * C:(s + 1) * C], ys[l].reshape(-1, ws[l].shape[0]), 0,
                           1.0 if s else 0.0) for l in range(4)], label="proj_fwd")
         slots = None
         if acc is not None:
@@ -1222,7 +1261,7 @@ class RankProj(torch.autograd.Function):
               for g, w, sh in zip(gy, ws, ctx.shapes[:4])]
         grads = []
         for s in range(ctx.n_sets):
-            need = [ctx.needs_input_grad[3 + 4 * s + l] for l in range(4)]
+            need = [ctx.needs_input_grad[4 + 4 * s + l] for l in range(4)]
             slot = ctx.slots[s] if ctx.slots is not None else None
             if slot is not None and slot.g is not None:
                 d, beta, out = slot.g, 1.0, [None] * 4
@@ -1239,11 +1278,12 @@ class RankProj(torch.autograd.Function):
                 if slot.arrived == slot.readers:
                     slot.g, slot.arrived = None, 0
             grads += out
-        return (None, None, None, *grads)
+        return (None, None, None, None, *grads)
 
 
-def rank_proj(ws, sets, acc=None):
+def rank_proj(ws, sets, acc=None, out0=None):
     """ws: 4 frozen proj weights (n_l, n_sets C); sets: list of 4-tuples of (k_l, N, C) moments;
     acc: a dict shared by the rank_proj calls of one forward whose sets nothing else reads (their
-    gradients then accumulate in place, see SetGrad), or None."""
-    return RankProj.apply(ws, len(sets), acc, *[t for S in sets for t in S])
+    gradients then accumulate in place, see SetGrad), or None; out0: (N, n_0) rows (unit column
+    stride, any row stride) that receive the rank-0 output, returned as a (1, N, n_0) view."""
+    return RankProj.apply(ws, len(sets), acc, (out0,) if out0 is not None else (), *[t for S in sets for t in S])

@@ -30,6 +30,7 @@
  *   face/model.py:498-533,537-544 mix / tmix / proj (+ elem_scale)   -> face_rows_linear
  *   face/model.py:474-493        directional edge features        -> face_dir_feats_fwd / _bwd
  *   face/model.py:514-533        transport sums + transport map   -> face_transport_fwd / _bwd
+ *   face/model.py:680-690        atom energies + per-structure sum -> face_atom_energy_fwd / _bwd
  *   face/model.py:670,464,692-694 index_select gathers and their index_add backward
  *                                                                  -> face_gather_rows, face_gather_rows_bwd,
  *                                                                     face_force_scatter
@@ -429,6 +430,17 @@ int face_gather_rows_bwd(const float* g, int32_t ld_g, const int32_t* row_ptr, c
 /* Row sums: out[k, :] = sum_{e in row k} g[e, :]. */
 int face_segment_sum(const float* g, int32_t ld_g, const int32_t* row_ptr, int64_t N, int32_t F, float* out,
                      int32_t ld_out, void* stream);
+/* Atom energies and their per-structure sums (replaces e_at = E0[z] + sum_p scale * e_p and the
+ * index_add over batch, face/model.py:680-690): e_at[a] = e0[a] + scale[0] * e_p[a * ld_e[p]],
+ * added pass by pass over the n_e (<= 8) passes (host arrays e, ld_e of device pointers / strides),
+ * and E[s] = sum of e_at over the atoms [struct_ptr[s], struct_ptr[s+1]) of structure s (atoms of
+ * a structure contiguous; fixed summation order). scale is a device scalar.                */
+int face_atom_energy_fwd(const float* e0, const float* scale, const float* const* e, const int64_t* ld_e,
+                         int32_t n_e, const int32_t* struct_ptr, int64_t nstr, float* e_at, float* E, void* stream);
+/* Backward: ge[a] = scale[0] * (gE[s] + g_at[a]) for the atoms a of structure s, the gradient of
+ * every pass's e_p; gE (nstr) or g_at (N) may be NULL (zero).                               */
+int face_atom_energy_bwd(const float* gE, const float* g_at, const float* scale, const int32_t* struct_ptr,
+                         int64_t nstr, float* ge, void* stream);
 /* dE/dpos from dE/dvec (vec_e = pos[col e] - pos[i] + shift): grad[k] = sum_{e in row k} (gvec[rev e] - gvec[e]).
  * Writes grad (N,3) (forces are its negative: sign = -1 writes -grad). */
 int face_force_scatter(const float* gvec, const int32_t* row_ptr, const int32_t* rev, int64_t N, float sign,

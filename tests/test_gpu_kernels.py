@@ -510,13 +510,16 @@ def test_radial_spline_order_is_a_cell_sorted_permutation(P, G, F, nb, E):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("packed", [False, True])
 @pytest.mark.parametrize("Kd,B,transport", [(16, 16, True), (4, 8, True), (5, 4, False), (16, 16, False)])
-def test_dir_transport_and_gradients(Kd, B, transport):
+def test_dir_transport_and_gradients(Kd, B, transport, packed, monkeypatch):
     """Directional features d = [u.V_j, u^T M_j u, u.V_i, u^T M_i u] (face/model.py:474-493) and the
     transport sums D1 = [sum phi V, sum phi M u], D2 = [sum phi M, sum phi sym(u V)] (face/model.py:
-    514-528) vs gathered einsums and the oracle's explicit per-edge transport tensors."""
+    514-528) vs gathered einsums and the oracle's explicit per-edge transport tensors, with the
+    tables read in place and packed node-major."""
     from face_amd import ops
-    say("dir/transport", Kd, B, transport)
+    monkeypatch.setattr(ops, "DIR_PACK_MIN_BYTES", 0 if packed else 1 << 40)
+    say("dir/transport", Kd, B, transport, "packed" if packed else "in place")
     g = _G(37, 300, Kd + 10)
     counts = g.counts
     E = sum(counts)
@@ -896,19 +899,25 @@ def test_scaled_mix_forward_backward(transport, Cin):
     assert max(errs) < 1e-5, errs
 
 
-@pytest.mark.parametrize("n_sets,C", [(1, 160), (2, 160), (2, 96), (3, 32)])
-def test_rank_proj_forward_backward(n_sets, C):
+@pytest.mark.parametrize("n_sets,C,in_row", [(1, 160, False), (2, 160, False), (2, 96, False), (3, 32, False),
+                                             (2, 96, True)])
+def test_rank_proj_forward_backward(n_sets, C, in_row):
     """proj of the concatenated moment sets for the four ranks (face/model.py:537-544) as one launch
     per set, with the row-sliced weights the node algebra uses (P0 | PQS | PQS | PQ), and the
-    sets' gradients, vs torch fp64 autograd."""
+    sets' gradients, vs torch fp64 autograd; in_row: rank 0 written into the first C columns of a
+    wider row buffer (as for the readout row), the other columns left as they were."""
     from face_amd import ops
-    say("rank proj", n_sets, C)
+    say("rank proj", n_sets, C, in_row)
     torch.manual_seed(n_sets * C)
     N = 613
     full = [torch.randn(3 * C, n_sets * C, device=DEV) / C ** 0.5 for _ in range(4)]
     ws = [w[:n] for w, n in zip(full, (C, 3 * C, 3 * C, 2 * C))]
     sets = [[torch.randn(k, N, C, device=DEV, requires_grad=True) for k in (1, 3, 6, 10)] for _ in range(n_sets)]
-    ys = ops.rank_proj(ws, sets)
+    buf = torch.full((N, 9 * C), 7.0, device=DEV) if in_row else None
+    ys = ops.rank_proj(ws, sets, out0=buf[:, :C] if in_row else None)
+    if in_row:
+        assert ys[0].data_ptr() == buf.data_ptr() and ys[0].stride(1) == 9 * C
+        assert (buf[:, C:] == 7.0).all()
     G = [torch.randn_like(y) for y in ys]
     flat = [t for S in sets for t in S]
     gr = torch.autograd.grad(sum((y * g).sum() for y, g in zip(ys, G)), flat)
@@ -973,3 +982,36 @@ def test_density_mix_fused_matches_reference(gathered, K, C, transport):
     # bitwise reproducible (fixed summation order)
     A3 = ops.density_mix(s_tab, grp, wm, wmt, wt, D1, D2, phi, msg, Y, g.G, gathered)
     assert all(torch.equal(a, b) for a, b in zip(A, A3))
+
+
+@pytest.mark.parametrize("with_at", [False, True])
+def test_atom_energy_matches_index_add(with_at):
+    """Atom energies e0 + scale * e_p added pass by pass and their per-structure sums (face/model.py:
+    680-690) against index_add, ragged structures (one of a single atom) and strided (N, 1) column
+    views; the backward against autograd through the torch expression."""
+    from face_amd import ops
+    say("atom energy", with_at)
+    torch.manual_seed(3)
+    sizes = [5, 300, 1, 700, 33, 260]
+    N, nstr = sum(sizes), len(sizes)
+    batch = torch.repeat_interleave(torch.arange(nstr), torch.tensor(sizes)).to(DEV)
+    sp = torch.tensor([0] + list(np.cumsum(sizes)), dtype=torch.int32, device=DEV)
+    e0 = torch.randn(N, device=DEV)
+    scale = torch.tensor(0.7, device=DEV)
+    rows = [torch.randn(N, w, device=DEV, requires_grad=True) for w in (1, 17, 9)]
+    es = [r[:, :1] for r in rows]
+    E, e_at = ops.atom_energy(e0, scale, sp, nstr, es)
+    ref_at = e0.clone()
+    for e in es:
+        ref_at = ref_at + scale * e.squeeze(-1)
+    ref_E = torch.zeros(nstr, device=DEV).index_add(0, batch, ref_at)
+    assert torch.allclose(e_at, ref_at, rtol=1e-6, atol=1e-6)
+    assert torch.allclose(E, ref_E, rtol=1e-5, atol=1e-4)
+    gE = torch.randn(nstr, device=DEV)
+    g_at = torch.randn(N, device=DEV) if with_at else None
+    outs, gouts = ([E, e_at], [gE, g_at]) if with_at else ([E], [gE])
+    got = torch.autograd.grad(outs, rows, gouts)
+    routs = [ref_E, ref_at] if with_at else [ref_E]
+    want = torch.autograd.grad(routs, rows, gouts)
+    for a, b in zip(got, want):
+        assert torch.allclose(a, b, rtol=1e-6, atol=1e-6)
