@@ -22,6 +22,23 @@ struct RadialWeights {
     const float *w_in, *b_in, *pair_tab, *w1, *b1, *w_phi, *b_phi;
 };
 
+// The passes of one launch: each set is one pass's weights and its outputs (forward) or upstream
+// and input gradients (backward) over the same edges (rb, pair, env shared); workgroups
+// [k * blocks_per_set, (k + 1) * blocks_per_set) serve set k, so independent passes share a
+// launch (at small edge counts one pass fills about one wave per SIMD).
+constexpr int kRadMaxSets = 4;
+struct RadialSets {
+    RadialWeights W[kRadMaxSets];
+    float* h2[kRadMaxSets];
+    float* phi[kRadMaxSets];
+    const float* gh2[kRadMaxSets];
+    const float* gphi[kRadMaxSets];
+    const float* gphi2[kRadMaxSets];
+    float* grb[kRadMaxSets];
+    float* genv[kRadMaxSets];
+    int n, blocks_per_set;
+};
+
 // sigmoid with the hardware exp2 and reciprocal (about 1 ulp each): the IEEE expf and divide
 // sequences dominated the instruction count of the radial kernels
 __device__ __forceinline__ float sigmoidf_(float x) {
@@ -161,17 +178,21 @@ __device__ __forceinline__ v4f load_cols(const float* row, int c0, int n) {
 template <int HB, int BB>
 __global__ __launch_bounds__(kRadWaves * kWave) void radial_fwd_kernel(
     const float* __restrict__ rb, int ld_rb, int nbasis, const int32_t* __restrict__ pair,
-    const float* __restrict__ env, int64_t E, RadialWeights W, int n_pair, int B, float* __restrict__ h2, int ld_h2,
-    float* __restrict__ phi, int ld_phi, int tiles_per_wave) {
+    const float* __restrict__ env, int64_t E, RadialSets S, int n_pair, int B, int ld_h2, int ld_phi,
+    int tiles_per_wave) {
     extern __shared__ float lds[];
     constexpr int H = 16 * HB;
+    const int set = blockIdx.x / S.blocks_per_set;
+    const int64_t bx = blockIdx.x - (int64_t)set * S.blocks_per_set;
+    float* __restrict__ h2 = S.h2[set];
+    float* __restrict__ phi = S.phi[set];
     const RadialLds L(H, BB, n_pair);
-    radial_stage(lds, L, W, H, BB, nbasis, n_pair, B);
+    radial_stage(lds, L, S.W[set], H, BB, nbasis, n_pair, B);
     __syncthreads();
     const int lane = threadIdx.x & (kWave - 1);
     const int j = lane & 15, q = lane >> 4;
     const int nkb = (nbasis + 3) >> 2;
-    const int64_t wave = (int64_t)blockIdx.x * kRadWaves + threadIdx.x / kWave;
+    const int64_t wave = bx * kRadWaves + threadIdx.x / kWave;
     for (int s = 0; s < tiles_per_wave; ++s) {
         const int64_t t0 = (wave * tiles_per_wave + s) * 16;
         if (t0 >= E) break;                            // uniform per wave
@@ -199,18 +220,24 @@ __global__ __launch_bounds__(kRadWaves * kWave) void radial_fwd_kernel(
 template <int HB, int BB>
 __global__ __launch_bounds__(kRadWaves * kWave) __attribute__((amdgpu_waves_per_eu(3))) void radial_bwd_kernel(
     const float* __restrict__ rb, int ld_rb, int nbasis, const int32_t* __restrict__ pair,
-    const float* __restrict__ env, int64_t E, RadialWeights W, int n_pair, int B, const float* __restrict__ gh2,
-    int ld_gh2, const float* __restrict__ gphi, const float* __restrict__ gphi2, int ld_gphi,
-    float* __restrict__ grb, int ld_grb, float* __restrict__ genv, int tiles_per_wave) {
+    const float* __restrict__ env, int64_t E, RadialSets S, int n_pair, int B, int ld_gh2, int ld_gphi, int ld_grb,
+    int tiles_per_wave) {
     extern __shared__ float lds[];
     constexpr int H = 16 * HB;
+    const int set = blockIdx.x / S.blocks_per_set;
+    const int64_t bx = blockIdx.x - (int64_t)set * S.blocks_per_set;
+    const float* __restrict__ gh2 = S.gh2[set];
+    const float* __restrict__ gphi = S.gphi[set];
+    const float* __restrict__ gphi2 = S.gphi2[set];
+    float* __restrict__ grb = S.grb[set];
+    float* __restrict__ genv = S.genv[set];
     const RadialLds L(H, BB, n_pair);
-    radial_stage(lds, L, W, H, BB, nbasis, n_pair, B);
+    radial_stage(lds, L, S.W[set], H, BB, nbasis, n_pair, B);
     __syncthreads();
     const int lane = threadIdx.x & (kWave - 1);
     const int j = lane & 15, q = lane >> 4;
     const int nkb = (nbasis + 3) >> 2;
-    const int64_t wave = (int64_t)blockIdx.x * kRadWaves + threadIdx.x / kWave;
+    const int64_t wave = bx * kRadWaves + threadIdx.x / kWave;
     const v4f z4 = {0.f, 0.f, 0.f, 0.f};
     for (int s = 0; s < tiles_per_wave; ++s) {
         const int64_t t0 = (wave * tiles_per_wave + s) * 16;
@@ -691,7 +718,8 @@ using namespace face;
     do {                                                                                                \
         const int hb_ = H / 16, bb_ = (B + 15) / 16;                                                    \
         const int64_t waves_ = ((E + 15) / 16 + tpw - 1) / tpw;                                         \
-        const dim3 grid_((unsigned)((waves_ + kRadWaves - 1) / kRadWaves)), block_(kRadWaves * kWave);   \
+        S.blocks_per_set = (int)((waves_ + kRadWaves - 1) / kRadWaves);                                 \
+        const dim3 grid_((unsigned)((int64_t)S.blocks_per_set * S.n)), block_(kRadWaves * kWave);        \
         const hipStream_t st_ = (hipStream_t)stream;                                                    \
         switch (hb_ * 10 + bb_) {                                                                       \
             case 11: hipLaunchKernelGGL((KERNEL<1, 1>), grid_, block_, lds, st_, __VA_ARGS__); break;   \
@@ -708,23 +736,59 @@ using namespace face;
         }                                                                                               \
     } while (0)
 
+static bool radial_sets_ok(const float* rb, int ld_rb, int nbasis, const int32_t* pair, int64_t E, int n_sets,
+                           const RadialSets& S, int n_pair, int H, int B) {
+    if (n_sets < 1 || n_sets > kRadMaxSets) return false;
+    for (int k = 0; k < n_sets; ++k)
+        if (!radial_args_ok(rb, ld_rb, nbasis, pair, E, S.W[k], n_pair, H, B)) return false;
+    return true;
+}
+
+static int radial_fwd_launch(const float* rb, int32_t ld_rb, int32_t n_basis, const int32_t* pair, const float* env,
+                             int64_t E, RadialSets& S, int32_t n_pair, int32_t H, int32_t B, int32_t ld_h2,
+                             int32_t ld_phi, void* stream) {
+    if (!radial_sets_ok(rb, ld_rb, n_basis, pair, E, S.n, S, n_pair, H, B) || ld_phi < B) return FACE_ERR_ARG;
+    for (int k = 0; k < S.n; ++k)
+        if ((E > 0 && !S.phi[k]) || (S.h2[k] && (ld_h2 < H || ld_h2 % 4 || ((uintptr_t)S.h2[k] & 15))))
+            return FACE_ERR_ARG;
+    if (E == 0) return 0;
+    const size_t lds = radial_lds_bytes(H, B, n_pair);
+    if (lds > 65536) return FACE_ERR_UNSUPPORTED;
+    const int tpw = radial_tiles_per_wave(E);
+    FACE_RADIAL_DISPATCH(radial_fwd_kernel, rb, ld_rb, n_basis, pair, env, E, S, n_pair, B, ld_h2, ld_phi, tpw);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+static int radial_bwd_launch(const float* rb, int32_t ld_rb, int32_t n_basis, const int32_t* pair, const float* env,
+                             int64_t E, RadialSets& S, int32_t n_pair, int32_t H, int32_t B, int32_t ld_gh2,
+                             int32_t ld_gphi, int32_t ld_grb, void* stream) {
+    if (!radial_sets_ok(rb, ld_rb, n_basis, pair, E, S.n, S, n_pair, H, B) || ld_gphi < B) return FACE_ERR_ARG;
+    for (int k = 0; k < S.n; ++k)
+        if ((E > 0 && !S.gphi[k]) || (S.gh2[k] && (ld_gh2 < H || ld_gh2 % 4 || ((uintptr_t)S.gh2[k] & 15))) ||
+            (S.grb[k] && ld_grb < n_basis))
+            return FACE_ERR_ARG;
+    if (E == 0) return 0;
+    const size_t lds = radial_lds_bytes(H, B, n_pair);
+    if (lds > 65536) return FACE_ERR_UNSUPPORTED;
+    const int tpw = radial_tiles_per_wave(E);
+    FACE_RADIAL_DISPATCH(radial_bwd_kernel, rb, ld_rb, n_basis, pair, env, E, S, n_pair, B, ld_gh2, ld_gphi, ld_grb,
+                         tpw);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
 extern "C" int face_radial_fwd(const float* rb, int32_t ld_rb, int32_t n_basis, const int32_t* pair,
                                const float* env, int64_t E, const float* w_in, const float* b_in,
                                const float* pair_tab, int32_t n_pair, int32_t H, const float* w1, const float* b1,
                                const float* w_phi, const float* b_phi, int32_t B, float* h2, int32_t ld_h2,
                                float* phi, int32_t ld_phi, void* stream) {
-    const RadialWeights W{w_in, b_in, pair_tab, w1, b1, w_phi, b_phi};
-    if (!radial_args_ok(rb, ld_rb, n_basis, pair, E, W, n_pair, H, B) || ld_phi < B || (E > 0 && !phi) ||
-        (h2 && (ld_h2 < H || ld_h2 % 4 || ((uintptr_t)h2 & 15))))
-        return FACE_ERR_ARG;
-    if (E == 0) return 0;
-    const size_t lds = radial_lds_bytes(H, B, n_pair);
-    if (lds > 65536) return FACE_ERR_UNSUPPORTED;
-    const int tpw = radial_tiles_per_wave(E);
-    FACE_RADIAL_DISPATCH(radial_fwd_kernel, rb, ld_rb, n_basis, pair, env, E, W, n_pair, B, h2, ld_h2, phi, ld_phi,
-                         tpw);
-    FACE_LAUNCH_CHECK();
-    return 0;
+    RadialSets S{};
+    S.n = 1;
+    S.W[0] = RadialWeights{w_in, b_in, pair_tab, w1, b1, w_phi, b_phi};
+    S.h2[0] = h2;
+    S.phi[0] = phi;
+    return radial_fwd_launch(rb, ld_rb, n_basis, pair, env, E, S, n_pair, H, B, ld_h2, ld_phi, stream);
 }
 
 extern "C" int face_radial_bwd(const float* rb, int32_t ld_rb, int32_t n_basis, const int32_t* pair,
@@ -733,18 +797,55 @@ extern "C" int face_radial_bwd(const float* rb, int32_t ld_rb, int32_t n_basis, 
                                const float* w_phi, const float* b_phi, int32_t B, const float* gh2, int32_t ld_gh2,
                                const float* gphi, const float* gphi2, int32_t ld_gphi, float* grb, int32_t ld_grb,
                                float* genv, void* stream) {
-    const RadialWeights W{w_in, b_in, pair_tab, w1, b1, w_phi, b_phi};
-    if (!radial_args_ok(rb, ld_rb, n_basis, pair, E, W, n_pair, H, B) || (E > 0 && !gphi) || ld_gphi < B ||
-        (gh2 && (ld_gh2 < H || ld_gh2 % 4 || ((uintptr_t)gh2 & 15))) || (grb && ld_grb < n_basis))
-        return FACE_ERR_ARG;
-    if (E == 0) return 0;
-    const size_t lds = radial_lds_bytes(H, B, n_pair);
-    if (lds > 65536) return FACE_ERR_UNSUPPORTED;
-    const int tpw = radial_tiles_per_wave(E);
-    FACE_RADIAL_DISPATCH(radial_bwd_kernel, rb, ld_rb, n_basis, pair, env, E, W, n_pair, B, gh2, ld_gh2, gphi,
-                         gphi2, ld_gphi, grb, ld_grb, genv, tpw);
-    FACE_LAUNCH_CHECK();
-    return 0;
+    RadialSets S{};
+    S.n = 1;
+    S.W[0] = RadialWeights{w_in, b_in, pair_tab, w1, b1, w_phi, b_phi};
+    S.gh2[0] = gh2;
+    S.gphi[0] = gphi;
+    S.gphi2[0] = gphi2;
+    S.grb[0] = grb;
+    S.genv[0] = genv;
+    return radial_bwd_launch(rb, ld_rb, n_basis, pair, env, E, S, n_pair, H, B, ld_gh2, ld_gphi, ld_grb, stream);
+}
+
+// weights of set k from the host arrays (w[k * 7 + 0..6] = w_in, b_in, pair_tab, w1, b1, w_phi, b_phi)
+static bool radial_sets_from(int32_t n_sets, const float* const* w, RadialSets& S) {
+    if (n_sets < 1 || n_sets > kRadMaxSets || !w) return false;
+    S.n = n_sets;
+    for (int k = 0; k < n_sets; ++k)
+        S.W[k] = RadialWeights{w[7 * k], w[7 * k + 1], w[7 * k + 2], w[7 * k + 3], w[7 * k + 4], w[7 * k + 5],
+                               w[7 * k + 6]};
+    return true;
+}
+
+extern "C" int face_radial_fwd_sets(const float* rb, int32_t ld_rb, int32_t n_basis, const int32_t* pair,
+                                    const float* env, int64_t E, int32_t n_sets, const float* const* weights,
+                                    int32_t n_pair, int32_t H, int32_t B, float* const* h2, int32_t ld_h2,
+                                    float* const* phi, int32_t ld_phi, void* stream) {
+    RadialSets S{};
+    if (!radial_sets_from(n_sets, weights, S) || !phi) return FACE_ERR_ARG;
+    for (int k = 0; k < n_sets; ++k) {
+        S.h2[k] = h2 ? h2[k] : nullptr;
+        S.phi[k] = phi[k];
+    }
+    return radial_fwd_launch(rb, ld_rb, n_basis, pair, env, E, S, n_pair, H, B, ld_h2, ld_phi, stream);
+}
+
+extern "C" int face_radial_bwd_sets(const float* rb, int32_t ld_rb, int32_t n_basis, const int32_t* pair,
+                                    const float* env, int64_t E, int32_t n_sets, const float* const* weights,
+                                    int32_t n_pair, int32_t H, int32_t B, const float* const* gh2, int32_t ld_gh2,
+                                    const float* const* gphi, const float* const* gphi2, int32_t ld_gphi,
+                                    float* const* grb, int32_t ld_grb, float* const* genv, void* stream) {
+    RadialSets S{};
+    if (!radial_sets_from(n_sets, weights, S) || !gphi) return FACE_ERR_ARG;
+    for (int k = 0; k < n_sets; ++k) {
+        S.gh2[k] = gh2 ? gh2[k] : nullptr;
+        S.gphi[k] = gphi[k];
+        S.gphi2[k] = gphi2 ? gphi2[k] : nullptr;
+        S.grb[k] = grb ? grb[k] : nullptr;
+        S.genv[k] = genv ? genv[k] : nullptr;
+    }
+    return radial_bwd_launch(rb, ld_rb, n_basis, pair, env, E, S, n_pair, H, B, ld_gh2, ld_gphi, ld_grb, stream);
 }
 
 extern "C" int face_radial_spline_fwd(const float* r, const int32_t* pair, int64_t E, const float* T, const float* dT,

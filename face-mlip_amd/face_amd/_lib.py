@@ -63,6 +63,9 @@ _SIGS = {
     "face_radial_fwd": (ctypes.c_int, [P, I32, I32, P, P, I64, P, P, P, I32, I32, P, P, P, P, I32, P, I32, P, I32, P]),
     "face_radial_bwd": (ctypes.c_int, [P, I32, I32, P, P, I64, P, P, P, I32, I32, P, P, P, P, I32, P, I32, P, P, I32,
                                        P, I32, P, P]),
+    "face_radial_fwd_sets": (ctypes.c_int, [P, I32, I32, P, P, I64, I32, P, I32, I32, I32, P, I32, P, I32, P]),
+    "face_radial_bwd_sets": (ctypes.c_int, [P, I32, I32, P, P, I64, I32, P, I32, I32, I32, P, I32, P, P, I32, P, I32,
+                                            P, P]),
     "face_radial_spline_fwd": (ctypes.c_int, [P, P, I64, P, P, I32, I32, I32, F32, P, I32, P, P, I32, P, I32, P]),
     "face_radial_spline_bwd": (ctypes.c_int, [P, P, I64, P, P, I32, I32, I32, F32, P, I32, P, P, I32, P, I32, P,
                                               P, P]),
@@ -77,7 +80,7 @@ _SIGS = {
     "face_layer_norm_bwd": (ctypes.c_int, [P, P, I64, I32, P, P, P, P, P]),
 }
 
-ABI_VERSION = 19
+ABI_VERSION = 20
 
 
 class LinProblem(ctypes.Structure):

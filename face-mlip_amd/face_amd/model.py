@@ -230,10 +230,19 @@ class FactorBlock(nn.Module):
             self.tmix3 = nn.Linear(B * 2 * K_dir, C, bias=False)
 
     # ------------------------------------------------------------------ moments
-    def moments(self, h, rb, r, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g, order=None):
+    def radial_weights(self):
+        """(w_in, b_in, pair_tab, w1, b1, w_phi, b_phi) of the fused radial MLP: the phi columns of
+        the last radial layer (its CP columns are a GEMM on h2)."""
+        Wi, bi = frozen(self.rad_in)
+        W1, b1 = frozen(self.radial[0])
+        W2, b2 = frozen(self.radial[2])
+        return Wi, bi, self.pair.weight.detach(), W1, b1, W2[:self.B], b2[:self.B]
+
+    def moments(self, h, rb, r, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g, order=None, radial=None):
         """Moments A_l as monomial-major (k_l, N, C) blocks (face/model.py:460-534). Y and env may be
         pairs of views of one tensor, (density reader, directional / radial reader), so that their
-        gradients reach the edge backward separately (FACE.forward)."""
+        gradients reach the edge backward separately (FACE.forward). radial: this pass's (phi,
+        phi again, h2) when the radial MLPs of the passes were evaluated together."""
         N, E = g.N, g.E
         B, C, Kd = self.B, self.C, self.K
         Y, Y_dir = Y if isinstance(Y, tuple) else (Y, Y)
@@ -245,13 +254,12 @@ class FactorBlock(nn.Module):
             sp = self.spline
             phi, R_sp = ops.radial_spline(r, env_rad, zp, sp.T, sp.dT, sp.dr, B, order)
             phi_dir = phi
+        elif radial is not None:
+            phi, phi_dir, h2 = radial
         else:
             # hidden layers and phi columns of the radial MLP in one HIP kernel; the CP columns of
             # the last layer are a GEMM on its h2 output; phi once per reader (density, transport)
-            Wi, bi = frozen(self.rad_in)
-            W1, b1 = frozen(self.radial[0])
-            phi, phi_dir, h2 = ops.radial_mlp(rb, env_rad, zp, Wi, bi, self.pair.weight.detach(), W1, b1, W2[:B],
-                                              b2[:B], self.cp)                   # (E, B) twice, (E, H)
+            phi, phi_dir, h2 = ops.radial_mlp(rb, env_rad, zp, *self.radial_weights(), self.cp)   # (E, B) x2, (E, H)
         msg_n = F.linear(h, *frozen(self.msg))                                   # (N, K)
         if self.directional:
             if self.eq_in:
@@ -361,12 +369,13 @@ class FactorBlock(nn.Module):
         return c[1]
 
     # ------------------------------------------------------------------ invariants + readout
-    def forward(self, h, rb, r, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g, order=None, acc=None, last=False):
+    def forward(self, h, rb, r, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g, order=None, acc=None, last=False,
+                radial=None):
         """(e (N, 1), h_new (N, C) | None, A, eq_new) of one pass. acc: the per-forward dict of
         shared moment-set gradients (ops.rank_proj) or None; last: the final pass, whose h_new is
-        not computed."""
+        not computed; radial: precomputed radial MLP outputs (see moments)."""
         C = self.C
-        A = self.moments(h, rb, r, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g, order)
+        A = self.moments(h, rb, r, Y, env, zp, zidx, zidx32, avg_nb, sets, eq, g, order, radial)
         allsets = sets + [A]
         # only P0 of rank 0 and P3, Q3 of rank 3 are used
         ws = [frozen(self.proj[l])[0][:(C, 3 * C, 3 * C, 2 * C)[l]] for l in range(4)]
@@ -542,15 +551,28 @@ class FACE(nn.Module):
         sets, eq, es = [], None, []
         nb = len(self.blocks)
         rb0, r0 = views[1][0], views[3][0]
+        # the radial MLPs of all MLP passes in one launch each way (they read only the edge basis)
+        mlp = [t for t, b in enumerate(self.blocks) if b.spline is None]
+        radial, pre = {}, {}
+        if len(mlp) > 1 and len({self.blocks[t].cp for t in mlp}) == 1 and \
+                len({tuple(w.shape for w in self.blocks[t].radial_weights()) for t in mlp}) == 1:
+            for t in mlp:
+                pre[t] = (take(1), take(2))
+            outs = ops.radial_mlp_sets(zp, [self.blocks[t].radial_weights() for t in mlp], self.blocks[mlp[0]].cp,
+                                       [pre[t][0] for t in mlp], [pre[t][1] for t in mlp])
+            radial = dict(zip(mlp, outs))
         for t, blk in enumerate(self.blocks):
             y_d = take(0)
             y_t = take(0) if blk.directional else y_d
-            rb_b = take(1) if blk.spline is None else rb0
-            env_r = take(2)
+            if t in pre:
+                rb_b, env_r = pre[t]
+            else:
+                rb_b = take(1) if blk.spline is None else rb0
+                env_r = take(2)
             env_d = take(2) if blk.cp else env_r
             r_b = take(3) if blk.spline is not None else r0
             e, h, A, eq = blk(h, rb_b, r_b, (y_d, y_t), (env_d, env_r), zp, zidx, zidx32, self.avg_nb, sets, eq, graph,
-                              order, acc, last=t == nb - 1)
+                              order, acc, last=t == nb - 1, radial=radial.get(t))
             sets.append(A)
             es.append(e)
         E, e_at = ops.atom_energy(e0, self.scale, graph.struct_ptr, graph.nstr, es)

@@ -922,6 +922,73 @@ class RadialMLP(torch.autograd.Function):
         return grb, genv, None, None, None, None, None, None, None, None, None
 
 
+class RadialMLPSets(torch.autograd.Function):
+    """The radial MLPs of several passes over the same edges (face/model.py:465-469 per pass) in one
+    launch each way: the passes' radial functions depend only on the edge basis, so they are
+    evaluated together (twice the waves of one pass per launch) and differentiated together once
+    every pass's gradients have arrived. rb_env: one rb view and one envelope view per pass (views
+    of the same tensors, so that each reader's gradient comes back on its own)."""
+
+    @staticmethod
+    def forward(ctx, pair, wsets, want_h2, *rb_env):
+        n = len(wsets)
+        rbs, envs = rb_env[:n], rb_env[n:]
+        _lib.require_gpu(*rb_env)
+        rb, env = rbs[0], envs[0]
+        if any(t.data_ptr() != rb.data_ptr() or t.stride() != rb.stride() for t in rbs) or \
+                any(t.data_ptr() != env.data_ptr() for t in envs):
+            raise ValueError("radial_mlp_sets: the rb (and envelope) views must be views of one tensor")
+        E, nb = rb.shape
+        rb_, ld_rb = _rows(rb, nb)
+        env_ = env.contiguous().float()
+        ws = [t.detach().contiguous().float() for w in wsets for t in w]
+        H, B, n_pair = ws[3].shape[0], ws[5].shape[0], ws[2].shape[0]
+        dev = rb.device
+        h2 = [torch.empty(E, H, device=dev) if want_h2 else torch.empty(0, H, device=dev) for _ in range(n)]
+        phi = [torch.empty(E, B, device=dev) for _ in range(n)]
+        call("face_radial_fwd_sets", ptr(rb_), ld_rb, nb, ptr(pair), ptr(env_), E, n, _lib.ptr_array(ws), n_pair, H, B,
+             _lib.ptr_array(h2) if want_h2 else None, H, _lib.ptr_array(phi), B, _lib.stream_of(rb_),
+             label="radial_fwd")
+        ctx.save_for_backward(rb_, env_, pair, *ws)
+        ctx.dims = (E, nb, H, B, n_pair, n)
+        ctx.set_materialize_grads(False)
+        out = []
+        for k in range(n):
+            out += [phi[k], phi[k].view(phi[k].shape), h2[k]]
+        return tuple(out)
+
+    @staticmethod
+    def backward(ctx, *grads):
+        rb, env, pair, *ws = ctx.saved_tensors
+        E, nb, H, B, n_pair, n = ctx.dims
+        dev = rb.device
+        gphi, gphi2, gh2 = [], [], []
+        for k in range(n):
+            g1, g2, gh = grads[3 * k:3 * k + 3]
+            g1 = g1.contiguous().float() if g1 is not None else None
+            g2 = g2.contiguous().float() if g2 is not None else None
+            if g1 is None:
+                g1, g2 = (g2, None) if g2 is not None else (torch.zeros(E, B, device=dev), None)
+            gphi.append(g1)
+            gphi2.append(g2)
+            gh2.append(gh.contiguous().float() if (gh is not None and gh.numel()) else None)
+        need_rb = ctx.needs_input_grad[3:3 + n]
+        need_env = ctx.needs_input_grad[3 + n:3 + 2 * n]
+        grb = [torch.empty(E, nb, device=dev) if need_rb[k] else None for k in range(n)]
+        genv = [torch.empty(E, device=dev) if need_env[k] else None for k in range(n)]
+        call("face_radial_bwd_sets", ptr(rb), rb.stride(0), nb, ptr(pair), ptr(env), E, n, _lib.ptr_array(ws), n_pair,
+             H, B, _lib.ptr_array(gh2), H, _lib.ptr_array(gphi), _lib.ptr_array(gphi2), B, _lib.ptr_array(grb), nb,
+             _lib.ptr_array(genv), _lib.stream_of(rb), label="radial_bwd")
+        return (None, None, None, *grb, *genv)
+
+
+def radial_mlp_sets(pair, wsets, want_h2, rbs, envs):
+    """Per pass (phi, phi again as a view for a second reader, h2) of the radial MLPs of several
+    passes in one launch each way; wsets: per pass (w_in, b_in, pair_tab, w1, b1, w_phi, b_phi)."""
+    out = RadialMLPSets.apply(pair, wsets, want_h2, *rbs, *envs)
+    return [tuple(out[3 * k:3 * k + 3]) for k in range(len(wsets))]
+
+
 def radial_mlp(rb, env, pair, w_in, b_in, pair_tab, w1, b1, w_phi, b_phi, want_h2):
     """(phi, phi again as a view for a second reader (its gradient is summed in the backward
     kernel), h2)."""

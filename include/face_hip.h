@@ -278,6 +278,20 @@ int face_radial_bwd(const float* rb, int32_t ld_rb, int32_t n_basis, const int32
                     int32_t H, const float* w1, const float* b1, const float* w_phi, const float* b_phi, int32_t B,
                     const float* gh2, int32_t ld_gh2, const float* gphi, const float* gphi2, int32_t ld_gphi,
                     float* grb, int32_t ld_grb, float* genv, void* stream);
+/* The radial MLPs of n_sets (<= 4) passes over the same edges in one launch (the passes'
+ * radial functions are independent of each other, face/model.py:465-469 per pass): weights is a
+ * host array of 7 n_sets device pointers (w_in, b_in, pair_tab, w1, b1, w_phi, b_phi of set k at
+ * 7k .. 7k + 6), h2 / phi host arrays of n_sets outputs (h2 may be NULL, or hold NULL entries);
+ * each set as face_radial_fwd. */
+int face_radial_fwd_sets(const float* rb, int32_t ld_rb, int32_t n_basis, const int32_t* pair, const float* env,
+                         int64_t E, int32_t n_sets, const float* const* weights, int32_t n_pair, int32_t H, int32_t B,
+                         float* const* h2, int32_t ld_h2, float* const* phi, int32_t ld_phi, void* stream);
+/* Backward of face_radial_fwd_sets: host arrays of n_sets gh2 / gphi / gphi2 / grb / genv (the
+ * arrays other than gphi may be NULL; entries may be NULL), each set as face_radial_bwd. */
+int face_radial_bwd_sets(const float* rb, int32_t ld_rb, int32_t n_basis, const int32_t* pair, const float* env,
+                         int64_t E, int32_t n_sets, const float* const* weights, int32_t n_pair, int32_t H, int32_t B,
+                         const float* const* gh2, int32_t ld_gh2, const float* const* gphi, const float* const* gphi2,
+                         int32_t ld_gphi, float* const* grb, int32_t ld_grb, float* const* genv, void* stream);
 
 /* ---------------------------------------------------------------- compiled radial (splines)
  * RadialSpline.forward (face/model.py:407-418), the table lookup that FACE.compile_radial

@@ -658,6 +658,50 @@ def test_radial_mlp_matches_torch(E, nb, H, B, n_pair, want_h2):
     assert max(errs) < TOL, errs
 
 
+@pytest.mark.parametrize("E,n_sets,want_h2", [(15552, 2, False), (20000, 2, True), (1001, 3, True), (37, 4, False)])
+def test_radial_mlp_sets_equal_single_launches(E, n_sets, want_h2):
+    """The radial MLPs of several passes in one launch each way give bitwise the outputs and
+    input gradients of one launch per pass (the same instructions per set): rb / envelope read
+    through per-pass views, a second phi reader on some passes, no gradient on others."""
+    from face_amd import ops
+    say("radial sets", E, n_sets, want_h2)
+    torch.manual_seed(E + n_sets)
+    nb, H, B, n_pair = 8, 64, 16, 9
+    base_rb = torch.randn(E, nb, device=DEV, requires_grad=True)
+    base_env = torch.rand(E, device=DEV, requires_grad=True)
+    pair = torch.randint(0, n_pair, (E,), device=DEV, dtype=torch.int32)
+    wsets = []
+    for _ in range(n_sets):
+        ws = [torch.randn(H, nb) / nb ** 0.5, torch.randn(H) * 0.1, torch.randn(n_pair, H) * 0.3,
+              torch.randn(H, H) / H ** 0.5, torch.randn(H) * 0.1, torch.randn(B, H) / H ** 0.5, torch.randn(B) * 0.1]
+        wsets.append([w.to(DEV) for w in ws])
+    gps = [torch.randn(E, B, device=DEV) for _ in range(n_sets)]
+    ghs = [torch.randn(E, H, device=DEV) for _ in range(n_sets)]
+
+    def loss(outs):
+        L = 0
+        for k, (phi, phi_b, h2) in enumerate(outs):
+            L = L + (phi * gps[k]).sum()
+            if k % 2 == 1:
+                L = L + (phi_b * (0.5 * gps[k])).sum()
+            if want_h2 and k != 1:
+                L = L + (h2 * ghs[k]).sum()
+        return L
+    rbs = [base_rb.view(base_rb.shape) for _ in range(n_sets)]
+    envs = [base_env.view(base_env.shape) for _ in range(n_sets)]
+    outs = ops.radial_mlp_sets(pair, wsets, want_h2, rbs, envs)
+    got = torch.autograd.grad(loss(outs), rbs + envs)
+    rbs2 = [base_rb.view(base_rb.shape) for _ in range(n_sets)]
+    envs2 = [base_env.view(base_env.shape) for _ in range(n_sets)]
+    outs2 = [ops.radial_mlp(rbs2[k], envs2[k], pair, *wsets[k], want_h2) for k in range(n_sets)]
+    want = torch.autograd.grad(loss(outs2), rbs2 + envs2)
+    for a, b in zip(outs, outs2):
+        for x, y in zip(a, b):
+            assert torch.equal(x, y)
+    for a, b in zip(got, want):
+        assert torch.equal(a, b)
+
+
 # ----------------------------------------------------------------------------- row-block linear layers
 def _lin_ref(x, w, w_kn, y0, beta, bias, xs, ys, grp, period, s_off):
     x, w = x.double().cpu(), w.double().cpu()
