@@ -33,7 +33,7 @@
 namespace face {
 
 constexpr int kGemmBB = 2;                 // 16-row blocks per wave
-constexpr int kGemmMaxProbs = 4;
+constexpr int kGemmMaxProbs = 8;                // problems per launch
 constexpr int kGemmMaxGroups = 64;         // scale-table rows (elements) staged in LDS
 
 struct GemmProb {

@@ -80,7 +80,7 @@ _SIGS = {
     "face_layer_norm_bwd": (ctypes.c_int, [P, P, I64, I32, P, P, P, P, P]),
 }
 
-ABI_VERSION = 20
+ABI_VERSION = 21
 
 
 class LinProblem(ctypes.Structure):

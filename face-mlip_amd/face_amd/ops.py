@@ -1179,7 +1179,7 @@ def lin(x, w, y, s_off=0, beta=0.0, x2=None, x_op=0, xz=None, bias=None, y0=None
 
 
 def rows_linear(probs, w_kn=False, bias=None, xs=None, ys=None, group=None, period=1, label="rows_linear"):
-    """One launch of up to four row-block linear problems (no autograd). probs: lin() dicts or
+    """One launch of up to eight row-block linear problems (no autograd). probs: lin() dicts or
     (x (m, k), w, y (m, n), s_off, beta) tuples; w is (n, k) or, with w_kn, (k, n).
     y[r] = (beta y0[r] + (op(x)[r] * xs[g(r), s_off:]) w^T + bias) * ys[g(r), s_off:],
     g(r) = group[r % period]; xs / ys are (n_groups, ld) tables or None; `bias` applies to the
@@ -1301,9 +1301,14 @@ class RankProj(torch.autograd.Function):
         ys = [torch.empty(sets[0][l].shape[0], N, w.shape[0], device=dev) for l, w in enumerate(ws)]
         if out0:
             ys[0] = out0[0].unsqueeze(0)                 # rank 0 (one monomial) into the caller's rows
-        for s, S_s in enumerate(sets):
-            rows_linear([(S_s[l].reshape(-1, C), ws[l][:, s * C:(s + 1) * C], ys[l].reshape(-1, ws[l].shape[0]), 0,
-                          1.0 if s else 0.0) for l in range(4)], label="proj_fwd")
+        # two sets per launch as one product of K = 2C (the second set's rows as the split input
+        # columns), a third accumulating in the epilogue of the next launch
+        for s in range(0, n_sets, 2):
+            pair = s + 1 < n_sets
+            rows_linear([lin(sets[s][l].reshape(-1, C), ws[l][:, s * C:(s + 1 + pair) * C],
+                             ys[l].reshape(-1, ws[l].shape[0]), 0, 1.0 if s else 0.0,
+                             x2=sets[s + 1][l].reshape(-1, C) if pair else None) for l in range(4)],
+                        label="proj_fwd")
         slots = None
         if acc is not None:
             # one SetGrad per set, keyed by its rank-0 tensor (the entry holds the tensor itself, so
@@ -1326,7 +1331,7 @@ class RankProj(torch.autograd.Function):
         dev = ws[0].device
         gy = [(_row_view(g, w.shape[0]) if g is not None else torch.zeros(sh[0] * sh[1], w.shape[0], device=dev))
               for g, w, sh in zip(gy, ws, ctx.shapes[:4])]
-        grads = []
+        grads, probs = [], []
         for s in range(ctx.n_sets):
             need = [ctx.needs_input_grad[4 + 4 * s + l] for l in range(4)]
             slot = ctx.slots[s] if ctx.slots is not None else None
@@ -1337,9 +1342,12 @@ class RankProj(torch.autograd.Function):
                 beta, out = 0.0, d
                 if slot is not None:
                     slot.g = d
-            probs = [(gy[l], ws[l][:, s * C:(s + 1) * C], d[l].view(-1, C), 0, beta) for l in range(4) if need[l]]
-            if probs:
-                rows_linear(probs, w_kn=True, label="proj_bwd")
+            # the four ranks of two sets per launch
+            probs += [(gy[l], ws[l][:, s * C:(s + 1) * C], d[l].view(-1, C), 0, beta) for l in range(4) if need[l]]
+            if len(probs) > 4 or s == ctx.n_sets - 1:
+                if probs:
+                    rows_linear(probs, w_kn=True, label="proj_bwd")
+                probs = []
             if slot is not None:
                 slot.arrived += 1
                 if slot.arrived == slot.readers:

@@ -364,7 +364,7 @@ typedef struct {
     int64_t ld_y0;
     int32_t n_y0, pad_;
 } face_lin_problem;
-/* For each problem (1..4 of them, host array):
+/* For each problem (1..8 of them, host array):
  *   y[r, :] = (beta y0[r, :] + (op(x)[r, :] * xs[r, :]) w^T + bias) * ys[r, :]
  * with xs[r, k] = x_scale[group[r % period] * ld_scale + s_off + k] and ys likewise over the
  * n output columns, group values in [0, n_groups) (n_groups <= 64: the scale tables' rows, staged
