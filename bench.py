@@ -97,10 +97,30 @@ def log(*a):
 
 
 # ----------------------------------------------------------------------------- algorithmic figures
+def split_label(label):
+    """(base label, n) of a call label "base*n": one launch doing the work of n calls of base
+    (passes or moment sets merged into one launch)."""
+    base, _, n = label.partition("*")
+    return base, int(n) if n else 1
+
+
+def family_of(label):
+    return KERNEL_FAMILY.get(split_label(label)[0])
+
+
 def algorithmic_bytes(label, g, kw):
     """Bytes per launch: every operand of the kernel's interface read once, every output written
-    once, fp32 / int32 (valid pairs E only)."""
+    once, fp32 / int32 (valid pairs E only); a merged launch (label "base*n") counts the inputs
+    its n units share once."""
     E, N = g.E, g.N
+    label, units = split_label(label)
+    if label.startswith("radial_") and units > 1:     # rb, pair, env shared by the passes
+        H, nb = kw.get("radial_hidden", 64), kw.get("n_basis", 8)
+        one = algorithmic_bytes(label, g, kw)
+        return one + (units - 1) * (one - 4 * E * (nb + 2))
+    if units > 1:
+        one = algorithmic_bytes(label, g, kw)
+        return units * one if one else None
     B, C = kw["B"], kw["C"]
     K = C if kw.get("cp") else kw["K"]
     Kt = 18 * kw["K_dir"]                 # transport table: 9 components x 2Kd channels
@@ -127,7 +147,14 @@ def algorithmic_bytes(label, g, kw):
     if label == "edge_fwd":
         return 4 * E * (11 + 29)
     if label == "edge_bwd":
-        return 4 * E * (11 + 29 + 3)
+        # geometry in, dL/dvec out, and every reader's gradient of Y, rb (or r), the envelope read
+        # once (the model hands each reader its own view: pass t reads Y once more when
+        # directional, t >= 1, the envelope once more in CP form; at most 4 buffers per input)
+        P = kw.get("n_passes", 2)
+        nY, nE = min(4, 2 * P - 1), min(4, P * (1 + int(bool(kw.get("cp")))))
+        nR = min(4, P)
+        radial = nR * (1 if kw.get("compiled") else kw.get("n_basis", 8))
+        return 4 * E * (11 + 3 + 20 * nY + radial + nE)
     if label == "force_scatter":
         return 4 * (3 * E + E + 3 * N)
     if label.startswith("spline_") and label != "spline_order":   # r, pair, env in, F columns out; tables once
@@ -183,6 +210,10 @@ def algorithmic_flops(label, g, kw):
     gradient, the fused CP radial backward (d h2 = dR W_cp, E x 4C by 4C x H, plus the two
     20-monomial contractions per edge and channel), and the factor density's per-monomial
     products (2 E 20 B K each way; 3 of them in the backward)."""
+    label, units = split_label(label)
+    if units > 1:
+        one = algorithmic_flops(label, g, kw)
+        return units * one if one else None
     N, E, C = g.N, g.E, kw["C"]
     H = kw.get("radial_hidden", 64)
     cin = C if kw.get("cp") else kw["B"] * kw["K"]
@@ -264,7 +295,7 @@ def label_stats(timers, steps, g, kw):
         fl = algorithmic_flops(label, g, kw)
         ib = interface_bytes(label, g, kw)
         fus, bound = floor_us(byts, fl)
-        kern[label] = {"family": KERNEL_FAMILY.get(label), "launches_per_step": len(evs) / steps, "avg_us": avg_us,
+        kern[label] = {"family": family_of(label), "launches_per_step": len(evs) / steps, "avg_us": avg_us,
                        "ms_per_step": float(np.sum(ms)) / steps, "alg_bytes": byts, "alg_flops": fl,
                        "GBps": (byts / (avg_us * 1e-6) / 1e9) if byts else None,
                        "GBps_interface": (ib / (avg_us * 1e-6) / 1e9) if ib else None,
@@ -343,7 +374,7 @@ def run_gpu(k, steps, warmup, use_graph=True, compiled_radial=False):
     m = model_for(kw, el)
     if compiled_radial:
         m.compile_radial()
-        kw = dict(kw, n_elem=len(el), n_grid=4096)
+        kw = dict(kw, n_elem=len(el), n_grid=4096, compiled=True)
 
     def step():
         return m(g.with_pos(g.pos.clone()))["forces"]
@@ -468,11 +499,12 @@ def pmc_probe(k, steps=2, copy_floats=1 << 28):
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
+    labs = sorted(set(TIMED) | {lab for lab in order if family_of(lab)})
     out = {"probe": desc, "workload": k, "steps": steps, "copy_bytes_read": 4 * copy_floats,
            "copy_bytes_written": 4 * copy_floats,
-           "alg_bytes": {lab: algorithmic_bytes(lab, g, kw) for lab in TIMED},
-           "interface_bytes": {lab: interface_bytes(lab, g, kw) for lab in TIMED},
-           "alg_flops": {lab: algorithmic_flops(lab, g, kw) for lab in TIMED}, "order": order}
+           "alg_bytes": {lab: algorithmic_bytes(lab, g, kw) for lab in labs},
+           "interface_bytes": {lab: interface_bytes(lab, g, kw) for lab in labs},
+           "alg_flops": {lab: algorithmic_flops(lab, g, kw) for lab in labs}, "order": order}
     print(json.dumps(out), flush=True)
 
 
@@ -494,7 +526,7 @@ def _label_dispatches(rows, order, what):
     for lab, fam in KERNEL_FAMILY.items():
         for kname in FAMILY_KERNELS[fam]:
             by_base[kname].append(lab)
-    seq = {b: [lab for lab in order if lab in labs] for b, labs in by_base.items()}
+    seq = {b: [lab for lab in order if split_label(lab)[0] in labs] for b, labs in by_base.items()}
     pos = collections.Counter()
     out = []
     for r in rows:
@@ -571,14 +603,15 @@ def pmc_summary(fetch_dir, write_dir, probe_log, out_path):
                "bytes of the label (operands of the drop-in read once, outputs written once).\n\n")
     out.append("| label | family | kernels | calls | traffic bytes/call | alg bytes/call | traffic/alg |\n"
                "|---|---|---|---:|---:|---:|---:|\n")
-    tracked = [lab for lab in KERNEL_FAMILY if calls.get(lab)]
+    tracked = [lab for lab in sorted(calls, key=lambda x: (list(KERNEL_FAMILY).index(split_label(x)[0])
+                                                             if family_of(x) else 1 << 30, x)) if family_of(lab)]
     fam_t = collections.defaultdict(lambda: [0.0, 0.0, 0])
     for lab in tracked:
         n = calls[lab]
         t = (acc["FETCH_SIZE"][lab] * 1024 * scale["FETCH_SIZE"] + acc["WRITE_SIZE"][lab] * 1024 *
              scale["WRITE_SIZE"]) / n
         alg = probe["alg_bytes"].get(lab)
-        fam = KERNEL_FAMILY[lab]
+        fam = family_of(lab)
         fam_t[fam][0] += t * n
         fam_t[fam][1] += (alg or 0) * n
         fam_t[fam][2] += n

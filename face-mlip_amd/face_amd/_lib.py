@@ -152,12 +152,13 @@ def call(name, *args, label=None):
     launch for time_calls (defaults to the entry-point name)."""
     fn = getattr(lib(), name)
     key = label or name
-    if _timing is not None and key in _timing:
+    # "name*n": a launch doing the work of n calls of "name" (passes or moment sets merged)
+    if _timing is not None and key.split("*")[0] in _timing:
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
         code = fn(*args)
         e.record()
-        _timing[key].append((s, e))
+        _timing.setdefault(key, []).append((s, e))
     else:
         code = fn(*args)
     if code != 0:

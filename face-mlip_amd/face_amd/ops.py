@@ -948,7 +948,7 @@ class RadialMLPSets(torch.autograd.Function):
         phi = [torch.empty(E, B, device=dev) for _ in range(n)]
         call("face_radial_fwd_sets", ptr(rb_), ld_rb, nb, ptr(pair), ptr(env_), E, n, _lib.ptr_array(ws), n_pair, H, B,
              _lib.ptr_array(h2) if want_h2 else None, H, _lib.ptr_array(phi), B, _lib.stream_of(rb_),
-             label="radial_fwd")
+             label=f"radial_fwd*{n}")
         ctx.save_for_backward(rb_, env_, pair, *ws)
         ctx.dims = (E, nb, H, B, n_pair, n)
         ctx.set_materialize_grads(False)
@@ -978,7 +978,7 @@ class RadialMLPSets(torch.autograd.Function):
         genv = [torch.empty(E, device=dev) if need_env[k] else None for k in range(n)]
         call("face_radial_bwd_sets", ptr(rb), rb.stride(0), nb, ptr(pair), ptr(env), E, n, _lib.ptr_array(ws), n_pair,
              H, B, _lib.ptr_array(gh2), H, _lib.ptr_array(gphi), _lib.ptr_array(gphi2), B, _lib.ptr_array(grb), nb,
-             _lib.ptr_array(genv), _lib.stream_of(rb), label="radial_bwd")
+             _lib.ptr_array(genv), _lib.stream_of(rb), label=f"radial_bwd*{n}")
         return (None, None, None, *grb, *genv)
 
 
@@ -1308,7 +1308,7 @@ class RankProj(torch.autograd.Function):
             rows_linear([lin(sets[s][l].reshape(-1, C), ws[l][:, s * C:(s + 1 + pair) * C],
                              ys[l].reshape(-1, ws[l].shape[0]), 0, 1.0 if s else 0.0,
                              x2=sets[s + 1][l].reshape(-1, C) if pair else None) for l in range(4)],
-                        label="proj_fwd")
+                        label="proj_fwd*2" if pair else "proj_fwd")
         slots = None
         if acc is not None:
             # one SetGrad per set, keyed by its rank-0 tensor (the entry holds the tensor itself, so
@@ -1331,7 +1331,7 @@ class RankProj(torch.autograd.Function):
         dev = ws[0].device
         gy = [(_row_view(g, w.shape[0]) if g is not None else torch.zeros(sh[0] * sh[1], w.shape[0], device=dev))
               for g, w, sh in zip(gy, ws, ctx.shapes[:4])]
-        grads, probs = [], []
+        grads, probs, n_in = [], [], 0
         for s in range(ctx.n_sets):
             need = [ctx.needs_input_grad[4 + 4 * s + l] for l in range(4)]
             slot = ctx.slots[s] if ctx.slots is not None else None
@@ -1344,10 +1344,11 @@ class RankProj(torch.autograd.Function):
                     slot.g = d
             # the four ranks of two sets per launch
             probs += [(gy[l], ws[l][:, s * C:(s + 1) * C], d[l].view(-1, C), 0, beta) for l in range(4) if need[l]]
+            n_in += 1
             if len(probs) > 4 or s == ctx.n_sets - 1:
                 if probs:
-                    rows_linear(probs, w_kn=True, label="proj_bwd")
-                probs = []
+                    rows_linear(probs, w_kn=True, label="proj_bwd*2" if n_in == 2 else "proj_bwd")
+                probs, n_in = [], 0
             if slot is not None:
                 slot.arrived += 1
                 if slot.arrived == slot.readers:
