@@ -53,7 +53,7 @@ KERNEL_FAMILY = {
     "cp_radial_bwd": "cp_radial_bwd", "cp_radial_bwd_tab": "cp_radial_bwd",
     "transport_fwd": "transport_fwd", "transport_bwd": "transport_bwd",
     "dir_fwd": "dir_feats_fwd", "dir_bwd": "dir_feats_bwd",
-    "node_fwd": "node_fwd", "node_bwd": "node_bwd",
+    "node_fwd": "node_fwd", "node_bwd": "node_bwd", "node_ln_fwd": "node_ln_fwd", "node_ln_bwd": "node_ln_bwd",
     "edge_fwd": "edge_geom_fwd", "edge_bwd": "edge_geom_bwd", "force_scatter": "force_scatter",
     "gather_bwd": "gather_rows_bwd", "radial_fwd": "radial_fwd", "radial_bwd": "radial_bwd",
     "radial_head": "edge_linear_fwd", "edge_msg_fwd": "edge_linear_fwd", "edge_msg_bwd": "edge_linear_bwd",
@@ -78,6 +78,7 @@ FAMILY_KERNELS = {
     "dir_feats_fwd": ["dir_feats_fwd_kernel"], "dir_feats_bwd": ["dir_feats_bwd_edge_kernel",
                                                                  "dir_feats_bwd_node_kernel"],
     "node_fwd": ["node_fwd_kernel"], "node_bwd": ["node_bwd_kernel"],
+    "node_ln_fwd": ["node_ln_fwd_kernel"], "node_ln_bwd": ["node_ln_bwd_kernel"],
     "edge_geom_fwd": ["edge_geom_fwd_kernel"], "edge_geom_bwd": ["edge_geom_bwd_seg_kernel", "edge_geom_bwd_kernel"],
     "force_scatter": ["force_scatter_rows_kernel", "force_scatter_kernel"],
     "gather_rows_bwd": ["gather_rows_bwd_kernel"],
@@ -144,6 +145,10 @@ def algorithmic_bytes(label, g, kw):
         return 4 * 67 * N * C           # 47 in; 8 invariants + V (3) + full Mf (9) out
     if label == "node_bwd":
         return 4 * 114 * N * C          # 47 in, 20 upstream, 47 out
+    if label == "node_ln_fwd":          # 47 + P0 in; the normalised row (9), V (3), full Mf (9) out
+        return 4 * 69 * N * C
+    if label == "node_ln_bwd":          # 47 + P0 in, 9 + 12 upstream, 47 + P0 out
+        return 4 * 117 * N * C
     if label == "edge_fwd":
         return 4 * E * (11 + 29)
     if label == "edge_bwd":

@@ -111,20 +111,10 @@ __device__ __forceinline__ void node_mid(const NodeRegs& r, NodeMid& m) {
         }
 }
 
-__global__ __launch_bounds__(256) void node_fwd_kernel(Strided8 in, const float* __restrict__ av,
-                                                       const float* __restrict__ bv, float* __restrict__ inv,
-                                                       Str3 si, float* __restrict__ V, Str3 sv,
-                                                       float* __restrict__ Mf, Str3 sm, int mf_mode, int64_t N,
-                                                       int C, int eq) {
-    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    if (t >= N * C) return;
-    const int64_t n = t / C;
-    const int c = (int)(t - n * C);
-    NodeRegs r;
-    load_node(in, n, c, r);
-    NodeMid m;
-    node_mid(r, m);
-    float f[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+// The eight invariant families of one (atom, channel) (face/node_kernel.py:18-64).
+__device__ __forceinline__ void node_invariants(const NodeRegs& r, const NodeMid& m, float (&f)[8]) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) f[k] = 0.f;
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
         f[0] = fmaf(r.p1[a], r.q1[a], f[0]);
@@ -148,15 +138,17 @@ __global__ __launch_bounds__(256) void node_fwd_kernel(Strided8 in, const float*
                 for (int e = 0; e < 3; ++e) x = fmaf(r.p3[e * 9 + b * 3 + a], r.q3[e * 9 + b * 3 + d], x);
             f[6] = fmaf(x, r.s2[a * 3 + d], f[6]);
         }
-    float* o = inv + n * si.sn + (int64_t)c * si.sc;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) o[k * si.sk] = f[k];
-    if (!eq) return;
+}
+
+// V (3) and Mf (9 full or 6 symmetrised) of one (atom, channel), written at vo / mo with the
+// component strides vsk / msk.
+__device__ __forceinline__ void node_eq_outputs(const NodeRegs& r, const NodeMid& m, const float* __restrict__ av,
+                                                const float* __restrict__ bv, int c, int C, float* vo, int64_t vsk,
+                                                float* mo, int64_t msk, int mf_mode) {
     const float a0 = av[c], a1 = av[C + c], a2 = av[2 * C + c], a3 = av[3 * C + c];
     const float b0 = bv[c], b1 = bv[C + c], b2 = bv[2 * C + c], b3 = bv[3 * C + c];
-    float* vo = V + n * sv.sn + (int64_t)c * sv.sc;
 #pragma unroll
-    for (int a = 0; a < 3; ++a) vo[a * sv.sk] = a0 * r.p1[a] + a1 * m.q2s1[a] + a2 * m.p3q2[a] + a3 * m.p2q1[a];
+    for (int a = 0; a < 3; ++a) vo[a * vsk] = a0 * r.p1[a] + a1 * m.q2s1[a] + a2 * m.p3q2[a] + a3 * m.p2q1[a];
     float mf[9];
 #pragma unroll
     for (int a = 0; a < 3; ++a)
@@ -164,61 +156,26 @@ __global__ __launch_bounds__(256) void node_fwd_kernel(Strided8 in, const float*
         for (int d = 0; d < 3; ++d)
             mf[a * 3 + d] = b0 * r.p2[a * 3 + d] + b1 * r.p1[a] * r.q1[d] + b2 * m.pq2[a * 3 + d] +
                             b3 * m.p3s1[a * 3 + d];
-    float* mo = Mf + n * sm.sn + (int64_t)c * sm.sc;
     if (mf_mode == 0) {
 #pragma unroll
-        for (int k = 0; k < 9; ++k) mo[k * sm.sk] = mf[k];
+        for (int k = 0; k < 9; ++k) mo[k * msk] = mf[k];
     } else {
 #pragma unroll
-        for (int a = 0; a < 3; ++a) mo[a * sm.sk] = mf[a * 4];
-        mo[3 * sm.sk] = 0.5f * (mf[1] + mf[3]);
-        mo[4 * sm.sk] = 0.5f * (mf[2] + mf[6]);
-        mo[5 * sm.sk] = 0.5f * (mf[5] + mf[7]);
+        for (int a = 0; a < 3; ++a) mo[a * msk] = mf[a * 4];
+        mo[3 * msk] = 0.5f * (mf[1] + mf[3]);
+        mo[4 * msk] = 0.5f * (mf[2] + mf[6]);
+        mo[5 * msk] = 0.5f * (mf[5] + mf[7]);
     }
 }
 
-// Gradients with respect to the FULL tensors are formed entry by entry and folded into the
-// symmetric components they were expanded from (sum over the entries of a component).
-__global__ __launch_bounds__(256) void node_bwd_kernel(Strided8 in, const float* __restrict__ av,
-                                                       const float* __restrict__ bv, const float* __restrict__ gI,
-                                                       Str3 sgi, const float* __restrict__ gV, Str3 sgv,
-                                                       const float* __restrict__ gM, Str3 sgm, int mf_mode,
-                                                       StridedOut8 out, float* __restrict__ da,
-                                                       float* __restrict__ db, int64_t N, int C, int eq) {
-    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    if (t >= N * C) return;
-    const int64_t n = t / C;
-    const int c = (int)(t - n * C);
-    NodeRegs r;
-    load_node(in, n, c, r);
-    NodeMid m;
-    node_mid(r, m);
-    float g[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) g[k] = gI ? gI[n * sgi.sn + (int64_t)c * sgi.sc + k * sgi.sk] : 0.f;
-    float a0 = 0, a1 = 0, a2 = 0, a3 = 0, b0 = 0, b1 = 0, b2 = 0, b3 = 0;
-    float gv[3] = {0, 0, 0}, gm[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
-    if (eq) {
-        a0 = av[c]; a1 = av[C + c]; a2 = av[2 * C + c]; a3 = av[3 * C + c];
-        b0 = bv[c]; b1 = bv[C + c]; b2 = bv[2 * C + c]; b3 = bv[3 * C + c];
-        if (gV) {
-#pragma unroll
-            for (int a = 0; a < 3; ++a) gv[a] = gV[n * sgv.sn + (int64_t)c * sgv.sc + a * sgv.sk];
-        }
-        if (gM) {
-            const float* gp = gM + n * sgm.sn + (int64_t)c * sgm.sc;
-            if (mf_mode == 0) {
-#pragma unroll
-                for (int k = 0; k < 9; ++k) gm[k] = gp[k * sgm.sk];
-            } else {
-#pragma unroll
-                for (int a = 0; a < 3; ++a)
-#pragma unroll
-                    for (int d = 0; d < 3; ++d)
-                        gm[a * 3 + d] = (a == d ? 1.f : 0.5f) * gp[sym2(a, d) * sgm.sk];
-            }
-        }
-    }
+// Input gradients of one (atom, channel) from the invariant-family gradients g, gV, gM (full
+// 3x3) and the V / Mf coefficients: the full tensors' gradients formed entry by entry and folded
+// into the symmetric components they were expanded from; the coefficient partials when dap.
+__device__ __forceinline__ void node_bwd_core(const NodeRegs& r, const NodeMid& m, const float (&g)[8],
+                                              const float (&gv)[3], const float (&gm)[9], float a0, float a1,
+                                              float a2, float a3, float b0, float b1, float b2, float b3,
+                                              const StridedOut8& out, int64_t n, int c, float* dap,
+                                              float* dbp) {
     // ---- rank 1
     float dp1[3], dq1[3], ds1[3];
 #pragma unroll
@@ -307,7 +264,7 @@ __global__ __launch_bounds__(256) void node_bwd_kernel(Strided8 in, const float*
         ST(7, k, dq3[k]);
     }
 #undef ST
-    if (eq && da && db) {
+    if (dap) {
         float d0 = 0, d1 = 0, d2 = 0, d3 = 0, e0 = 0, e1 = 0, e2 = 0, e3 = 0;
 #pragma unroll
         for (int a = 0; a < 3; ++a) {
@@ -324,11 +281,218 @@ __global__ __launch_bounds__(256) void node_bwd_kernel(Strided8 in, const float*
                 e3 = fmaf(w, m.p3s1[a * 3 + d], e3);
             }
         }
-        float* dap = da + t * 4;
-        float* dbp = db + t * 4;
         dap[0] = d0; dap[1] = d1; dap[2] = d2; dap[3] = d3;
         dbp[0] = e0; dbp[1] = e1; dbp[2] = e2; dbp[3] = e3;
     }
+}
+
+__global__ __launch_bounds__(256) void node_fwd_kernel(Strided8 in, const float* __restrict__ av,
+                                                       const float* __restrict__ bv, float* __restrict__ inv,
+                                                       Str3 si, float* __restrict__ V, Str3 sv,
+                                                       float* __restrict__ Mf, Str3 sm, int mf_mode, int64_t N,
+                                                       int C, int eq) {
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (t >= N * C) return;
+    const int64_t n = t / C;
+    const int c = (int)(t - n * C);
+    NodeRegs r;
+    load_node(in, n, c, r);
+    NodeMid m;
+    node_mid(r, m);
+    float f[8];
+    node_invariants(r, m, f);
+    float* o = inv + n * si.sn + (int64_t)c * si.sc;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) o[k * si.sk] = f[k];
+    if (!eq) return;
+    node_eq_outputs(r, m, av, bv, c, C, V + n * sv.sn + (int64_t)c * sv.sc, sv.sk,
+                    Mf + n * sm.sn + (int64_t)c * sm.sc, sm.sk, mf_mode);
+}
+
+// Gradients with respect to the FULL tensors are formed entry by entry and folded into the
+// symmetric components they were expanded from (sum over the entries of a component).
+__global__ __launch_bounds__(256) void node_bwd_kernel(Strided8 in, const float* __restrict__ av,
+                                                       const float* __restrict__ bv, const float* __restrict__ gI,
+                                                       Str3 sgi, const float* __restrict__ gV, Str3 sgv,
+                                                       const float* __restrict__ gM, Str3 sgm, int mf_mode,
+                                                       StridedOut8 out, float* __restrict__ da,
+                                                       float* __restrict__ db, int64_t N, int C, int eq) {
+    const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (t >= N * C) return;
+    const int64_t n = t / C;
+    const int c = (int)(t - n * C);
+    NodeRegs r;
+    load_node(in, n, c, r);
+    NodeMid m;
+    node_mid(r, m);
+    float g[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) g[k] = gI ? gI[n * sgi.sn + (int64_t)c * sgi.sc + k * sgi.sk] : 0.f;
+    float a0 = 0, a1 = 0, a2 = 0, a3 = 0, b0 = 0, b1 = 0, b2 = 0, b3 = 0;
+    float gv[3] = {0, 0, 0}, gm[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
+    if (eq) {
+        a0 = av[c]; a1 = av[C + c]; a2 = av[2 * C + c]; a3 = av[3 * C + c];
+        b0 = bv[c]; b1 = bv[C + c]; b2 = bv[2 * C + c]; b3 = bv[3 * C + c];
+        if (gV) {
+#pragma unroll
+            for (int a = 0; a < 3; ++a) gv[a] = gV[n * sgv.sn + (int64_t)c * sgv.sc + a * sgv.sk];
+        }
+        if (gM) {
+            const float* gp = gM + n * sgm.sn + (int64_t)c * sgm.sc;
+            if (mf_mode == 0) {
+#pragma unroll
+                for (int k = 0; k < 9; ++k) gm[k] = gp[k * sgm.sk];
+            } else {
+#pragma unroll
+                for (int a = 0; a < 3; ++a)
+#pragma unroll
+                    for (int d = 0; d < 3; ++d)
+                        gm[a * 3 + d] = (a == d ? 1.f : 0.5f) * gp[sym2(a, d) * sgm.sk];
+            }
+        }
+    }
+    node_bwd_core(r, m, g, gv, gm, a0, a1, a2, a3, b0, b1, b2, b3, out, n, c,
+                  (eq && da && db) ? da + t * 4 : nullptr, (eq && da && db) ? db + t * 4 : nullptr);
+}
+
+// ------------------------------------------------------------------ node algebra + readout LayerNorm
+// The readout row x = [P0 | inv_1 .. inv_8] (9C, family-major, face/model.py:244-249) normalised
+// by the readout LayerNorm (face/model.py:140, :332) in the kernel that forms it: one workgroup per
+// atom, thread = channel (C <= 256; the workgroup is C rounded up to whole waves), each thread
+// holding its 9 row entries; the row's mean and biased variance are two workgroup sums (mean
+// first, then the centred squares). The row itself is never written: the backward recomputes it
+// from the projection outputs, then applies the LayerNorm backward and the node-algebra backward
+// to the same registers.
+__device__ __forceinline__ float wg_sum(float v, float* sh) {
+    v = group_sum(v, kWave);
+    __syncthreads();                                   // sh is free again (an earlier sum read it)
+    if ((threadIdx.x & (kWave - 1)) == 0) sh[threadIdx.x / kWave] = v;
+    __syncthreads();
+    float t = 0.f;
+    for (int i = 0; i < (int)(blockDim.x / kWave); ++i) t += sh[i];
+    return t;
+}
+
+__global__ __launch_bounds__(256) void node_ln_fwd_kernel(Strided8 in, const float* __restrict__ p0, int64_t p0_sn,
+                                                          const float* __restrict__ av, const float* __restrict__ bv,
+                                                          const float* __restrict__ lw, const float* __restrict__ lb,
+                                                          float eps, float* __restrict__ y, int64_t ld_y,
+                                                          float* __restrict__ stats, float* __restrict__ V, Str3 sv,
+                                                          float* __restrict__ Mf, Str3 sm, int mf_mode, int C,
+                                                          int eq) {
+    __shared__ float sh[256 / kWave];
+    const int64_t n = blockIdx.x;
+    const int c = threadIdx.x;
+    const bool act = c < C;
+    float x[9];
+    NodeRegs r;
+    NodeMid m;
+    if (act) {
+        load_node(in, n, c, r);
+        node_mid(r, m);
+        float f[8];
+        node_invariants(r, m, f);
+        x[0] = p0[n * p0_sn + c];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) x[1 + k] = f[k];
+    } else {
+#pragma unroll
+        for (int k = 0; k < 9; ++k) x[k] = 0.f;
+    }
+    const float F = 9.f * (float)C;
+    float s = 0.f;
+#pragma unroll
+    for (int k = 0; k < 9; ++k) s += x[k];
+    const float mu = wg_sum(s, sh) / F;
+    float ss = 0.f;
+    if (act) {
+#pragma unroll
+        for (int k = 0; k < 9; ++k) ss = fmaf(x[k] - mu, x[k] - mu, ss);
+    }
+    const float rs = 1.f / sqrtf(wg_sum(ss, sh) / F + eps);
+    if (act) {
+        float* yr = y + n * ld_y + c;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) yr[k * C] = (x[k] - mu) * rs * lw[k * C + c] + lb[k * C + c];
+        if (eq)
+            node_eq_outputs(r, m, av, bv, c, C, V + n * sv.sn + (int64_t)c * sv.sc, sv.sk,
+                            Mf + n * sm.sn + (int64_t)c * sm.sc, sm.sk, mf_mode);
+    }
+    if (c == 0) {
+        stats[2 * n] = mu;
+        stats[2 * n + 1] = rs;
+    }
+}
+
+// dx = rstd (g - mean(g) - xh mean(g xh)) with g = dy w, xh = (x - mean) rstd, then dx[0] -> dP0 and
+// dx[1..8] as the invariant-family gradients of the node-algebra backward.
+__global__ __launch_bounds__(256) void node_ln_bwd_kernel(Strided8 in, const float* __restrict__ p0, int64_t p0_sn,
+                                                          const float* __restrict__ av, const float* __restrict__ bv,
+                                                          const float* __restrict__ lw, const float* __restrict__ gy,
+                                                          int64_t ld_gy, const float* __restrict__ stats,
+                                                          const float* __restrict__ gV, Str3 sgv,
+                                                          const float* __restrict__ gM, Str3 sgm, int mf_mode,
+                                                          StridedOut8 out, float* __restrict__ dp0, int64_t dp0_sn,
+                                                          float* __restrict__ da, float* __restrict__ db, int C,
+                                                          int eq) {
+    __shared__ float sh[256 / kWave];
+    const int64_t n = blockIdx.x;
+    const int c = threadIdx.x;
+    const bool act = c < C;
+    const float mu = stats[2 * n], rs = stats[2 * n + 1];
+    NodeRegs r;
+    NodeMid m;
+    float xh[9], g[9];
+    float sg = 0.f, sgx = 0.f;
+    if (act) {
+        load_node(in, n, c, r);
+        node_mid(r, m);
+        float f[8];
+        node_invariants(r, m, f);
+        xh[0] = (p0[n * p0_sn + c] - mu) * rs;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) xh[1 + k] = (f[k] - mu) * rs;
+        const float* gr = gy + n * ld_gy + c;
+#pragma unroll
+        for (int k = 0; k < 9; ++k) {
+            g[k] = gr[k * C] * lw[k * C + c];
+            sg += g[k];
+            sgx = fmaf(g[k], xh[k], sgx);
+        }
+    }
+    const float F = 9.f * (float)C;
+    const float ag = wg_sum(sg, sh) / F, agx = wg_sum(sgx, sh) / F;
+    if (!act) return;                                  // every barrier is behind
+    dp0[n * dp0_sn + c] = rs * (g[0] - ag - xh[0] * agx);
+    float gi[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) gi[k] = rs * (g[1 + k] - ag - xh[1 + k] * agx);
+    float a0 = 0, a1 = 0, a2 = 0, a3 = 0, b0 = 0, b1 = 0, b2 = 0, b3 = 0;
+    float gv[3] = {0, 0, 0}, gm[9] = {0, 0, 0, 0, 0, 0, 0, 0, 0};
+    if (eq) {
+        a0 = av[c]; a1 = av[C + c]; a2 = av[2 * C + c]; a3 = av[3 * C + c];
+        b0 = bv[c]; b1 = bv[C + c]; b2 = bv[2 * C + c]; b3 = bv[3 * C + c];
+        if (gV) {
+#pragma unroll
+            for (int a = 0; a < 3; ++a) gv[a] = gV[n * sgv.sn + (int64_t)c * sgv.sc + a * sgv.sk];
+        }
+        if (gM) {
+            const float* gp = gM + n * sgm.sn + (int64_t)c * sgm.sc;
+            if (mf_mode == 0) {
+#pragma unroll
+                for (int k = 0; k < 9; ++k) gm[k] = gp[k * sgm.sk];
+            } else {
+#pragma unroll
+                for (int a = 0; a < 3; ++a)
+#pragma unroll
+                    for (int d = 0; d < 3; ++d)
+                        gm[a * 3 + d] = (a == d ? 1.f : 0.5f) * gp[sym2(a, d) * sgm.sk];
+            }
+        }
+    }
+    const int64_t t = n * C + c;
+    node_bwd_core(r, m, gi, gv, gm, a0, a1, a2, a3, b0, b1, b2, b3, out, n, c,
+                  (eq && da && db) ? da + t * 4 : nullptr, (eq && da && db) ? db + t * 4 : nullptr);
 }
 
 static bool fill_in(const float* const* ins, const int64_t* st, Strided8& s) {
@@ -395,6 +559,63 @@ extern "C" int face_node_bwd(const float* const* ins, const int64_t* in_strides,
     const int64_t total = N * (int64_t)C;
     hipLaunchKernelGGL(node_bwd_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream, s,
                        a, b, gI, sgi, gV, sgv, gM, sgm, mf_mode, o, da, db, N, C, eq);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int face_node_ln_fwd(const float* const* ins, const int64_t* in_strides, const float* p0, int64_t p0_sn,
+                                const float* a, const float* b, const float* ln_w, const float* ln_b, float eps,
+                                float* y, int64_t ld_y, float* stats, float* V, const int64_t* V_strides, float* Mf,
+                                const int64_t* Mf_strides, int32_t mf_mode, int64_t N, int32_t C, int32_t eq,
+                                void* stream) {
+    if (N < 0 || C <= 0 || C > 256 || !ins || !in_strides || !p0 || p0_sn < C || !ln_w || !ln_b || !y ||
+        ld_y < 9 * (int64_t)C || !stats)
+        return FACE_ERR_ARG;
+    if (eq && (!a || !b || !V || !V_strides || !Mf || !Mf_strides || (mf_mode != 0 && mf_mode != 1)))
+        return FACE_ERR_ARG;
+    if (N == 0) return 0;
+    Strided8 s;
+    if (!fill_in(ins, in_strides, s)) return FACE_ERR_ARG;
+    Str3 sv{0, 0, 0}, sm{0, 0, 0};
+    if (eq) {
+        sv = Str3{V_strides[0], V_strides[1], V_strides[2]};
+        sm = Str3{Mf_strides[0], Mf_strides[1], Mf_strides[2]};
+    }
+    const int block = (C + kWave - 1) / kWave * kWave;
+    hipLaunchKernelGGL(node_ln_fwd_kernel, dim3((unsigned)N), dim3(block), 0, (hipStream_t)stream, s, p0, p0_sn, a,
+                       b, ln_w, ln_b, eps, y, ld_y, stats, V, sv, Mf, sm, mf_mode, C, eq);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int face_node_ln_bwd(const float* const* ins, const int64_t* in_strides, const float* p0, int64_t p0_sn,
+                                const float* a, const float* b, const float* ln_w, const float* gy, int64_t ld_gy,
+                                const float* stats, const float* gV, const int64_t* gV_strides, const float* gM,
+                                const int64_t* gM_strides, int32_t mf_mode, float* const* outs,
+                                const int64_t* out_strides, float* dp0, int64_t dp0_sn, float* da, float* db,
+                                int64_t N, int32_t C, int32_t eq, void* stream) {
+    if (N < 0 || C <= 0 || C > 256 || !ins || !in_strides || !p0 || p0_sn < C || !ln_w || !gy ||
+        ld_gy < 9 * (int64_t)C || !stats || !outs || !out_strides || !dp0 || dp0_sn < C)
+        return FACE_ERR_ARG;
+    if (eq && (!a || !b || (mf_mode != 0 && mf_mode != 1))) return FACE_ERR_ARG;
+    if ((gV && !gV_strides) || (gM && !gM_strides)) return FACE_ERR_ARG;
+    if (N == 0) return 0;
+    Strided8 s;
+    if (!fill_in(ins, in_strides, s)) return FACE_ERR_ARG;
+    StridedOut8 o;
+    for (int k = 0; k < 8; ++k) {
+        if (!outs[k]) return FACE_ERR_ARG;
+        o.p[k] = outs[k];
+        o.sn[k] = out_strides[3 * k];
+        o.sc[k] = out_strides[3 * k + 1];
+        o.sk[k] = out_strides[3 * k + 2];
+    }
+    Str3 sgv{0, 0, 0}, sgm{0, 0, 0};
+    if (gV) sgv = Str3{gV_strides[0], gV_strides[1], gV_strides[2]};
+    if (gM) sgm = Str3{gM_strides[0], gM_strides[1], gM_strides[2]};
+    const int block = (C + kWave - 1) / kWave * kWave;
+    hipLaunchKernelGGL(node_ln_bwd_kernel, dim3((unsigned)N), dim3(block), 0, (hipStream_t)stream, s, p0, p0_sn, a,
+                       b, ln_w, gy, ld_gy, stats, gV, sgv, gM, sgm, mf_mode, o, dp0, dp0_sn, da, db, C, eq);
     FACE_LAUNCH_CHECK();
     return 0;
 }

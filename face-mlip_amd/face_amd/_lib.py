@@ -36,6 +36,9 @@ _SIGS = {
                                            P, I32, P, I32, P, P]),
     "face_node_fwd": (ctypes.c_int, [P, P, P, P, P, P, P, P, P, P, I32, I64, I32, I32, P]),
     "face_node_bwd": (ctypes.c_int, [P, P, P, P, P, P, P, P, P, P, I32, P, P, P, P, I64, I32, I32, P]),
+    "face_node_ln_fwd": (ctypes.c_int, [P, P, P, I64, P, P, P, P, F32, P, I64, P, P, P, P, P, I32, I64, I32, I32, P]),
+    "face_node_ln_bwd": (ctypes.c_int, [P, P, P, I64, P, P, P, P, I64, P, P, P, P, P, I32, P, P, P, I64, P, P, I64,
+                                        I32, I32, P]),
     "face_nbr_bin": (ctypes.c_int, [P, I64, P, P, P, P, P, P, P, P, P]),
     "face_nbr_count": (ctypes.c_int, [P, I64, P, P, P, P, P, F64, P, P, P, P, P, P, P]),
     "face_nbr_fill": (ctypes.c_int, [P, I64, P, P, P, P, P, F64, P, P, P, P, P, P, P, P, P, P, P, P]),
@@ -80,7 +83,7 @@ _SIGS = {
     "face_layer_norm_bwd": (ctypes.c_int, [P, P, I64, I32, P, P, P, P, P]),
 }
 
-ABI_VERSION = 21
+ABI_VERSION = 22
 
 
 class LinProblem(ctypes.Structure):

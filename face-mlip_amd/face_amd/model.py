@@ -379,13 +379,18 @@ class FactorBlock(nn.Module):
         allsets = sets + [A]
         # only P0 of rank 0 and P3, Q3 of rank 3 are used
         ws = [frozen(self.proj[l])[0][:(C, 3 * C, 3 * C, 2 * C)[l]] for l in range(4)]
+        nf = self.N_INV * C
+        # node algebra and the readout LayerNorm in one launch each way (the row never written)
+        fused_ln = not (READOUT_ROW_GEMM and C % 16 == 0 and nf <= 2048) and C <= 256
         feats_buf = None
         if C % 16 == 0:
             # proj over the concatenated moment sets as a sum of per-set products (no concat copy),
-            # all four ranks per launch, later sets accumulating in the epilogue; P0 (rank 0) is
-            # written straight into the first C columns of the readout row
-            feats_buf = torch.empty(g.N, self.N_INV * C, device=h.device)
-            ys = list(ops.rank_proj(ws, allsets, acc, out0=feats_buf[:, :C]))   # (k_l, N, C | 3C | 3C | 2C)
+            # all four ranks per launch, later sets accumulating in the epilogue; unless the
+            # LayerNorm is fused, P0 (rank 0) is written straight into the first C columns of the
+            # readout row
+            feats_buf = None if fused_ln else torch.empty(g.N, nf, device=h.device)
+            ys = list(ops.rank_proj(ws, allsets, acc,
+                                    out0=None if fused_ln else feats_buf[:, :C]))    # (k_l, N, C | 3C | 3C | 2C)
         else:
             ys = []
             for l in range(4):
@@ -395,13 +400,13 @@ class FactorBlock(nn.Module):
                     x2 = S[l].reshape(-1, C)
                     y = x2 @ Ws.t() if y is None else y.addmm_(x2, Ws.t())
                 ys.append(y.view(S[l].shape[0], S[l].shape[1], -1))
-        if self.eq_out:
-            feats, V, Ms = ops.node_features(ys[0], ys[1], ys[2], ys[3], self.vpath.detach(), self.mpath.detach(),
-                                             True, C, feats_buf)
+        ab = (self.vpath.detach(), self.mpath.detach()) if self.eq_out else (None, None)
+        if fused_ln:
+            inv, V, Ms = ops.node_ln(ys[0], ys[1], ys[2], ys[3], *ab, self.eq_out, C, self.norm.weight,
+                                     self.norm.bias, self.norm.eps)
         else:
-            feats, V, Ms = ops.node_features(ys[0], ys[1], ys[2], ys[3], None, None, False, C, feats_buf)
-        nf = self.N_INV * C
-        if READOUT_ROW_GEMM and C % 16 == 0 and nf <= 2048:
+            feats, V, Ms = ops.node_features(ys[0], ys[1], ys[2], ys[3], *ab, self.eq_out, C, feats_buf)
+        if not fused_ln and READOUT_ROW_GEMM and C % 16 == 0 and nf <= 2048:
             # LayerNorm, the out MLP and the residual split on the row GEMM (four launches forward;
             # opt-in: slower than the library GEMMs at the benchmark widths)
             rw = self._readout_weights()
@@ -411,10 +416,11 @@ class FactorBlock(nn.Module):
             if self.eq_out:
                 eq_new = ops.eq_gate(V, Ms, gvm)                                  # (3,N,C), (6,N,C)
             return e, h_new, A, eq_new
-        if nf % 4 == 0 and nf <= 2048:
-            inv = ops.layer_norm(feats, self.norm.weight.detach(), self.norm.bias.detach(), self.norm.eps)
-        else:
-            inv = F.layer_norm(feats, (nf,), self.norm.weight.detach(), self.norm.bias.detach(), self.norm.eps)
+        if not fused_ln:
+            if nf % 4 == 0 and nf <= 2048:
+                inv = ops.layer_norm(feats, self.norm.weight.detach(), self.norm.bias.detach(), self.norm.eps)
+            else:
+                inv = F.layer_norm(feats, (nf,), self.norm.weight.detach(), self.norm.bias.detach(), self.norm.eps)
         W0, b0 = frozen(self.out[0])
         W1, b1 = frozen(self.out[2])
         W2, b2 = frozen(self.out[4])

@@ -1169,6 +1169,87 @@ def node_features(y0, y1, y2, y3, a, b, eq, C, out=None):
     return NodeFeatures.apply(y0, y1, y2, y3, a, b, eq, C, (out,) if out is not None else ())
 
 
+class NodeLN(torch.autograd.Function):
+    """NodeFeatures followed by the readout LayerNorm (face/model.py:244-264, :140, :332) in one
+    launch each way: returns inv = LayerNorm([P0 | inv_1..inv_8]) (N, 9C) and, when eq, V, Ms.
+    The un-normalised row is never written (the backward recomputes it); the LayerNorm weight and
+    bias and the coefficients a, b are frozen."""
+
+    @staticmethod
+    def forward(ctx, y0, y1, y2, y3, a, b, eq, C, lw, lb, eps):
+        _lib.require_gpu(y0, y1, y2, y3)
+        N = y1.shape[1]
+        dev = y1.device
+        y1, y2, y3 = [y.contiguous().float() for y in (y1, y2, y3)]
+        p0 = y0[0, :, :C]
+        if p0.stride(1) != 1:
+            p0 = p0.contiguous()
+        ins = _pqs_views(y1, y2, y3, C)
+        st = sum((_s3(t) for t in ins), [])
+        lw_, lb_ = lw.detach().contiguous().float(), lb.detach().contiguous().float()
+        inv = torch.empty(N, 9 * C, device=dev)
+        stats = torch.empty(N, 2, device=dev)
+        V = Ms = None
+        z3 = [0, 0, 0]
+        if eq:
+            V = torch.empty(3, N, C, device=dev)
+            Ms = torch.empty(6, N, C, device=dev)
+            a_, b_ = a.contiguous().float(), b.contiguous().float()
+        else:
+            a_ = b_ = None
+        call("face_node_ln_fwd", _lib.ptr_array(ins), _lib.i64_array(st), ptr(p0), p0.stride(0), ptr(a_), ptr(b_),
+             ptr(lw_), ptr(lb_), float(eps), ptr(inv), 9 * C, ptr(stats), ptr(V),
+             _lib.i64_array(_s3(V.permute(1, 2, 0)) if eq else z3), ptr(Ms),
+             _lib.i64_array(_s3(Ms.permute(1, 2, 0)) if eq else z3), 1, N, C, int(bool(eq)), _lib.stream_of(y1),
+             label="node_ln_fwd")
+        ctx.save_for_backward(p0, y1, y2, y3, a_ if eq else torch.empty(0), b_ if eq else torch.empty(0), lw_, stats)
+        ctx.eq, ctx.C, ctx.y0_shape = eq, C, y0.shape
+        ctx.set_materialize_grads(False)
+        return inv, V, Ms
+
+    @staticmethod
+    def backward(ctx, ginv, gV, gMs):
+        p0, y1, y2, y3, a, b, lw, stats = ctx.saved_tensors
+        C, eq = ctx.C, ctx.eq
+        N = y1.shape[1]
+        dev = y1.device
+        ins = _pqs_views(y1, y2, y3, C)
+        st = sum((_s3(t) for t in ins), [])
+        dy1 = torch.empty_like(y1)
+        dy2 = torch.empty_like(y2)
+        dy3 = torch.empty_like(y3)
+        if dy3.shape[2] > 2 * C:
+            dy3[:, :, 2 * C:] = 0
+        outs = _pqs_views(dy1, dy2, dy3, C)
+        ginv = torch.zeros(N, 9 * C, device=dev) if ginv is None else ginv.contiguous().float()
+        # the kernel writes P0's gradient; wider y0 rows (other channels unused) start at zero
+        dy0 = torch.empty(ctx.y0_shape, device=dev) if ctx.y0_shape[2] == C else torch.zeros(ctx.y0_shape, device=dev)
+        need_ab = eq and (ctx.needs_input_grad[4] or ctx.needs_input_grad[5])
+        da = torch.empty(N, C, 4, device=dev) if need_ab else None
+        db = torch.empty(N, C, 4, device=dev) if need_ab else None
+        z3 = [0, 0, 0]
+        if gV is not None:
+            gV = gV.contiguous().float()
+        if gMs is not None:
+            gMs = gMs.contiguous().float()
+        dp0 = dy0[0, :, :C]
+        call("face_node_ln_bwd", _lib.ptr_array(ins), _lib.i64_array(st), ptr(p0), p0.stride(0),
+             ptr(a) if eq else None, ptr(b) if eq else None, ptr(lw), ptr(ginv), 9 * C, ptr(stats),
+             ptr(gV), _lib.i64_array(_s3(gV.permute(1, 2, 0)) if gV is not None else z3),
+             ptr(gMs), _lib.i64_array(_s3(gMs.permute(1, 2, 0)) if gMs is not None else z3), 1,
+             _lib.ptr_array(outs), _lib.i64_array(sum((_s3(t) for t in outs), [])), ptr(dp0), dp0.stride(0),
+             ptr(da), ptr(db), N, C, int(bool(eq)), _lib.stream_of(y1), label="node_ln_bwd")
+        ga = da.sum(0).t() if need_ab else None
+        gb = db.sum(0).t() if need_ab else None
+        return dy0, dy1, dy2, dy3, ga, gb, None, None, None, None, None
+
+
+def node_ln(y0, y1, y2, y3, a, b, eq, C, lw, lb, eps):
+    """(LayerNorm(feats) (N, 9C), V | None, Ms | None): node_features and the readout LayerNorm in
+    one launch each way (C <= 256)."""
+    return NodeLN.apply(y0, y1, y2, y3, a, b, eq, C, lw, lb, eps)
+
+
 # ----------------------------------------------------------------------------- row-block linear layers
 def lin(x, w, y, s_off=0, beta=0.0, x2=None, x_op=0, xz=None, bias=None, y0=None, n_y0=None):
     """One problem of rows_linear: y = (beta y0 + op(x | x2) w^T + bias) [* scales]; x (m, k1),

@@ -18,6 +18,7 @@
  *                                                                  -> face_density_mix_fwd / _bwd
  *   face/model.py:496-502        CP pooling bmm                   -> face_cp_density_fwd / _bwd
  *   face/node_kernel.py:164-209  NodeAlgebra / node_algebra       -> face_node_fwd / _bwd
+ *   face/model.py:244-249,332    node algebra + readout LayerNorm -> face_node_ln_fwd / _bwd
  *   face/model.py:286-296        gated equivariant outputs V*gv, Ms*gm -> face_eq_gate_fwd / _bwd
  *   face/model.py:140,332        readout nn.LayerNorm             -> face_layer_norm_fwd / _bwd
  *   face/neighbors.py:7-37       padded_graph (ASE neighbor_list) -> face_nbr_* (count, fill, rev, padded)
@@ -166,6 +167,26 @@ int face_node_bwd(const float* const* ins, const int64_t* in_strides, const floa
                   const float* gI, const int64_t* gI_strides, const float* gV, const int64_t* gV_strides,
                   const float* gM, const int64_t* gM_strides, int32_t mf_mode, float* const* outs,
                   const int64_t* out_strides, float* da, float* db, int64_t N, int32_t C, int32_t eq, void* stream);
+/* Node algebra fused with the readout LayerNorm (face/model.py:244-249, :140, :332): the row
+ * x = [P0 | inv_1 .. inv_8] (9C, family-major) of every atom is formed in registers and written
+ * normalised: y[n, k C + c] = (x - mean) rstd ln_w[kC + c] + ln_b[kC + c] (row stride ld_y), with
+ * stats[2n] = mean, stats[2n + 1] = rstd = 1 / sqrt(biased var + eps); P0 (N, C) row stride p0_sn;
+ * V / Mf as face_node_fwd. C <= 256. The row x itself is not written. */
+int face_node_ln_fwd(const float* const* ins, const int64_t* in_strides, const float* p0, int64_t p0_sn,
+                     const float* a, const float* b, const float* ln_w, const float* ln_b, float eps, float* y,
+                     int64_t ld_y, float* stats, float* V, const int64_t* V_strides, float* Mf,
+                     const int64_t* Mf_strides, int32_t mf_mode, int64_t N, int32_t C, int32_t eq, void* stream);
+/* Backward of face_node_ln_fwd for gy = dL/dy (row stride ld_gy) and gV, gM (may be NULL): the row
+ * recomputed from the inputs, dx = rstd (g - mean(g) - xh mean(g xh)), g = gy ln_w; dx's first C
+ * entries go to dp0 (row stride dp0_sn), the others through the node-algebra backward into outs
+ * (as face_node_bwd, with da / db). No LayerNorm weight gradients. */
+int face_node_ln_bwd(const float* const* ins, const int64_t* in_strides, const float* p0, int64_t p0_sn,
+                     const float* a, const float* b, const float* ln_w, const float* gy, int64_t ld_gy,
+                     const float* stats, const float* gV, const int64_t* gV_strides, const float* gM,
+                     const int64_t* gM_strides, int32_t mf_mode, float* const* outs, const int64_t* out_strides,
+                     float* dp0, int64_t dp0_sn, float* da, float* db, int64_t N, int32_t C, int32_t eq,
+                     void* stream);
+
 
 /* Gated equivariant outputs of a pass: Vo = V * gv, Mo = Ms * gm per (atom, channel), with
  * gvm = [gv | gm] (N, 2C) the gate row; V (3, N, C), Ms (6, N, C), Vo, Mo likewise, all

@@ -306,6 +306,58 @@ def test_node_features_product_layout():
     assert max(errs) < TOL, errs
 
 
+@pytest.mark.parametrize("N,C,eq,wide", [(37, 20, True, False), (50, 96, True, True), (23, 160, False, False),
+                                         (9, 256, True, False), (5, 40, False, True)])
+def test_node_layer_norm_fused_matches_oracle(N, C, eq, wide):
+    """Node algebra with the readout LayerNorm in one kernel each way (face/model.py:244-264, :332)
+    against the oracle's node algebra + torch layer_norm in fp64: the normalised row, V, Ms and
+    every input gradient; C not a multiple of the wave width, y0 rows wider than C."""
+    from face_amd import ops
+    say("node + layer norm", N, C, eq, wide)
+    torch.manual_seed(N + C)
+    y0 = torch.randn(1, N, 2 * C if wide else C, device=DEV, requires_grad=True)
+    y1 = torch.randn(3, N, 3 * C, device=DEV, requires_grad=True)
+    y2 = torch.randn(6, N, 3 * C, device=DEV, requires_grad=True)
+    y3 = torch.randn(10, N, 2 * C, device=DEV, requires_grad=True)
+    a = torch.randn(4, C, device=DEV) if eq else None
+    b = torch.randn(4, C, device=DEV) if eq else None
+    lw = torch.rand(9 * C, device=DEV) + 0.5
+    lb = torch.randn(9 * C, device=DEV) * 0.1
+    inv, V, Ms = ops.node_ln(y0, y1, y2, y3, a, b, eq, C, lw, lb, 1e-5)
+    gi = torch.randn_like(inv)
+    L = (inv * gi).sum()
+    if eq:
+        gv, gm = torch.randn_like(V), torch.randn_like(Ms)
+        L = L + (V * gv).sum() + (Ms * gm).sum()
+    vars1 = [y0, y1, y2, y3]
+    g1 = torch.autograd.grad(L, vars1)
+    yc = [t.detach().double().cpu().requires_grad_(True) for t in vars1]
+    c0, c1, c2, c3 = yc
+    ac = a.double().cpu() if eq else torch.zeros(4, C, dtype=torch.float64)
+    bc = b.double().cpu() if eq else torch.zeros(4, C, dtype=torch.float64)
+    split = lambda y, k: [y[..., j * C:(j + 1) * C].permute(1, 2, 0) for j in range(k)]
+    P1, Q1, S1 = split(c1, 3)
+    P2, Q2, S2 = split(c2, 3)
+    P3, Q3 = split(c3, 2)
+    invr, Vr, Mf = oops.node_algebra_sym(P1, Q1, S1, P2, Q2, S2, P3, Q3, ac, bc)
+    feats = torch.cat([c0[0, :, :C]] + list(invr.unbind(-1)), 1)
+    inv2 = torch.nn.functional.layer_norm(feats, (9 * C,), lw.double().cpu(), lb.double().cpu(), 1e-5)
+    L2 = (inv2 * gi.double().cpu()).sum()
+    outs, refs = [inv], [inv2]
+    if eq:
+        Ms2 = cartesian.to_sym2(0.5 * (Mf + Mf.transpose(-1, -2))).permute(2, 0, 1)
+        V2 = Vr.permute(2, 0, 1)
+        L2 = L2 + (V2 * gv.double().cpu()).sum() + (Ms2 * gm.double().cpu()).sum()
+        outs += [V, Ms]
+        refs += [V2, Ms2]
+    g2 = torch.autograd.grad(L2, yc)
+    errs = [rel(u, v) for u, v in zip(outs, refs)] + [rel(u, v) for u, v in zip(g1, g2)]
+    say("   errs", errs)
+    assert max(errs) < TOL, errs
+    if wide:
+        assert float(g1[0][0, :, C:].abs().max()) == 0.0
+
+
 # ----------------------------------------------------------------------------- gathers / scatter
 def test_gathers_and_force_scatter_match_index_add():
     from face_amd import ops
