@@ -57,7 +57,8 @@ KERNEL_FAMILY = {
     "edge_fwd": "edge_geom_fwd", "edge_bwd": "edge_geom_bwd", "force_scatter": "force_scatter",
     "gather_bwd": "gather_rows_bwd", "radial_fwd": "radial_fwd", "radial_bwd": "radial_bwd",
     "radial_head": "edge_linear_fwd", "edge_msg_fwd": "edge_linear_fwd", "edge_msg_bwd": "edge_linear_bwd",
-    "mix_fwd": "rows_gemm", "mix_bwd": "rows_gemm", "tmix_bwd": "rows_gemm", "proj_fwd": "rows_gemm",
+    "mix_fwd": "rows_gemm", "mix_bwd": "rows_gemm", "tmix_bwd": "rows_gemm", "mix_tmix_bwd": "rows_gemm",
+    "proj_fwd": "rows_gemm",
     "proj_bwd": "rows_gemm", "readout_in": "rows_gemm", "readout_hid": "rows_gemm", "readout_out": "rows_gemm",
     "readout_in_bwd": "rows_gemm", "readout_hid_bwd": "rows_gemm", "readout_out_bwd": "rows_gemm",
     "eq_gate_fwd": "eq_gate_fwd", "eq_gate_bwd": "eq_gate_bwd",
@@ -229,6 +230,8 @@ def algorithmic_flops(label, g, kw):
         return 2 * N * C * (C + 3 * 3 * C + 6 * 3 * C + 10 * 2 * C)
     if label == "tmix_bwd":             # (3 + 6) N rows of C -> B * 2 K_dir transport columns
         return 2 * 9 * N * C * kw["B"] * 2 * kw["K_dir"]
+    if label == "mix_tmix_bwd":         # both in one launch
+        return algorithmic_flops("mix_bwd", g, kw) + algorithmic_flops("tmix_bwd", g, kw)
     if label == "radial_head":
         return 2 * E * H * 4 * C
     if label in ("edge_msg_fwd", "edge_msg_bwd"):

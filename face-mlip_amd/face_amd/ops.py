@@ -1328,8 +1328,8 @@ class ScaledMix(torch.autograd.Function):
               for g, sh in zip(gA, ctx.shapes)]
         dAf = [torch.empty(sh, device=dev) for sh in ctx.shapes]
         probs = [(g.view(-1, C), ctx.wm[l], dAf[l].view(-1, dAf[l].shape[-1]), l * C, 0.0) for l, g in enumerate(gA)]
-        rows_linear(probs, w_kn=True, xs=s_tab, group=group, period=N, label="mix_bwd")
-        # transport mix: dD_l = (gA_l * s_l) wt, the scale applied to the rows as they load
+        # transport mix: dD_l = (gA_l * s_l) wt, the scale applied to the rows as they load; in
+        # the same launch as the mix backward (same scale table, up to 6 problems)
         dD = [None, None]
         tp = []
         for i, l in enumerate((1, 2)):
@@ -1337,8 +1337,8 @@ class ScaledMix(torch.autograd.Function):
                 wt = ctx.wt[i]
                 dD[i] = torch.empty(gA[l].shape[0], N, wt.shape[1], device=dev)
                 tp.append((gA[l].view(-1, C), wt, dD[i].view(-1, wt.shape[1]), l * C, 0.0))
-        if tp:
-            rows_linear(tp, w_kn=True, xs=s_tab, group=group, period=N, label="tmix_bwd")
+        rows_linear(probs + tp, w_kn=True, xs=s_tab, group=group, period=N,
+                    label="mix_tmix_bwd" if tp else "mix_bwd")
         return (None, None, None, None, dD[0], dD[1], *dAf)
 
 
