@@ -1293,6 +1293,11 @@ def rows_linear(probs, w_kn=False, bias=None, xs=None, ys=None, group=None, peri
          _lib.stream_of(ref), label=label)
 
 
+# mix and transport-mix backward in one launch up to this many atoms (launch-bound sizes; at
+# 24,000 atoms the six-problem launch measured 646 us against 238 + 354 us for the two)
+MIX_MERGE_MAX_ATOMS = 4096
+
+
 class ScaledMix(torch.autograd.Function):
     """A_l = (Af_l W_l^T [+ D_l T_l^T]) * s[z] for the four ranks l (face/model.py:498-501, the
     transport terms of :530-533 for l = 1, 2): s = elem_scale / avg_nb per atom (s_tab (n_el, 4C),
@@ -1328,8 +1333,8 @@ class ScaledMix(torch.autograd.Function):
               for g, sh in zip(gA, ctx.shapes)]
         dAf = [torch.empty(sh, device=dev) for sh in ctx.shapes]
         probs = [(g.view(-1, C), ctx.wm[l], dAf[l].view(-1, dAf[l].shape[-1]), l * C, 0.0) for l, g in enumerate(gA)]
-        # transport mix: dD_l = (gA_l * s_l) wt, the scale applied to the rows as they load; in
-        # the same launch as the mix backward (same scale table, up to 6 problems)
+        # transport mix: dD_l = (gA_l * s_l) wt, the scale applied to the rows as they load; for
+        # small systems in the same launch as the mix backward (same scale table, 6 problems)
         dD = [None, None]
         tp = []
         for i, l in enumerate((1, 2)):
@@ -1337,8 +1342,12 @@ class ScaledMix(torch.autograd.Function):
                 wt = ctx.wt[i]
                 dD[i] = torch.empty(gA[l].shape[0], N, wt.shape[1], device=dev)
                 tp.append((gA[l].view(-1, C), wt, dD[i].view(-1, wt.shape[1]), l * C, 0.0))
-        rows_linear(probs + tp, w_kn=True, xs=s_tab, group=group, period=N,
-                    label="mix_tmix_bwd" if tp else "mix_bwd")
+        if tp and N <= MIX_MERGE_MAX_ATOMS:
+            rows_linear(probs + tp, w_kn=True, xs=s_tab, group=group, period=N, label="mix_tmix_bwd")
+        else:
+            rows_linear(probs, w_kn=True, xs=s_tab, group=group, period=N, label="mix_bwd")
+            if tp:
+                rows_linear(tp, w_kn=True, xs=s_tab, group=group, period=N, label="tmix_bwd")
         return (None, None, None, None, dD[0], dD[1], *dAf)
 
 

@@ -961,12 +961,15 @@ def test_readout_matches_torch(C, gate):
     assert max(errs) < 1e-5, errs
 
 
-@pytest.mark.parametrize("transport,Cin", [(True, 160), (False, 160), (False, 512), (True, 32)])
-def test_scaled_mix_forward_backward(transport, Cin):
+@pytest.mark.parametrize("transport,Cin,merge", [(True, 160, True), (True, 160, False), (False, 160, True),
+                                                  (False, 512, True), (True, 32, True)])
+def test_scaled_mix_forward_backward(transport, Cin, merge, monkeypatch):
     """A_l = (Af_l W_l^T [+ D_l T_l^T]) * s[z] for the four ranks (face/model.py:498-501, :530-533)
-    and the gradients of Af_l and D_l vs torch fp64 autograd."""
+    and the gradients of Af_l and D_l vs torch fp64 autograd (the transport-mix backward in the
+    mix backward's launch and on its own)."""
     from face_amd import ops
-    say("scaled mix", transport, Cin)
+    monkeypatch.setattr(ops, "MIX_MERGE_MAX_ATOMS", 1 << 30 if merge else 0)
+    say("scaled mix", transport, Cin, merge)
     torch.manual_seed(Cin + transport)
     N, C, Dw = 517, 96 if Cin != 32 else 32, 64
     grp = torch.randint(0, 3, (N,), device=DEV, dtype=torch.int32)
