@@ -230,6 +230,20 @@ class FactorBlock(nn.Module):
             self.tmix3 = nn.Linear(B * 2 * K_dir, C, bias=False)
 
     # ------------------------------------------------------------------ moments
+    def h_products(self, h):
+        """(msg(h), b0 + h W0b^T) of a pass whose h is a constant of the evaluation (the first pass's
+        embedding rows, a function of the species): cached per h and weights."""
+        Wm, bm = frozen(self.msg)
+        W0, b0 = frozen(self.out[0])
+        nf = self.N_INV * self.C
+        key = _key(h, Wm, bm, W0, b0)
+        c = self.__dict__.get("_hprod")
+        if c is None or not _same(c[0], key):
+            with torch.no_grad():
+                c = (key, F.linear(h, Wm, bm), torch.addmm(b0, h, W0[:, nf:nf + self.C].t()))
+            self.__dict__["_hprod"] = c
+        return c[1], c[2]
+
     def radial_weights(self):
         """(w_in, b_in, pair_tab, w1, b1, w_phi, b_phi) of the fused radial MLP: the phi columns of
         the last radial layer (its CP columns are a GEMM on h2)."""
@@ -260,7 +274,8 @@ class FactorBlock(nn.Module):
             # hidden layers and phi columns of the radial MLP in one HIP kernel; the CP columns of
             # the last layer are a GEMM on its h2 output; phi once per reader (density, transport)
             phi, phi_dir, h2 = ops.radial_mlp(rb, env_rad, zp, *self.radial_weights(), self.cp)   # (E, B) x2, (E, H)
-        msg_n = F.linear(h, *frozen(self.msg))                                   # (N, K)
+        # (N, K); the first pass's h is the embedding rows, a constant: its products are cached
+        msg_n = self.h_products(h)[0] if not h.requires_grad else F.linear(h, *frozen(self.msg))
         if self.directional:
             if self.eq_in:
                 src1, src2 = eq                                                  # (3,N,C), (6,N,C)
@@ -427,7 +442,8 @@ class FactorBlock(nn.Module):
         Wg, bg = frozen(self.gate) if self.eq_out else (None, None)
         # out MLP on cat([inv, h, 0 (4)]) (two accumulating GEMMs, no concatenated copy), residual
         # and gate row as one autograd node; the last pass computes the energy row only
-        e, h_new, gvm = ops.readout_mlp(inv, h, W0[:, :nf], W0[:, nf:nf + C], b0, W1, b1, W2, b2, Wg, bg, last)
+        hb = self.h_products(h)[1] if not h.requires_grad else None
+        e, h_new, gvm = ops.readout_mlp(inv, h, W0[:, :nf], W0[:, nf:nf + C], b0, W1, b1, W2, b2, Wg, bg, last, hb)
         eq_new = None
         if self.eq_out:
             if C % 4 == 0:

@@ -360,12 +360,15 @@ class ReadoutMLP(torch.autograd.Function):
     term in the second GEMM's epilogue, d h = gh + dz0 W0[:, 9C:10C] in one GEMM. last (the final
     pass, whose h_new nobody reads): only the energy row of the last layer is computed and its
     input gradient is the outer product ge W2[0]. W0a / W0b are the inv / h column blocks of W0.
-    Weights receive no gradient."""
+    Weights receive no gradient; h's only when h takes one (the first pass's rows are constants)."""
 
     @staticmethod
-    def forward(ctx, inv, h, W0a, W0b, b0, W1, b1, W2, b2, Wg, bg, last):
-        z0 = torch.addmm(b0, inv, W0a.t())
-        z0.addmm_(h, W0b.t())
+    def forward(ctx, inv, h, W0a, W0b, b0, W1, b1, W2, b2, Wg, bg, last, hb):
+        if hb is not None:                                # b0 + h W0b^T precomputed (h a constant)
+            z0 = torch.addmm(hb, inv, W0a.t())
+        else:
+            z0 = torch.addmm(b0, inv, W0a.t())
+            z0.addmm_(h, W0b.t())
         z1 = torch.addmm(b1, torch.nn.functional.silu(z0), W1.t())
         a1 = torch.nn.functional.silu(z1)
         if last:
@@ -400,13 +403,16 @@ class ReadoutMLP(torch.autograd.Function):
         dinv = dz0 @ W0a
         if ggvm is not None and Wg is not None:
             dinv.addmm_(ggvm, Wg)
-        dh = torch.addmm(gh, dz0, W0b) if (not ctx.last) else dz0 @ W0b
-        return dinv, dh, None, None, None, None, None, None, None, None, None, None
+        dh = None
+        if ctx.needs_input_grad[1]:                       # not for the first pass's constant rows
+            dh = torch.addmm(gh, dz0, W0b) if (not ctx.last) else dz0 @ W0b
+        return dinv, dh, None, None, None, None, None, None, None, None, None, None, None
 
 
-def readout_mlp(inv, h, W0a, W0b, b0, W1, b1, W2, b2, Wg=None, bg=None, last=False):
-    """(e (N, 1), h_new (N, C) | None when last, gvm (N, 2C) | None); see ReadoutMLP."""
-    return ReadoutMLP.apply(inv, h, W0a, W0b, b0, W1, b1, W2, b2, Wg, bg, last)
+def readout_mlp(inv, h, W0a, W0b, b0, W1, b1, W2, b2, Wg=None, bg=None, last=False, hb=None):
+    """(e (N, 1), h_new (N, C) | None when last, gvm (N, 2C) | None); see ReadoutMLP. hb: b0 + h W0b^T
+    when h is a constant of the evaluation (no gradient), computed once."""
+    return ReadoutMLP.apply(inv, h, W0a, W0b, b0, W1, b1, W2, b2, Wg, bg, last, hb)
 
 
 class AtomEnergy(torch.autograd.Function):
