@@ -61,6 +61,7 @@ KERNEL_FAMILY = {
     "proj_fwd": "rows_gemm",
     "proj_bwd": "rows_gemm", "readout_in": "rows_gemm", "readout_hid": "rows_gemm", "readout_out": "rows_gemm",
     "readout_in_bwd": "rows_gemm", "readout_hid_bwd": "rows_gemm", "readout_out_bwd": "rows_gemm",
+    "table_linear_fwd": "rows_gemm", "table_linear_bwd": "rows_gemm",
     "eq_gate_fwd": "eq_gate_fwd", "eq_gate_bwd": "eq_gate_bwd",
     "ln_fwd": "layer_norm_fwd", "ln_bwd": "layer_norm_bwd", "spline_order": "spline_order",
     "spline_fwd": "radial_spline_fwd", "spline_bwd": "radial_spline_bwd",
@@ -230,6 +231,8 @@ def algorithmic_flops(label, g, kw):
         return 2 * N * C * (C + 3 * 3 * C + 6 * 3 * C + 10 * 2 * C)
     if label == "tmix_bwd":             # (3 + 6) N rows of C -> B * 2 K_dir transport columns
         return 2 * 9 * N * C * kw["B"] * 2 * kw["K_dir"]
+    if label in ("table_linear_fwd", "table_linear_bwd"):   # (3 + 6) N rows, C <-> nt K_dir
+        return 2 * 9 * N * C * 2 * kw["K_dir"]
     if label == "mix_tmix_bwd":         # both in one launch
         return algorithmic_flops("mix_bwd", g, kw) + algorithmic_flops("tmix_bwd", g, kw)
     if label == "radial_head":

@@ -282,8 +282,8 @@ class FactorBlock(nn.Module):
             else:
                 src1 = torch.cat([S[1] for S in sets], -1)
                 src2 = torch.cat([S[2] for S in sets], -1)
-            Vb = F.linear(src1, frozen(self.pvt)[0])                             # (3, N, nt*Kd)
-            Mb = F.linear(src2, frozen(self.pmt)[0])                             # (6, N, nt*Kd)
+            # (3, N, nt*Kd), (6, N, nt*Kd): one launch each way
+            Vb, Mb = ops.table_linears(src1, src2, frozen(self.pvt)[0], frozen(self.pmt)[0])
             d, D1, D2 = ops.dir_transport(Vb, Mb, phi_dir, Y_dir, g, Kd, self.transport)   # (E, 4Kd), sums
             # gather(msg(h)) + dir_mix(d) as one per-edge matrix-core launch (and one backward)
             Wd, bd = frozen(self.dir_mix)

@@ -348,6 +348,48 @@ def layer_norm(x, w, b, eps):
     return LayerNorm.apply(x, w.contiguous(), b.contiguous(), eps)
 
 
+class TableLinears(torch.autograd.Function):
+    """The directional table linears of a pass, Vb = V pvt^T (3, N, n) and Mb = Ms pmt^T (6, N, n)
+    (face/model.py:474-479), as one row-GEMM launch of two problems each way (input gradients
+    only; the weights are constants of the evaluation)."""
+
+    @staticmethod
+    def forward(ctx, V, Ms, wv, wm):
+        _lib.require_gpu(V, Ms, wv, wm)
+        C = V.shape[-1]
+        V_, Ms_ = V.contiguous().float(), Ms.contiguous().float()
+        Vb = torch.empty(V.shape[0], V.shape[1], wv.shape[0], device=V.device)
+        Mb = torch.empty(Ms.shape[0], Ms.shape[1], wm.shape[0], device=V.device)
+        rows_linear([(V_.view(-1, C), wv, Vb.view(-1, wv.shape[0]), 0, 0.0),
+                     (Ms_.view(-1, C), wm, Mb.view(-1, wm.shape[0]), 0, 0.0)], label="table_linear_fwd")
+        ctx.wv, ctx.wm, ctx.shapes = wv, wm, (V.shape, Ms.shape)
+        ctx.set_materialize_grads(False)
+        return Vb, Mb
+
+    @staticmethod
+    def backward(ctx, gVb, gMb):
+        wv, wm = ctx.wv, ctx.wm
+        (sv, sm), dev = ctx.shapes, wv.device
+        probs, dV, dMs = [], None, None
+        if gVb is not None and ctx.needs_input_grad[0]:
+            dV = torch.empty(sv, device=dev)
+            probs.append((gVb.contiguous().float().view(-1, wv.shape[0]), wv, dV.view(-1, sv[-1]), 0, 0.0))
+        if gMb is not None and ctx.needs_input_grad[1]:
+            dMs = torch.empty(sm, device=dev)
+            probs.append((gMb.contiguous().float().view(-1, wm.shape[0]), wm, dMs.view(-1, sm[-1]), 0, 0.0))
+        if probs:
+            rows_linear(probs, w_kn=True, label="table_linear_bwd")
+        return dV, dMs, None, None
+
+
+def table_linears(V, Ms, wv, wm):
+    """(V wv^T, Ms wm^T) for (3|6, N, C) tables: one launch each way (C and the output width
+    multiples of 16), else torch's linears."""
+    if V.shape[-1] % 16 == 0 and wv.shape[0] % 16 == 0 and wm.shape[0] % 16 == 0:
+        return TableLinears.apply(V, Ms, wv.contiguous(), wm.contiguous())
+    return torch.nn.functional.linear(V, wv), torch.nn.functional.linear(Ms, wm)
+
+
 def dir_transport(Vb, Mb, phi, Y, graph, Kd, transport):
     return DirTransport.apply(Vb, Mb, phi, Y, graph, Kd, transport)
 

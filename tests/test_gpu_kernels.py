@@ -1114,3 +1114,24 @@ def test_atom_energy_matches_index_add(with_at):
     want = torch.autograd.grad(routs, rows, gouts)
     for a, b in zip(got, want):
         assert torch.allclose(a, b, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("N,C,n", [(864, 96, 32), (37, 160, 48)])
+def test_table_linears_match_torch(N, C, n):
+    """The pass's directional table linears V pvt^T, Ms pmt^T (face/model.py:474-479) in one
+    launch each way, forward and input gradients against torch fp64."""
+    from face_amd import ops
+    say("table linears", N, C, n)
+    torch.manual_seed(N + C)
+    V = torch.randn(3, N, C, device=DEV, requires_grad=True)
+    Ms = torch.randn(6, N, C, device=DEV, requires_grad=True)
+    wv = torch.randn(n, C, device=DEV) / C ** 0.5
+    wm = torch.randn(n, C, device=DEV) / C ** 0.5
+    Vb, Mb = ops.table_linears(V, Ms, wv, wm)
+    gv, gm = torch.randn_like(Vb), torch.randn_like(Mb)
+    got = torch.autograd.grad((Vb * gv).sum() + (Mb * gm).sum(), (V, Ms))
+    Vc, Mc = V.detach().double().cpu().requires_grad_(True), Ms.detach().double().cpu().requires_grad_(True)
+    Vr, Mr = Vc @ wv.double().cpu().T, Mc @ wm.double().cpu().T
+    want = torch.autograd.grad((Vr * gv.double().cpu()).sum() + (Mr * gm.double().cpu()).sum(), (Vc, Mc))
+    errs = [rel(Vb, Vr), rel(Mb, Mr)] + [rel(a, b) for a, b in zip(got, want)]
+    assert max(errs) < 1e-5, errs
