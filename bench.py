@@ -877,7 +877,7 @@ def main():
         "steps": a.steps, "warmup": a.warmup, "ms_per_step": main_run["ms_per_step"], "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
         "config": {"workload": main_run["desc"], "atoms": main_run["N"], "pairs": main_run["E"],
-                   "model": {k: kw[k] for k in ("C", "B", "K", "rc") if k in kw} | {"cp": bool(kw.get("cp"))},
+                   "potential": {k: kw[k] for k in ("C", "B", "K", "rc") if k in kw} | {"cp": bool(kw.get("cp"))},
                    "weights": "random init, torch.manual_seed(0) + unit_parameterise", "parallelism": "single GPU",
                    "library_gemms": ("fp32 hipBLASLt/rocBLAS, solutions picked by PyTorch TunableOp in the warm-up"
                                      if tunable else "fp32 hipBLASLt default solutions"),
