@@ -13,13 +13,17 @@ it from its timings, tools/bench.py:4). Workloads (face_amd.systems.workload):
   4  100,000-atom H:C:O liquid, FACE C256 B16 K64 rc 5.5
 Timing follows the reference's protocol (tools/bench_review.py:53-69): W warm-up steps, then
 rounds of 5 calls, each round bracketed by torch.cuda.synchronize(); ms/step is the median
-over the rounds (min and max reported beside it). K = 35 steps = 7 rounds by default.
-Prints ONE JSON line; progress goes to stderr.
+over the rounds (min and max reported beside it). At least 7 rounds are timed whatever K is
+(K is raised to whole rounds, >= 35 steps); the line's `steps` is the number actually timed.
+Prints ONE compact JSON line (a few KB: headline, roofline, CPU baseline, one short record per
+other workload); progress and the per-label / per-family detail ([bench-detail] lines) go to
+stderr, and to --detail-out FILE when given.
 
 Profile summaries (text under profiles/) are written by the summary modes from rocprofv3 output:
   --pmc-probe                       short eager run for `rocprofv3 --pmc` passes (one counter each)
   --pmc-summary FETCH_DIR WRITE_DIR  HBM traffic per call label / kernel family from the two passes
-  --trace-summary STATS_CSV          kernel-time summary of a `rocprofv3 --kernel-trace --stats` run
+  --trace-summary STATS_CSV          per-workload kernel-time summary of a `rocprofv3 --kernel-trace
+                                    --stats` run (the timed replays between each workload's two marks)
 """
 import argparse
 import json
@@ -185,6 +189,23 @@ def algorithmic_bytes(label, g, kw):
         return 4 * 20 * N * C
     if label == "eq_gate_bwd":          # + upstream (9); dV, dMs (9), gate-row gradient (2) out
         return 4 * 31 * N * C
+    if label == "dir_fwd":              # the 9 used monomials, col, the directional half of V|M (9 Kd per
+        return 4 * (E * (9 + 1 + Kd4) + 9 * N * kw["K_dir"])  # node) in; d (E, 4 Kd) out
+    if label == "dir_bwd":              # gd, 9 monomials, col + rev, tables in; gY (20), table grads out
+        return 4 * (E * (Kd4 + 9 + 2 + 20) + 18 * N * kw["K_dir"])
+    # row GEMMs: the rows read once, the weights once, the outputs written once (no initial sums)
+    cin = C if kw.get("cp") else B * kw["K"]
+    T = B * 2 * kw["K_dir"]             # transport columns
+    if label in ("mix_fwd", "mix_bwd"):   # 20 N rows, cin <-> C, one weight per rank
+        return 4 * (20 * N * (cin + C) + 4 * cin * C)
+    if label in ("proj_fwd", "proj_bwd"):  # 20 N rows of C <-> N (C + 9C + 18C + 20C); weights 9 C^2
+        return 4 * (20 * N * C + 48 * N * C + 9 * C * C)
+    if label == "tmix_bwd":             # 9 N rows, C -> T
+        return 4 * (9 * N * (C + T) + C * T)
+    if label == "mix_tmix_bwd":
+        return algorithmic_bytes("mix_bwd", g, kw) + algorithmic_bytes("tmix_bwd", g, kw)
+    if label in ("table_linear_fwd", "table_linear_bwd"):   # (3 + 6) N rows, C <-> 2 K_dir, two weights
+        return 4 * (9 * N * (C + 2 * kw["K_dir"]) + 2 * C * 2 * kw["K_dir"])
     if label == "ln_fwd":               # row of 9C in and out (+ mean, rstd)
         return 4 * (2 * 9 * C + 2) * N
     if label == "ln_bwd":
@@ -216,7 +237,8 @@ def algorithmic_flops(label, g, kw):
     head (E x H by H x 4C), the pass message's d W_d^T (E x 4Kd by 4Kd x K) and its input
     gradient, the fused CP radial backward (d h2 = dR W_cp, E x 4C by 4C x H, plus the two
     20-monomial contractions per edge and channel), and the factor density's per-monomial
-    products (2 E 20 B K each way; 3 of them in the backward)."""
+    products (2 E 20 B K each way; 3 of them in the backward), and the radial MLP of each pass (nb ->
+    H -> H -> B per edge; the backward recomputes the hidden layers instead of reading them)."""
     label, units = split_label(label)
     if units > 1:
         one = algorithmic_flops(label, g, kw)
@@ -241,6 +263,11 @@ def algorithmic_flops(label, g, kw):
         return 2 * E * 4 * kw["K_dir"] * K
     if label.startswith("cp_radial_bwd"):
         return 2 * E * (4 * C * H + 2 * 20 * C)
+    nb, B = kw.get("n_basis", 8), kw["B"]
+    if label == "radial_fwd":           # per pass: nb -> H -> H -> B (phi; h2 is the second layer)
+        return 2 * E * (nb * H + H * H + H * B)
+    if label == "radial_bwd":           # the two hidden layers recomputed, then B -> H -> H -> nb
+        return 2 * E * (nb * H + H * H) + 2 * E * (B * H + H * H + H * nb)
     # readout (per launch, averaged over the passes: the gate row only where a pass has
     # equivariant outputs, i.e. all passes but the last with eqmsg)
     gate = (kw.get("n_passes", 2) - 1) / kw.get("n_passes", 2) if kw.get("eqmsg") else 0.0
@@ -369,6 +396,19 @@ def roofline_of(fam, tag):
             else None}
 
 
+def trace_mark():
+    """One launch of a kernel the model never runs (the gather form of the force scatter, on one
+    atom), outside any timed region: in a kernel trace, the dispatches between two marks are
+    exactly the timed replays of one workload."""
+    from face_amd import _lib
+    torch.cuda.synchronize()
+    z = torch.zeros(2, dtype=torch.int32, device="cuda")
+    mark = torch.empty(1, 3, device="cuda")
+    _lib.call("face_force_scatter", _lib.ptr(mark), _lib.ptr(z), _lib.ptr(z), 1, 1.0, _lib.ptr(mark),
+              _lib.stream_of(mark))
+    torch.cuda.synchronize()
+
+
 def run_gpu(k, steps, warmup, use_graph=True, compiled_radial=False):
     from face_amd import _lib, systems
     from face_amd.neighbors import build_graph
@@ -412,7 +452,9 @@ def run_gpu(k, steps, warmup, use_graph=True, compiled_radial=False):
         pos = g.pos.clone()
         for _ in range(warmup):
             run(pos)
+        trace_mark()
         rounds = timed_rounds(lambda: run(pos), steps)
+        trace_mark()
         mode = "hipgraph"
         del run
     ms = [1e3 * x for x in rounds]
@@ -476,7 +518,8 @@ def run_cpu(k, budget_s=10.0, full=False):
             "ms_per_step": 1e3 * med, "ms_min": 1e3 * min(ts), "ms_max": 1e3 * max(ts),
             "sample": f"{what} ({N} atoms, {desc.split(',')[-1].strip()}), oracle torch path (unfused, as the "
                       f"reference's torch path), fp32, median of {rounds} single E+F calls after 1 warm-up "
-                      f"({t_warm:.1f} s), torch.set_num_threads({cores})"}
+                      f"({t_warm:.1f} s), torch.set_num_threads({cores}); bounded to ~{budget_s:.0f} s of CPU "
+                      f"work instead of the planned 3 warm-ups + 7 x 5 calls"}
 
 
 # ----------------------------------------------------------------------------- profiler helpers
@@ -494,13 +537,17 @@ def pmc_probe(k, steps=2, copy_floats=1 << 28):
     # launch (the gather form of the force scatter, which the model does not use) whose dispatch
     # separates that step's (and the shape timing's) dispatches from the recorded steps'
     m(g.with_pos(g.pos.clone()))["forces"]
-    torch.cuda.synchronize()
+    trace_mark()
+    # a marker after every library call: the dispatches between two markers are one call's
+    L = _lib.lib()
     z = torch.zeros(2, dtype=torch.int32, device="cuda")
     mark = torch.empty(1, 3, device="cuda")
-    _lib.call("face_force_scatter", _lib.ptr(mark), _lib.ptr(z), _lib.ptr(z), 1, 1.0, _lib.ptr(mark),
-              _lib.stream_of(mark))
-    torch.cuda.synchronize()
-    order = _lib.record_order(True)
+    st = _lib.stream_of(mark)
+
+    def after_call():
+        L.face_force_scatter(_lib.ptr(mark), _lib.ptr(z), _lib.ptr(z), 1, 1.0, _lib.ptr(mark), st)
+
+    order = _lib.record_order(True, after=after_call)
     for _ in range(steps):
         m(g.with_pos(g.pos.clone()))["forces"]
     torch.cuda.synchronize()
@@ -523,35 +570,28 @@ PROBE_MARK = "force_scatter_kernel"
 
 
 def _after_mark(rows):
-    """Dispatch records (sorted by Dispatch_Id) after the probe's marker launch."""
+    """Dispatch records (sorted by Dispatch_Id) after the probe's first marker launch (the one
+    between the untimed first step and the recorded steps)."""
     ids = [i for i, r in enumerate(rows) if _kernel_base(r["Kernel_Name"]) == PROBE_MARK]
-    return rows[ids[-1] + 1:] if ids else rows
+    return rows[ids[0] + 1:] if ids else rows
 
 
 def _label_dispatches(rows, order, what):
-    """(label, record) for the library dispatches of a probe run, in order: a dispatch of a kernel
-    that serves call labels (KERNEL_FAMILY) takes the next of those labels in the probe's call order;
-    other library kernels get label None."""
-    import collections
-    by_base = collections.defaultdict(list)
-    for lab, fam in KERNEL_FAMILY.items():
-        for kname in FAMILY_KERNELS[fam]:
-            by_base[kname].append(lab)
-    seq = {b: [lab for lab in order if split_label(lab)[0] in labs] for b, labs in by_base.items()}
-    pos = collections.Counter()
-    out = []
+    """(label, record) for the library dispatches of a probe run, in order. The probe launches a
+    marker after every library call of the recorded steps, so the dispatches between marker i-1
+    and marker i are exactly those of call i (one call may launch several kernels); the
+    dispatches after the last call's marker get label None."""
+    out, seg, marks = [], 0, 0
     for r in rows:
         if "face::" not in r["Kernel_Name"]:
             continue
-        b = _kernel_base(r["Kernel_Name"])
-        if b not in seq or not seq[b]:
-            out.append((None, r))
+        if _kernel_base(r["Kernel_Name"]) == PROBE_MARK:
+            seg += 1
+            marks += 1
             continue
-        i = pos[b]
-        pos[b] += 1
-        if i >= len(seq[b]):
-            sys.exit(f"{what}: more dispatches of {b} than calls that launch it")
-        out.append((seq[b][i], r))
+        out.append((order[seg] if seg < len(order) else None, r))
+    if marks < len(order):
+        sys.exit(f"{what}: {marks} call markers for {len(order)} recorded calls")
     return out
 
 
@@ -604,10 +644,10 @@ def pmc_summary(fetch_dir, write_dir, probe_log, out_path):
     out.append(f"python bench.py --pmc-summary gpurun_out/pmc_FETCH_SIZE_w{k} gpurun_out/pmc_WRITE_SIZE_w{k} "
                f"gpurun_out/pmc_FETCH_SIZE_w{k}.log {out_path}\n```\n\n")
     out.append("`bench.py --pmc-probe` runs one eager E+F step (the row GEMM's launch shapes are timed there) "
-               "and a marker launch, then 2 recorded eager E+F steps, then three device-to-device copies of 1 GiB; "
-               "only dispatches after the marker are counted. Its JSON line lists the library calls of the "
-               "recorded steps in launch order, which assigns each dispatch of a kernel shared by several call "
-               "labels to its label.\n\n")
+               "and a marker launch, then 2 recorded eager E+F steps with a marker launch after every library "
+               "call, then three device-to-device copies of 1 GiB; only dispatches after the first marker are "
+               "counted. Its JSON line lists the library calls of the recorded steps in launch order: the "
+               "dispatches between two markers belong to one call (a call may launch several kernels).\n\n")
     out.append(f"Calibration on the 1 GiB copy: bytes = FETCH_SIZE x 1024 x {scale['FETCH_SIZE']:.4f} and "
                f"WRITE_SIZE x 1024 x {scale['WRITE_SIZE']:.4f}.\n\n")
     out.append("traffic = scaled FETCH + scaled WRITE per call (kernels of one call summed); alg = algorithmic "
@@ -735,63 +775,101 @@ def measured_traffic(tag, labels):
 
 
 def trace_summary(stats_csv, bench_log, out_path, title):
-    """Kernel-time summary of a `rocprofv3 --kernel-trace --stats` run of bench.py (its kernel
-    stats CSV and the run's JSON line): the kernel families of the library with their trace
-    averages, then the top kernels."""
+    """Kernel-time summary of a `rocprofv3 --kernel-trace --stats` run of bench.py, per workload:
+    the dispatches between the two trace marks of each workload (exactly its timed HIP-graph
+    replays) grouped by library kernel family, per step, beside the bench's HIP-event figures of
+    the same run; then the library kernels' register / LDS / scratch footprint. BENCH_LOG is the
+    run's stdout + stderr (its JSON line and its [bench] / [bench-detail] lines)."""
     import csv
-    rows = list(csv.DictReader(open(stats_csv)))
-    d = [json.loads(x) for x in open(bench_log) if x.startswith('{"metric"')][0]
-    tot = sum(float(r["TotalDurationNs"]) for r in rows)
+    lines = open(bench_log).read().splitlines()
+    d = [json.loads(x) for x in lines if x.startswith('{"metric"')][0]
+    detail = {}
+    for x in lines:
+        if x.startswith("[bench-detail] "):
+            key, _, js = x[len("[bench-detail] "):].partition(" ")
+            detail[key] = json.loads(js)
+    order = []                          # workload keys in run order
+    for x in lines:
+        if x.startswith("[bench] workload "):
+            k = x.split()[2].rstrip(":")
+            order.append(f"workload{k}" + ("_compiled_radial" if "compiled radial" in x else ""))
+    trace_csv = stats_csv.replace("kernel_stats.csv", "kernel_trace.csv")
+    rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Dispatch_Id"]))
+    marks = [i for i, r in enumerate(rows) if _kernel_base(r["Kernel_Name"]) == PROBE_MARK]
     base_fam = {kn: fam for fam, kns in FAMILY_KERNELS.items() for kn in kns}
+    steps = d["steps"]
     out = [f"# Kernel-time summary: {title}\n\nCommand (repo root, MI355X, ROCm 7.2):\n\n```\n"
            f"rocprofv3 --kernel-trace --stats --output-format csv -d {os.path.dirname(stats_csv)} -o bench -- "
-           f"python -u bench.py "
-           f"{d.get('_argv', '')}\npython bench.py --trace-summary {stats_csv} <bench stdout> {out_path}\n```\n\n"]
-    out.append(f"Bench line of the same run: value {d['value']:.0f} atom-steps/s, {d['ms_per_step']:.3f} ms/step "
-               f"({d['config']['workload']}).\n\n")
-    r = d.get("roofline")
-    if r:
-        out.append(f"Bench roofline kernel family `{r['kernel']}` ({', '.join(r['labels'])}): HIP-event average "
-                   f"{r['avg_launch_us']:.1f} us/launch, {r['achieved']:.1f} {r['unit']} of {r['peak']} "
-                   f"({100 * r['frac']:.1f} %).\n\n")
-    out.append("Library kernel families in the trace (all workloads of the run, warm-up, eager and replayed "
-               "steps; sizes differ between workloads, so averages mix them):\n\n"
-               "| family | calls | total ms | avg us |\n|---|---:|---:|---:|\n")
-    fam = {}
+           f"python -u bench.py {d.get('_argv', '')}\n"
+           f"python bench.py --trace-summary {stats_csv} <bench stdout+stderr> {out_path} '<title>'\n```\n\n"
+           f"Each workload's section covers only the dispatches between its two trace marks: the {steps} timed "
+           f"HIP-graph replays of the E+F step (warm-ups, the instrumented eager steps and TunableOp's tuning "
+           f"fall outside). Per-step figures divide by {steps}. \"bench us\" is the HIP-event average per launch "
+           f"of the same run's instrumented eager steps.\n\n"]
+    if len(marks) != 2 * len(order):
+        out.append(f"**{len(marks)} trace marks for {len(order)} workloads: sections not attributable.**\n")
+        order = []
+    for w, key in enumerate(order):
+        sel = rows[marks[2 * w] + 1:marks[2 * w + 1]]
+        rec = detail.get(key, {})
+        tot_ns = sum(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in sel)
+        ms_step = rec.get("ms_per_step")
+        out.append(f"## {key}: {rec.get('desc', '')}\n\n{len(sel) / steps:.0f} dispatches per step, kernel "
+                   f"time {tot_ns / 1e6 / steps:.3f} ms per step"
+                   + (f" against {ms_step:.3f} ms per replayed step by the bench's clock" if ms_step else "")
+                   + ".\n\n| family / kernel | per step | trace avg us | bench us | us per step | % of kernel time |\n"
+                   "|---|---:|---:|---:|---:|---:|\n")
+        grp = {}
+        for r in sel:
+            b = _kernel_base(r["Kernel_Name"])
+            name = base_fam.get(b) if "face::" in r["Kernel_Name"] else None
+            name = name or ("lib: " + r["Kernel_Name"].replace("|", "/")[:70])
+            gk = grp.setdefault(name, [0, 0])
+            gk[0] += 1
+            gk[1] += int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+        fams = rec.get("families", {})
+        for name, (c, t) in sorted(grp.items(), key=lambda kv: -kv[1][1]):
+            bus = fams.get(name, {}).get("avg_us")
+            out.append(f"| `{name}` | {c / steps:.2f} | {t / c / 1e3:.1f} | "
+                       + (f"{bus:.1f}" if bus else "") + f" | {t / steps / 1e3:.1f} | {100 * t / tot_ns:.1f} |\n")
+        rf = rec.get("roofline")
+        if rf and rf["kernel"] in grp:
+            c, t = grp[rf["kernel"]]
+            out.append(f"\nRoofline family `{rf['kernel']}` ({rf['bound']}): trace average {t / c / 1e3:.1f} us per "
+                       f"launch against the bench's {rf['avg_launch_us']:.1f} us; bench fraction "
+                       f"{rf['frac']:.3f} of {rf['peak']} {rf['unit']}.\n")
+        out.append("\n")
+    res = {}
     for x in rows:
-        b = _kernel_base(x["Name"])
-        if "face::" in x["Name"] and b in base_fam:
-            f = fam.setdefault(base_fam[b], [0, 0.0])
-            f[0] += int(x["Calls"])
-            f[1] += float(x["TotalDurationNs"])
-    for f, (c, t) in sorted(fam.items(), key=lambda kv: -kv[1][1]):
-        out.append(f"| {f} | {c} | {t / 1e6:.2f} | {t / c / 1e3:.1f} |\n")
-    # register / scratch footprint per library kernel from the dispatch records beside the stats
-    trace_csv = stats_csv.replace("kernel_stats.csv", "kernel_trace.csv")
-    if trace_csv != stats_csv and os.path.exists(trace_csv):
-        res = {}
-        for x in csv.DictReader(open(trace_csv)):
-            if "face::" in x["Kernel_Name"]:
-                nm = x["Kernel_Name"].replace("void ", "").split("(")[0].replace("face::", "")
-                res[nm] = (x.get("VGPR_Count"), x.get("Accum_VGPR_Count"), x.get("SGPR_Count"),
-                           x.get("LDS_Block_Size"), x.get("Scratch_Size"))
-        out.append("\nLibrary kernels' resources (dispatch records of the same run; scratch = per-lane private "
-                   "segment bytes, non-zero when registers spill):\n\n| kernel | VGPR | AGPR | SGPR | LDS bytes | "
-                   "scratch |\n|---|---:|---:|---:|---:|---:|\n")
-        for nm, v in sorted(res.items()):
-            out.append(f"| `{nm}` | " + " | ".join(str(t) for t in v) + " |\n")
-    out.append(f"\nAll kernels of the run: {tot / 1e6:.1f} ms total. Top 30:\n\n"
-               "| total ms | calls | avg us | % | kernel |\n|---:|---:|---:|---:|---|\n")
-    for x in sorted(rows, key=lambda r: -float(r["TotalDurationNs"]))[:30]:
-        nm = x["Name"].replace("|", "/")[:110]
-        out.append(f"| {float(x['TotalDurationNs']) / 1e6:.2f} | {x['Calls']} | {float(x['AverageNs']) / 1e3:.1f} | "
-                   f"{float(x['Percentage']):.1f} | `{nm}` |\n")
+        if "face::" in x["Kernel_Name"]:
+            nm = x["Kernel_Name"].replace("void ", "").split("(")[0].replace("face::", "")
+            res[nm] = (x.get("VGPR_Count"), x.get("Accum_VGPR_Count"), x.get("SGPR_Count"),
+                       x.get("LDS_Block_Size"), x.get("Scratch_Size"))
+    out.append("## Library kernels' resources\n\nDispatch records of the same run; scratch = per-lane private "
+               "segment bytes, non-zero when registers spill.\n\n| kernel | VGPR | AGPR | SGPR | LDS bytes | "
+               "scratch |\n|---|---:|---:|---:|---:|---:|\n")
+    for nm, v in sorted(res.items()):
+        out.append(f"| `{nm}` | " + " | ".join(str(t) for t in v) + " |\n")
     open(out_path, "w").write("".join(out))
     print("".join(out)[:3000])
 
 
 # ----------------------------------------------------------------------------- main
+MIN_ROUNDS = 7                          # the reference's protocol: >= 7 rounds of 5 calls
+LINE_MAX_CHARS = 8000                   # the one stdout line stays a few KB (per-label detail -> stderr)
+DENSITY_FAMILIES = ("density_fwd", "density_bwd", "cp_density_fwd", "cp_radial_bwd", "cp_density_bwd",
+                    "density_mix_fwd", "density_mix_bwd")
+
+
+def timed_steps(requested):
+    """Steps actually timed: the requested count, raised to whole rounds and to at least
+    MIN_ROUNDS rounds of CALLS_PER_ROUND calls."""
+    rounds = max(MIN_ROUNDS, -(-requested // CALLS_PER_ROUND))
+    return rounds * CALLS_PER_ROUND
+
+
 def workload_record(r, cpu=None):
+    """Full per-workload record (every label and family): written to stderr, not the stdout line."""
     return {"desc": r["desc"], "atoms": r["N"], "pairs": r["E"], "max_row": r["max_row"],
             "atom_steps_per_s": r["atom_steps_per_s"], "ms_per_step": r["ms_per_step"], "ms_min": r["ms_min"],
             "ms_max": r["ms_max"], "rounds": r["rounds"], "pairlist_ms": r["pairlist_ms"], "mode": r["mode"],
@@ -803,6 +881,90 @@ def workload_record(r, cpu=None):
             "families": {k: {"ms_per_step": v["ms_per_step"], "launches_per_step": v["launches_per_step"],
                              "avg_us": v["avg_us"], "bound": v["bound"], "frac": v["frac"]}
                          for k, v in r["families"].items()}}
+
+
+def _r(x, nd=4):
+    """Round a figure for the compact line (None stays None)."""
+    if x is None:
+        return None
+    return float(f"{x:.{nd}g}")
+
+
+def compact_roofline(rf):
+    """The roofline object of the stdout line: the dominant kernel family's bound, achieved /
+    peak, fraction and counter traffic per launch, with the per-launch figures it comes from."""
+    if rf is None:
+        return None
+    out = {"kernel": rf["kernel"], "bound": rf["bound"], "achieved": _r(rf["achieved"]), "peak": rf["peak"],
+           "unit": rf["unit"], "frac": _r(rf["frac"]), "traffic": _r(rf["traffic"]),
+           "avg_launch_us": _r(rf["avg_launch_us"]), "launches_per_step": _r(rf["launches_per_step"])}
+    if rf.get("alg_flops_per_launch"):
+        out["alg_flops_per_launch"] = _r(rf["alg_flops_per_launch"])
+    if rf.get("alg_bytes_per_launch"):
+        out["alg_bytes_per_launch"] = _r(rf["alg_bytes_per_launch"])
+    return out
+
+
+def compact_cpu(cpu):
+    if cpu is None:
+        return None
+    return {"value": _r(cpu["value"]), "unit": cpu["unit"], "cores": cpu["cores"], "kind": cpu["kind"],
+            "sample": cpu["sample"]}
+
+
+def north_star_kernels(r):
+    """HBM fraction of the density kernels and of the force scatter (the kernels the target is
+    quoted on): per family present, the fraction of 8 TB/s its algorithmic bytes reach."""
+    out = {}
+    for fam_name in DENSITY_FAMILIES + ("force_scatter",):
+        f = r["families"].get(fam_name)
+        if not f or not f.get("alg_bytes_per_launch"):
+            continue
+        gbs = f["alg_bytes_per_launch"] / (f["avg_us"] * 1e-6) / 1e9
+        out[fam_name] = {"us": _r(f["avg_us"]), "GBps": _r(gbs), "hbm_frac": _r(gbs / HBM_PEAK_GBS, 3)}
+    return out
+
+
+def compact_workload(r, cpu=None):
+    """One workload's entry under 'also' in the stdout line."""
+    rf = r["roofline"]
+    out = {"workload": r["desc"], "atoms": r["N"], "pairs": r["E"], "ms_per_step": _r(r["ms_per_step"]),
+           "value": _r(r["atom_steps_per_s"]), "rounds": r["rounds"],
+           "roofline": None if rf is None else {"kernel": rf["kernel"], "bound": rf["bound"],
+                                                "frac": _r(rf["frac"], 3)},
+           "hbm": north_star_kernels(r)}
+    if r.get("route"):
+        out["route"] = r["route"]
+    if cpu is not None:
+        out["cpu_baseline"] = _r(cpu["value"])
+    return out
+
+
+def bench_line(main_run, results, cpu, workload, steps, steps_requested, warmup, tunable):
+    """The one JSON line bench.py prints: the headline workload's throughput, its roofline and CPU
+    baseline, and a compact record per other workload. Everything per label goes to stderr."""
+    also = {}
+    for (k, comp), r in results.items():
+        also[f"workload{k}" + ("_compiled_radial" if comp else "")] = compact_workload(r, None if comp else
+                                                                                         cpu.get(k))
+    return {
+        "metric": METRIC, "value": _r(main_run["atom_steps_per_s"], 6), "unit": "atom-steps/s", "n_gpus": 1,
+        "steps": steps, "steps_requested": steps_requested, "warmup": warmup,
+        "ms_per_step": _r(main_run["ms_per_step"], 6), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": main_run["desc"], "atoms": main_run["N"], "pairs": main_run["E"],
+                   "parallelism": "single GPU", "step": main_run["mode"],
+                   "timing": f"median of {main_run['rounds']} rounds of {CALLS_PER_ROUND} calls after {warmup} "
+                             f"warm-ups (tools/bench_review.py:53-69)",
+                   "ms_min": _r(main_run["ms_min"]), "ms_max": _r(main_run["ms_max"]),
+                   "library_gemms": "TunableOp" if tunable else "default", "graph_nodes": main_run["graph_nodes"],
+                   "peak_mem_gb": _r(main_run["peak_mem_gb"], 3)},
+        "roofline": compact_roofline(main_run["roofline"]),
+        "cpu_baseline": compact_cpu(cpu.get(workload)),
+        "hbm": north_star_kernels(main_run),
+        "also": also,
+        "_argv": " ".join(sys.argv[1:]),
+    }
 
 
 def main():
@@ -824,6 +986,7 @@ def main():
     ap.add_argument("--trace-summary", nargs=4, metavar=("STATS_CSV", "BENCH_LOG", "OUT", "TITLE"))
     ap.add_argument("--sq-summary", nargs="+", metavar="OUT TITLE PROBE_ARGS DIR",
                     help="OUT TITLE PROBE_ARGS DIR1 [DIR2 DIR3]: SQ counter summary of rocprofv3 --pmc passes")
+    ap.add_argument("--detail-out", default=None, help="also write the per-label detail of every workload here")
     ap.add_argument("--no-tunable", action="store_true",
                     help="library GEMMs with hipBLASLt's default solutions instead of PyTorch TunableOp")
     a = ap.parse_args()
@@ -855,46 +1018,34 @@ def main():
     if a.pmc_probe:
         pmc_probe(a.workload)
         return
-    main_run = run_gpu(a.workload, a.steps, a.warmup, not a.eager)
+    steps = timed_steps(a.steps)
+    if steps != a.steps:
+        log(f"[bench] timing {steps} steps ({steps // CALLS_PER_ROUND} rounds of {CALLS_PER_ROUND} calls; "
+            f"{a.steps} requested): at least {MIN_ROUNDS} rounds per workload")
+    main_run = run_gpu(a.workload, steps, a.warmup, not a.eager)
     runs = [(int(x), False) for x in a.also.split(",") if x.strip() and int(x) != a.workload]
     runs += [(int(x), True) for x in a.compiled.split(",") if x.strip()]
     results = {}
     for k, comp in runs:
-        results[(k, comp)] = run_gpu(k, a.steps, a.warmup, not a.eager, compiled_radial=comp)
+        results[(k, comp)] = run_gpu(k, steps, a.warmup, not a.eager, compiled_radial=comp)
     cpu = {}
     if not a.no_cpu:
         for k in [a.workload] + [k for k, comp in runs if not comp]:
             log(f"[bench] cpu baseline, workload {k} ...")
             cpu[k] = run_cpu(k, a.cpu_budget, a.cpu_full)
             log(f"[bench]   cpu {cpu[k]['value']:.1f} atom-steps/s on {cpu[k]['cores']} cores ({cpu[k]['sample']})")
-    also = {}
+    # per-label and per-family detail of every workload: stderr (and a file when asked)
+    detail = {f"workload{a.workload}": workload_record(main_run, cpu.get(a.workload))}
     for (k, comp), r in results.items():
-        also[f"workload{k}" + ("_compiled_radial" if comp else "")] = workload_record(r, None if comp else cpu.get(k))
-    kw = main_run["kw"]
-    rec = workload_record(main_run)
-    out = {
-        "metric": METRIC, "value": main_run["atom_steps_per_s"], "unit": "atom-steps/s", "n_gpus": 1,
-        "steps": a.steps, "warmup": a.warmup, "ms_per_step": main_run["ms_per_step"], "higher_is_better": True,
-        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-        "config": {"workload": main_run["desc"], "atoms": main_run["N"], "pairs": main_run["E"],
-                   "potential": {k: kw[k] for k in ("C", "B", "K", "rc") if k in kw} | {"cp": bool(kw.get("cp"))},
-                   "weights": "random init, torch.manual_seed(0) + unit_parameterise", "parallelism": "single GPU",
-                   "library_gemms": ("fp32 hipBLASLt/rocBLAS, solutions picked by PyTorch TunableOp in the warm-up"
-                                     if tunable else "fp32 hipBLASLt default solutions"),
-                   "step": main_run["mode"], "timing": f"median of {main_run['rounds']} rounds of "
-                   f"{CALLS_PER_ROUND} calls after {a.warmup} warm-ups (tools/bench_review.py:53-69)",
-                   "ms_min": main_run["ms_min"], "ms_max": main_run["ms_max"],
-                   "eager_ms_per_step": main_run["eager_ms_per_step"], "peak_mem_gb": main_run["peak_mem_gb"],
-                   "graph_nodes": main_run["graph_nodes"]},
-        "roofline": main_run["roofline"],
-        "cpu_baseline": cpu.get(a.workload),
-        "kernels": rec["kernels"],
-        "families": rec["families"],
-        "pairlist_ms": main_run["pairlist_ms"],
-        "also": also,
-        "_argv": " ".join(sys.argv[1:]),
-    }
-    print(json.dumps(out), flush=True)
+        detail[f"workload{k}" + ("_compiled_radial" if comp else "")] = workload_record(r, None if comp
+                                                                                        else cpu.get(k))
+    for key, rec in detail.items():
+        log(f"[bench-detail] {key} " + json.dumps(rec))
+    if a.detail_out:
+        with open(a.detail_out, "w") as f:
+            json.dump(detail, f, indent=1)
+    line = bench_line(main_run, results, cpu, a.workload, steps, a.steps, a.warmup, tunable)
+    print(json.dumps(line, separators=(",", ":")), flush=True)
 
 
 if __name__ == "__main__":

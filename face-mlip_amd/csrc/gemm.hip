@@ -26,6 +26,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <cstdio>
 #include <map>
 #include <mutex>
 #include <vector>
@@ -917,6 +918,12 @@ extern "C" int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, 
     c.y_scale = y_scale != nullptr, c.any_bias = any_bias, c.any_ext = any_ext, c.n_groups = n_groups;
     c.st = (hipStream_t)stream;
     if (x_scale && any_ext) return FACE_ERR_UNSUPPORTED;                 // x scale with split / op / y0
+    // FACE_GEMM_SHAPE="nw,n_sl,xcd" forces one launch shape (no timing, nothing cached), for tests
+    // that compare every shape's results; FACE_ERR_UNSUPPORTED if that shape does not fit
+    if (const char* fs = getenv("FACE_GEMM_SHAPE")) {
+        int nw = 0, ns = 0, xcd = 0;
+        if (sscanf(fs, "%d,%d,%d", &nw, &ns, &xcd) == 3) return launch_rows(c, nw, ns, xcd ? 1 : 0);
+    }
     ShapePlan plan{default_nw(c, NS), n_sl, 0};
     pick_shape(c, plan);
     return launch_rows(c, plan.nw, plan.n_sl, plan.xcd);

@@ -141,12 +141,16 @@ def stop_timing():
 # Optional call log: the label (or entry-point name) of every successful call, in call order,
 # for matching a profiler's dispatch list to the calls that launched it.
 _order = None
+_after_call = None
 
 
-def record_order(on=True):
-    """Start (on) or stop logging call labels; returns the list being filled (or None)."""
-    global _order
+def record_order(on=True, after=None):
+    """Start (on) or stop logging call labels; returns the list being filled (or None). `after`
+    (optional) is run after every logged call, e.g. a marker launch that separates the calls'
+    dispatches in a profiler's record."""
+    global _order, _after_call
     _order = [] if on else None
+    _after_call = after if on else None
     return _order
 
 
@@ -169,6 +173,8 @@ def call(name, *args, label=None):
         raise RuntimeError(f"{name} failed: {msg} (code {code})")
     if _order is not None:
         _order.append(key)
+        if _after_call is not None:
+            _after_call()
 
 
 FACE_ERR_UNSUPPORTED = -2

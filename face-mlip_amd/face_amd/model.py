@@ -547,19 +547,19 @@ class FACE(nn.Module):
         r = views[3][0]                  # the spline order (no gradient) reads the first r view
         # per-atom element index, element-pair row of every edge, the embedding rows and the energy
         # offsets: functions of the graph's species and of constants only, cached on the graph per
-        # model (the entry holds the tensors it depends on and their in-place versions, so it can
-        # be neither recycled by another model nor outlive a change of the weights)
+        # model (keyed like every weight cache: the tensors it depends on, their in-place versions,
+        # data pointers and devices, so it can be neither recycled by another model nor outlive a
+        # change of the weights, in place or by a swapped .data)
         w, E0 = self.embed.weight, self.E0
-        dep = (self.zmap, w, E0)
-        ver = tuple(t._version for t in dep)
+        dep = _key(self.zmap, w, E0)
         akey = ("atoms", id(self))
         ent = graph.cache.get(akey)
-        if ent is None or any(a is not b for a, b in zip(ent[0], dep)) or ent[1] != ver:
+        if ent is None or not _same(ent[0], dep):
             zidx = self.zmap[graph.Z]
             zp = (zidx[graph.recv.long()] * len(E0) + zidx[graph.col.long()]).to(torch.int32)
-            ent = (dep, ver, (zidx, zidx.to(torch.int32), zp, F.embedding(zidx, w.detach()), E0[zidx]))
+            ent = (dep, (zidx, zidx.to(torch.int32), zp, F.embedding(zidx, w.detach()), E0[zidx]))
             graph.cache[akey] = ent
-        zidx, zidx32, zp, h, e0 = ent[2]
+        zidx, zidx32, zp, h, e0 = ent[1]
         # table-cell edge order for large compiled tables: one sort per step, shared by the passes
         order = None
         big = [b.spline for b in self.blocks if b.spline is not None and ops.spline_wants_order(b.spline.T)]

@@ -865,6 +865,75 @@ def test_rows_linear_launch_shapes_give_bitwise_equal_rows(monkeypatch):
         assert torch.equal(rule[l], full[l][:rule[l].shape[0]])
 
 
+def _gemm_shapes(n_widest, ns_max=160):
+    """Every (waves per workgroup, column slices) pair face_rows_linear's shape timing tries."""
+    out = []
+    for nw in (16, 8, 4):
+        seen = set()
+        for ns in range(16, ns_max + 1, 16):
+            k = -(-n_widest // ns)
+            if k <= 32 and k not in seen:
+                seen.add(k)
+                out.append((nw, k))
+    return out
+
+
+@pytest.mark.parametrize("case", ["fcc864_mix_bwd", "liquid24k_mix_fwd"])
+def test_rows_linear_every_launch_shape_gives_bitwise_equal_rows(case, monkeypatch):
+    """Every launch shape the timing may pick (4, 8, 16 waves per workgroup x every slice count x
+    plain / XCD-aware item order, forced through FACE_GEMM_SHAPE) gives the same bits as the rules'
+    shape: the 864-atom factor mix backward ((k, n) weight 96 -> 512, input scale: one item per
+    workgroup) and the 24,000-atom CP mix forward (480,000 rows of 160 -> 160 over four ranks,
+    (n, k) weights, output scale: more tiles than resident workgroups, so the persistent runs)."""
+    from face_amd import ops
+    say("rows_linear every shape", case)
+    torch.manual_seed(13)
+    if case == "fcc864_mix_bwd":
+        N, C, n = 864, 96, 512
+        w_kn, scale = True, "xs"
+        ws = [torch.randn(C, n, device=DEV) / C ** 0.5 for _ in range(4)]
+    else:
+        N, C, n = 24000, 160, 160
+        w_kn, scale = False, "ys"
+        ws = [torch.randn(n, C, device=DEV) / C ** 0.5 for _ in range(4)]
+    tab = torch.rand(3, 4 * max(C, n), device=DEV) + 0.5
+    grp = torch.randint(0, 3, (N,), device=DEV, dtype=torch.int32)
+    xs = [torch.randn(k * N, C, device=DEV) for k in (1, 3, 6, 10)]
+
+    def run():
+        ys = [torch.empty(x.shape[0], n, device=DEV) for x in xs]
+        ops.rows_linear([(x, w, y, l * (C if scale == "xs" else n), 0.0)
+                         for l, (x, w, y) in enumerate(zip(xs, ws, ys))], w_kn=w_kn,
+                        xs=tab if scale == "xs" else None, ys=tab if scale == "ys" else None, group=grp, period=N)
+        torch.cuda.synchronize()
+        return ys
+
+    monkeypatch.setenv("FACE_GEMM_TUNE", "0")
+    rule = run()
+    for l, (x, w) in enumerate(zip(xs, ws)):
+        g = grp.long().repeat(x.shape[0] // N)
+        if scale == "xs":
+            ref = (x.double() * tab.double()[g, l * C:(l + 1) * C]) @ w.double()
+        else:
+            ref = (x.double() @ w.double().T) * tab.double()[g, l * n:(l + 1) * n]
+        assert (rule[l].double() - ref).abs().max() <= 1e-5 * ref.abs().max()
+    ran = refused = 0
+    for nw, n_sl in _gemm_shapes(n):
+        for xcd in (0, 1):
+            monkeypatch.setenv("FACE_GEMM_SHAPE", f"{nw},{n_sl},{xcd}")
+            try:
+                out = run()
+            except RuntimeError as err:                  # a shape whose slice does not fit LDS
+                assert "(code -2)" in str(err), err
+                refused += 1
+                continue
+            for a, b in zip(out, rule):
+                assert torch.equal(a, b), (nw, n_sl, xcd)
+            ran += 1
+    say(f"   {ran} shapes bitwise equal to the rules' shape, {refused} refused")
+    assert ran >= 24
+
+
 @pytest.mark.parametrize("kc", [None, "1"])
 @pytest.mark.parametrize("w_kn", [False, True])
 def test_rows_linear_split_input_transforms_and_initial_sum(w_kn, kc, monkeypatch):

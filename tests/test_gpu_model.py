@@ -390,6 +390,88 @@ def test_workload4_full_size_properties():
     assert nodes and nodes.get("kernel", 0) > 0 and nodes.get("memset", 0) == 0
 
 
+def _rotation(rng):
+    q, r = np.linalg.qr(rng.standard_normal((3, 3)))
+    q = q * np.sign(np.diag(r))
+    return q * np.sign(np.linalg.det(q))
+
+
+def _ef(m, sts, rc):
+    from face_amd.neighbors import build_graph
+    g = build_graph(sts, rc)
+    o = m(g.with_pos(g.pos.clone()))
+    return g, o["energy"].detach().double(), o["forces"].detach().double()
+
+
+def _assert_close(E2, F2, E, F, what):
+    """The hot-path tolerances: energies within 1e-5 relative, forces within 1e-4 x RMS(F)."""
+    rms = F.pow(2).mean().sqrt()
+    dE = ((E2 - E).abs() / E.abs().clamp_min(1e-30)).max().item()
+    dF = ((F2 - F).abs().max() / rms).item()
+    say(f"  {what}: dE/E {dE:.2e}  max|dF|/rms {dF:.2e}")
+    assert dE <= E_TOL and dF <= F_TOL, (what, dE, dF)
+
+
+@pytest.mark.parametrize("k", [1, 3])
+def test_workload_full_size_properties(k):
+    """The 512-molecule FACE-CP C160 batch (10,752 atoms) and the 24,000-atom FACE-CP C160 liquid
+    (1.25 M pairs) at full size, the systems the benchmark times, through the symmetry checks of
+    the reference's tests/test_symmetry.py:24-46 at the hot-path tolerances: finite energies and
+    forces; zero net force per structure (every pair term enters two atoms with opposite signs);
+    rotation + translation of every structure (molecules) or of atoms and cell together (periodic
+    box, positions wrapped back) gives the same energies and rotated forces; a permutation of the
+    atoms gives the same energies and permuted forces; a second eager call is bitwise equal; the
+    HIP-graph replay equals the eager step."""
+    from face_amd import systems
+    from face_amd.runner import StepGraph
+    sts, kw, el, desc = systems.workload(k)
+    say("full size", desc)
+    m = product_model(kw, el)
+    g, E, F = _ef(m, sts, kw["rc"])
+    say(f"  N {g.N} E {g.E} max_row {g.max_row}")
+    assert g.N == (10752 if k == 1 else 24000) and g.E > (150_000 if k == 1 else 1_200_000)
+    assert torch.isfinite(E).all() and torch.isfinite(F).all()
+    rms = F.pow(2).mean().sqrt()
+    batch = g.batch.long()
+    net = torch.zeros(len(sts), 3, dtype=torch.float64, device=F.device).index_add_(0, batch, F)
+    say(f"  E[0] {E[0].item():.6e}  rms(F) {rms.item():.4e}  max|sum F| per structure {net.abs().max().item():.3e}")
+    assert net.abs().max() <= 1e-3 * rms
+    # bitwise reproducible: a second eager call
+    _, E1, F1 = _ef(m, sts, kw["rc"])
+    assert torch.equal(E1, E) and torch.equal(F1, F)
+    # rotation + translation (+ wrap into the rotated cell for the periodic box)
+    rng = np.random.default_rng(11 + k)
+    Q = _rotation(rng)
+    rot = []
+    for s in sts:
+        p = s["pos"] @ Q.T + rng.standard_normal(3)
+        cell = s["cell"] @ Q.T
+        if s["pbc"].any():
+            frac = p @ np.linalg.inv(cell)
+            p = (frac - np.floor(frac)) @ cell
+        rot.append(dict(s, pos=p, cell=cell))
+    _, E2, F2 = _ef(m, rot, kw["rc"])
+    Qt = torch.tensor(Q.T, dtype=torch.float64, device=F.device)
+    _assert_close(E2, F2, E, F @ Qt, "rotation + translation")
+    # permutation of the atoms of every structure
+    perms = [rng.permutation(len(s["pos"])) for s in sts]
+    per = [dict(s, pos=s["pos"][p], Z=np.asarray(s["Z"])[p]) for s, p in zip(sts, perms)]
+    _, E3, F3 = _ef(m, per, kw["rc"])
+    off = np.cumsum([0] + [len(s["pos"]) for s in sts[:-1]])
+    idx = torch.tensor(np.concatenate([o + p for o, p in zip(off, perms)]), device=F.device)
+    _assert_close(E3, F3, E, F[idx], "permutation")
+    # HIP-graph replay of the step
+    run = StepGraph(m, g)
+    for _ in range(2):
+        Er, Fr = run(g.pos)
+        torch.cuda.synchronize()
+        assert torch.allclose(Er.double(), E, rtol=1e-6, atol=0), (Er, E)
+        assert (Fr.double() - F).abs().max() <= 1e-5 * F.abs().max()
+    nodes = run.node_counts()
+    say(f"  graph nodes {nodes}")
+    assert nodes and nodes.get("kernel", 0) > 0 and nodes.get("memset", 0) == 0
+
+
 @pytest.mark.parametrize("fused", [True, False])
 def test_factor_density_mix_routes_match_oracle(fused, monkeypatch):
     """The factorised passes with the fused density + mix kernels and with the unfused route

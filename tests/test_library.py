@@ -176,3 +176,60 @@ def test_bench_labels_map_to_kernel_families():
     import bench
     for lab, fam in bench.KERNEL_FAMILY.items():
         assert fam in bench.FAMILY_KERNELS, lab
+
+
+def _stub_run(bench, N, E, ms, desc):
+    """A run_gpu result as the bench builds it, from made-up per-label figures."""
+    kern = {
+        "mix_fwd": {"family": "rows_gemm", "launches_per_step": 2.0, "ms_per_step": 0.5 * ms,
+                    "alg_bytes": None, "alg_flops": 3.0e10, "avg_us": 250.0 * ms},
+        "cp_fwd": {"family": "cp_density_fwd", "launches_per_step": 1.0, "ms_per_step": 0.1 * ms,
+                   "alg_bytes": 4.5e9, "alg_flops": None, "avg_us": 100.0 * ms},
+        "force_scatter": {"family": "force_scatter", "launches_per_step": 1.0, "ms_per_step": 0.001 * ms,
+                          "alg_bytes": 2.0e7, "alg_flops": None, "avg_us": 1.0 * ms},
+    }
+    fam = bench.family_stats(kern)
+    return {"N": N, "E": E, "max_row": 78, "ms_per_step": ms, "ms_min": ms * 0.99, "ms_max": ms * 1.01,
+            "rounds": 7, "atom_steps_per_s": N / ms * 1e3, "kernels": kern, "families": fam,
+            "roofline": bench.roofline_of(fam, "none"), "pairlist_ms": 5.9, "desc": desc, "kw": {},
+            "mode": "hipgraph", "graph_nodes": {"kernel": 79, "memcpy": 1}, "eager_ms_per_step": ms * 1.05,
+            "peak_mem_gb": 16.4}
+
+
+def test_bench_line_is_compact_strict_json():
+    """The one stdout line parses as strict JSON (no NaN / Infinity), stays under the size bound
+    with all seven workload records, carries the contract keys, a roofline and a CPU baseline,
+    and names the workload only in its config (no model hyper-parameters)."""
+    import json
+    import bench
+    desc = "H:C:O 8:9:4 liquid, 24000 atoms, rho 0.10, FACE-CP C160 B16 rc5.0, compiled radial (4096-point splines)"
+    main = _stub_run(bench, 24000, 1249484, 18.3, desc)
+    results = {(k, c): _stub_run(bench, 1000 * (k + 1), 20000 * (k + 1), 1.0 + k, desc)
+               for k, c in [(0, False), (1, False), (2, False), (4, False), (2, True), (3, True)]}
+    sample = ("the whole system (24000 atoms, FACE-CP C160 B16 rc5.0), oracle torch path (unfused, as the "
+              "reference's torch path), fp32, median of 2 single E+F calls after 1 warm-up (17.5 s), "
+              "torch.set_num_threads(16)")
+    cpu = {k: {"value": 1392.0 + k, "unit": "atom-steps/s", "cores": 16, "kind": "port", "sample": sample}
+           for k in (0, 1, 2, 3, 4)}
+    steps = bench.timed_steps(20)
+    assert steps == 35 and bench.timed_steps(36) == 40 and bench.timed_steps(1) == 35
+    line = bench.bench_line(main, results, cpu, 3, steps, 20, 5, True)
+    s = json.dumps(line, separators=(",", ":"), allow_nan=False)
+    assert "\n" not in s and len(s) < bench.LINE_MAX_CHARS, len(s)
+    d = json.loads(s)
+    for key in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better",
+                "scaling", "vs_baseline", "dtype", "data", "config", "roofline", "cpu_baseline"):
+        assert key in d, key
+    assert d["n_gpus"] == 1 and d["steps"] == 35 and d["steps_requested"] == 20 and d["dtype"] == "f32"
+    assert abs(d["value"] - 24000 / 18.3 * 1e3) / d["value"] < 1e-5
+    assert "potential" not in d["config"] and d["config"]["workload"] == desc
+    r = d["roofline"]
+    assert r["kernel"] == "rows_gemm" and r["bound"] == "mfma" and r["unit"] == "TFLOP/s"
+    assert abs(r["achieved"] - r["frac"] * r["peak"]) / r["achieved"] < 1e-3
+    assert d["cpu_baseline"]["cores"] == 16 and d["cpu_baseline"]["kind"] == "port"
+    assert set(d["also"]) == {"workload0", "workload1", "workload2", "workload4", "workload2_compiled_radial",
+                              "workload3_compiled_radial"}
+    w = d["also"]["workload1"]
+    assert w["cpu_baseline"] == 1393.0 and w["roofline"]["kernel"] == "rows_gemm"
+    assert "force_scatter" in w["hbm"] and "cp_density_fwd" in w["hbm"]
+    assert "cpu_baseline" not in d["also"]["workload3_compiled_radial"]
