@@ -72,7 +72,7 @@ KERNEL_FAMILY = {
 }
 # kernel family -> kernel functions of libface_hip.so it stands for (rocprofv3 names, namespace face)
 FAMILY_KERNELS = {
-    "density_fwd": ["density_fwd_mfma_kernel", "density_fwd_kernel"],
+    "density_fwd": ["density_fwd_row_kernel", "density_fwd_kernel"],
     "density_bwd": ["density_bwd_split_kernel", "density_bwd_mfma_kernel", "density_bwd_lds_kernel",
                     "density_bwd_kernel"],
     "density_mix_fwd": ["density_mix_fwd_kernel"], "density_mix_bwd": ["density_mix_bwd_kernel"],
@@ -720,7 +720,8 @@ def sq_summary(out_path, title, probe_args, *dirs):
         log = d.rstrip("/") + ".log"
         order = []
         if os.path.exists(log):
-            order = [json.loads(x) for x in open(log) if x.startswith('{"probe"')][0]["order"]
+            probes = [json.loads(x) for x in open(log) if x.startswith('{"probe"')]
+            order = probes[0]["order"] if probes else []
         # a dispatch carries one record per counter: label the dispatches, then their records
         disp = {}
         for r in recs:

@@ -33,11 +33,21 @@ def compile_one(src):
     return obj, r.stderr
 
 
-def build(jobs=None, verbose=False):
+def stale(src):
+    """True when the object of src is missing or older than src or a header it includes."""
+    obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
+    if not os.path.exists(obj):
+        return True
+    t = os.path.getmtime(obj)
+    return any(os.path.getmtime(os.path.join(HERE, f)) > t for f in (src, "common.h", "../../include/face_hip.h"))
+
+
+def build(jobs=None, verbose=False, changed_only=False):
     os.makedirs(BUILD, exist_ok=True)
-    with cf.ThreadPoolExecutor(max_workers=jobs or min(8, len(SOURCES))) as ex:
-        results = list(ex.map(compile_one, SOURCES))
-    objs = [o for o, _ in results]
+    todo = [s for s in SOURCES if stale(s)] if changed_only else list(SOURCES)
+    with cf.ThreadPoolExecutor(max_workers=jobs or min(8, max(1, len(todo)))) as ex:
+        results = list(ex.map(compile_one, todo))
+    objs = [os.path.join(BUILD, os.path.splitext(s)[0] + ".o") for s in SOURCES]
     if verbose:
         for _, err in results:
             if err.strip():
@@ -55,5 +65,6 @@ if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
     ap.add_argument("-v", action="store_true")
+    ap.add_argument("--changed", action="store_true", help="recompile only sources newer than their objects")
     a = ap.parse_args()
-    print(build(a.jobs, a.v))
+    print(build(a.jobs, a.v, a.changed))

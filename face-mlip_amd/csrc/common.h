@@ -37,6 +37,26 @@ __device__ __forceinline__ float group_sum(float v, int width) {
     return v;
 }
 
+// Cross-lane data movement on the VALU (DPP), no LDS round trip: the value of the lane that the
+// DPP control selects within the lane's 16-lane row (all lanes of the row active).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over each aligned group of 16 lanes, every lane ending with its group's total: lane ^ 1 and
+// lane ^ 2 (quad permutes), then the other quad of the half row (row_half_mirror, 7 - i) and the
+// other half row (row_mirror, 15 - i), which after the first two steps hold the same partial sums
+// that lane ^ 4 and lane ^ 8 would: the pairing and rounding of group_sum(v, 16), bit for bit,
+// in four VALU instructions instead of four LDS permutes.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f<0xB1>(v);                                 // quad_perm [1, 0, 3, 2]
+    v += dpp_f<0x4E>(v);                                 // quad_perm [2, 3, 0, 1]
+    v += dpp_f<0x141>(v);                                // row_half_mirror
+    v += dpp_f<0x140>(v);                                // row_mirror
+    return v;
+}
+
 // fp32 matrix-core helpers. v_mfma_f32_16x16x4f32 operand layouts (wave64): A[i][k] in lane
 // i + 16k, B[k][j] in lane j + 16k, D[4q + r][j] in register r of lane j + 16q.
 typedef float v4f __attribute__((ext_vector_type(4)));

@@ -111,18 +111,29 @@ __global__ __launch_bounds__(kBlock) void density_fwd_kernel(
 
 // ------------------------------------------------------------------ factor forward on MFMA
 // B = 16, NX = 20, K = 16 KB: for monomial x, D[x] (16 b x K) = sum_e U_x[e, :]^T msg[e, :] with
-// U_x[e, b] = Y[e, x] phi[e, b] -- per 16-edge tile a v_mfma_f32_16x16x4f32 chain with A = U_x^T
-// (basis j, K index q of instruction r = edge 4q + r) and B = msg rows, accumulating basis
-// 4q + r, channel j in register r of lane j + 16q. One atom per workgroup, its 4 waves own 5
-// monomials each (no cross-wave sums).
-constexpr int kDfWaves = 4;
+// U_x[e, b] = Y[e, x] phi[e, b], a v_mfma_f32_16x16x4f32 chain per (monomial, 16-channel block):
+// A = U_x^T (basis j, K index q), B = msg rows, basis 4q + r and channel j in register r of lane
+// j + 16q. One atom per workgroup, its 4 waves own 5 monomials each (no cross-wave sums). The
+// row is walked in chunks of 32 edges held in registers; instruction r of a chunk takes edges
+// 4r .. 4r + 3 (K index q = edge 4r + q), so a chunk of ne edges issues ceil(ne / 4)
+// instructions per chain instead of whole 16-edge tiles (an 18-edge row: 5 instead of 8). Every
+// load of a chunk is issued before its first product (one memory latency per chunk), and in the
+// row's last chunk (the only one for rows of <= 32 edges) each monomial's D_x is stored as soon
+// as its chain ends, while the next monomial's products run. Against 16-edge tiles with the next
+// tile prefetched and all stores at the end (the same products, summed in another order): 864-atom FCC
+// 14.0 -> 13.4 us, 64 molecules 16.5 -> 16.3 us, 100,000 atoms at K = 64 4453 -> 4168 us.
+// Measured and not kept: 5 or 10 waves per atom (each reloads the chunk's phi and message rows:
+// 864 atoms 15.2 / 16.9 us), and a workgroup whose computing waves hand finished tiles through
+// LDS to a storing wave so that no product waits behind a store (864 atoms 14.4 us).
+constexpr int kDrWaves = 4;
+constexpr int kDrCh = 32;                                // edges per register chunk
 
 template <int KB>
-__global__ __launch_bounds__(kDfWaves * kWave) void density_fwd_mfma_kernel(
+__global__ __launch_bounds__(kDrWaves * kWave) void density_fwd_row_kernel(
     const float* __restrict__ phi, int ld_phi, const float* __restrict__ msg, int ld_msg,
     const int32_t* __restrict__ msg_row, const float* __restrict__ Y, int ld_Y, const int32_t* __restrict__ row_ptr,
     int M, RankOut D) {
-    constexpr int K = 16 * KB, NXW = 20 / kDfWaves;
+    constexpr int K = 16 * KB, NXW = 20 / kDrWaves, NI = kDrCh / 4;
     const int lane = threadIdx.x & (kWave - 1), j = lane & 15, q = lane >> 4;
     const int x0 = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave) * NXW;
     const int64_t n = blockIdx.x;
@@ -134,59 +145,66 @@ __global__ __launch_bounds__(kDfWaves * kWave) void density_fwd_mfma_kernel(
         for (int c = 0; c < KB; ++c) acc[xx][c] = z4;
     int64_t a, bnd;
     row_range(row_ptr, n, M, a, bnd);
-    // tile rows (phi at basis j, msg channels, Y of the wave's monomials) of edges e0 + 4q + r,
-    // clamped into the row (phi zero past its end). K <= 32: the next tile's rows load while this
-    // one's MFMAs run (864-atom FCC 15.0 -> 14.1 us, 2,000 atoms of 70 neighbours 51 -> 49 us);
-    // at K = 64 the second set of rows costs occupancy (184 registers) and the loads stay in order
-    // (833 against 855 us on a 20,000-atom liquid).
-    constexpr bool PF = KB <= 2;
-    auto load_tile = [&](int64_t e0, float (&phT)[4], float (&yv)[NXW][4], float (&mb)[KB][4]) {
-        const int ne = (int)min((int64_t)16, bnd - e0);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int t = 4 * q + r;
-            const int64_t e = e0 + min(t, ne - 1);
-            const float p = phi[e * ld_phi + j];
-            phT[r] = t < ne ? p : 0.f;
-            const int64_t row = msg_row ? (int64_t)msg_row[e] : e;
-#pragma unroll
-            for (int c = 0; c < KB; ++c) mb[c][r] = msg[row * ld_msg + 16 * c + j];
-#pragma unroll
-            for (int xx = 0; xx < NXW; ++xx) yv[xx][r] = Y[e * ld_Y + x0 + xx];
-        }
-    };
-    float phT[4], yv[NXW][4], mb[KB][4];
-    if (PF && a < bnd) load_tile(a, phT, yv, mb);
-    for (int64_t e0 = a; e0 < bnd; e0 += 16) {
-        if (!PF) load_tile(e0, phT, yv, mb);
-        float phN[4], yN[NXW][4], mN[KB][4];
-        if (PF && e0 + 16 < bnd) load_tile(e0 + 16, phN, yN, mN);
-#pragma unroll
-        for (int xx = 0; xx < NXW; ++xx)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const float u = yv[xx][r] * phT[r];
-#pragma unroll
-                for (int c = 0; c < KB; ++c) acc[xx][c] = mfma_16x16x4(u, mb[c][r], acc[xx][c]);
-            }
-        if (PF && e0 + 16 < bnd) {
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                phT[r] = phN[r];
-#pragma unroll
-                for (int c = 0; c < KB; ++c) mb[c][r] = mN[c][r];
-#pragma unroll
-                for (int xx = 0; xx < NXW; ++xx) yv[xx][r] = yN[xx][r];
-            }
-        }
-    }
-#pragma unroll
-    for (int xx = 0; xx < NXW; ++xx) {
+    auto store = [&](int xx) {
         float* dx = D.at(n, x0 + xx);
 #pragma unroll
         for (int c = 0; c < KB; ++c)
 #pragma unroll
             for (int r = 0; r < 4; ++r) dx[(4 * q + r) * K + 16 * c + j] = acc[xx][c][r];
+    };
+    if (a >= bnd) {                                      // empty row: zeros
+#pragma unroll
+        for (int xx = 0; xx < NXW; ++xx) store(xx);
+        return;
+    }
+    for (int64_t c0 = a; c0 < bnd; c0 += kDrCh) {
+        const int ne = (int)min((int64_t)kDrCh, bnd - c0);
+        const int ni = (ne + 3) >> 2;                    // uniform over the workgroup
+        const bool last = c0 + kDrCh >= bnd;
+        // every slot loads (edges past the row end clamped to its last edge, phi zeroed there): no
+        // branches between the loads, so the gathered rows' indices all issue before one wait
+        float ph[NI], yv[NXW][NI], mb[KB][NI];
+        int64_t ev[NI], rw[NI];
+#pragma unroll
+        for (int r = 0; r < NI; ++r) ev[r] = c0 + min(4 * r + q, ne - 1);
+        if (msg_row) {                                   // one uniform branch around all slots
+#pragma unroll
+            for (int r = 0; r < NI; ++r) rw[r] = msg_row[ev[r]];
+        } else {
+#pragma unroll
+            for (int r = 0; r < NI; ++r) rw[r] = ev[r];
+        }
+#pragma unroll
+        for (int r = 0; r < NI; ++r) {
+            const float p = phi[ev[r] * ld_phi + j];
+            ph[r] = 4 * r + q < ne ? p : 0.f;
+#pragma unroll
+            for (int c = 0; c < KB; ++c) mb[c][r] = msg[rw[r] * ld_msg + 16 * c + j];
+#pragma unroll
+            for (int xx = 0; xx < NXW; ++xx) yv[xx][r] = Y[ev[r] * ld_Y + x0 + xx];
+        }
+        // keep every load here, ahead of the products (the compiler would otherwise sink each slot's
+        // loads into its conditional block: a memory latency per slot)
+#pragma unroll
+        for (int r = 0; r < NI; ++r) {
+            asm volatile("" ::"v"(ph[r]));
+#pragma unroll
+            for (int c = 0; c < KB; ++c) asm volatile("" ::"v"(mb[c][r]));
+#pragma unroll
+            for (int xx = 0; xx < NXW; ++xx) asm volatile("" ::"v"(yv[xx][r]));
+        }
+#pragma unroll
+        for (int xx = 0; xx < NXW; ++xx) {
+#pragma unroll
+            for (int r = 0; r < NI; ++r) {
+                if (r < ni) {
+                    const float u = yv[xx][r] * ph[r];
+#pragma unroll
+                    for (int c = 0; c < KB; ++c) acc[xx][c] = mfma_16x16x4(u, mb[c][r], acc[xx][c]);
+                }
+            }
+            if (last) store(xx);
+        }
     }
 }
 
@@ -377,10 +395,7 @@ __global__ __launch_bounds__((WPA > 1 ? WPA : kDbWaves) * kWave) void density_bw
             for (int r = 0; r < 4; ++r) {
                 dph[r] = fmaf(sv[r], ys[(4 * q + r) * kDbYS + x], dph[r]);
                 float v = sv[r] * phT[r];
-                v += __shfl_xor(v, 1, kWave);
-                v += __shfl_xor(v, 2, kWave);
-                v += __shfl_xor(v, 4, kWave);
-                v += __shfl_xor(v, 8, kWave);
+                v = row16_sum(v);
                 if (j == (xx & 15)) dyk[r][xx >> 4] = v;
             }
         }
@@ -527,10 +542,7 @@ __global__ __launch_bounds__(kDsWaves * kWave) void density_bwd_split_kernel(
             for (int r = 0; r < 4; ++r) {
                 dph[r] = fmaf(sv[r], sY[(4 * q + r) * kDbYS + x], dph[r]);
                 float v = sv[r] * phT[r];
-                v += __shfl_xor(v, 1, kWave);
-                v += __shfl_xor(v, 2, kWave);
-                v += __shfl_xor(v, 4, kWave);
-                v += __shfl_xor(v, 8, kWave);
+                v = row16_sum(v);
                 if (j == xx) dyk[r] = v;
             }
         }
@@ -676,10 +688,7 @@ __global__ __launch_bounds__(kDbLWaves * kWave) void density_bwd_lds_kernel(
                     for (int r = 0; r < 4; ++r) {
                         dph[r] = fmaf(sv[r], ys[(4 * q + r) * kDbYS + x], dph[r]);
                         float v = sv[r] * phT[r];
-                        v += __shfl_xor(v, 1, kWave);
-                        v += __shfl_xor(v, 2, kWave);
-                        v += __shfl_xor(v, 4, kWave);
-                        v += __shfl_xor(v, 8, kWave);
+                        v = row16_sum(v);
                         if (j == xl) dyk[r] = v;
                     }
                 }
@@ -1703,16 +1712,16 @@ extern "C" int face_density_fwd(const float* phi, int32_t ld_phi, const float* m
     RankOut D;
     if (!phi || !msg || !Y || !rank_out(D_ranks, atom_stride, x_stride, NX, D)) return FACE_ERR_ARG;
     if (NX == 20 && B == 16 && K % 16 == 0 && K <= 64) {          // matrix cores
-#define FACE_DFM(KB_)                                                                                          \
-    hipLaunchKernelGGL(density_fwd_mfma_kernel<KB_>, dim3((unsigned)N), dim3(kDfWaves * kWave), 0,             \
+#define FACE_DFR(KB_)                                                                                         \
+    hipLaunchKernelGGL((density_fwd_row_kernel<KB_>), dim3((unsigned)N), dim3(kDrWaves * kWave), 0,              \
                        (hipStream_t)stream, phi, ld_phi, msg, ld_msg, msg_row, Y, ld_Y, row_ptr, M, D)
         switch (K / 16) {
-            case 1: FACE_DFM(1); break;
-            case 2: FACE_DFM(2); break;
-            case 3: FACE_DFM(3); break;
-            default: FACE_DFM(4); break;
+            case 1: FACE_DFR(1); break;
+            case 2: FACE_DFR(2); break;
+            case 3: FACE_DFR(3); break;
+            default: FACE_DFR(4); break;
         }
-#undef FACE_DFM
+#undef FACE_DFR
         FACE_LAUNCH_CHECK();
         return 0;
     }

@@ -271,10 +271,7 @@ __global__ __launch_bounds__(kDmWaves * kWave) void density_mix_bwd_kernel(
                     for (int r = 0; r < 4; ++r) {
                         dph[r] = fmaf(sv[r], ys[(4 * q + r) * kDmYS + x], dph[r]);
                         float v = sv[r] * phT[r];
-                        v += __shfl_xor(v, 1, kWave);
-                        v += __shfl_xor(v, 2, kWave);
-                        v += __shfl_xor(v, 4, kWave);
-                        v += __shfl_xor(v, 8, kWave);
+                        v = row16_sum(v);
                         if (j == xx) dyk[r] = v;
                     }
                 }
