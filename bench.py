@@ -237,7 +237,7 @@ def algorithmic_flops(label, g, kw):
     head (E x H by H x 4C), the pass message's d W_d^T (E x 4Kd by 4Kd x K) and its input
     gradient, the fused CP radial backward (d h2 = dR W_cp, E x 4C by 4C x H, plus the two
     20-monomial contractions per edge and channel), and the factor density's per-monomial
-    products (2 E 20 B K each way; 3 of them in the backward), and the radial MLP of each pass (nb ->
+    products (2 E 20 B K forward; two such in the backward, plus the 2 E 20 B of dphi and dY), and the radial MLP of each pass (nb ->
     H -> H -> B per edge; the backward recomputes the hidden layers instead of reading them)."""
     label, units = split_label(label)
     if units > 1:
@@ -281,12 +281,12 @@ def algorithmic_flops(label, g, kw):
         return 2 * N * 2 * C * 10 * C + gate * 2 * N * 2 * C * 9 * C
     if label == "density_fwd20":
         return 2 * E * 20 * kw["B"] * kw["K"]
-    if label == "density_bwd20":
-        return 3 * 2 * E * 20 * kw["B"] * kw["K"]
+    if label == "density_bwd20":         # S = msg G_x^T and dmsg = (Y_x phi) G_x; dphi, dY from S
+        return 2 * 2 * E * 20 * kw["B"] * kw["K"] + 2 * 2 * E * 20 * kw["B"]
     if label == "density_mix_fwd":        # density products + the four mixes (20 rows per atom)
         return 2 * E * 20 * kw["B"] * kw["K"] + 2 * 20 * N * cin * C
     if label == "density_mix_bwd":
-        return 3 * 2 * E * 20 * kw["B"] * kw["K"] + 2 * 20 * N * cin * C
+        return 2 * 2 * E * 20 * kw["B"] * kw["K"] + 2 * 2 * E * 20 * kw["B"] + 2 * 20 * N * cin * C
     return None
 
 
@@ -915,7 +915,9 @@ def compact_cpu(cpu):
 
 def north_star_kernels(r):
     """HBM fraction of the density kernels and of the force scatter (the kernels the target is
-    quoted on): per family present, the fraction of 8 TB/s its algorithmic bytes reach."""
+    quoted on): per family present, the fraction of 8 TB/s its algorithmic bytes reach. The force
+    backward is also given as one unit, the edge backward (which writes every edge's dL/dvec into
+    its reverse edge's slot) and the row scatter that completes it: their bytes over their time."""
     out = {}
     for fam_name in DENSITY_FAMILIES + ("force_scatter",):
         f = r["families"].get(fam_name)
@@ -923,6 +925,12 @@ def north_star_kernels(r):
             continue
         gbs = f["alg_bytes_per_launch"] / (f["avg_us"] * 1e-6) / 1e9
         out[fam_name] = {"us": _r(f["avg_us"]), "GBps": _r(gbs), "hbm_frac": _r(gbs / HBM_PEAK_GBS, 3)}
+    fe, fs = r["families"].get("edge_geom_bwd"), r["families"].get("force_scatter")
+    if fe and fs and fe.get("alg_bytes_per_launch") and fs.get("alg_bytes_per_launch"):
+        byts = fe["bytes_per_step"] + fs["bytes_per_step"]
+        ms = fe["ms_per_step"] + fs["ms_per_step"]
+        gbs = byts / (ms * 1e-3) / 1e9
+        out["force_bwd"] = {"us": _r(1e3 * ms), "GBps": _r(gbs), "hbm_frac": _r(gbs / HBM_PEAK_GBS, 3)}
     return out
 
 

@@ -140,29 +140,14 @@ __device__ __forceinline__ bool any_slot(const float* const (&p)[kEdgeGradSlots]
     return a;
 }
 
-// edge_dvec with the gradients of each input summed over its slots. Each slot's values are read
-// in one batch (float4 rows) under a uniform branch before they are added: loads split over
-// separate branches would each wait for the one before.
-__device__ __forceinline__ void edge_dvec_slots(const EdgeGeom& g, int64_t e, const float* __restrict__ freq, int nb,
-                                                float rc, float bes_scale, const EdgeGrads& G, float* out) {
+// dL/dvec of one edge from its input gradients already summed over the readers' slots: q (20) the
+// monomial gradients (has_y), qb (nb <= 16) the radial-basis gradients (has_rb), genv_t and g_r
+// the envelope and distance gradients.
+__device__ __forceinline__ void edge_dvec_sums(const EdgeGeom& g, const float* __restrict__ freq, int nb, float rc,
+                                               float bes_scale, bool has_y, const float (&q)[20], bool has_rb,
+                                               const float (&qb)[16], float genv_t, float g_r, float* out) {
     float gu[3] = {0.f, 0.f, 0.f};
-    if (any_slot(G.y)) {
-        float q[20];
-#pragma unroll
-        for (int k = 0; k < 20; ++k) q[k] = 0.f;
-#pragma unroll
-        for (int s = 0; s < kEdgeGradSlots; ++s) {
-            if (G.y[s]) {
-                const v4f* src = reinterpret_cast<const v4f*>(G.y[s] + e * 20);
-                v4f t[5];
-#pragma unroll
-                for (int c = 0; c < 5; ++c) t[c] = src[c];
-#pragma unroll
-                for (int c = 0; c < 5; ++c)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) q[4 * c + r] += t[c][r];
-            }
-        }
+    if (has_y) {
         const float x = g.u[0], y = g.u[1], z = g.u[2];
         gu[0] = q[1] + 2.f * x * q[4] + y * q[7] + z * q[8] + 3.f * x * x * q[10] + 2.f * x * y * q[13] +
                 2.f * x * z * q[14] + y * y * q[15] + z * z * q[17] + y * z * q[19];
@@ -173,23 +158,7 @@ __device__ __forceinline__ void edge_dvec_slots(const EdgeGeom& g, int64_t e, co
     }
     if (g.valid) {
         const float ev = envelope(g);
-        float genv_t = slot_sum(G.env, e);
-        float g_r = slot_sum(G.r, e);
-        if (any_slot(G.rb)) {
-            // rb gradient rows (nb <= 16), summed over the slots, each slot read in one batch
-            float qb[16];
-#pragma unroll
-            for (int n = 0; n < 16; ++n) qb[n] = 0.f;
-#pragma unroll
-            for (int s = 0; s < kEdgeGradSlots; ++s) {
-                if (G.rb[s]) {
-                    float t[16];
-#pragma unroll
-                    for (int n = 0; n < 16; ++n) t[n] = n < nb ? G.rb[s][e * nb + n] : 0.f;
-#pragma unroll
-                    for (int n = 0; n < 16; ++n) qb[n] += t[n];
-                }
-            }
+        if (has_rb) {
             const float inv_r = 1.f / g.r;
 #pragma unroll
             for (int n = 0; n < 16; ++n) {
@@ -228,30 +197,112 @@ __global__ __launch_bounds__(256) void edge_geom_bwd_kernel(
 }
 
 // Edge backward with the own-row half of the force scatter folded in (CSR lists, no mask). One
-// thread per edge computes dL/dvec_e as edge_geom_bwd_kernel does and writes it to the slot of
-// the edge's REVERSE, gvec_rev[rev e], so that row k of gvec_rev holds the dL/dvec of the edges
-// whose neighbour is k, contiguous for the scatter that follows. The row's own sum is reduced
-// inside the wave: rows are contiguous edge ranges, so a segmented scan over the wave's 64 edges
-// (segments = receiver atoms) leaves, at the last edge of each row inside a 64-edge window, the sum
-// of the row's edges in that window; it is written to wsum at that edge's index (the other wsum
-// slots are never written or read). Every sum has a fixed order: no atomics.
+// lane per edge computes dL/dvec_e as edge_geom_bwd_kernel does and writes it, as one 16-byte row
+// (x, y, z, 0), to the slot of the edge's REVERSE, gvec_rev[rev e], so that row k of gvec_rev holds
+// the dL/dvec of the edges whose neighbour is k, contiguous for the scatter that follows.
+// Each wave takes a window of 64 consecutive edges, and every global load of the window is issued
+// before the first use: the lane's own Y gradient rows (float4 pieces), the window's radial-basis
+// gradient rows read as consecutive 4-byte pieces (256 bytes per instruction), summed over the
+// slots in that layout and handed to each edge's lane through LDS (rows padded to nb + 1 floats
+// against bank conflicts), then the geometry. Measured at the 24,000-atom liquid against a lane
+// reading every row itself, each slot under its own branch: 151 -> 119 us; staging the Y rows
+// through LDS as well: 131 us; basis rows read by their own lane (4-byte loads at a 32-byte
+// stride): 138 us. The reverse-slot writes are scattered 16-byte rows: written in edge order
+// instead (a timing probe only) the kernel takes 106 us; non-temporal stores: 139 us.
+// The row's own sum is reduced inside the wave: rows are contiguous edge ranges, so a segmented
+// scan over the window (segments = receiver atoms) leaves, at the last edge of each row inside the
+// window, the sum of the row's edges in that window; it is written to wsum at that edge's index
+// (the other wsum rows are never written or read). Every sum has a fixed order: no atomics.
 __global__ __launch_bounds__(256) void edge_geom_bwd_seg_kernel(
     const float* __restrict__ pos, const int32_t* __restrict__ recv, const int32_t* __restrict__ col,
     const float* __restrict__ shift, const int32_t* __restrict__ rev, int64_t E, const float* __restrict__ freq,
-    int nb, float rc, float bes_scale, EdgeGrads G, float* __restrict__ gvec_rev, float* __restrict__ wsum) {
-    const int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;   // windows of 64 edges = one wave
-    const int lane = threadIdx.x & (kWave - 1);
-    const bool valid = e < E;
-    float out[3] = {0.f, 0.f, 0.f};
+    int nb, float rc, float bes_scale, EdgeGrads G, v4f* __restrict__ gvec_rev, v4f* __restrict__ wsum) {
+    __shared__ float sB[4][17 * kWave];
+    const int lane = threadIdx.x & (kWave - 1), w = threadIdx.x / kWave;
+    const int64_t e0 = ((int64_t)blockIdx.x * 4 + w) * kWave;   // the wave's window
+    if (e0 >= E) return;                                // whole wave past the end (no workgroup barrier)
+    const int nwin = E - e0 < kWave ? (int)(E - e0) : kWave;
+    const int64_t e = e0 + lane;
+    const bool valid = lane < nwin;
+    const bool has_y = any_slot(G.y), has_rb = any_slot(G.rb);
+    // every global load of the window issued first: the staged rows, then the lane's own operands
+    v4f ay[5];
+    float ab[16];
+#pragma unroll
+    for (int c = 0; c < 5; ++c) ay[c] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 16; ++c) ab[c] = 0.f;
+    if (has_y && valid) {
+#pragma unroll
+        for (int s = 0; s < kEdgeGradSlots; ++s) {
+            if (G.y[s]) {
+                const v4f* src = reinterpret_cast<const v4f*>(G.y[s] + e * 20);
+                v4f t[5];
+#pragma unroll
+                for (int c = 0; c < 5; ++c) t[c] = src[c];
+#pragma unroll
+                for (int c = 0; c < 5; ++c) ay[c] += t[c];
+            }
+        }
+    }
+    if (has_rb) {
+#pragma unroll
+        for (int s = 0; s < kEdgeGradSlots; ++s) {
+            if (G.rb[s]) {
+                const float* src = G.rb[s] + e0 * nb;
+                float t[16];
+#pragma unroll
+                for (int c = 0; c < 16; ++c) {
+                    const int f = c * kWave + lane;
+                    t[c] = c < nb && f < nwin * nb ? src[f] : 0.f;
+                }
+#pragma unroll
+                for (int c = 0; c < 16; ++c) ab[c] += t[c];
+            }
+        }
+    }
+    float genv_t = 0.f, g_r = 0.f;
+    EdgeGeom g;
     int key = -1;
+    int64_t r_e = 0;
     if (valid) {
-        const EdgeGeom g = edge_geom(pos, recv, col, shift, nullptr, e, rc);
-        edge_dvec_slots(g, e, freq, nb, rc, bes_scale, G, out);
-        const int64_t r = rev[e];
-        gvec_rev[r * 3 + 0] = out[0];
-        gvec_rev[r * 3 + 1] = out[1];
-        gvec_rev[r * 3 + 2] = out[2];
+        genv_t = slot_sum(G.env, e);
+        g_r = slot_sum(G.r, e);
+        g = edge_geom(pos, recv, col, shift, nullptr, e, rc);
         key = recv[e];
+        r_e = rev[e];
+    }
+    if (has_rb) {
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+            if (c < nb) {                                // piece f = edge f / nb, basis f % nb
+                const int f = c * kWave + lane, ed = f / nb;
+                sB[w][ed * (nb + 1) + (f - ed * nb)] = ab[c];
+            }
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+    float q[20], qb[16];
+#pragma unroll
+    for (int k = 0; k < 20; ++k) q[k] = 0.f;
+#pragma unroll
+    for (int n = 0; n < 16; ++n) qb[n] = 0.f;
+    if (has_y) {
+#pragma unroll
+        for (int c = 0; c < 5; ++c) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) q[4 * c + r] = ay[c][r];
+        }
+    }
+    if (has_rb) {
+#pragma unroll
+        for (int n = 0; n < 16; ++n)
+            if (n < nb) qb[n] = sB[w][lane * (nb + 1) + n];
+    }
+    float out[3] = {0.f, 0.f, 0.f};
+    if (valid) {
+        edge_dvec_sums(g, freq, nb, rc, bes_scale, has_y, q, has_rb, qb, genv_t, g_r, out);
+        gvec_rev[r_e] = v4f{out[0], out[1], out[2], 0.f};
     }
     // segmented inclusive scan: keys are non-decreasing along the wave, so equal keys d lanes
     // apart bound a run of one row
@@ -266,11 +317,7 @@ __global__ __launch_bounds__(256) void edge_geom_bwd_seg_kernel(
         }
     }
     const int kn = __shfl_down(key, 1, kWave);
-    if (valid && (lane == kWave - 1 || kn != key)) {
-        wsum[e * 3 + 0] = out[0];
-        wsum[e * 3 + 1] = out[1];
-        wsum[e * 3 + 2] = out[2];
-    }
+    if (valid && (lane == kWave - 1 || kn != key)) wsum[e] = v4f{out[0], out[1], out[2], 0.f};
 }
 
 __global__ __launch_bounds__(256) void gather_rows_kernel(const float* __restrict__ X, int ld_X,
@@ -364,11 +411,12 @@ __global__ __launch_bounds__(256) void force_scatter_kernel(const float* __restr
 
 // grad[k] = sign * sum_{e in row k} (gvec_rev[e] - own_e), own_e = wsum[e] at the last edge of the
 // row in each 64-edge window (e % 64 == 63 or e == end of row) and 0 elsewhere: the force scatter
-// as one contiguous pass over each row (gvec_rev and wsum from edge_geom_bwd_seg_kernel). G lanes
-// per atom read the row's 12-byte entries coalesced; partial sums reduced by butterfly shuffles.
+// as one contiguous pass over each row (gvec_rev and wsum from edge_geom_bwd_seg_kernel, 16-byte
+// rows). G lanes per atom read the row's entries coalesced; partial sums reduced by butterfly
+// shuffles.
 template <int G>
-__global__ __launch_bounds__(256) void force_scatter_rows_kernel(const float* __restrict__ gvec_rev,
-                                                                 const float* __restrict__ wsum,
+__global__ __launch_bounds__(256) void force_scatter_rows_kernel(const v4f* __restrict__ gvec_rev,
+                                                                 const v4f* __restrict__ wsum,
                                                                  const int32_t* __restrict__ row_ptr, int64_t N,
                                                                  float sign, float* __restrict__ grad) {
     const int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
@@ -378,13 +426,15 @@ __global__ __launch_bounds__(256) void force_scatter_rows_kernel(const float* __
     const int64_t e0 = live ? row_ptr[k] : 0, e1 = live ? row_ptr[k + 1] : 0;
     float s0 = 0.f, s1 = 0.f, s2 = 0.f;
     for (int64_t e = e0 + l; e < e1; e += G) {
-        s0 += gvec_rev[e * 3 + 0];
-        s1 += gvec_rev[e * 3 + 1];
-        s2 += gvec_rev[e * 3 + 2];
+        const v4f a = gvec_rev[e];
+        s0 += a[0];
+        s1 += a[1];
+        s2 += a[2];
         if ((e & (kWave - 1)) == kWave - 1 || e == e1 - 1) {
-            s0 -= wsum[e * 3 + 0];
-            s1 -= wsum[e * 3 + 1];
-            s2 -= wsum[e * 3 + 2];
+            const v4f b = wsum[e];
+            s0 -= b[0];
+            s1 -= b[1];
+            s2 -= b[2];
         }
     }
     s0 = group_sum(s0, G);
@@ -660,12 +710,15 @@ extern "C" int face_edge_geom_bwd_seg(const float* pos, const int32_t* recv, con
         G.env[k] = genv ? genv[k] : nullptr;
         G.r[k] = gr ? gr[k] : nullptr;
         if (G.rb[k] && (!freq || n_basis == 0 || n_basis > 16)) return FACE_ERR_ARG;
-        if (G.y[k] && ((uintptr_t)G.y[k] & 15)) return FACE_ERR_UNSUPPORTED;     // float4 rows of 20
+        if (G.y[k] && ((uintptr_t)G.y[k] & 15)) return FACE_ERR_UNSUPPORTED;     // 16-byte pieces of Y rows
     }
     if (E == 0) return 0;
     if (!pos || !recv || !col || !shift || !rev || !gvec_rev || !wsum) return FACE_ERR_ARG;
-    hipLaunchKernelGGL(edge_geom_bwd_seg_kernel, dim3(blocks_for(E)), dim3(256), 0, (hipStream_t)stream, pos, recv,
-                       col, shift, rev, E, freq, n_basis, rc, bes_scale, G, gvec_rev, wsum);
+    if (((uintptr_t)gvec_rev & 15) || ((uintptr_t)wsum & 15)) return FACE_ERR_UNSUPPORTED;
+    const unsigned grid = (unsigned)((E + 4 * kWave - 1) / (4 * kWave));
+    hipLaunchKernelGGL(edge_geom_bwd_seg_kernel, dim3(grid), dim3(4 * kWave), 0, (hipStream_t)stream, pos, recv, col,
+                       shift, rev, E, freq, n_basis, rc, bes_scale, G, reinterpret_cast<v4f*>(gvec_rev),
+                       reinterpret_cast<v4f*>(wsum));
     FACE_LAUNCH_CHECK();
     return 0;
 }
@@ -675,13 +728,16 @@ extern "C" int face_force_scatter_rows(const float* gvec_rev, const float* wsum,
     if (N < 0) return FACE_ERR_ARG;
     if (N == 0) return 0;
     if (!gvec_rev || !wsum || !row_ptr || !grad) return FACE_ERR_ARG;
+    if (((uintptr_t)gvec_rev & 15) || ((uintptr_t)wsum & 15)) return FACE_ERR_UNSUPPORTED;
     const hipStream_t st = (hipStream_t)stream;
+    const v4f* gv = reinterpret_cast<const v4f*>(gvec_rev);
+    const v4f* ws = reinterpret_cast<const v4f*>(wsum);
     // lanes per row ~ a third of the mean row length: two or three edges per lane
     if (mean_row <= 24) {
-        hipLaunchKernelGGL(force_scatter_rows_kernel<8>, dim3(blocks_for(N * 8)), dim3(256), 0, st, gvec_rev, wsum,
-                           row_ptr, N, sign, grad);
+        hipLaunchKernelGGL(force_scatter_rows_kernel<8>, dim3(blocks_for(N * 8)), dim3(256), 0, st, gv, ws, row_ptr,
+                           N, sign, grad);
     } else {
-        hipLaunchKernelGGL(force_scatter_rows_kernel<16>, dim3(blocks_for(N * 16)), dim3(256), 0, st, gvec_rev, wsum,
+        hipLaunchKernelGGL(force_scatter_rows_kernel<16>, dim3(blocks_for(N * 16)), dim3(256), 0, st, gv, ws,
                            row_ptr, N, sign, grad);
     }
     FACE_LAUNCH_CHECK();

@@ -83,7 +83,7 @@ _SIGS = {
     "face_layer_norm_bwd": (ctypes.c_int, [P, P, I64, I32, P, P, P, P, P]),
 }
 
-ABI_VERSION = 22
+ABI_VERSION = 23
 
 
 class LinProblem(ctypes.Structure):

@@ -87,7 +87,7 @@ class EdgeGeometry(torch.autograd.Function):
     def backward(ctx, *grads):
         pos, freq = ctx.saved_tensors
         g = ctx.graph
-        gvec = torch.empty(g.E, 3, device=pos.device)
+        gvec = torch.empty(g.E, 4, device=pos.device)          # 16-byte rows (x, y, z, unused)
         keep = []
 
         def slots(gs):
@@ -105,7 +105,7 @@ class EdgeGeometry(torch.autograd.Function):
         # edge backward: each edge's dL/dvec lands in its reverse edge's slot and the own-row sums are
         # reduced per 64-edge window in the same pass (wsum), so the scatter reads one contiguous row
         # per atom, no reverse-edge gathers: grad_k = sum_{e in row k} gvec[rev e] - gvec[e]
-        wsum = torch.empty(g.E, 3, device=pos.device)
+        wsum = torch.empty(g.E, 4, device=pos.device)
         call("face_edge_geom_bwd_seg", ptr(pos), ptr(g.recv), ptr(g.col), ptr(g.shift), ptr(g.rev), g.E, ptr(freq),
              freq.numel(), float(ctx.rc), float(ctx.bes_scale), *groups, ptr(gvec), ptr(wsum), st, label="edge_bwd")
         gpos = torch.empty_like(pos)

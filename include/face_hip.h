@@ -482,9 +482,10 @@ int face_force_scatter(const float* gvec, const int32_t* row_ptr, const int32_t*
                        float* grad, void* stream);
 /* The same force scatter without reverse-edge gathers, in two passes over a CSR list (no mask):
  * face_edge_geom_bwd_seg computes dL/dvec of every edge as face_edge_geom_bwd does and writes it
- * to the slot of the edge's reverse, gvec_rev[rev e] (E,3); its own-row sums are reduced per
- * window of 64 consecutive edges (e / 64) and written to wsum (E,3) at the last edge of the row
- * in the window (wsum's other rows are left unwritten). face_force_scatter_rows then writes
+ * to the slot of the edge's reverse, gvec_rev[rev e], as a 16-byte row (x, y, z, 0) of an (E,4)
+ * buffer; its own-row sums are reduced per window of 64 consecutive edges (e / 64) and written to
+ * wsum (E,4) at the last edge of the row in the window (wsum's other rows are left unwritten).
+ * Both buffers 16-byte aligned; Y gradient buffers too. face_force_scatter_rows then writes
  * grad[k] = sign * sum_{e in row k} (gvec_rev[e] - [e is the row's last edge in its window] wsum[e]),
  * reading each row contiguously. mean_row (~E/N) picks the lanes per row. Fixed summation
  * order, no atomics. Replaces the index_add backward of pos[nbr] - pos[i] (face/model.py:670;

@@ -385,13 +385,15 @@ def test_gathers_and_force_scatter_match_index_add():
     # the contiguous row form: reverse slots and per-window own-row sums laid out as the edge backward
     # (face_edge_geom_bwd_seg) writes them, wsum filled only at the last edge of each row in each
     # 64-edge window (NaN elsewhere: never read), then the row pass (both lane widths)
-    gvec_rev = gvec[g.rev.long()].contiguous()
+    # (16-byte rows: x, y, z and an unused fourth float, NaN here)
+    gvec_rev = torch.full((g.E, 4), float("nan"), device=DEV)
+    gvec_rev[:, :3] = gvec[g.rev.long()]
     e_idx = torch.arange(g.E, device=DEV)
     seg = recv * ((g.E + 63) // 64) + e_idx // 64
     _, inv, cnt = torch.unique_consecutive(seg, return_inverse=True, return_counts=True)
     sums = torch.zeros(cnt.numel(), 3, device=DEV).index_add(0, inv, gvec)
-    wsum = torch.full((g.E, 3), float("nan"), device=DEV)
-    wsum[torch.cumsum(cnt, 0) - 1] = sums
+    wsum = torch.full((g.E, 4), float("nan"), device=DEV)
+    wsum[torch.cumsum(cnt, 0) - 1, :3] = sums
     for mean_row in (16, 40):
         grad2 = torch.full((g.N, 3), float("nan"), device=DEV)
         call("face_force_scatter_rows", ptr(gvec_rev), ptr(wsum), ptr(g.row_ptr), g.N, mean_row, -1.0, ptr(grad2),
