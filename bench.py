@@ -463,11 +463,21 @@ def run_gpu(k, steps, warmup, use_graph=True, compiled_radial=False):
         f"{g.N / ms_step * 1e3:.0f} atom-steps/s; graph nodes {nodes}")
     kern = label_stats(timers, steps, g, kw)
     fam = family_stats(kern)
+    # the density route the step took (labels of the launches it made)
+    if any(lab.startswith("density_mix") for lab in kern):
+        route = "fused factor density + mix (density_mix)"
+    elif any(lab.startswith("density_fwd") for lab in kern):
+        route = "factor density written, then the row-GEMM mix"
+    elif any(lab.startswith("cp_") for lab in kern):
+        route = "CP pooling written, then the row-GEMM mix"
+    else:
+        route = None
     tag = TAGS[k] + ("_compiled" if compiled_radial else "")
     out = {"N": g.N, "E": g.E, "max_row": g.max_row, "ms_per_step": ms_step, "ms_min": min(ms), "ms_max": max(ms),
            "rounds": len(ms), "atom_steps_per_s": g.N / ms_step * 1e3, "kernels": kern, "families": fam,
            "roofline": roofline_of(fam, tag), "pairlist_ms": 1e3 * t_nbr, "desc": desc, "kw": kw, "mode": mode,
-           "graph_nodes": nodes, "eager_ms_per_step": 1e3 * statistics.median(eager), "peak_mem_gb": peak_gb}
+           "graph_nodes": nodes, "eager_ms_per_step": 1e3 * statistics.median(eager), "peak_mem_gb": peak_gb,
+           "route": route}
     del m, g
     torch.cuda.empty_cache()
     return out
