@@ -396,6 +396,25 @@ def roofline_of(fam, tag):
             else None}
 
 
+_SPIN_PER_S = None
+
+
+def spin_cycles(seconds):
+    """Argument of torch.cuda._sleep for a device spin of about `seconds` (rate measured once)."""
+    global _SPIN_PER_S
+    if _SPIN_PER_S is None:
+        n = 1 << 22
+        torch.cuda._sleep(n)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        torch.cuda._sleep(4 * n)
+        e.record()
+        torch.cuda.synchronize()
+        _SPIN_PER_S = 4 * n / (s.elapsed_time(e) * 1e-3)
+    return int(seconds * _SPIN_PER_S)
+
+
 def trace_mark():
     """One launch of a kernel the model never runs (the gather form of the force scatter, on one
     atom), outside any timed region: in a kernel trace, the dispatches between two marks are
@@ -435,14 +454,26 @@ def run_gpu(k, steps, warmup, use_graph=True, compiled_radial=False):
     torch.cuda.synchronize()
     log(f"[bench]   warm-up done ({warmup} steps)")
     torch.cuda.reset_peak_memory_stats()
-    # eager steps with HIP events around every hot-kernel launch (kernel durations), recorded on
-    # torch's current stream, the stream every entry point launches on
-    timers = _lib.time_calls(TIMED)
-    eager = timed_rounds(step, steps)
-    _lib.stop_timing()
+    eager = timed_rounds(step, min(steps, 2 * CALLS_PER_ROUND))
     peak_gb = torch.cuda.max_memory_allocated() / 1e9
-    log(f"[bench]   eager (instrumented): {1e3 * statistics.median(eager):.3f} ms/step, peak device memory "
-        f"{peak_gb:.2f} GB")
+    log(f"[bench]   eager: {1e3 * statistics.median(eager):.3f} ms/step, peak device memory {peak_gb:.2f} GB")
+    # eager steps with HIP events around every hot-kernel launch (kernel durations), recorded on
+    # torch's current stream, the stream every entry point launches on. Each step is queued behind
+    # a device spin longer than the host takes to enqueue it, so its launches run back to back:
+    # otherwise, where the host enqueues slower than the GPU runs (small systems), a start event
+    # fires while the GPU waits for the launch and the wait counts as kernel time.
+    t0 = time.perf_counter()
+    step()
+    t_host = time.perf_counter() - t0
+    spin = spin_cycles(2.0 * t_host + 2e-3)
+    torch.cuda.synchronize()
+    timers = _lib.time_calls(TIMED)
+    for _ in range(steps):
+        torch.cuda._sleep(spin)
+        step()
+    torch.cuda.synchronize()
+    _lib.stop_timing()
+    log(f"[bench]   instrumented: {steps} steps, each queued behind a {1e3 * (2.0 * t_host + 2e-3):.1f} ms device spin")
     rounds, mode, nodes = eager, "eager", None
     if use_graph:
         # HIP-graph replay of the whole E+F step, positions copied into the static input
@@ -580,10 +611,10 @@ PROBE_MARK = "force_scatter_kernel"
 
 
 def _after_mark(rows):
-    """Dispatch records (sorted by Dispatch_Id) after the probe's first marker launch (the one
-    between the untimed first step and the recorded steps)."""
-    ids = [i for i, r in enumerate(rows) if _kernel_base(r["Kernel_Name"]) == PROBE_MARK]
-    return rows[ids[0] + 1:] if ids else rows
+    """Dispatch records (sorted by Dispatch_Id; one per counter of a dispatch) after the probe's
+    first marker launch (the one between the untimed first step and the recorded steps)."""
+    ids = [int(r["Dispatch_Id"]) for r in rows if _kernel_base(r["Kernel_Name"]) == PROBE_MARK]
+    return [r for r in rows if int(r["Dispatch_Id"]) > ids[0]] if ids else rows
 
 
 def _label_dispatches(rows, order, what):

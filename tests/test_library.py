@@ -233,3 +233,24 @@ def test_bench_line_is_compact_strict_json():
     assert w["cpu_baseline"] == 1393.0 and w["roofline"]["kernel"] == "rows_gemm"
     assert "force_scatter" in w["hbm"] and "cp_density_fwd" in w["hbm"]
     assert "cpu_baseline" not in d["also"]["workload3_compiled_radial"]
+
+
+def test_probe_dispatches_are_labelled_by_call_markers():
+    """Counter records of a probe run (one record per counter of a dispatch) are labelled by the
+    marker launched after every library call: the dispatches between two markers belong to one
+    call, whatever kernels it launched, and the start marker's own records do not shift them."""
+    import bench
+    mark = "void face::force_scatter_kernel<16>(float const*)"
+    seq = [("face::edge_geom_fwd_kernel(float)", 1), (mark, 2), ("face::edge_geom_fwd_kernel(float)", 3), (mark, 4),
+           ("void face::rows_gemm_kc_kernel<16>(x)", 5), ("void face::rows_gemm_kernel<8, 16, false, 1>(x)", 6),
+           (mark, 7), ("face::node_ln_fwd_kernel(x)", 8), (mark, 9), ("__amd_rocclr_copyBuffer", 10)]
+    rows = [{"Kernel_Name": n, "Dispatch_Id": str(i), "Counter_Name": c} for n, i in seq for c in ("A", "B", "C")]
+    recs = bench._after_mark(rows)
+    disp = {}
+    for r in recs:
+        disp.setdefault(r["Dispatch_Id"], r)
+    labs = [(lab, int(r["Dispatch_Id"])) for lab, r in bench._label_dispatches(list(disp.values()), ["edge_fwd",
+                                                                                                      "mix_fwd",
+                                                                                                      "node_ln_fwd"],
+                                                                             "t")]
+    assert labs == [("edge_fwd", 3), ("mix_fwd", 5), ("mix_fwd", 6), ("node_ln_fwd", 8)], labs
