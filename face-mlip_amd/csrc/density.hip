@@ -12,6 +12,7 @@
 // tensor (p[l] = D_l, sa = W, sx = N*W) so the channel-mixing GEMMs read contiguous blocks.
 #include "common.h"
 
+#include <algorithm>
 #include <cstdlib>
 
 namespace face {
@@ -123,8 +124,12 @@ __global__ __launch_bounds__(kBlock) void density_fwd_kernel(
 // tile prefetched and all stores at the end (the same products, summed in another order): 864-atom FCC
 // 14.0 -> 13.4 us, 64 molecules 16.5 -> 16.3 us, 100,000 atoms at K = 64 4453 -> 4168 us.
 // Measured and not kept: 5 or 10 waves per atom (each reloads the chunk's phi and message rows:
-// 864 atoms 15.2 / 16.9 us), and a workgroup whose computing waves hand finished tiles through
-// LDS to a storing wave so that no product waits behind a store (864 atoms 14.4 us).
+// 864 atoms 15.2 / 16.9 us); a workgroup whose computing waves hand finished tiles through LDS to
+// a storing wave so that no product waits behind a store (864 atoms 14.4 us); persistent
+// workgroups streaming several atoms each, the next atom's chunk staged through a double-buffered
+// LDS tile while the current one is multiplied and stored (one, two or four workgroups per CU:
+// 864 atoms 18.2 / 13.4 / 14.3 us, 64 molecules 24.7 / 17.2 / 16.3 us, 100,000 atoms 7.2 / 4.9 /
+// 4.9 ms).
 constexpr int kDrWaves = 4;
 constexpr int kDrCh = 32;                                // edges per register chunk
 
