@@ -461,7 +461,7 @@ __global__ __launch_bounds__((WPA > 1 ? WPA : kDbWaves) * kWave) void density_bw
 // rows load, and stay in registers over the atom's tiles; per 16-edge tile the Y tile, the message
 // rows and phi are issued together before the workgroup barrier. A tile then costs one memory
 // latency instead of one per pair of monomials (the G reads of density_bwd_mfma_kernel). The
-// four waves' dphi / dmsg partials are summed by wave 0 through LDS. At K = 32 the kernel holds
+// four waves' dphi / dmsg partials are summed through LDS by all four. At K = 32 the kernel holds
 // ~230 registers (two waves per SIMD); capped at four waves per SIMD it spills 312 bytes and runs
 // 1.8x slower. Measured against density_bwd_mfma_kernel<2, 4>: 35.5 -> 27.3 us (864-atom FCC),
 // 37.6 -> 32.3 us (1,344 atoms), 153 -> 113 us (2,000 atoms of 70 neighbours), same bits.
@@ -557,7 +557,10 @@ __global__ __launch_bounds__(kDsWaves * kWave) void density_bwd_split_kernel(
             const int t = 4 * q + r;
             if (dY && t < ne && j < NXW) dY[(e0 + t) * ld_dY + x0 + j] = dyk[r];
         }
-        // partials of the four waves summed by wave 0
+        // partials of the four waves, summed by all four: thread tid takes values tid, tid + 256, ...
+        // of the block (dphi | dmsg), adding the waves' partials in wave order (one wave doing all
+        // the sums and stores left the other three waiting at the next tile's barrier: 864 atoms
+        // 27.6 -> 27.0 us, 64 molecules 32.1 -> 31.0 us)
         float* mine = sP[wv];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -566,27 +569,20 @@ __global__ __launch_bounds__(kDsWaves * kWave) void density_bwd_split_kernel(
             for (int c = 0; c < KB; ++c) mine[256 + (4 * q + r) * K + 16 * c + j] = dm[c][r];
         }
         __syncthreads();
-        if (wv == 0) {
+        constexpr int NV = 16 * (16 + K), NU = (NV + kDsWaves * kWave - 1) / (kDsWaves * kWave);
 #pragma unroll
-            for (int w = 1; w < kDsWaves; ++w) {
-                const float* o = sP[w];
+        for (int u = 0; u < NU; ++u) {
+            const int v = u * kDsWaves * kWave + tid;
+            if (v < NV) {
+                float sum = sP[0][v];
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    dph[r] += o[(4 * q + r) * 16 + j];
-#pragma unroll
-                    for (int c = 0; c < KB; ++c) dm[c][r] += o[256 + (4 * q + r) * K + 16 * c + j];
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int t = 4 * q + r;
-                if (t < ne) {
-                    const int64_t e = e0 + t;
-                    if (dphi) dphi[e * ld_dphi + j] = dph[r];
-                    if (dmsg) {
-#pragma unroll
-                        for (int c = 0; c < KB; ++c) dmsg[e * ld_dmsg + 16 * c + j] = dm[c][r];
-                    }
+                for (int w = 1; w < kDsWaves; ++w) sum += sP[w][v];
+                if (v < 256) {
+                    const int t = v >> 4, b = v & 15;
+                    if (dphi && t < ne) dphi[(e0 + t) * ld_dphi + b] = sum;
+                } else {
+                    const int t = (v - 256) / K, k = (v - 256) - t * K;
+                    if (dmsg && t < ne) dmsg[(e0 + t) * ld_dmsg + k] = sum;
                 }
             }
         }
