@@ -62,7 +62,9 @@ __device__ __forceinline__ v4f dsilu4_sh(v4f s, v4f h) { return s + h * (1.f - s
 struct RadialLds {
     int SI, S1, o_bin, o_pt, o_w1, o_b1, o_wp, o_bp, total;
     __host__ __device__ RadialLds(int H, int BB, int n_pair) {
-        SI = 16;
+        // w_in rows at a stride of 20 floats: the forward's read (row j, column 4kb+q) and the
+        // backward's (row 4q+r, column j) each touch 64 distinct banks; at 16 the backward's was 4-way
+        SI = 20;
         S1 = H + 4;
         o_bin = H * SI;
         o_pt = o_bin + H;
