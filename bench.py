@@ -54,6 +54,7 @@ KERNEL_FAMILY = {
     "density_mix_fwd": "density_mix_fwd", "density_mix_bwd": "density_mix_bwd",
     "cp_fwd": "cp_density_fwd", "cp_fwd_tab": "cp_density_fwd",
     "cp_bwd": "cp_density_bwd", "cp_bwd_tab": "cp_density_bwd",
+    "cp_radial_fwd": "cp_radial_fwd", "cp_radial_fwd_tab": "cp_radial_fwd",
     "cp_radial_bwd": "cp_radial_bwd", "cp_radial_bwd_tab": "cp_radial_bwd",
     "transport_fwd": "transport_fwd", "transport_bwd": "transport_bwd",
     "dir_fwd": "dir_feats_fwd", "dir_bwd": "dir_feats_bwd",
@@ -78,6 +79,7 @@ FAMILY_KERNELS = {
     "density_mix_fwd": ["density_mix_fwd_kernel"], "density_mix_bwd": ["density_mix_bwd_kernel"],
     "cp_density_fwd": ["cp_density_fwd_wave_kernel", "cp_density_fwd_kernel"],
     "cp_density_bwd": ["cp_density_bwd_mfma_kernel", "cp_density_bwd_kernel"],
+    "cp_radial_fwd": ["cp_radial_fwd_kernel"],
     "cp_radial_bwd": ["cp_radial_bwd_res_kernel", "cp_radial_bwd_lds_kernel"],
     "transport_fwd": ["transport_fwd_kernel"],
     "transport_bwd": ["transport_bwd_mfma_kernel", "transport_bwd_kernel", "transport_table_grad_kernel"],
@@ -145,6 +147,9 @@ def algorithmic_bytes(label, g, kw):
         return 4 * (E * (B + 3 + Kt // 2) + 18 * N * B * kw["K_dir"] + E * (B + 3 + Kt // 2))
     if label.startswith("cp_fwd"):          # the CP pooling drop-in: R (4C), msg (C), Y (20) per edge in
         return 4 * (E * (5 * C + 20) + 20 * N * C)
+    if label.startswith("cp_radial_fwd"):   # the fused radial head + pooling: h2 (H) in, R (4C) out once,
+        H = kw.get("radial_hidden", 64)   # msg (C), Y (20), env per edge in, A out (R is not read back)
+        return 4 * (E * (H + 4 * C + C + 21) + 20 * N * C)
     if label.startswith(("cp_bwd", "cp_radial_bwd")):   # + dR, dmsg, dY per edge out (fused or not)
         return 4 * (2 * E * (5 * C + 20) + 20 * N * C)
     if label == "node_fwd":
@@ -226,6 +231,8 @@ def interface_bytes(label, g, kw):
     if label.startswith("cp_fwd"):
         return 4 * ins
     H = kw.get("radial_hidden", 64)
+    if label.startswith("cp_radial_fwd"):     # h2 and W_cp in instead of R; R written once
+        return 4 * (E * (H + 1 + 20) + msg + 4 * C * H + E * 4 * C + 20 * N * C)
     if label.startswith("cp_radial_bwd"):
         return 4 * (ins + 4 * C * H + E * (H + C + 20 + 1))
     return 4 * (ins + E * (4 * C + C + 20 + 1))
@@ -263,6 +270,8 @@ def algorithmic_flops(label, g, kw):
         return 2 * E * 4 * kw["K_dir"] * K
     if label.startswith("cp_radial_bwd"):
         return 2 * E * (4 * C * H + 2 * 20 * C)
+    if label.startswith("cp_radial_fwd"):     # R = h2 W^T (E x H by H x 4C), then the 20-monomial pooling
+        return 2 * E * (4 * C * H + 20 * C)
     nb, B = kw.get("n_basis", 8), kw["B"]
     if label == "radial_fwd":           # per pass: nb -> H -> H -> B (phi; h2 is the second layer)
         return 2 * E * (nb * H + H * H + H * B)

@@ -12,4 +12,4 @@ extern "C" const char* face_hip_error_string(int code) {
     }
 }
 
-extern "C" int face_hip_abi_version(void) { return 23; }
+extern "C" int face_hip_abi_version(void) { return 24; }

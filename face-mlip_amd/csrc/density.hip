@@ -1577,6 +1577,241 @@ __global__ __launch_bounds__(NW * kWave) void cp_radial_bwd_res_kernel(
     }
 }
 
+// ------------------------------------------------------------------ CP radial forward, fused
+// R = h2 W^T + b (the CP columns of the last radial layer) and the CP pooling of R in one launch:
+// each 16-edge tile's R is computed on the matrix cores, written once (the backward reads it) and
+// pooled from the same registers, so R is never read back. Orientation: D = h2 . W^T with the
+// tile's edges as rows, so lane (j, q) holds R[edge 4q + r][column c0 + j] in register r — the B
+// operand layout of the pooling product A_l[x, c] += sum_e Y[e, x] * w_l[e, c] (w_l = env m R_l)
+// with edge 4q + r in K slot q of instruction r, whose A operand is Y^T (row x = lane j).
+// Workgroup = (channel part, group of kCrfWaves edge shares): the part's W rows (4 ranks x NCB
+// 16-channel blocks) sit in LDS for the whole launch; wave w walks the atom rows whose first
+// edge lies in its equal share of the edges, in tiles of 16 consecutive edges that may span
+// atom rows: the pooling of a tile runs once per atom segment it holds (Y masked to the
+// segment), and an atom's accumulators are stored and cleared when its last edge is pooled.
+// Rows with no edges get zero rows. Accumulation order: K slot then edge, so A differs from the
+// edge-serial cp_density_fwd kernels in rounding only; R is bitwise the edge_linear_fwd product
+// (same K split per instruction, same order). R goes out through non-temporal stores (read next
+// by the backward, milliseconds later).
+// Measured on the 24,000-atom liquid (C = 160, H = 64, 1.25 M edges, per-edge messages): 1.85 ms
+// against 1.07 + 0.96 ms for the radial head and the pooling kernel; with node-table messages
+// gathered through msg_row, 2.03 ms against 1.07 + 0.82: the model takes this launch for per-edge
+// messages only. The kernel runs at two waves per SIMD (LDS: 80 KB of W per workgroup; about 250
+// registers, of which 80 hold the pooling accumulators of 5 channel blocks) and is bound by
+// latency rather than by its 0.86 ms of MFMA issue: without the R stores it takes 1.38 ms, as
+// loads and stores share the in-order vmcnt counter and each channel block's loads wait for the
+// previous block's stores. Measured and not kept: message and bias values issued a block ahead
+// (1.93 ms), message rows issued a tile ahead (1.91 / 1.96 ms with gathered rows: spills),
+// ranks 0-2 sharing one accumulator tile through the K slots (2.24 ms: twelve dependent
+// products per segment).
+constexpr int kCrfWaves = 4;
+
+// LDS row stride of the W image: H + 4 floats keeps the 16 rows one read touches on distinct banks;
+// at H = 64 the rows are unpadded with float4 chunk c of row f stored at chunk (c + f) mod 16
+// (lin_off), which does the same in 80 KB for 5 channel blocks: two workgroups per CU.
+__host__ __device__ constexpr int crf_stride(int H) { return H == 64 ? 64 : H + 4; }
+
+template <int HB, int NCB>
+__global__ __launch_bounds__(kCrfWaves * kWave) __attribute__((amdgpu_waves_per_eu(2))) void cp_radial_fwd_kernel(
+    const float* __restrict__ h2, int ld_h2, const float* __restrict__ w, const float* __restrict__ b,
+    const float* __restrict__ env, const float* __restrict__ msg, int ld_msg, const int32_t* __restrict__ msg_row,
+    const float* __restrict__ Y, int ld_Y, const int32_t* __restrict__ row_ptr, int64_t N, int C, int nparts,
+    RankOut A, float* __restrict__ R, int ld_R) {
+    constexpr int H = 16 * HB, NCH = H / 4, ROWS = 4 * NCB * 16, S = crf_stride(H);
+    constexpr bool rot = S == H;
+    extern __shared__ float lds[];                    // W rows (l, cb, jj) of this part, lin_off image
+    const int tid = threadIdx.x, lane = tid & (kWave - 1);
+    const int j = lane & 15, q = lane >> 4;
+    // blocks b and b + 8 run on the same XCD: both parts of an edge share read its h2 / Y rows
+    // through one L2
+    const int bid = blockIdx.x;
+    const int part = (bid / 8) % nparts;
+    const int64_t grp = (int64_t)(bid / (8 * nparts)) * 8 + (bid & 7);
+    const int64_t ngrp = gridDim.x / nparts;
+    const int cb0 = part * NCB;
+    const int ncb = min(NCB, C / 16 - cb0);
+    const int64_t E = row_ptr[N];
+    // W and h2 may be NULL when there are no edges (then only zero rows are written); W is staged
+    // only when there are edges to multiply
+    if (E > 0 && (w == nullptr || h2 == nullptr)) return;
+    if (E > 0) {
+        stage4<8>(
+            ROWS * NCH,
+            [&](int f) {
+                const int rr = f / NCH, c4 = f - rr * NCH;
+                const int l = rr / (NCB * 16), cb = (rr >> 4) - l * NCB, jj = rr & 15;
+                const v4f z = {0.f, 0.f, 0.f, 0.f};
+                return cb < ncb ? ld4(w + (int64_t)(l * C + 16 * (cb0 + cb) + jj) * H + 4 * c4) : z;
+            },
+            [&](int f, v4f x) {
+                const int rr = f / NCH, c4 = f - rr * NCH;
+                st4(lds + lin_off(rr, c4, S, NCH, rot), x);
+            });
+    }
+    __syncthreads();
+    const int64_t W = ngrp * kCrfWaves;
+    const int64_t gw = grp * kCrfWaves + __builtin_amdgcn_readfirstlane(tid / kWave);
+    int64_t at = uniform64(wave_lower_bound(row_ptr, N, E * gw / W, lane));
+    const int64_t a_end = gw + 1 == W ? N : uniform64(wave_lower_bound(row_ptr, N, E * (gw + 1) / W, lane));
+    if (at >= a_end) return;
+    const int64_t e_beg = row_ptr[at], e_end = row_ptr[a_end];
+    // row_ptr[i] with i made wave-uniform: a scalar load (the segment walks below follow stores
+    // in divergent branches, after which a vector load and a vmcnt(0) wait, i.e. a wait for every
+    // store in flight, would otherwise be emitted)
+    auto rp = [&](int64_t i) __attribute__((always_inline)) { return (int64_t)row_ptr[uniform64(i)]; };
+    const v4f z4 = {0.f, 0.f, 0.f, 0.f};
+    const int sx = (int)A.sx;                         // the host checks 19 sx + C < 2^31
+    // rows x = 4q + r of each rank block of one atom for the part's channel block cb; (jl, ql)
+    // are the lane's (j, q) passed through an empty asm once per tile, so that the compiler
+    // rebuilds these addresses per tile instead of holding one 64-bit address per (block, row)
+    auto store_rank_rows = [&](int64_t atom, int cb, const v4f (&v)[4], int jl, int ql) __attribute__((always_inline)) {
+        const int c = 16 * (cb0 + cb) + jl;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const int nl = l == 0 ? 1 : (l == 1 ? 3 : (l == 2 ? 6 : 10));
+            float* base = A.p[l] + atom * A.sa;
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (4 * ql + r < nl) base[(4 * ql + r) * sx + c] = v[l][r];
+        }
+    };
+    const v4f zrow[4] = {z4, z4, z4, z4};
+    // leading rows with no edges (and the whole share when it has none)
+    while (at < a_end && rp(at + 1) == rp(at)) {
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb)
+            if (cb < ncb) store_rank_rows(at, cb, zrow, j, q);
+        ++at;
+    }
+    if (e_beg >= e_end) return;
+    v4f pacc[NCB][4];
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+        for (int l = 0; l < 4; ++l) pacc[cb][l] = z4;
+    // h2 rows of a tile (A operand, K index q of instruction r of chunk kb = feature 16 kb + 4q + r)
+    v4f hn[HB];
+    auto load_h2 = [&](int64_t t0) __attribute__((always_inline)) {
+        const int64_t e = min(t0 + j, e_end - 1);
+#pragma unroll
+        for (int kb = 0; kb < HB; ++kb) hn[kb] = ld4(h2 + e * ld_h2 + 16 * kb + 4 * q);
+    };
+    load_h2(e_beg);
+    for (int64_t t0 = e_beg; t0 < e_end; t0 += 16) {
+        const int64_t t1 = min(t0 + 16, e_end);
+        int jl = j, ql = q;
+        asm volatile("" : "+v"(jl), "+v"(ql));
+        // lane part of the W reads of chunk kb (row j, float4 chunk 4 kb + q); the rows of rank l
+        // and block cb add the constant (l NCB + cb) 16 S, an immediate offset of the read
+        int lw[HB];
+#pragma unroll
+        for (int kb = 0; kb < HB; ++kb) lw[kb] = lin_off(jl, 4 * kb + ql, S, NCH, rot);
+        v4f hv[HB];
+#pragma unroll
+        for (int kb = 0; kb < HB; ++kb) hv[kb] = hn[kb];
+        if (t0 + 16 < e_end) load_h2(t0 + 16);
+        // pooling-side values of edges t0 + 4q + r: Y rows of each rank (row x = lane j), envelope,
+        // message row
+        float yv[4][4], ev[4];
+        const float* mp[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t e = min(t0 + 4 * ql + r, t1 - 1);
+            ev[r] = env ? env[e] : 1.f;
+            mp[r] = msg + (msg_row ? (int64_t)msg_row[e] : e) * ld_msg + 16 * cb0 + jl;
+            const float* ye = Y + e * ld_Y + jl;
+#pragma unroll
+            for (int l = 0; l < 4; ++l) {
+                const int nl = l == 0 ? 1 : (l == 1 ? 3 : (l == 2 ? 6 : 10));
+                yv[l][r] = jl < nl ? ye[rank_start(l)] : 0.f;
+            }
+        }
+        float* const Rt = R ? R + t0 * ld_R : nullptr;
+        const float* const bt = b ? b + 16 * cb0 + jl : nullptr;
+        int64_t nxt = at;
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) {
+            if (cb < ncb) {
+                __builtin_amdgcn_sched_barrier(0);       // one channel block's operands live at a time
+                const int c = 16 * (cb0 + cb) + jl;
+                float mv[4], bias[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) mv[r] = mp[r][16 * cb];
+#pragma unroll
+                for (int l = 0; l < 4; ++l) bias[l] = bt ? bt[l * C + 16 * cb] : 0.f;
+                v4f acc[4] = {z4, z4, z4, z4};
+                // W operands of chunk kb + 1 read while chunk kb's products issue
+                v4f wv[2][4];
+                auto read_w = [&](int kb, v4f (&w4)[4]) __attribute__((always_inline)) {
+#pragma unroll
+                    for (int l = 0; l < 4; ++l)
+                        w4[l] = lds4_at(lds, lw[kb] + (l * NCB + cb) * 16 * S);
+                };
+                read_w(0, wv[0]);
+#pragma unroll
+                for (int kb = 0; kb < HB; ++kb) {
+                    if (kb + 1 < HB) read_w(kb + 1, wv[(kb + 1) & 1]);
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+#pragma unroll
+                        for (int l = 0; l < 4; ++l) acc[l] = mfma_16x16x4(hv[kb][r], wv[kb & 1][l][r], acc[l]);
+                }
+                // R rows out, then w_l = env m R_l in place
+#pragma unroll
+                for (int l = 0; l < 4; ++l) acc[l] += bias[l];
+                if (Rt) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        if (t0 + 4 * ql + r < t1) {
+#pragma unroll
+                            for (int l = 0; l < 4; ++l)
+                                __builtin_nontemporal_store(acc[l][r], Rt + (4 * ql + r) * ld_R + l * C + c);
+                        }
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float me = mv[r] * ev[r];
+#pragma unroll
+                    for (int l = 0; l < 4; ++l) acc[l][r] *= me;
+                }
+                // the tile's atom segments (row ends read through a wave-uniform index: scalar
+                // loads, one per atom; atom a starts where atom a - 1 ends)
+                int64_t a = at, lo = t0;
+                int64_t a_hi = rp(a + 1);
+                while (true) {
+                    const int64_t hi = min(a_hi, t1);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int64_t e = t0 + 4 * ql + r;
+                        const bool in = e >= lo && e < hi;
+#pragma unroll
+                        for (int l = 0; l < 4; ++l)
+                            pacc[cb][l] = mfma_16x16x4(in ? yv[l][r] : 0.f, acc[l][r], pacc[cb][l]);
+                    }
+                    if (a_hi > t1) break;             // the atom goes on into the next tile
+                    store_rank_rows(a, cb, pacc[cb], jl, ql);
+#pragma unroll
+                    for (int l = 0; l < 4; ++l) pacc[cb][l] = z4;
+                    const int64_t start = a_hi;       // where the next atom's edges begin
+                    ++a;
+                    while (a < a_end) {
+                        a_hi = rp(a + 1);
+                        if (a_hi != start) break;
+                        store_rank_rows(a, cb, zrow, jl, ql);
+                        ++a;
+                    }
+                    if (a >= a_end || start >= t1) break;
+                    lo = start;
+                }
+                nxt = a;
+            }
+        }
+        at = nxt;
+    }
+}
+
 // ------------------------------------------------------------------ launch helpers
 
 template <int NX>
@@ -1892,6 +2127,65 @@ extern "C" int face_cp_density_bwd(const float* R, int32_t ld_R, const float* en
     if ((int64_t)lds > 65536) return FACE_ERR_UNSUPPORTED;
     hipLaunchKernelGGL(cp_density_bwd_kernel, dim3((unsigned)N), dim3(nthr), lds, (hipStream_t)stream, R, ld_R, env,
                        msg, ld_msg, msg_row, Y, ld_Y, row_ptr, M, C, gA, dR, ld_dR, dmsg, ld_dmsg, dY, ld_dY, denv);
+    FACE_LAUNCH_CHECK();
+    return 0;
+}
+
+extern "C" int face_cp_radial_fwd(const float* h2, int32_t ld_h2, int32_t H, const float* w, const float* b,
+                                  const float* env, const float* msg, int32_t ld_msg, const int32_t* msg_row,
+                                  const float* Y, int32_t ld_Y, const int32_t* row_ptr, int64_t N, int64_t E,
+                                  int32_t C, float* const* A_ranks, int64_t atom_stride, int64_t x_stride, float* R,
+                                  int32_t ld_R, void* stream) {
+    if (N < 0 || E < 0 || C <= 0 || H < 16 || H > 64 || H % 16 || ld_h2 < H || ld_msg < C || ld_Y < 20 ||
+        (R && ld_R < 4 * C))
+        return FACE_ERR_ARG;
+    if (N == 0) return 0;
+    RankOut A;
+    if ((E > 0 && (!h2 || !w)) || !msg || !Y || !row_ptr || !rank_out(A_ranks, atom_stride, x_stride, 20, A))
+        return FACE_ERR_ARG;
+    if (C % 16 || ld_h2 % 4 || !aligned16(h2) || !aligned16(w) || A.sx * 19 + C >= ((int64_t)1 << 31) ||
+        (int64_t)ld_R * 16 >= ((int64_t)1 << 31))
+        return FACE_ERR_UNSUPPORTED;
+    const int nblk = C / 16;
+    const int nparts = (nblk + 4) / 5;
+    const int ncb = (nblk + nparts - 1) / nparts;   // 16-channel blocks per part, <= 5
+    const int rows = 4 * (ncb < 2 ? 2 : ncb) * 16;   // the kernel's NCB rows (NCB >= 2)
+    const int64_t max_lds = device_max_lds();
+    const size_t lds = (size_t)rows * crf_stride(H) * sizeof(float);
+    if ((int64_t)lds > max_lds) return FACE_ERR_UNSUPPORTED;
+    // edge shares: one group per CU at most, and at least 8 tiles per wave; a multiple of 8
+    // groups, so that blocks b and b + 8 (one XCD) hold the parts of one group
+    int64_t ngrp = (E + 16 * 8 * kCrfWaves - 1) / (16 * 8 * kCrfWaves);
+    const int64_t n_cu = device_cu_count();
+    if (ngrp > n_cu) ngrp = n_cu;
+    ngrp = ((ngrp < 1 ? 1 : ngrp) + 7) / 8 * 8;
+    const dim3 grid((unsigned)(ngrp * nparts)), block(kCrfWaves * kWave);
+    const hipStream_t st = (hipStream_t)stream;
+#define FACE_CRF(HB_, NCB_)                                                                                       \
+    do {                                                                                                          \
+        auto kern = cp_radial_fwd_kernel<HB_, NCB_>;                                                              \
+        if (lds > 65536 &&                                                                                        \
+            hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) \
+            return FACE_ERR_UNSUPPORTED;                                                                          \
+        hipLaunchKernelGGL(kern, grid, block, lds, st, h2, ld_h2, w, b, env, msg, ld_msg, msg_row, Y, ld_Y,         \
+                           row_ptr, N, C, nparts, A, R, ld_R);                                                    \
+    } while (0)
+#define FACE_CRF_H(NCB_)                    \
+    switch (H / 16) {                       \
+        case 1: FACE_CRF(1, NCB_); break;   \
+        case 2: FACE_CRF(2, NCB_); break;   \
+        case 3: FACE_CRF(3, NCB_); break;   \
+        default: FACE_CRF(4, NCB_); break;  \
+    }
+    switch (ncb) {
+        case 1:
+        case 2: FACE_CRF_H(2); break;
+        case 3: FACE_CRF_H(3); break;
+        case 4: FACE_CRF_H(4); break;
+        default: FACE_CRF_H(5); break;
+    }
+#undef FACE_CRF_H
+#undef FACE_CRF
     FACE_LAUNCH_CHECK();
     return 0;
 }

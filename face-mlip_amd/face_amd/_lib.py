@@ -61,6 +61,8 @@ _SIGS = {
     "face_force_scatter": (ctypes.c_int, [P, P, P, I64, F32, P, P]),
     "face_edge_geom_bwd_seg": (ctypes.c_int, [P, P, P, P, P, I64, P, I32, F32, F32, P, P, P, P, P, P, P]),
     "face_force_scatter_rows": (ctypes.c_int, [P, P, P, I64, I32, F32, P, P]),
+    "face_cp_radial_fwd": (ctypes.c_int, [P, I32, I32, P, P, P, P, I32, P, P, I32, P, I64, I64, I32, P, I64, I64, P,
+                                           I32, P]),
     "face_cp_radial_bwd": (ctypes.c_int, [P, I32, P, P, I32, P, P, I32, P, I64, I32, I32, P, I64, I64, P, I32, P, I32,
                                           P, I32, P, I32, P, P]),
     "face_radial_fwd": (ctypes.c_int, [P, I32, I32, P, P, I64, P, P, P, I32, I32, P, P, P, P, I32, P, I32, P, I32, P]),
@@ -83,7 +85,7 @@ _SIGS = {
     "face_layer_norm_bwd": (ctypes.c_int, [P, P, I64, I32, P, P, P, P, P]),
 }
 
-ABI_VERSION = 23
+ABI_VERSION = 24
 
 
 class LinProblem(ctypes.Structure):

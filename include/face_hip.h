@@ -133,6 +133,21 @@ int face_cp_density_bwd(const float* R, int32_t ld_R, const float* env, const fl
                         int64_t x_stride, float* dR, int32_t ld_dR, float* dmsg, int32_t ld_dmsg, float* dY,
                         int32_t ld_dY, float* denv, void* stream);
 
+/* CP pooling forward fused with the CP columns of the last radial layer (face/model.py:469-472,
+ * 496-502): R = h2 W^T + b (W (4C, H) row-major, b (4C) or NULL) computed on the matrix cores, written
+ * to R (E, ld_R >= 4C; NULL = not written) for the backward, and pooled into A as
+ * face_cp_density_fwd from the same registers (R is not read back). E = row_ptr[N] (the number of
+ * edges; sizes the launch); row_ptr is required (CSR rows). Served when C is a multiple of 16,
+ * H in {16, 32, 48, 64}, h2 and W are 16-byte aligned with ld_h2 % 4 == 0 and the part of W one
+ * workgroup holds fits LDS; FACE_ERR_UNSUPPORTED otherwise (then R = h2 W^T + b by
+ * face_edge_linear_fwd and face_cp_density_fwd give the same result). A equals
+ * face_cp_density_fwd's within fp32 rounding (another summation order); R is bitwise
+ * face_edge_linear_fwd's. */
+int face_cp_radial_fwd(const float* h2, int32_t ld_h2, int32_t H, const float* w, const float* b, const float* env,
+                       const float* msg, int32_t ld_msg, const int32_t* msg_row, const float* Y, int32_t ld_Y,
+                       const int32_t* row_ptr, int64_t N, int64_t E, int32_t C, float* const* A_ranks,
+                       int64_t atom_stride, int64_t x_stride, float* R, int32_t ld_R, void* stream);
+
 /* CP pooling backward fused with the CP columns of the last radial layer (face/model.py:469-472):
  * with R = h2 W^T + b (W (4C, H)), returns dh2 (E, ld_dh2) = dR W instead of dR, computed on the
  * matrix cores inside the pooling kernel. w_t = W^T (H, 4C) row-major, 16-byte aligned;

@@ -203,6 +203,85 @@ def test_cp_radial_density_fused_backward(gathered, C, H, N, pairs):
     assert max(errs) < TOL, errs
 
 
+def _ragged_counts(N, seed):
+    """Row lengths with runs of empty rows at the start, inside and at the end, a run of one-edge
+    rows (16-edge tiles holding up to 16 atom segments) and rows longer than a tile."""
+    rng = np.random.default_rng(seed)
+    body = rng.integers(0, 60, N - 3 - 40 - 6 - 5)
+    body[rng.integers(0, body.size, body.size // 8)] = 0
+    return [0, 0, 0] + [1] * 40 + [0] * 6 + body.tolist() + [70, 0, 0, 0, 0]
+
+
+@pytest.mark.parametrize("C,H,N,gathered,with_b,with_env,with_R", [
+    (160, 64, 700, False, True, True, True), (160, 64, 700, True, True, True, True),
+    (96, 32, 700, True, False, True, True), (16, 16, 300, False, True, False, True),
+    (320, 64, 300, False, True, True, False), (48, 48, 300, True, True, True, True),
+    (192, 64, 3000, False, True, True, True), (160, 64, 60, True, True, True, True)])
+def test_cp_radial_fused_forward_matches_two_launch_route(C, H, N, gathered, with_b, with_env, with_R):
+    """The fused CP radial forward (R = h2 W^T + b computed, written and pooled in one launch)
+    through the C ABI against the two-launch route on the same inputs (face_edge_linear_fwd then
+    face_cp_density_fwd): R bitwise equal, A within fp32 rounding of the edge-serial pooling and
+    within TOL of the fp64 oracle; every output row written (outputs start as NaN), empty rows
+    exactly zero. Channel widths give 1 to 5 16-channel blocks per part and 1 to 4 parts."""
+    from face_amd import _lib, ops
+    say("cp radial fused fwd", C, H, N, gathered, with_b, with_env, with_R)
+    counts = _ragged_counts(N, C + H)
+    E = int(sum(counts))
+    rng = np.random.default_rng(N + C)
+    row_ptr = torch.as_tensor(np.concatenate([[0], np.cumsum(counts)]).astype(np.int32), device=DEV)
+    col = torch.as_tensor(rng.integers(0, N, E).astype(np.int32), device=DEV)
+    torch.manual_seed(C * H + N)
+    h2 = torch.randn(E, H, device=DEV)
+    W = torch.randn(4 * C, H, device=DEV) / H ** 0.5
+    b = torch.randn(4 * C, device=DEV) * 0.1 if with_b else None
+    env = torch.rand(E, device=DEV) if with_env else None
+    msg = torch.randn(N if gathered else E, C, device=DEV)
+    Y = torch.randn(E, 20, device=DEV)
+    row = col if gathered else None
+    st = _lib.stream_of(h2)
+    outs = [torch.full((k, N, C), float("nan"), device=DEV) for k in ops.RANK_K]
+    R = torch.full((E, 4 * C), float("nan"), device=DEV) if with_R else None
+    P = _lib.ptr
+    _lib.call("face_cp_radial_fwd", P(h2), H, H, P(W), P(b), P(env), P(msg), C, P(row), P(Y), 20, P(row_ptr), N, E,
+              C, *_lib.ranks_of_blocks(outs), P(R), 4 * C, st)
+    R2 = ops.edge_linear(h2, W, b)
+    outs2 = [torch.empty(k, N, C, device=DEV) for k in ops.RANK_K]
+    _lib.call("face_cp_density_fwd", P(R2), 4 * C, P(env), P(msg), C, P(row), P(Y), 20, P(row_ptr), N, 0, C,
+              *_lib.ranks_of_blocks(outs2), st)
+    torch.cuda.synchronize()
+    if with_R:
+        assert torch.equal(R, R2)
+    A = torch.cat(outs, 0).permute(1, 0, 2)                               # (N, 20, C)
+    A2 = torch.cat(outs2, 0).permute(1, 0, 2)
+    assert torch.isfinite(A).all()
+    empty = torch.as_tensor(counts, device=DEV) == 0
+    assert (A[empty] == 0).all()
+    scale = A2.abs().max().item()
+    assert (A - A2).abs().max().item() <= 2e-6 * scale
+    M = max(counts)
+    pd = lambda t: _pad(t, counts, M)
+    Rc = h2.double().cpu() @ W.double().cpu().T + (b.double().cpu() if with_b else 0)
+    ec = env.double().cpu() if with_env else torch.ones(E, dtype=torch.float64)
+    ms = msg.double().cpu()
+    A3 = oops.cp_density(pd((Rc * ec[:, None]).view(E, 4, C)), pd(ms[col.long().cpu()] if gathered else ms),
+                         pd(Y.double().cpu()))
+    assert rel(A, A3) < TOL
+
+
+def test_cp_radial_fused_forward_without_edges():
+    """No edges at all: every row of A is zero, and h2 / W may be NULL."""
+    from face_amd import _lib, ops
+    N, C = 37, 32
+    row_ptr = torch.zeros(N + 1, dtype=torch.int32, device=DEV)
+    msg = torch.randn(N, C, device=DEV)
+    Y = torch.randn(1, 20, device=DEV)
+    outs = [torch.full((k, N, C), float("nan"), device=DEV) for k in ops.RANK_K]
+    _lib.call("face_cp_radial_fwd", None, 64, 64, None, None, None, _lib.ptr(msg), C, None, _lib.ptr(Y), 20,
+              _lib.ptr(row_ptr), N, 0, C, *_lib.ranks_of_blocks(outs), None, 4 * C, _lib.stream_of(msg))
+    torch.cuda.synchronize()
+    assert all((o == 0).all() for o in outs)
+
+
 # ----------------------------------------------------------------------------- gated outputs
 @pytest.mark.parametrize("N,C", [(1000, 160), (37, 96), (1, 4)])
 def test_eq_gate_matches_torch(N, C):
