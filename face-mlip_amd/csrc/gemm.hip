@@ -109,8 +109,8 @@ struct GemmSide {
 // Stage the side tables of (problem P, slice n0 .. n0 + ns) into LDS (callers synchronise);
 // columns past ns are zero. The xs rows are restaged only with a new problem.
 __device__ __forceinline__ void gemm_stage_side(const GemmArgs& A, const GemmProb& P, const GemmSide& S, int nsb, int n0,
-                                                int ns, bool new_prob) {
-    const int tid = threadIdx.x, nthr = blockDim.x;
+                                                int ns, bool new_prob, int tid) {
+    const int nthr = blockDim.x;
     if (A.ys) {
         for (int v = tid; v < A.n_groups * nsb; v += nthr) {
             const int g = v / nsb, c = v - g * nsb;
@@ -139,9 +139,9 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
     const v4f z4 = {0.f, 0.f, 0.f, 0.f};
     auto item_at = [&](int64_t target) -> int64_t {     // first item starting at or past target
         int p = 0;
-#pragma unroll
-        for (int k = 1; k < kGemmMaxProbs; ++k)
-            if (k < A.n_probs && target >= A.p[k].cost0) p = k;
+#pragma unroll 1
+        for (int k = 1; k < A.n_probs; ++k)
+            if (target >= A.p[k].cost0) p = k;
         const int64_t i = A.p[p].first_block + (target - A.p[p].cost0 + A.p[p].cost - 1) / A.p[p].cost;
         return min(i, A.items);
     };
@@ -155,9 +155,9 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
     // tile of 32 NW rows.
     auto locate = [&](int64_t it, int& pi, int& slice, int64_t& tile) {
         pi = 0;
-#pragma unroll
-        for (int k = 1; k < kGemmMaxProbs; ++k)
-            if (k < A.n_probs && it >= A.p[k].first_block) pi = k;
+#pragma unroll 1
+        for (int k = 1; k < A.n_probs; ++k)
+            if (it >= A.p[k].first_block) pi = k;
         const int64_t local = it - A.p[pi].first_block;
         slice = PERSIST ? (int)(local / A.p[pi].tiles) : (int)(local % A.p[pi].slices);
         tile = PERSIST ? local - (int64_t)slice * A.p[pi].tiles : local / A.p[pi].slices;
@@ -173,6 +173,10 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
             // stage W[n0 : n0 + ns, :] as rows of K (+ 4 pad); rows ns .. 16 NB - 1 are zero, so
             // the MFMA loop below runs all NB blocks without branches
             if (PERSIST) __syncthreads();                                // every wave is done with the old slice
+            // the thread index through an empty asm: the staging addresses are rebuilt per staging
+            // instead of being held (spilled) across the persistent loop
+            int tid = threadIdx.x;
+            asm volatile("" : "+v"(tid));
             // four loads per thread issued before their LDS stores (a loop that stores each
             // float4 before loading the next waits a memory latency per round)
             const float* __restrict__ wsrc = P.w;
@@ -215,7 +219,7 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
                     }
                 }
             }
-            gemm_stage_side(A, P, side, 16 * NB, n0, ns, pi != cur_pi);
+            gemm_stage_side(A, P, side, 16 * NB, n0, ns, pi != cur_pi, tid);
             __syncthreads();
             cur_pi = pi, cur_slice = slice;
         }
@@ -228,18 +232,19 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
         const int ns = min(A.NS, P.n - n0);
         const GemmSide side(sW + A.side_off, A, 16 * NB);
         if (m0 >= P.m) return;
+        // rows as 32-bit element offsets from the problem's base pointers (the host checks that
+        // every operand's rows fit), so that each row costs one register per operand
         bool ok[kGemmBB];
-        int64_t rcs[kGemmBB];
-        const float* xr[kGemmBB];
-        float* yr[kGemmBB];
+        int rcs[kGemmBB];
+        int xo[kGemmBB], yo[kGemmBB];
         int xso[kGemmBB], yso[kGemmBB];                                  // LDS offsets of the row's scale rows
 #pragma unroll
         for (int bb = 0; bb < kGemmBB; ++bb) {
             const int64_t row = m0 + 16 * bb + j;
             ok[bb] = row < P.m;
-            rcs[bb] = ok[bb] ? row : 0;
-            xr[bb] = P.x + rcs[bb] * P.ld_x + 4 * q;
-            yr[bb] = P.y + rcs[bb] * P.ld_y + 4 * q;
+            rcs[bb] = ok[bb] ? (int)row : 0;
+            xo[bb] = rcs[bb] * (int)P.ld_x + 4 * q;
+            yo[bb] = rcs[bb] * (int)P.ld_y + 4 * q;
             const int g = A.group ? A.group[rcs[bb] % A.period] : 0;
             xso[bb] = g * A.kmax + 4 * q;
             yso[bb] = g * (16 * NB) + 4 * q;
@@ -248,15 +253,15 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
         // the XM = 2 kernels; k1 is a multiple of 16)
         auto x_at = [&](int bb, int kc) -> const float* {
             const int c0 = 16 * kc;
-            if (!XO) return xr[bb] + c0;
-            return c0 < P.k1 ? xr[bb] + c0 : P.x2 + rcs[bb] * P.ld_x2 + (c0 - P.k1) + 4 * q;
+            if (!XO) return P.x + (xo[bb] + c0);
+            return c0 < P.k1 ? P.x + (xo[bb] + c0) : P.x2 + (rcs[bb] * (int)P.ld_x2 + (c0 - P.k1) + 4 * q);
         };
         auto load_x = [&](int kc, v4f (&xv)[kGemmBB], v4f (&zv)[kGemmBB]) {
 #pragma unroll
             for (int bb = 0; bb < kGemmBB; ++bb) {
                 xv[bb] = ok[bb] ? ld4(x_at(bb, kc)) : z4;
                 if (XO && P.x_op == 2 && 16 * kc < P.k1)
-                    zv[bb] = ok[bb] ? ld4(P.xz + rcs[bb] * P.ld_xz + 16 * kc + 4 * q) : z4;
+                    zv[bb] = ok[bb] ? ld4(P.xz + (rcs[bb] * (int)P.ld_xz + 16 * kc + 4 * q)) : z4;
             }
         };
         // accumulators start at beta y (XM = 2: beta y0 over its first n_y0 columns), the loads
@@ -269,10 +274,10 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
                 acc[nb][bb] = z4;
                 if (P.beta != 0.f && ok[bb] && 16 * nb < ns) {
                     if (!XO) {
-                        acc[nb][bb] = ld4(yr[bb] + n0 + 16 * nb);
+                        acc[nb][bb] = ld4(P.y + (yo[bb] + n0 + 16 * nb));
                     } else if (n0 + 16 * nb + 4 * q < P.n_y0) {
-                        acc[nb][bb] = P.y0 ? ld4(P.y0 + rcs[bb] * P.ld_y0 + n0 + 16 * nb + 4 * q)
-                                           : ld4(yr[bb] + n0 + 16 * nb);
+                        acc[nb][bb] = P.y0 ? ld4(P.y0 + (rcs[bb] * (int)P.ld_y0 + n0 + 16 * nb + 4 * q))
+                                           : ld4(P.y + (yo[bb] + n0 + 16 * nb));
                     }
                     if (P.beta != 1.f) acc[nb][bb] *= P.beta;
                 }
@@ -323,7 +328,7 @@ __global__ __launch_bounds__(NW * kWave) void rows_gemm_kernel(GemmArgs A) {
                 for (int bb = 0; bb < kGemmBB; ++bb) {
                     v4f v = acc[nb][bb] + bias;
                     if (A.ys) v *= *reinterpret_cast<const v4f*>(side.ys + yso[bb] + 16 * nb);
-                    if (ok[bb]) st4(yr[bb] + n0 + 16 * nb, v);
+                    if (ok[bb]) st4(P.y + (yo[bb] + n0 + 16 * nb), v);
                 }
             }
         }
@@ -461,7 +466,7 @@ __global__ __launch_bounds__(kKcWaves * kWave) void rows_gemm_kc_kernel(GemmArgs
         load_w(0, bw);
         store_w(0, bw);
     }
-    gemm_stage_side(A, P, side, NSB, n0, ns, true);
+    gemm_stage_side(A, P, side, NSB, n0, ns, true, tid);
     // accumulators start at beta y (loads in flight with the first x rows), else zero
     v4f acc[NB][kGemmBB];
 #pragma unroll
@@ -567,6 +572,11 @@ static int fill_prob(const face_lin_problem& s, int w_kn, bool scaled, const flo
                    s.s_off + (y_scale ? s.n : 0) > ld_scale))
         return FACE_ERR_ARG;
     if (s.m > 0 && (!s.x || !s.w || !s.y)) return FACE_ERR_ARG;
+    // rows_gemm_kernel addresses rows by 32-bit element offsets from each operand's base
+    const int64_t lim = (int64_t)1 << 31;
+    if (s.m * s.ld_x >= lim || s.m * s.ld_y >= lim || (s.x2 && s.m * s.ld_x2 >= lim) ||
+        (s.x_op == 2 && s.m * s.ld_xz >= lim) || (s.y0 && s.m * s.ld_y0 >= lim))
+        return FACE_ERR_UNSUPPORTED;
     if (s.ld_x % 4 || s.ld_y % 4 || !al16(s.x) || !al16(s.y) || (!w_kn && (!al16(s.w) || s.ld_w % 4)) ||
         (s.x2 && (!al16(s.x2) || s.ld_x2 % 4)) || (s.x_op == 2 && (!al16(s.xz) || s.ld_xz % 4)) ||
         (s.bias && !al16(s.bias)) || (s.y0 && (!al16(s.y0) || s.ld_y0 % 4)))

@@ -408,7 +408,8 @@ typedef struct {
  * node features: mix / tmix / proj (face/model.py:498-533, :537-544) with the elem_scale factor,
  * the readout MLP (face/model.py:331-339: [inv | h] W0^T + b0, then SiLU-on-load layers, the
  * residual as y0) and their input gradients (w_kn = 1). x, x2, xz, y, y0, bias and the scale
- * tables 16-byte aligned, every ld and s_off a multiple of 4. */
+ * tables 16-byte aligned, every ld and s_off a multiple of 4; FACE_ERR_UNSUPPORTED when an operand
+ * spans 2^31 elements or more (m * ld of x, x2, xz, y or y0: rows are addressed by 32-bit offsets). */
 int face_rows_linear(const face_lin_problem* probs, int32_t n_probs, int32_t w_kn, const float* x_scale,
                      const float* y_scale, int32_t ld_scale, int32_t n_groups, const int32_t* group, int64_t period,
                      void* stream);
