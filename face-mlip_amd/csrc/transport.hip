@@ -123,6 +123,72 @@ __global__ __launch_bounds__(1024) void transport_fwd_kernel(const float* __rest
     }
 }
 
+// Matrix-core forward for B == 16, Kd == 16 (the flagship widths): per atom the sums are the
+// product D_o[b][kd] = sum_e phi[e][b] F_o[e][kd] with the row's edges as K. One wave per atom
+// row; per step of 4 edges (edge e0 + 4s + q in K slot q), lane (j, q) forms the 18 features of
+// its edge at channel kd = j from u and the neighbour's table row, and each feature o is one
+// v_mfma_f32_16x16x4f32 with A = phi^T (lane (j, q): phi[e][b = j]) and B = F_o (lane (j, q):
+// F_o[e][kd = j]); tile o holds b = 4q + r of channel j in register r of lane (j, q). Edges past
+// the row carry phi = 0. The next step's operands are loaded while the current one multiplies,
+// and the neighbour indices one step earlier still, so no gather waits on its index.
+constexpr int kTfWaves = 4;
+
+__global__ __launch_bounds__(kTfWaves * kWave) void transport_fwd_mfma_kernel(
+    const float* __restrict__ phi, int ld_phi, Tables T, const float* __restrict__ Y, int ld_Y,
+    const int32_t* __restrict__ col, const int32_t* __restrict__ row_ptr, int64_t N, float scale,
+    float* __restrict__ D1, float* __restrict__ D2) {
+    constexpr int Kd = 16, B = 16, W = 2 * B * Kd;
+    const int lane = threadIdx.x & (kWave - 1);
+    const int j = lane & 15, q = lane >> 4;
+    const int64_t i = (int64_t)blockIdx.x * kTfWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    if (i >= N) return;
+    const int64_t e0 = row_ptr[i], e1 = row_ptr[i + 1];
+    const v4f z4 = {0.f, 0.f, 0.f, 0.f};
+    v4f acc[18];
+#pragma unroll
+    for (int o = 0; o < 18; ++o) acc[o] = z4;
+    if (e1 > e0) {
+        const int64_t ns = (e1 - e0 + 3) / 4;
+        auto edge = [&](int64_t s) { return min(e0 + 4 * s + q, e1 - 1); };
+        struct Op {
+            float p, u[3], V[3], M[6];
+        };
+        auto load = [&](int64_t s, int32_t c, Op& o) __attribute__((always_inline)) {
+            const int64_t e = e0 + 4 * s + q;
+            const int64_t ec = min(e, e1 - 1);
+            o.p = e < e1 ? phi[ec * ld_phi + j] : 0.f;
+            const float* y = Y + ec * ld_Y;
+            o.u[0] = y[1];
+            o.u[1] = y[2];
+            o.u[2] = y[3];
+            load_tables(T, c, j, o.V, o.M);
+        };
+        Op cur, nxt;
+        int32_t cn = col[edge(ns > 1 ? 1 : 0)];          // neighbour of step 1
+        load(0, col[edge(0)], cur);
+        for (int64_t s = 0; s < ns; ++s) {
+            const int32_t cnn = col[edge(s + 2 < ns ? s + 2 : s)];
+            if (s + 1 < ns) load(s + 1, cn, nxt);
+            float F[18];
+            transport_features(cur.u, cur.V, cur.M, F);
+#pragma unroll
+            for (int o = 0; o < 18; ++o) acc[o] = mfma_16x16x4(cur.p, F[o], acc[o]);
+            cur = nxt;
+            cn = cnn;
+        }
+    }
+    // feature o -> (table, component, half): D1 = [V | M u], D2 = [M | sym(u V)]
+#pragma unroll
+    for (int o = 0; o < 18; ++o) {
+        float* const base = o < 6 ? D1 : D2;
+        const int comp = o < 6 ? o % 3 : (o - 6) % 6;
+        const int half = o < 6 ? o / 3 : (o - 6) / 6;
+        float* const dst = base + (comp * N + i) * W + half * Kd + j;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dst[(4 * q + r) * 2 * Kd] = scale * acc[o][r];
+    }
+}
+
 // Workgroup = atom i; gD (B x Kd x 18, scaled) staged in LDS. Lane = (edge slot, kd), KP lanes
 // per edge (Kd rounded up to a power of two). Per edge and channel kd:
 //   dphi[b] = sum_{kd,o} gD[b,kd,o] F[kd,o]   (summed over the KP lanes)
@@ -427,6 +493,13 @@ extern "C" int face_transport_fwd(const float* phi, int32_t ld_phi, int32_t B, c
     const size_t lds = ((size_t)kTT * Kd * kFP + kTT * B) * sizeof(float);
     if (lds > 65536) return FACE_ERR_UNSUPPORTED;
     Tables T{V, M, v_sn, v_sq, m_sn, m_sq};
+    if (B == 16 && Kd == 16) {
+        hipLaunchKernelGGL(transport_fwd_mfma_kernel, dim3((unsigned)((N + kTfWaves - 1) / kTfWaves)),
+                           dim3(kTfWaves * kWave), 0, (hipStream_t)stream, phi, ld_phi, T, Y, ld_Y, col, row_ptr, N,
+                           scale, D1, D2);
+        FACE_LAUNCH_CHECK();
+        return 0;
+    }
     hipLaunchKernelGGL(transport_fwd_kernel, dim3((unsigned)N), dim3(nthr), lds, (hipStream_t)stream, phi, ld_phi, B,
                        T, Kd, Y, ld_Y, col, row_ptr, N, scale, D1, D2);
     FACE_LAUNCH_CHECK();
