@@ -496,6 +496,56 @@ __global__ __launch_bounds__(256) void dir_feats_fwd_kernel(DirTables T, int Kd,
     de[3 * Kd] = a3;
 }
 
+// Row form of the dL/dY kernel below for Kd == 16: one wave per receiver atom, lane (j, q) on
+// channel kd = j of the row's edges e0 + 4s + q; the receiver's 9 table rows at channel j are
+// loaded once per atom, so an edge gathers only its neighbour's. (The same row form of the
+// forward measured slower than its per-edge kernel: 186 against 170 us at 24,000 atoms.)
+constexpr int kDirWaves = 4;
+
+// dL/dY of the directional features, row form (Kd == 16): the 9 products per (edge, channel)
+// summed over the 16 channel lanes of a group with DPP row sums; lane j of the group then writes
+// monomial j of the edge's gY row (and lanes j < 4 monomials 16 .. 19, all zero).
+__global__ __launch_bounds__(kDirWaves * kWave) void dir_feats_bwd_row_kernel(DirTables T, const int32_t* __restrict__ col,
+                                                                            const int32_t* __restrict__ row_ptr,
+                                                                            const float* __restrict__ gd, int64_t N,
+                                                                            float* __restrict__ gY) {
+    constexpr int Kd = 16;
+    const int lane = threadIdx.x & (kWave - 1), j = lane & 15, q = lane >> 4;
+    const int64_t i = (int64_t)blockIdx.x * kDirWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    if (i >= N) return;
+    const int64_t e0 = row_ptr[i], e1 = row_ptr[i + 1];
+    if (e1 <= e0) return;
+    float Ti[9];
+#pragma unroll
+    for (int k = 0; k < 9; ++k) Ti[k] = T.at(k, i, j);
+    const int64_t ns = (e1 - e0 + 3) / 4;
+    for (int64_t st = 0; st < ns; ++st) {                 // uniform: every lane takes part in the row sums
+        const int64_t e = e0 + 4 * st + q;
+        const int64_t ec = e < e1 ? e : e1 - 1;
+        const int64_t c = col[ec];
+        float Tj[9];
+#pragma unroll
+        for (int k = 0; k < 9; ++k) Tj[k] = T.at(k, c, j);
+        const float* g = gd + ec * 4 * Kd + j;
+        const float g0 = g[0], g1 = g[Kd], g2 = g[2 * Kd], g3 = g[3 * Kd];
+        float acc[9];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) acc[k] = row16_sum(g0 * Tj[k] + g2 * Ti[k]);
+#pragma unroll
+        for (int k = 3; k < 9; ++k) acc[k] = row16_sum(g1 * Tj[k] + g3 * Ti[k]);
+        if (e < e1) {
+            // monomial x = j: 0 for x = 0 and x >= 10, acc[x - 1] for x = 1..6, 2 acc[x - 1] for 7..9
+            float v = 0.f;
+#pragma unroll
+            for (int k = 0; k < 9; ++k)
+                if (j == k + 1) v = k < 6 ? acc[k] : 2.f * acc[k];
+            float* o = gY + e * 20;
+            o[j] = v;
+            if (j < 4) o[16 + j] = 0.f;
+        }
+    }
+}
+
 // dL/dY for the directional features (monomials 1..9; 0 and 10..19 are written as 0).
 // Thread = (edge, channel slot); the KP lanes of an edge (KP = Kd rounded up to a power of two,
 // <= 64) sum their partial products with butterfly shuffles.
@@ -844,7 +894,10 @@ extern "C" int face_dir_feats_bwd(const float* V, int64_t v_sn, int64_t v_sq, co
     if (!V || !M || !row_ptr || !recv || !col || !rev || !Y || !gd || (!gV != !gM)) return FACE_ERR_ARG;
     DirTables T{V, M, v_sn, v_sq, m_sn, m_sq};
     hipStream_t st = (hipStream_t)stream;
-    if (gY && E > 0) {
+    if (gY && E > 0 && Kd == 16 && N > 0) {
+        hipLaunchKernelGGL(dir_feats_bwd_row_kernel, dim3((unsigned)((N + kDirWaves - 1) / kDirWaves)),
+                           dim3(kDirWaves * kWave), 0, st, T, col, row_ptr, gd, N, gY);
+    } else if (gY && E > 0) {
         int KP = 1;
         while (KP < Kd) KP <<= 1;
         hipLaunchKernelGGL(dir_feats_bwd_edge_kernel, dim3(blocks_for(E * KP)), dim3(256), 0, st, T, Kd, KP, recv, col,
