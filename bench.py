@@ -467,17 +467,18 @@ def run_gpu(k, steps, warmup, use_graph=True, compiled_radial=False):
     peak_gb = torch.cuda.max_memory_allocated() / 1e9
     log(f"[bench]   eager: {1e3 * statistics.median(eager):.3f} ms/step, peak device memory {peak_gb:.2f} GB")
     # eager steps with HIP events around every hot-kernel launch (kernel durations), recorded on
-    # torch's current stream, the stream every entry point launches on. Where the host enqueues a
-    # step in a time comparable to the GPU's (small systems), a start event fires while the GPU
-    # waits for the launch and the wait counts as kernel time: there each step is queued behind a
-    # device spin longer than the host takes to enqueue it, so its launches run back to back (864
-    # atoms: density forward 17.5 -> 15.4 us by events, 12.6-13.4 us in the kernel trace). Where
-    # the GPU step is far longer the host is ahead anyway and the steps run as they come (the spin
-    # there raised the 24k row-GEMM average from 409 to 462 us against 404 us in the trace).
+    # torch's current stream, the stream every entry point launches on. Where the host sets the
+    # pace (its enqueue time per step above half the eager step time: the small systems), a start
+    # event fires while the GPU waits for the launch and the wait counts as kernel time: there
+    # each step is queued behind a device spin longer than the host takes to enqueue it, so its
+    # launches run back to back (864 atoms: density forward 17.5 -> 15.4 us by events, 12.6-13.4
+    # us in the kernel trace). Where the GPU sets the pace the host runs ahead anyway and the steps
+    # run as they come (the spin there raised the 24k row-GEMM average from 409 to 462 us against
+    # 404 us in the trace; under a profiler the host enqueues a 24k step in 7 of its 18 ms).
     t0 = time.perf_counter()
     step()
     t_host = time.perf_counter() - t0
-    spin = spin_cycles(2.0 * t_host + 2e-3) if t_host > 0.25 * statistics.median(eager) else 0
+    spin = spin_cycles(2.0 * t_host + 2e-3) if t_host > 0.5 * statistics.median(eager) else 0
     torch.cuda.synchronize()
     timers = _lib.time_calls(TIMED)
     for _ in range(steps):
