@@ -915,8 +915,8 @@ def trace_summary(stats_csv, bench_log, out_path, title):
 # ----------------------------------------------------------------------------- main
 MIN_ROUNDS = 7                          # the reference's protocol: >= 7 rounds of 5 calls
 LINE_MAX_CHARS = 8000                   # the one stdout line stays a few KB (per-label detail -> stderr)
-DENSITY_FAMILIES = ("density_fwd", "density_bwd", "cp_density_fwd", "cp_radial_bwd", "cp_density_bwd",
-                    "density_mix_fwd", "density_mix_bwd")
+DENSITY_FAMILIES = ("density_fwd", "density_bwd", "cp_density_fwd", "cp_radial_fwd", "cp_radial_bwd",
+                    "cp_density_bwd", "density_mix_fwd", "density_mix_bwd")
 
 
 def timed_steps(requested):
@@ -972,9 +972,11 @@ def compact_cpu(cpu):
 
 def north_star_kernels(r):
     """HBM fraction of the density kernels and of the force scatter (the kernels the target is
-    quoted on): per family present, the fraction of 8 TB/s its algorithmic bytes reach. The force
-    backward is also given as one unit, the edge backward (which writes every edge's dL/dvec into
-    its reverse edge's slot) and the row scatter that completes it: their bytes over their time."""
+    quoted on): per family present, the fraction of 8 TB/s its algorithmic bytes reach, and for a
+    family whose binding floor is its matrix work (the fused CP kernels, the factor density at
+    100k atoms) also its fraction of the fp32 MFMA peak. The force backward is also given as one
+    unit, the edge backward (which writes every edge's dL/dvec into its reverse edge's slot) and
+    the row scatter that completes it: their bytes over their time."""
     out = {}
     for fam_name in DENSITY_FAMILIES + ("force_scatter",):
         f = r["families"].get(fam_name)
@@ -982,6 +984,9 @@ def north_star_kernels(r):
             continue
         gbs = f["alg_bytes_per_launch"] / (f["avg_us"] * 1e-6) / 1e9
         out[fam_name] = {"us": _r(f["avg_us"]), "GBps": _r(gbs), "hbm_frac": _r(gbs / HBM_PEAK_GBS, 3)}
+        if f.get("bound") == "mfma" and f.get("alg_flops_per_launch"):
+            tfs = f["alg_flops_per_launch"] / (f["avg_us"] * 1e-6) / 1e12
+            out[fam_name]["mfma_frac"] = _r(tfs / MFMA_PEAK_TFS, 3)
     fe, fs = r["families"].get("edge_geom_bwd"), r["families"].get("force_scatter")
     if fe and fs and fe.get("alg_bytes_per_launch") and fs.get("alg_bytes_per_launch"):
         byts = fe["bytes_per_step"] + fs["bytes_per_step"]

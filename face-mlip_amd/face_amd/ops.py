@@ -806,9 +806,10 @@ class CPRadialDensity(torch.autograd.Function):
     """CP pooling fed by the CP columns of the last radial layer: R = h2 W_cp^T + b_cp (E, 4C), then
     A_l as in CPDensity (face/model.py:469-472, 496-502). With per-edge messages the forward computes
     R on the matrix cores and pools it in the same launch (R is written once, for the backward, and
-    not read back: 1.85 ms against 2.03 ms for the two launches at 24,000 atoms, C = 160); with
-    node-table messages gathered through col, and for shapes that launch cannot serve, R comes from
-    the radial head and is pooled in a second launch (1.89 ms against 2.03 ms fused there). The
+    not read back: 1.85 ms against 2.03 ms for the two launches at 24,000 atoms, C = 160; 0.345
+    against 0.385 ms at 512 molecules); with node-table messages gathered through col, and for
+    shapes that launch cannot serve, R comes from the radial head and is pooled in a second launch
+    (1.89 ms against 2.03 ms fused there). The
     backward multiplies the pooling's dR by W_cp on the matrix cores inside the pooling kernel and
     returns d h2 (E, H) without writing dR. W_cp / b_cp receive no gradient (forces only)."""
 
