@@ -1601,7 +1601,9 @@ __global__ __launch_bounds__(NW * kWave) void cp_radial_bwd_res_kernel(
 // latency rather than by its 0.86 ms of MFMA issue: without the R stores it takes 1.38 ms, as
 // loads and stores share the in-order vmcnt counter and each channel block's loads wait for the
 // previous block's stores. Measured and not kept: message and bias values issued a block ahead
-// (1.93 ms), message rows issued a tile ahead (1.91 / 1.96 ms with gathered rows: spills),
+// (1.93 ms), message rows issued a tile ahead (1.91 / 1.96 ms with gathered rows: spills; as
+// 32-bit row indices with addresses formed per channel block, 1.89 / 1.94 ms against the
+// two-launch 1.90 ms),
 // ranks 0-2 sharing one accumulator tile through the K slots (2.24 ms: twelve dependent
 // products per segment).
 constexpr int kCrfWaves = 4;
