@@ -1,0 +1,156 @@
+"""Symmetries of the GPU energy and forces, after face/tests/test_symmetry.py:24-68, at the fp32
+tolerances of the parity tests (energy 1e-5 relative, forces 1e-4 x RMS(F) max-abs): rotations
+and reflections with a translation (E invariant, F rotating along), atom permutations (E
+invariant, F permuted), a periodic box moved by a translation and rotated together with its
+cell, and C1 continuity of E and F across the cutoff. Each case runs the factor and the CP
+model forms through the HIP kernels (MFMA widths B = 16, C = 32)."""
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+E_TOL, F_TOL = 1e-5, 1e-4
+FLAG = dict(n_basis=8, n_passes=2, radial_hidden=64, K_dir=16, norm="layer", transport=True, eqmsg=True,
+            factor=True, B=16, K=32, rc=4.5)
+MODELS = {"factor": dict(FLAG, C=32), "cp": dict(FLAG, C=32, cp=True)}
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def model(name):
+    from face_amd import model as fm
+    torch.manual_seed(0)
+    m = fm.FACE([1, 6, 8], **MODELS[name])
+    fm.unit_parameterise(m)
+    g = torch.Generator().manual_seed(1)
+    with torch.no_grad():                       # test_symmetry.py:32-33: weights off their init
+        for p in m.parameters():
+            p.add_(0.1 * torch.randn(p.shape, generator=g))
+    return m.cuda().eval()
+
+
+def evaluate(m, structures, rc):
+    from face_amd.neighbors import build_graph
+    o = m(build_graph(structures, rc))
+    return o["energy"].detach().double().cpu().numpy(), o["forces"].detach().double().cpu().numpy()
+
+
+def rand_rot(rng, reflect=False):
+    q, _ = np.linalg.qr(rng.standard_normal((3, 3)))
+    q = q * np.sign(np.linalg.det(q))
+    return -q if reflect else q
+
+
+def assert_close(E, F, E0, F0):
+    dE = np.abs(E - E0).max() / np.abs(E0).max()
+    dF = np.abs(F - F0).max() / np.sqrt((F0 ** 2).mean())
+    say(f"  dE/E {dE:.1e}  max|dF|/rms {dF:.1e}")
+    assert dE <= E_TOL and dF <= F_TOL, (dE, dF)
+
+
+def molecules():
+    from face_amd import systems
+    return systems.molecules(3, np.random.default_rng(7))
+
+
+def liquid_box():
+    from face_amd import systems
+    sts, _, _, _ = systems.workload(3, n_atoms=400)
+    return sts[0]
+
+
+@pytest.mark.parametrize("name", list(MODELS))
+def test_rotation_reflection_translation(name):
+    """test_symmetry.py:37-40: E(Q x + t) = E(x), F(Q x + t) = F(x) Q^T for a rotation and a
+    rotation with reflection, on a batch of three molecules."""
+    say("rotation", name)
+    m, rc = model(name), MODELS[name]["rc"]
+    sts = molecules()
+    E0, F0 = evaluate(m, sts, rc)
+    rng = np.random.default_rng(3)
+    for reflect in (False, True):
+        Q, t = rand_rot(rng, reflect), rng.standard_normal(3)
+        moved = [dict(s, pos=s["pos"] @ Q.T + t) for s in sts]
+        E, F = evaluate(m, moved, rc)
+        assert_close(E, F, E0, F0 @ Q.T)
+
+
+@pytest.mark.parametrize("name", list(MODELS))
+def test_permutation(name):
+    """test_symmetry.py:42-45: renumbering the atoms leaves each structure's energy unchanged and
+    permutes the forces; molecules and a 400-atom periodic liquid box (cell list)."""
+    say("permutation", name)
+    m, rc = model(name), MODELS[name]["rc"]
+    rng = np.random.default_rng(5)
+    for sts in (molecules(), [liquid_box()]):
+        E0, F0 = evaluate(m, sts, rc)
+        perms = [rng.permutation(len(s["Z"])) for s in sts]
+        moved = [dict(s, pos=s["pos"][p], Z=s["Z"][p]) for s, p in zip(sts, perms)]
+        E, F = evaluate(m, moved, rc)
+        offs = np.concatenate([[0], np.cumsum([len(s["Z"]) for s in sts])])
+        Fp = np.concatenate([F0[o:o + len(p)][p] for o, p in zip(offs, perms)])
+        assert_close(E, F, E0, Fp)
+
+
+@pytest.mark.parametrize("name", list(MODELS))
+def test_periodic_box_translation_and_rotation(name):
+    """A periodic box moved by a translation (positions left unwrapped), then rotated together
+    with its cell vectors (a general, non-diagonal cell for the cell-list pair build)."""
+    say("periodic box", name)
+    m, rc = model(name), MODELS[name]["rc"]
+    st = liquid_box()
+    E0, F0 = evaluate(m, [st], rc)
+    rng = np.random.default_rng(11)
+    t = rng.standard_normal(3) * 3.0
+    E, F = evaluate(m, [dict(st, pos=st["pos"] + t)], rc)
+    assert_close(E, F, E0, F0)
+    Q = rand_rot(rng)
+    E, F = evaluate(m, [dict(st, pos=st["pos"] @ Q.T, cell=st["cell"] @ Q.T)], rc)
+    assert_close(E, F, E0, F0 @ Q.T)
+
+
+@pytest.mark.parametrize("name", list(MODELS))
+def test_cutoff_continuity(name):
+    """test_symmetry.py:58-66: a third atom just inside and just outside r_c of the first: the
+    energy changes by about slope x distance and the force on it by less than 1e-5."""
+    say("cutoff", name)
+    m, rc = model(name), MODELS[name]["rc"]
+    vals = []
+    for x in (rc - 1e-5, rc + 1e-5):
+        pos = np.zeros((3, 3))
+        pos[1, 0] = 1.0
+        pos[2, 0] = x
+        st = {"pos": pos, "Z": np.array([6, 1, 8]), "cell": np.zeros((3, 3)), "pbc": np.zeros(3, bool)}
+        E, F = evaluate(m, [st], rc)
+        vals.append((float(E.sum()), float(F[2, 0])))
+    dE, dF = abs(vals[0][0] - vals[1][0]), abs(vals[0][1] - vals[1][1])
+    say(f"  dE {dE:.1e}  dF {dF:.1e}")
+    slope = abs(vals[0][1])
+    assert dE < 2e-5 * (slope + 1) + 1e-6 * abs(vals[0][0]), (dE, vals)
+    assert dF < 1e-5 * (1 + slope), (dF, vals)
+
+
+@pytest.mark.parametrize("name", list(MODELS))
+def test_forces_match_energy_central_differences(name):
+    """test_symmetry.py:47-52: F = -dE/dx against central differences of the GPU energy at three
+    coordinates (fp32 energies: h = 1e-2 A; the measured gaps are 0-3e-5 eV/A, the tolerance
+    2e-4 (1 + |F|))."""
+    say("finite differences", name)
+    m, rc = model(name), MODELS[name]["rc"]
+    st = molecules()[:1]
+    _, F = evaluate(m, st, rc)
+    h = 1e-2
+    for i, c in [(0, 0), (7, 2), (15, 1)]:
+        vals = []
+        for sgn in (1, -1):
+            pos = st[0]["pos"].copy()
+            pos[i, c] += sgn * h
+            vals.append(float(evaluate(m, [dict(st[0], pos=pos)], rc)[0].sum()))
+        fd = -(vals[0] - vals[1]) / (2 * h)
+        say(f"  atom {i} axis {c}: fd {fd:.5f}  F {F[i, c]:.5f}")
+        assert abs(fd - F[i, c]) < 2e-4 * (1 + abs(F[i, c])), (fd, F[i, c])
