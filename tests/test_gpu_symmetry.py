@@ -46,11 +46,11 @@ def rand_rot(rng, reflect=False):
     return -q if reflect else q
 
 
-def assert_close(E, F, E0, F0):
+def assert_close(E, F, E0, F0, f_tol=F_TOL):
     dE = np.abs(E - E0).max() / np.abs(E0).max()
     dF = np.abs(F - F0).max() / np.sqrt((F0 ** 2).mean())
     say(f"  dE/E {dE:.1e}  max|dF|/rms {dF:.1e}")
-    assert dE <= E_TOL and dF <= F_TOL, (dE, dF)
+    assert dE <= E_TOL and dF <= f_tol, (dE, dF)
 
 
 def molecules():
@@ -154,3 +154,32 @@ def test_forces_match_energy_central_differences(name):
         fd = -(vals[0] - vals[1]) / (2 * h)
         say(f"  atom {i} axis {c}: fd {fd:.5f}  F {F[i, c]:.5f}")
         assert abs(fd - F[i, c]) < 2e-4 * (1 + abs(F[i, c])), (fd, F[i, c])
+
+
+@pytest.mark.parametrize("k", [1, 3])
+def test_benchmark_systems_rotated(k):
+    """The rotation check at full benchmark size with the benchmark models (random-init, unit
+    parameterisation): 512 molecules (each rotated and moved by the same Q, t) and the
+    24,000-atom periodic liquid rotated with its cell (1.25 M pairs through the cell list with
+    a general cell). Two fp32 evaluations, each within the parity bar of the exact forces, may
+    differ by twice it: the liquid's net forces (RMS 0.0075 eV/A) are sums of much larger pair
+    terms, and over its 72,000 components the largest difference is 8e-5 x RMS (6e-7 eV/A;
+    median 3.5e-6 x RMS), so the forces are held to 2e-4 x RMS here."""
+    from face_amd import systems
+    from face_amd import model as fm
+    say("benchmark system rotated", k)
+    sts, kw, el, _ = systems.workload(k)
+    torch.manual_seed(0)
+    m = fm.FACE(el, **kw)
+    fm.unit_parameterise(m)
+    m = m.cuda().eval()
+    E0, F0 = evaluate(m, sts, kw["rc"])
+    rng = np.random.default_rng(13)
+    Q, t = rand_rot(rng), rng.standard_normal(3)
+    if k == 3:
+        moved = [dict(s, pos=s["pos"] @ Q.T, cell=s["cell"] @ Q.T) for s in sts]
+    else:
+        moved = [dict(s, pos=s["pos"] @ Q.T + t) for s in sts]
+    E, F = evaluate(m, moved, kw["rc"])
+    assert np.isfinite(E).all() and np.isfinite(F).all()
+    assert_close(E, F, E0, F0 @ Q.T, f_tol=2 * F_TOL)
