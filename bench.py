@@ -693,13 +693,14 @@ def pmc_summary(fetch_dir, write_dir, probe_log, out_path):
             names[lab].add(r["Kernel_Name"].replace("void ", "").split("(")[0].replace("face::", ""))
     k = probe.get("workload", 3)
     out = [f"# HBM traffic per launch: {probe['probe']}\n\n",
-           "Commands (repo root, MI355X, ROCm 7.2), one counter per pass, then the summary:\n\n```\n"]
+           "Commands (repo root, MI355X, ROCm 7.2; OUT is the output directory), one counter per pass, "
+           "then the summary:\n\n```\n"]
     for C in ("FETCH_SIZE", "WRITE_SIZE"):
         out.append(f"rocprofv3 --pmc {C} --kernel-include-regex 'face::|copy' --output-format csv "
-                   f"-d gpurun_out/pmc_{C}_w{k} -o p -- python -u bench.py --pmc-probe --workload {k} "
-                   f"> gpurun_out/pmc_{C}_w{k}.log\n")
-    out.append(f"python bench.py --pmc-summary gpurun_out/pmc_FETCH_SIZE_w{k} gpurun_out/pmc_WRITE_SIZE_w{k} "
-               f"gpurun_out/pmc_FETCH_SIZE_w{k}.log {out_path}\n```\n\n")
+                   f"-d $OUT/pmc_{C}_w{k} -o p -- python -u bench.py --pmc-probe --workload {k} "
+                   f"> $OUT/pmc_{C}_w{k}.log\n")
+    out.append(f"python bench.py --pmc-summary $OUT/pmc_FETCH_SIZE_w{k} $OUT/pmc_WRITE_SIZE_w{k} "
+               f"$OUT/pmc_FETCH_SIZE_w{k}.log {out_path}\n```\n\n")
     out.append("`bench.py --pmc-probe` runs one eager E+F step (the row GEMM's launch shapes are timed there) "
                "and a marker launch, then 2 recorded eager E+F steps with a marker launch after every library "
                "call, then three device-to-device copies of 1 GiB; only dispatches after the first marker are "
@@ -970,7 +971,7 @@ def compact_cpu(cpu):
             "sample": cpu["sample"]}
 
 
-def north_star_kernels(r):
+def hot_path_kernels(r):
     """HBM fraction of the density kernels and of the force scatter (the kernels the target is
     quoted on): per family present, the fraction of 8 TB/s its algorithmic bytes reach, and for a
     family whose binding floor is its matrix work (the fused CP kernels, the factor density at
@@ -1003,7 +1004,7 @@ def compact_workload(r, cpu=None):
            "value": _r(r["atom_steps_per_s"]), "rounds": r["rounds"],
            "roofline": None if rf is None else {"kernel": rf["kernel"], "bound": rf["bound"],
                                                 "frac": _r(rf["frac"], 3)},
-           "hbm": north_star_kernels(r)}
+           "hbm": hot_path_kernels(r)}
     if r.get("route"):
         out["route"] = r["route"]
     if cpu is not None:
@@ -1032,7 +1033,7 @@ def bench_line(main_run, results, cpu, workload, steps, steps_requested, warmup,
                    "peak_mem_gb": _r(main_run["peak_mem_gb"], 3)},
         "roofline": compact_roofline(main_run["roofline"]),
         "cpu_baseline": compact_cpu(cpu.get(workload)),
-        "hbm": north_star_kernels(main_run),
+        "hbm": hot_path_kernels(main_run),
         "also": also,
         "_argv": " ".join(sys.argv[1:]),
     }
