@@ -459,9 +459,10 @@ def readout_mlp(inv, h, W0a, W0b, b0, W1, b1, W2, b2, Wg=None, bg=None, last=Fal
 
 class AtomEnergy(torch.autograd.Function):
     """Atom energies e_at = e0 + scale * e_1 + scale * e_2 + ... (N,) and their per-structure sums
-    E (nstr,) (face/model.py:680-690) in one launch (atoms of a structure contiguous, ranges
-    struct_ptr); the backward gives every pass the same gradient scale * (gE[structure] + g_at),
-    again one launch. e_p may be strided (N, 1) column views."""
+    E (nstr,) (face/model.py:680-690) in two launches (the atoms over the whole device, then one
+    fixed-order sum per structure; atoms of a structure contiguous, ranges struct_ptr); the
+    backward gives every pass the same gradient scale * (gE[structure] + g_at) in one launch.
+    e_p may be strided (N, 1) column views."""
 
     @staticmethod
     def forward(ctx, e0, scale, struct_ptr, nstr, *es):
