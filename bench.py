@@ -757,6 +757,15 @@ SQ_PASSES = [
 ]
 
 
+def _out_rel(path):
+    """A path of the run's output directory written as $OUT/... (the summaries' commands name the
+    output directory OUT); paths under profiles/ are kept."""
+    path = str(path)
+    if path.startswith("profiles/") or "/" not in path:
+        return path
+    return "$OUT/" + path.split("/", 1)[1]
+
+
 def sq_summary(out_path, title, probe_args, *dirs):
     """Per-kernel SQ counter summary of `rocprofv3 --pmc` passes (SQ_PASSES, one directory each) over
     `bench.py --pmc-probe ...`: wave occupancy and wait fractions, instruction mix and MFMA busy
@@ -791,11 +800,13 @@ def sq_summary(out_path, title, probe_args, *dirs):
                 r["Kernel_Name"].split("(")[0].replace("void ", "").replace("face::", "")
             data[k][r["Counter_Name"]].append(float(r["Counter_Value"]))
             data[k]["_dur_ns"].append(float(r["End_Timestamp"]) - float(r["Start_Timestamp"]))
-    out = [f"# SQ counters: {title}\n\nCommands (repo root, MI355X, ROCm 7.2), one pass per counter group:\n\n```\n"]
+    out = [f"# SQ counters: {title}\n\nCommands (repo root, MI355X, ROCm 7.2; OUT is the output directory), one "
+           "pass per counter group:\n\n```\n"]
     for P, d in zip(SQ_PASSES, dirs):
         out.append(f"rocprofv3 --pmc {P} --kernel-include-regex 'face::' --output-format csv "
-                   f"-d {d} -o p -- python -u bench.py --pmc-probe {probe_args}\n")
-    out.append(f"python bench.py --sq-summary {out_path} '{title}' '{probe_args}' " + " ".join(dirs) + "\n```\n\n")
+                   f"-d {_out_rel(d)} -o p -- python -u bench.py --pmc-probe {probe_args}\n")
+    out.append(f"python bench.py --sq-summary {_out_rel(out_path)} '{title}' '{probe_args}' "
+               + " ".join(_out_rel(d) for d in dirs) + "\n```\n\n")
     out.append("Per dispatch averages. wave-cycle fractions: time a wave spends waiting on anything / on "
                "s_waitcnt / issuing. mfma_util: SQ_VALU_MFMA_BUSY_CYCLES over (1024 SIMDs x duration x 2.4 GHz).\n\n"
                "| kernel | dispatches | waves | us | wait_any | wait_inst | active | mfma insts | "
@@ -857,10 +868,12 @@ def trace_summary(stats_csv, bench_log, out_path, title):
     marks = [i for i, r in enumerate(rows) if _kernel_base(r["Kernel_Name"]) == PROBE_MARK]
     base_fam = {kn: fam for fam, kns in FAMILY_KERNELS.items() for kn in kns}
     steps = d["steps"]
-    out = [f"# Kernel-time summary: {title}\n\nCommand (repo root, MI355X, ROCm 7.2):\n\n```\n"
-           f"rocprofv3 --kernel-trace --stats --output-format csv -d {os.path.dirname(stats_csv)} -o bench -- "
-           f"python -u bench.py {d.get('_argv', '')}\n"
-           f"python bench.py --trace-summary {stats_csv} <bench stdout+stderr> {out_path} '<title>'\n```\n\n"
+    out = [f"# Kernel-time summary: {title}\n\nCommand (repo root, MI355X, ROCm 7.2; OUT is the output "
+           f"directory):\n\n```\n"
+           f"rocprofv3 --kernel-trace --stats --output-format csv -d {_out_rel(os.path.dirname(stats_csv))} -o bench "
+           f"-- python -u bench.py {d.get('_argv', '')}\n"
+           f"python bench.py --trace-summary {_out_rel(stats_csv)} <bench stdout+stderr> {_out_rel(out_path)} "
+           f"'<title>'\n```\n\n"
            f"Each workload's section covers only the dispatches between its two trace marks: the {steps} timed "
            f"HIP-graph replays of the E+F step (warm-ups, the instrumented eager steps and TunableOp's tuning "
            f"fall outside). Per-step figures divide by {steps}. \"bench us\" is the HIP-event average per launch "
